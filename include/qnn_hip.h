@@ -1,0 +1,230 @@
+/*
+ * qnn_hip.h -- C ABI of libqnn_hip.so, the MI355X (gfx950) backend for
+ * QuickNN's quantized-weight decode path.
+ *
+ * The library stands in for the Vulkan resident context TQNNGPUContext
+ * (src/backends/vulkan/QuickNN.Vulkan.Context.API.inc:14-165) on the methods
+ * the LLM engine in src/models calls for packed matvec, fused gate/up + SwiGLU
+ * and routed-expert execution.  Every entry point is cdecl, takes plain
+ * pointers and sizes, and returns a status code; the Object Pascal unit re-raises
+ * the matching exception class (see INTEGRATION.md for the binding).
+ *
+ * Conventions (as in the reference):
+ *  - One context exists at a time; it is bound to the thread that created it
+ *    (Context.Implementation.inc:10-18, :70-71).  Calls from another thread
+ *    fail with QNN_E_INVALID_OP.
+ *  - Ops record asynchronously on the context's HIP stream; qnn_flush and
+ *    qnn_download wait (Context.Implementation.inc:399-419, :707-758).
+ *  - Tensors are context-owned fp32 device buffers of `count` floats, pooled
+ *    best-fit (Context.Implementation.inc:110-169).
+ *  - Weights are host views described by qnn_weight (TMemoryBlock,
+ *    src/core/QuickNN.Common.pas:135-155) and are copied into a device cache
+ *    keyed by identity/dtype/encoding/offset/bytes (QuickNN.Vulkan.pas:641-662).
+ *    Host memory need only stay valid during the call that uploads it.
+ *    On upload the bytes are re-laid into the backend's tiled device layout;
+ *    values and byte counts are unchanged.
+ */
+#ifndef QNN_HIP_H
+#define QNN_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: exception classes of the reference ---- */
+#define QNN_OK 0
+#define QNN_NOT_HANDLED 1        /* TrySwiGLUVector returned False (caller falls back) */
+#define QNN_E_ARGUMENT (-1)      /* EArgumentException */
+#define QNN_E_RANGE (-2)         /* ERangeError (budgets, device limits) */
+#define QNN_E_NOT_SUPPORTED (-3) /* ENotSupportedException */
+#define QNN_E_INVALID_OP (-4)    /* EInvalidOp (wrong thread, non-finite results, device failure) */
+
+/* ---- TQNNDataType ordinals (src/core/QuickNN.Common.pas:71-90) ---- */
+#define QNN_DT_F16 1
+#define QNN_DT_BF16 2
+#define QNN_DT_F32 3
+#define QNN_DT_S8 5
+#define QNN_DT_U8 6
+
+/* ---- TQNNWeightEncoding ordinals (src/core/QuickNN.Common.pas:130-131) ---- */
+#define QNN_WE_NATIVE 0
+#define QNN_WE_Q8_0 1
+#define QNN_WE_Q4_K 2
+#define QNN_WE_Q6_K 3
+#define QNN_WE_Q3_K 4
+#define QNN_WE_Q2_K 9
+
+/* ---- op codes accepted by qnn_kernel / qnn_kernel_weights
+        (Context.API.inc:167-258) ---- */
+#define QNN_GO_FILL 0
+#define QNN_GO_NORM 2
+#define QNN_GO_ADD 4
+#define QNN_GO_SWIGLU 9
+#define QNN_GO_FINITE 13
+#define QNN_GO_MOE_ROUTE 52
+#define QNN_GO_MOE_GATHER 53
+#define QNN_GO_MOE_SCATTER 54
+#define QNN_GO_GEGLU 75
+
+typedef struct qnn_ctx_s qnn_ctx;       /* TQNNGPUContext */
+typedef struct qnn_tensor_s qnn_tensor; /* TQNNGPUTensor: fp32 device buffer */
+typedef struct qnn_expert_set_s qnn_expert_set;
+
+/* TMemoryBlock view of a weight (src/core/QuickNN.Common.pas:135-155).
+ * Native INT4: dtype U8, encoding NATIVE, shape [N, Int4RowBytes(K)], size in bytes, offset 0.
+ * GGUF: dtype U8, encoding Q*, shape [N, K] in elements, size in elements,
+ *       offset in elements (block-aligned); data points at element 0. */
+typedef struct {
+  uint64_t identity; /* WeightIdentity: non-zero; equal identity means the same immutable bytes */
+  const void *data;  /* host storage base (element 0, before offset) */
+  int64_t offset;    /* Offset */
+  int64_t size;      /* Size */
+  int64_t shape0;    /* Shape[0] */
+  int64_t shape1;    /* Shape[1] */
+  int32_t dtype;     /* TQNNDataType ordinal */
+  int32_t encoding;  /* TQNNWeightEncoding ordinal */
+} qnn_weight;
+
+/* TQNNGPUStatus counters (src/backends/vulkan/QuickNN.Vulkan.pas:17-29). */
+typedef struct {
+  uint64_t gemm_calls, gguf_calls, int4_calls, moe_calls;
+  uint64_t weight_uploads, weight_upload_bytes, weight_cache_hits, weight_cache_misses, weight_evictions;
+  uint64_t readbacks, submissions;
+  uint64_t weight_bytes, weight_limit, activation_bytes, activation_peak_bytes;
+} qnn_status;
+
+/* ---------------------------------------------------------------------------
+ * Errors
+ * ------------------------------------------------------------------------- */
+/* Copies the calling thread's last error message; returns its length. */
+int qnn_last_error(char *buf, int len);
+
+/* ---------------------------------------------------------------------------
+ * Context lifetime -- TQNNGPUContext.Create/Destroy (Context.Implementation.inc:14-80)
+ * ------------------------------------------------------------------------- */
+/* weight_cache_bytes = 0 selects 85% of the device's free memory. */
+int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out);
+int qnn_ctx_destroy(qnn_ctx *ctx);
+int qnn_get_status(qnn_ctx *ctx, qnn_status *out);
+
+/* ---------------------------------------------------------------------------
+ * Resident tensors (Context.API.inc:79-106)
+ * ------------------------------------------------------------------------- */
+int qnn_tensor_new(qnn_ctx *ctx, int count, qnn_tensor **out);                 /* NewTensor */
+int qnn_recycle(qnn_ctx *ctx, qnn_tensor **tensor);                            /* Recycle */
+int qnn_scratch(qnn_ctx *ctx, int slot, int count, qnn_tensor **out);          /* Scratch */
+int qnn_upload_raw(qnn_ctx *ctx, const void *data, int count, qnn_tensor **out); /* UploadRaw */
+int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count);           /* Download (-1 = all) */
+int qnn_copy(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, int count, int dst_offset, int src_offset); /* Copy */
+int qnn_flush(qnn_ctx *ctx);                                                   /* Flush */
+int qnn_tensor_count(const qnn_tensor *t);
+void *qnn_tensor_device_ptr(const qnn_tensor *t);
+
+/* ---------------------------------------------------------------------------
+ * Weight residency (Context.API.inc:83-97; QuickNN.Vulkan.pas:551-740)
+ * ------------------------------------------------------------------------- */
+int qnn_retain_weight(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols);  /* RetainWeight */
+int qnn_preload_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, uint64_t staging_limit); /* PreloadWeights */
+int qnn_is_weight_resident(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols, int *resident); /* IsWeightResident */
+int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /* WeightBatchCapacity */
+
+/* ---------------------------------------------------------------------------
+ * Hot-path ops
+ * ------------------------------------------------------------------------- */
+/* Linear (Context.API.inc:117-122, Implementation.inc:813-899).  GGUF weights:
+ * rows == 1 runs the packed matvec (op 65), rows > 1 the multi-row product
+ * (gemm.comp); Q8_0 with rows > 1 runs the int8-MFMA GEMM.  bias (optional,
+ * F32 or BF16 [out]) is added afterwards.  scales must be NULL (INT8 ConvRot
+ * weights are outside this backend). */
+int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,
+               const qnn_weight *bias, int rows, int in_dim, int out_dim);
+
+/* Int4Linear (Context.API.inc:138-142, Implementation.inc:1080-1135):
+ * 1 <= rows <= 128; weight U8/NATIVE [out_dim, Int4RowBytes(in_dim)], offset 0. */
+int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
+                    int out_dim);
+
+/* TrySwiGLUVector (Context.API.inc:132-133, Implementation.inc:1003-1056):
+ * dst[o] = silu(gate.x)[o] * (up.x)[o].  Returns QNN_OK, or QNN_NOT_HANDLED
+ * where the reference returns False (unsupported dtype mix, or the pair does
+ * not fit the weight budget and is not resident). */
+int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *gate, const qnn_weight *up,
+                      int in_dim, int out_dim);
+
+/* Int4LinearAccumulate (Context.API.inc:134-135, Implementation.inc:1058-1078):
+ * dst[o] += probabilities[prob_index] * (W src)[o]. */
+int qnn_int4_linear_accumulate(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, qnn_tensor *probabilities,
+                               const qnn_weight *w, int in_dim, int out_dim, int prob_index);
+
+/* Kernel (Context.API.inc:110) for the hot-path ops:
+ *   QNN_GO_FILL        args [bits]                       dst[i] = float(bits), i < n
+ *   QNN_GO_ADD         args [cols, dst_stride, alpha_bits, dst_off, src_off]  (tensor.comp:221)
+ *   QNN_GO_SWIGLU      args [I, interleaved]             (tensor.comp:228)
+ *   QNN_GO_GEGLU       args [I, 0]                       (tensor.comp:228)
+ *   QNN_GO_FINITE      args []                           same as qnn_check_finite
+ *   QNN_GO_MOE_ROUTE   args [rows, experts, topk, normalize]   (moe.comp:25-50)
+ *   QNN_GO_MOE_GATHER  args [hidden, topk, offset]             (moe.comp:124)
+ *   QNN_GO_MOE_SCATTER args [hidden, topk, offset, route_index, single_row, prob_base] (moe.comp:125-126)
+ * a, b, c may be NULL where the op does not read them. */
+int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_tensor *b, qnn_tensor *c,
+               const int *args, int nargs);
+
+/* KernelWeights (Context.API.inc:111-116) for GO_NORM (tensor.comp:63-73):
+ *   args [rows, dim, flags, 0, 0, src_offset, unit_gamma, eps_bits]; b = gamma (F32/BF16 [dim]). */
+int qnn_kernel_weights(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, const qnn_weight *b,
+                       const qnn_weight *c, const int *args, int nargs);
+
+/* CheckFinite (Context.API.inc:158): a later qnn_download fails with
+ * QNN_E_INVALID_OP if any checked value was NaN or infinite. */
+int qnn_check_finite(qnn_ctx *ctx, qnn_tensor *t, int count);
+
+/* ---------------------------------------------------------------------------
+ * Routed experts on the device.  Replaces the host loop of TLLMMoE.forward
+ * (src/models/QuickNN.Models.LLM.MoE.pas:376-448: route readback, per-expert
+ * grouping, per-expert dispatches) for native-INT4 experts: all experts of a
+ * layer are resident (registered once), routing and dispatch stay on the GPU
+ * and only the routed experts' blocks are read.
+ * ------------------------------------------------------------------------- */
+/* gate/up: [inter, Int4RowBytes(hidden)]; down: [hidden, Int4RowBytes(inter)]; arrays of `experts`. */
+int qnn_expert_set_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight *up, const qnn_weight *down,
+                          int experts, int hidden, int inter, qnn_expert_set **out);
+int qnn_expert_set_destroy(qnn_ctx *ctx, qnn_expert_set *set);
+/* routes: output of GO_MOE_ROUTE ([rows*topk ids][rows*topk probabilities]).
+ * dst[r] = sum over the token's routed experts in ascending id of
+ *          p * down(silu(gate x_r) * (up x_r)). */
+int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tensor *src, qnn_tensor *routes,
+                    int rows, int topk);
+
+/* ---------------------------------------------------------------------------
+ * Diagnostics (no reference counterpart)
+ * ------------------------------------------------------------------------- */
+/* Writes the dequantized weight, fp32 [rows, cols], from the device-resident copy. */
+int qnn_dequantize(qnn_ctx *ctx, qnn_tensor *dst, const qnn_weight *w, int rows, int cols);
+/* HIP events on the context stream, for timing (slot < 64). */
+int qnn_event_record(qnn_ctx *ctx, int slot);
+int qnn_event_elapsed_ms(qnn_ctx *ctx, int slot_begin, int slot_end, float *ms);
+/* Capture the ops recorded between begin and end into a HIP graph; replay it
+ * with qnn_graph_launch.  All weights must already be resident. */
+int qnn_graph_begin(qnn_ctx *ctx);
+int qnn_graph_end(qnn_ctx *ctx, int *graph_id);
+int qnn_graph_launch(qnn_ctx *ctx, int graph_id);
+void *qnn_stream(qnn_ctx *ctx);
+
+/* ---------------------------------------------------------------------------
+ * Host utilities
+ * ------------------------------------------------------------------------- */
+/* Int4RowBytes (src/core/QuickNN.Quantization.Int4.pas:25-33); -1 if invalid. */
+int qnn_int4_row_bytes(int cols);
+/* QuantizeInt4 (src/core/QuickNN.Quantization.Int4.pas:96-144): src F32 or BF16
+ * [rows, cols] -> dst U8 [rows, Int4RowBytes(cols)].  Non-finite input -> QNN_E_ARGUMENT. */
+int qnn_quantize_int4(const void *src, int dtype, int rows, int cols, uint8_t *dst);
+/* GGML block encoder for synthetic weights (the reference ships no GGUF
+ * quantizer): n elements (a multiple of the block size) -> blocks. */
+int qnn_gguf_quantize(int encoding, const float *src, int64_t n, uint8_t *dst);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

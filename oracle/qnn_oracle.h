@@ -1,0 +1,90 @@
+/*
+ * qnn_oracle.h -- CPU restatement of QuickNN's quantized-decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP backend
+ * (libqnn_hip.so) is compared against.  Only tests/, __graft_entry__.smoke()
+ * and the cpu_baseline leg of bench.py may load it.  Nothing in the product
+ * package links or calls it.
+ *
+ * Every function names the reference file:line it restates (paths relative to
+ * the QuickNN source tree).  Pinning of each function (known answers,
+ * invariants, brute force) lives in tests/test_oracle_*.py.
+ *
+ * Encodings follow TQNNWeightEncoding (src/core/QuickNN.Common.pas:130-131):
+ *   0 native, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q3_K, 9 Q2_K.
+ * The oracle uses QO_ENC_INT4 (-1) for QuickNN's native packed INT4 rows.
+ */
+#ifndef QNN_ORACLE_H
+#define QNN_ORACLE_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QO_ENC_INT4 (-1)
+#define QO_ENC_Q8_0 1
+#define QO_ENC_Q4_K 2
+#define QO_ENC_Q6_K 3
+#define QO_ENC_Q3_K 4
+#define QO_ENC_Q2_K 9
+
+/* Status codes: 0 ok, -1 argument error (EArgumentException). */
+
+/* ---- INT4 (src/core/QuickNN.Quantization.Int4.pas) ---- */
+int qo_int4_row_bytes(int cols);                                      /* :25-33 */
+int qo_quantize_int4(const void *src, int is_bf16, int rows, int cols, uint8_t *dst); /* :35-144 */
+float qo_int4_value(const uint8_t *row, int k);          /* CPU.Inference.pas:413-420 */
+void qo_int4_dequant_row(const uint8_t *row, int cols, float *out);
+
+/* ---- GGUF formats (src/io/QuickNN.GGUF.Quantization.pas) ---- */
+int qo_gguf_block_elements(int enc);                                  /* :67-75 */
+int qo_gguf_block_bytes(int enc);                                     /* :77-93 */
+float qo_gguf_value(const uint8_t *data, int enc, int64_t index);     /* :136-253 */
+int qo_gguf_decode_block(const uint8_t *block, int enc, float *out);  /* :274-368 */
+int qo_gguf_dequantize(const uint8_t *data, int enc, int64_t count, float *out); /* :370-383 */
+int qo_gguf_read4(const uint8_t *data, int enc, int64_t index, float *out4);
+                                /* shaders/gguf.glsl:591-655 (readGGUF4) */
+
+/* ---- AVX2 dots (CPU.Inference.AVX2.inc, GGUF.Dot.AVX2.inc) ---- */
+float qo_vector_dot(int n, const float *a, const float *b);           /* AVX2.inc:7-67 */
+float qo_int4_vector_dot(int n, const float *x, const uint8_t *w);    /* AVX2.inc:210-285 */
+float qo_packed_dot(const uint8_t *data, int enc, const float *x, int count);
+            /* GGUFTryDot (GGUF.Quantization.pas:255-272) -> PackedDot* (Dot.AVX2.inc) */
+
+/* ---- CPU projection (src/backends/cpu/QuickNN.CPU.Inference.pas) ---- */
+void *qo_pool_create(int threads);                                    /* :109-116 */
+void qo_pool_destroy(void *pool);
+int qo_pool_threads(void *pool);
+int qo_cpu_linear(void *pool, const uint8_t *w, int enc, const float *x, float *y,
+                  int in_dim, int out_dim);                            /* :316-428 */
+
+/* ---- Decode-layer composites (src/models/QuickNN.Models.QwenHybrid.CPU.pas) ---- */
+int qo_rmsnorm(const float *x, const float *gamma, int rows, int dim, float eps,
+               int add_one, float *out);                              /* :110-120 */
+float qo_silu(float g);                      /* :78-82 + :242-246 (clamps +-20) */
+int qo_cpu_mlp(void *pool, const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+               int enc, const float *x, int rows, int hidden, int inter, float *out);
+                                                                       /* :238-248 */
+
+/* ---- MoE (src/backends/vulkan/shaders/moe.comp:25-50, LLM.MoE.pas:230-449) ---- */
+int qo_moe_route(const float *logits, int rows, int experts, int k, int normalize,
+                 int select_on_logits, uint32_t *ids, float *probs);
+int qo_cpu_moe(void *pool, const uint8_t *const *gate, const uint8_t *const *up,
+               const uint8_t *const *down, const float *x, const uint32_t *ids,
+               const float *probs, int rows, int topk, int hidden, int inter, float *out);
+
+/* ---- Multi-row GGUF (src/core/QuickNN.Quantization.pas:247-258) ---- */
+int qo_gguf_gemm_scalar(const uint8_t *w, int enc, const float *a, int m, int k, int n,
+                        float *c, int row_begin, int row_end);
+int qo_q8_act_quant(const float *a, int m, int k, int8_t *hi, int8_t *lo, float *scale);
+int qo_q8_gemm_quantized(const uint8_t *w, const int8_t *hi, const int8_t *lo,
+                         const float *scale, int m, int k, int n, float *c);
+
+/* ---- numerics helpers ---- */
+float qo_half_to_float(uint16_t h);            /* src/core/QuickNN.Common.pas:1799+ */
+uint16_t qo_float_to_half(float f);            /* round-to-nearest-even (test helper) */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,991 @@
+// qnn_context.hip -- the resident context behind the C ABI (include/qnn_hip.h).
+//
+// Host-side counterpart of TQNNGPUContext
+// (src/backends/vulkan/QuickNN.Vulkan.Context.Implementation.inc) and the
+// weight cache of TQNNVulkan (src/backends/vulkan/QuickNN.Vulkan.pas:551-740),
+// built on one HIP stream per context.
+#include <algorithm>
+#include <cinttypes>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "qnn_internal.h"
+
+namespace qnn {
+
+thread_local std::string t_last_error;
+
+struct GraphRec {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<WeightEntry *> pinned;
+};
+
+struct ExpertSetImpl;
+
+}  // namespace qnn
+
+struct qnn_tensor_s : qnn::Tensor {};
+
+struct qnn_expert_set_s {
+  int experts = 0, hidden = 0, inter = 0;
+  std::vector<qnn::WeightEntry *> gate, up, down;
+  uint64_t *table = nullptr;  // device: [gate nib, gate scl, up nib, up scl, down nib, down scl] x experts
+};
+
+struct qnn_ctx_s {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::thread::id owner;
+  std::vector<qnn_tensor_s *> tensors;
+  qnn_tensor_s *scratch[4] = {nullptr, nullptr, nullptr, nullptr};
+  std::unordered_map<std::string, qnn::WeightEntry *> weights;
+  uint64_t weight_bytes = 0, weight_limit = 0, clock = 0;
+  int *error_flag = nullptr;
+  // split-K workspace: partial sums + per-tile tickets (zeroed once, self-resetting)
+  float *partial = nullptr;
+  size_t partial_floats = 0;
+  unsigned *counters = nullptr;
+  size_t counter_count = 0;
+  // generic workspace (MoE plan and hidden states, activation quantisation)
+  void *work = nullptr;
+  size_t work_bytes = 0;
+  // upload staging
+  void *staging = nullptr;
+  size_t staging_bytes = 0;
+  hipEvent_t events[64] = {};
+  bool capturing = false;
+  std::vector<qnn::WeightEntry *> capture_pins;
+  std::vector<qnn::GraphRec> graphs;
+  std::vector<qnn_expert_set_s *> sets;
+  qnn_status st{};
+  uint64_t act_bytes = 0;
+};
+
+namespace qnn {
+namespace {
+
+std::mutex g_lock;
+qnn_ctx_s *g_ctx = nullptr;
+
+template <typename F>
+int guarded(F &&f) {
+  try {
+    return f();
+  } catch (const Error &e) {
+    t_last_error = e.what();
+    return e.code;
+  } catch (const std::bad_alloc &) {
+    t_last_error = "host allocation failed";
+    return QNN_E_RANGE;
+  } catch (const std::exception &e) {
+    t_last_error = e.what();
+    return QNN_E_INVALID_OP;
+  }
+}
+
+void check_ctx(qnn_ctx_s *ctx) {
+  if (!ctx || ctx != g_ctx) fail(QNN_E_ARGUMENT, "invalid context");
+  // Context.Implementation.inc:70-71: resident work stays on its creating thread.
+  if (std::this_thread::get_id() != ctx->owner) fail(QNN_E_INVALID_OP, "context used from a thread other than its creator");
+  hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+}
+
+// Check (Context.Implementation.inc): a live tensor of at least `minimum` floats.
+void check_tensor(qnn_ctx_s *ctx, const qnn_tensor_s *t, int64_t minimum = 1) {
+  if (!t) fail(QNN_E_ARGUMENT, "missing tensor");
+  bool owned = std::find(ctx->tensors.begin(), ctx->tensors.end(), t) != ctx->tensors.end();
+  if (!owned || !t->live) fail(QNN_E_ARGUMENT, "tensor is not live in this context");
+  if (int64_t(t->count) < minimum) fail(QNN_E_ARGUMENT, "tensor too small for the operation");
+}
+
+void sync(qnn_ctx_s *ctx) {
+  if (ctx->capturing) fail(QNN_E_INVALID_OP, "synchronisation requested during graph capture");
+  hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  ctx->st.submissions++;
+}
+
+// ---------------------------------------------------------------- tensors
+qnn_tensor_s *new_tensor(qnn_ctx_s *ctx, int count) {
+  if (count < 1) fail(QNN_E_RANGE, "resident tensor size");
+  const size_t bytes = size_t(count) * 4;
+  qnn_tensor_s *best = nullptr;
+  for (auto *t : ctx->tensors)  // best-fit reuse (Context.Implementation.inc:123-127)
+    if (!t->live && t->capacity >= bytes && (!best || t->capacity < best->capacity)) best = t;
+  if (!best) {
+    if (ctx->capturing) fail(QNN_E_INVALID_OP, "tensor allocation during graph capture");
+    best = new qnn_tensor_s();
+    const size_t cap = (bytes + 255) & ~size_t(255);
+    if (hipMalloc(&best->ptr, cap) != hipSuccess) {
+      delete best;
+      (void)hipGetLastError();
+      fail(QNN_E_RANGE, "GPU activation allocation failed");
+    }
+    best->capacity = cap;
+    ctx->tensors.push_back(best);
+    ctx->act_bytes += cap;
+    ctx->st.activation_bytes = ctx->act_bytes;
+    ctx->st.activation_peak_bytes = std::max(ctx->st.activation_peak_bytes, ctx->act_bytes);
+  }
+  best->count = count;
+  best->live = true;
+  return best;
+}
+
+// ---------------------------------------------------------------- workspace
+void ensure_splitk(qnn_ctx_s *ctx, size_t partial_floats, size_t counters) {
+  if (partial_floats <= ctx->partial_floats && counters <= ctx->counter_count) return;
+  if (ctx->capturing) fail(QNN_E_INVALID_OP, "split-K workspace growth during graph capture (run the sequence once first)");
+  sync(ctx);
+  partial_floats = std::max(partial_floats, ctx->partial_floats);
+  counters = std::max(counters, ctx->counter_count);
+  if (ctx->partial) (void)hipFree(ctx->partial);
+  if (ctx->counters) (void)hipFree(ctx->counters);
+  ctx->partial = nullptr;
+  ctx->counters = nullptr;
+  hip_check(hipMalloc(&ctx->partial, std::max<size_t>(partial_floats, 1) * 4), "workspace allocation");
+  hip_check(hipMalloc(&ctx->counters, std::max<size_t>(counters, 1) * 4), "workspace allocation");
+  hip_check(hipMemset(ctx->counters, 0, std::max<size_t>(counters, 1) * 4), "workspace clear");
+  ctx->partial_floats = partial_floats;
+  ctx->counter_count = counters;
+}
+
+void *ensure_work(qnn_ctx_s *ctx, size_t bytes) {
+  if (bytes <= ctx->work_bytes) return ctx->work;
+  if (ctx->capturing) fail(QNN_E_INVALID_OP, "workspace growth during graph capture (run the sequence once first)");
+  sync(ctx);
+  if (ctx->work) (void)hipFree(ctx->work);
+  ctx->work = nullptr;
+  hip_check(hipMalloc(&ctx->work, bytes), "workspace allocation");
+  ctx->work_bytes = bytes;
+  return ctx->work;
+}
+
+void *ensure_staging(qnn_ctx_s *ctx, size_t bytes) {
+  if (bytes <= ctx->staging_bytes) return ctx->staging;
+  if (ctx->staging) (void)hipFree(ctx->staging);
+  ctx->staging = nullptr;
+  ctx->staging_bytes = 0;
+  if (hipMalloc(&ctx->staging, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    fail(QNN_E_RANGE, "weight upload staging allocation failed");
+  }
+  ctx->staging_bytes = bytes;
+  return ctx->staging;
+}
+
+// ---------------------------------------------------------------- weight cache
+int gguf_block_elements(int enc) {  // GGUF.Quantization.pas:67-75 (formats in this backend)
+  switch (enc) {
+    case QNN_WE_Q8_0: return 32;
+    case QNN_WE_Q4_K: case QNN_WE_Q6_K: case QNN_WE_Q3_K: case QNN_WE_Q2_K: return 256;
+  }
+  return -1;
+}
+int gguf_block_bytes(int enc) {  // GGUF.Quantization.pas:77-93
+  switch (enc) {
+    case QNN_WE_Q8_0: return 34;
+    case QNN_WE_Q4_K: return 144;
+    case QNN_WE_Q6_K: return 210;
+    case QNN_WE_Q3_K: return 110;
+    case QNN_WE_Q2_K: return 84;
+  }
+  return -1;
+}
+bool is_gguf(int enc) { return enc != QNN_WE_NATIVE; }
+
+void check_weight_desc(const qnn_weight *w) {
+  if (!w) fail(QNN_E_ARGUMENT, "missing weight");
+  if (w->identity == 0 || !w->data) fail(QNN_E_ARGUMENT, "Weight must have immutable identity and assigned storage");
+}
+
+// GGUFWeightBytes (GGUF.Quantization.pas:105-113).
+uint64_t gguf_weight_bytes(const qnn_weight *w, int rows, int cols) {
+  const int be = gguf_block_elements(w->encoding);
+  if (be < 0) fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
+  if (w->dtype != QNN_DT_U8 || rows < 1 || cols < 1 || cols % be != 0 || w->offset < 0 || w->offset % be != 0 ||
+      int64_t(rows) * cols > w->size - w->offset)
+    fail(QNN_E_ARGUMENT, "Invalid packed GGUF matrix span");
+  return uint64_t(int64_t(rows) * cols / be) * uint64_t(gguf_block_bytes(w->encoding));
+}
+
+// WeightKey (QuickNN.Vulkan.pas:641-662): identity/dtype:encoding/offset/bytes.
+std::string weight_key(const char *kind, const qnn_weight *w, uint64_t bytes) {
+  char buf[160];
+  snprintf(buf, sizeof buf, "%s/%016" PRIx64 "/%d:%d/%" PRId64 "/%" PRIu64, kind, w->identity, w->dtype, w->encoding,
+           w->offset, bytes);
+  return buf;
+}
+
+void evict_one_or_fail(qnn_ctx_s *ctx) {  // EvictOne (QuickNN.Vulkan.pas:551-579): LRU of unpinned entries
+  qnn::WeightEntry *oldest = nullptr;
+  for (auto &kv : ctx->weights) {
+    auto *e = kv.second;
+    if (e->pins == 0 && e->op_pins == 0 && (!oldest || e->last_use < oldest->last_use)) oldest = e;
+  }
+  if (!oldest) fail(QNN_E_RANGE, "VRAM cache cannot hold the active chain");
+  ctx->weights.erase(oldest->key);
+  ctx->weight_bytes -= oldest->bytes;
+  (void)hipFree(oldest->dptr);
+  delete oldest;
+  ctx->st.weight_evictions++;
+}
+
+void make_room(qnn_ctx_s *ctx, size_t bytes) {
+  if (bytes > ctx->weight_limit) fail(QNN_E_RANGE, "Weight exceeds VRAM cache limit");
+  while (ctx->weight_bytes + bytes > ctx->weight_limit) evict_one_or_fail(ctx);
+}
+
+WeightEntry *lookup(qnn_ctx_s *ctx, const std::string &key) {
+  auto it = ctx->weights.find(key);
+  if (it == ctx->weights.end()) return nullptr;
+  it->second->last_use = ++ctx->clock;
+  ctx->st.weight_cache_hits++;
+  if (ctx->capturing) {
+    it->second->pins++;
+    ctx->capture_pins.push_back(it->second);
+  }
+  return it->second;
+}
+
+WeightEntry *insert(qnn_ctx_s *ctx, WeightEntry *e) {
+  e->last_use = ++ctx->clock;
+  ctx->weights[e->key] = e;
+  ctx->weight_bytes += e->bytes;
+  ctx->st.weight_uploads++;
+  ctx->st.weight_upload_bytes += e->source_bytes;
+  return e;
+}
+
+void begin_miss(qnn_ctx_s *ctx) {
+  ctx->st.weight_cache_misses++;
+  if (ctx->capturing) fail(QNN_E_INVALID_OP, "weight not resident during graph capture (preload it first)");
+  sync(ctx);  // AcquireWeight flushes the resident context on a miss (QuickNN.Vulkan.pas:687-688)
+}
+
+void *alloc_weight(qnn_ctx_s *ctx, size_t bytes) {
+  make_room(ctx, bytes);
+  void *p = nullptr;
+  while (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    evict_one_or_fail(ctx);  // device memory fragmented or shared: yield another unpinned entry
+  }
+  return p;
+}
+
+// Native INT4 matrix [rows, Int4RowBytes(cols)] -> tiled device copy.
+WeightEntry *acquire_int4(qnn_ctx_s *ctx, const qnn_weight *w, int rows, int cols) {
+  check_weight_desc(w);
+  const int rb = qnn_int4_row_bytes(cols);
+  if (w->dtype != QNN_DT_U8 || w->encoding != QNN_WE_NATIVE || w->offset != 0 || rb < 0 || w->shape0 != rows ||
+      w->shape1 != rb || int64_t(rows) * rb > w->size)
+    fail(QNN_E_ARGUMENT, "Invalid packed INT4 projection");
+  const uint64_t bytes = uint64_t(rows) * rb;
+  const std::string key = weight_key("i4", w, bytes);
+  if (auto *e = lookup(ctx, key)) return e;
+  begin_miss(ctx);
+  auto *e = new WeightEntry();
+  e->key = key;
+  e->kind = WKind::Int4;
+  e->i4 = int4_layout(rows, cols);
+  e->bytes = e->i4.bytes();
+  e->source_bytes = bytes;
+  try {
+    e->dptr = alloc_weight(ctx, e->bytes);
+    void *stg = ensure_staging(ctx, bytes);
+    hip_check(hipMemcpyAsync(stg, w->data, bytes, hipMemcpyHostToDevice, ctx->stream), "weight upload");
+    int4_repack_launch(static_cast<const uint8_t *>(stg), e->i4, e->dptr, ctx->stream);
+    sync(ctx);  // host storage need only stay valid during acquisition
+  } catch (...) {
+    if (e->dptr) (void)hipFree(e->dptr);
+    delete e;
+    throw;
+  }
+  return insert(ctx, e);
+}
+
+// GGUF matrix [rows, cols] elements -> tiled device copy.
+WeightEntry *acquire_gguf(qnn_ctx_s *ctx, const qnn_weight *w, int rows, int cols) {
+  check_weight_desc(w);
+  const uint64_t bytes = gguf_weight_bytes(w, rows, cols);
+  const std::string key = weight_key("gg", w, bytes);
+  if (auto *e = lookup(ctx, key)) return e;
+  begin_miss(ctx);
+  auto *e = new WeightEntry();
+  e->key = key;
+  e->kind = WKind::Gguf;
+  e->gg = gguf_layout(w->encoding, rows, cols);
+  e->bytes = e->gg.bytes();
+  e->source_bytes = bytes;
+  try {
+    e->dptr = alloc_weight(ctx, e->bytes);
+    void *stg = ensure_staging(ctx, bytes);
+    // GGUFWeightPointer (GGUF.Quantization.pas:115-121): the slice starts at
+    // the quant bytes of `offset` elements.
+    const uint8_t *src = static_cast<const uint8_t *>(w->data) +
+                         uint64_t(w->offset / gguf_block_elements(w->encoding)) * gguf_block_bytes(w->encoding);
+    hip_check(hipMemcpyAsync(stg, src, bytes, hipMemcpyHostToDevice, ctx->stream), "weight upload");
+    gguf_repack_launch(static_cast<const uint8_t *>(stg), e->gg, e->dptr, ctx->stream);
+    sync(ctx);
+  } catch (...) {
+    if (e->dptr) (void)hipFree(e->dptr);
+    delete e;
+    throw;
+  }
+  return insert(ctx, e);
+}
+
+// F32/BF16 vector (norm gamma, bias) copied as is.
+WeightEntry *acquire_raw(qnn_ctx_s *ctx, const qnn_weight *w, int64_t count) {
+  check_weight_desc(w);
+  if ((w->dtype != QNN_DT_F32 && w->dtype != QNN_DT_BF16) || w->encoding != QNN_WE_NATIVE || w->offset < 0 ||
+      count > w->size - w->offset)
+    fail(QNN_E_ARGUMENT, "vector weight must be F32 or BF16 with enough elements");
+  const int es = w->dtype == QNN_DT_F32 ? 4 : 2;
+  const uint64_t bytes = uint64_t(count) * es;
+  const std::string key = weight_key("raw", w, bytes);
+  if (auto *e = lookup(ctx, key)) return e;
+  begin_miss(ctx);
+  auto *e = new WeightEntry();
+  e->key = key;
+  e->kind = WKind::Raw;
+  e->raw_dtype = w->dtype;
+  e->bytes = (bytes + 255) & ~uint64_t(255);
+  e->source_bytes = bytes;
+  try {
+    e->dptr = alloc_weight(ctx, e->bytes);
+    hip_check(hipMemcpy(e->dptr, static_cast<const uint8_t *>(w->data) + w->offset * es, bytes, hipMemcpyHostToDevice),
+              "vector upload");
+  } catch (...) {
+    if (e->dptr) (void)hipFree(e->dptr);
+    delete e;
+    throw;
+  }
+  return insert(ctx, e);
+}
+
+// Holds entries against eviction for the duration of one call.
+struct OpPins {
+  std::vector<WeightEntry *> held;
+  ~OpPins() {
+    for (auto *e : held) e->op_pins--;
+  }
+  WeightEntry *operator()(WeightEntry *e) {
+    e->op_pins++;
+    held.push_back(e);
+    return e;
+  }
+};
+
+// ---------------------------------------------------------------- INT4 projection
+void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
+              int rows, int in_dim, int out_dim, const float *prob) {
+  const I4Layout &l = w->i4;
+  for (int r0 = 0; r0 < rows; r0 += 16) {
+    const int m = std::min(16, rows - r0);
+    I4Launch a;
+    a.nib = w->dptr;
+    a.scl = static_cast<const uint8_t *>(w->dptr) + l.nib_bytes();
+    if (w2) {
+      a.nib2 = w2->dptr;
+      a.scl2 = static_cast<const uint8_t *>(w2->dptr) + l.nib_bytes();
+    }
+    a.x = x + size_t(r0) * in_dim;
+    a.x_stride = in_dim;
+    a.y = y + size_t(r0) * out_dim;
+    a.y_stride = out_dim;
+    a.k = in_dim;
+    a.n = out_dim;
+    a.m = m;
+    a.g4 = l.g4;
+    a.tiles = mode == I4_SWIGLU ? (out_dim + 31) / 32 : l.tiles;
+    a.mode = mode;
+    a.prob = prob;
+    I4Layout plan_l = l;
+    plan_l.tiles = a.tiles;
+    int gs, slices;
+    int4_plan(plan_l, m, &gs, &slices);
+    ensure_splitk(ctx, int4_partial_floats(plan_l, m, slices), size_t(a.tiles) * kCounterStride);
+    a.partial = ctx->partial;
+    a.counters = ctx->counters;
+    int4_matvec_launch(a, gs, slices, ctx->stream);
+  }
+}
+
+}  // namespace
+}  // namespace qnn
+
+using namespace qnn;
+
+extern "C" {
+
+int qnn_last_error(char *buf, int len) {
+  const int n = int(t_last_error.size());
+  if (buf && len > 0) {
+    const int c = std::min(n, len - 1);
+    std::memcpy(buf, t_last_error.data(), c);
+    buf[c] = 0;
+  }
+  return n;
+}
+
+int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out) {
+  return guarded([&] {
+    if (!out) fail(QNN_E_ARGUMENT, "out");
+    std::lock_guard<std::mutex> g(g_lock);
+    // Context.Implementation.inc:14-17: one resident context per process.
+    if (g_ctx) fail(QNN_E_INVALID_OP, "a resident HIP context already exists");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+      (void)hipGetLastError();
+      fail(QNN_E_NOT_SUPPORTED, "no HIP device available");
+    }
+    if (device < 0 || device >= n) fail(QNN_E_ARGUMENT, "device index");
+    hip_check(hipSetDevice(device), "hipSetDevice");
+    auto *ctx = new qnn_ctx_s();
+    ctx->device = device;
+    ctx->owner = std::this_thread::get_id();
+    try {
+      hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
+      hip_check(hipMalloc(&ctx->error_flag, 256), "error word");
+      hip_check(hipMemset(ctx->error_flag, 0, 256), "error word");
+      size_t free_b = 0, total_b = 0;
+      hip_check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+      ctx->weight_limit = weight_cache_bytes ? weight_cache_bytes : uint64_t(double(free_b) * 0.85);
+    } catch (...) {
+      if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+      if (ctx->error_flag) (void)hipFree(ctx->error_flag);
+      delete ctx;
+      throw;
+    }
+    g_ctx = ctx;
+    *out = ctx;
+    return QNN_OK;
+  });
+}
+
+int qnn_ctx_destroy(qnn_ctx *ctx) {
+  return guarded([&] {
+    check_ctx(ctx);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto &g : ctx->graphs) {
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+      if (g.graph) (void)hipGraphDestroy(g.graph);
+    }
+    for (auto *s : ctx->sets) {
+      if (s->table) (void)hipFree(s->table);
+      delete s;
+    }
+    for (auto &kv : ctx->weights) {
+      (void)hipFree(kv.second->dptr);
+      delete kv.second;
+    }
+    for (auto *t : ctx->tensors) {
+      (void)hipFree(t->ptr);
+      delete t;
+    }
+    for (auto &e : ctx->events)
+      if (e) (void)hipEventDestroy(e);
+    if (ctx->partial) (void)hipFree(ctx->partial);
+    if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->work) (void)hipFree(ctx->work);
+    if (ctx->staging) (void)hipFree(ctx->staging);
+    (void)hipFree(ctx->error_flag);
+    (void)hipStreamDestroy(ctx->stream);
+    std::lock_guard<std::mutex> g(g_lock);
+    g_ctx = nullptr;
+    delete ctx;
+    return QNN_OK;
+  });
+}
+
+int qnn_get_status(qnn_ctx *ctx, qnn_status *out) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!out) fail(QNN_E_ARGUMENT, "out");
+    ctx->st.weight_bytes = ctx->weight_bytes;
+    ctx->st.weight_limit = ctx->weight_limit;
+    *out = ctx->st;
+    return QNN_OK;
+  });
+}
+
+// ---------------------------------------------------------------- tensors
+int qnn_tensor_new(qnn_ctx *ctx, int count, qnn_tensor **out) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!out) fail(QNN_E_ARGUMENT, "out");
+    *out = new_tensor(ctx, count);
+    return QNN_OK;
+  });
+}
+
+int qnn_recycle(qnn_ctx *ctx, qnn_tensor **tensor) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!tensor || !*tensor) return QNN_OK;
+    check_tensor(ctx, *tensor);
+    (*tensor)->live = false;
+    *tensor = nullptr;
+    return QNN_OK;
+  });
+}
+
+int qnn_scratch(qnn_ctx *ctx, int slot, int count, qnn_tensor **out) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (slot < 0 || slot > 3 || !out) fail(QNN_E_ARGUMENT, "Resident scratch slot");
+    if (!ctx->scratch[slot] || ctx->scratch[slot]->count < count) {
+      if (ctx->scratch[slot]) ctx->scratch[slot]->live = false;
+      ctx->scratch[slot] = new_tensor(ctx, count);
+    }
+    *out = ctx->scratch[slot];
+    return QNN_OK;
+  });
+}
+
+int qnn_upload_raw(qnn_ctx *ctx, const void *data, int count, qnn_tensor **out) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!data || !out) fail(QNN_E_ARGUMENT, "UploadRaw");
+    if (ctx->capturing) fail(QNN_E_INVALID_OP, "upload during graph capture");
+    auto *t = new_tensor(ctx, count);
+    hip_check(hipMemcpyAsync(t->ptr, data, size_t(count) * 4, hipMemcpyHostToDevice, ctx->stream), "upload");
+    sync(ctx);
+    *out = t;
+    return QNN_OK;
+  });
+}
+
+int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (count < 0) count = t ? t->count : 0;
+    check_tensor(ctx, t, count);
+    if (!dst) fail(QNN_E_ARGUMENT, "Download destination");
+    hip_check(hipMemcpyAsync(dst, t->ptr, size_t(count) * 4, hipMemcpyDeviceToHost, ctx->stream), "download");
+    int flag = 0;
+    hip_check(hipMemcpyAsync(&flag, ctx->error_flag, 4, hipMemcpyDeviceToHost, ctx->stream), "error word");
+    sync(ctx);
+    ctx->st.readbacks++;
+    if (flag) {  // Download raises on the non-finite flag (Context.Implementation.inc:747-756)
+      hip_check(hipMemsetAsync(ctx->error_flag, 0, 4, ctx->stream), "error word reset");
+      sync(ctx);
+      fail(QNN_E_INVALID_OP, "GPU produced a non-finite value");
+    }
+    return QNN_OK;
+  });
+}
+
+int qnn_copy(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, int count, int dst_offset, int src_offset) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (count < 0 || dst_offset < 0 || src_offset < 0) fail(QNN_E_ARGUMENT, "Copy span");
+    check_tensor(ctx, dst, int64_t(dst_offset) + count);
+    check_tensor(ctx, src, int64_t(src_offset) + count);
+    if (count)
+      hip_check(hipMemcpyAsync(dst->ptr + dst_offset, src->ptr + src_offset, size_t(count) * 4,
+                               hipMemcpyDeviceToDevice, ctx->stream),
+                "copy");
+    return QNN_OK;
+  });
+}
+
+int qnn_flush(qnn_ctx *ctx) {
+  return guarded([&] {
+    check_ctx(ctx);
+    sync(ctx);
+    return QNN_OK;
+  });
+}
+
+int qnn_tensor_count(const qnn_tensor *t) { return t ? t->count : -1; }
+void *qnn_tensor_device_ptr(const qnn_tensor *t) { return t ? t->ptr : nullptr; }
+
+// ---------------------------------------------------------------- residency
+static WeightEntry *acquire_matrix(qnn_ctx_s *ctx, const qnn_weight *w, int rows, int cols) {
+  check_weight_desc(w);
+  if (is_gguf(w->encoding)) return acquire_gguf(ctx, w, rows, cols);
+  if (w->dtype == QNN_DT_U8) {
+    // Native INT4: cols is the stored row width Int4RowBytes(K); recover K from shape.
+    const int k = (cols / 20) * 32;
+    if (qnn_int4_row_bytes(k) != cols) fail(QNN_E_ARGUMENT, "INT4 row width is not a multiple of 20 bytes");
+    return acquire_int4(ctx, w, rows, k);
+  }
+  fail(QNN_E_NOT_SUPPORTED, "only packed INT4 and GGUF matrices are resident in the HIP backend");
+}
+
+int qnn_retain_weight(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols) {
+  return guarded([&] {
+    check_ctx(ctx);
+    WeightEntry *e = acquire_matrix(ctx, w, rows, cols);
+    e->pins++;  // RetainWeight: never evicted while the context lives (Context.Implementation.inc:361-387)
+    return QNN_OK;
+  });
+}
+
+int qnn_preload_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, uint64_t staging_limit) {
+  return guarded([&] {
+    check_ctx(ctx);
+    (void)staging_limit;
+    if (n < 0 || (n > 0 && !ws)) fail(QNN_E_ARGUMENT, "PreloadWeights");
+    OpPins pin;
+    for (int i = 0; i < n; ++i) pin(acquire_matrix(ctx, &ws[i], int(ws[i].shape0), int(ws[i].shape1)));
+    return QNN_OK;
+  });
+}
+
+int qnn_is_weight_resident(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols, int *resident) {
+  return guarded([&] {
+    check_ctx(ctx);
+    check_weight_desc(w);
+    if (!resident) fail(QNN_E_ARGUMENT, "out");
+    std::string key;
+    if (is_gguf(w->encoding)) key = weight_key("gg", w, gguf_weight_bytes(w, rows, cols));
+    else key = weight_key("i4", w, uint64_t(rows) * cols);
+    *resident = ctx->weights.count(key) ? 1 : 0;
+    return QNN_OK;
+  });
+}
+
+int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!bytes) fail(QNN_E_ARGUMENT, "out");
+    uint64_t pinned = 0;
+    for (auto &kv : ctx->weights)
+      if (kv.second->pins) pinned += kv.second->bytes;
+    *bytes = ctx->weight_limit > pinned ? ctx->weight_limit - pinned : 0;
+    return QNN_OK;
+  });
+}
+
+// ---------------------------------------------------------------- ops
+int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
+                    int out_dim) {
+  return guarded([&] {
+    check_ctx(ctx);
+    // Int4Linear validation (Context.Implementation.inc:1091-1104).
+    if (rows < 1 || rows > 128 || in_dim < 1 || out_dim < 1 || src == dst || int64_t(rows) * out_dim > 0x7fffffff)
+      fail(QNN_E_ARGUMENT, "Invalid packed INT4 projection");
+    check_tensor(ctx, src, int64_t(rows) * in_dim);
+    check_tensor(ctx, dst, int64_t(rows) * out_dim);
+    OpPins pin;
+    WeightEntry *e = pin(acquire_int4(ctx, w, out_dim, in_dim));
+    run_int4(ctx, e, nullptr, I4_STORE, src->ptr, dst->ptr, rows, in_dim, out_dim, nullptr);
+    ctx->st.gemm_calls++;
+    ctx->st.int4_calls++;
+    return QNN_OK;
+  });
+}
+
+int qnn_int4_linear_accumulate(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, qnn_tensor *probabilities,
+                               const qnn_weight *w, int in_dim, int out_dim, int prob_index) {
+  return guarded([&] {
+    check_ctx(ctx);
+    // Int4LinearAccumulate validation (Context.Implementation.inc:1064-1068).
+    if (in_dim < 1 || out_dim < 1 || prob_index < 0 || dst == src || dst == probabilities)
+      fail(QNN_E_ARGUMENT, "Invalid accumulated INT4 vector projection");
+    check_tensor(ctx, dst, out_dim);
+    check_tensor(ctx, src, in_dim);
+    check_tensor(ctx, probabilities, int64_t(prob_index) + 1);
+    OpPins pin;
+    WeightEntry *e = pin(acquire_int4(ctx, w, out_dim, in_dim));
+    run_int4(ctx, e, nullptr, I4_ACCUM, src->ptr, dst->ptr, 1, in_dim, out_dim, probabilities->ptr + prob_index);
+    ctx->st.int4_calls++;
+    return QNN_OK;
+  });
+}
+
+int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *gate, const qnn_weight *up,
+                      int in_dim, int out_dim) {
+  return guarded([&] {
+    check_ctx(ctx);
+    check_tensor(ctx, src, in_dim);
+    check_tensor(ctx, dst, out_dim);
+    if (in_dim < 1 || out_dim < 1 || dst == src) fail(QNN_E_ARGUMENT, "Invalid fused SwiGLU dimensions");
+    check_weight_desc(gate);
+    check_weight_desc(up);
+    const bool gg = is_gguf(gate->encoding) && is_gguf(up->encoding);
+    const bool i4 = gate->dtype == QNN_DT_U8 && up->dtype == QNN_DT_U8 && gate->encoding == QNN_WE_NATIVE &&
+                    up->encoding == QNN_WE_NATIVE;
+    // Implementation.inc:1017-1022: any other mix is not handled here.
+    if (!gg && !i4) return QNN_NOT_HANDLED;
+    const int width = i4 ? qnn_int4_row_bytes(in_dim) : in_dim;
+    if (gate->shape0 != out_dim || up->shape0 != out_dim || gate->shape1 != width || up->shape1 != width)
+      fail(QNN_E_ARGUMENT, "Invalid fused SwiGLU weight shape");
+    uint64_t pair = i4 ? uint64_t(2) * out_dim * width
+                       : gguf_weight_bytes(gate, out_dim, in_dim) + gguf_weight_bytes(up, out_dim, in_dim);
+    uint64_t capacity = 0;
+    qnn_weight_batch_capacity(ctx, &capacity);
+    if (pair > capacity) {  // Implementation.inc:1033-1034
+      int ra = 0, rb = 0;
+      qnn_is_weight_resident(ctx, gate, out_dim, width, &ra);
+      qnn_is_weight_resident(ctx, up, out_dim, width, &rb);
+      if (!(ra && rb)) return QNN_NOT_HANDLED;
+    }
+    OpPins pin;
+    if (i4) {
+      WeightEntry *eg = pin(acquire_int4(ctx, gate, out_dim, in_dim));
+      WeightEntry *eu = pin(acquire_int4(ctx, up, out_dim, in_dim));
+      run_int4(ctx, eg, eu, I4_SWIGLU, src->ptr, dst->ptr, 1, in_dim, out_dim, nullptr);
+      ctx->st.int4_calls += 2;
+    } else {
+      fail(QNN_E_NOT_SUPPORTED, "GGUF fused SwiGLU not built yet");
+    }
+    ctx->st.gemm_calls += 2;
+    return QNN_OK;
+  });
+}
+
+int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,
+               const qnn_weight *bias, int rows, int in_dim, int out_dim) {
+  return guarded([&] {
+    check_ctx(ctx);
+    check_tensor(ctx, src, int64_t(rows) * in_dim);
+    check_tensor(ctx, dst, int64_t(rows) * out_dim);
+    if (rows < 1 || in_dim < 1 || out_dim < 1 || src == dst)
+      fail(QNN_E_ARGUMENT, "Invalid resident linear dimensions/alias");
+    (void)scales;
+    (void)bias;
+    check_weight_desc(w);
+    fail(QNN_E_NOT_SUPPORTED, "GGUF projections not built yet");
+    return QNN_OK;
+  });
+}
+
+int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_tensor *b, qnn_tensor *c,
+               const int *args, int nargs) {
+  return guarded([&] {
+    check_ctx(ctx);
+    auto arg = [&](int i) -> int {
+      if (i >= nargs || !args) fail(QNN_E_ARGUMENT, "missing kernel argument");
+      return args[i];
+    };
+    if (n < 0) fail(QNN_E_ARGUMENT, "kernel element count");
+    switch (op) {
+      case QNN_GO_FILL:
+        check_tensor(ctx, dst, n);
+        if (n) misc_fill(dst->ptr, n, uint32_t(arg(0)), ctx->stream);
+        return QNN_OK;
+      case QNN_GO_ADD: {
+        const int cols = arg(0), stride = arg(1), doff = arg(3), soff = arg(4);
+        float alpha;
+        const int bits = arg(2);
+        std::memcpy(&alpha, &bits, 4);
+        if (cols < 1 || stride < cols || doff < 0 || soff < 0) fail(QNN_E_ARGUMENT, "GO_ADD geometry");
+        check_tensor(ctx, a, int64_t(soff) + n);
+        const int64_t rows = (int64_t(n) + cols - 1) / cols;
+        check_tensor(ctx, dst, doff + (rows - 1) * stride + cols);
+        if (n) misc_add(dst->ptr, a->ptr, n, cols, stride, alpha, doff, soff, ctx->stream);
+        return QNN_OK;
+      }
+      case QNN_GO_SWIGLU:
+      case QNN_GO_GEGLU: {
+        const int inter = arg(0), inter_leaved = op == QNN_GO_SWIGLU ? arg(1) : 0;
+        if (inter < 1) fail(QNN_E_ARGUMENT, "GLU width");
+        check_tensor(ctx, dst, n);
+        check_tensor(ctx, a, inter_leaved ? int64_t(n) * 2 : n);
+        if (!inter_leaved) check_tensor(ctx, b, n);
+        if (n) misc_glu(dst->ptr, a->ptr, inter_leaved ? nullptr : b->ptr, n, inter, inter_leaved,
+                        op == QNN_GO_GEGLU, ctx->stream);
+        return QNN_OK;
+      }
+      case QNN_GO_FINITE:
+        check_tensor(ctx, a ? a : dst, n);
+        if (n) misc_finite((a ? a : dst)->ptr, n, ctx->error_flag, ctx->stream);
+        return QNN_OK;
+      case QNN_GO_MOE_ROUTE: {
+        const int rows = arg(0), experts = arg(1), k = arg(2), norm = arg(3);
+        if (rows < 1 || experts < 1 || experts > 8192 || k < 1 || k > 64 || k > experts)
+          fail(QNN_E_ARGUMENT, "GO_MOE_ROUTE geometry");
+        check_tensor(ctx, a, int64_t(rows) * experts);
+        check_tensor(ctx, dst, int64_t(rows) * k * 2);
+        misc_moe_route(dst->ptr, a->ptr, rows, experts, k, norm, ctx->stream);
+        ctx->st.moe_calls++;
+        return QNN_OK;
+      }
+      case QNN_GO_MOE_GATHER: {
+        const int hidden = arg(0), topk = arg(1), offset = arg(2);
+        if (hidden < 1 || topk < 1 || offset < 0) fail(QNN_E_ARGUMENT, "GO_MOE_GATHER geometry");
+        check_tensor(ctx, dst, n);
+        check_tensor(ctx, b, int64_t(offset) + (n + hidden - 1) / hidden);
+        check_tensor(ctx, a, 1);
+        if (n) misc_moe_gather(dst->ptr, a->ptr, b->ptr, n, hidden, topk, offset, ctx->stream);
+        return QNN_OK;
+      }
+      case QNN_GO_MOE_SCATTER: {
+        const int hidden = arg(0), topk = arg(1), offset = arg(2), route = arg(3), single = arg(4), pbase = arg(5);
+        if (hidden < 1 || topk < 1 || offset < 0 || pbase < 0) fail(QNN_E_ARGUMENT, "GO_MOE_SCATTER geometry");
+        check_tensor(ctx, a, n);
+        check_tensor(ctx, dst, 1);
+        check_tensor(ctx, c, int64_t(pbase) + 1);
+        if (!single) check_tensor(ctx, b, int64_t(offset) + (n + hidden - 1) / hidden);
+        if (n)
+          misc_moe_scatter(dst->ptr, a->ptr, single ? nullptr : b->ptr, c->ptr, n, hidden, topk, offset, route,
+                           single, pbase, ctx->stream);
+        return QNN_OK;
+      }
+    }
+    fail(QNN_E_NOT_SUPPORTED, "op code not implemented by the HIP backend");
+    return QNN_OK;
+  });
+}
+
+int qnn_kernel_weights(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, const qnn_weight *b,
+                       const qnn_weight *c, const int *args, int nargs) {
+  return guarded([&] {
+    check_ctx(ctx);
+    (void)n;
+    if (op != QNN_GO_NORM) fail(QNN_E_NOT_SUPPORTED, "KernelWeights op not implemented by the HIP backend");
+    if (!args || nargs < 8) fail(QNN_E_ARGUMENT, "GO_NORM needs 8 arguments");
+    const int rows = args[0], dim = args[1], flags = args[2], soff = args[5], unit = args[6], epsb = args[7];
+    if (rows < 1 || dim < 1 || soff < 0 || (flags & 2)) fail(QNN_E_ARGUMENT, "GO_NORM geometry (CHW layout not supported)");
+    float eps = 1e-6f;
+    if (epsb) std::memcpy(&eps, &epsb, 4);
+    check_tensor(ctx, a, int64_t(soff) + int64_t(rows) * dim);
+    check_tensor(ctx, dst, int64_t(soff) + int64_t(rows) * dim);
+    OpPins pin;
+    const void *gp = nullptr, *bp = nullptr;
+    int gbf = 0, bbf = 0;
+    if (!unit) {
+      WeightEntry *g = pin(acquire_raw(ctx, b, dim));
+      gp = g->dptr;
+      gbf = g->raw_dtype == QNN_DT_BF16;
+    }
+    if ((flags & 1) && !(flags & 8)) {
+      WeightEntry *be = pin(acquire_raw(ctx, c, dim));
+      bp = be->dptr;
+      bbf = be->raw_dtype == QNN_DT_BF16;
+    }
+    misc_norm(dst->ptr, a->ptr, gp, gbf, bp, bbf, rows, dim, flags, soff, unit, eps, ctx->stream);
+    return QNN_OK;
+  });
+}
+
+int qnn_check_finite(qnn_ctx *ctx, qnn_tensor *t, int count) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (count < 0) count = t ? t->count : 0;
+    check_tensor(ctx, t, count);
+    if (count) misc_finite(t->ptr, count, ctx->error_flag, ctx->stream);
+    return QNN_OK;
+  });
+}
+
+int qnn_dequantize(qnn_ctx *ctx, qnn_tensor *dst, const qnn_weight *w, int rows, int cols) {
+  return guarded([&] {
+    check_ctx(ctx);
+    check_weight_desc(w);
+    check_tensor(ctx, dst, int64_t(rows) * cols);
+    OpPins pin;
+    if (is_gguf(w->encoding)) {
+      WeightEntry *e = pin(acquire_gguf(ctx, w, rows, cols));
+      gguf_dequant_launch(e->gg, e->dptr, dst->ptr, ctx->stream);
+    } else {
+      WeightEntry *e = pin(acquire_int4(ctx, w, rows, cols));
+      I4Layout l = e->i4;  // the resident layout depends on the group count only
+      l.cols = cols;
+      int4_dequant_launch(l, e->dptr, dst->ptr, ctx->stream);
+    }
+    return QNN_OK;
+  });
+}
+
+// ---------------------------------------------------------------- routed experts
+int qnn_expert_set_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight *up, const qnn_weight *down,
+                          int experts, int hidden, int inter, qnn_expert_set **out) {
+  return guarded([&] {
+    check_ctx(ctx);
+    (void)gate; (void)up; (void)down; (void)experts; (void)hidden; (void)inter; (void)out;
+    fail(QNN_E_NOT_SUPPORTED, "routed experts not built yet");
+    return QNN_OK;
+  });
+}
+
+int qnn_expert_set_destroy(qnn_ctx *ctx, qnn_expert_set *set) {
+  return guarded([&] {
+    check_ctx(ctx);
+    (void)set;
+    return QNN_OK;
+  });
+}
+
+int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tensor *src, qnn_tensor *routes, int rows,
+                    int topk) {
+  return guarded([&] {
+    check_ctx(ctx);
+    (void)set; (void)dst; (void)src; (void)routes; (void)rows; (void)topk;
+    fail(QNN_E_NOT_SUPPORTED, "routed experts not built yet");
+    return QNN_OK;
+  });
+}
+
+// ---------------------------------------------------------------- timing / graphs
+int qnn_event_record(qnn_ctx *ctx, int slot) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (slot < 0 || slot >= 64) fail(QNN_E_ARGUMENT, "event slot");
+    if (!ctx->events[slot]) hip_check(hipEventCreate(&ctx->events[slot]), "hipEventCreate");
+    hip_check(hipEventRecord(ctx->events[slot], ctx->stream), "hipEventRecord");
+    return QNN_OK;
+  });
+}
+
+int qnn_event_elapsed_ms(qnn_ctx *ctx, int a, int b, float *ms) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (a < 0 || a >= 64 || b < 0 || b >= 64 || !ctx->events[a] || !ctx->events[b] || !ms)
+      fail(QNN_E_ARGUMENT, "event slots");
+    hip_check(hipEventSynchronize(ctx->events[b]), "hipEventSynchronize");
+    hip_check(hipEventElapsedTime(ms, ctx->events[a], ctx->events[b]), "hipEventElapsedTime");
+    return QNN_OK;
+  });
+}
+
+int qnn_graph_begin(qnn_ctx *ctx) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (ctx->capturing) fail(QNN_E_INVALID_OP, "capture already active");
+    hip_check(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+    ctx->capturing = true;
+    ctx->capture_pins.clear();
+    return QNN_OK;
+  });
+}
+
+int qnn_graph_end(qnn_ctx *ctx, int *graph_id) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!ctx->capturing) fail(QNN_E_INVALID_OP, "no capture active");
+    GraphRec g;
+    ctx->capturing = false;
+    const hipError_t ec = hipStreamEndCapture(ctx->stream, &g.graph);
+    if (ec != hipSuccess) {
+      for (auto *e : ctx->capture_pins) e->pins--;
+      ctx->capture_pins.clear();
+      hip_check(ec, "hipStreamEndCapture");
+    }
+    hip_check(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    g.pinned = ctx->capture_pins;  // weights a graph reads stay resident
+    ctx->capture_pins.clear();
+    ctx->graphs.push_back(g);
+    if (graph_id) *graph_id = int(ctx->graphs.size()) - 1;
+    return QNN_OK;
+  });
+}
+
+int qnn_graph_launch(qnn_ctx *ctx, int graph_id) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (graph_id < 0 || graph_id >= int(ctx->graphs.size())) fail(QNN_E_ARGUMENT, "graph id");
+    hip_check(hipGraphLaunch(ctx->graphs[graph_id].exec, ctx->stream), "hipGraphLaunch");
+    return QNN_OK;
+  });
+}
+
+void *qnn_stream(qnn_ctx *ctx) { return ctx ? ctx->stream : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,173 @@
+// qnn_internal.h -- shared declarations of libqnn_hip.so (host + kernels).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <list>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/qnn_hip.h"
+
+namespace qnn {
+
+// Error carrying one of the QNN_E_* codes; converted to a status at the C ABI.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+[[noreturn]] inline void fail(int code, const std::string &msg) { throw Error(code, msg); }
+inline void hip_check(hipError_t e, const char *what) {
+  if (e != hipSuccess) fail(QNN_E_INVALID_OP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------------------
+// Device layouts
+// ---------------------------------------------------------------------------
+// Native INT4 tiled layout.  A packed INT4 matrix [N][G*20 B] (G = ceil(K/32)
+// groups of fp32 scale + 16 nibble bytes) is stored as tiles of 64 rows, one
+// row per lane of a wavefront:
+//   nibble plane: 16 B at ((t*g4 + g)*64 + r)       -- group g of row r of tile t
+//   scale plane:  16 B at ((t*(g4/4) + g/4)*64 + r)  -- scales of groups 4q..4q+3
+// g4 = G rounded up to a multiple of 4.  Padding rows/groups carry nibble 8 and
+// scale 0 (value 0).  The fused gate/up kernel reads two such matrices: lanes
+// 0-31 stream 32 gate rows and lanes 32-63 the same 32 up rows.
+struct I4Layout {
+  int rows = 0, cols = 0, groups = 0, g4 = 0, tiles = 0;
+  size_t nib_bytes() const { return size_t(tiles) * g4 * 64 * 16; }
+  size_t scale_bytes() const { return size_t(tiles) * g4 * 64 * 4; }
+  size_t bytes() const { return nib_bytes() + scale_bytes(); }
+};
+
+// GGUF tiled layout: tiles of 64 rows, one row per lane; the 16-byte-aligned
+// "main" part of each super-block and its small side fields are stored as
+// lane-interleaved planes (see qnn_gguf.hip).
+struct GGLayout {
+  int enc = 0, rows = 0, cols = 0, blocks = 0, tiles = 0;  // blocks per row
+  int main_chunks = 0;  // 16-B chunks of the main plane per (row, block)
+  int side_bytes = 0;   // bytes of the side plane per (row, block)
+  size_t main_bytes() const { return size_t(tiles) * blocks * main_chunks * 64 * 16; }
+  size_t side_plane_bytes() const { return size_t(tiles) * blocks * 64 * side_bytes; }
+  size_t bytes() const { return main_bytes() + ((side_plane_bytes() + 255) & ~size_t(255)); }
+};
+
+enum class WKind { Int4, Gguf, Raw };
+
+struct WeightEntry {
+  std::string key;
+  WKind kind = WKind::Raw;
+  void *dptr = nullptr;
+  size_t bytes = 0;        // device bytes held
+  size_t source_bytes = 0; // algorithmic (host) bytes
+  int pins = 0;            // RetainWeight / graph references: never evicted
+  int op_pins = 0;         // held during one call's acquisitions
+  uint64_t last_use = 0;
+  int raw_dtype = 0;       // Raw: dtype of the copied vector
+  I4Layout i4;
+  GGLayout gg;
+};
+
+struct Tensor {
+  float *ptr = nullptr;
+  int count = 0;
+  size_t capacity = 0;
+  bool live = false;
+};
+
+// ---------------------------------------------------------------------------
+// Kernel launchers (device code in qnn_int4.hip / qnn_misc.hip / ...)
+// ---------------------------------------------------------------------------
+enum I4Mode { I4_STORE = 0, I4_ACCUM = 1, I4_SWIGLU = 2 };
+
+// Split-K tickets sit 256 bytes apart: atomics on one cache line serialise in
+// a single L2 channel (about 16 ns each), so neighbouring tiles must not share.
+constexpr int kCounterStride = 64;
+
+struct I4Launch {
+  const void *nib = nullptr;   // tiled nibble plane (gate in I4_SWIGLU mode)
+  const void *scl = nullptr;   // tiled scale plane
+  const void *nib2 = nullptr;  // I4_SWIGLU: up matrix planes (same layout)
+  const void *scl2 = nullptr;
+  const float *x = nullptr;
+  int x_stride = 0;  // floats between activation rows
+  float *y = nullptr;
+  int y_stride = 0;
+  int k = 0, n = 0, m = 1;  // input features, valid output rows, tokens (<= 16)
+  int tiles = 0, g4 = 0;    // wave tiles (64 output rows; 32 in I4_SWIGLU mode), groups/4*4
+  int mode = I4_STORE;
+  const float *prob = nullptr;  // I4_ACCUM: pointer to p
+  float *partial = nullptr;     // split-K scratch
+  unsigned *counters = nullptr;
+};
+// Chooses the split-K slice and returns (partial floats, counters) needed.
+void int4_plan(const I4Layout &l, int m, int *gs, int *slices);
+size_t int4_partial_floats(const I4Layout &l, int m, int slices);
+void int4_matvec_launch(const I4Launch &a, int gs, int slices, hipStream_t s);
+void int4_repack_launch(const uint8_t *src, const I4Layout &l, void *dst, hipStream_t s);
+I4Layout int4_layout(int rows, int cols);
+void int4_dequant_launch(const I4Layout &l, const void *w, float *out, hipStream_t s);
+
+void misc_fill(float *dst, int n, uint32_t bits, hipStream_t s);
+void misc_add(float *dst, const float *a, int n, int cols, int dst_stride, float alpha, int dst_off, int src_off,
+              hipStream_t s);
+void misc_glu(float *dst, const float *a, const float *b, int n, int inter, int interleaved, int gelu,
+              hipStream_t s);
+void misc_finite(const float *a, int n, int *flag, hipStream_t s);
+void misc_norm(float *dst, const float *a, const void *gamma, int gamma_bf16, const void *beta, int beta_bf16,
+               int rows, int dim, int flags, int src_off, int unit_gamma, float eps, hipStream_t s);
+void misc_moe_route(float *routes, const float *logits, int rows, int experts, int k, int normalize,
+                    hipStream_t s);
+void misc_moe_gather(float *dst, const float *src, const float *indices, int n, int hidden, int topk, int offset,
+                     hipStream_t s);
+void misc_moe_scatter(float *dst, const float *y, const float *indices, const float *routes, int n, int hidden,
+                      int topk, int offset, int route_index, int single_row, int prob_base, hipStream_t s);
+void misc_bias_add(float *dst, const void *bias, int bias_bf16, int rows, int cols, hipStream_t s);
+
+// Device-side routed experts (qnn_moe.hip).
+struct MoELaunch {
+  const uint64_t *gateup_table = nullptr;  // per expert: device address of the paired gate/up tiles
+  const uint64_t *down_table = nullptr;    // per expert: device address of the down tiles
+  int experts = 0, hidden = 0, inter = 0, topk = 0, rows = 0;
+  I4Layout gu, dn;                          // layouts shared by every expert
+  const float *x = nullptr;                 // [rows][hidden]
+  const float *routes = nullptr;            // [rows*topk ids][rows*topk probs]
+  float *out = nullptr;                     // [rows][hidden]
+  // workspace
+  int *plan = nullptr;          // see qnn_moe.hip
+  float *h = nullptr;           // [rows*topk][inter]
+  float *y = nullptr;           // [rows*topk][hidden]
+  float *partial = nullptr;
+  unsigned *counters = nullptr;
+};
+size_t moe_workspace_bytes(const MoELaunch &a, size_t *plan_off, size_t *h_off, size_t *y_off, size_t *part_off,
+                           size_t *cnt_off);
+void moe_launch(const MoELaunch &a, hipStream_t s);
+
+// GGUF (qnn_gguf.hip).
+GGLayout gguf_layout(int enc, int rows, int cols);
+void gguf_repack_launch(const uint8_t *src, const GGLayout &l, void *dst, hipStream_t s);
+void gguf_dequant_launch(const GGLayout &l, const void *w, float *out, hipStream_t s);
+struct GGLaunch {
+  const void *w = nullptr;
+  const float *x = nullptr;
+  int x_stride = 0;
+  float *y = nullptr;
+  int y_stride = 0;
+  int m = 1;
+  float *partial = nullptr;
+  unsigned *counters = nullptr;
+};
+void gguf_plan(const GGLayout &l, int m, int *bs, int *slices);
+size_t gguf_partial_floats(const GGLayout &l, int m, int slices);
+void gguf_matvec_launch(const GGLayout &l, const GGLaunch &a, int bs, int slices, hipStream_t s);
+
+// Q8_0 GEMM (qnn_gemm.hip).
+size_t q8_act_bytes(int m, int k);
+void q8_act_quant_launch(const float *a, int m, int k, void *act, hipStream_t s);
+void q8_gemm_launch(const GGLayout &l, const void *w, const void *act, int m, float *c, hipStream_t s);
+
+}  // namespace qnn

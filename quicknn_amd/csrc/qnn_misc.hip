@@ -1,0 +1,265 @@
+// qnn_misc.hip -- small ops on the decode path: fill, add, SwiGLU/GEGLU,
+// finite check, RMS/LayerNorm, MoE route, gather and scatter.  Semantics
+// follow the Vulkan shaders cited per kernel.
+#include "qnn_internal.h"
+
+namespace qnn {
+namespace {
+
+__device__ __forceinline__ float silu_dev(float x) {  // tensor.comp:22
+  return x >= 20.0f ? x : (x <= -20.0f ? 0.0f : x / (1.0f + expf(-x)));
+}
+__device__ __forceinline__ float gelu_dev(float x) {  // tensor.comp:23 (tanh approximation)
+  return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+}
+__device__ __forceinline__ float load_vec(const void *p, int bf16, int i) {
+  if (bf16) return __uint_as_float(uint32_t(static_cast<const uint16_t *>(p)[i]) << 16);
+  return static_cast<const float *>(p)[i];
+}
+
+__global__ void k_fill(float *dst, int n, uint32_t bits) {  // tensor.comp:219 (GO_FILL)
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = __uint_as_float(bits);
+}
+
+// GO_ADD (tensor.comp:221): dst[doff + r*stride + j] += alpha * a[soff + id], r = id / cols.
+__global__ void k_add(float *dst, const float *a, int n, int cols, int stride, float alpha, int doff, int soff) {
+  int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  int r = id / cols, j = id % cols;
+  size_t t = size_t(doff) + size_t(r) * stride + j;
+  dst[t] = dst[t] + alpha * a[soff + id];
+}
+
+// GO_SWIGLU / GO_GEGLU (tensor.comp:228).
+__global__ void k_glu(float *dst, const float *a, const float *b, int n, int inter, int interleaved, int gelu) {
+  int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  if (interleaved) {
+    int r = id / inter, j = id % inter;
+    dst[id] = silu_dev(a[size_t(r) * 2 * inter + j]) * a[size_t(r) * 2 * inter + inter + j];
+  } else {
+    dst[id] = (gelu ? gelu_dev(a[id]) : silu_dev(a[id])) * b[id];
+  }
+}
+
+// GO_FINITE (tensor.comp:235): OR 1 into the error word on NaN/Inf.
+__global__ void k_finite(const float *a, int n, int *flag) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  bool bad = false;
+  if (i < n) {
+    float x = a[i];
+    bad = isnan(x) || isinf(x);
+  }
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
+// GO_NORM (tensor.comp:63-73), row-major rows: optional mean subtraction
+// (flags&1), x*inversesqrt(mean(x^2)+eps)*(gamma|1 [+1 if flags&4]) [+beta].
+__global__ __launch_bounds__(256) void k_norm(float *dst, const float *a, const void *gamma, int gamma_bf16,
+                                              const void *beta, int beta_bf16, int dim, int flags, int soff,
+                                              int unit_gamma, float eps) {
+  __shared__ float red[256];
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const float *x = a + soff + size_t(row) * dim;
+  auto sum_group = [&](float v) {
+    red[lane] = v;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if (lane < s) red[lane] += red[lane + s];
+      __syncthreads();
+    }
+    float r = red[0];
+    __syncthreads();
+    return r;
+  };
+  float mean = 0.0f, part = 0.0f;
+  if (flags & 1) {
+    for (int j = lane; j < dim; j += 256) part += x[j];
+    mean = sum_group(part) / float(dim);
+  }
+  part = 0.0f;
+  for (int j = lane; j < dim; j += 256) {
+    float v = x[j] - mean;
+    part += v * v;
+  }
+  const float squares = sum_group(part);
+  const float inv = rsqrtf(squares / float(dim) + eps);
+  for (int j = lane; j < dim; j += 256) {
+    float scale = (unit_gamma ? 1.0f : load_vec(gamma, gamma_bf16, j)) + ((flags & 4) ? 1.0f : 0.0f);
+    float b = ((flags & 1) && !(flags & 8) && beta) ? load_vec(beta, beta_bf16, j) : 0.0f;
+    dst[soff + size_t(row) * dim + j] = (x[j] - mean) * inv * scale + b;
+  }
+}
+
+// GO_MOE_ROUTE (moe.comp:25-50): fp32 softmax, exact top-k with ties to the
+// lower id, optional renormalisation by the rank-ordered top-k sum.  Ranking
+// uses the logits (softmax is monotone), which keeps the selection identical
+// to the CPU oracle regardless of exp() rounding.  One block per token row.
+__global__ __launch_bounds__(256) void k_moe_route(float *routes, const float *logits, int rows, int experts, int k,
+                                                   int normalize) {
+  extern __shared__ float sh[];  // experts floats of probabilities + 2*256 scratch
+  float *prob = sh;
+  float *rv = sh + experts;
+  int *ri = reinterpret_cast<int *>(rv + 256);
+  __shared__ int top_ids[64];
+  __shared__ float top_p[64];
+  __shared__ float top_total;
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const float *l = logits + size_t(row) * experts;
+  float mx = -3.402823466e38f;
+  for (int e = lane; e < experts; e += 256) mx = fmaxf(mx, l[e]);
+  rv[lane] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (lane < s) rv[lane] = fmaxf(rv[lane], rv[lane + s]);
+    __syncthreads();
+  }
+  const float maximum = rv[0];
+  __syncthreads();
+  float part = 0.0f;
+  for (int e = lane; e < experts; e += 256) {
+    float v = expf(l[e] - maximum);
+    prob[e] = v;
+    part += v;
+  }
+  rv[lane] = part;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (lane < s) rv[lane] += rv[lane + s];
+    __syncthreads();
+  }
+  const float denominator = rv[0];
+  __syncthreads();
+  for (int e = lane; e < experts; e += 256) prob[e] = prob[e] / denominator;
+  __syncthreads();
+  // k rounds of (logit desc, id asc) argmax over the not-yet-taken experts.
+  for (int rank = 0; rank < k; ++rank) {
+    float best = -INFINITY;
+    int best_id = 0x7fffffff;
+    for (int e = lane; e < experts; e += 256) {
+      bool taken = false;
+      for (int t = 0; t < rank; ++t) taken |= (top_ids[t] == e);
+      float v = l[e];
+      if (!taken && (best_id == 0x7fffffff || v > best || (v == best && e < best_id))) {
+        best = v;
+        best_id = e;
+      }
+    }
+    rv[lane] = best;
+    ri[lane] = best_id;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if (lane < s) {
+        float ov = rv[lane + s];
+        int oi = ri[lane + s];
+        bool better = (oi != 0x7fffffff) &&
+                      (ri[lane] == 0x7fffffff || ov > rv[lane] || (ov == rv[lane] && oi < ri[lane]));
+        if (better) {
+          rv[lane] = ov;
+          ri[lane] = oi;
+        }
+      }
+      __syncthreads();
+    }
+    if (lane == 0) {
+      top_ids[rank] = ri[0];
+      top_p[rank] = prob[ri[0]];
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+    float total = 0.0f;
+    for (int r = 0; r < k; ++r) total += top_p[r];
+    top_total = total;
+  }
+  __syncthreads();
+  if (lane < k) {
+    const int target = row * k + lane;
+    routes[target] = __uint_as_float(uint32_t(top_ids[lane]));
+    routes[size_t(rows) * k + target] = normalize ? top_p[lane] / top_total : top_p[lane];
+  }
+}
+
+// GO_MOE_GATHER (moe.comp:124).
+__global__ void k_moe_gather(float *dst, const float *src, const float *indices, int n, int hidden, int topk,
+                             int offset) {
+  int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  int r = id / hidden, j = id % hidden;
+  uint32_t route = __float_as_uint(indices[offset + r]);
+  dst[id] = src[size_t(route / topk) * hidden + j];
+}
+
+// GO_MOE_SCATTER (moe.comp:125-126).
+__global__ void k_moe_scatter(float *dst, const float *y, const float *indices, const float *routes, int n,
+                              int hidden, int topk, int offset, int route_index, int single_row, int prob_base) {
+  int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  int r = id / hidden, j = id % hidden;
+  uint32_t route = single_row ? uint32_t(route_index) : __float_as_uint(indices[offset + r]);
+  size_t target = size_t(route / topk) * hidden + j;
+  dst[target] = dst[target] + y[id] * routes[prob_base + route];
+}
+
+// Bias after a projection (GO_CONV_OUTPUT with bias in Linear, Implementation.inc:848-849, :892-893).
+__global__ void k_bias_add(float *dst, const void *bias, int bf16, int rows, int cols) {
+  int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= rows * cols) return;
+  dst[id] = dst[id] + load_vec(bias, bf16, id % cols);
+}
+
+inline int blocks(long long n, int t) { return int((n + t - 1) / t); }
+
+}  // namespace
+
+void misc_fill(float *dst, int n, uint32_t bits, hipStream_t s) {
+  hipLaunchKernelGGL(k_fill, dim3(blocks(n, 256)), dim3(256), 0, s, dst, n, bits);
+  hip_check(hipGetLastError(), "fill");
+}
+void misc_add(float *dst, const float *a, int n, int cols, int dst_stride, float alpha, int dst_off, int src_off,
+              hipStream_t s) {
+  hipLaunchKernelGGL(k_add, dim3(blocks(n, 256)), dim3(256), 0, s, dst, a, n, cols, dst_stride, alpha, dst_off,
+                     src_off);
+  hip_check(hipGetLastError(), "add");
+}
+void misc_glu(float *dst, const float *a, const float *b, int n, int inter, int interleaved, int gelu,
+              hipStream_t s) {
+  hipLaunchKernelGGL(k_glu, dim3(blocks(n, 256)), dim3(256), 0, s, dst, a, b, n, inter, interleaved, gelu);
+  hip_check(hipGetLastError(), "glu");
+}
+void misc_finite(const float *a, int n, int *flag, hipStream_t s) {
+  hipLaunchKernelGGL(k_finite, dim3(blocks(n, 256)), dim3(256), 0, s, a, n, flag);
+  hip_check(hipGetLastError(), "finite");
+}
+void misc_norm(float *dst, const float *a, const void *gamma, int gamma_bf16, const void *beta, int beta_bf16,
+               int rows, int dim, int flags, int src_off, int unit_gamma, float eps, hipStream_t s) {
+  hipLaunchKernelGGL(k_norm, dim3(rows), dim3(256), 0, s, dst, a, gamma, gamma_bf16, beta, beta_bf16, dim, flags,
+                     src_off, unit_gamma, eps);
+  hip_check(hipGetLastError(), "norm");
+}
+void misc_moe_route(float *routes, const float *logits, int rows, int experts, int k, int normalize,
+                    hipStream_t s) {
+  size_t shmem = size_t(experts) * 4 + 256 * 8;
+  hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(256), shmem, s, routes, logits, rows, experts, k, normalize);
+  hip_check(hipGetLastError(), "moe route");
+}
+void misc_moe_gather(float *dst, const float *src, const float *indices, int n, int hidden, int topk, int offset,
+                     hipStream_t s) {
+  hipLaunchKernelGGL(k_moe_gather, dim3(blocks(n, 256)), dim3(256), 0, s, dst, src, indices, n, hidden, topk,
+                     offset);
+  hip_check(hipGetLastError(), "moe gather");
+}
+void misc_moe_scatter(float *dst, const float *y, const float *indices, const float *routes, int n, int hidden,
+                      int topk, int offset, int route_index, int single_row, int prob_base, hipStream_t s) {
+  hipLaunchKernelGGL(k_moe_scatter, dim3(blocks(n, 256)), dim3(256), 0, s, dst, y, indices, routes, n, hidden, topk,
+                     offset, route_index, single_row, prob_base);
+  hip_check(hipGetLastError(), "moe scatter");
+}
+void misc_bias_add(float *dst, const void *bias, int bias_bf16, int rows, int cols, hipStream_t s) {
+  hipLaunchKernelGGL(k_bias_add, dim3(blocks((long long)rows * cols, 256)), dim3(256), 0, s, dst, bias, bias_bf16,
+                     rows, cols);
+  hip_check(hipGetLastError(), "bias add");
+}
+
+}  // namespace qnn

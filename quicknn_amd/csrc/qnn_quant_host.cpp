@@ -1,0 +1,284 @@
+// qnn_quant_host.cpp -- host-side weight preparation.
+//
+//  * qnn_quantize_int4: QuickNN's INT4 packer (QuantizeInt4,
+//    src/core/QuickNN.Quantization.Int4.pas:35-144): per group of 32, scale =
+//    max|v|/7, q = Round(v/scale) clamped to [-7,7] (half-to-even), one
+//    least-squares refit scale = sum(v*q)/sum(q*q) in double, stored as fp32,
+//    then nibbles q+8 from the refitted scale; tail elements store 8.
+//  * qnn_gguf_quantize: block encoders for synthetic GGML weights.  The
+//    reference ships no GGUF quantizer; these produce valid blocks of the
+//    layouts its decoders read (src/io/QuickNN.GGUF.Quantization.pas:136-253).
+#include <algorithm>
+#include <atomic>
+#include <cfenv>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "../../include/qnn_hip.h"
+
+namespace {
+
+float f32_from_bits(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
+uint32_t bits_from_f32(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
+
+// binary32 -> binary16, round to nearest even.
+uint16_t to_half(float f) {
+  uint32_t x = bits_from_f32(f);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return uint16_t(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0));
+  if (ax >= 0x477ff000u) return uint16_t(sign | 0x7c00u);  // rounds to >= 65520 -> inf
+  if (ax < 0x38800000u) {                                   // subnormal half
+    float a = f32_from_bits(ax);
+    uint32_t m = uint32_t(std::nearbyint(a * 16777216.0f));  // a / 2^-24
+    return uint16_t(sign | m);
+  }
+  uint32_t e = (ax >> 23) - 112;
+  uint32_t man = ax & 0x7fffffu;
+  uint32_t h = (e << 10) | (man >> 13);
+  uint32_t rest = man & 0x1fffu;
+  if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;
+  return uint16_t(sign | h);
+}
+float from_half(uint16_t h) {
+  uint32_t sign = uint32_t(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
+  if (e == 0) return (sign ? -1.0f : 1.0f) * float(m) * 5.9604644775390625e-8f;
+  if (e == 31) return f32_from_bits(sign | 0x7f800000u | (m << 13));
+  return f32_from_bits(sign | ((e + 112) << 23) | (m << 13));
+}
+void put_half(uint8_t *p, float v) {
+  uint16_t h = to_half(v);
+  p[0] = uint8_t(h & 255);
+  p[1] = uint8_t(h >> 8);
+}
+int clampi(long v, int lo, int hi) { return int(std::min<long>(std::max<long>(v, lo), hi)); }
+int rnd(float v) { return int(std::nearbyint(v)); }
+
+long long round_half_even(double v) { return (long long)std::nearbyint(v); }
+
+int pack_int4_row(const float *f32, const uint16_t *bf16, uint8_t *dst, int row, int cols, int row_bytes) {
+  float vals[32];
+  for (int group = 0; group * 32 < cols; ++group) {
+    const int base = group * 32, count = std::min(32, cols - base);
+    float maximum = 0.0f;
+    for (int j = 0; j < count; ++j) {
+      const size_t i = size_t(row) * cols + base + j;
+      vals[j] = bf16 ? f32_from_bits(uint32_t(bf16[i]) << 16) : f32[i];
+      if (!std::isfinite(vals[j])) return -1;
+      maximum = std::max(maximum, std::fabs(vals[j]));
+    }
+    float scale = float(double(maximum) / 7.0);
+    if (maximum > 0 && scale == 0) scale = maximum;
+    if (scale > 0) {
+      double num = 0.0;
+      int den = 0;
+      for (int j = 0; j < count; ++j) {
+        const int q = clampi(long(round_half_even(double(vals[j]) / double(scale))), -7, 7);
+        num += double(vals[j]) * double(q);
+        den += q * q;
+      }
+      if (den > 0) scale = float(num / double(den));
+    }
+    uint8_t *blk = dst + size_t(row) * row_bytes + size_t(group) * 20;
+    std::memcpy(blk, &scale, 4);
+    for (int wd = 0; wd < 4; ++wd) {
+      uint32_t word = 0;
+      for (int nb = 0; nb < 8; ++nb) {
+        const int j = wd * 8 + nb;
+        int q = 0;
+        if (j < count && scale > 0) q = clampi(long(round_half_even(double(vals[j]) / double(scale))), -7, 7);
+        word |= uint32_t(q + 8) << (4 * nb);
+      }
+      std::memcpy(blk + 4 + 4 * wd, &word, 4);
+    }
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------- GGML encoders
+void enc_q8_0(const float *x, uint8_t *b) {
+  float amax = 0;
+  for (int i = 0; i < 32; ++i) amax = std::max(amax, std::fabs(x[i]));
+  put_half(b, amax / 127.0f);
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8)));
+  for (int i = 0; i < 32; ++i) b[2 + i] = uint8_t(int8_t(d > 0 ? clampi(rnd(x[i] / d), -127, 127) : 0));
+}
+
+void enc_q4_k(const float *x, uint8_t *b) {
+  std::memset(b, 0, 144);
+  float scale[8], mins[8];
+  for (int j = 0; j < 8; ++j) {
+    float lo = 0, hi = -INFINITY;
+    for (int i = 0; i < 32; ++i) { lo = std::min(lo, x[j * 32 + i]); hi = std::max(hi, x[j * 32 + i]); }
+    scale[j] = (hi - lo) / 15.0f;
+    mins[j] = -lo;
+  }
+  const float ms = *std::max_element(scale, scale + 8), mm = *std::max_element(mins, mins + 8);
+  put_half(b, ms / 63.0f);
+  put_half(b + 2, mm / 63.0f);
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8))), dmin = from_half(uint16_t(b[2] | (b[3] << 8)));
+  int sc[8], m[8];
+  for (int j = 0; j < 8; ++j) {
+    sc[j] = d > 0 ? clampi(rnd(scale[j] / d), 0, 63) : 0;
+    m[j] = dmin > 0 ? clampi(rnd(mins[j] / dmin), 0, 63) : 0;
+  }
+  for (int j = 0; j < 4; ++j) {
+    b[4 + j] = uint8_t((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+    b[8 + j] = uint8_t((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+    b[12 + j] = uint8_t((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+  }
+  for (int i = 0; i < 256; ++i) {
+    const int j = i / 32;
+    const float s = d * float(sc[j]), off = dmin * float(m[j]);
+    const int q = s > 0 ? clampi(rnd((x[i] + off) / s), 0, 15) : 0;
+    b[16 + (i / 64) * 32 + i % 32] |= uint8_t(q << ((j & 1) * 4));
+  }
+}
+
+void enc_q6_k(const float *x, uint8_t *b) {
+  std::memset(b, 0, 210);
+  float scale[16], amax_all = 0;
+  for (int j = 0; j < 16; ++j) {
+    float a = 0;
+    for (int i = 0; i < 16; ++i) a = std::max(a, std::fabs(x[j * 16 + i]));
+    scale[j] = a / 31.0f;
+    amax_all = std::max(amax_all, scale[j]);
+  }
+  put_half(b + 208, amax_all / 127.0f);
+  const float d = from_half(uint16_t(b[208] | (b[209] << 8)));
+  for (int j = 0; j < 16; ++j) {
+    const int sc = d > 0 ? clampi(rnd(scale[j] / d), -128, 127) : 0;
+    b[192 + j] = uint8_t(int8_t(sc));
+  }
+  for (int i = 0; i < 256; ++i) {
+    const float s = d * float(int8_t(b[192 + i / 16]));
+    const int q = (s != 0 ? clampi(rnd(x[i] / s), -32, 31) : 0) + 32;
+    const int part = i / 128, quarter = (i % 128) / 32, lane = i % 32;
+    b[part * 64 + (quarter & 1) * 32 + lane] |= uint8_t((q & 15) << ((quarter / 2) * 4));
+    b[128 + part * 32 + lane] |= uint8_t(((q >> 4) & 3) << (quarter * 2));
+  }
+}
+
+void enc_q3_k(const float *x, uint8_t *b) {
+  std::memset(b, 0, 110);
+  float scale[16], smax = 0;
+  for (int j = 0; j < 16; ++j) {
+    float a = 0;
+    for (int i = 0; i < 16; ++i) a = std::max(a, std::fabs(x[j * 16 + i]));
+    scale[j] = a / 4.0f;
+    smax = std::max(smax, scale[j]);
+  }
+  put_half(b + 108, smax / 31.0f);
+  const float d = from_half(uint16_t(b[108] | (b[109] << 8)));
+  int sc6[16];
+  for (int g = 0; g < 16; ++g) {
+    sc6[g] = (d > 0 ? clampi(rnd(scale[g] / d), -32, 31) : 0) + 32;
+    b[96 + g % 8] |= uint8_t((sc6[g] & 15) << ((g / 8) * 4));
+    b[104 + g % 4] |= uint8_t(((sc6[g] >> 4) & 3) << ((g / 4) * 2));
+  }
+  for (int i = 0; i < 256; ++i) {
+    const float s = d * float(sc6[i / 16] - 32);
+    const int q = s != 0 ? clampi(rnd(x[i] / s), -4, 3) : 0;
+    const int low = q < 0 ? q + 4 : q;
+    b[32 + (i / 128) * 32 + i % 32] |= uint8_t(low << (((i % 128) / 32) * 2));
+    if (q >= 0) b[i % 32] |= uint8_t(1 << (i / 32));
+  }
+}
+
+void enc_q2_k(const float *x, uint8_t *b) {
+  std::memset(b, 0, 84);
+  float scale[16], mins[16];
+  for (int j = 0; j < 16; ++j) {
+    float lo = 0, hi = -INFINITY;
+    for (int i = 0; i < 16; ++i) { lo = std::min(lo, x[j * 16 + i]); hi = std::max(hi, x[j * 16 + i]); }
+    scale[j] = (hi - lo) / 3.0f;
+    mins[j] = -lo;
+  }
+  put_half(b + 80, *std::max_element(scale, scale + 16) / 15.0f);
+  put_half(b + 82, *std::max_element(mins, mins + 16) / 15.0f);
+  const float d = from_half(uint16_t(b[80] | (b[81] << 8))), dmin = from_half(uint16_t(b[82] | (b[83] << 8)));
+  for (int j = 0; j < 16; ++j) {
+    const int sc = d > 0 ? clampi(rnd(scale[j] / d), 0, 15) : 0;
+    const int m = dmin > 0 ? clampi(rnd(mins[j] / dmin), 0, 15) : 0;
+    b[j] = uint8_t(sc | (m << 4));
+  }
+  for (int i = 0; i < 256; ++i) {
+    const int j = i / 16;
+    const float s = d * float(b[j] & 15), off = dmin * float(b[j] >> 4);
+    const int q = s > 0 ? clampi(rnd((x[i] + off) / s), 0, 3) : 0;
+    b[16 + (i / 128) * 32 + i % 32] |= uint8_t(q << (((i % 128) / 32) * 2));
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qnn_int4_row_bytes(int cols) {
+  if (cols < 1) return -1;
+  const long long bytes = ((long long)cols + 31) / 32 * 20;
+  return bytes > 0x7fffffffLL ? -1 : int(bytes);
+}
+
+int qnn_quantize_int4(const void *src, int dtype, int rows, int cols, uint8_t *dst) {
+  if (!src || !dst || rows < 1 || cols < 1 || (dtype != QNN_DT_F32 && dtype != QNN_DT_BF16)) return QNN_E_ARGUMENT;
+  const int rb = qnn_int4_row_bytes(cols);
+  if (rb < 0) return QNN_E_ARGUMENT;
+  std::fesetround(FE_TONEAREST);
+  const float *f32 = dtype == QNN_DT_F32 ? static_cast<const float *>(src) : nullptr;
+  const uint16_t *b16 = dtype == QNN_DT_BF16 ? static_cast<const uint16_t *>(src) : nullptr;
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const int threads = (rows >= 64 && (long long)rows * cols >= 32768) ? int(std::min(hw, 64u)) : 1;
+  std::atomic<int> bad{0};
+  auto work = [&](int t) {
+    for (long long r = (long long)rows * t / threads; r < (long long)rows * (t + 1) / threads; ++r)
+      if (pack_int4_row(f32, b16, dst, int(r), cols, rb)) bad = 1;
+  };
+  if (threads == 1) {
+    work(0);
+  } else {
+    std::vector<std::thread> ts;
+    for (int t = 0; t < threads; ++t) ts.emplace_back(work, t);
+    for (auto &t : ts) t.join();
+  }
+  return bad ? QNN_E_ARGUMENT : QNN_OK;
+}
+
+int qnn_gguf_quantize(int encoding, const float *src, int64_t n, uint8_t *dst) {
+  int elems, bytes;
+  void (*fn)(const float *, uint8_t *);
+  switch (encoding) {
+    case QNN_WE_Q8_0: elems = 32; bytes = 34; fn = enc_q8_0; break;
+    case QNN_WE_Q4_K: elems = 256; bytes = 144; fn = enc_q4_k; break;
+    case QNN_WE_Q6_K: elems = 256; bytes = 210; fn = enc_q6_k; break;
+    case QNN_WE_Q3_K: elems = 256; bytes = 110; fn = enc_q3_k; break;
+    case QNN_WE_Q2_K: elems = 256; bytes = 84; fn = enc_q2_k; break;
+    default: return QNN_E_NOT_SUPPORTED;
+  }
+  if (!src || !dst || n < 0 || n % elems) return QNN_E_ARGUMENT;
+  const int64_t nb = n / elems;
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const int threads = nb >= 4096 ? int(std::min(hw, 64u)) : 1;
+  std::atomic<int> bad{0};
+  auto work = [&](int t) {
+    for (int64_t blk = nb * t / threads; blk < nb * (t + 1) / threads; ++blk) {
+      const float *x = src + blk * elems;
+      for (int i = 0; i < elems; ++i)
+        if (!std::isfinite(x[i])) bad = 1;
+      fn(x, dst + blk * bytes);
+    }
+  };
+  if (threads == 1) {
+    work(0);
+  } else {
+    std::vector<std::thread> ts;
+    for (int t = 0; t < threads; ++t) ts.emplace_back(work, t);
+    for (auto &t : ts) t.join();
+  }
+  return bad ? QNN_E_ARGUMENT : QNN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,425 @@
+"""Python mirror of the HIP backend's C ABI (include/qnn_hip.h).
+
+``GPUContext`` follows the resident context QuickNN's LLM engine calls,
+TQNNGPUContext (src/backends/vulkan/QuickNN.Vulkan.Context.API.inc:14-165):
+same method names, argument meaning and exception classes, so tests read like
+the engine's own call sites.  ``MemoryBlock`` mirrors the TMemoryBlock weight
+descriptor (src/core/QuickNN.Common.pas:135-155).
+
+The library is loaded from the package directory; if it is missing the import
+of this module raises -- there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import itertools
+import os
+import struct
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqnn_hip.so")
+
+# ---- status codes -> the reference's exception classes ----
+QNN_OK = 0
+QNN_NOT_HANDLED = 1
+QNN_E_ARGUMENT = -1
+QNN_E_RANGE = -2
+QNN_E_NOT_SUPPORTED = -3
+QNN_E_INVALID_OP = -4
+
+
+class QNNError(RuntimeError):
+    code = 0
+
+
+class EArgumentException(QNNError, ValueError):
+    code = QNN_E_ARGUMENT
+
+
+class ERangeError(QNNError):
+    code = QNN_E_RANGE
+
+
+class ENotSupportedException(QNNError):
+    code = QNN_E_NOT_SUPPORTED
+
+
+class EInvalidOp(QNNError):
+    code = QNN_E_INVALID_OP
+
+
+_ERRORS = {c.code: c for c in (EArgumentException, ERangeError, ENotSupportedException, EInvalidOp)}
+
+# ---- TQNNDataType / TQNNWeightEncoding ordinals ----
+DT_F16, DT_BF16, DT_F32, DT_S8, DT_U8 = 1, 2, 3, 5, 6
+WE_NATIVE, WE_Q8_0, WE_Q4_K, WE_Q6_K, WE_Q3_K, WE_Q2_K = 0, 1, 2, 3, 4, 9
+GGUF_BLOCK = {WE_Q8_0: (32, 34), WE_Q4_K: (256, 144), WE_Q6_K: (256, 210), WE_Q3_K: (256, 110),
+              WE_Q2_K: (256, 84)}
+
+# ---- op codes (Context.API.inc:167-258) ----
+GO_FILL, GO_NORM, GO_ADD, GO_SWIGLU, GO_FINITE = 0, 2, 4, 9, 13
+GO_MOE_ROUTE, GO_MOE_GATHER, GO_MOE_SCATTER, GO_GEGLU = 52, 53, 54, 75
+
+
+class _Weight(ctypes.Structure):
+    _fields_ = [("identity", ctypes.c_uint64), ("data", ctypes.c_void_p), ("offset", ctypes.c_int64),
+                ("size", ctypes.c_int64), ("shape0", ctypes.c_int64), ("shape1", ctypes.c_int64),
+                ("dtype", ctypes.c_int32), ("encoding", ctypes.c_int32)]
+
+
+class Status(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "gemm_calls", "gguf_calls", "int4_calls", "moe_calls", "weight_uploads", "weight_upload_bytes",
+        "weight_cache_hits", "weight_cache_misses", "weight_evictions", "readbacks", "submissions",
+        "weight_bytes", "weight_limit", "activation_bytes", "activation_peak_bytes")]
+
+
+_lib = None
+_vp = ctypes.c_void_p
+_ip = ctypes.POINTER(ctypes.c_int)
+
+
+def lib():
+    """Loads libqnn_hip.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libqnn_hip.so not built at {LIB_PATH}: run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        W = ctypes.POINTER(_Weight)
+        sig = {
+            "qnn_last_error": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int]),
+            "qnn_ctx_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(_vp)]),
+            "qnn_ctx_destroy": (ctypes.c_int, [_vp]),
+            "qnn_get_status": (ctypes.c_int, [_vp, ctypes.POINTER(Status)]),
+            "qnn_tensor_new": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp)]),
+            "qnn_recycle": (ctypes.c_int, [_vp, ctypes.POINTER(_vp)]),
+            "qnn_scratch": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+            "qnn_upload_raw": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.POINTER(_vp)]),
+            "qnn_download": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int]),
+            "qnn_copy": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "qnn_flush": (ctypes.c_int, [_vp]),
+            "qnn_tensor_count": (ctypes.c_int, [_vp]),
+            "qnn_tensor_device_ptr": (_vp, [_vp]),
+            "qnn_retain_weight": (ctypes.c_int, [_vp, W, ctypes.c_int, ctypes.c_int]),
+            "qnn_preload_weights": (ctypes.c_int, [_vp, W, ctypes.c_int, ctypes.c_uint64]),
+            "qnn_is_weight_resident": (ctypes.c_int, [_vp, W, ctypes.c_int, ctypes.c_int, _ip]),
+            "qnn_weight_batch_capacity": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
+            "qnn_linear": (ctypes.c_int, [_vp, _vp, _vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "qnn_int4_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "qnn_swiglu_vector": (ctypes.c_int, [_vp, _vp, _vp, W, W, ctypes.c_int, ctypes.c_int]),
+            "qnn_int4_linear_accumulate": (ctypes.c_int, [_vp, _vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int,
+                                                          ctypes.c_int]),
+            "qnn_kernel": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp, _vp, _ip, ctypes.c_int]),
+            "qnn_kernel_weights": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp, W, W, _ip,
+                                                  ctypes.c_int]),
+            "qnn_check_finite": (ctypes.c_int, [_vp, _vp, ctypes.c_int]),
+            "qnn_expert_set_create": (ctypes.c_int, [_vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                     ctypes.POINTER(_vp)]),
+            "qnn_expert_set_destroy": (ctypes.c_int, [_vp, _vp]),
+            "qnn_moe_experts": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int]),
+            "qnn_dequantize": (ctypes.c_int, [_vp, _vp, W, ctypes.c_int, ctypes.c_int]),
+            "qnn_event_record": (ctypes.c_int, [_vp, ctypes.c_int]),
+            "qnn_event_elapsed_ms": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int,
+                                                    ctypes.POINTER(ctypes.c_float)]),
+            "qnn_graph_begin": (ctypes.c_int, [_vp]),
+            "qnn_graph_end": (ctypes.c_int, [_vp, _ip]),
+            "qnn_graph_launch": (ctypes.c_int, [_vp, ctypes.c_int]),
+            "qnn_stream": (_vp, [_vp]),
+            "qnn_int4_row_bytes": (ctypes.c_int, [ctypes.c_int]),
+            "qnn_quantize_int4": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]),
+            "qnn_gguf_quantize": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_int64, _vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+EXPORTED = (
+    "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_tensor_new", "qnn_recycle",
+    "qnn_scratch", "qnn_upload_raw", "qnn_download", "qnn_copy", "qnn_flush", "qnn_tensor_count",
+    "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
+    "qnn_weight_batch_capacity", "qnn_linear", "qnn_int4_linear", "qnn_swiglu_vector",
+    "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
+    "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
+    "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
+    "qnn_stream", "qnn_int4_row_bytes", "qnn_quantize_int4", "qnn_gguf_quantize",
+)
+
+
+def _raise(rc: int) -> int:
+    if rc < 0:
+        buf = ctypes.create_string_buffer(1024)
+        lib().qnn_last_error(buf, 1024)
+        raise _ERRORS.get(rc, QNNError)(buf.value.decode(errors="replace"))
+    return rc
+
+
+def float_bits(v: float) -> int:
+    """QNNGPUFloatBits (Context.API.inc:166): reinterpret a float as an Integer argument."""
+    return struct.unpack("<i", struct.pack("<f", v))[0]
+
+
+# ---------------------------------------------------------------------------
+# Weight descriptors
+# ---------------------------------------------------------------------------
+_identity = itertools.count(1)
+
+
+class MemoryBlock:
+    """TMemoryBlock view of host weight storage (Common.pas:135-155).
+
+    ``identity`` plays the role of WeightIdentity: blocks with the same identity
+    must hold the same immutable bytes.  Keep the array alive while the block
+    may be uploaded.
+    """
+
+    def __init__(self, data: np.ndarray, shape, dtype: int, encoding: int = WE_NATIVE, offset: int = 0,
+                 size: int | None = None, identity: int | None = None):
+        self.data = np.ascontiguousarray(data)
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = dtype
+        self.encoding = encoding
+        self.offset = offset
+        self.size = int(size if size is not None else int(np.prod(self.shape)))
+        self.identity = identity if identity is not None else next(_identity)
+
+    def desc(self) -> _Weight:
+        return _Weight(self.identity, self.data.ctypes.data, self.offset, self.size, self.shape[0],
+                       self.shape[1] if len(self.shape) > 1 else 1, self.dtype, self.encoding)
+
+    @staticmethod
+    def int4(packed: np.ndarray, **kw) -> "MemoryBlock":
+        """Native INT4 cache matrix: dtU8 [N, Int4RowBytes(K)] (LLM.Quantization.pas:299-317)."""
+        packed = np.ascontiguousarray(packed, np.uint8)
+        return MemoryBlock(packed, packed.shape, DT_U8, WE_NATIVE, 0, packed.size, **kw)
+
+    @staticmethod
+    def gguf(blocks: np.ndarray, rows: int, cols: int, encoding: int, **kw) -> "MemoryBlock":
+        """GGUF tensor: dtU8 with element shape [N, K] (SafeTensors.pas:874-890)."""
+        blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+        return MemoryBlock(blocks, (rows, cols), DT_U8, encoding, 0, rows * cols, **kw)
+
+    @staticmethod
+    def vector(values: np.ndarray, **kw) -> "MemoryBlock":
+        v = np.ascontiguousarray(values)
+        dt = DT_BF16 if v.dtype == np.uint16 else DT_F32
+        if dt == DT_F32:
+            v = v.astype(np.float32, copy=False)
+        return MemoryBlock(v, (v.size,), dt, WE_NATIVE, 0, v.size, **kw)
+
+
+def _wd(w: MemoryBlock | None):
+    return None if w is None else ctypes.byref(w.desc())
+
+
+# ---------------------------------------------------------------------------
+# Host utilities
+# ---------------------------------------------------------------------------
+def int4_row_bytes(cols: int) -> int:
+    """Int4RowBytes (Quantization.Int4.pas:25-33)."""
+    r = lib().qnn_int4_row_bytes(cols)
+    if r < 0:
+        raise EArgumentException("INT4 matrix width")
+    return r
+
+
+def quantize_int4(w: np.ndarray) -> np.ndarray:
+    """QuantizeInt4 (Quantization.Int4.pas:96-144): fp32 or bf16 bits (uint16) [N, K] -> U8 [N, RowBytes]."""
+    w = np.ascontiguousarray(w)
+    dt = DT_BF16 if w.dtype == np.uint16 else DT_F32
+    if dt == DT_F32:
+        w = w.astype(np.float32, copy=False)
+    rows, cols = w.shape
+    out = np.empty((rows, int4_row_bytes(cols)), np.uint8)
+    _raise(lib().qnn_quantize_int4(w.ctypes.data, dt, rows, cols, out.ctypes.data))
+    return out
+
+
+def gguf_quantize(encoding: int, w: np.ndarray) -> np.ndarray:
+    """Synthetic GGML blocks of fp32 values (row-major, rows are whole blocks)."""
+    w = np.ascontiguousarray(w, np.float32)
+    elems, nbytes = GGUF_BLOCK[encoding]
+    out = np.empty(w.size // elems * nbytes, np.uint8)
+    _raise(lib().qnn_gguf_quantize(encoding, w.ctypes.data, w.size, out.ctypes.data))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Resident context
+# ---------------------------------------------------------------------------
+class Tensor:
+    """TQNNGPUTensor: context-owned fp32 device buffer of ``count`` floats."""
+
+    __slots__ = ("handle", "count", "ctx")
+
+    def __init__(self, ctx: "GPUContext", handle: int):
+        self.ctx = ctx
+        self.handle = handle
+        self.count = lib().qnn_tensor_count(handle)
+
+    @property
+    def device_ptr(self) -> int:
+        return lib().qnn_tensor_device_ptr(self.handle)
+
+
+def _th(t: Tensor | None):
+    return None if t is None else t.handle
+
+
+class GPUContext:
+    """TQNNGPUContext over libqnn_hip.so (one per process, bound to its creating thread)."""
+
+    def __init__(self, device: int = 0, weight_cache_bytes: int = 0):
+        h = _vp()
+        _raise(lib().qnn_ctx_create(device, weight_cache_bytes, ctypes.byref(h)))
+        self.h = h.value
+
+    # -- lifetime
+    def close(self) -> None:
+        if self.h:
+            _raise(lib().qnn_ctx_destroy(self.h))
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def status(self) -> Status:
+        s = Status()
+        _raise(lib().qnn_get_status(self.h, ctypes.byref(s)))
+        return s
+
+    # -- tensors
+    def NewTensor(self, count: int) -> Tensor:
+        h = _vp()
+        _raise(lib().qnn_tensor_new(self.h, count, ctypes.byref(h)))
+        return Tensor(self, h.value)
+
+    def Recycle(self, t: Tensor) -> None:
+        h = _vp(t.handle)
+        _raise(lib().qnn_recycle(self.h, ctypes.byref(h)))
+
+    def Scratch(self, slot: int, count: int) -> Tensor:
+        h = _vp()
+        _raise(lib().qnn_scratch(self.h, slot, count, ctypes.byref(h)))
+        return Tensor(self, h.value)
+
+    def UploadRaw(self, data: np.ndarray) -> Tensor:
+        a = np.ascontiguousarray(data)
+        if a.dtype.itemsize != 4:
+            a = a.astype(np.float32)
+        h = _vp()
+        _raise(lib().qnn_upload_raw(self.h, a.ctypes.data, a.size, ctypes.byref(h)))
+        return Tensor(self, h.value)
+
+    Upload = UploadRaw
+
+    def Download(self, t: Tensor, count: int = -1, dtype=np.float32) -> np.ndarray:
+        n = t.count if count < 0 else count
+        out = np.empty(n, dtype)
+        _raise(lib().qnn_download(self.h, t.handle, out.ctypes.data, n))
+        return out
+
+    def Copy(self, dst: Tensor, src: Tensor, count: int, dst_offset: int = 0, src_offset: int = 0) -> None:
+        _raise(lib().qnn_copy(self.h, dst.handle, src.handle, count, dst_offset, src_offset))
+
+    def Flush(self) -> None:
+        _raise(lib().qnn_flush(self.h))
+
+    # -- weights
+    def RetainWeight(self, w: MemoryBlock, rows: int, cols: int) -> None:
+        _raise(lib().qnn_retain_weight(self.h, _wd(w), rows, cols))
+
+    def PreloadWeights(self, ws, staging_limit: int = 134217728) -> None:
+        arr = (_Weight * len(ws))(*[w.desc() for w in ws])
+        _raise(lib().qnn_preload_weights(self.h, arr, len(ws), staging_limit))
+
+    def IsWeightResident(self, w: MemoryBlock, rows: int, cols: int) -> bool:
+        r = ctypes.c_int()
+        _raise(lib().qnn_is_weight_resident(self.h, _wd(w), rows, cols, ctypes.byref(r)))
+        return bool(r.value)
+
+    def WeightBatchCapacity(self) -> int:
+        v = ctypes.c_uint64()
+        _raise(lib().qnn_weight_batch_capacity(self.h, ctypes.byref(v)))
+        return v.value
+
+    # -- hot-path ops
+    def Linear(self, dst: Tensor, src: Tensor, weight: MemoryBlock, scales: MemoryBlock | None,
+               bias: MemoryBlock | None, rows: int, input_dim: int, output_dim: int) -> None:
+        _raise(lib().qnn_linear(self.h, dst.handle, src.handle, _wd(weight), _wd(scales), _wd(bias), rows,
+                                input_dim, output_dim))
+
+    def Int4Linear(self, dst: Tensor, src: Tensor, weight: MemoryBlock, rows: int, input_dim: int,
+                   output_dim: int) -> None:
+        _raise(lib().qnn_int4_linear(self.h, dst.handle, src.handle, _wd(weight), rows, input_dim, output_dim))
+
+    def TrySwiGLUVector(self, dst: Tensor, src: Tensor, gate: MemoryBlock, up: MemoryBlock, input_dim: int,
+                        output_dim: int) -> bool:
+        rc = _raise(lib().qnn_swiglu_vector(self.h, dst.handle, src.handle, _wd(gate), _wd(up), input_dim,
+                                            output_dim))
+        return rc == QNN_OK
+
+    def Int4LinearAccumulate(self, dst: Tensor, src: Tensor, probabilities: Tensor, weight: MemoryBlock,
+                             input_dim: int, output_dim: int, probability_index: int) -> None:
+        _raise(lib().qnn_int4_linear_accumulate(self.h, dst.handle, src.handle, probabilities.handle, _wd(weight),
+                                                input_dim, output_dim, probability_index))
+
+    def Kernel(self, op: int, n: int, dst: Tensor | None, a: Tensor | None, b: Tensor | None, c: Tensor | None,
+               args) -> None:
+        arr = (ctypes.c_int * max(1, len(args)))(*args)
+        _raise(lib().qnn_kernel(self.h, op, n, _th(dst), _th(a), _th(b), _th(c), arr, len(args)))
+
+    def KernelWeights(self, op: int, n: int, dst: Tensor, a: Tensor, b: MemoryBlock | None,
+                      c: MemoryBlock | None, args) -> None:
+        arr = (ctypes.c_int * max(1, len(args)))(*args)
+        _raise(lib().qnn_kernel_weights(self.h, op, n, dst.handle, a.handle, _wd(b), _wd(c), arr, len(args)))
+
+    def CheckFinite(self, t: Tensor, count: int = -1) -> None:
+        _raise(lib().qnn_check_finite(self.h, t.handle, count))
+
+    # -- routed experts on the device
+    def CreateExpertSet(self, gates, ups, downs, hidden: int, inter: int) -> int:
+        E = len(gates)
+        mk = lambda ws: (_Weight * E)(*[w.desc() for w in ws])
+        h = _vp()
+        _raise(lib().qnn_expert_set_create(self.h, mk(gates), mk(ups), mk(downs), E, hidden, inter,
+                                           ctypes.byref(h)))
+        return h.value
+
+    def DestroyExpertSet(self, s: int) -> None:
+        _raise(lib().qnn_expert_set_destroy(self.h, s))
+
+    def MoEExperts(self, expert_set: int, dst: Tensor, src: Tensor, routes: Tensor, rows: int, topk: int) -> None:
+        _raise(lib().qnn_moe_experts(self.h, expert_set, dst.handle, src.handle, routes.handle, rows, topk))
+
+    # -- diagnostics
+    def Dequantize(self, dst: Tensor, w: MemoryBlock, rows: int, cols: int) -> None:
+        _raise(lib().qnn_dequantize(self.h, dst.handle, _wd(w), rows, cols))
+
+    def EventRecord(self, slot: int) -> None:
+        _raise(lib().qnn_event_record(self.h, slot))
+
+    def EventElapsedMs(self, a: int, b: int) -> float:
+        v = ctypes.c_float()
+        _raise(lib().qnn_event_elapsed_ms(self.h, a, b, ctypes.byref(v)))
+        return v.value
+
+    def GraphBegin(self) -> None:
+        _raise(lib().qnn_graph_begin(self.h))
+
+    def GraphEnd(self) -> int:
+        g = ctypes.c_int()
+        _raise(lib().qnn_graph_end(self.h, ctypes.byref(g)))
+        return g.value
+
+    def GraphLaunch(self, graph_id: int) -> None:
+        _raise(lib().qnn_graph_launch(self.h, graph_id))

@@ -1,0 +1,50 @@
+"""Shared pytest configuration.
+
+`gpu` tests need an MI355X (libqnn_hip.so + a visible HIP device); everything
+else runs on the CPU.  One resident context per process is allowed (as in the
+reference), so GPU tests share the session-scoped `ctx` fixture.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an AMD GPU and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def ctx():
+    from quicknn_amd import hip
+
+    c = hip.GPUContext(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(1234)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits by truncation, as SingleToBF16 (src/core/QuickNN.Common.pas:1779-1797)."""
+    return (np.ascontiguousarray(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def normwise_rel_err(y: np.ndarray, r: np.ndarray) -> float:
+    """max_i |y - r| / max_i |r|: the tolerance metric for matvec/MLP/GEMM outputs."""
+    y = np.asarray(y, np.float64)
+    r = np.asarray(r, np.float64)
+    den = np.max(np.abs(r))
+    return float(np.max(np.abs(y - r)) / den) if den > 0 else float(np.max(np.abs(y - r)))
