@@ -4,14 +4,17 @@
 // fp32 scale s then 16 bytes of offset-binary nibbles n (element j in byte j/2,
 // low nibble for even j); value = fl32((n-8)*s).
 //
-// Device layout: see I4Layout in qnn_internal.h.  One wavefront owns a tile of
-// 64 rows (one row per lane) and a K-slice of GS groups: every load is a
-// 16-byte global_load_dwordx4 and consecutive lanes read consecutive 16-byte
-// pieces, so each load instruction moves 1 KiB of packed weights.  The
-// activation slice is staged in LDS with its per-group sums; the inner product
-// folds the offset and scale per group:
-//     sum_j (n_j - 8) s x_j = s * (sum_j n_j x_j - 8 * X_g),  X_g = sum_j x_j
-// Slices of one tile are combined by the last wavefront to finish (an atomic
+// Device layout: see I4Layout in qnn_internal.h.  One wavefront streams a tile
+// of 64 rows (one row per lane): every load is a 16-byte global_load_dwordx4
+// and consecutive lanes read consecutive 16-byte pieces, so each load
+// instruction moves 1 KiB of packed weights.  The activation slice is staged
+// in LDS as 16-bit fixed point per 32-group (two int8 planes); the inner
+// product runs on the raw nibble bytes with v_dot4_i32_i8 and folds the
+// offset and both scales once per group:
+//     sum_j (n_j - 8) s x_j ~= s * s2 * (sum_j n_j (256 q1_j + q2_j) - 8 sum_j (256 q1_j + q2_j))
+// (exact integer arithmetic inside a group; fp32 across groups; relative
+// error of the activation representation <= 2^-16 of the group's max|x|).
+// Slices of one tile are combined by the last workgroup to finish (an atomic
 // ticket per tile), in slice order, so results do not depend on timing.
 #include "qnn_internal.h"
 
@@ -41,49 +44,40 @@ __device__ __forceinline__ bool map_tile_slice(int b, int slices, int tiles, int
   return tile < tiles;
 }
 
-template <int MT, int GS>
-__global__ __launch_bounds__(64) void k_int4_matvec(const I4Launch a, const int slices) {
+// Workgroup = 4 wavefronts on one 64-row tile.  The workgroup owns a K-slice
+// of 4*GSW groups; wave w streams groups [w*GSW, (w+1)*GSW) of it.  The x
+// slice is staged once per workgroup; the four partial sums meet in LDS.
+template <int MT, int GSW>
+__global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int slices) {
+  constexpr int GS = 4 * GSW;  // groups per workgroup slice
   int tile, slice;
   if (!map_tile_slice(blockIdx.x, slices, a.tiles, tile, slice)) return;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g0 = slice * GS;
   const int ng = min(GS, a.g4 - g0);  // multiple of 4
+  const int gw0 = wave * GSW;         // this wave's first group within the slice
+  const int ngw = max(0, min(GSW, ng - gw0));
 
-  // 1) Issue every weight load of the slice first; HBM latency overlaps the
-  //    activation staging below.  In I4_SWIGLU mode wave tile t covers output
-  //    rows 32t..32t+31: lanes 0-31 read them from the gate matrix, lanes 32-63
+  // 1) Activation slice first (L2-resident, short latency): 4 floats per
+  //    thread per pass.  Then this wave's weight stream: scales, nibbles in
+  //    group order.  Loads return in issue order, so group g is consumed as
+  //    soon as it lands.  In I4_SWIGLU mode tile t covers output rows
+  //    32t..32t+31: lanes 0-31 read them from the gate matrix, lanes 32-63
   //    from the up matrix (rows (t&1)*32.. of stored tile t/2).
-  int stile = tile, srow = lane;
-  const void *nb = a.nib, *sb = a.scl;
-  if (a.mode == I4_SWIGLU) {
-    stile = tile >> 1;
-    srow = (tile & 1) * 32 + (lane & 31);
-    if (lane >= 32) { nb = a.nib2; sb = a.scl2; }
-  }
-  const uint4 *nib = static_cast<const uint4 *>(nb) + (size_t(stile) * a.g4 + g0) * 64 + srow;
-  const float4 *scl = static_cast<const float4 *>(sb) + (size_t(stile) * (a.g4 >> 2) + (g0 >> 2)) * 64 + srow;
-  uint4 w[GS];
-  float4 s[GS / 4];
-#pragma unroll
-  for (int q = 0; q < GS / 4; ++q)
-    if (4 * q < ng) s[q] = scl[q * 64];
-#pragma unroll
-  for (int g = 0; g < GS; ++g)
-    if (g < ng) w[g] = nib[g * 64];
-
-  // 2) Stage x[m][g0*32 .. g0*32+GS*32) and its per-group sums in LDS.
-  __shared__ float xs[MT][GS * 32];
-  __shared__ float xsum[MT][GS];
+  constexpr int XIT = (GS * 32 + 1023) / 1024;
+  float4 xr_[MT][XIT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
-    for (int it = 0; it < (GS + 7) / 8; ++it) {  // 256 floats per pass
-      const int e = (it * 64 + lane) * 4;
+    for (int it = 0; it < XIT; ++it) {
+      const int e = (it * 256 + tid) * 4;
       const int kk = g0 * 32 + e;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (m < a.m && e < ng * 32) {
         const float *xr = a.x + size_t(m) * a.x_stride;
-        if (kk + 3 < a.k) {
+        if (kk + 3 < a.k && a.x_vec4) {
+          v = *reinterpret_cast<const float4 *>(xr + kk);
+        } else if (kk + 3 < a.k) {
           v.x = xr[kk]; v.y = xr[kk + 1]; v.z = xr[kk + 2]; v.w = xr[kk + 3];
         } else {
           if (kk < a.k) v.x = xr[kk];
@@ -91,68 +85,181 @@ __global__ __launch_bounds__(64) void k_int4_matvec(const I4Launch a, const int 
           if (kk + 2 < a.k) v.z = xr[kk + 2];
         }
       }
-      if (e < GS * 32) *reinterpret_cast<float4 *>(&xs[m][e]) = v;
-      float part = (v.x + v.y) + (v.z + v.w);
-      part += __shfl_xor(part, 1);
-      part += __shfl_xor(part, 2);
-      part += __shfl_xor(part, 4);
-      if ((lane & 7) == 0 && e < GS * 32) xsum[m][e >> 5] = part;
+      xr_[m][it] = v;
+    }
+  }
+  int stile = tile, srow = lane;
+  const void *nb = a.nib, *sb = a.scl;
+  if (a.mode == I4_SWIGLU) {
+    stile = tile >> 1;
+    srow = (tile & 1) * 32 + (lane & 31);
+    if (lane >= 32) { nb = a.nib2; sb = a.scl2; }
+  }
+  const int gq0 = g0 + gw0;  // first group of this wave (multiple of GSW)
+  const uint4 *nib = static_cast<const uint4 *>(nb) + (size_t(stile) * a.g4 + gq0) * 64 + srow;
+  const float *sclf = static_cast<const float *>(sb) + (size_t(stile) * (a.g4 >> 2) + (gq0 >> 2)) * 256 + srow * 4;
+  uint4 w[GSW];
+  float sc[GSW];
+  if (GSW >= 4) {  // whole scale quads: one 16-byte load per 4 groups
+#pragma unroll
+    for (int q = 0; q < GSW / 4; ++q)
+      if (4 * q < ngw) {
+        const float4 s4 = *reinterpret_cast<const float4 *>(sclf + q * 256);
+        sc[4 * q] = s4.x;
+        sc[4 * q + 1] = s4.y;
+        sc[4 * q + 2] = s4.z;
+        sc[4 * q + 3] = s4.w;
+      }
+  } else {
+#pragma unroll
+    for (int g = 0; g < GSW; ++g) {
+      if (g < ngw) {
+        const int gg = gq0 + g;  // scale of group gg: quad gg/4, component gg%4
+        sc[g] = sclf[((gg >> 2) - (gq0 >> 2)) * 256 + (gg & 3)];
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < GSW; ++g)
+    if (g < ngw) w[g] = nib[g * 64];
+
+  // 2) Quantise the x slice per 32-element group to 16-bit fixed point,
+  //    x ~= s2 * (256*q1 + q2) with q1, q2 in [-127, 127]:
+  //      s1 = amax/127, q1 = rint(x/s1), r = x - q1*s1, s2 = s1/256, q2 = rint(r/s2)
+  //    (|x - s2(256 q1 + q2)| <= s2/2 = amax/65024).  The int8 planes are laid
+  //    out to match the nibble bytes of a weight dword: dword c of a group
+  //    holds elements 8c..8c+7, its low nibbles are the even elements and its
+  //    high nibbles the odd ones, so word 2c packs x[8c+0,2,4,6] and word 2c+1
+  //    x[8c+1,3,5,7].  Per group: 8 hi words, 8 lo words, s2 and -8*sum(q).
+  __shared__ uint32_t xqh[MT][GS][8];
+  __shared__ uint32_t xql[MT][GS][8];
+  __shared__ float xs2[MT][GS];
+  __shared__ int xoff[MT][GS];
+  __shared__ float red[3][MT][64];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      const int e = (it * 256 + tid) * 4;  // first element of this thread, within the slice
+      const float4 v = xr_[m][it];
+      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      amax = fmaxf(amax, __shfl_xor(amax, 4));
+      const float s1 = amax / 127.0f;
+      const float inv = s1 > 0.0f ? 1.0f / s1 : 0.0f;
+      const float inv2 = inv * 256.0f;
+      int h[4], l[4];
+      const float xv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float q1 = fminf(127.0f, fmaxf(-127.0f, rintf(xv[j] * inv)));
+        const float r = fmaf(-q1, s1, xv[j]);
+        const float q2 = fminf(127.0f, fmaxf(-127.0f, rintf(r * inv2)));
+        h[j] = int(q1);
+        l[j] = int(q2);
+      }
+      int sumq = (256 * h[0] + l[0]) + (256 * h[1] + l[1]) + (256 * h[2] + l[2]) + (256 * h[3] + l[3]);
+      sumq += __shfl_xor(sumq, 1);
+      sumq += __shfl_xor(sumq, 2);
+      sumq += __shfl_xor(sumq, 4);
+      if (e < GS * 32) {
+        const int g = e >> 5, i0 = e & 31;  // i0 = 0 or 4 within dword c = i0/8... element 8c + (i0 & 7)
+        const int c = i0 >> 3, half = (i0 >> 2) & 1;
+        // bytes for even slots (elements +0, +2) and odd slots (+1, +3) of this half dword
+        const uint32_t he = (uint32_t(h[0]) & 255u) | ((uint32_t(h[2]) & 255u) << 8);
+        const uint32_t ho = (uint32_t(h[1]) & 255u) | ((uint32_t(h[3]) & 255u) << 8);
+        const uint32_t le = (uint32_t(l[0]) & 255u) | ((uint32_t(l[2]) & 255u) << 8);
+        const uint32_t lo = (uint32_t(l[1]) & 255u) | ((uint32_t(l[3]) & 255u) << 8);
+        uint16_t *ph = reinterpret_cast<uint16_t *>(&xqh[m][g][0]);
+        uint16_t *pl = reinterpret_cast<uint16_t *>(&xql[m][g][0]);
+        ph[(2 * c) * 2 + half] = uint16_t(he);
+        ph[(2 * c + 1) * 2 + half] = uint16_t(ho);
+        pl[(2 * c) * 2 + half] = uint16_t(le);
+        pl[(2 * c + 1) * 2 + half] = uint16_t(lo);
+        if ((lane & 7) == 0) {
+          xs2[m][g] = s1 * 0.00390625f;
+          xoff[m][g] = -8 * sumq;
+        }
+      }
     }
   }
   __syncthreads();
 
-  // 3) Dequantise in registers and accumulate.
+  // 3) Dequantise-free integer dot: per group and token
+  //    isum = 256 * dot(n, q1) + dot(n, q2) - 8 * sum(256 q1 + q2)  (exact, < 2^24)
+  //    acc += float(isum) * (s * s2).
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
 #pragma unroll
-  for (int g = 0; g < GS; ++g) {
-    if (g < ng) {
-      const float sc = sel4(s[g >> 2], g & 3);
-      float nv[32];  // nibble values of this group, element order
+  for (int g = 0; g < GSW; ++g) {
+    if (g < ngw) {
+      const int gl = gw0 + g;
+      uint32_t nlo[4], nhi[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const uint32_t wd = sel4u(w[g], c);
-        const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-          nv[c * 8 + 2 * bb] = float((lo >> (8 * bb)) & 0xFFu);
-          nv[c * 8 + 2 * bb + 1] = float((hi >> (8 * bb)) & 0xFFu);
-        }
+        nlo[c] = wd & 0x0F0F0F0Fu;
+        nhi[c] = (wd >> 4) & 0x0F0F0F0Fu;
       }
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const float4 *xv = reinterpret_cast<const float4 *>(&xs[m][g * 32]);
-        float pc[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float4 xa = xv[2 * c], xb = xv[2 * c + 1];
-          float t = nv[c * 8] * xa.x;
-          t = fmaf(nv[c * 8 + 1], xa.y, t);
-          t = fmaf(nv[c * 8 + 2], xa.z, t);
-          t = fmaf(nv[c * 8 + 3], xa.w, t);
-          t = fmaf(nv[c * 8 + 4], xb.x, t);
-          t = fmaf(nv[c * 8 + 5], xb.y, t);
-          t = fmaf(nv[c * 8 + 6], xb.z, t);
-          t = fmaf(nv[c * 8 + 7], xb.w, t);
-          pc[c] = t;
-        }
-        const float pg = (pc[0] + pc[1]) + (pc[2] + pc[3]);
-        acc[m] = fmaf(sc, pg - 8.0f * xsum[m][g], acc[m]);
+        const uint4 *qh = reinterpret_cast<const uint4 *>(&xqh[m][gl][0]);
+        const uint4 *ql = reinterpret_cast<const uint4 *>(&xql[m][gl][0]);
+        const uint4 h0 = qh[0], h1 = qh[1], l0 = ql[0], l1 = ql[1];
+        int ah0 = 0, ah1 = 0, al0 = 0, al1 = 0;
+        ah0 = __builtin_amdgcn_sdot4(int(nlo[0]), int(h0.x), ah0, false);
+        ah1 = __builtin_amdgcn_sdot4(int(nhi[0]), int(h0.y), ah1, false);
+        al0 = __builtin_amdgcn_sdot4(int(nlo[0]), int(l0.x), al0, false);
+        al1 = __builtin_amdgcn_sdot4(int(nhi[0]), int(l0.y), al1, false);
+        ah0 = __builtin_amdgcn_sdot4(int(nlo[1]), int(h0.z), ah0, false);
+        ah1 = __builtin_amdgcn_sdot4(int(nhi[1]), int(h0.w), ah1, false);
+        al0 = __builtin_amdgcn_sdot4(int(nlo[1]), int(l0.z), al0, false);
+        al1 = __builtin_amdgcn_sdot4(int(nhi[1]), int(l0.w), al1, false);
+        ah0 = __builtin_amdgcn_sdot4(int(nlo[2]), int(h1.x), ah0, false);
+        ah1 = __builtin_amdgcn_sdot4(int(nhi[2]), int(h1.y), ah1, false);
+        al0 = __builtin_amdgcn_sdot4(int(nlo[2]), int(l1.x), al0, false);
+        al1 = __builtin_amdgcn_sdot4(int(nhi[2]), int(l1.y), al1, false);
+        ah0 = __builtin_amdgcn_sdot4(int(nlo[3]), int(h1.z), ah0, false);
+        ah1 = __builtin_amdgcn_sdot4(int(nhi[3]), int(h1.w), ah1, false);
+        al0 = __builtin_amdgcn_sdot4(int(nlo[3]), int(l1.z), al0, false);
+        al1 = __builtin_amdgcn_sdot4(int(nhi[3]), int(l1.w), al1, false);
+        const int isum = ((ah0 + ah1) << 8) + (al0 + al1) + xoff[m][gl];
+        acc[m] = fmaf(float(isum), sc[g] * xs2[m][gl], acc[m]);
       }
     }
   }
 
-  // 4) Split-K combine: the last slice of a tile to finish sums all slices.
-  //    Partials travel as device-scope atomic stores/loads, which are coherent
-  //    across XCDs by themselves; the writer only has to wait for their
-  //    completion before taking its ticket.  (A device-scope fence would write
-  //    back and invalidate the whole L2 in every workgroup.)
+  // 4) Combine the four waves in LDS (fixed order: 0+1+2+3).
+  if (wave > 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) red[wave - 1][m][lane] = acc[m];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = ((acc[m] + red[0][m][lane]) + red[1][m][lane]) + red[2][m][lane];
+
+  // 5) Split-K across workgroups: the last slice of a tile to finish sums all
+  //    slices in slice order.  Partials travel as device-scope atomic
+  //    stores/loads, which are coherent across XCDs by themselves; the writer
+  //    only waits for their completion before taking its ticket (a
+  //    device-scope fence would write back and invalidate the whole L2).
   if (slices > 1) {
     float *part = a.partial + (size_t(tile) * slices + slice) * MT * 64;
+    if (a.xcd_local) {
+      // Every slice of this tile runs on XCD (blockIdx % 8); the partials meet
+      // in that XCD's L2.  Verify the placement: a mismatch is reported, never
+      // silently combined.
+      if (lane == 0 && int(__builtin_amdgcn_s_getreg((3 << 11) | 20)) != int(blockIdx.x & 7)) atomicOr(a.err, 4);
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-      __hip_atomic_store(part + m * 64 + lane, acc[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int m = 0; m < MT; ++m) part[m * 64 + lane] = acc[m];
+    } else {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        __hip_atomic_store(part + m * 64 + lane, acc[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);  // partial stores complete before the ticket
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -162,18 +269,37 @@ __global__ __launch_bounds__(64) void k_int4_matvec(const I4Launch a, const int 
     ticket = __shfl(ticket, 0);
     if (ticket != unsigned(slices - 1)) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const float *pt = a.partial + size_t(tile) * slices * MT * 64;
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-    for (int s2 = 0; s2 < slices; ++s2) {
-      const float *ps = a.partial + (size_t(tile) * slices + s2) * MT * 64;
+    constexpr int PU = MT >= 8 ? 2 : (MT >= 4 ? 4 : 16);  // independent partial loads in flight
+    for (int s0 = 0; s0 < slices; s0 += PU) {
+      float v[PU][MT];
+      if (a.xcd_local) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
-        acc[m] += __hip_atomic_load(ps + m * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < PU; ++j)
+          if (s0 + j < slices)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) v[j][m] = pt[(size_t(s0 + j) * MT + m) * 64 + lane];
+      } else {
+#pragma unroll
+        for (int j = 0; j < PU; ++j)
+          if (s0 + j < slices)
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+              v[j][m] = __hip_atomic_load(pt + (size_t(s0 + j) * MT + m) * 64 + lane, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int j = 0; j < PU; ++j)
+        if (s0 + j < slices)
+#pragma unroll
+          for (int m = 0; m < MT; ++m) acc[m] += v[j][m];
     }
     if (lane == 0) __hip_atomic_store(&a.counters[tile * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  // 5) Epilogue.
+  // 6) Epilogue.
   if (a.mode == I4_SWIGLU) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -234,12 +360,12 @@ __global__ void k_int4_dequant(I4Layout l, const uint4 *__restrict__ nib, const 
 }
 
 template <int MT>
-void launch_mt(const I4Launch &a, int gs, int slices, int grid, hipStream_t st) {
-  switch (gs) {
-    case 4: hipLaunchKernelGGL((k_int4_matvec<MT, 4>), dim3(grid), dim3(64), 0, st, a, slices); break;
-    case 8: hipLaunchKernelGGL((k_int4_matvec<MT, 8>), dim3(grid), dim3(64), 0, st, a, slices); break;
-    case 16: hipLaunchKernelGGL((k_int4_matvec<MT, 16>), dim3(grid), dim3(64), 0, st, a, slices); break;
-    default: hipLaunchKernelGGL((k_int4_matvec<MT, 32>), dim3(grid), dim3(64), 0, st, a, slices); break;
+void launch_mt(const I4Launch &a, int gsw, int slices, int grid, hipStream_t st) {
+  switch (gsw) {
+    case 1: hipLaunchKernelGGL((k_int4_matvec<MT, 1>), dim3(grid), dim3(256), 0, st, a, slices); break;
+    case 2: hipLaunchKernelGGL((k_int4_matvec<MT, 2>), dim3(grid), dim3(256), 0, st, a, slices); break;
+    case 4: hipLaunchKernelGGL((k_int4_matvec<MT, 4>), dim3(grid), dim3(256), 0, st, a, slices); break;
+    default: hipLaunchKernelGGL((k_int4_matvec<MT, 8>), dim3(grid), dim3(256), 0, st, a, slices); break;
   }
 }
 
@@ -250,23 +376,25 @@ int env_int(const char *name, int dflt) {
 
 }  // namespace
 
-void int4_plan(const I4Layout &l, int m, int *gs, int *slices) {
+// Groups per wavefront (GSW); a workgroup slice is 4*GSW groups.  The default
+// targets about 6k wavefronts per launch with at most ~40 slices per tile.
+void int4_plan(const I4Layout &l, int m, int *gsw, int *slices) {
   const int tiles8 = (l.tiles + 7) / 8 * 8;
-  const int target = env_int("QNN_I4_TARGET_WAVES", 2048);
-  int forced = env_int("QNN_I4_GS", 0);
-  int cap = m >= 8 ? 16 : 32;  // LDS and VGPR budget for many tokens
-  int pick = 4;
-  if (forced == 4 || forced == 8 || forced == 16 || forced == 32) {
+  const int target = env_int("QNN_I4_TARGET_WAVES", 3000);
+  const int forced = env_int("QNN_I4_GSW", 0);
+  const int cap = m >= 8 ? 4 : 8;  // LDS and VGPR budget for many tokens
+  int pick = 1;
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) {
     pick = std::min(forced, cap);
   } else {
-    const int cands[] = {32, 16, 8};
+    const int cands[] = {4, 2};  // 8 groups per wave was never faster at M = 1
     for (int c : cands) {
       if (c > cap) continue;
-      if (size_t(tiles8) * ((l.g4 + c - 1) / c) >= size_t(target)) { pick = c; break; }
+      if (size_t(tiles8) * ((l.g4 + 4 * c - 1) / (4 * c)) * 4 >= size_t(target)) { pick = c; break; }
     }
   }
-  *gs = pick;
-  *slices = (l.g4 + pick - 1) / pick;
+  *gsw = pick;
+  *slices = (l.g4 + 4 * pick - 1) / (4 * pick);
 }
 
 size_t int4_partial_floats(const I4Layout &l, int m, int slices) {
@@ -281,7 +409,7 @@ void int4_matvec_launch(const I4Launch &a, int gs, int slices, hipStream_t st) {
   else if (a.m <= 2) launch_mt<2>(a, gs, slices, grid, st);
   else if (a.m <= 4) launch_mt<4>(a, gs, slices, grid, st);
   else if (a.m <= 8) launch_mt<8>(a, gs, slices, grid, st);
-  else launch_mt<16>(a, std::min(gs, 16), slices, grid, st);
+  else launch_mt<16>(a, std::min(gs, 4), slices, grid, st);
   hip_check(hipGetLastError(), "int4 matvec launch");
 }
 

@@ -94,6 +94,7 @@ struct I4Launch {
   const void *scl2 = nullptr;
   const float *x = nullptr;
   int x_stride = 0;  // floats between activation rows
+  int x_vec4 = 0;    // x and x_stride allow 16-byte loads
   float *y = nullptr;
   int y_stride = 0;
   int k = 0, n = 0, m = 1;  // input features, valid output rows, tokens (<= 16)
@@ -102,7 +103,10 @@ struct I4Launch {
   const float *prob = nullptr;  // I4_ACCUM: pointer to p
   float *partial = nullptr;     // split-K scratch
   unsigned *counters = nullptr;
+  int xcd_local = 0;            // combine slices through the XCD's L2 (placement verified)
+  int *err = nullptr;           // error word (bit 4: unexpected XCD placement)
 };
+bool xcd_probe(hipStream_t s);  // true when workgroup b runs on XCD b % 8
 // Chooses the split-K slice and returns (partial floats, counters) needed.
 void int4_plan(const I4Layout &l, int m, int *gs, int *slices);
 size_t int4_partial_floats(const I4Layout &l, int m, int slices);
@@ -146,6 +150,30 @@ struct MoELaunch {
 size_t moe_workspace_bytes(const MoELaunch &a, size_t *plan_off, size_t *h_off, size_t *y_off, size_t *part_off,
                            size_t *cnt_off);
 void moe_launch(const MoELaunch &a, hipStream_t s);
+
+// Persistent INT4 MLP layer stack (qnn_mlp.hip).
+struct MlpLayerPtrs {
+  const uint4 *gnib; const float *gscl;  // gate
+  const uint4 *unib; const float *uscl;  // up
+  const uint4 *dnib; const float *dscl;  // down
+};
+struct MlpArgs {
+  const MlpLayerPtrs *w = nullptr;  // device array [layers]
+  int layers = 0, hidden = 0, inter = 0;
+  int g4_gu = 0, g4_d = 0, tiles_gu = 0, tiles_d = 0, slices_gu = 0, slices_d = 0;
+  const float *x0 = nullptr;
+  float *out = nullptr;
+  float *hbuf = nullptr, *ybuf = nullptr;      // [2][inter], [2][hidden]
+  float *part_gu = nullptr, *part_d = nullptr;  // [tiles][slices][64]
+  unsigned *tick_gu = nullptr, *tick_d = nullptr;                 // stride kCounterStride
+  unsigned long long *flag_gu = nullptr, *flag_d = nullptr;       // stride 8
+  unsigned long long *epoch = nullptr;
+  unsigned *exit_count = nullptr, *abort = nullptr;
+  int *err = nullptr;
+  unsigned spin_limit = 0;
+};
+int mlp_stack_grid(int gswu, int gswd, int want);
+void mlp_stack_launch(const MlpArgs &a, int gswu, int gswd, int grid, hipStream_t s);
 
 // GGUF (qnn_gguf.hip).
 GGLayout gguf_layout(int enc, int rows, int cols);
