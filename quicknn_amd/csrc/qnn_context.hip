@@ -427,6 +427,35 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
   }
 }
 
+// ---------------------------------------------------------------- Q8_0 multi-row GEMM
+bool q8_gemm_available() { return false; }
+void run_q8_gemm(qnn_ctx_s *, const WeightEntry *, const float *, float *, int, int, int) {
+  fail(QNN_E_NOT_SUPPORTED, "Q8_0 GEMM not built yet");
+}
+
+// ---------------------------------------------------------------- GGUF projection
+void run_gguf(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
+              int out_dim) {
+  GGArgs a;
+  a.l = w->gg;
+  a.w = w->dptr;
+  a.w2 = w2 ? w2->dptr : nullptr;
+  a.x = x;
+  a.x_vec4 = (w->gg.cols % 4 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  a.y = y;
+  a.n = out_dim;
+  a.tiles = mode >= GG_SWIGLU ? (out_dim + 31) / 32 : w->gg.tiles;
+  a.mode = mode;
+  int bw, slices;
+  gguf_plan(w->gg, a.tiles, &bw, &slices);
+  ensure_splitk(ctx, slices > 1 ? size_t(a.tiles) * slices * 64 : 0, size_t(a.tiles) * kCounterStride);
+  a.partial = ctx->partial;
+  a.counters = ctx->counters;
+  a.xcd_local = ctx->xcd_local ? 1 : 0;
+  a.err = ctx->error_flag;
+  gguf_matvec_launch(a, bw, slices, ctx->stream);
+}
+
 }  // namespace
 }  // namespace qnn
 
@@ -755,7 +784,19 @@ int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_
       run_int4(ctx, eg, eu, I4_SWIGLU, src->ptr, dst->ptr, 1, in_dim, out_dim, nullptr);
       ctx->st.int4_calls += 2;
     } else {
-      fail(QNN_E_NOT_SUPPORTED, "GGUF fused SwiGLU not built yet");
+      WeightEntry *eg = pin(acquire_gguf(ctx, gate, out_dim, in_dim));
+      WeightEntry *eu = pin(acquire_gguf(ctx, up, out_dim, in_dim));
+      if (gate->encoding == up->encoding) {
+        run_gguf(ctx, eg, eu, GG_SWIGLU, src->ptr, dst->ptr, out_dim);  // one weight stream (op 67)
+      } else {  // encodings differ: two matvecs and the elementwise SwiGLU
+        qnn_tensor_s *g = new_tensor(ctx, out_dim), *u = new_tensor(ctx, out_dim);
+        run_gguf(ctx, eg, nullptr, GG_STORE, src->ptr, g->ptr, out_dim);
+        run_gguf(ctx, eu, nullptr, GG_STORE, src->ptr, u->ptr, out_dim);
+        misc_glu(dst->ptr, g->ptr, u->ptr, out_dim, out_dim, 0, 0, ctx->stream);
+        g->live = false;
+        u->live = false;
+      }
+      ctx->st.gguf_calls += 2;
     }
     ctx->st.gemm_calls += 2;
     return QNN_OK;
@@ -770,10 +811,25 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
     check_tensor(ctx, dst, int64_t(rows) * out_dim);
     if (rows < 1 || in_dim < 1 || out_dim < 1 || src == dst)
       fail(QNN_E_ARGUMENT, "Invalid resident linear dimensions/alias");
-    (void)scales;
-    (void)bias;
     check_weight_desc(w);
-    fail(QNN_E_NOT_SUPPORTED, "GGUF projections not built yet");
+    if (scales && scales->data) fail(QNN_E_NOT_SUPPORTED, "INT8 ConvRot weights are not handled by the HIP backend");
+    if (!is_gguf(w->encoding))
+      fail(QNN_E_NOT_SUPPORTED, "Linear handles GGUF weights; native INT4 goes through Int4Linear");
+    OpPins pin;
+    WeightEntry *e = pin(acquire_gguf(ctx, w, out_dim, in_dim));
+    if (rows == 1 || w->encoding != QNN_WE_Q8_0 || !q8_gemm_available()) {
+      // Matvec per row (op 65); rows > 1 of K-quants reuse it row by row.
+      for (int r = 0; r < rows; ++r)
+        run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim, out_dim);
+    } else {
+      run_q8_gemm(ctx, e, src->ptr, dst->ptr, rows, in_dim, out_dim);
+    }
+    if (bias && bias->data) {
+      WeightEntry *b = pin(acquire_raw(ctx, bias, out_dim));
+      misc_bias_add(dst->ptr, b->dptr, b->raw_dtype == QNN_DT_BF16, rows, out_dim, ctx->stream);
+    }
+    ctx->st.gemm_calls++;
+    ctx->st.gguf_calls++;
     return QNN_OK;
   });
 }

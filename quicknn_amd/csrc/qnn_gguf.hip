@@ -1,15 +1,609 @@
-// qnn_gguf.hip -- GGUF K-quant / Q8_0 kernels (placeholder until the GGUF path lands).
+// qnn_gguf.hip -- GGML block formats (Q8_0, Q4_K, Q6_K, Q3_K, Q2_K) for gfx950.
+//
+// Formats and decode rules: src/io/QuickNN.GGUF.Quantization.pas:136-253
+// (GGUFValue); the matvec replaces op 65 (ggufvector.comp:34-52) and the GGUF
+// gate/up SwiGLU op 67.
+//
+// Device layout.  Rows are tiled by 64 (one row per lane).  Each row is cut
+// into 256-element units (a K-quant super-block, or 8 Q8_0 blocks).  The bytes
+// of a unit are split into a "main" part whose size is a multiple of 16 bytes
+// and up to two small side fields, each stored lane-interleaved:
+//     main:  16 B at ((t*U + u)*C + c)*64 + r      (C chunks per unit)
+//     side1: S1 B at ((t*U + u)*64 + r)            side2 likewise
+//   Q4_K  (144 B): main 144 (C=9)
+//   Q6_K  (210 B): main ql|qh|scales 208 (C=13), side1 d (2)
+//   Q3_K  (110 B): main hmask|qs 96 (C=6), side1 scales (12), side2 d (2)
+//   Q2_K   (84 B): main scales|qs 80 (C=5), side1 d|dmin (4)
+//   Q8_0 (8x34 B): main 8x32 quants (C=16), side1 8 fp16 d (16)
+// so every wave load is a 16-byte (or 12/4/2-byte) load by 64 consecutive
+// lanes.  Bytes per weight are unchanged.
+//
+// Matvec.  The activation slice is quantised per 32 elements to 16-bit fixed
+// point (x ~= s2 (256 q1 + q2), as in qnn_int4.hip) and each format's quants
+// are unpacked into byte lanes for v_dot4_i32_i8; scale and min terms are
+// applied once per sub-block:
+//   Q4_K: sum = s2 * (d*sc * dot(q, X) - dmin*m * sum(X))       (sub-block 32)
+//   Q2_K: sum = s2 * (d*sc * dot(q, X) - dmin*m * sum(X))       (sub-block 16)
+//   Q6_K: sum = s2 * d*sc * (dot(q6, X) - 32 sum(X))            (q6 = q + 32)
+//   Q3_K: sum = s2 * d*(sc-32) * (dot(q3, X) - 4 sum(X))        (q3 = q + 4)
+//   Q8_0: sum = s2 * d * dot(q, X)
+// where X = 256 q1 + q2 and every dot is exact integer arithmetic.
 #include "qnn_internal.h"
 
 namespace qnn {
+namespace {
+
+__device__ __forceinline__ float silu_dev(float g) {
+  return g >= 20.0f ? g : (g <= -20.0f ? 0.0f : g / (1.0f + expf(-g)));
+}
+__device__ __forceinline__ uint32_t sel4u(const uint4 &v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+// Exact binary16 -> binary32 (v_cvt_f32_f16; fp16 denormals are preserved).
+__device__ __forceinline__ float half_f(uint32_t h) {
+  const uint16_t b = uint16_t(h);
+  _Float16 f;
+  __builtin_memcpy(&f, &b, 2);
+  return float(f);
+}
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(int(a), int(b), c, false);
+}
+
+__device__ __forceinline__ bool map_tile_slice(int b, int slices, int tiles, int &tile, int &slice) {
+  const int xcd = b & 7, k = b >> 3;
+  const int q = k / slices;
+  tile = q * 8 + xcd;
+  slice = k - q * slices;
+  return tile < tiles;
+}
+
+// ---------------------------------------------------------------- format table
+template <int ENC> struct Fmt;
+template <> struct Fmt<QNN_WE_Q4_K> { static constexpr int C = 9, S1 = 0, S2 = 0; };
+template <> struct Fmt<QNN_WE_Q6_K> { static constexpr int C = 13, S1 = 2, S2 = 0; };
+template <> struct Fmt<QNN_WE_Q3_K> { static constexpr int C = 6, S1 = 12, S2 = 2; };
+template <> struct Fmt<QNN_WE_Q2_K> { static constexpr int C = 5, S1 = 4, S2 = 0; };
+template <> struct Fmt<QNN_WE_Q8_0> { static constexpr int C = 16, S1 = 16, S2 = 0; };
+
+struct Planes {
+  const uint8_t *main;
+  const uint8_t *side1;
+  const uint8_t *side2;
+};
+
+__device__ __forceinline__ Planes planes_of(const GGLayout &l, const void *w) {
+  const uint8_t *b = static_cast<const uint8_t *>(w);
+  Planes p;
+  p.main = b;
+  p.side1 = b + l.side1_off;
+  p.side2 = b + l.side2_off;
+  return p;
+}
+
+// Original byte `o` (0 <= o < unit bytes) of unit (t, u) row r, through the
+// plane mapping.  Used by the repack (inverse) and the bit-exact dequant.
+__device__ __forceinline__ void plane_addr(int enc, const GGLayout &l, int t, int u, int r, int o, int &plane,
+                                           size_t &off) {
+  const size_t tu = size_t(t) * l.units + u;
+  auto main_at = [&](int m) { plane = 0; off = ((tu * l.main_chunks + (m >> 4)) * 64 + r) * 16 + (m & 15); };
+  auto s1_at = [&](int m) { plane = 1; off = (tu * 64 + r) * l.side1_bytes + m; };
+  auto s2_at = [&](int m) { plane = 2; off = (tu * 64 + r) * l.side2_bytes + m; };
+  switch (enc) {
+    case QNN_WE_Q4_K: main_at(o); break;
+    case QNN_WE_Q6_K: if (o < 208) main_at(o); else s1_at(o - 208); break;
+    case QNN_WE_Q3_K: if (o < 96) main_at(o); else if (o < 108) s1_at(o - 96); else s2_at(o - 108); break;
+    case QNN_WE_Q2_K: if (o < 80) main_at(o); else s1_at(o - 80); break;
+    default: {  // Q8_0 unit: block k = o / 34, byte j = o % 34: d at j < 2, quants after
+      const int k = o / 34, j = o % 34;
+      if (j < 2) s1_at(2 * k + j); else main_at(32 * k + j - 2);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t fetch(int enc, const GGLayout &l, const Planes &p, int t, int u, int r, int o) {
+  int plane;
+  size_t off;
+  plane_addr(enc, l, t, u, r, o, plane, off);
+  return plane == 0 ? p.main[off] : (plane == 1 ? p.side1[off] : p.side2[off]);
+}
+
+// GGUFValue (src/io/QuickNN.GGUF.Quantization.pas:136-253) over the tiled
+// copy: element i of unit (t, u), row r.  Same arithmetic, so the same bits.
+__device__ float gguf_value_tiled(int enc, const GGLayout &l, const Planes &p, int t, int u, int r, int i) {
+  auto B = [&](int o) { return fetch(enc, l, p, t, u, r, o); };
+  auto H = [&](int o) { return half_f(B(o) | (B(o + 1) << 8)); };
+  auto SB = [](uint32_t v) { return v >= 128 ? int(v) - 256 : int(v); };
+  switch (enc) {
+    case QNN_WE_Q8_0: {
+      const int k = i / 32, j = i % 32;
+      return H(34 * k) * float(SB(B(34 * k + 2 + j)));
+    }
+    case QNN_WE_Q2_K: {
+      const int group = i / 16;
+      const int q = int((B(16 + (i / 128) * 32 + i % 32) >> (((i % 128) / 32) * 2)) & 3);
+      return (H(80) * float(B(group) & 15)) * float(q) - H(82) * float(B(group) >> 4);
+    }
+    case QNN_WE_Q4_K: {
+      const int group = i / 32;
+      int scale, minimum;
+      if (group < 4) {
+        scale = int(B(4 + group) & 63);
+        minimum = int(B(8 + group) & 63);
+      } else {
+        scale = int((B(8 + group) & 15) | ((B(group) >> 6) << 4));
+        minimum = int((B(8 + group) >> 4) | ((B(4 + group) >> 6) << 4));
+      }
+      const int q = int((B(16 + (i / 64) * 32 + i % 32) >> ((group & 1) * 4)) & 15);
+      return (H(0) * float(scale)) * float(q) - H(2) * float(minimum);
+    }
+    case QNN_WE_Q6_K: {
+      const int part = i / 128, quarter = (i % 128) / 32, lane = i % 32;
+      const int q = int(((B(part * 64 + (quarter & 1) * 32 + lane) >> ((quarter / 2) * 4)) & 15) |
+                        (((B(128 + part * 32 + lane) >> (quarter * 2)) & 3) << 4));
+      const int scale = SB(B(192 + i / 16));
+      return (H(208) * float(scale)) * float(q - 32);
+    }
+    default: {  // Q3_K
+      const int group = i / 16;
+      const int scale = int(((B(96 + group % 8) >> ((group / 8) * 4)) & 15) |
+                            (((B(104 + group % 4) >> ((group / 4) * 2)) & 3) << 4));
+      int q = int((B(32 + (i / 128) * 32 + i % 32) >> (((i % 128) / 32) * 2)) & 3);
+      if ((B(i % 32) & (1u << (i / 32))) == 0) q -= 4;
+      return (H(108) * float(scale - 32)) * float(q);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- repack / dequant kernels
+__global__ void k_gguf_repack(const uint8_t *__restrict__ src, GGLayout l, uint8_t *__restrict__ dst) {
+  const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t total = size_t(l.tiles) * l.units * 64;
+  if (idx >= total) return;
+  const int r = int(idx & 63);
+  const int u = int((idx >> 6) % l.units);
+  const int t = int(idx / (size_t(l.units) * 64));
+  const int row = t * 64 + r;
+  const int ub = l.unit_bytes;
+  const size_t row_bytes = size_t(l.src_row_bytes);
+  for (int o = 0; o < ub; ++o) {
+    uint8_t v = 0;
+    if (row < l.rows) {
+      const size_t so = size_t(u) * ub + o;  // Q8_0 units past the row end are zero blocks (d = 0)
+      if (so < row_bytes) v = src[size_t(row) * row_bytes + so];
+    }
+    int plane;
+    size_t off;
+    plane_addr(l.enc, l, t, u, r, o, plane, off);
+    dst[(plane == 0 ? 0 : (plane == 1 ? l.side1_off : l.side2_off)) + off] = v;
+  }
+}
+
+__global__ void k_gguf_dequant(GGLayout l, const uint8_t *__restrict__ w, float *__restrict__ out) {
+  const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t total = size_t(l.rows) * l.cols;
+  if (idx >= total) return;
+  const int row = int(idx / l.cols), k = int(idx % l.cols);
+  const Planes p = planes_of(l, w);
+  out[idx] = gguf_value_tiled(l.enc, l, p, row / 64, k / 256, row & 63, k % 256);
+}
+
+// ---------------------------------------------------------------- matvec
+// Fixed-point activation slice of one token, in LDS: per 32-group 8 words of
+// q1 and q2 bytes (element order), s2, and the sums of X = 256 q1 + q2 over
+// the group and over each 16-element half.
+template <int NG>
+struct XSlice {
+  uint32_t h[NG][8];
+  uint32_t l[NG][8];
+  float s2[NG];
+  int sum32[NG];
+  int sum16[NG][2];
+};
+
+// Exact integer dot of four quant bytes with four activation bytes (q1, q2).
+__device__ __forceinline__ int xdot(uint32_t q, uint32_t xh, uint32_t xl, int &acc_h, int &acc_l) {
+  acc_h = dot4(q, xh, acc_h);
+  acc_l = dot4(q, xl, acc_l);
+  return 0;
+}
+
+template <int NG>
+__device__ __forceinline__ int combine(int ah, int al) { return (ah << 8) + al; }
+
+// Unit dot products.  `mw` = main chunks (registers), s1/s2 side words.
+// g0: first 32-group of this unit within the LDS slice.
+template <int NG>
+__device__ float unit_q8_0(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int g0) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {  // block k: quants in chunks 2k, 2k+1
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xdot(sel4u(mw[2 * k + c], j), xs.h[g0 + k][4 * c + j], xs.l[g0 + k][4 * c + j], ah, al);
+    const uint32_t dw = sel4u(s1, k >> 1);
+    const float d = half_f((k & 1) ? (dw >> 16) : (dw & 0xFFFFu));
+    acc = fmaf(float(combine<NG>(ah, al)), d * xs.s2[g0 + k], acc);
+  }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_q4_k(const uint4 *mw, const XSlice<NG> &xs, int g0) {
+  const uint4 hd = mw[0];
+  const float d = half_f(hd.x & 0xFFFFu), dmin = half_f(hd.x >> 16);
+  const uint32_t s0 = hd.y, s4 = hd.z, s8 = hd.w;  // scale bytes 0-3, 4-7, 8-11
+  auto byte = [&](int b) -> uint32_t {
+    const uint32_t w = b < 4 ? s0 : (b < 8 ? s4 : s8);
+    return (w >> (8 * (b & 3))) & 255u;
+  };
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int sc, m;
+    if (j < 4) {
+      sc = int(byte(j) & 63);
+      m = int(byte(4 + j) & 63);
+    } else {
+      sc = int((byte(4 + j) & 15) | ((byte(j - 4) >> 6) << 4));
+      m = int((byte(4 + j) >> 4) | ((byte(j) >> 6) << 4));
+    }
+    int ah = 0, al = 0;
+    // quants of sub-block j: bytes (j/2)*32 .. +31 of the quant area (chunks 1 + 2*(j/2), +1)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t qd = sel4u(mw[1 + 2 * (j >> 1) + c], w);
+        const uint32_t q = (j & 1) ? ((qd >> 4) & 0x0F0F0F0Fu) : (qd & 0x0F0F0F0Fu);
+        xdot(q, xs.h[g0 + j][4 * c + w], xs.l[g0 + j][4 * c + w], ah, al);
+      }
+    const float isum = float(combine<NG>(ah, al));
+    acc = fmaf(xs.s2[g0 + j], (d * float(sc)) * isum - (dmin * float(m)) * float(xs.sum32[g0 + j]), acc);
+  }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_q6_k(const uint4 *mw, uint32_t side, const XSlice<NG> &xs, int g0) {
+  const float d = half_f(side & 0xFFFFu);
+  float acc = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // elements 128p + 32q .. +31 = 32-group 4p + q
+      const int g = 4 * p + q;
+      int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int qlw = p * 16 + (q & 1) * 8 + k;  // ql dword (chunks 0-7)
+        const int qhw = 32 + p * 8 + k;            // qh dword (chunks 8-11)
+        const uint32_t ql = sel4u(mw[qlw >> 2], qlw & 3), qh = sel4u(mw[qhw >> 2], qhw & 3);
+        const uint32_t v = ((ql >> ((q >> 1) * 4)) & 0x0F0F0F0Fu) | (((qh >> (2 * q)) & 0x03030303u) << 4);
+        if (k < 4) xdot(v, xs.h[g0 + g][k], xs.l[g0 + g][k], ah0, al0);
+        else xdot(v, xs.h[g0 + g][k], xs.l[g0 + g][k], ah1, al1);
+      }
+      const uint4 scw = mw[12];
+      const int sb0 = 2 * g, sb1 = 2 * g + 1;  // 16-element sub-blocks
+      const int sc0 = int(int8_t((sel4u(scw, sb0 >> 2) >> (8 * (sb0 & 3))) & 255u));
+      const int sc1 = int(int8_t((sel4u(scw, sb1 >> 2) >> (8 * (sb1 & 3))) & 255u));
+      const int i0 = combine<NG>(ah0, al0) - 32 * xs.sum16[g0 + g][0];
+      const int i1 = combine<NG>(ah1, al1) - 32 * xs.sum16[g0 + g][1];
+      acc = fmaf(xs.s2[g0 + g] * d, float(sc0) * float(i0) + float(sc1) * float(i1), acc);
+    }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_q3_k(const uint4 *mw, uint4 s1, uint32_t s2w, const XSlice<NG> &xs, int g0) {
+  const float d = half_f(s2w & 0xFFFFu);
+  auto sbyte = [&](int b) -> uint32_t { return (sel4u(s1, b >> 2) >> (8 * (b & 3))) & 255u; };
+  float acc = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int g = 4 * p + q;
+      int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int qsw = 8 + p * 8 + k;  // qs dword (chunks 2-5)
+        const int hmw = k;              // hmask dword (chunks 0-1)
+        const uint32_t qs = sel4u(mw[qsw >> 2], qsw & 3), hm = sel4u(mw[hmw >> 2], hmw & 3);
+        const uint32_t v = ((qs >> (2 * q)) & 0x03030303u) | (((hm >> (4 * p + q)) & 0x01010101u) << 2);
+        if (k < 4) xdot(v, xs.h[g0 + g][k], xs.l[g0 + g][k], ah0, al0);
+        else xdot(v, xs.h[g0 + g][k], xs.l[g0 + g][k], ah1, al1);
+      }
+      int sc[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int sb = 2 * g + hh;
+        sc[hh] = int(((sbyte(sb % 8) >> ((sb / 8) * 4)) & 15) | (((sbyte(8 + sb % 4) >> ((sb / 4) * 2)) & 3) << 4)) - 32;
+      }
+      const int i0 = combine<NG>(ah0, al0) - 4 * xs.sum16[g0 + g][0];
+      const int i1 = combine<NG>(ah1, al1) - 4 * xs.sum16[g0 + g][1];
+      acc = fmaf(xs.s2[g0 + g] * d, float(sc[0]) * float(i0) + float(sc[1]) * float(i1), acc);
+    }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_q2_k(const uint4 *mw, uint32_t side, const XSlice<NG> &xs, int g0) {
+  const float d = half_f(side & 0xFFFFu), dmin = half_f(side >> 16);
+  float acc = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int g = 4 * p + q;
+      int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int qsw = 4 + p * 8 + k;  // qs dword (chunks 1-4)
+        const uint32_t qs = sel4u(mw[qsw >> 2], qsw & 3);
+        const uint32_t v = (qs >> (2 * q)) & 0x03030303u;
+        if (k < 4) xdot(v, xs.h[g0 + g][k], xs.l[g0 + g][k], ah0, al0);
+        else xdot(v, xs.h[g0 + g][k], xs.l[g0 + g][k], ah1, al1);
+      }
+      float part = 0.0f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int sb = 2 * g + hh;
+        const uint32_t sm = (sel4u(mw[0], sb >> 2) >> (8 * (sb & 3))) & 255u;
+        const int isum = hh ? combine<NG>(ah1, al1) : combine<NG>(ah0, al0);
+        part += (d * float(sm & 15)) * float(isum) - (dmin * float(sm >> 4)) * float(xs.sum16[g0 + g][hh]);
+      }
+      acc = fmaf(xs.s2[g0 + g], part, acc);
+    }
+  return acc;
+}
+
+// Workgroup = 4 waves on one 64-row tile (SWIGLU: 32 gate rows in lanes
+// 0-31, the same 32 up rows in lanes 32-63); slice = 4*BW units, wave w
+// streams units [w*BW, (w+1)*BW) of it.
+template <int ENC, int BW>
+__global__ __launch_bounds__(256) void k_gguf_matvec(const GGArgs a, const int slices) {
+  using F = Fmt<ENC>;
+  constexpr int U = 4 * BW;   // units per slice
+  constexpr int NG = U * 8;   // 32-groups per slice
+  int tile, slice;
+  if (!map_tile_slice(blockIdx.x, slices, a.tiles, tile, slice)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const GGLayout &l = a.l;
+  const int u0 = slice * U;
+  const int nu = min(U, l.units - u0);
+  const int uw0 = wave * BW;
+  const int nuw = max(0, min(BW, nu - uw0));
+
+  // 1) activation slice (elements [u0*256, (u0+nu)*256) of token 0)
+  constexpr int XIT = (U * 256 + 1023) / 1024;
+  float4 xr[XIT];
+#pragma unroll
+  for (int it = 0; it < XIT; ++it) {
+    const int e = (it * 256 + tid) * 4, kk = u0 * 256 + e;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e < nu * 256) {
+      if (kk + 3 < l.cols && a.x_vec4) v = *reinterpret_cast<const float4 *>(a.x + kk);
+      else {
+        if (kk < l.cols) v.x = a.x[kk];
+        if (kk + 1 < l.cols) v.y = a.x[kk + 1];
+        if (kk + 2 < l.cols) v.z = a.x[kk + 2];
+        if (kk + 3 < l.cols) v.w = a.x[kk + 3];
+      }
+    }
+    xr[it] = v;
+  }
+  // 2) weights of this wave's units
+  int stile = tile, srow = lane;
+  const void *wb = a.w;
+  if (a.mode >= GG_SWIGLU) {
+    stile = tile >> 1;
+    srow = (tile & 1) * 32 + (lane & 31);
+    if (lane >= 32) wb = a.w2;
+  }
+  const Planes P = planes_of(l, wb);
+  uint4 mw[BW][F::C];
+  uint4 s1v[BW];
+  uint32_t s1w[BW], s2w[BW];
+#pragma unroll
+  for (int b = 0; b < BW; ++b) {
+    if (b < nuw) {
+      const size_t tu = size_t(stile) * l.units + (u0 + uw0 + b);
+      const uint4 *mp = reinterpret_cast<const uint4 *>(P.main) + (tu * F::C) * 64 + srow;
+#pragma unroll
+      for (int c = 0; c < F::C; ++c) mw[b][c] = mp[c * 64];
+      if (F::S1 == 16) s1v[b] = reinterpret_cast<const uint4 *>(P.side1)[tu * 64 + srow];
+      if (F::S1 == 12) {
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(P.side1 + (tu * 64 + srow) * 12);
+        s1v[b] = make_uint4(q[0], q[1], q[2], 0u);
+      }
+      if (F::S1 == 4) s1w[b] = reinterpret_cast<const uint32_t *>(P.side1)[tu * 64 + srow];
+      if (F::S1 == 2) s1w[b] = reinterpret_cast<const uint16_t *>(P.side1)[tu * 64 + srow];
+      if (F::S2 == 2) s2w[b] = reinterpret_cast<const uint16_t *>(P.side2)[tu * 64 + srow];
+    }
+  }
+  // 3) quantise the activation slice (natural element order)
+  __shared__ XSlice<NG> xs;
+  __shared__ float red[3][64];
+#pragma unroll
+  for (int it = 0; it < XIT; ++it) {
+    const int e = (it * 256 + tid) * 4;
+    const float4 v = xr[it];
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const float s1 = amax / 127.0f;
+    const float inv = s1 > 0.0f ? 1.0f / s1 : 0.0f;
+    const float inv2 = inv * 256.0f;
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t hw = 0, lw = 0;
+    int sumq = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q1 = fminf(127.0f, fmaxf(-127.0f, rintf(vv[j] * inv)));
+      const float r = fmaf(-q1, s1, vv[j]);
+      const float q2 = fminf(127.0f, fmaxf(-127.0f, rintf(r * inv2)));
+      hw |= (uint32_t(int(q1)) & 255u) << (8 * j);
+      lw |= (uint32_t(int(q2)) & 255u) << (8 * j);
+      sumq += 256 * int(q1) + int(q2);
+    }
+    sumq += __shfl_xor(sumq, 1);
+    sumq += __shfl_xor(sumq, 2);  // 16-element sum
+    const int s16 = sumq;
+    const int s32 = s16 + __shfl_xor(s16, 4);
+    if (e < U * 256) {
+      const int g = e >> 5, k = (e >> 2) & 7;
+      xs.h[g][k] = hw;
+      xs.l[g][k] = lw;
+      if ((lane & 3) == 0) xs.sum16[g][(lane >> 2) & 1] = s16;
+      if ((lane & 7) == 0) {
+        xs.s2[g] = s1 * 0.00390625f;
+        xs.sum32[g] = s32;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4) unit dots
+  float acc = 0.0f;
+#pragma unroll
+  for (int b = 0; b < BW; ++b) {
+    if (b < nuw) {
+      const int g0 = (uw0 + b) * 8;
+      if (ENC == QNN_WE_Q8_0) acc += unit_q8_0<NG>(mw[b], s1v[b], xs, g0);
+      if (ENC == QNN_WE_Q4_K) acc += unit_q4_k<NG>(mw[b], xs, g0);
+      if (ENC == QNN_WE_Q6_K) acc += unit_q6_k<NG>(mw[b], s1w[b], xs, g0);
+      if (ENC == QNN_WE_Q3_K) acc += unit_q3_k<NG>(mw[b], s1v[b], s2w[b], xs, g0);
+      if (ENC == QNN_WE_Q2_K) acc += unit_q2_k<NG>(mw[b], s1w[b], xs, g0);
+    }
+  }
+
+  // 5) combine the 4 waves (fixed order), then split-K across workgroups
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave > 0) return;
+  acc = ((acc + red[0][lane]) + red[1][lane]) + red[2][lane];
+  if (slices > 1) {
+    float *part = a.partial + (size_t(tile) * slices + slice) * 64;
+    if (a.xcd_local) {
+      if (lane == 0 && int(__builtin_amdgcn_s_getreg((3 << 11) | 20)) != int(blockIdx.x & 7)) atomicOr(a.err, 4);
+      part[lane] = acc;
+    } else {
+      __hip_atomic_store(part + lane, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    unsigned ticket = 0;
+    if (lane == 0)
+      ticket = __hip_atomic_fetch_add(&a.counters[tile * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __shfl(ticket, 0);
+    if (ticket != unsigned(slices - 1)) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const float *pt = a.partial + size_t(tile) * slices * 64 + lane;
+    acc = 0.0f;
+    for (int s0 = 0; s0 < slices; s0 += 16) {
+      float v[16];
+      if (a.xcd_local) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (s0 + j < slices) v[j] = pt[size_t(s0 + j) * 64];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (s0 + j < slices) v[j] = __hip_atomic_load(pt + size_t(s0 + j) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (s0 + j < slices) acc += v[j];
+    }
+    if (lane == 0) __hip_atomic_store(&a.counters[tile * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // 6) epilogue
+  if (a.mode >= GG_SWIGLU) {
+    const float u = __shfl_down(acc, 32);
+    const int row = tile * 32 + lane;
+    if (lane < 32 && row < a.n) a.y[row] = silu_dev(acc) * u;
+  } else {
+    const int row = tile * 64 + lane;
+    if (row < a.n) a.y[row] = acc;
+  }
+}
+
+template <int ENC>
+void launch_enc(const GGArgs &a, int bw, int slices, int grid, hipStream_t st) {
+  if (bw == 2) hipLaunchKernelGGL((k_gguf_matvec<ENC, 2>), dim3(grid), dim3(256), 0, st, a, slices);
+  else hipLaunchKernelGGL((k_gguf_matvec<ENC, 1>), dim3(grid), dim3(256), 0, st, a, slices);
+}
+
+int env_int(const char *name, int dflt) {
+  const char *v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+
+}  // namespace
+
 GGLayout gguf_layout(int enc, int rows, int cols) {
-  (void)enc; (void)rows; (void)cols;
-  fail(QNN_E_NOT_SUPPORTED, "GGUF weights not built yet");
+  GGLayout l;
+  l.enc = enc;
+  l.rows = rows;
+  l.cols = cols;
+  l.tiles = (rows + 63) / 64;
+  l.units = (cols + 255) / 256;
+  switch (enc) {
+    case QNN_WE_Q4_K: l.main_chunks = 9; l.side1_bytes = 0; l.side2_bytes = 0; l.unit_bytes = 144; break;
+    case QNN_WE_Q6_K: l.main_chunks = 13; l.side1_bytes = 2; l.side2_bytes = 0; l.unit_bytes = 210; break;
+    case QNN_WE_Q3_K: l.main_chunks = 6; l.side1_bytes = 12; l.side2_bytes = 2; l.unit_bytes = 110; break;
+    case QNN_WE_Q2_K: l.main_chunks = 5; l.side1_bytes = 4; l.side2_bytes = 0; l.unit_bytes = 84; break;
+    case QNN_WE_Q8_0: l.main_chunks = 16; l.side1_bytes = 16; l.side2_bytes = 0; l.unit_bytes = 272; break;
+    default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
+  }
+  l.src_row_bytes = enc == QNN_WE_Q8_0 ? (cols / 32) * 34 : (cols / 256) * l.unit_bytes;
+  const size_t tu64 = size_t(l.tiles) * l.units * 64;
+  auto up256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+  l.side1_off = up256(tu64 * l.main_chunks * 16);
+  l.side2_off = l.side1_off + up256(tu64 * l.side1_bytes);
+  l.total = l.side2_off + up256(tu64 * l.side2_bytes);
+  return l;
 }
-void gguf_repack_launch(const uint8_t *, const GGLayout &, void *, hipStream_t) {
-  fail(QNN_E_NOT_SUPPORTED, "GGUF weights not built yet");
+
+void gguf_repack_launch(const uint8_t *src, const GGLayout &l, void *dst, hipStream_t s) {
+  const size_t total = size_t(l.tiles) * l.units * 64;
+  hipLaunchKernelGGL(k_gguf_repack, dim3((total + 255) / 256), dim3(256), 0, s, src, l, static_cast<uint8_t *>(dst));
+  hip_check(hipGetLastError(), "gguf repack launch");
 }
-void gguf_dequant_launch(const GGLayout &, const void *, float *, hipStream_t) {
-  fail(QNN_E_NOT_SUPPORTED, "GGUF weights not built yet");
+
+void gguf_dequant_launch(const GGLayout &l, const void *w, float *out, hipStream_t s) {
+  const size_t total = size_t(l.rows) * l.cols;
+  hipLaunchKernelGGL(k_gguf_dequant, dim3((total + 255) / 256), dim3(256), 0, s, l,
+                     static_cast<const uint8_t *>(w), out);
+  hip_check(hipGetLastError(), "gguf dequant launch");
 }
+
+void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {
+  const int tiles8 = (tiles + 7) / 8 * 8;
+  const int forced = env_int("QNN_GG_BW", 0);
+  int pick = 1;
+  if (forced == 1 || forced == 2) pick = forced;
+  else if (size_t(tiles8) * ((l.units + 7) / 8) * 4 >= 3000) pick = 2;
+  *bw = pick;
+  *slices = (l.units + 4 * pick - 1) / (4 * pick);
+}
+
+void gguf_matvec_launch(const GGArgs &a, int bw, int slices, hipStream_t s) {
+  const int grid = (a.tiles + 7) / 8 * 8 * slices;
+  switch (a.l.enc) {
+    case QNN_WE_Q4_K: launch_enc<QNN_WE_Q4_K>(a, bw, slices, grid, s); break;
+    case QNN_WE_Q6_K: launch_enc<QNN_WE_Q6_K>(a, bw, slices, grid, s); break;
+    case QNN_WE_Q3_K: launch_enc<QNN_WE_Q3_K>(a, bw, slices, grid, s); break;
+    case QNN_WE_Q2_K: launch_enc<QNN_WE_Q2_K>(a, bw, slices, grid, s); break;
+    case QNN_WE_Q8_0: launch_enc<QNN_WE_Q8_0>(a, bw, slices, grid, s); break;
+    default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
+  }
+  hip_check(hipGetLastError(), "gguf matvec launch");
+}
+
 }  // namespace qnn

@@ -43,16 +43,13 @@ struct I4Layout {
   size_t bytes() const { return nib_bytes() + scale_bytes(); }
 };
 
-// GGUF tiled layout: tiles of 64 rows, one row per lane; the 16-byte-aligned
-// "main" part of each super-block and its small side fields are stored as
-// lane-interleaved planes (see qnn_gguf.hip).
+// GGUF tiled layout (qnn_gguf.hip): tiles of 64 rows, 256-element units,
+// a 16-byte-aligned main plane plus up to two small side planes.
 struct GGLayout {
-  int enc = 0, rows = 0, cols = 0, blocks = 0, tiles = 0;  // blocks per row
-  int main_chunks = 0;  // 16-B chunks of the main plane per (row, block)
-  int side_bytes = 0;   // bytes of the side plane per (row, block)
-  size_t main_bytes() const { return size_t(tiles) * blocks * main_chunks * 64 * 16; }
-  size_t side_plane_bytes() const { return size_t(tiles) * blocks * 64 * side_bytes; }
-  size_t bytes() const { return main_bytes() + ((side_plane_bytes() + 255) & ~size_t(255)); }
+  int enc = 0, rows = 0, cols = 0, tiles = 0, units = 0;
+  int main_chunks = 0, side1_bytes = 0, side2_bytes = 0, unit_bytes = 0, src_row_bytes = 0;
+  size_t side1_off = 0, side2_off = 0, total = 0;
+  size_t bytes() const { return total; }
 };
 
 enum class WKind { Int4, Gguf, Raw };
@@ -176,22 +173,27 @@ int mlp_stack_grid(int gswu, int gswd, int want);
 void mlp_stack_launch(const MlpArgs &a, int gswu, int gswd, int grid, hipStream_t s);
 
 // GGUF (qnn_gguf.hip).
+enum GGMode { GG_STORE = 0, GG_SWIGLU = 2 };
+struct GGArgs {
+  GGLayout l;
+  const void *w = nullptr;   // tiled weight (gate in pair modes)
+  const void *w2 = nullptr;  // pair modes: up weight (same layout)
+  const float *x = nullptr;
+  int x_vec4 = 0;
+  float *y = nullptr;
+  int n = 0;       // valid output rows
+  int tiles = 0;   // wave tiles (64 rows; 32 in pair modes)
+  int mode = GG_STORE;
+  float *partial = nullptr;
+  unsigned *counters = nullptr;
+  int xcd_local = 0;
+  int *err = nullptr;
+};
 GGLayout gguf_layout(int enc, int rows, int cols);
 void gguf_repack_launch(const uint8_t *src, const GGLayout &l, void *dst, hipStream_t s);
 void gguf_dequant_launch(const GGLayout &l, const void *w, float *out, hipStream_t s);
-struct GGLaunch {
-  const void *w = nullptr;
-  const float *x = nullptr;
-  int x_stride = 0;
-  float *y = nullptr;
-  int y_stride = 0;
-  int m = 1;
-  float *partial = nullptr;
-  unsigned *counters = nullptr;
-};
-void gguf_plan(const GGLayout &l, int m, int *bs, int *slices);
-size_t gguf_partial_floats(const GGLayout &l, int m, int slices);
-void gguf_matvec_launch(const GGLayout &l, const GGLaunch &a, int bs, int slices, hipStream_t s);
+void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices);
+void gguf_matvec_launch(const GGArgs &a, int bw, int slices, hipStream_t s);
 
 // Q8_0 GEMM (qnn_gemm.hip).
 size_t q8_act_bytes(int m, int k);

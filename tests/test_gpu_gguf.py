@@ -1,0 +1,148 @@
+"""GPU parity of the GGUF K-quant path against the CPU oracle.
+
+Dequantised weights must equal GGUFValue (GGUF.Quantization.pas:136-253) bit
+for bit (as floats: +0 == -0, the reference's own decoders differ there);
+matvec and fused gate/up outputs must match the reference CPU path
+(TCPUProjection.Linear, CPU.Inference.pas:316-428, packed AVX2 dots) within a
+normwise relative error of 1e-3 (max|y-r| / max|r|).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import BLOCK_BYTES, BLOCK_ELEMENTS, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q6_K, ENC_Q8_0
+from quicknn_amd import hip
+from tests.conftest import normwise_rel_err
+from tests.test_oracle_gguf import random_blocks
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K]
+NAMES = {ENC_Q8_0: "q8_0", ENC_Q4_K: "q4_k", ENC_Q6_K: "q6_k", ENC_Q3_K: "q3_k", ENC_Q2_K: "q2_k"}
+
+
+def quantized(rng, enc, n, k, scale=0.02):
+    """Library-encoded blocks of N(0, scale) weights (the benchmark's weight recipe)."""
+    return hip.gguf_quantize(enc, (rng.standard_normal((n, k)) * scale).astype(np.float32))
+
+
+def equal_as_floats(a, b):
+    return bool(np.all(a == b)) and not np.any(np.isnan(a))
+
+
+@pytest.mark.parametrize("enc", FMTS, ids=NAMES.get)
+@pytest.mark.parametrize("n,kb", [(1, 1), (33, 3), (64, 2), (100, 5), (257, 14)])
+def test_dequant_bit_exact_random_blocks(ctx, rng, enc, n, kb):
+    k = kb * BLOCK_ELEMENTS[enc]
+    data = random_blocks(rng, enc, n * kb)
+    out = ctx.NewTensor(n * k)
+    ctx.Dequantize(out, hip.MemoryBlock.gguf(data, n, k, enc), n, k)
+    got = ctx.Download(out)
+    want = oracle.gguf_dequant_scalar(data, enc, n * k)
+    assert equal_as_floats(got, want)
+    ctx.Recycle(out)
+
+
+@pytest.mark.parametrize("enc", FMTS, ids=NAMES.get)
+def test_dequant_bit_exact_encoded_weight(ctx, rng, enc):
+    n, k = 300, 3584 if enc != ENC_Q8_0 else 3072
+    data = quantized(rng, enc, n, k)
+    out = ctx.NewTensor(n * k)
+    ctx.Dequantize(out, hip.MemoryBlock.gguf(data, n, k, enc), n, k)
+    assert equal_as_floats(ctx.Download(out), oracle.gguf_dequant_scalar(data, enc, n * k))
+
+
+def test_dequant_offset_slice(ctx, rng):
+    """GGUFWeightPointer (GGUF.Quantization.pas:115-121): an element offset selects whole blocks."""
+    enc, n, k = ENC_Q4_K, 40, 512
+    data = random_blocks(rng, enc, 3 * n * k // 256)
+    off = n * k  # the second of three [n, k] matrices packed back to back
+    w = hip.MemoryBlock(data, (3 * n, k), hip.DT_U8, enc, off, 3 * n * k)
+    out = ctx.NewTensor(n * k)
+    ctx.Dequantize(out, w, n, k)
+    full = oracle.gguf_dequant_scalar(data, enc, 3 * n * k)
+    assert equal_as_floats(ctx.Download(out), full[off:off + n * k])
+
+
+@pytest.mark.parametrize("enc,n,k", [
+    (ENC_Q4_K, 4096, 3584), (ENC_Q3_K, 2048, 3584), (ENC_Q2_K, 14336, 3584), (ENC_Q6_K, 3584, 14336),
+    (ENC_Q8_0, 6144, 2048), (ENC_Q8_0, 12288, 3072),
+    (ENC_Q4_K, 5, 256), (ENC_Q6_K, 70, 768), (ENC_Q3_K, 129, 1280), (ENC_Q2_K, 63, 512), (ENC_Q8_0, 33, 96),
+])
+def test_linear_m1(ctx, rng, enc, n, k):
+    data = quantized(rng, enc, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
+    ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, k, enc), None, None, 1, k, n)
+    got = ctx.Download(dst)
+    want = oracle.cpu_linear(data, enc, x, k, n)
+    assert normwise_rel_err(got, want) <= TOL
+    ctx.Recycle(src)
+    ctx.Recycle(dst)
+
+
+@pytest.mark.parametrize("enc", FMTS, ids=NAMES.get)
+def test_linear_m1_random_blocks(ctx, rng, enc):
+    """Arbitrary block bytes (every scale/min/quant pattern), not just encoder output."""
+    n, kb = 200, 6 if enc != ENC_Q8_0 else 40
+    k = kb * BLOCK_ELEMENTS[enc]
+    data = random_blocks(rng, enc, n * kb)
+    x = rng.standard_normal(k).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
+    ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, k, enc), None, None, 1, k, n)
+    assert normwise_rel_err(ctx.Download(dst), oracle.cpu_linear(data, enc, x, k, n)) <= TOL
+
+
+@pytest.mark.parametrize("enc", FMTS, ids=NAMES.get)
+def test_linear_rows_and_bias(ctx, rng, enc):
+    n, k, rows = 300, 1024, 3
+    data = quantized(rng, enc, n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(rows * n)
+    ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, k, enc), None, hip.MemoryBlock.vector(bias), rows, k, n)
+    got = ctx.Download(dst).reshape(rows, n)
+    for r in range(rows):
+        want = oracle.cpu_linear(data, enc, x[r], k, n) + bias
+        assert normwise_rel_err(got[r], want) <= TOL, r
+
+
+def test_linear_deterministic(ctx, rng):
+    enc, n, k = ENC_Q6_K, 3584, 14336
+    w = hip.MemoryBlock.gguf(quantized(rng, enc, n, k), n, k, enc)
+    src, dst = ctx.UploadRaw(rng.standard_normal(k).astype(np.float32)), ctx.NewTensor(n)
+    outs = []
+    for _ in range(3):
+        ctx.Linear(dst, src, w, None, None, 1, k, n)
+        outs.append(ctx.Download(dst).view(np.uint32).copy())
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def _swiglu_want(pg, eg, pu, eu, x, k, n):
+    g = oracle.cpu_linear(pg, eg, x, k, n)
+    u = oracle.cpu_linear(pu, eu, x, k, n)
+    return np.array([oracle.silu(float(a)) for a in g], np.float32) * u
+
+
+@pytest.mark.parametrize("eg,eu,n,k", [
+    (ENC_Q2_K, ENC_Q2_K, 14336, 3584), (ENC_Q4_K, ENC_Q4_K, 1000, 768), (ENC_Q8_0, ENC_Q8_0, 96, 64),
+    (ENC_Q6_K, ENC_Q6_K, 33, 256), (ENC_Q3_K, ENC_Q3_K, 257, 512), (ENC_Q4_K, ENC_Q6_K, 500, 512),
+])
+def test_swiglu_vector(ctx, rng, eg, eu, n, k):
+    pg, pu = quantized(rng, eg, n, k), quantized(rng, eu, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
+    assert ctx.TrySwiGLUVector(dst, src, hip.MemoryBlock.gguf(pg, n, k, eg), hip.MemoryBlock.gguf(pu, n, k, eu), k, n)
+    assert normwise_rel_err(ctx.Download(dst), _swiglu_want(pg, eg, pu, eu, x, k, n)) <= TOL
+
+
+def test_gguf_argument_errors(ctx, rng):
+    enc, n, k = ENC_Q4_K, 16, 512
+    data = quantized(rng, enc, n, k)
+    src, dst = ctx.NewTensor(k), ctx.NewTensor(n)
+    with pytest.raises(hip.EArgumentException):  # width not a whole number of blocks
+        ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, 500, enc), None, None, 1, 500, n)
+    with pytest.raises(hip.EArgumentException):  # more rows than the block holds
+        ctx.Linear(ctx.NewTensor(2 * n), src, hip.MemoryBlock.gguf(data, n, k, enc), None, None, 1, k, 2 * n)
+    with pytest.raises(hip.ENotSupportedException):  # IQ-family / unknown encodings are not handled
+        ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, k, 7), None, None, 1, k, n)

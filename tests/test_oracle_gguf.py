@@ -1,0 +1,166 @@
+"""Pins the GGUF part of the oracle (src/io/QuickNN.GGUF.Quantization.pas):
+the three independent reference decoders (scalar GGUFValue :136-253, the AVX2
+block decoders :274-368, the shader's readGGUF4 gguf.glsl:591-655) must agree
+on random valid blocks; hand-built blocks give known answers from the format
+definitions; the packed AVX2 dots agree with a double-precision dot over the
+decoded weights; the product's block encoders round-trip."""
+import struct
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q6_K, ENC_Q8_0, BLOCK_BYTES, BLOCK_ELEMENTS
+
+FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K]
+# fp16 fields (byte offsets within a block)
+HALF_FIELDS = {ENC_Q8_0: [0], ENC_Q4_K: [0, 2], ENC_Q6_K: [208], ENC_Q3_K: [108], ENC_Q2_K: [80, 82]}
+
+
+def f16(v: float) -> int:
+    return int(np.array([v], np.float16).view(np.uint16)[0])
+
+
+def random_blocks(rng, enc: int, nblocks: int) -> np.ndarray:
+    """Random bytes with every fp16 field replaced by a finite value (incl. negatives and subnormals)."""
+    bb = BLOCK_BYTES[enc]
+    b = rng.integers(0, 256, (nblocks, bb), dtype=np.uint8)
+    for off in HALF_FIELDS[enc]:
+        vals = rng.standard_normal(nblocks) * 0.01
+        vals[::7] = 3.0e-6  # fp16 subnormal
+        vals[1::11] = -vals[1::11]
+        h = np.array(vals, np.float16).view(np.uint16)
+        b[:, off] = h & 255
+        b[:, off + 1] = h >> 8
+    return b.reshape(-1)
+
+
+def same_values(a: np.ndarray, b: np.ndarray) -> bool:
+    """Equal as floats (+0 == -0; the reference's decoders differ only in the sign of zero)."""
+    return bool(np.all(a == b)) and not np.any(np.isnan(a)) and not np.any(np.isnan(b))
+
+
+def test_half_to_float_known_answers():
+    assert oracle.half_to_float(0x3C00) == 1.0
+    assert oracle.half_to_float(0xC000) == -2.0
+    assert oracle.half_to_float(0x0001) == 2.0 ** -24
+    assert oracle.half_to_float(0x03FF) == 1023 * 2.0 ** -24
+    assert oracle.half_to_float(0x7BFF) == 65504.0
+    assert np.isinf(oracle.half_to_float(0x7C00))
+    for v in [0.5, -3.25, 1e-3, 6.1e-5, 1e-7]:
+        h = f16(v)
+        assert oracle.half_to_float(h) == float(np.array([h], np.uint16).view(np.float16)[0])
+
+
+@pytest.mark.parametrize("enc", FMTS)
+def test_three_decoders_agree(rng, enc):
+    n = 12 * BLOCK_ELEMENTS[enc]
+    data = random_blocks(rng, enc, 12)
+    scalar = oracle.gguf_dequant_scalar(data, enc, n)
+    block = oracle.gguf_dequantize(data, enc, n)
+    shader = oracle.gguf_read4_all(data, enc, n)
+    assert same_values(scalar, block)
+    assert same_values(scalar, shader)
+
+
+def test_q8_0_known_answer():
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.frombuffer(struct.pack("<H", f16(0.5)), np.uint8)
+    q = np.arange(-16, 16, dtype=np.int8)
+    b[2:] = q.view(np.uint8)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q8_0, 32), q.astype(np.float32) * 0.5)
+
+
+def test_q4_k_known_answer():
+    # d = 1, dmin = 0.25; sub-block j: scale 2j+1, min j; quants ramp i % 16.
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.frombuffer(struct.pack("<H", f16(1.0)), np.uint8)
+    b[2:4] = np.frombuffer(struct.pack("<H", f16(0.25)), np.uint8)
+    sc = [2 * j + 1 for j in range(8)]
+    mn = [j for j in range(8)]
+    for j in range(4):
+        b[4 + j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        b[8 + j] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        b[12 + j] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    q = np.array([i % 16 for i in range(256)])
+    for i in range(256):
+        j = i // 32
+        b[16 + (i // 64) * 32 + i % 32] |= q[i] << ((j & 1) * 4)
+    want = np.array([sc[i // 32] * q[i] - 0.25 * mn[i // 32] for i in range(256)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q4_K, 256), want)
+
+
+def test_q6_k_known_answer():
+    # d = 0.5; sub-block scales alternate +-(j+1); q = (i * 7) % 64.
+    b = np.zeros(210, np.uint8)
+    b[208:210] = np.frombuffer(struct.pack("<H", f16(0.5)), np.uint8)
+    scales = [(j + 1) * (1 if j % 2 == 0 else -1) for j in range(16)]
+    b[192:208] = np.array(scales, np.int8).view(np.uint8)
+    q = np.array([(i * 7) % 64 for i in range(256)])
+    for i in range(256):
+        part, quarter, lane = i // 128, (i % 128) // 32, i % 32
+        b[part * 64 + (quarter & 1) * 32 + lane] |= (q[i] & 15) << ((quarter // 2) * 4)
+        b[128 + part * 32 + lane] |= ((q[i] >> 4) & 3) << (quarter * 2)
+    want = np.array([0.5 * scales[i // 16] * (q[i] - 32) for i in range(256)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q6_K, 256), want)
+
+
+def test_q3_k_known_answer():
+    # d = 2; 6-bit scales sc = 20 + g (value sc - 32); q in [-4, 3] = (i % 8) - 4.
+    b = np.zeros(110, np.uint8)
+    b[108:110] = np.frombuffer(struct.pack("<H", f16(2.0)), np.uint8)
+    sc6 = [20 + g for g in range(16)]
+    for g in range(16):
+        b[96 + g % 8] |= (sc6[g] & 15) << ((g // 8) * 4)
+        b[104 + g % 4] |= ((sc6[g] >> 4) & 3) << ((g // 4) * 2)
+    q = np.array([(i % 8) - 4 for i in range(256)])
+    for i in range(256):
+        low = q[i] + 4 if q[i] < 0 else q[i]
+        b[32 + (i // 128) * 32 + i % 32] |= low << (((i % 128) // 32) * 2)
+        if q[i] >= 0:
+            b[i % 32] |= 1 << (i // 32)
+    want = np.array([2.0 * (sc6[i // 16] - 32) * q[i] for i in range(256)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q3_K, 256), want)
+
+
+def test_q2_k_known_answer():
+    # d = 1, dmin = 0.5; scale nibble = j % 16, min nibble = 15 - j; q = i % 4.
+    b = np.zeros(84, np.uint8)
+    b[80:82] = np.frombuffer(struct.pack("<H", f16(1.0)), np.uint8)
+    b[82:84] = np.frombuffer(struct.pack("<H", f16(0.5)), np.uint8)
+    for j in range(16):
+        b[j] = (j % 16) | ((15 - j) << 4)
+    q = np.array([i % 4 for i in range(256)])
+    for i in range(256):
+        b[16 + (i // 128) * 32 + i % 32] |= q[i] << (((i % 128) // 32) * 2)
+    want = np.array([(i // 16 % 16) * q[i] - 0.5 * (15 - i // 16) for i in range(256)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q2_K, 256), want)
+
+
+@pytest.mark.parametrize("enc", FMTS)
+def test_packed_dot_and_linear_brute_force(rng, enc):
+    k = 1024
+    rows = 8
+    data = random_blocks(rng, enc, rows * k // BLOCK_ELEMENTS[enc])
+    x = rng.standard_normal(k).astype(np.float32)
+    y = oracle.cpu_linear(data, enc, x, k, rows)
+    rb = k // BLOCK_ELEMENTS[enc] * BLOCK_BYTES[enc]
+    for r in range(rows):
+        w = oracle.gguf_dequant_scalar(np.ascontiguousarray(data[r * rb:(r + 1) * rb]), enc, k).astype(np.float64)
+        want = float(w @ x.astype(np.float64))
+        assert abs(y[r] - want) <= 4e-6 * float(np.abs(w) @ np.abs(x)) + 1e-30, (enc, r)
+
+
+@pytest.mark.parametrize("enc", FMTS)
+def test_product_encoder_round_trip(rng, enc):
+    """qnn_gguf_quantize writes valid blocks whose decode tracks the input."""
+    from quicknn_amd import hip
+
+    w = (rng.standard_normal(4096) * 0.02).astype(np.float32)
+    blocks = hip.gguf_quantize(enc, w)
+    assert blocks.size == 4096 // BLOCK_ELEMENTS[enc] * BLOCK_BYTES[enc]
+    dec = oracle.gguf_dequant_scalar(blocks, enc, 4096)
+    assert np.all(np.isfinite(dec))
+    rel = np.linalg.norm(dec - w) / np.linalg.norm(w)
+    bound = {ENC_Q8_0: 0.01, ENC_Q6_K: 0.03, ENC_Q4_K: 0.12, ENC_Q3_K: 0.25, ENC_Q2_K: 0.45}[enc]
+    assert rel < bound, rel
