@@ -31,8 +31,9 @@ struct qnn_tensor_s : qnn::Tensor {};
 
 struct qnn_expert_set_s {
   int experts = 0, hidden = 0, inter = 0;
-  std::vector<qnn::WeightEntry *> gate, up, down;
-  uint64_t *table = nullptr;  // device: [gate nib, gate scl, up nib, up scl, down nib, down scl] x experts
+  qnn::I4Layout gu, dn;
+  void *mem = nullptr;  // device: [gate x experts][up x experts][down x experts], tiled INT4
+  size_t bytes = 0, source_bytes = 0;
 };
 
 struct qnn_mlp_stack_s {
@@ -519,7 +520,7 @@ int qnn_ctx_destroy(qnn_ctx *ctx) {
       if (g.graph) (void)hipGraphDestroy(g.graph);
     }
     for (auto *s : ctx->sets) {
-      if (s->table) (void)hipFree(s->table);
+      if (s->mem) (void)hipFree(s->mem);
       delete s;
     }
     for (auto *s : ctx->stacks) {
@@ -624,6 +625,8 @@ int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count) {
       sync(ctx);
       if (flag & 2) fail(QNN_E_INVALID_OP, "persistent kernel dependency wait timed out");
       if (flag & 4) fail(QNN_E_INVALID_OP, "workgroup placement differs from the probed XCD mapping");
+      if (flag & 8) fail(QNN_E_INVALID_OP, "Invalid GPU expert ID");  // LLM.MoE.pas:384-385
+      if (flag & 16) fail(QNN_E_INVALID_OP, "MoE dispatch index outside its tensor");
       fail(QNN_E_INVALID_OP, "GPU produced a non-finite value");
     }
     return QNN_OK;
@@ -891,7 +894,8 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
         check_tensor(ctx, dst, n);
         check_tensor(ctx, b, int64_t(offset) + (n + hidden - 1) / hidden);
         check_tensor(ctx, a, 1);
-        if (n) misc_moe_gather(dst->ptr, a->ptr, b->ptr, n, hidden, topk, offset, ctx->stream);
+        if (n) misc_moe_gather(dst->ptr, a->ptr, size_t(a->count), b->ptr, n, hidden, topk, offset, ctx->error_flag,
+                               ctx->stream);
         return QNN_OK;
       }
       case QNN_GO_MOE_SCATTER: {
@@ -902,8 +906,8 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
         check_tensor(ctx, c, int64_t(pbase) + 1);
         if (!single) check_tensor(ctx, b, int64_t(offset) + (n + hidden - 1) / hidden);
         if (n)
-          misc_moe_scatter(dst->ptr, a->ptr, single ? nullptr : b->ptr, c->ptr, n, hidden, topk, offset, route,
-                           single, pbase, ctx->stream);
+          misc_moe_scatter(dst->ptr, size_t(dst->count), a->ptr, single ? nullptr : b->ptr, c->ptr, size_t(c->count),
+                           n, hidden, topk, offset, route, single, pbase, ctx->error_flag, ctx->stream);
         return QNN_OK;
       }
     }
@@ -977,8 +981,59 @@ int qnn_expert_set_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight
                           int experts, int hidden, int inter, qnn_expert_set **out) {
   return guarded([&] {
     check_ctx(ctx);
-    (void)gate; (void)up; (void)down; (void)experts; (void)hidden; (void)inter; (void)out;
-    fail(QNN_E_NOT_SUPPORTED, "routed experts not built yet");
+    if (!gate || !up || !down || !out || experts < 1 || experts > kMoEMaxExperts || hidden < 1 || inter < 1)
+      fail(QNN_E_ARGUMENT, "Invalid expert set");
+    if (ctx->capturing) fail(QNN_E_INVALID_OP, "expert set creation during graph capture");
+    const int rbh = qnn_int4_row_bytes(hidden), rbi = qnn_int4_row_bytes(inter);
+    // Same descriptor rules as Int4Linear (Context.Implementation.inc:1093-1104).
+    auto check = [&](const qnn_weight *w, int rows, int rb) {
+      check_weight_desc(w);
+      if (w->dtype != QNN_DT_U8 || w->encoding != QNN_WE_NATIVE || w->offset != 0 || rb < 0 || w->shape0 != rows ||
+          w->shape1 != rb || int64_t(rows) * rb > w->size)
+        fail(QNN_E_ARGUMENT, "Invalid packed INT4 expert projection");
+    };
+    for (int e = 0; e < experts; ++e) {
+      check(&gate[e], inter, rbh);
+      check(&up[e], inter, rbh);
+      check(&down[e], hidden, rbi);
+    }
+    auto *set = new qnn_expert_set_s();
+    set->experts = experts;
+    set->hidden = hidden;
+    set->inter = inter;
+    set->gu = int4_layout(inter, hidden);
+    set->dn = int4_layout(hidden, inter);
+    const size_t gub = set->gu.bytes(), dnb = set->dn.bytes();
+    set->bytes = size_t(experts) * (2 * gub + dnb);
+    set->source_bytes = size_t(experts) * (2 * size_t(inter) * rbh + size_t(hidden) * rbi);
+    try {
+      if (hipMalloc(&set->mem, set->bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        set->mem = nullptr;
+        fail(QNN_E_RANGE, "expert set does not fit in device memory");
+      }
+      uint8_t *base = static_cast<uint8_t *>(set->mem);
+      const size_t src_max = std::max(size_t(inter) * rbh, size_t(hidden) * rbi);
+      for (int e = 0; e < experts; ++e) {
+        const qnn_weight *ws[3] = {&gate[e], &up[e], &down[e]};
+        uint8_t *dst[3] = {base + size_t(e) * gub, base + size_t(experts + e) * gub,
+                           base + size_t(2 * experts) * gub + size_t(e) * dnb};
+        for (int j = 0; j < 3; ++j) {
+          const I4Layout &l = j < 2 ? set->gu : set->dn;
+          const size_t nbytes = size_t(l.rows) * (j < 2 ? rbh : rbi);
+          void *stg = ensure_staging(ctx, src_max);
+          hip_check(hipMemcpyAsync(stg, ws[j]->data, nbytes, hipMemcpyHostToDevice, ctx->stream), "expert upload");
+          int4_repack_launch(static_cast<const uint8_t *>(stg), l, dst[j], ctx->stream);
+          sync(ctx);  // staging is reused by the next matrix
+        }
+      }
+    } catch (...) {
+      if (set->mem) (void)hipFree(set->mem);
+      delete set;
+      throw;
+    }
+    ctx->sets.push_back(set);
+    *out = set;
     return QNN_OK;
   });
 }
@@ -986,7 +1041,12 @@ int qnn_expert_set_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight
 int qnn_expert_set_destroy(qnn_ctx *ctx, qnn_expert_set *set) {
   return guarded([&] {
     check_ctx(ctx);
-    (void)set;
+    auto it = std::find(ctx->sets.begin(), ctx->sets.end(), set);
+    if (it == ctx->sets.end()) fail(QNN_E_ARGUMENT, "unknown expert set");
+    sync(ctx);  // queued launches may still read it
+    if (set->mem) (void)hipFree(set->mem);
+    ctx->sets.erase(it);
+    delete set;
     return QNN_OK;
   });
 }
@@ -995,8 +1055,45 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
                     int topk) {
   return guarded([&] {
     check_ctx(ctx);
-    (void)set; (void)dst; (void)src; (void)routes; (void)rows; (void)topk;
-    fail(QNN_E_NOT_SUPPORTED, "routed experts not built yet");
+    if (std::find(ctx->sets.begin(), ctx->sets.end(), set) == ctx->sets.end())
+      fail(QNN_E_ARGUMENT, "unknown expert set");
+    // TLLMMoE.forward geometry (LLM.MoE.pas:376-377) and the route op's limits.
+    if (rows < 1 || rows > 128 || topk < 1 || topk > 64 || topk > set->experts || rows * topk > kMoEMaxRoutes)
+      fail(QNN_E_ARGUMENT, "Invalid MoE forward geometry");
+    check_tensor(ctx, src, int64_t(rows) * set->hidden);
+    check_tensor(ctx, dst, int64_t(rows) * set->hidden);
+    check_tensor(ctx, routes, int64_t(2) * rows * topk);
+    if (dst == src || dst == routes) fail(QNN_E_ARGUMENT, "MoE output aliases an input");
+    MoELaunch a;
+    const uint8_t *base = static_cast<const uint8_t *>(set->mem);
+    a.gu_stride = set->gu.bytes();
+    a.dn_stride = set->dn.bytes();
+    a.gate = base;
+    a.up = base + size_t(set->experts) * a.gu_stride;
+    a.down = base + size_t(2 * set->experts) * a.gu_stride;
+    a.gu = set->gu;
+    a.dn = set->dn;
+    a.experts = set->experts;
+    a.hidden = set->hidden;
+    a.inter = set->inter;
+    a.topk = topk;
+    a.rows = rows;
+    a.x = src->ptr;
+    a.routes = routes->ptr;
+    a.out = dst->ptr;
+    const MoEPlanSizes p = moe_plan(a);
+    const size_t n = size_t(rows) * topk;
+    const size_t hfl = (n * set->inter + 63) / 64 * 64;
+    float *w = static_cast<float *>(ensure_work(ctx, (hfl + n * set->hidden) * 4));
+    a.h = w;
+    a.y = w + hfl;
+    ensure_splitk(ctx, p.partial_floats, p.counters);
+    a.partial = ctx->partial;
+    a.counters = ctx->counters;
+    a.xcd_local = ctx->xcd_local ? 1 : 0;
+    a.err = ctx->error_flag;
+    moe_launch(a, p, ctx->stream);
+    ctx->st.int4_calls += 3;
     return QNN_OK;
   });
 }

@@ -539,11 +539,6 @@ void launch_enc(const GGArgs &a, int bw, int slices, int grid, hipStream_t st) {
   else hipLaunchKernelGGL((k_gguf_matvec<ENC, 1>), dim3(grid), dim3(256), 0, st, a, slices);
 }
 
-int env_int(const char *name, int dflt) {
-  const char *v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
-
 }  // namespace
 
 GGLayout gguf_layout(int enc, int rows, int cols) {
@@ -588,7 +583,7 @@ void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {
   const int forced = env_int("QNN_GG_BW", 0);
   int pick = 1;
   if (forced == 1 || forced == 2) pick = forced;
-  else if (size_t(tiles8) * ((l.units + 7) / 8) * 4 >= 3000) pick = 2;
+  else if (size_t(tiles8) * ((l.units + 7) / 8) * 4 >= 16384) pick = 2;  // BW=1 measured faster up to 7k waves
   *bw = pick;
   *slices = (l.units + 4 * pick - 1) / (4 * pick);
 }

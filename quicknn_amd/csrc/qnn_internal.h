@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <list>
 #include <memory>
 #include <stdexcept>
@@ -24,6 +25,18 @@ struct Error : std::runtime_error {
 inline void hip_check(hipError_t e, const char *what) {
   if (e != hipSuccess) fail(QNN_E_INVALID_OP, std::string(what) + ": " + hipGetErrorString(e));
 }
+// a + b*c with the product rounded before the sum (never fused into an fma):
+// the accumulate of moe.comp:70 / :126 as the reference's CPU path computes it.
+__host__ __device__ inline float add_mul_nofma(float a, float b, float c) {
+#pragma clang fp contract(off)
+  return a + b * c;
+}
+
+// Integer tuning override from the environment (0 or unset: the default).
+inline int env_int(const char *name, int dflt) {
+  const char *v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
 
 // ---------------------------------------------------------------------------
 // Device layouts
@@ -38,9 +51,9 @@ inline void hip_check(hipError_t e, const char *what) {
 // 0-31 stream 32 gate rows and lanes 32-63 the same 32 up rows.
 struct I4Layout {
   int rows = 0, cols = 0, groups = 0, g4 = 0, tiles = 0;
-  size_t nib_bytes() const { return size_t(tiles) * g4 * 64 * 16; }
-  size_t scale_bytes() const { return size_t(tiles) * g4 * 64 * 4; }
-  size_t bytes() const { return nib_bytes() + scale_bytes(); }
+  __host__ __device__ size_t nib_bytes() const { return size_t(tiles) * g4 * 64 * 16; }
+  __host__ __device__ size_t scale_bytes() const { return size_t(tiles) * g4 * 64 * 4; }
+  __host__ __device__ size_t bytes() const { return nib_bytes() + scale_bytes(); }
 };
 
 // GGUF tiled layout (qnn_gguf.hip): tiles of 64 rows, 256-element units,
@@ -122,31 +135,38 @@ void misc_norm(float *dst, const float *a, const void *gamma, int gamma_bf16, co
                int rows, int dim, int flags, int src_off, int unit_gamma, float eps, hipStream_t s);
 void misc_moe_route(float *routes, const float *logits, int rows, int experts, int k, int normalize,
                     hipStream_t s);
-void misc_moe_gather(float *dst, const float *src, const float *indices, int n, int hidden, int topk, int offset,
-                     hipStream_t s);
-void misc_moe_scatter(float *dst, const float *y, const float *indices, const float *routes, int n, int hidden,
-                      int topk, int offset, int route_index, int single_row, int prob_base, hipStream_t s);
+void misc_moe_gather(float *dst, const float *src, size_t src_n, const float *indices, int n, int hidden, int topk,
+                     int offset, int *err, hipStream_t s);
+void misc_moe_scatter(float *dst, size_t dst_n, const float *y, const float *indices, const float *routes,
+                      size_t routes_n, int n, int hidden, int topk, int offset, int route_index, int single_row,
+                      int prob_base, int *err, hipStream_t s);
 void misc_bias_add(float *dst, const void *bias, int bias_bf16, int rows, int cols, hipStream_t s);
 
-// Device-side routed experts (qnn_moe.hip).
+// Device-side routed experts (qnn_moe.hip).  Every expert of a set is one
+// contiguous tiled INT4 matrix per projection at base + e * stride.
+constexpr int kMoEMaxExperts = 512;  // the route op's limit (moe.comp:13, 512-entry score array)
+constexpr int kMoEMaxRoutes = 2048;  // rows * topk per call
 struct MoELaunch {
-  const uint64_t *gateup_table = nullptr;  // per expert: device address of the paired gate/up tiles
-  const uint64_t *down_table = nullptr;    // per expert: device address of the down tiles
+  const uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+  size_t gu_stride = 0, dn_stride = 0;  // bytes per expert matrix
+  I4Layout gu, dn;                      // gate/up [inter, hidden]; down [hidden, inter]
   int experts = 0, hidden = 0, inter = 0, topk = 0, rows = 0;
-  I4Layout gu, dn;                          // layouts shared by every expert
-  const float *x = nullptr;                 // [rows][hidden]
-  const float *routes = nullptr;            // [rows*topk ids][rows*topk probs]
-  float *out = nullptr;                     // [rows][hidden]
-  // workspace
-  int *plan = nullptr;          // see qnn_moe.hip
-  float *h = nullptr;           // [rows*topk][inter]
-  float *y = nullptr;           // [rows*topk][hidden]
+  const float *x = nullptr;       // [rows][hidden]
+  const float *routes = nullptr;  // [rows*topk ids as u32][rows*topk probabilities]
+  float *out = nullptr;           // [rows][hidden]
+  float *h = nullptr;             // workspace [rows*topk][inter]
+  float *y = nullptr;             // workspace [rows*topk][hidden]
   float *partial = nullptr;
   unsigned *counters = nullptr;
+  int xcd_local = 0;
+  int *err = nullptr;  // bit 8: invalid route ids
 };
-size_t moe_workspace_bytes(const MoELaunch &a, size_t *plan_off, size_t *h_off, size_t *y_off, size_t *part_off,
-                           size_t *cnt_off);
-void moe_launch(const MoELaunch &a, hipStream_t s);
+struct MoEPlanSizes {
+  int slots = 0, mt = 1, gsw = 4, slices_gu = 1, slices_dn = 1;
+  size_t partial_floats = 0, counters = 0;
+};
+MoEPlanSizes moe_plan(const MoELaunch &a);
+void moe_launch(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s);
 
 // Persistent INT4 MLP layer stack (qnn_mlp.hip).
 struct MlpLayerPtrs {

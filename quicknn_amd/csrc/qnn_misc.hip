@@ -181,25 +181,38 @@ __global__ __launch_bounds__(256) void k_moe_route(float *routes, const float *l
   }
 }
 
-// GO_MOE_GATHER (moe.comp:124).
-__global__ void k_moe_gather(float *dst, const float *src, const float *indices, int n, int hidden, int topk,
-                             int offset) {
+// GO_MOE_GATHER (moe.comp:124).  Dispatch indices come from the caller: one
+// that points outside src/dst is reported (error bit 16), never dereferenced.
+__global__ void k_moe_gather(float *dst, const float *src, size_t src_n, const float *indices, int n, int hidden,
+                             int topk, int offset, int *err) {
   int id = blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= n) return;
   int r = id / hidden, j = id % hidden;
   uint32_t route = __float_as_uint(indices[offset + r]);
-  dst[id] = src[size_t(route / topk) * hidden + j];
+  const size_t si = size_t(route / topk) * hidden + j;
+  if (si < src_n) {
+    dst[id] = src[si];
+  } else {
+    dst[id] = 0.0f;
+    atomicOr(err, 16);
+  }
 }
 
 // GO_MOE_SCATTER (moe.comp:125-126).
-__global__ void k_moe_scatter(float *dst, const float *y, const float *indices, const float *routes, int n,
-                              int hidden, int topk, int offset, int route_index, int single_row, int prob_base) {
+__global__ void k_moe_scatter(float *dst, size_t dst_n, const float *y, const float *indices, const float *routes,
+                              size_t routes_n, int n, int hidden, int topk, int offset, int route_index,
+                              int single_row, int prob_base, int *err) {
   int id = blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= n) return;
   int r = id / hidden, j = id % hidden;
   uint32_t route = single_row ? uint32_t(route_index) : __float_as_uint(indices[offset + r]);
   size_t target = size_t(route / topk) * hidden + j;
-  dst[target] = dst[target] + y[id] * routes[prob_base + route];
+  const size_t pi = size_t(prob_base) + route;
+  if (target >= dst_n || pi >= routes_n) {
+    atomicOr(err, 16);
+    return;
+  }
+  dst[target] = add_mul_nofma(dst[target], y[id], routes[pi]);
 }
 
 // Bias after a projection (GO_CONV_OUTPUT with bias in Linear, Implementation.inc:848-849, :892-893).
@@ -267,16 +280,17 @@ void misc_moe_route(float *routes, const float *logits, int rows, int experts, i
   hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(256), shmem, s, routes, logits, rows, experts, k, normalize);
   hip_check(hipGetLastError(), "moe route");
 }
-void misc_moe_gather(float *dst, const float *src, const float *indices, int n, int hidden, int topk, int offset,
-                     hipStream_t s) {
-  hipLaunchKernelGGL(k_moe_gather, dim3(blocks(n, 256)), dim3(256), 0, s, dst, src, indices, n, hidden, topk,
-                     offset);
+void misc_moe_gather(float *dst, const float *src, size_t src_n, const float *indices, int n, int hidden, int topk,
+                     int offset, int *err, hipStream_t s) {
+  hipLaunchKernelGGL(k_moe_gather, dim3(blocks(n, 256)), dim3(256), 0, s, dst, src, src_n, indices, n, hidden, topk,
+                     offset, err);
   hip_check(hipGetLastError(), "moe gather");
 }
-void misc_moe_scatter(float *dst, const float *y, const float *indices, const float *routes, int n, int hidden,
-                      int topk, int offset, int route_index, int single_row, int prob_base, hipStream_t s) {
-  hipLaunchKernelGGL(k_moe_scatter, dim3(blocks(n, 256)), dim3(256), 0, s, dst, y, indices, routes, n, hidden, topk,
-                     offset, route_index, single_row, prob_base);
+void misc_moe_scatter(float *dst, size_t dst_n, const float *y, const float *indices, const float *routes,
+                      size_t routes_n, int n, int hidden, int topk, int offset, int route_index, int single_row,
+                      int prob_base, int *err, hipStream_t s) {
+  hipLaunchKernelGGL(k_moe_scatter, dim3(blocks(n, 256)), dim3(256), 0, s, dst, dst_n, y, indices, routes, routes_n,
+                     n, hidden, topk, offset, route_index, single_row, prob_base, err);
   hip_check(hipGetLastError(), "moe scatter");
 }
 void misc_bias_add(float *dst, const void *bias, int bias_bf16, int rows, int cols, hipStream_t s) {

@@ -48,3 +48,14 @@ def normwise_rel_err(y: np.ndarray, r: np.ndarray) -> float:
     r = np.asarray(r, np.float64)
     den = np.max(np.abs(r))
     return float(np.max(np.abs(y - r)) / den) if den > 0 else float(np.max(np.abs(y - r)))
+
+
+def rand_int4(rng, n: int, k: int) -> np.ndarray:
+    """Valid packed INT4 rows [n, Int4RowBytes(k)] drawn directly (k a multiple of 32):
+    positive fp32 group scales in [0.001, 0.004) and uniform nibbles, the shape of
+    QuantizeInt4's output for N(0, 0.02) weights, without the packing cost."""
+    assert k % 32 == 0
+    g = k // 32
+    p = rng.integers(0, 256, (n, g, 20), dtype=np.uint8)
+    p[:, :, :4] = rng.uniform(0.001, 0.004, (n, g)).astype(np.float32)[..., None].view(np.uint8).reshape(n, g, 4)
+    return p.reshape(n, g * 20)
