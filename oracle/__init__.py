@@ -32,7 +32,6 @@ _lib = None
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
-_i8p = ctypes.POINTER(ctypes.c_int8)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _vp = ctypes.c_void_p
 
@@ -77,9 +76,6 @@ def lib():
                                           ctypes.c_int, _f32p]),
             "qo_gguf_gemm_scalar": (ctypes.c_int, [_u8p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int,
                                                    ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int]),
-            "qo_q8_act_quant": (ctypes.c_int, [_f32p, ctypes.c_int, ctypes.c_int, _i8p, _i8p, _f32p]),
-            "qo_q8_gemm_quantized": (ctypes.c_int, [_u8p, _i8p, _i8p, _f32p, ctypes.c_int, ctypes.c_int,
-                                                    ctypes.c_int, _f32p]),
             "qo_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
             "qo_float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
         }
@@ -277,25 +273,6 @@ def gguf_gemm_scalar(w, enc, a, n, row_begin=0, row_end=None) -> np.ndarray:
     c = np.zeros((m, n), np.float32)
     _check(lib().qo_gguf_gemm_scalar(_p(w, _u8p), enc, _p(a, _f32p), m, k, n, _p(c, _f32p), row_begin, row_end),
            "gguf_gemm_scalar")
-    return c
-
-
-def q8_act_quant(a: np.ndarray):
-    """Per-32 hi/lo int8 activation quantiser (no reference counterpart)."""
-    a = np.ascontiguousarray(a, np.float32)
-    m, k = a.shape
-    hi = np.zeros((m, k), np.int8)
-    lo = np.zeros((m, k), np.int8)
-    sc = np.zeros((m, k // 32), np.float32)
-    _check(lib().qo_q8_act_quant(_p(a, _f32p), m, k, _p(hi, _i8p), _p(lo, _i8p), _p(sc, _f32p)), "q8_act_quant")
-    return hi, lo, sc
-
-
-def q8_gemm_quantized(w, hi, lo, sc, n) -> np.ndarray:
-    m, k = hi.shape
-    c = np.zeros((m, n), np.float32)
-    _check(lib().qo_q8_gemm_quantized(_p(w, _u8p), _p(hi, _i8p), _p(lo, _i8p), _p(sc, _f32p), m, k, n,
-                                      _p(c, _f32p)), "q8_gemm_quantized")
     return c
 
 

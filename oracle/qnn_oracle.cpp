@@ -826,57 +826,4 @@ int qo_gguf_gemm_scalar(const uint8_t *w, int enc, const float *a, int m, int k,
   return 0;
 }
 
-// Per-32 activation quantiser used by the int8-MFMA Q8_0 GEMM (no reference
-// counterpart: the reference GEMM keeps fp32 activations).  Each element is
-// x ~= s2 * (256*hi + lo), hi, lo in [-127,127]:
-//   s1 = amax/127, hi = rint(x/s1), r = fma(-hi, s1, x), s2 = s1/256, lo = rint(r/s2).
-int qo_q8_act_quant(const float *a, int m, int k, int8_t *hi, int8_t *lo, float *scale) {
-  if (k % 32) return -1;
-  std::fesetround(FE_TONEAREST);
-  for (int r = 0; r < m; ++r)
-    for (int b = 0; b < k / 32; ++b) {
-      const float *x = a + (size_t)r * k + b * 32;
-      float amax = 0;
-      for (int i = 0; i < 32; ++i) amax = std::max(amax, std::fabs(x[i]));
-      float s1 = amax / 127.0f;
-      float s2 = s1 * 0.00390625f;
-      for (int i = 0; i < 32; ++i) {
-        int h = 0, l = 0;
-        if (s1 > 0) {
-          h = int(std::min(127.0f, std::max(-127.0f, std::nearbyint(x[i] / s1))));
-          float rr = std::fma(-float(h), s1, x[i]);
-          if (s2 > 0) l = int(std::min(127.0f, std::max(-127.0f, std::nearbyint(rr / s2))));
-        }
-        hi[(size_t)r * k + b * 32 + i] = int8_t(h);
-        lo[(size_t)r * k + b * 32 + i] = int8_t(l);
-      }
-      scale[(size_t)r * (k / 32) + b] = s2;
-    }
-  return 0;
-}
-
-// GEMM over the quantised activations: per 32-block exact int32 sum of
-// q_w * (256*hi + lo), then acc = fma(float(isum), d_w*s2, acc) in block order.
-int qo_q8_gemm_quantized(const uint8_t *w, const int8_t *hi, const int8_t *lo, const float *scale, int m, int k,
-                         int n, float *c) {
-  if (k % 32) return -1;
-  int nb = k / 32;
-  for (int r = 0; r < m; ++r)
-    for (int o = 0; o < n; ++o) {
-      float acc = 0;
-      for (int b = 0; b < nb; ++b) {
-        const uint8_t *blk = w + ((size_t)o * nb + b) * 34;
-        int32_t isum = 0;
-        for (int i = 0; i < 32; ++i) {
-          int qw = signed_byte(blk[2 + i]);
-          int v = 256 * hi[(size_t)r * k + b * 32 + i] + lo[(size_t)r * k + b * 32 + i];
-          isum += qw * v;
-        }
-        acc = std::fma(float(isum), half_at(blk) * scale[(size_t)r * nb + b], acc);
-      }
-      c[(size_t)r * n + o] = acc;
-    }
-  return 0;
-}
-
 }  // extern "C"

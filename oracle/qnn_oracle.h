@@ -76,9 +76,6 @@ int qo_cpu_moe(void *pool, const uint8_t *const *gate, const uint8_t *const *up,
 /* ---- Multi-row GGUF (src/core/QuickNN.Quantization.pas:247-258) ---- */
 int qo_gguf_gemm_scalar(const uint8_t *w, int enc, const float *a, int m, int k, int n,
                         float *c, int row_begin, int row_end);
-int qo_q8_act_quant(const float *a, int m, int k, int8_t *hi, int8_t *lo, float *scale);
-int qo_q8_gemm_quantized(const uint8_t *w, const int8_t *hi, const int8_t *lo,
-                         const float *scale, int m, int k, int n, float *c);
 
 /* ---- numerics helpers ---- */
 float qo_half_to_float(uint16_t h);            /* src/core/QuickNN.Common.pas:1799+ */

@@ -339,6 +339,7 @@ WeightEntry *acquire_gguf(qnn_ctx_s *ctx, const qnn_weight *w, int rows, int col
                          uint64_t(w->offset / gguf_block_elements(w->encoding)) * gguf_block_bytes(w->encoding);
     hip_check(hipMemcpyAsync(stg, src, bytes, hipMemcpyHostToDevice, ctx->stream), "weight upload");
     gguf_repack_launch(static_cast<const uint8_t *>(stg), e->gg, e->dptr, ctx->stream);
+    if (e->gg.rowexp_off) q8_rowexp_launch(e->gg, e->dptr, ctx->stream);
     sync(ctx);
   } catch (...) {
     if (e->dptr) (void)hipFree(e->dptr);
@@ -429,9 +430,15 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
 }
 
 // ---------------------------------------------------------------- Q8_0 multi-row GEMM
-bool q8_gemm_available() { return false; }
-void run_q8_gemm(qnn_ctx_s *, const WeightEntry *, const float *, float *, int, int, int) {
-  fail(QNN_E_NOT_SUPPORTED, "Q8_0 GEMM not built yet");
+// Rows at which the MFMA GEMM replaces per-row matvecs (one weight pass per row).
+int q8_gemm_min_rows() { return std::max(2, env_int("QNN_Q8_GEMM_MIN_ROWS", 4)); }
+
+void run_q8_gemm(qnn_ctx_s *ctx, const WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
+  const Q8GemmPlan p = q8_gemm_plan(rows, in_dim, out_dim);
+  const size_t frag_off = 0, exp_off = (p.frag_bytes + 255) & ~size_t(255);
+  uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, exp_off + p.exp_bytes));
+  q8_gemm_launch(p, x, rows, in_dim, out_dim, w->gg, w->dptr, ws + frag_off, reinterpret_cast<int *>(ws + exp_off), y,
+                 ctx->stream);
 }
 
 // ---------------------------------------------------------------- GGUF projection
@@ -820,7 +827,7 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
       fail(QNN_E_NOT_SUPPORTED, "Linear handles GGUF weights; native INT4 goes through Int4Linear");
     OpPins pin;
     WeightEntry *e = pin(acquire_gguf(ctx, w, out_dim, in_dim));
-    if (rows == 1 || w->encoding != QNN_WE_Q8_0 || !q8_gemm_available()) {
+    if (w->encoding != QNN_WE_Q8_0 || rows < q8_gemm_min_rows()) {
       // Matvec per row (op 65); rows > 1 of K-quants reuse it row by row.
       for (int r = 0; r < rows; ++r)
         run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim, out_dim);

@@ -1,0 +1,308 @@
+// qnn_gemm.hip -- multi-row GGUF Q8_0 projection (prefill GEMM) on fp16 MFMA.
+//
+// Replaces TQNNGPUContext.Linear with Rows > 1 on a Q8_0 weight
+// (Context.Implementation.inc:852-883 -> gemm.comp:27-44, :75-105: an fp32
+// SIMT GEMM that decodes every weight element into its LDS tile).
+//     C[m][n] = sum_k A[m][k] * W[n][k],   W[n][k] = d_b * q_k  (GGUFValue, exact in fp32)
+//
+// Operands run through v_mfma_f32_32x32x16_f16 in fp16, accumulated in fp32:
+//   * A is scaled per row by an exact power of two 2^-ea[m] (max |A[m][.]| in
+//     (2^13, 2^14]) and rounded once to fp16;
+//   * W is rounded once to fp16 as fp16(q * d * 2^-ew[n]), with the per-row
+//     power of two ew[n] taken at upload (max |d*q| of the row in (2^13, 2^14]);
+//   * C = acc * 2^(ea[m] + ew[n]).
+// fp16 keeps 11 significant bits: the normwise error at the cfg5 shape is
+// ~3e-4 (an int8 activation pass would give ~5e-3, bf16 ~2e-3).
+//
+// Tiling.  A workgroup computes 256 x 96 of C with 4 waves of 64 x 96
+// (2 x 3 MFMA tiles of 32 x 32).  A is prepared once per call in MFMA
+// fragment order (1 KiB per 32 rows x 16 k, one 16-byte piece per lane), so a
+// wave loads its A fragments straight from L2 with fully coalesced 16-byte
+// loads.  The 96 weight rows of a K-step are decoded once per workgroup into a
+// double-buffered LDS tile (fp16, rows padded by 16 bytes: conflict-free
+// ds_read_b128) that all four waves read.  Both M-tiles of an N-tile run on
+// one XCD, so the weight bytes are fetched from HBM once.
+#include "qnn_internal.h"
+
+namespace qnn {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256, BN = 96, BK = 64, LDB = BK + 8;  // LDB: halfs per LDS weight row
+
+__device__ __forceinline__ float half_bits_to_f(uint32_t h) {
+  const uint16_t b = uint16_t(h);
+  _Float16 f;
+  __builtin_memcpy(&f, &b, 2);
+  return float(f);
+}
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {  // two RNE fp16 in one dword
+  const _Float16 x = _Float16(a), y = _Float16(b);
+  uint16_t u, v;
+  __builtin_memcpy(&u, &x, 2);
+  __builtin_memcpy(&v, &y, 2);
+  return uint32_t(u) | (uint32_t(v) << 16);
+}
+// Exponent e with |v| * 2^-e in (2^13, 2^14] (0 for zero or non-finite v).
+__device__ __forceinline__ int range_exp(float amax) {
+  if (!(amax > 0.0f) || !isfinite(amax)) return 0;
+  int ex;
+  (void)frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+  return ex - 14;
+}
+
+// ---- activation preparation ------------------------------------------------
+// One wave per row: ea[m] from max |A[m][.]|.
+__global__ __launch_bounds__(256) void k_act_rowexp(const float *__restrict__ a, int M, int K, int m_pad,
+                                                    int *__restrict__ ea) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= m_pad) return;
+  float amax = 0.0f;
+  if (row < M) {
+    const float *r = a + size_t(row) * K;
+    for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(r[k]));
+  }
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if (lane == 0) ea[row] = range_exp(amax);
+}
+
+// Fragment order for v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane)
+// = 8 halfs A[m32*32 + lane%32][ks*16 + 8*(lane/32) + 0..7].
+__global__ __launch_bounds__(256) void k_act_frag(const float *__restrict__ a, const int *__restrict__ ea, int M,
+                                                  int K, int ksteps, size_t pieces, uint4 *__restrict__ out) {
+  const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= pieces) return;
+  const int lane = int(idx & 63);
+  const size_t mk = idx >> 6;
+  const int ks = int(mk % ksteps), m32 = int(mk / ksteps);
+  const int row = m32 * 32 + (lane & 31), k0 = ks * 16 + 8 * (lane >> 5);
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  if (row < M) {
+    const float *r = a + size_t(row) * K;
+    const float s = ldexpf(1.0f, -ea[row]);
+    if (k0 + 8 <= K && (K & 3) == 0) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(r + k0), x1 = *reinterpret_cast<const float4 *>(r + k0 + 4);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (k0 + i < K) v[i] = r[k0 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] *= s;  // exact: power of two
+  }
+  out[idx] = make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7]));
+}
+
+// ---- weight row exponents (at upload) --------------------------------------
+__global__ void k_q8_rowexp(GGLayout l, uint8_t *__restrict__ w) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= l.tiles * 64) return;
+  const int t = row >> 6, r = row & 63;
+  const uint8_t *side = w + l.side1_off;
+  float dmax = 0.0f;
+  for (int u = 0; u < l.units; ++u) {
+    const uint4 ds = *reinterpret_cast<const uint4 *>(side + ((size_t(t) * l.units + u) * 64 + r) * 16);
+    const uint32_t dw[4] = {ds.x, ds.y, ds.z, ds.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dmax = fmaxf(dmax, fabsf(half_bits_to_f(dw[j] & 0xFFFFu)));
+      dmax = fmaxf(dmax, fabsf(half_bits_to_f(dw[j] >> 16)));
+    }
+  }
+  reinterpret_cast<int *>(w + l.rowexp_off)[row] = range_exp(dmax * 127.0f);
+}
+
+// ---- GEMM ---------------------------------------------------------------------
+struct GemmArgs {
+  const uint4 *afrag;  // [m_pad/32][ksteps][64] pieces
+  const int *ea;       // [m_pad]
+  const uint8_t *w;    // Q8_0 tiled layout
+  GGLayout l;
+  float *c;            // [M][N]
+  int M, N, ksteps, ktiles, mtiles, ntiles;
+};
+
+// Weight loader: threads 0..191 each own (row i = t/2, block h = t%2) of the
+// 96 x 64 K-step: two 16-byte quant pieces and the block's fp16 scale.
+struct BRaw {
+  uint4 q0, q1;
+  uint32_t d;
+};
+
+__device__ __forceinline__ void load_b(BRaw &b, const GemmArgs &g, int ntile, int kt, int tid) {
+  b.q0 = make_uint4(0u, 0u, 0u, 0u);
+  b.q1 = b.q0;
+  b.d = 0u;
+  if (tid >= 2 * BN) return;
+  const int n = ntile * BN + (tid >> 1);
+  const int kb = kt * 2 + (tid & 1);  // 32-element block
+  if (n >= g.l.tiles * 64 || kb >= g.l.units * 8) return;
+  const int t = n >> 6, r = n & 63, u = kb >> 3, k8 = kb & 7;
+  const size_t tu = size_t(t) * g.l.units + u;
+  const uint4 *mp = reinterpret_cast<const uint4 *>(g.w) + (tu * 16 + 2 * k8) * 64 + r;
+  b.q0 = mp[0];
+  b.q1 = mp[64];
+  b.d = *reinterpret_cast<const uint16_t *>(g.w + g.l.side1_off + (tu * 64 + r) * 16 + 2 * k8);
+}
+
+__device__ __forceinline__ void store_b(_Float16 (*bs)[LDB], const BRaw &b, float scale, int tid) {
+  if (tid >= 2 * BN) return;
+  const float ds = half_bits_to_f(b.d) * scale;  // d * 2^-ew (exact)
+  const uint32_t qw[8] = {b.q0.x, b.q0.y, b.q0.z, b.q0.w, b.q1.x, b.q1.y, b.q1.z, b.q1.w};
+  uint32_t hw[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int q0 = int(int8_t(qw[i] & 255u)), q1 = int(int8_t((qw[i] >> 8) & 255u));
+    const int q2 = int(int8_t((qw[i] >> 16) & 255u)), q3 = int(int8_t(qw[i] >> 24));
+    hw[2 * i] = pack_h2(float(q0) * ds, float(q1) * ds);
+    hw[2 * i + 1] = pack_h2(float(q2) * ds, float(q3) * ds);
+  }
+  uint4 *dst = reinterpret_cast<uint4 *>(&bs[tid >> 1][(tid & 1) * 32]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) dst[j] = make_uint4(hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]);
+}
+
+__global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
+  const int b = blockIdx.x;
+  // XCD-aware: the M-tiles of one N-tile share an XCD (workgroup b runs on XCD b % 8).
+  const int xcd = b & 7, kq = b >> 3;
+  const int q = kq / g.mtiles;
+  const int ntile = q * 8 + xcd, mtile = kq - q * g.mtiles;
+  if (ntile >= g.ntiles) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  __shared__ __attribute__((aligned(16))) _Float16 bs[2][BN][LDB];
+  __shared__ float wscale[BN];
+  if (tid < BN) {
+    const int n = ntile * BN + tid;
+    const int e = n < g.l.tiles * 64 ? reinterpret_cast<const int *>(g.w + g.l.rowexp_off)[n] : 0;
+    wscale[tid] = ldexpf(1.0f, -e);
+  }
+  const int m32 = (mtile * BM + wave * 64) >> 5;  // first 32-row block of this wave
+  const uint4 *ap0 = g.afrag + (size_t(m32) * g.ksteps) * 64 + lane;
+  const uint4 *ap1 = g.afrag + (size_t(m32 + 1) * g.ksteps) * 64 + lane;
+
+  f32x16 acc[2][3];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  BRaw braw;
+  uint4 a[2][4], an[2][4];
+  load_b(braw, g, ntile, 0, tid);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    a[0][ks] = ap0[ks * 64];
+    a[1][ks] = ap1[ks * 64];
+  }
+  __syncthreads();  // wscale
+  store_b(bs[0], braw, tid < 2 * BN ? wscale[tid >> 1] : 0.0f, tid);
+  __syncthreads();
+
+  for (int kt = 0; kt < g.ktiles; ++kt) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < g.ktiles;
+    if (more) {
+      load_b(braw, g, ntile, kt + 1, tid);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        an[0][ks] = ap0[((kt + 1) * 4 + ks) * 64];
+        an[1][ks] = ap1[((kt + 1) * 4 + ks) * 64];
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      half8 bf[3];
+#pragma unroll
+      for (int nb = 0; nb < 3; ++nb) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(&bs[buf][nb * 32 + (lane & 31)][ks * 16 + 8 * (lane >> 5)]);
+        __builtin_memcpy(&bf[nb], &v, 16);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        half8 af;
+        __builtin_memcpy(&af, &a[mb][ks], 16);
+#pragma unroll
+        for (int nb = 0; nb < 3; ++nb) acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);
+      }
+    }
+    if (more) {
+      store_b(bs[buf ^ 1], braw, tid < 2 * BN ? wscale[tid >> 1] : 0.0f, tid);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        a[0][ks] = an[0][ks];
+        a[1][ks] = an[1][ks];
+      }
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32x32 tile.
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) {
+    const int col = ntile * BN + nb * 32 + (lane & 31);
+    if (col >= g.N) continue;
+    const int ew = reinterpret_cast<const int *>(g.w + g.l.rowexp_off)[col];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = mtile * BM + wave * 64 + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], g.ea[row] + ew);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s) {
+  const int rows = l.tiles * 64;
+  hipLaunchKernelGGL(k_q8_rowexp, dim3((rows + 255) / 256), dim3(256), 0, s, l, static_cast<uint8_t *>(w));
+  hip_check(hipGetLastError(), "q8 row exponents");
+}
+
+Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
+  Q8GemmPlan p;
+  p.m_pad = (M + BM - 1) / BM * BM;
+  p.k_pad = (K + BK - 1) / BK * BK;
+  p.ksteps = p.k_pad / 16;
+  p.mtiles = p.m_pad / BM;
+  p.ntiles = (N + BN - 1) / BN;
+  p.frag_bytes = size_t(p.m_pad) * p.k_pad * 2;
+  p.exp_bytes = size_t(p.m_pad) * 4;
+  return p;
+}
+
+void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
+                    void *frag, int *ea, float *c, hipStream_t s) {
+  hipLaunchKernelGGL(k_act_rowexp, dim3(p.m_pad / 4), dim3(256), 0, s, a, M, K, p.m_pad, ea);
+  const size_t pieces = size_t(p.m_pad / 32) * p.ksteps * 64;
+  hipLaunchKernelGGL(k_act_frag, dim3((pieces + 255) / 256), dim3(256), 0, s, a, ea, M, K, p.ksteps, pieces,
+                     static_cast<uint4 *>(frag));
+  GemmArgs g;
+  g.afrag = static_cast<const uint4 *>(frag);
+  g.ea = ea;
+  g.w = static_cast<const uint8_t *>(w);
+  g.l = l;
+  g.c = c;
+  g.M = M;
+  g.N = N;
+  g.ksteps = p.ksteps;
+  g.ktiles = p.k_pad / BK;
+  g.mtiles = p.mtiles;
+  g.ntiles = p.ntiles;
+  const int grid = (p.ntiles + 7) / 8 * 8 * p.mtiles;
+  hipLaunchKernelGGL(k_q8_gemm, dim3(grid), dim3(256), 0, s, g);
+  hip_check(hipGetLastError(), "q8 gemm launch");
+}
+
+}  // namespace qnn

@@ -562,6 +562,10 @@ GGLayout gguf_layout(int enc, int rows, int cols) {
   l.side1_off = up256(tu64 * l.main_chunks * 16);
   l.side2_off = l.side1_off + up256(tu64 * l.side1_bytes);
   l.total = l.side2_off + up256(tu64 * l.side2_bytes);
+  if (enc == QNN_WE_Q8_0) {
+    l.rowexp_off = l.total;
+    l.total += up256(size_t(l.tiles) * 64 * 4);
+  }
   return l;
 }
 

@@ -62,6 +62,7 @@ struct GGLayout {
   int enc = 0, rows = 0, cols = 0, tiles = 0, units = 0;
   int main_chunks = 0, side1_bytes = 0, side2_bytes = 0, unit_bytes = 0, src_row_bytes = 0;
   size_t side1_off = 0, side2_off = 0, total = 0;
+  size_t rowexp_off = 0;  // Q8_0: int per row, the GEMM's fp16 range exponent (qnn_gemm.hip)
   size_t bytes() const { return total; }
 };
 
@@ -167,6 +168,16 @@ struct MoEPlanSizes {
 };
 MoEPlanSizes moe_plan(const MoELaunch &a);
 void moe_launch(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s);
+
+// Multi-row Q8_0 projection on fp16 MFMA (qnn_gemm.hip).
+struct Q8GemmPlan {
+  int m_pad = 0, k_pad = 0, ksteps = 0, mtiles = 0, ntiles = 0;
+  size_t frag_bytes = 0, exp_bytes = 0;  // workspace: fp16 A fragments, per-row exponents
+};
+Q8GemmPlan q8_gemm_plan(int M, int K, int N);
+void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
+                    void *frag, int *ea, float *c, hipStream_t s);
+void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
 
 // Persistent INT4 MLP layer stack (qnn_mlp.hip).
 struct MlpLayerPtrs {

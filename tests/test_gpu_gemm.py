@@ -1,0 +1,109 @@
+"""GPU parity of the multi-row Q8_0 projection (prefill GEMM on fp16 MFMA).
+
+TQNNGPUContext.Linear with Rows > 1 on a Q8_0 weight (Context.Implementation.inc:852-883,
+gemm.comp) must match the reference CPU paths within a normwise relative error of 1e-3
+(max|y-r| / max|r|, per output row): the per-row AVX2 projection (TCPUProjection.Linear,
+CPU.Inference.pas:316-428, PackedDotQ8) and the scalar double-accumulated GGUF GEMM
+(QuickNN.Quantization.pas:247-258).  The device rounds both operands once to fp16
+(after exact power-of-two row scaling) and accumulates in fp32.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import ENC_Q8_0
+from quicknn_amd import hip
+from tests.conftest import normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def q8(rng, n, k, scale=0.02):
+    return hip.gguf_quantize(ENC_Q8_0, (rng.standard_normal((n, k)) * scale).astype(np.float32))
+
+
+def run_linear(ctx, w, a, n, bias=None):
+    m, k = a.shape
+    src, dst = ctx.UploadRaw(a), ctx.NewTensor(m * n)
+    ctx.Linear(dst, src, hip.MemoryBlock.gguf(w, n, k, ENC_Q8_0), None,
+               None if bias is None else hip.MemoryBlock.vector(bias), m, k, n)
+    out = ctx.Download(dst).reshape(m, n)
+    ctx.Recycle(src)
+    ctx.Recycle(dst)
+    return out
+
+
+def test_prefill_shape_matches_cpu_paths(ctx, rng):
+    """cfg5: A [512, 3072] x Q8_0 W [12288, 3072] (FLUX / Qwen-Image MLP)."""
+    m, k, n = 512, 3072, 12288
+    w = q8(rng, n, k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    got = run_linear(ctx, w, a, n)
+    for r in [0, 1, 255, 256, 300, 511]:
+        assert normwise_rel_err(got[r], oracle.cpu_linear(w, ENC_Q8_0, a[r], k, n)) <= TOL, r
+    want = oracle.gguf_gemm_scalar(w, ENC_Q8_0, a, n, row_begin=137, row_end=139)
+    for r in (137, 138):
+        assert normwise_rel_err(got[r], want[r]) <= TOL, r
+
+
+@pytest.mark.parametrize("m,k,n", [(4, 96, 100), (5, 32, 64), (257, 1024, 97), (300, 640, 200), (33, 4096, 4096),
+                                   (16, 2048, 6144)])
+def test_ragged_shapes(ctx, rng, m, k, n):
+    w = q8(rng, n, k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    got = run_linear(ctx, w, a, n)
+    rows = min(m, 40)
+    want = oracle.gguf_gemm_scalar(w, ENC_Q8_0, a, n, row_end=rows)
+    for r in range(rows):
+        assert normwise_rel_err(got[r], want[r]) <= TOL, r
+    # Element-wise: one fp16 rounding of each operand bounds every output by
+    # 2^-10 * sum_k |w x| (plus fp32 accumulation, far smaller).
+    wd = oracle.gguf_dequant_scalar(w, ENC_Q8_0, n * k).reshape(n, k).astype(np.float64)
+    bound = np.abs(a[:rows].astype(np.float64)) @ np.abs(wd).T * 2.0 ** -10
+    assert np.all(np.abs(got[:rows] - want[:rows]) <= bound)
+
+
+def test_operand_range_scaling(ctx, rng):
+    """Rows far outside fp16's range and weight blocks with large scales (|d*q| > 65504)."""
+    m, k, n = 8, 512, 192
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wf[3] *= 5e4    # |w| up to ~4e3, d up to ~30
+    wf[100] *= 1e6  # |d*q| beyond fp16
+    wf[7] *= 1e-3   # d in the fp16 subnormal range
+    w = hip.gguf_quantize(ENC_Q8_0, wf)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[1] *= 1e8
+    a[2] *= 1e-8
+    a[5, ::3] = 0.0
+    got = run_linear(ctx, w, a, n)
+    want = oracle.gguf_gemm_scalar(w, ENC_Q8_0, a, n)
+    for r in range(m):
+        assert np.all(np.isfinite(got[r]))
+        assert normwise_rel_err(got[r], want[r]) <= TOL, r
+    # columns far below the row's largest are still right (per-row weight scale, per-element fp16)
+    assert np.max(np.abs(got[:, 7] - want[:, 7])) <= 1e-3 * np.max(np.abs(want[:, 7])) * 10
+
+
+def test_bias_and_determinism(ctx, rng):
+    m, k, n = 64, 1024, 512
+    w = q8(rng, n, k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    g1 = run_linear(ctx, w, a, n, bias)
+    g2 = run_linear(ctx, w, a, n, bias)
+    assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
+    want = oracle.gguf_gemm_scalar(w, ENC_Q8_0, a, n, row_end=8) + bias
+    for r in range(8):
+        assert normwise_rel_err(g1[r], want[r]) <= TOL, r
+
+
+def test_small_rows_use_matvec_and_agree(ctx, rng):
+    """Rows below the GEMM threshold take the per-row matvec; both paths agree."""
+    k, n = 1024, 300
+    w = q8(rng, n, k)
+    a = rng.standard_normal((6, k)).astype(np.float32)
+    full = run_linear(ctx, w, a, n)        # GEMM (6 rows)
+    two = run_linear(ctx, w, a[:2], n)     # matvec per row
+    for r in range(2):
+        assert normwise_rel_err(full[r], two[r]) <= TOL
