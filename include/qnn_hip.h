@@ -198,24 +198,6 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
                     int rows, int topk);
 
 /* ---------------------------------------------------------------------------
- * Persistent decode MLP stack (no reference counterpart; replaces the per-layer
- * pair TrySwiGLUVector + Int4Linear of the decode loop,
- * src/models/QuickNN.Models.QwenHybrid.pas:692-702, for consecutive layers).
- * One cooperative launch computes, for l = 0..layers-1,
- *     x_{l+1} = down_l( silu(gate_l x_l) * (up_l x_l) )
- * and writes x_layers to dst.  Weights are native INT4 (gate/up
- * [inter, Int4RowBytes(hidden)], down [hidden, Int4RowBytes(inter)]); they are
- * made resident and pinned when the stack is created.  Batch 1.
- * A wait that does not complete (an internal error) makes the next
- * qnn_download fail with QNN_E_INVALID_OP instead of hanging.
- * ------------------------------------------------------------------------- */
-typedef struct qnn_mlp_stack_s qnn_mlp_stack;
-int qnn_mlp_stack_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight *up, const qnn_weight *down,
-                         int layers, int hidden, int inter, qnn_mlp_stack **out);
-int qnn_mlp_stack_run(qnn_ctx *ctx, qnn_mlp_stack *stack, qnn_tensor *dst, qnn_tensor *src);
-int qnn_mlp_stack_destroy(qnn_ctx *ctx, qnn_mlp_stack *stack);
-
-/* ---------------------------------------------------------------------------
  * Diagnostics (no reference counterpart)
  * ------------------------------------------------------------------------- */
 /* Writes the dequantized weight, fp32 [rows, cols], from the device-resident copy. */

@@ -36,13 +36,6 @@ struct qnn_expert_set_s {
   size_t bytes = 0, source_bytes = 0;
 };
 
-struct qnn_mlp_stack_s {
-  int layers = 0, hidden = 0, inter = 0, gswu = 8, gswd = 8, grid = 0;
-  std::vector<qnn::WeightEntry *> pinned;
-  qnn::MlpArgs args;
-  void *table = nullptr;  // device MlpLayerPtrs[layers]
-  void *ws = nullptr;     // device workspace (zeroed once)
-};
 
 struct qnn_ctx_s {
   int device = 0;
@@ -69,7 +62,6 @@ struct qnn_ctx_s {
   std::vector<qnn::WeightEntry *> capture_pins;
   std::vector<qnn::GraphRec> graphs;
   std::vector<qnn_expert_set_s *> sets;
-  std::vector<qnn_mlp_stack_s *> stacks;
   bool xcd_local = false;  // workgroup b runs on XCD b % 8 (probed at creation)
   qnn_status st{};
   uint64_t act_bytes = 0;
@@ -395,6 +387,16 @@ struct OpPins {
 void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
               int rows, int in_dim, int out_dim, const float *prob) {
   const I4Layout &l = w->i4;
+  // The kernels read activation rows as aligned 4-float pieces: a row length
+  // that is not a multiple of 4 goes through a zero-padded copy.
+  int k = in_dim;
+  qnn_tensor_s *padded = nullptr;
+  if (in_dim % 4 != 0) {
+    k = (in_dim + 3) / 4 * 4;
+    padded = new_tensor(ctx, rows * k);
+    misc_pad_rows(padded->ptr, x, rows, in_dim, k, ctx->stream);
+    x = padded->ptr;
+  }
   for (int r0 = 0; r0 < rows; r0 += 16) {
     const int m = std::min(16, rows - r0);
     I4Launch a;
@@ -404,29 +406,26 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
       a.nib2 = w2->dptr;
       a.scl2 = static_cast<const uint8_t *>(w2->dptr) + l.nib_bytes();
     }
-    a.x = x + size_t(r0) * in_dim;
-    a.x_stride = in_dim;
-    a.x_vec4 = (in_dim % 4 == 0) && (reinterpret_cast<uintptr_t>(a.x) % 16 == 0);
+    a.x = x + size_t(r0) * k;
+    a.x_stride = k;
     a.y = y + size_t(r0) * out_dim;
     a.y_stride = out_dim;
-    a.k = in_dim;
+    a.k = k;
     a.n = out_dim;
     a.m = m;
-    a.g4 = l.g4;
-    a.tiles = mode == I4_SWIGLU ? (out_dim + 31) / 32 : l.tiles;
+    a.l = l;
+    a.tiles = mode == I4_SWIGLU ? 2 * l.blocks : l.blocks;
     a.mode = mode;
     a.prob = prob;
-    I4Layout plan_l = l;
-    plan_l.tiles = a.tiles;
-    int gs, slices;
-    int4_plan(plan_l, m, &gs, &slices);
-    ensure_splitk(ctx, int4_partial_floats(plan_l, m, slices), size_t(a.tiles) * kCounterStride);
+    const I4Plan p = int4_plan(l, m, mode);
+    ensure_splitk(ctx, p.partial_floats, p.counters);
     a.partial = ctx->partial;
     a.counters = ctx->counters;
     a.xcd_local = ctx->xcd_local ? 1 : 0;
     a.err = ctx->error_flag;
-    int4_matvec_launch(a, gs, slices, ctx->stream);
+    int4_matvec_launch(a, p, ctx->stream);
   }
+  if (padded) padded->live = false;  // later users of the buffer are ordered after this launch
 }
 
 // ---------------------------------------------------------------- Q8_0 multi-row GEMM
@@ -528,11 +527,6 @@ int qnn_ctx_destroy(qnn_ctx *ctx) {
     }
     for (auto *s : ctx->sets) {
       if (s->mem) (void)hipFree(s->mem);
-      delete s;
-    }
-    for (auto *s : ctx->stacks) {
-      if (s->table) (void)hipFree(s->table);
-      if (s->ws) (void)hipFree(s->ws);
       delete s;
     }
     for (auto &kv : ctx->weights) {
@@ -1071,6 +1065,8 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     check_tensor(ctx, dst, int64_t(rows) * set->hidden);
     check_tensor(ctx, routes, int64_t(2) * rows * topk);
     if (dst == src || dst == routes) fail(QNN_E_ARGUMENT, "MoE output aliases an input");
+    if (set->hidden % 4 != 0 || set->inter % 4 != 0)
+      fail(QNN_E_NOT_SUPPORTED, "device MoE needs hidden and intermediate sizes that are multiples of 4");
     MoELaunch a;
     const uint8_t *base = static_cast<const uint8_t *>(set->mem);
     a.gu_stride = set->gu.bytes();
@@ -1105,127 +1101,6 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
   });
 }
 
-// ---------------------------------------------------------------- persistent MLP stack
-int qnn_mlp_stack_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight *up, const qnn_weight *down,
-                         int layers, int hidden, int inter, qnn_mlp_stack **out) {
-  return guarded([&] {
-    check_ctx(ctx);
-    if (!gate || !up || !down || !out || layers < 1 || layers > 60000 || hidden < 1 || inter < 1)
-      fail(QNN_E_ARGUMENT, "Invalid MLP stack");
-    if (ctx->capturing) fail(QNN_E_INVALID_OP, "MLP stack creation during graph capture");
-    auto *st = new qnn_mlp_stack_s();
-    st->layers = layers;
-    st->hidden = hidden;
-    st->inter = inter;
-    try {
-      std::vector<MlpLayerPtrs> tab(layers);
-      I4Layout lgu, ld;
-      for (int l = 0; l < layers; ++l) {
-        WeightEntry *g = acquire_int4(ctx, &gate[l], inter, hidden);
-        g->pins++;
-        st->pinned.push_back(g);
-        WeightEntry *u = acquire_int4(ctx, &up[l], inter, hidden);
-        u->pins++;
-        st->pinned.push_back(u);
-        WeightEntry *d = acquire_int4(ctx, &down[l], hidden, inter);
-        d->pins++;
-        st->pinned.push_back(d);
-        lgu = g->i4;
-        ld = d->i4;
-        auto nib = [](WeightEntry *e) { return static_cast<const uint4 *>(e->dptr); };
-        auto scl = [](WeightEntry *e) {
-          return reinterpret_cast<const float *>(static_cast<const uint8_t *>(e->dptr) + e->i4.nib_bytes());
-        };
-        tab[l] = {nib(g), scl(g), nib(u), scl(u), nib(d), scl(d)};
-      }
-      MlpArgs &a = st->args;
-      a.layers = layers;
-      a.hidden = hidden;
-      a.inter = inter;
-      a.g4_gu = lgu.g4;
-      a.g4_d = ld.g4;
-      a.tiles_gu = (inter + 31) / 32;
-      a.tiles_d = ld.tiles;
-      const char *env = getenv("QNN_MLP_GSWU");
-      st->gswu = env && (atoi(env) == 4 || atoi(env) == 20) ? atoi(env) : 8;
-      const char *envd = getenv("QNN_MLP_GSWD");
-      st->gswd = envd && atoi(envd) == 16 ? 16 : 8;
-      a.slices_gu = (a.g4_gu + 4 * st->gswu - 1) / (4 * st->gswu);
-      a.slices_d = (a.g4_d + 4 * st->gswd - 1) / (4 * st->gswd);
-      // Workspace: h[2][inter], y[2][hidden], partials, tickets, flags, epoch/exit/abort.
-      auto up256 = [](size_t b) { return (b + 255) & ~size_t(255); };
-      const size_t n_hb = up256(size_t(2) * inter * 4), n_yb = up256(size_t(2) * hidden * 4);
-      const size_t n_pgu = up256(size_t(a.tiles_gu) * a.slices_gu * 64 * 4);
-      const size_t n_pd = up256(size_t(a.tiles_d) * a.slices_d * 64 * 4);
-      const size_t n_tgu = up256(size_t(a.tiles_gu) * kCounterStride * 4), n_td = up256(size_t(a.tiles_d) * kCounterStride * 4);
-      const size_t n_fgu = up256(size_t(a.tiles_gu) * 8 * 8), n_fd = up256(size_t(a.tiles_d) * 8 * 8);
-      const size_t n_ctl = 256 * 3;
-      const size_t total = n_hb + n_yb + n_pgu + n_pd + n_tgu + n_td + n_fgu + n_fd + n_ctl;
-      hip_check(hipMalloc(&st->ws, total), "MLP stack workspace");
-      hip_check(hipMemset(st->ws, 0, total), "MLP stack workspace clear");
-      uint8_t *p = static_cast<uint8_t *>(st->ws);
-      auto take = [&](size_t n) { uint8_t *r = p; p += n; return r; };
-      a.hbuf = reinterpret_cast<float *>(take(n_hb));
-      a.ybuf = reinterpret_cast<float *>(take(n_yb));
-      a.part_gu = reinterpret_cast<float *>(take(n_pgu));
-      a.part_d = reinterpret_cast<float *>(take(n_pd));
-      a.tick_gu = reinterpret_cast<unsigned *>(take(n_tgu));
-      a.tick_d = reinterpret_cast<unsigned *>(take(n_td));
-      a.flag_gu = reinterpret_cast<unsigned long long *>(take(n_fgu));
-      a.flag_d = reinterpret_cast<unsigned long long *>(take(n_fd));
-      a.epoch = reinterpret_cast<unsigned long long *>(take(256));
-      a.exit_count = reinterpret_cast<unsigned *>(take(256));
-      a.abort = reinterpret_cast<unsigned *>(take(256));
-      a.err = ctx->error_flag;
-      a.spin_limit = 1u << 20;  // ~1 s of polling before giving up
-      hip_check(hipMalloc(&st->table, sizeof(MlpLayerPtrs) * layers), "MLP stack table");
-      hip_check(hipMemcpy(st->table, tab.data(), sizeof(MlpLayerPtrs) * layers, hipMemcpyHostToDevice), "MLP table");
-      a.w = static_cast<const MlpLayerPtrs *>(st->table);
-      st->grid = mlp_stack_grid(st->gswu, st->gswd, std::max(a.tiles_gu * a.slices_gu, a.tiles_d * a.slices_d));
-    } catch (...) {
-      for (auto *e : st->pinned) e->pins--;
-      if (st->table) (void)hipFree(st->table);
-      if (st->ws) (void)hipFree(st->ws);
-      delete st;
-      throw;
-    }
-    ctx->stacks.push_back(st);
-    *out = st;
-    return QNN_OK;
-  });
-}
-
-int qnn_mlp_stack_run(qnn_ctx *ctx, qnn_mlp_stack *stack, qnn_tensor *dst, qnn_tensor *src) {
-  return guarded([&] {
-    check_ctx(ctx);
-    if (!stack || std::find(ctx->stacks.begin(), ctx->stacks.end(), stack) == ctx->stacks.end())
-      fail(QNN_E_ARGUMENT, "unknown MLP stack");
-    check_tensor(ctx, src, stack->hidden);
-    check_tensor(ctx, dst, stack->hidden);
-    if (src == dst) fail(QNN_E_ARGUMENT, "MLP stack input and output alias");
-    MlpArgs a = stack->args;
-    a.x0 = src->ptr;
-    a.out = dst->ptr;
-    mlp_stack_launch(a, stack->gswu, stack->gswd, stack->grid, ctx->stream);
-    ctx->st.int4_calls += 3 * stack->layers;
-    return QNN_OK;
-  });
-}
-
-int qnn_mlp_stack_destroy(qnn_ctx *ctx, qnn_mlp_stack *stack) {
-  return guarded([&] {
-    check_ctx(ctx);
-    auto it = std::find(ctx->stacks.begin(), ctx->stacks.end(), stack);
-    if (it == ctx->stacks.end()) fail(QNN_E_ARGUMENT, "unknown MLP stack");
-    sync(ctx);
-    for (auto *e : stack->pinned) e->pins--;
-    (void)hipFree(stack->table);
-    (void)hipFree(stack->ws);
-    ctx->stacks.erase(it);
-    delete stack;
-    return QNN_OK;
-  });
-}
 
 // ---------------------------------------------------------------- timing / graphs
 int qnn_event_record(qnn_ctx *ctx, int slot) {

@@ -2,81 +2,105 @@
 // gfx950: matvec / multi-token matvec (Int4Linear, op 55/56), fused gate/up
 // SwiGLU (op 68) and weighted accumulate (Int4LinearAccumulate, op 69), plus
 // the repack and dequant kernels.  Format, layout and the fixed-point inner
-// product: qnn_int4_dev.h.  Slices of one tile are combined by the last
-// workgroup to finish (an atomic ticket per tile), in slice order, so results
-// do not depend on timing.
+// product: qnn_int4_dev.h.
+//
+// A workgroup is 4 waves on 4 consecutive tiles (64-lane blocks; in SwiGLU
+// mode half a block of gate rows in lanes 0-31 and the same up rows in lanes
+// 32-63) and one K-slice; the activation slice is staged once in LDS for all
+// four.  Each lane accumulates its groups, the L lanes of a row are reduced
+// across the wave, and when the K-range is split over several workgroups the
+// last slice of a tile to finish (an atomic ticket per tile) sums the slices
+// in slice order, so results do not depend on timing.  At batch 1 the planner
+// keeps whole rows in one wave wherever the matrix has enough rows, so no
+// split is needed.
 #include "qnn_int4_dev.h"
 
 namespace qnn {
 namespace {
 using dev::sel4u;
 
-// Workgroup = 4 wavefronts on one 64-row tile and a K-slice of 4*GSW groups;
-// the x slice is staged once per workgroup, the four partial sums meet in LDS.
-// In I4_SWIGLU mode tile t covers output rows 32t..32t+31: lanes 0-31 read them
-// from the gate matrix, lanes 32-63 from the up matrix (rows (t&1)*32.. of
-// stored tile t/2).
-template <int MT, int GSW>
+template <int MT, int GSW, int T>
 __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int slices) {
-  constexpr int GS = 4 * GSW;  // groups per workgroup slice
-  int tile, slice;
-  if (!dev::map_tile(blockIdx.x, slices, a.tiles, tile, slice)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g0 = slice * GS;
-  const int ng = min(GS, a.g4 - g0);  // multiple of 4
-  const int gw0 = wave * GSW;         // this wave's first group within the slice
-  const int ngw = max(0, min(GSW, ng - gw0));
+  extern __shared__ uint4 dyn_lds[];
+  __shared__ float red[4][MT][64];
+  constexpr int P = 4 / T;  // waves per tile: parts of the workgroup's K-slice
+  const int wave = dev::wave_id(), tid = threadIdx.x, lane = tid & 63;
+  const int units = (a.tiles + T - 1) / T;
+  int unit, slice;
+  if (!dev::map_tile(blockIdx.x, slices, units, unit, slice)) return;
+  const I4Layout &l = a.l;
+  const int L = l.lanes, j = lane & (L - 1);
+  const int sps = a.steps_per_slice;  // steps per wave
+  const int part = wave % P;
+  const int ws0 = slice * P * sps;                     // first step of the workgroup's slice
+  const int s0 = ws0 + part * sps;                     // first step of this wave
+  const int ns = max(0, min(sps, l.steps - s0));
+  const int sgroups = min(P * sps * L, l.groups - ws0 * L);  // groups of x in the slice
 
   // 1) Activation slice first (L2-resident, short latency), then this wave's
-  //    weight stream.
-  float4 xr[MT][dev::x_iters<GS>()];
-  dev::load_x<MT, GS>(
-      xr, [&](int m) -> const float * { return m < a.m ? a.x + size_t(m) * a.x_stride : nullptr; }, g0, ng, a.k,
-      a.x_vec4 != 0, tid);
-  int stile = tile, srow = lane;
+  //    weight stream.  All loads are unconditional (buffer loads past the end
+  //    return 0); a wave past the last tile reads tile 0 and stops after the
+  //    barrier.
+  // The slice is P*sps*L <= 16*GSW groups (the planner keeps P*L <= 16).
+  float4 xr[MT][dev::x_iters<GSW>()];
+  dev::load_x<MT, GSW>(
+      xr, dev::rsrc(a.x, size_t(a.m) * a.x_stride * 4), [&](int m) { return uint32_t(m) * uint32_t(a.x_stride) * 4u; },
+      a.m, ws0 * L * 32, tid);
+  const int tile = unit * T + wave / P;
+  const bool active = tile < a.tiles;
+  const int t = active ? tile : 0;
+  int b = t, wl = lane;
   const void *nb = a.nib, *sb = a.scl;
   if (a.mode == I4_SWIGLU) {
-    stile = tile >> 1;
-    srow = (tile & 1) * 32 + (lane & 31);
+    b = t >> 1;
+    wl = (t & 1) * 32 + (lane & 31);
     if (lane >= 32) { nb = a.nib2; sb = a.scl2; }
   }
-  const int gq0 = g0 + gw0;  // first group of this wave (multiple of GSW)
   uint4 w[GSW];
   float sc[GSW];
-  dev::load_w<GSW>(w, sc, static_cast<const uint4 *>(nb) + (size_t(stile) * a.g4 + gq0) * 64 + srow,
-                   static_cast<const float *>(sb) + (size_t(stile) * (a.g4 >> 2) + (gq0 >> 2)) * 256 + srow * 4, gq0,
-                   ngw);
+  dev::load_w<GSW>(w, sc, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, wl);
 
   // 2) Fixed-point activation planes in LDS.
-  __shared__ dev::XTile<MT, GS> xs;
-  __shared__ float red[3][MT][64];
-  dev::stage_x<MT, GS>(xs, xr, tid, lane);
+  const dev::XPlanes xs = dev::xplanes_at(dyn_lds, MT, P * sps * L);
+  dev::stage_x<MT, GSW>(xs, xr, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
   __syncthreads();
 
-  // 3) Integer dot per group and token.
+  // 3) Integer dot per group and token, the L lanes of each row, then the P
+  //    parts of each tile (fixed order 0+1+2+3).
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-  dev::dot<MT, GS, GSW>(acc, w, sc, xs, gw0, ngw);
-
-  // 4) Combine the four waves in LDS (fixed order: 0+1+2+3).
-  if (wave > 0) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) red[wave - 1][m][lane] = acc[m];
+  if (active && ns > 0) {
+    dev::XPlanes xp = xs;
+    const int g0 = part * sps * L;
+    xp.q = xs.q + size_t(g0) * dev::kXWords;
+    xp.s2 = xs.s2 + g0;
+    xp.off = xs.off + g0;
+    dev::dot<MT, GSW>(acc, w, sc, xp, L, j, ns);
+    dev::reduce_lanes<MT>(acc, L);
   }
-  __syncthreads();
-  if (wave > 0) return;
+  if (P > 1) {
+    if (part > 0) {
 #pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = ((acc[m] + red[0][m][lane]) + red[1][m][lane]) + red[2][m][lane];
+      for (int m = 0; m < MT; ++m) red[wave][m][lane] = acc[m];
+    }
+    __syncthreads();
+    if (part > 0) return;
+#pragma unroll
+    for (int q = 1; q < P; ++q)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[m] += red[wave + q][m][lane];
+  }
+  if (!active) return;
 
-  // 5) Split-K across workgroups: the last slice of a tile to finish sums all
+  // 4) Split-K across workgroups: the last slice of a tile to finish sums all
   //    slices in slice order.
   if (slices > 1) {
-    float *part = a.partial + (size_t(tile) * slices + slice) * MT * 64;
+    float *part_p = a.partial + (size_t(tile) * slices + slice) * MT * 64 + lane;
     dev::check_xcd(a.xcd_local, a.err, lane);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) dev::xstore(part + m * 64 + lane, acc[m], a.xcd_local);
-    unsigned *ctr = &a.counters[tile * kCounterStride];
+    for (int m = 0; m < MT; ++m) dev::xstore(part_p + m * 64, acc[m], a.xcd_local);
+    unsigned *ctr = &a.counters[size_t(tile) * kCounterStride];
     if (!dev::last_arrival(ctr, unsigned(slices), lane)) return;
     const float *pt = a.partial + size_t(tile) * slices * MT * 64 + lane;
     constexpr int PU = MT >= 8 ? 2 : (MT >= 4 ? 4 : 16);  // independent partial loads in flight
@@ -85,17 +109,17 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
     dev::reset_counter(ctr, lane);
   }
 
-  // 6) Epilogue.
+  // 5) Epilogue: the first lane of each row writes it.
   if (a.mode == I4_SWIGLU) {
+    const int row = b * l.rpb + wl / L;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const float u = __shfl_down(acc[m], 32);
-      const int row = tile * 32 + lane;
-      if (lane < 32 && row < a.n && m < a.m) a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * u;
+      if (lane < 32 && j == 0 && row < a.n && m < a.m) a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * u;
     }
   } else {
-    const int row = tile * 64 + lane;
-    if (row < a.n) {
+    const int row = b * l.rpb + lane / L;
+    if (j == 0 && row < a.n) {
       if (a.mode == I4_ACCUM) {
         a.y[row] = add_mul_nofma(a.y[row], acc[0], a.prob[0]);  // moe.comp:70
       } else {
@@ -107,105 +131,162 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   }
 }
 
-// Raw packed rows -> tiled planes.  One thread per (tile, group, lane).
+// Raw packed rows -> device layout.  One thread per (block, step, lane).
 __global__ void k_int4_repack(const uint8_t *__restrict__ src, I4Layout l, uint4 *__restrict__ nib,
                               float *__restrict__ scl) {
   const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const size_t total = size_t(l.tiles) * l.g4 * 64;
+  const size_t total = size_t(l.blocks) * l.steps * 64;
   if (idx >= total) return;
-  const int r = int(idx & 63);
-  const int g = int((idx >> 6) % l.g4);
-  const int t = int(idx / (size_t(l.g4) * 64));
-  const int srow = t * 64 + r;
+  const int lane = int(idx & 63);
+  const int s = int((idx >> 6) % l.steps);
+  const int b = int(idx / (size_t(l.steps) * 64));
+  const int row = b * l.rpb + lane / l.lanes, g = s * l.lanes + (lane & (l.lanes - 1));
   uint4 words = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-  float s = 0.0f;
-  if (srow < l.rows && g < l.groups) {
-    const uint8_t *blk = src + size_t(srow) * (size_t(l.groups) * 20) + size_t(g) * 20;
+  float sv = 0.0f;
+  if (row < l.rows && g < l.groups) {
+    const uint8_t *blk = src + size_t(row) * (size_t(l.groups) * 20) + size_t(g) * 20;
     const uint32_t *w32 = reinterpret_cast<const uint32_t *>(blk);  // 20-byte groups are 4-aligned
-    s = __uint_as_float(w32[0]);
+    sv = __uint_as_float(w32[0]);
     words = make_uint4(w32[1], w32[2], w32[3], w32[4]);
   }
-  nib[(size_t(t) * l.g4 + g) * 64 + r] = words;
-  scl[((size_t(t) * (l.g4 >> 2) + (g >> 2)) * 64 + r) * 4 + (g & 3)] = s;
+  nib[idx] = words;
+  scl[idx] = sv;
 }
 
-// Bit-exact dequantisation fl32((n-8)*s) of the resident tiled copy -> [rows][cols].
+// Bit-exact dequantisation fl32((n-8)*s) of the resident copy -> [rows][cols].
 __global__ void k_int4_dequant(I4Layout l, const uint4 *__restrict__ nib, const float *__restrict__ scl,
                                float *__restrict__ out) {
   const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const size_t total = size_t(l.rows) * l.cols;
   if (idx >= total) return;
   const int row = int(idx / l.cols), k = int(idx % l.cols);
-  const int t = row / 64, r = row & 63;
-  const int g = k >> 5, j = k & 31;
-  const uint4 w = nib[(size_t(t) * l.g4 + g) * 64 + r];
-  const uint32_t word = sel4u(w, j >> 3);
-  const int n = int((word >> (4 * (j & 7))) & 15u);
-  const float s = scl[((size_t(t) * (l.g4 >> 2) + (g >> 2)) * 64 + r) * 4 + (g & 3)];
-  out[idx] = float(n - 8) * s;
+  const int b = row / l.rpb, r = row % l.rpb;
+  const int g = k >> 5, e = k & 31;
+  const int s = g / l.lanes, lane = r * l.lanes + (g & (l.lanes - 1));
+  const size_t at = (size_t(b) * l.steps + s) * 64 + lane;
+  const uint32_t word = sel4u(nib[at], e >> 3);
+  const int n = int((word >> (4 * (e & 7))) & 15u);
+  out[idx] = float(n - 8) * scl[at];
 }
 
-template <int MT>
-void launch_mt(const I4Launch &a, int gsw, int slices, int grid, hipStream_t st) {
-  switch (gsw) {
-    case 1: hipLaunchKernelGGL((k_int4_matvec<MT, 1>), dim3(grid), dim3(256), 0, st, a, slices); break;
-    case 2: hipLaunchKernelGGL((k_int4_matvec<MT, 2>), dim3(grid), dim3(256), 0, st, a, slices); break;
-    case 4: hipLaunchKernelGGL((k_int4_matvec<MT, 4>), dim3(grid), dim3(256), 0, st, a, slices); break;
-    default: hipLaunchKernelGGL((k_int4_matvec<MT, 8>), dim3(grid), dim3(256), 0, st, a, slices); break;
+template <int MT, int GSW>
+void launch_one(const I4Launch &a, const I4Plan &p, hipStream_t st) {
+  switch (p.tiles_per_wg) {
+    case 1: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 1>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
+    case 2: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 2>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
+    default: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 4>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
   }
+}
+
+// Steps-per-wave templates by token count (register budget).
+constexpr int kGsw1[] = {1, 2, 4, 8};
+constexpr int kGswN[] = {1, 2, 4};
+constexpr int kGswBig[] = {1, 2};
+
+template <int MT>
+void launch_mt(const I4Launch &a, const I4Plan &p, hipStream_t st) {
+  switch (p.gsw) {
+    case 1: launch_one<MT, 1>(a, p, st); return;
+    case 2: launch_one<MT, 2>(a, p, st); return;
+    default: break;
+  }
+  if constexpr (MT <= 4) {
+    if (p.gsw == 4) {
+      launch_one<MT, 4>(a, p, st);
+      return;
+    }
+  }
+  if constexpr (MT == 1) {
+    if (p.gsw == 8) {
+      launch_one<1, 8>(a, p, st);
+      return;
+    }
+  }
+  fail(QNN_E_INVALID_OP, "int4 plan: steps per wave");
+}
+
+int pick_template(int sps, const int *set, int n) {
+  for (int i = 0; i < n; ++i)
+    if (set[i] >= sps) return set[i];
+  return set[n - 1];
 }
 
 }  // namespace
-
-// Groups per wavefront (GSW); a workgroup slice is 4*GSW groups.  The default
-// targets about 6k wavefronts per launch with at most ~40 slices per tile.
-void int4_plan(const I4Layout &l, int m, int *gsw, int *slices) {
-  const int tiles8 = (l.tiles + 7) / 8 * 8;
-  const int target = env_int("QNN_I4_TARGET_WAVES", 3000);
-  const int forced = env_int("QNN_I4_GSW", 0);
-  const int cap = m >= 8 ? 4 : 8;  // LDS and VGPR budget for many tokens
-  int pick = 1;
-  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) {
-    pick = std::min(forced, cap);
-  } else {
-    const int cands[] = {4, 2};  // 8 groups per wave was never faster at M = 1
-    for (int c : cands) {
-      if (c > cap) continue;
-      if (size_t(tiles8) * ((l.g4 + 4 * c - 1) / (4 * c)) * 4 >= size_t(target)) { pick = c; break; }
-    }
-  }
-  *gsw = pick;
-  *slices = (l.g4 + 4 * pick - 1) / (4 * pick);
-}
-
-size_t int4_partial_floats(const I4Layout &l, int m, int slices) {
-  int mt = m <= 1 ? 1 : (m <= 2 ? 2 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16)));
-  return slices > 1 ? size_t(l.tiles) * slices * mt * 64 : 0;
-}
-
-void int4_matvec_launch(const I4Launch &a, int gs, int slices, hipStream_t st) {
-  const int tiles8 = (a.tiles + 7) / 8 * 8;
-  const int grid = tiles8 * slices;
-  if (a.m <= 1) launch_mt<1>(a, gs, slices, grid, st);
-  else if (a.m <= 2) launch_mt<2>(a, gs, slices, grid, st);
-  else if (a.m <= 4) launch_mt<4>(a, gs, slices, grid, st);
-  else if (a.m <= 8) launch_mt<8>(a, gs, slices, grid, st);
-  else launch_mt<16>(a, std::min(gs, 4), slices, grid, st);
-  hip_check(hipGetLastError(), "int4 matvec launch");
-}
 
 I4Layout int4_layout(int rows, int cols) {
   I4Layout l;
   l.rows = rows;
   l.cols = cols;
   l.groups = (cols + 31) / 32;
-  l.g4 = (l.groups + 3) / 4 * 4;
-  l.tiles = (rows + 63) / 64;
+  // Lanes per row: 1 (a wave streams 64 rows, one per lane, and all lanes
+  // share each activation group), measured fastest at the decode shapes.
+  // QNN_I4_LANES selects 2..16 lanes per row instead.
+  l.lanes = 1;
+  const int forced = env_int("QNN_I4_LANES", 0);
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) l.lanes = forced;
+  l.rpb = 64 / l.lanes;
+  l.steps = (l.groups + l.lanes - 1) / l.lanes;
+  l.blocks = (rows + l.rpb - 1) / l.rpb;
   return l;
 }
 
+I4Plan int4_plan(const I4Layout &l, int m, int mode) {
+  I4Plan p;
+  p.mt = m <= 1 ? 1 : (m <= 2 ? 2 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16)));
+  const int tiles = mode == I4_SWIGLU ? 2 * l.blocks : l.blocks;
+  // Tiles per workgroup (the other 4/T waves of a tile split its K-slice and
+  // meet in LDS before any cross-workgroup exchange).
+  const int ft = env_int("QNN_I4_TPW", 1);
+  p.tiles_per_wg = ft == 2 || ft == 4 ? ft : 1;
+  while (p.tiles_per_wg < 4 && (4 / p.tiles_per_wg) * l.lanes > 16) p.tiles_per_wg *= 2;  // slice fits x_iters
+  const int P = 4 / p.tiles_per_wg;
+  // Steps per wave: bounded by the template set (registers) and by the LDS of
+  // the workgroup's activation slice (at most 48 KiB).
+  const int set_max = p.mt == 1 ? 8 : (p.mt <= 4 ? 4 : 2);
+  const int lds_max = int((48 << 10) / (size_t(p.mt) * P * l.lanes * (dev::kXWords * 4 + 8)));
+  const int cap = std::max(1, std::min(set_max, lds_max));
+  // Steps per wave: the largest that splits the K-range into equal workgroup
+  // slices (an uneven last slice was measured up to 40% slower) while giving
+  // at least `target` waves; failing that, the largest that gives the waves.
+  const int target = env_int("QNN_I4_TARGET_WAVES", 3000);
+  const int units = (tiles + p.tiles_per_wg - 1) / p.tiles_per_wg;
+  auto waves = [&](int sps) { return size_t(units) * 4 * ((l.steps + P * sps - 1) / (P * sps)); };
+  const int *set0 = p.mt == 1 ? kGsw1 : (p.mt <= 4 ? kGswN : kGswBig);
+  const int nset0 = p.mt == 1 ? int(sizeof kGsw1 / sizeof(int)) : (p.mt <= 4 ? 3 : 2);
+  int sps = 0;
+  for (int i = nset0 - 1; i >= 0 && !sps; --i)
+    if (set0[i] <= cap && l.steps % (P * set0[i]) == 0 && waves(set0[i]) >= size_t(target)) sps = set0[i];
+  for (int i = nset0 - 1; i >= 0 && !sps; --i)
+    if (set0[i] <= cap && waves(set0[i]) >= size_t(target)) sps = set0[i];
+  if (!sps) sps = 1;
+  const int forced = env_int("QNN_I4_SPS", 0);
+  if (forced > 0) sps = std::min(forced, cap);
+  const int *set = p.mt == 1 ? kGsw1 : (p.mt <= 4 ? kGswN : kGswBig);
+  const int nset = p.mt == 1 ? int(sizeof kGsw1 / sizeof(int)) : (p.mt <= 4 ? 3 : 2);
+  sps = std::min(sps, pick_template(sps, set, nset));
+  p.gsw = pick_template(sps, set, nset);
+  p.steps_per_slice = sps;
+  p.slices = (l.steps + P * sps - 1) / (P * sps);
+  p.lds = dev::xplanes_bytes(p.mt, P * sps * l.lanes);
+  p.grid = (units + 7) / 8 * 8 * p.slices;
+  p.partial_floats = p.slices > 1 ? size_t(tiles) * p.slices * p.mt * 64 : 0;
+  p.counters = size_t(tiles) * kCounterStride;
+  return p;
+}
+
+void int4_matvec_launch(const I4Launch &a0, const I4Plan &p, hipStream_t st) {
+  I4Launch a = a0;
+  a.steps_per_slice = p.steps_per_slice;
+  if (p.mt == 1) launch_mt<1>(a, p, st);
+  else if (p.mt == 2) launch_mt<2>(a, p, st);
+  else if (p.mt == 4) launch_mt<4>(a, p, st);
+  else if (p.mt == 8) launch_mt<8>(a, p, st);
+  else launch_mt<16>(a, p, st);
+  hip_check(hipGetLastError(), "int4 matvec launch");
+}
+
 void int4_repack_launch(const uint8_t *src, const I4Layout &l, void *dst, hipStream_t st) {
-  const size_t total = size_t(l.tiles) * l.g4 * 64;
+  const size_t total = size_t(l.blocks) * l.steps * 64;
   uint4 *nib = static_cast<uint4 *>(dst);
   float *scl = reinterpret_cast<float *>(static_cast<uint8_t *>(dst) + l.nib_bytes());
   hipLaunchKernelGGL(k_int4_repack, dim3((total + 255) / 256), dim3(256), 0, st, src, l, nib, scl);

@@ -1,20 +1,33 @@
 // qnn_int4_dev.h -- device building blocks of the native INT4 matvec kernels
-// (qnn_int4.hip: dense projections; qnn_moe.hip: routed experts).
+// (qnn_int4.hip: dense projections; qnn_moe.hip: routed experts; qnn_mlp.hip:
+// persistent layer stack).
 //
 // Format (src/core/QuickNN.Quantization.Int4.pas:10-94): per 32 weights an
 // fp32 scale s then 16 bytes of offset-binary nibbles n (element j in byte j/2,
-// low nibble for even j); value = fl32((n-8)*s).  Device layout: I4Layout.
+// low nibble for even j); value = fl32((n-8)*s).
 //
-// A workgroup is 4 wavefronts on one 64-row tile (one row per lane) and a
-// K-slice of GS = 4*GSW groups; wave w streams groups [w*GSW, (w+1)*GSW).
-// Every weight load is a 16-byte global_load_dwordx4 and consecutive lanes
-// read consecutive 16-byte pieces.  The activation slice is staged in LDS as
-// 16-bit fixed point per 32-group (two int8 planes); the inner product runs on
-// the raw nibble bytes with v_dot4_i32_i8 and folds the offset and both scales
-// once per group:
+// Device layout (I4Layout): a row is spread over L lanes ("lanes per row",
+// a power of two <= 16) and a 64-lane block holds R = 64/L rows.  Lane
+// l = r*L + j of block b carries groups j, j+L, j+2L, ... of row b*R + r; its
+// step-s group (group s*L + j) sits at
+//     nibbles: 16 B at ((b*S + s)*64 + l)          S = ceil(groups / L)
+//     scale:    4 B at ((b*S + s)*64 + l)
+// so every step of a wave is one 16-byte load per lane over 1 KiB of
+// contiguous nibbles plus one 4-byte load over 256 B of scales.  Padding
+// groups/rows hold scale 0.
+//
+// A wave computes the rows of one block ("tile") over a K-range of steps; the
+// L partial sums of a row meet by cross-lane reduction.  The activation slice
+// of a workgroup is staged in LDS as 16-bit fixed point per 32-group (two int8
+// planes); the inner product runs on the raw nibble bytes with v_dot4_i32_i8
+// and folds the offset and both scales once per group:
 //     sum_j (n_j - 8) s x_j ~= s * s2 * (sum_j n_j (256 q1_j + q2_j) - 8 sum_j (256 q1_j + q2_j))
 // (exact integer arithmetic inside a group; fp32 across groups; relative
 // error of the activation representation <= 2^-16 of the group's max|x|).
+//
+// Loads are issued without branches (out-of-range steps and tokens re-read a
+// valid address and are masked), so the compiler can wait for the activation
+// loads alone while the weight loads are still in flight.
 #pragma once
 #include "qnn_internal.h"
 
@@ -33,76 +46,85 @@ __device__ __forceinline__ uint32_t sel4u(const uint4 &v, int i) {
 // Hardware XCC id of the executing wave (HW_REG_XCC_ID, bits 3:0).
 __device__ __forceinline__ int xcc_id() { return int(__builtin_amdgcn_s_getreg((3 << 11) | 20)) & 15; }
 
-// Activation rows staged for one K-slice: per token and group, 8 words of the
-// high int8 plane, 8 of the low plane, s2 and -8*sum(256 q1 + q2).
-template <int MT, int GS>
-struct XTile {
-  uint32_t h[MT][GS][8];
-  uint32_t l[MT][GS][8];
-  float s2[MT][GS];
-  int off[MT][GS];
+// Wave index as a scalar (uniform) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Activation planes of a K-slice in (dynamic) LDS: per token and group, 8
+// words of the high int8 plane and 8 of the low plane, padded to 80 bytes (an
+// odd number of 16-byte quads: the 16 lanes of a row read 16 consecutive
+// groups, whose 16-byte pieces then fall in distinct bank quads), s2 and
+// -8*sum(256 q1 + q2).
+struct XPlanes {
+  uint32_t *q;  // [tokens][groups][kXWords]: words 0-7 high plane, 8-15 low plane, 16-19 padding
+  float *s2;    // [tokens][groups]
+  int *off;     // [tokens][groups]
+  int groups;   // groups per token in the slice
 };
+constexpr int kXWords = 20;  // words per (token, group): 8 high + 8 low + 4 padding
 
-template <int GS>
-constexpr int x_iters() { return (GS * 32 + 1023) / 1024; }
+__host__ __device__ constexpr size_t xplanes_bytes(int tokens, int groups) {
+  return size_t(tokens) * groups * (kXWords * 4 + 8);
+}
+__device__ __forceinline__ XPlanes xplanes_at(void *lds, int tokens, int groups) {
+  XPlanes p;
+  p.q = static_cast<uint32_t *>(lds);
+  p.s2 = reinterpret_cast<float *>(p.q + size_t(tokens) * groups * kXWords);
+  p.off = reinterpret_cast<int *>(p.s2 + size_t(tokens) * groups);
+  p.groups = groups;
+  return p;
+}
 
-// Loads elements [g0*32, g0*32 + ng*32) of MT activation rows, 4 per thread per
-// pass; row(m) returns the row's base or nullptr (token absent: zeros).
-template <int MT, int GS, class RowF>
-__device__ __forceinline__ void load_x(float4 (&xr)[MT][x_iters<GS>()], RowF row, int g0, int ng, int k, bool vec4,
+// float4 loads per thread and token covering a slice of GSW steps at up to 16
+// lanes per row.
+template <int GSW>
+constexpr int x_iters() { return (GSW * 16 * 32 + 1023) / 1024; }
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 raw-buffer word 3):
+// loads at offsets >= bytes return 0 instead of touching memory, and the
+// per-step offsets of a load sequence travel in scalar registers.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc rsrc(const void *base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(uint32_t(min(bytes, size_t(0xFFFFFFFFu)))),
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 ld128(Rsrc r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float ld32f(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), 0));
+}
+
+// Loads the 4-float pieces of elements [e0, ...) of MT activation rows, one
+// per thread per pass; row m starts at byte rowoff(m) of buffer xr_src (rows
+// hold a multiple of 4 floats, 16-byte aligned).  Nothing is masked here, so
+// no load waits for another; stage_x zeroes the pieces outside the slice, the
+// row or the token count.
+template <int MT, int GSW, class OffF>
+__device__ __forceinline__ void load_x(float4 (&xr)[MT][x_iters<GSW>()], Rsrc src, OffF rowoff, int mt, int e0,
                                        int tid) {
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
-    const float *xp = row(m);
+    const uint32_t base = rowoff(m < mt ? m : 0) + uint32_t(e0 + tid * 4) * 4u;
 #pragma unroll
-    for (int it = 0; it < x_iters<GS>(); ++it) {
-      const int e = (it * 256 + tid) * 4;
-      const int kk = g0 * 32 + e;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (xp != nullptr && e < ng * 32) {
-        if (kk + 3 < k && vec4) {
-          v = *reinterpret_cast<const float4 *>(xp + kk);
-        } else if (kk + 3 < k) {
-          v.x = xp[kk]; v.y = xp[kk + 1]; v.z = xp[kk + 2]; v.w = xp[kk + 3];
-        } else {
-          if (kk < k) v.x = xp[kk];
-          if (kk + 1 < k) v.y = xp[kk + 1];
-          if (kk + 2 < k) v.z = xp[kk + 2];
-        }
-      }
-      xr[m][it] = v;
+    for (int it = 0; it < x_iters<GSW>(); ++it) {
+      const uint4 v = ld128(src, base, uint32_t(it) * 4096u);
+      xr[m][it] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
     }
   }
 }
 
-// This wave's weight stream: GSW scales then GSW nibble pieces, in group
-// order (loads return in issue order, so group g is usable once it lands).
-// nib/sclf point at the wave's first group gq0 of row srow of the stored tile.
+// This wave's weight stream for GSW steps from step s0 of block b (lane wl of
+// the block): nibble pieces and scales.  Steps at or past the matrix's last
+// step read other blocks or zeros (masked in dot).
 template <int GSW>
-__device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], const uint4 *nib, const float *sclf,
-                                       int gq0, int ngw) {
-  if (GSW >= 4) {  // whole scale quads: one 16-byte load per 4 groups
+__device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc nib, Rsrc scl, const I4Layout &l, int b,
+                                       int s0, int wl) {
+  const uint32_t at = uint32_t((size_t(b) * l.steps + s0) * 64 + wl);
 #pragma unroll
-    for (int q = 0; q < GSW / 4; ++q)
-      if (4 * q < ngw) {
-        const float4 s4 = *reinterpret_cast<const float4 *>(sclf + q * 256);
-        sc[4 * q] = s4.x;
-        sc[4 * q + 1] = s4.y;
-        sc[4 * q + 2] = s4.z;
-        sc[4 * q + 3] = s4.w;
-      }
-  } else {
+  for (int g = 0; g < GSW; ++g) sc[g] = ld32f(scl, at * 4u, uint32_t(g) * 256u);
 #pragma unroll
-    for (int g = 0; g < GSW; ++g) {
-      if (g < ngw) {
-        const int gg = gq0 + g;  // scale of group gg: quad gg/4, component gg%4
-        sc[g] = sclf[((gg >> 2) - (gq0 >> 2)) * 256 + (gg & 3)];
-      }
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < GSW; ++g)
-    if (g < ngw) w[g] = nib[g * 64];
+  for (int g = 0; g < GSW; ++g) w[g] = ld128(nib, at * 16u, uint32_t(g) * 1024u);
 }
 
 // Quantises the loaded slice per 32-element group to 16-bit fixed point,
@@ -111,15 +133,20 @@ __device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], const 
 // (|x - s2(256 q1 + q2)| <= s2/2 = amax/65024).  The int8 planes match the
 // nibble bytes of a weight dword: dword c of a group holds elements 8c..8c+7,
 // its low nibbles are the even elements and its high nibbles the odd ones, so
-// word 2c packs x[8c+0,2,4,6] and word 2c+1 x[8c+1,3,5,7].
-template <int MT, int GS>
-__device__ __forceinline__ void stage_x(XTile<MT, GS> &xs, const float4 (&xr)[MT][x_iters<GS>()], int tid, int lane) {
+// plane word 2c packs x[8c+0,2,4,6] and word 2c+1 x[8c+1,3,5,7].  Words 0-7 of
+// an entry are the high plane, 8-15 the low plane.
+// Pieces of token m >= mt, of element >= ne within the slice or of row
+// element >= k are zero (e0 = first element of the slice).
+template <int MT, int GSW>
+__device__ __forceinline__ void stage_x(const XPlanes &xs, const float4 (&xr)[MT][x_iters<GSW>()], int mt, int e0,
+                                        int ne, int k, int tid, int lane) {
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
-    for (int it = 0; it < x_iters<GS>(); ++it) {
+    for (int it = 0; it < x_iters<GSW>(); ++it) {
       const int e = (it * 256 + tid) * 4;  // first element of this thread, within the slice
-      const float4 v = xr[m][it];
+      const bool ok = m < mt && e < ne && e0 + e < k;
+      const float4 v = ok ? xr[m][it] : make_float4(0.f, 0.f, 0.f, 0.f);
       float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
       amax = fmaxf(amax, __shfl_xor(amax, 1));
       amax = fmaxf(amax, __shfl_xor(amax, 2));
@@ -141,39 +168,42 @@ __device__ __forceinline__ void stage_x(XTile<MT, GS> &xs, const float4 (&xr)[MT
       sumq += __shfl_xor(sumq, 1);
       sumq += __shfl_xor(sumq, 2);
       sumq += __shfl_xor(sumq, 4);
-      if (e < GS * 32) {
-        const int g = e >> 5, i0 = e & 31;  // element 8c + (i0 & 7) of group g
+      const int g = e >> 5;
+      if (g < xs.groups) {
+        const int i0 = e & 31;  // element 8c + (i0 & 7) of group g
         const int c = i0 >> 3, half = (i0 >> 2) & 1;
         // bytes for even slots (elements +0, +2) and odd slots (+1, +3) of this half dword
         const uint32_t he = (uint32_t(h[0]) & 255u) | ((uint32_t(h[2]) & 255u) << 8);
         const uint32_t ho = (uint32_t(h[1]) & 255u) | ((uint32_t(h[3]) & 255u) << 8);
         const uint32_t le = (uint32_t(l[0]) & 255u) | ((uint32_t(l[2]) & 255u) << 8);
         const uint32_t lo = (uint32_t(l[1]) & 255u) | ((uint32_t(l[3]) & 255u) << 8);
-        uint16_t *ph = reinterpret_cast<uint16_t *>(&xs.h[m][g][0]);
-        uint16_t *pl = reinterpret_cast<uint16_t *>(&xs.l[m][g][0]);
+        const size_t mg = size_t(m) * xs.groups + g;
+        uint16_t *ph = reinterpret_cast<uint16_t *>(xs.q + mg * kXWords);
+        uint16_t *pl = ph + 16;
         ph[(2 * c) * 2 + half] = uint16_t(he);
         ph[(2 * c + 1) * 2 + half] = uint16_t(ho);
         pl[(2 * c) * 2 + half] = uint16_t(le);
         pl[(2 * c + 1) * 2 + half] = uint16_t(lo);
         if ((lane & 7) == 0) {
-          xs.s2[m][g] = s1 * 0.00390625f;
-          xs.off[m][g] = -8 * sumq;
+          xs.s2[mg] = s1 * 0.00390625f;
+          xs.off[mg] = -8 * sumq;
         }
       }
     }
   }
 }
 
-// Dequantise-free integer dot over this wave's groups, per group and token:
+// Dequantise-free integer dot over this lane's groups (steps 0..ns-1 of the
+// slice; group s*L + j of the slice for lane j of its row):
 //   isum = 256 * dot(n, q1) + dot(n, q2) - 8 * sum(256 q1 + q2)  (exact, < 2^24)
 //   acc += float(isum) * (s * s2).
-template <int MT, int GS, int GSW>
+template <int MT, int GSW>
 __device__ __forceinline__ void dot(float (&acc)[MT], const uint4 (&w)[GSW], const float (&sc)[GSW],
-                                    const XTile<MT, GS> &xs, int gw0, int ngw) {
+                                    const XPlanes &xs, int lanes, int j, int ns) {
 #pragma unroll
   for (int g = 0; g < GSW; ++g) {
-    if (g < ngw) {
-      const int gl = gw0 + g;
+    if (g < ns) {
+      const int gl = g * lanes + j;
       uint32_t nlo[4], nhi[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -183,9 +213,9 @@ __device__ __forceinline__ void dot(float (&acc)[MT], const uint4 (&w)[GSW], con
       }
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const uint4 *qh = reinterpret_cast<const uint4 *>(&xs.h[m][gl][0]);
-        const uint4 *ql = reinterpret_cast<const uint4 *>(&xs.l[m][gl][0]);
-        const uint4 h0 = qh[0], h1 = qh[1], l0 = ql[0], l1 = ql[1];
+        const size_t mg = size_t(m) * xs.groups + gl;
+        const uint4 *q = reinterpret_cast<const uint4 *>(xs.q + mg * kXWords);
+        const uint4 h0 = q[0], h1 = q[1], l0 = q[2], l1 = q[3];
         int ah0 = 0, ah1 = 0, al0 = 0, al1 = 0;
         ah0 = __builtin_amdgcn_sdot4(int(nlo[0]), int(h0.x), ah0, false);
         ah1 = __builtin_amdgcn_sdot4(int(nhi[0]), int(h0.y), ah1, false);
@@ -203,10 +233,20 @@ __device__ __forceinline__ void dot(float (&acc)[MT], const uint4 (&w)[GSW], con
         ah1 = __builtin_amdgcn_sdot4(int(nhi[3]), int(h1.w), ah1, false);
         al0 = __builtin_amdgcn_sdot4(int(nlo[3]), int(l1.z), al0, false);
         al1 = __builtin_amdgcn_sdot4(int(nhi[3]), int(l1.w), al1, false);
-        const int isum = ((ah0 + ah1) << 8) + (al0 + al1) + xs.off[m][gl];
-        acc[m] = fmaf(float(isum), sc[g] * xs.s2[m][gl], acc[m]);
+        const int isum = ((ah0 + ah1) << 8) + (al0 + al1) + xs.off[mg];
+        acc[m] = fmaf(float(isum), sc[g] * xs.s2[mg], acc[m]);
       }
     }
+  }
+}
+
+// Sum over the L lanes of each row (L a power of two): afterwards every lane
+// of a row holds the row total.  Pairwise order, identical in every launch.
+template <int MT>
+__device__ __forceinline__ void reduce_lanes(float (&acc)[MT], int lanes) {
+  for (int o = 1; o < lanes; o <<= 1) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] += __shfl_xor(acc[m], o);
   }
 }
 
@@ -266,15 +306,15 @@ __device__ __forceinline__ void sum_slices(float (&acc)[MT], AddrF part, int sli
   }
 }
 
-// blockIdx -> (tile, rest): every workgroup of a tile goes to the same XCD
+// blockIdx -> (unit, rest): every workgroup of a unit goes to the same XCD
 // (workgroups are dealt round-robin over the 8 XCDs), so the split-K partial
-// sums of a tile stay in one L2.  `per` = workgroups per tile.
-__device__ __forceinline__ bool map_tile(int b, int per, int tiles, int &tile, int &rest) {
+// sums of a unit stay in one L2.  `per` = workgroups per unit.
+__device__ __forceinline__ bool map_tile(int b, int per, int units, int &unit, int &rest) {
   const int xcd = b & 7, k = b >> 3;
   const int q = k / per;
-  tile = q * 8 + xcd;
+  unit = q * 8 + xcd;
   rest = k - q * per;
-  return tile < tiles;
+  return unit < units;
 }
 
 }  // namespace dev

@@ -41,18 +41,20 @@ inline int env_int(const char *name, int dflt) {
 // ---------------------------------------------------------------------------
 // Device layouts
 // ---------------------------------------------------------------------------
-// Native INT4 tiled layout.  A packed INT4 matrix [N][G*20 B] (G = ceil(K/32)
-// groups of fp32 scale + 16 nibble bytes) is stored as tiles of 64 rows, one
-// row per lane of a wavefront:
-//   nibble plane: 16 B at ((t*g4 + g)*64 + r)       -- group g of row r of tile t
-//   scale plane:  16 B at ((t*(g4/4) + g/4)*64 + r)  -- scales of groups 4q..4q+3
-// g4 = G rounded up to a multiple of 4.  Padding rows/groups carry nibble 8 and
-// scale 0 (value 0).  The fused gate/up kernel reads two such matrices: lanes
-// 0-31 stream 32 gate rows and lanes 32-63 the same 32 up rows.
+// Native INT4 device layout (qnn_int4_dev.h).  A packed INT4 matrix
+// [N][G*20 B] (G = ceil(K/32) groups of fp32 scale + 16 nibble bytes) is held
+// as 64-lane blocks of R = 64/L rows, L lanes per row; lane l = r*L + j of
+// block b carries groups j, j+L, ... of row b*R + r, step s at
+//   nibbles: 16 B at ((b*S + s)*64 + l),   scales: 4 B at ((b*S + s)*64 + l)
+// with S = ceil(G / L) steps.  Padding rows/groups hold scale 0 and nibble 8.
 struct I4Layout {
-  int rows = 0, cols = 0, groups = 0, g4 = 0, tiles = 0;
-  __host__ __device__ size_t nib_bytes() const { return size_t(tiles) * g4 * 64 * 16; }
-  __host__ __device__ size_t scale_bytes() const { return size_t(tiles) * g4 * 64 * 4; }
+  int rows = 0, cols = 0, groups = 0;
+  int lanes = 1;   // L: lanes per row (power of two <= 16)
+  int rpb = 64;    // R = 64 / L rows per block
+  int steps = 0;   // S
+  int blocks = 0;  // ceil(rows / R)
+  __host__ __device__ size_t nib_bytes() const { return size_t(blocks) * steps * 64 * 16; }
+  __host__ __device__ size_t scale_bytes() const { return size_t(blocks) * steps * 64 * 4; }
   __host__ __device__ size_t bytes() const { return nib_bytes() + scale_bytes(); }
 };
 
@@ -99,17 +101,18 @@ enum I4Mode { I4_STORE = 0, I4_ACCUM = 1, I4_SWIGLU = 2 };
 constexpr int kCounterStride = 64;
 
 struct I4Launch {
-  const void *nib = nullptr;   // tiled nibble plane (gate in I4_SWIGLU mode)
-  const void *scl = nullptr;   // tiled scale plane
+  I4Layout l;                  // layout of the (gate) matrix
+  const void *nib = nullptr;   // nibble plane (gate in I4_SWIGLU mode)
+  const void *scl = nullptr;   // scale plane
   const void *nib2 = nullptr;  // I4_SWIGLU: up matrix planes (same layout)
   const void *scl2 = nullptr;
-  const float *x = nullptr;
-  int x_stride = 0;  // floats between activation rows
-  int x_vec4 = 0;    // x and x_stride allow 16-byte loads
+  const float *x = nullptr;  // rows of k floats (k % 4 == 0, 16-byte aligned), x_stride apart
+  int x_stride = 0;
   float *y = nullptr;
   int y_stride = 0;
-  int k = 0, n = 0, m = 1;  // input features, valid output rows, tokens (<= 16)
-  int tiles = 0, g4 = 0;    // wave tiles (64 output rows; 32 in I4_SWIGLU mode), groups/4*4
+  int k = 0, n = 0, m = 1;  // input features, valid output rows, tokens
+  int tiles = 0;            // wave tiles: blocks (I4_SWIGLU: 2 per block, 32 lanes of gate + 32 of up)
+  int steps_per_slice = 0;  // steps per wave (a workgroup slice is 4/T times that)
   int mode = I4_STORE;
   const float *prob = nullptr;  // I4_ACCUM: pointer to p
   float *partial = nullptr;     // split-K scratch
@@ -117,11 +120,16 @@ struct I4Launch {
   int xcd_local = 0;            // combine slices through the XCD's L2 (placement verified)
   int *err = nullptr;           // error word (bit 4: unexpected XCD placement)
 };
+struct I4Plan {
+  int mt = 1, gsw = 1, slices = 1, grid = 0, steps_per_slice = 1, tiles_per_wg = 1;
+  size_t lds = 0;             // dynamic LDS bytes
+  size_t partial_floats = 0;  // split-K scratch
+  size_t counters = 0;
+};
 bool xcd_probe(hipStream_t s);  // true when workgroup b runs on XCD b % 8
-// Chooses the split-K slice and returns (partial floats, counters) needed.
-void int4_plan(const I4Layout &l, int m, int *gs, int *slices);
-size_t int4_partial_floats(const I4Layout &l, int m, int slices);
-void int4_matvec_launch(const I4Launch &a, int gs, int slices, hipStream_t s);
+// Launch geometry for m tokens (at most 16 per launch) in the given mode.
+I4Plan int4_plan(const I4Layout &l, int m, int mode);
+void int4_matvec_launch(const I4Launch &a, const I4Plan &p, hipStream_t s);
 void int4_repack_launch(const uint8_t *src, const I4Layout &l, void *dst, hipStream_t s);
 I4Layout int4_layout(int rows, int cols);
 void int4_dequant_launch(const I4Layout &l, const void *w, float *out, hipStream_t s);
@@ -142,6 +150,7 @@ void misc_moe_scatter(float *dst, size_t dst_n, const float *y, const float *ind
                       size_t routes_n, int n, int hidden, int topk, int offset, int route_index, int single_row,
                       int prob_base, int *err, hipStream_t s);
 void misc_bias_add(float *dst, const void *bias, int bias_bf16, int rows, int cols, hipStream_t s);
+void misc_pad_rows(float *dst, const float *src, int rows, int cols, int cols_pad, hipStream_t s);
 
 // Device-side routed experts (qnn_moe.hip).  Every expert of a set is one
 // contiguous tiled INT4 matrix per projection at base + e * stride.
@@ -163,7 +172,8 @@ struct MoELaunch {
   int *err = nullptr;  // bit 8: invalid route ids
 };
 struct MoEPlanSizes {
-  int slots = 0, mt = 1, gsw = 4, slices_gu = 1, slices_dn = 1;
+  int slots = 0, mt = 1, gsw = 4, slices_gu = 1, slices_dn = 1, sps_gu = 1, sps_dn = 1;
+  size_t lds_gu = 0, lds_dn = 0;  // dynamic LDS per launch
   size_t partial_floats = 0, counters = 0;
 };
 MoEPlanSizes moe_plan(const MoELaunch &a);
@@ -179,29 +189,6 @@ void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, co
                     void *frag, int *ea, float *c, hipStream_t s);
 void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
 
-// Persistent INT4 MLP layer stack (qnn_mlp.hip).
-struct MlpLayerPtrs {
-  const uint4 *gnib; const float *gscl;  // gate
-  const uint4 *unib; const float *uscl;  // up
-  const uint4 *dnib; const float *dscl;  // down
-};
-struct MlpArgs {
-  const MlpLayerPtrs *w = nullptr;  // device array [layers]
-  int layers = 0, hidden = 0, inter = 0;
-  int g4_gu = 0, g4_d = 0, tiles_gu = 0, tiles_d = 0, slices_gu = 0, slices_d = 0;
-  const float *x0 = nullptr;
-  float *out = nullptr;
-  float *hbuf = nullptr, *ybuf = nullptr;      // [2][inter], [2][hidden]
-  float *part_gu = nullptr, *part_d = nullptr;  // [tiles][slices][64]
-  unsigned *tick_gu = nullptr, *tick_d = nullptr;                 // stride kCounterStride
-  unsigned long long *flag_gu = nullptr, *flag_d = nullptr;       // stride 8
-  unsigned long long *epoch = nullptr;
-  unsigned *exit_count = nullptr, *abort = nullptr;
-  int *err = nullptr;
-  unsigned spin_limit = 0;
-};
-int mlp_stack_grid(int gswu, int gswd, int want);
-void mlp_stack_launch(const MlpArgs &a, int gswu, int gswd, int grid, hipStream_t s);
 
 // GGUF (qnn_gguf.hip).
 enum GGMode { GG_STORE = 0, GG_SWIGLU = 2 };

@@ -222,6 +222,14 @@ __global__ void k_bias_add(float *dst, const void *bias, int bf16, int rows, int
   dst[id] = dst[id] + load_vec(bias, bf16, id % cols);
 }
 
+// Rows of `cols` floats -> rows of `cols_pad` floats, zero tail.
+__global__ void k_pad_rows(float *dst, const float *src, int rows, int cols, int cols_pad) {
+  const long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long long)rows * cols_pad) return;
+  const int r = int(id / cols_pad), c = int(id % cols_pad);
+  dst[id] = c < cols ? src[(long long)r * cols + c] : 0.0f;
+}
+
 // Records the hardware XCC id (HW_REG_XCC_ID) of each workgroup.
 __global__ void k_xcc_probe(int *out) {
   if (threadIdx.x == 0) out[blockIdx.x] = int(__builtin_amdgcn_s_getreg((3 << 11) | 20));
@@ -297,6 +305,12 @@ void misc_bias_add(float *dst, const void *bias, int bias_bf16, int rows, int co
   hipLaunchKernelGGL(k_bias_add, dim3(blocks((long long)rows * cols, 256)), dim3(256), 0, s, dst, bias, bias_bf16,
                      rows, cols);
   hip_check(hipGetLastError(), "bias add");
+}
+
+void misc_pad_rows(float *dst, const float *src, int rows, int cols, int cols_pad, hipStream_t s) {
+  hipLaunchKernelGGL(k_pad_rows, dim3(blocks((long long)rows * cols_pad, 256)), dim3(256), 0, s, dst, src, rows, cols,
+                     cols_pad);
+  hip_check(hipGetLastError(), "pad rows");
 }
 
 }  // namespace qnn

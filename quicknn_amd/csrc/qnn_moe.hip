@@ -13,7 +13,7 @@
 //   2. down:    y[R] = W_d[e] h[R], then out[t] = sum over the token's routes in
 //      ascending expert id of p[R] * y[R] (starting from 0, the reference's
 //      GO_FILL + accumulate order).
-// The grid is (tile, slot, K-slice); slot s is the s-th smallest expert id
+// The grid is (4 tiles, slot, K-slice); slot s is the s-th smallest expert id
 // present in the routes, so only routed experts' weights are read, each once
 // per launch for all of its tokens.  Every workgroup derives its slot's expert
 // and token positions from the route ids itself (a few LDS operations), so no
@@ -94,8 +94,8 @@ __device__ void build_plan(MoEPlan &pl, const MoELaunch &a, int n, int slot, int
   }
 }
 
-// Wave 0 of the combining workgroup: ord[t*k + r] = j of the token's r-th
-// smallest route id (ties: lower j).
+// ord[t*k + r] = j of token t's r-th smallest route id (ties: lower j), by
+// wave 0 of every down-launch workgroup (only a tile's last arrival reads it).
 __device__ void build_order(MoEPlan &pl, int n, int k, int lane) {
   for (int i = lane; i < n; i += 64) {
     const int t0 = (i / k) * k;
@@ -107,90 +107,95 @@ __device__ void build_order(MoEPlan &pl, int n, int k, int lane) {
     }
     pl.ord[t0 + r] = uint8_t(i - t0);
   }
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// DOWN = false: gate/up launch (tile = 32 output rows, lanes 0-31 gate, 32-63
-// up).  DOWN = true: down launch (tile = 64 rows) + expert combine.
+// DOWN = false: gate/up launch (a tile is half a 64-lane block: its gate rows
+// in lanes 0-31 and the same up rows in lanes 32-63).  DOWN = true: down
+// launch (a tile is one block) + expert combine.  A workgroup is one tile of
+// one slot and a K-slice of 4*sps steps; wave w takes steps [w*sps, (w+1)*sps)
+// of it and the four partial sums meet in LDS in wave order.
 template <int MT, int GSW, bool DOWN>
-__global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices, const int slots) {
-  constexpr int GS = 4 * GSW;
+__global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices, const int sps, const int slots) {
+  extern __shared__ uint4 dyn_lds[];
+  __shared__ float red[3][MT][64];
   const int n = a.rows * a.topk;
-  const I4Layout &L = DOWN ? a.dn : a.gu;
-  const int tiles = DOWN ? a.dn.tiles : (a.inter + 31) / 32;
+  const I4Layout &l = DOWN ? a.dn : a.gu;
+  const int tiles = DOWN ? l.blocks : 2 * l.blocks;
   const int nout = DOWN ? a.hidden : a.inter;
   int tile, rest;
   if (!dev::map_tile(blockIdx.x, slots * slices, tiles, tile, rest)) return;
   const int slot = rest / slices, slice = rest - slot * slices;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = dev::wave_id();
 
   __shared__ MoEPlan pl;
-  if (wave == 0) build_plan(pl, a, n, slot, lane);
+  if (wave == 0) {
+    build_plan(pl, a, n, slot, lane);
+    if (DOWN) build_order(pl, n, a.topk, lane);
+  }
   __syncthreads();
   const int e = pl.e, c = pl.c;
   if (e < 0) return;  // fewer routed experts than slots
 
-  const int g0 = slice * GS;
-  const int ng = min(GS, L.g4 - g0);
-  const int gw0 = wave * GSW;
-  const int ngw = max(0, min(GSW, ng - gw0));
-  const int gq0 = g0 + gw0;
+  const int L = l.lanes, j = lane & (L - 1);
+  const int ws0 = slice * 4 * sps;                         // first step of the slice
+  const int s0 = ws0 + wave * sps;                         // first step of this wave
+  const int ns = max(0, min(sps, l.steps - s0));
+  const int sgroups = min(4 * sps * L, l.groups - ws0 * L);
+  const int kin = DOWN ? a.inter : a.hidden;  // both multiples of 4 (checked by the host)
 
-  // weights of expert e: one contiguous tiled matrix per expert
-  int stile = tile, srow = lane;
+  // weights of expert e: one contiguous matrix per expert
+  int b = tile, wl = lane;
   const uint8_t *wbase;
   if (DOWN) {
     wbase = a.down + size_t(e) * a.dn_stride;
   } else {
-    stile = tile >> 1;
-    srow = (tile & 1) * 32 + (lane & 31);
+    b = tile >> 1;
+    wl = (tile & 1) * 32 + (lane & 31);
     wbase = (lane < 32 ? a.gate : a.up) + size_t(e) * a.gu_stride;
   }
-  const uint4 *nib = reinterpret_cast<const uint4 *>(wbase) + (size_t(stile) * L.g4 + gq0) * 64 + srow;
-  const float *scl =
-      reinterpret_cast<const float *>(wbase + L.nib_bytes()) + (size_t(stile) * (L.g4 >> 2) + (gq0 >> 2)) * 256 + srow * 4;
-  const int kin = DOWN ? a.inter : a.hidden;
-  auto xrow = [&](int m) -> const float * {
-    if (m >= c) return nullptr;
-    const int R = pl.pos[m];
-    return DOWN ? a.h + size_t(R) * a.inter : a.x + size_t(R / a.topk) * a.hidden;
+  // activation rows: h[R] (down) or x[token of R] (gate/up)
+  const dev::Rsrc xsrc = DOWN ? dev::rsrc(a.h, size_t(n) * a.inter * 4) : dev::rsrc(a.x, size_t(a.rows) * a.hidden * 4);
+  auto xoff = [&](int m) -> uint32_t {
+    const int R = pl.pos[min(m, c - 1)];
+    return DOWN ? uint32_t(R) * uint32_t(a.inter) * 4u : uint32_t(R / a.topk) * uint32_t(a.hidden) * 4u;
   };
-  const bool vec4 = (kin % 4) == 0;
-
-  float4 xr[MT][dev::x_iters<GS>()];
-  dev::load_x<MT, GS>(xr, xrow, g0, ng, kin, vec4, tid);
+  float4 xr[MT][dev::x_iters<GSW>()];
+  dev::load_x<MT, GSW>(xr, xsrc, xoff, min(c, MT), ws0 * L * 32, tid);
   uint4 w[GSW];
   float sc[GSW];
-  dev::load_w<GSW>(w, sc, nib, scl, gq0, ngw);
+  dev::load_w<GSW>(w, sc, dev::rsrc(wbase, l.nib_bytes()), dev::rsrc(wbase + l.nib_bytes(), l.scale_bytes()), l, b, s0,
+                   wl);
 
-  __shared__ dev::XTile<MT, GS> xs;
-  __shared__ float red[3][MT][64];
+  const dev::XPlanes xs = dev::xplanes_at(dyn_lds, MT, 4 * sps * L);
+  dev::XPlanes xw = xs;  // this wave's groups
+  xw.q = xs.q + size_t(wave) * sps * L * dev::kXWords;
+  xw.s2 = xs.s2 + wave * sps * L;
+  xw.off = xs.off + wave * sps * L;
   float *part = a.partial + (size_t(tile) * slices + slice) * n * 64 + lane;
-  auto finish = [&](int R, float v) {  // final value of row (tile, lane) for position R
+  const int row = DOWN ? b * l.rpb + lane / L : b * l.rpb + wl / L;
+  auto finish = [&](int R, float v) {  // final value of this lane's row for position R
     if (DOWN) {
-      const int row = tile * 64 + lane;
-      if (row < nout) dev::xstore(a.y + size_t(R) * a.hidden + row, v, a.xcd_local);
+      if (j == 0 && row < nout) dev::xstore(a.y + size_t(R) * a.hidden + row, v, a.xcd_local);
     } else {
       const float u = __shfl_down(v, 32);
-      const int row = tile * 32 + lane;
-      if (lane < 32 && row < nout) a.h[size_t(R) * a.inter + row] = dev::silu(v) * u;
+      if (lane < 32 && j == 0 && row < nout) a.h[size_t(R) * a.inter + row] = dev::silu(v) * u;
     }
   };
 
   for (int m0 = 0; m0 < c; m0 += MT) {
     if (m0 > 0) {
-      auto xrow_c = [&](int m) { return xrow(m0 + m); };
-      dev::load_x<MT, GS>(xr, xrow_c, g0, ng, kin, vec4, tid);
+      dev::load_x<MT, GSW>(xr, xsrc, [&](int m) { return xoff(m0 + m); }, min(c - m0, MT), ws0 * L * 32, tid);
       __syncthreads();  // the previous chunk's LDS reads are done
     }
-    dev::stage_x<MT, GS>(xs, xr, tid, lane);
+    dev::stage_x<MT, GSW>(xs, xr, min(c - m0, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
     __syncthreads();
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-    dev::dot<MT, GS, GSW>(acc, w, sc, xs, gw0, ngw);
+    if (ns > 0) {
+      dev::dot<MT, GSW>(acc, w, sc, xw, L, j, ns);
+      dev::reduce_lanes<MT>(acc, L);
+    }
     if (wave > 0) {
 #pragma unroll
       for (int m = 0; m < MT; ++m) red[wave - 1][m][lane] = acc[m];
@@ -219,8 +224,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
     for (int m0 = 0; m0 < c; m0 += MT) {
       float acc[MT];
       dev::sum_slices<MT, 4>(
-          acc,
-          [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices,
+          acc, [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices,
           a.xcd_local);
 #pragma unroll
       for (int m = 0; m < MT; ++m)
@@ -230,33 +234,34 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   }
   if (!DOWN) return;
 
-  // expert combine: the last (slot, tile) of this tile to finish
+  // expert combine: the last (slot, tile) of this tile to finish; lane (r, j)
+  // combines row r for tokens j, j+L, ...
   dev::check_xcd(a.xcd_local, a.err, lane);
   unsigned *cctr = &a.counters[(size_t(tiles) * slots + tile) * kCounterStride];
   if (!dev::last_arrival(cctr, unsigned(pl.active), lane)) return;
-  build_order(pl, n, a.topk, lane);
-  const int row = tile * 64 + lane;
-  for (int t = 0; t < a.rows; ++t) {
-    float acc = 0.0f;
-    for (int r = 0; r < a.topk; ++r) {
-      const int R = t * a.topk + pl.ord[t * a.topk + r];
-      if (pl.ids[R] >= uint32_t(a.experts)) continue;
-      const float p = a.routes[n + R];
-      const float v = row < nout ? dev::xload(a.y + size_t(R) * a.hidden + row, a.xcd_local) : 0.0f;
-      acc = add_mul_nofma(acc, v, p);  // moe.comp:70 / :126: out + y*p
+  if (row < nout) {
+    for (int tk = j; tk < a.rows; tk += L) {
+      float acc = 0.0f;
+      for (int r = 0; r < a.topk; ++r) {
+        const int R = tk * a.topk + pl.ord[tk * a.topk + r];
+        if (pl.ids[R] >= uint32_t(a.experts)) continue;
+        const float p = a.routes[n + R];
+        const float v = dev::xload(a.y + size_t(R) * a.hidden + row, a.xcd_local);
+        acc = add_mul_nofma(acc, v, p);  // moe.comp:70 / :126: out + y*p
+      }
+      a.out[size_t(tk) * a.hidden + row] = acc;
     }
-    if (row < nout) a.out[size_t(t) * a.hidden + row] = acc;
   }
   dev::reset_counter(cctr, lane);
 }
 
 template <int MT, int GSW>
-void launch_mt(const MoELaunch &a, int slices_gu, int slices_dn, int slots, hipStream_t s) {
-  const int tgu = (a.inter + 31) / 32, tdn = a.dn.tiles;
-  const int ggu = (tgu + 7) / 8 * 8 * slots * slices_gu;
-  const int gdn = (tdn + 7) / 8 * 8 * slots * slices_dn;
-  hipLaunchKernelGGL((k_moe<MT, GSW, false>), dim3(ggu), dim3(256), 0, s, a, slices_gu, slots);
-  hipLaunchKernelGGL((k_moe<MT, GSW, true>), dim3(gdn), dim3(256), 0, s, a, slices_dn, slots);
+void launch_mt(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
+  const int tgu = 2 * a.gu.blocks, tdn = a.dn.blocks;
+  const int ggu = (tgu + 7) / 8 * 8 * p.slots * p.slices_gu;
+  const int gdn = (tdn + 7) / 8 * 8 * p.slots * p.slices_dn;
+  hipLaunchKernelGGL((k_moe<MT, GSW, false>), dim3(ggu), dim3(256), p.lds_gu, s, a, p.slices_gu, p.sps_gu, p.slots);
+  hipLaunchKernelGGL((k_moe<MT, GSW, true>), dim3(gdn), dim3(256), p.lds_dn, s, a, p.slices_dn, p.sps_dn, p.slots);
 }
 
 }  // namespace
@@ -266,18 +271,24 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
   const int n = a.rows * a.topk;
   p.slots = std::min(a.experts, n);
   p.mt = a.rows == 1 ? 1 : (a.rows * a.topk <= 2 * a.experts ? 2 : 4);
-  p.gsw = env_int("QNN_MOE_GSW", 0);
-  if (p.gsw != 1 && p.gsw != 2 && p.gsw != 4) {
-    // largest slice whose group count divides both matrices' groups evenly
-    p.gsw = 1;
-    for (int g : {4, 2}) {
-      if (a.gu.g4 % (4 * g) == 0 && a.dn.g4 % (4 * g) == 0) { p.gsw = g; break; }
-    }
-  }
-  const int gs = 4 * p.gsw;
-  p.slices_gu = (a.gu.g4 + gs - 1) / gs;
-  p.slices_dn = (a.dn.g4 + gs - 1) / gs;
-  const int tgu = (a.inter + 31) / 32, tdn = a.dn.tiles;
+  // Steps per wave: 2 (a workgroup slice of 8 groups per 64-row tile),
+  // measured fastest at 1 and 16 tokens for 128 experts of 768 x 2048;
+  // QNN_MOE_SPS overrides.  Bounded by the activation-slice LDS budget.
+  const int forced = env_int("QNN_MOE_SPS", 0);
+  auto steps = [&](const I4Layout &l, int) {
+    const int lds_cap = int((48 << 10) / (size_t(p.mt) * 4 * l.lanes * (dev::kXWords * 4 + 8)));
+    const int cap = std::max(1, std::min(8, lds_cap));
+    return std::min(forced > 0 ? forced : 2, cap);
+  };
+  p.sps_gu = steps(a.gu, 2 * a.gu.blocks);
+  p.sps_dn = steps(a.dn, a.dn.blocks);
+  p.slices_gu = (a.gu.steps + 4 * p.sps_gu - 1) / (4 * p.sps_gu);
+  p.slices_dn = (a.dn.steps + 4 * p.sps_dn - 1) / (4 * p.sps_dn);
+  const int need = std::max(p.sps_gu, p.sps_dn);
+  p.gsw = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+  p.lds_gu = dev::xplanes_bytes(p.mt, 4 * p.sps_gu * a.gu.lanes);
+  p.lds_dn = dev::xplanes_bytes(p.mt, 4 * p.sps_dn * a.dn.lanes);
+  const int tgu = 2 * a.gu.blocks, tdn = a.dn.blocks;
   p.partial_floats = std::max(size_t(tgu) * p.slices_gu, size_t(tdn) * p.slices_dn) * n * 64;
   p.counters = (size_t(std::max(tgu, tdn)) * p.slots + tdn) * kCounterStride;
   return p;
@@ -285,15 +296,18 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
 
 void moe_launch(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
   switch (p.mt * 16 + p.gsw) {
-    case 1 * 16 + 1: launch_mt<1, 1>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 1 * 16 + 2: launch_mt<1, 2>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 1 * 16 + 4: launch_mt<1, 4>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 2 * 16 + 1: launch_mt<2, 1>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 2 * 16 + 2: launch_mt<2, 2>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 2 * 16 + 4: launch_mt<2, 4>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 4 * 16 + 1: launch_mt<4, 1>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 4 * 16 + 2: launch_mt<4, 2>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
-    case 4 * 16 + 4: launch_mt<4, 4>(a, p.slices_gu, p.slices_dn, p.slots, s); break;
+    case 1 * 16 + 1: launch_mt<1, 1>(a, p, s); break;
+    case 1 * 16 + 2: launch_mt<1, 2>(a, p, s); break;
+    case 1 * 16 + 4: launch_mt<1, 4>(a, p, s); break;
+    case 1 * 16 + 8: launch_mt<1, 8>(a, p, s); break;
+    case 2 * 16 + 1: launch_mt<2, 1>(a, p, s); break;
+    case 2 * 16 + 2: launch_mt<2, 2>(a, p, s); break;
+    case 2 * 16 + 4: launch_mt<2, 4>(a, p, s); break;
+    case 2 * 16 + 8: launch_mt<2, 8>(a, p, s); break;
+    case 4 * 16 + 1: launch_mt<4, 1>(a, p, s); break;
+    case 4 * 16 + 2: launch_mt<4, 2>(a, p, s); break;
+    case 4 * 16 + 4: launch_mt<4, 4>(a, p, s); break;
+    case 4 * 16 + 8: launch_mt<4, 8>(a, p, s); break;
     default: fail(QNN_E_INVALID_OP, "MoE launch plan");
   }
   hip_check(hipGetLastError(), "moe launch");

@@ -120,10 +120,6 @@ def lib():
                                                      ctypes.POINTER(_vp)]),
             "qnn_expert_set_destroy": (ctypes.c_int, [_vp, _vp]),
             "qnn_moe_experts": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int]),
-            "qnn_mlp_stack_create": (ctypes.c_int, [_vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                                    ctypes.POINTER(_vp)]),
-            "qnn_mlp_stack_run": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
-            "qnn_mlp_stack_destroy": (ctypes.c_int, [_vp, _vp]),
             "qnn_dequantize": (ctypes.c_int, [_vp, _vp, W, ctypes.c_int, ctypes.c_int]),
             "qnn_event_record": (ctypes.c_int, [_vp, ctypes.c_int]),
             "qnn_event_elapsed_ms": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int,
@@ -150,8 +146,7 @@ EXPORTED = (
     "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
     "qnn_weight_batch_capacity", "qnn_linear", "qnn_int4_linear", "qnn_swiglu_vector",
     "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
-    "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_mlp_stack_create",
-    "qnn_mlp_stack_run", "qnn_mlp_stack_destroy", "qnn_dequantize",
+    "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
     "qnn_stream", "qnn_int4_row_bytes", "qnn_quantize_int4", "qnn_gguf_quantize",
 )
@@ -405,21 +400,6 @@ class GPUContext:
 
     def MoEExperts(self, expert_set: int, dst: Tensor, src: Tensor, routes: Tensor, rows: int, topk: int) -> None:
         _raise(lib().qnn_moe_experts(self.h, expert_set, dst.handle, src.handle, routes.handle, rows, topk))
-
-    # -- persistent decode MLP stack (one launch for consecutive layers)
-    def CreateMLPStack(self, gates, ups, downs, hidden: int, inter: int) -> int:
-        L = len(gates)
-        mk = lambda ws: (_Weight * L)(*[w.desc() for w in ws])
-        h = _vp()
-        _raise(lib().qnn_mlp_stack_create(self.h, mk(gates), mk(ups), mk(downs), L, hidden, inter,
-                                          ctypes.byref(h)))
-        return h.value
-
-    def RunMLPStack(self, stack: int, dst: Tensor, src: Tensor) -> None:
-        _raise(lib().qnn_mlp_stack_run(self.h, stack, dst.handle, src.handle))
-
-    def DestroyMLPStack(self, stack: int) -> None:
-        _raise(lib().qnn_mlp_stack_destroy(self.h, stack))
 
     # -- diagnostics
     def Dequantize(self, dst: Tensor, w: MemoryBlock, rows: int, cols: int) -> None:

@@ -164,46 +164,3 @@ def test_non_finite_raises_at_download(ctx):
     with pytest.raises(hip.EInvalidOp):
         ctx.Download(t)
     ctx.Download(t)  # the flag is cleared once reported
-
-
-@pytest.mark.parametrize("layers,hidden,inter", [(3, 2560, 9728), (4, 256, 384), (2, 100, 300)])
-def test_mlp_stack_matches_cpu_path(ctx, rng, layers, hidden, inter):
-    """Persistent layer stack == the CPU path applied layer by layer (x_{l+1} = down(silu(gate x)*(up x)))."""
-    ws = [(make_int4(rng, inter, hidden), make_int4(rng, inter, hidden), make_int4(rng, hidden, inter))
-          for _ in range(layers)]
-    blocks = [tuple(hip.MemoryBlock.int4(p) for p in w) for w in ws]
-    x = rng.standard_normal(hidden).astype(np.float32)
-    st = ctx.CreateMLPStack([b[0] for b in blocks], [b[1] for b in blocks], [b[2] for b in blocks], hidden, inter)
-    src, dst = ctx.UploadRaw(x), ctx.NewTensor(hidden)
-    want = x
-    for g, u, d in ws:
-        want = oracle.cpu_mlp(g, u, d, oracle.ENC_INT4, want, hidden, inter)[0]
-    outs = []
-    for _ in range(3):  # repeated launches: flags/tickets/epoch are self-resetting
-        ctx.RunMLPStack(st, dst, src)
-        outs.append(ctx.Download(dst))
-    ctx.DestroyMLPStack(st)
-    for got in outs:
-        assert normwise_rel_err(got, want) <= TOL
-    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))  # slice order fixed: bit-identical
-
-
-def test_mlp_stack_matches_per_op_sequence(ctx, rng):
-    hidden, inter, layers = 2560, 9728, 2
-    ws = [tuple(hip.MemoryBlock.int4(make_int4(rng, n, k)) for n, k in ((inter, hidden), (inter, hidden),
-                                                                          (hidden, inter))) for _ in range(layers)]
-    x = ctx.UploadRaw(rng.standard_normal(hidden).astype(np.float32))
-    h, ya, yb = ctx.NewTensor(inter), ctx.NewTensor(hidden), ctx.NewTensor(hidden)
-    src = x
-    for l, (g, u, d) in enumerate(ws):
-        ctx.TrySwiGLUVector(h, src, g, u, hidden, inter)
-        y = (ya, yb)[l & 1]
-        ctx.Int4Linear(y, h, d, 1, inter, hidden)
-        src = y
-    per_op = ctx.Download(src)
-    st = ctx.CreateMLPStack([w[0] for w in ws], [w[1] for w in ws], [w[2] for w in ws], hidden, inter)
-    out = ctx.NewTensor(hidden)
-    ctx.RunMLPStack(st, out, x)
-    got = ctx.Download(out)
-    ctx.DestroyMLPStack(st)
-    assert normwise_rel_err(got, per_op) <= 5e-4  # fp32 stack vs fixed-point activations per op
