@@ -164,3 +164,34 @@ def test_non_finite_raises_at_download(ctx):
     with pytest.raises(hip.EInvalidOp):
         ctx.Download(t)
     ctx.Download(t)  # the flag is cleared once reported
+
+
+@pytest.mark.parametrize("lanes,tpw", [(2, 1), (4, 2), (16, 4), (8, 2)])
+def test_lane_layouts_and_tile_groupings(ctx, rng, monkeypatch, lanes, tpw):
+    """Rows spread over L lanes (QNN_I4_LANES, read when a weight is uploaded) and T tiles per
+    workgroup (QNN_I4_TPW) compute the same projections."""
+    monkeypatch.setenv("QNN_I4_LANES", str(lanes))
+    monkeypatch.setenv("QNN_I4_TPW", str(tpw))
+    for n, k in [(2560, 9728), (1000, 2560), (100, 40)]:
+        p = make_int4(rng, n, k)
+        w = hip.MemoryBlock.int4(p)
+        x = rng.standard_normal(k).astype(np.float32)
+        src, dst, deq = ctx.UploadRaw(x), ctx.NewTensor(n), ctx.NewTensor(n * k)
+        ctx.Int4Linear(dst, src, w, 1, k, n)
+        assert normwise_rel_err(ctx.Download(dst), oracle.cpu_linear(p, oracle.ENC_INT4, x, k, n)) <= TOL
+        ctx.Dequantize(deq, w, n, k)
+        assert np.array_equal(ctx.Download(deq).view(np.uint32), oracle.int4_dequant(p, k).reshape(-1).view(np.uint32))
+    pg, pu = make_int4(rng, 768, 2048), make_int4(rng, 768, 2048)
+    x = rng.standard_normal(2048).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(768)
+    assert ctx.TrySwiGLUVector(dst, src, hip.MemoryBlock.int4(pg), hip.MemoryBlock.int4(pu), 2048, 768)
+    g = oracle.cpu_linear(pg, oracle.ENC_INT4, x, 2048, 768)
+    u = oracle.cpu_linear(pu, oracle.ENC_INT4, x, 2048, 768)
+    want = np.array([oracle.silu(float(a)) for a in g], np.float32) * u
+    assert normwise_rel_err(ctx.Download(dst), want) <= TOL
+    x8 = rng.standard_normal((8, 2048)).astype(np.float32)
+    src8, dst8 = ctx.UploadRaw(x8), ctx.NewTensor(8 * 768)
+    ctx.Int4Linear(dst8, src8, hip.MemoryBlock.int4(pg), 8, 2048, 768)
+    got8 = ctx.Download(dst8).reshape(8, 768)
+    for r in range(8):
+        assert normwise_rel_err(got8[r], oracle.cpu_linear(pg, oracle.ENC_INT4, x8[r], 2048, 768)) <= TOL, r
