@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   float4 xr[MT][dev::x_iters<GSW>()];
   dev::load_x<MT, GSW>(
       xr, dev::rsrc(a.x, size_t(a.m) * a.x_stride * 4), [&](int m) { return uint32_t(m) * uint32_t(a.x_stride) * 4u; },
-      a.m, ws0 * L * 32, tid);
+      a.m, ws0 * L * 32, sgroups * 32, tid);
   const int tile = unit * T + wave / P;
   const bool active = tile < a.tiles;
   const int t = active ? tile : 0;
@@ -181,7 +181,7 @@ void launch_one(const I4Launch &a, const I4Plan &p, hipStream_t st) {
 // Steps-per-wave templates by token count (register budget).
 constexpr int kGsw1[] = {1, 2, 4, 8};
 constexpr int kGswN[] = {1, 2, 4};
-constexpr int kGswBig[] = {1, 2};
+constexpr int kGswBig[] = {1, 2, 4};
 
 template <int MT>
 void launch_mt(const I4Launch &a, const I4Plan &p, hipStream_t st) {
@@ -190,7 +190,7 @@ void launch_mt(const I4Launch &a, const I4Plan &p, hipStream_t st) {
     case 2: launch_one<MT, 2>(a, p, st); return;
     default: break;
   }
-  if constexpr (MT <= 4) {
+  if constexpr (MT <= 8) {
     if (p.gsw == 4) {
       launch_one<MT, 4>(a, p, st);
       return;
@@ -242,7 +242,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   const int P = 4 / p.tiles_per_wg;
   // Steps per wave: bounded by the template set (registers) and by the LDS of
   // the workgroup's activation slice (at most 48 KiB).
-  const int set_max = p.mt == 1 ? 8 : (p.mt <= 4 ? 4 : 2);
+  const int set_max = p.mt == 1 ? 8 : (p.mt <= 8 ? 4 : 2);
   const int lds_max = int((48 << 10) / (size_t(p.mt) * P * l.lanes * (dev::kXWords * 4 + 8)));
   const int cap = std::max(1, std::min(set_max, lds_max));
   // Steps per wave: the largest that splits the K-range into equal workgroup
@@ -252,7 +252,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   const int units = (tiles + p.tiles_per_wg - 1) / p.tiles_per_wg;
   auto waves = [&](int sps) { return size_t(units) * 4 * ((l.steps + P * sps - 1) / (P * sps)); };
   const int *set0 = p.mt == 1 ? kGsw1 : (p.mt <= 4 ? kGswN : kGswBig);
-  const int nset0 = p.mt == 1 ? int(sizeof kGsw1 / sizeof(int)) : (p.mt <= 4 ? 3 : 2);
+  const int nset0 = p.mt == 1 ? int(sizeof kGsw1 / sizeof(int)) : 3;
   int sps = 0;
   for (int i = nset0 - 1; i >= 0 && !sps; --i)
     if (set0[i] <= cap && l.steps % (P * set0[i]) == 0 && waves(set0[i]) >= size_t(target)) sps = set0[i];
@@ -262,7 +262,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   const int forced = env_int("QNN_I4_SPS", 0);
   if (forced > 0) sps = std::min(forced, cap);
   const int *set = p.mt == 1 ? kGsw1 : (p.mt <= 4 ? kGswN : kGswBig);
-  const int nset = p.mt == 1 ? int(sizeof kGsw1 / sizeof(int)) : (p.mt <= 4 ? 3 : 2);
+  const int nset = p.mt == 1 ? int(sizeof kGsw1 / sizeof(int)) : 3;
   sps = std::min(sps, pick_template(sps, set, nset));
   p.gsw = pick_template(sps, set, nset);
   p.steps_per_slice = sps;

@@ -100,16 +100,22 @@ __device__ __forceinline__ float ld32f(Rsrc r, uint32_t voff, uint32_t soff) {
 // hold a multiple of 4 floats, 16-byte aligned).  Nothing is masked here, so
 // no load waits for another; stage_x zeroes the pieces outside the slice, the
 // row or the token count.
+// `ne` (uniform) bounds the passes to those the slice needs.
 template <int MT, int GSW, class OffF>
 __device__ __forceinline__ void load_x(float4 (&xr)[MT][x_iters<GSW>()], Rsrc src, OffF rowoff, int mt, int e0,
-                                       int tid) {
+                                       int ne, int tid) {
+  const int passes = (ne + 1023) >> 10;
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     const uint32_t base = rowoff(m < mt ? m : 0) + uint32_t(e0 + tid * 4) * 4u;
 #pragma unroll
     for (int it = 0; it < x_iters<GSW>(); ++it) {
-      const uint4 v = ld128(src, base, uint32_t(it) * 4096u);
-      xr[m][it] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (it < passes) {
+        const uint4 v = ld128(src, base, uint32_t(it) * 4096u);
+        f = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+      }
+      xr[m][it] = f;
     }
   }
 }
@@ -144,6 +150,7 @@ __device__ __forceinline__ void stage_x(const XPlanes &xs, const float4 (&xr)[MT
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
     for (int it = 0; it < x_iters<GSW>(); ++it) {
+      if (it * 1024 >= ne) break;  // uniform: passes past the slice
       const int e = (it * 256 + tid) * 4;  // first element of this thread, within the slice
       const bool ok = m < mt && e < ne && e0 + e < k;
       const float4 v = ok ? xr[m][it] : make_float4(0.f, 0.f, 0.f, 0.f);

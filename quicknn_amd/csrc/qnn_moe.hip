@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
     return DOWN ? uint32_t(R) * uint32_t(a.inter) * 4u : uint32_t(R / a.topk) * uint32_t(a.hidden) * 4u;
   };
   float4 xr[MT][dev::x_iters<GSW>()];
-  dev::load_x<MT, GSW>(xr, xsrc, xoff, min(c, MT), ws0 * L * 32, tid);
+  dev::load_x<MT, GSW>(xr, xsrc, xoff, min(c, MT), ws0 * L * 32, sgroups * 32, tid);
   uint4 w[GSW];
   float sc[GSW];
   dev::load_w<GSW>(w, sc, dev::rsrc(wbase, l.nib_bytes()), dev::rsrc(wbase + l.nib_bytes(), l.scale_bytes()), l, b, s0,
@@ -184,7 +184,8 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
 
   for (int m0 = 0; m0 < c; m0 += MT) {
     if (m0 > 0) {
-      dev::load_x<MT, GSW>(xr, xsrc, [&](int m) { return xoff(m0 + m); }, min(c - m0, MT), ws0 * L * 32, tid);
+      dev::load_x<MT, GSW>(xr, xsrc, [&](int m) { return xoff(m0 + m); }, min(c - m0, MT), ws0 * L * 32, sgroups * 32,
+                           tid);
       __syncthreads();  // the previous chunk's LDS reads are done
     }
     dev::stage_x<MT, GSW>(xs, xr, min(c - m0, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
