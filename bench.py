@@ -88,7 +88,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path's multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
+              "(sharding the path over several GPUs is a design note, not built)", file=sys.stderr)
         return 2
 
     from quicknn_amd import hip

@@ -7,7 +7,7 @@
  * the LLM engine in src/models calls for packed matvec, fused gate/up + SwiGLU
  * and routed-expert execution.  Every entry point is cdecl, takes plain
  * pointers and sizes, and returns a status code; the Object Pascal unit re-raises
- * the matching exception class (see INTEGRATION.md for the binding).
+ * the matching exception class.
  *
  * Conventions (as in the reference):
  *  - One context exists at a time; it is bound to the thread that created it
@@ -135,7 +135,7 @@ int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /
  * ------------------------------------------------------------------------- */
 /* Linear (Context.API.inc:117-122, Implementation.inc:813-899).  GGUF weights:
  * rows == 1 runs the packed matvec (op 65), rows > 1 the multi-row product
- * (gemm.comp); Q8_0 with rows > 1 runs the int8-MFMA GEMM.  bias (optional,
+ * (gemm.comp); Q8_0 with rows >= 4 runs the fp16-MFMA GEMM.  bias (optional,
  * F32 or BF16 [out]) is added afterwards.  scales must be NULL (INT8 ConvRot
  * weights are outside this backend). */
 int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,
