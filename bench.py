@@ -1,14 +1,15 @@
 #!/usr/bin/env python3
-"""Benchmark: Qwen3-4B-shaped native-INT4 decode-layer MLP on one MI355X.
+"""Benchmark: QuickNN's quantized-weight decode path on one MI355X.
 
-Workload: hidden 2560, intermediate 9728; per layer
-the fused gate+up projection with SwiGLU (TrySwiGLUVector, one kernel) then the
-down projection (Int4Linear), 36 layers with independent seeds, batch 1.  A
-"step" is one token through the 36 layers, the output of layer l feeding layer
-l+1.  Weights are bf16 N(0, 0.02) (truncated from fp32 as SingleToBF16 does)
-packed with QuickNN's INT4 algorithm; activations fp32 N(0,1) RMS-normalised
-with unit gamma.  The 36-layer weight set (1.68 GB) exceeds the 256 MB MALL,
-so every step streams its weights from HBM.
+Default (`--config 2`, the headline): Qwen3-4B-shaped native-INT4 decode-layer
+MLP.  hidden 2560, intermediate 9728; per layer the fused gate+up projection
+with SwiGLU (TrySwiGLUVector, one kernel) then the down projection
+(Int4Linear); 36 layers with independent seeds, batch 1.  A "step" is one token
+through the 36 layers, the output of layer l feeding layer l+1.  Weights are
+bf16 N(0, 0.02) (truncated from fp32 as SingleToBF16 does) packed with
+QuickNN's INT4 algorithm; activations fp32 N(0,1) RMS-normalised with unit
+gamma.  The 36-layer weight set (1.68 GB) exceeds the 256 MB MALL, so every
+step streams its weights from HBM.
 
 value = algorithmic bytes per step (packed weights + activations read once +
 outputs written once) / measured time per step, in GB/s.
@@ -18,6 +19,17 @@ fused gate/up SwiGLU matvec: algorithmic bytes per launch over its average
 launch time, from HIP events on the context stream around 36-launch runs of
 it); batch-8 figures; and the reference's CPU SIMD path (an AVX2 restatement in
 the CPU oracle) timed on this host on the same packed weights.
+
+The other workloads of the benchmark definition are measured with
+`--config 1|3|4|5` (one JSON line each, same fields):
+  1  one INT4 matvec 6144x2048 (Qwen3-1.7B gate shape), batch 1;
+  3  Gemma-2-9B-shaped GGUF K-quant decode layer (Q4_K q/o, Q3_K k/v, Q2_K
+     gate/up + GEGLU, Q6_K down) and the Q6_K output head;
+  4  Qwen3-30B-A3B-shaped MoE expert layer (128 INT4 experts, top-8) at batch
+     1 and 16, routed on the device;
+  5  Q8_0 prefill GEMM 512x3072x12288.
+Each rotates over enough distinct weight copies (> 256 MB) that the weights
+come from HBM, not from the MALL.
 """
 from __future__ import annotations
 
@@ -34,6 +46,13 @@ sys.path.insert(0, ROOT)
 
 HIDDEN, INTER, LAYERS = 2560, 9728, 36
 HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+METRIC = "quant matvec HBM GB/s (% of 8 TB/s) + decode us/layer, Qwen3-4B-shape INT4"
+
+
+def bf16_trunc(w: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits by truncation (SingleToBF16)."""
+    return (w.view(np.uint32) >> 16).astype(np.uint16)
 
 
 def make_layer(seed: int, hip):
@@ -42,8 +61,7 @@ def make_layer(seed: int, hip):
     def mat(n, k):
         w = rng.standard_normal((n, k), dtype=np.float32)
         w *= np.float32(0.02)
-        b = (w.view(np.uint32) >> 16).astype(np.uint16)  # SingleToBF16 truncation
-        return hip.quantize_int4(b)
+        return hip.quantize_int4(bf16_trunc(w))
 
     return mat(INTER, HIDDEN), mat(INTER, HIDDEN), mat(HIDDEN, INTER)
 
@@ -55,7 +73,41 @@ def layer_bytes(m: int, hip) -> tuple[int, int]:
     return w, act
 
 
-def cpu_baseline(packed, x0: np.ndarray, budget_s: float, wbytes: int, abytes: int) -> dict:
+def timed_ms(ctx, fn, reps: int) -> float:
+    """Average ms of fn() over `reps` back-to-back runs, HIP events on the context stream."""
+    ctx.EventRecord(2)
+    for _ in range(reps):
+        fn()
+    ctx.EventRecord(3)
+    ctx.Flush()
+    return ctx.EventElapsedMs(2, 3) / reps
+
+
+def gguf_matrix(hip, enc: int, n: int, k: int, seed: int, max_rows: int = 16384) -> np.ndarray:
+    """N(0, 0.02) fp32 [n, k] encoded to GGML blocks; rows beyond max_rows repeat the first max_rows
+    (same statistics, bounded generation time)."""
+    rng = np.random.default_rng(seed)
+    base = min(n, max_rows)
+    w = rng.standard_normal(base * k, dtype=np.float32)
+    w *= np.float32(0.02)
+    b = hip.gguf_quantize(enc, w).reshape(base, -1)
+    if base < n:
+        b = np.concatenate([b] * ((n + base - 1) // base))[:n]
+    return np.ascontiguousarray(b).reshape(-1)
+
+
+def base_line(args, metric, value, unit, ms_step, dtype, data, config, **extra) -> dict:
+    line = {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": data, "config": config}
+    line.update(extra)
+    return line
+
+
+# ---------------------------------------------------------------------------
+# cfg2 (default): Qwen3-4B INT4 MLP, 36 layers
+# ---------------------------------------------------------------------------
+def cpu_baseline_mlp(packed, x0: np.ndarray, budget_s: float, wbytes: int, abytes: int) -> dict:
     """The reference's CPU direct-matvec path (TCPUProjection.Linear with the
     AVX2 Int4VectorDot, QwenHybrid.CPU.pas:238-248 composition), restated in
     the oracle, at the reference default of min(8, nproc) worker threads."""
@@ -78,21 +130,7 @@ def cpu_baseline(packed, x0: np.ndarray, budget_s: float, wbytes: int, abytes: i
                       f"{us_layer:.0f} us/layer; nproc={os.cpu_count()}"}
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(sharding the path over several GPUs is a design note, not built)", file=sys.stderr)
-        return 2
-
-    from quicknn_amd import hip
-
+def run_cfg2(args, hip) -> dict:
     t0 = time.perf_counter()
     packed = [make_layer(1000 + l, hip) for l in range(LAYERS)]
     gen_s = time.perf_counter() - t0
@@ -190,41 +228,326 @@ def main() -> int:
             traffic = None
     ctx.close()
 
+    cpu = None if args.no_cpu else cpu_baseline_mlp(packed, x1, args.cpu_seconds, wbytes, abytes1)
+    return base_line(
+        args, METRIC, value, "GB/s", ms_step, "int4-w/fp32-acc",
+        "synthetic (seeded N(0,0.02) bf16 weights packed to QuickNN INT4; N(0,1) RMS-normalised activations)",
+        {"workload": "configs[1]: Qwen3-4B MLP, hidden 2560, intermediate 9728, fused gate+up SwiGLU "
+                     "then down, native INT4, 36 layers, batch 1",
+         "global_batch": 1, "layers": LAYERS, "hidden": HIDDEN, "intermediate": INTER},
+        pct_of_hbm_peak=round(100 * value / HBM_PEAK_GBS, 2),
+        us_per_layer=round(us_layer, 3),
+        tokens_per_s=round(1000.0 / ms_step, 1),
+        batch8={"us_per_layer": round(ms8 * 1000 / LAYERS, 3),
+                "GBps": round((wbytes + abytes8) * LAYERS / (ms8 * 1e-3) / 1e9, 1),
+                "tokens_per_s": round(8000.0 / ms8, 1)},
+        roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                  "kernel": "k_int4_matvec (I4_SWIGLU: fused gate+up SwiGLU, 9728x2560 pair)",
+                  "kernel_us": round(gu_us, 3), "bytes_per_launch": gu_bytes,
+                  "timing": f"HIP events around {reps}x{LAYERS} back-to-back launches on the context stream"},
+        cpu_baseline=cpu,
+        setup_s=round(gen_s, 1))
+
+
+# ---------------------------------------------------------------------------
+# cfg1: one INT4 matvec 6144 x 2048
+# ---------------------------------------------------------------------------
+def run_cfg1(args, hip) -> dict:
+    N, K, R = 6144, 2048, 64  # 64 distinct copies: 503 MB, beyond the MALL
+    rng = np.random.default_rng(11)
+    w = rng.standard_normal((N, K), dtype=np.float32)
+    w *= np.float32(0.02)
+    packed = hip.quantize_int4(bf16_trunc(w))
+    x = rng.standard_normal(K).astype(np.float32)
+    ctx = hip.GPUContext(0)
+    blocks = [hip.MemoryBlock.int4(packed) for _ in range(R)]  # distinct identities, same bytes
+    ctx.PreloadWeights(blocks)
+    xt, yt = ctx.UploadRaw(x), ctx.NewTensor(N)
+
+    def step():
+        for b in blocks:
+            ctx.Int4Linear(yt, xt, b, 1, K, N)
+
+    for _ in range(args.warmup):
+        step()
+    ms_step = timed_ms(ctx, step, args.steps)
+    ctx.close()
+    nbytes = packed.size + 4 * (K + N)
+    us = ms_step * 1000 / R
+    achieved = nbytes / (us * 1e-6) / 1e9
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(packed, x1, args.cpu_seconds, wbytes, abytes1)
+        import oracle
 
-    line = {
-        "metric": "quant matvec HBM GB/s (% of 8 TB/s) + decode us/layer, Qwen3-4B-shape INT4",
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int4-w/fp32-acc",
-        "data": "synthetic (seeded N(0,0.02) bf16 weights packed to QuickNN INT4; N(0,1) RMS-normalised activations)",
-        "config": {"workload": "configs[1]: Qwen3-4B MLP, hidden 2560, intermediate 9728, fused gate+up SwiGLU "
-                               "then down, native INT4, 36 layers, batch 1",
-                   "global_batch": 1, "layers": LAYERS, "hidden": HIDDEN, "intermediate": INTER},
-        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "us_per_layer": round(us_layer, 3),
-        "tokens_per_s": round(1000.0 / ms_step, 1),
-        "batch8": {"us_per_layer": round(ms8 * 1000 / LAYERS, 3),
-                   "GBps": round((wbytes + abytes8) * LAYERS / (ms8 * 1e-3) / 1e9, 1),
-                   "tokens_per_s": round(8000.0 / ms8, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_int4_matvec (I4_SWIGLU: fused gate+up SwiGLU, 9728x2560 pair)",
-                     "kernel_us": round(gu_us, 3), "bytes_per_launch": gu_bytes,
-                     "timing": f"HIP events around {reps}x{LAYERS} back-to-back launches on the context stream"},
-        "cpu_baseline": cpu,
-        "setup_s": round(gen_s, 1),
+        pool = oracle.Pool(0)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or n < 3:
+            oracle.cpu_linear(packed, oracle.ENC_INT4, x, K, N, pool)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu = {"value": round(nbytes * n / el / 1e9, 2), "unit": "GB/s", "cores": pool.threads, "kind": "port",
+               "sample": f"{n} matvecs ({el:.1f} s), {el / n * 1e6:.0f} us each; nproc={os.cpu_count()}"}
+    return base_line(
+        args, "INT4 matvec HBM GB/s, 6144x2048", achieved, "GB/s", ms_step, "int4-w/fp32-acc",
+        f"synthetic (seeded N(0,0.02) bf16 packed to QuickNN INT4; x N(0,1)); {R} distinct weight copies rotated",
+        {"workload": "configs[0]: native INT4 matvec, N 6144, K 2048, batch 1", "global_batch": 1},
+        us_per_matvec=round(us, 3), pct_of_hbm_peak=round(100 * achieved / HBM_PEAK_GBS, 2),
+        roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                  "kernel": "k_int4_matvec (I4_STORE)", "kernel_us": round(us, 3), "bytes_per_launch": nbytes,
+                  "timing": f"HIP events around {args.steps}x{R} back-to-back launches"},
+        cpu_baseline=cpu)
+
+
+# ---------------------------------------------------------------------------
+# cfg3: Gemma-2-9B GGUF decode layer + Q6_K head
+# ---------------------------------------------------------------------------
+def run_cfg3(args, hip) -> dict:
+    H, I, Q, KV, V, L = 3584, 14336, 4096, 2048, 256000, 8
+    t0 = time.perf_counter()
+    shapes = {"q": (hip.WE_Q4_K, Q, H), "k": (hip.WE_Q3_K, KV, H), "v": (hip.WE_Q3_K, KV, H),
+              "o": (hip.WE_Q4_K, H, Q), "gate": (hip.WE_Q2_K, I, H), "up": (hip.WE_Q2_K, I, H),
+              "down": (hip.WE_Q6_K, H, I)}
+    data = {nm: gguf_matrix(hip, e, n, k, 300 + i) for i, (nm, (e, n, k)) in enumerate(shapes.items())}
+    head = gguf_matrix(hip, hip.WE_Q6_K, V, H, 399)
+    gen_s = time.perf_counter() - t0
+    layers = [{nm: hip.MemoryBlock.gguf(data[nm], n, k, e) for nm, (e, n, k) in shapes.items()} for _ in range(L)]
+    head_b = hip.MemoryBlock.gguf(head, V, H, hip.WE_Q6_K)
+    wbytes = {nm: d.size for nm, d in data.items()}
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal(H).astype(np.float32)
+    ctx = hip.GPUContext(0)
+    for lay in layers:
+        ctx.PreloadWeights(list(lay.values()))
+    ctx.PreloadWeights([head_b])
+    xt = ctx.UploadRaw(x)
+    q, k_, v_, o = ctx.NewTensor(Q), ctx.NewTensor(KV), ctx.NewTensor(KV), ctx.NewTensor(H)
+    g, u, hh, y, logits = ctx.NewTensor(I), ctx.NewTensor(I), ctx.NewTensor(I), ctx.NewTensor(H), ctx.NewTensor(V)
+    # Gemma2's layer (Gemma2.pas:142-198): q, k, v, o, gate, up, GEGLU, down.
+    # Attention itself is outside the path; o reads q's output.
+    ops = {
+        "q": lambda lay: ctx.Linear(q, xt, lay["q"], None, None, 1, H, Q),
+        "k": lambda lay: ctx.Linear(k_, xt, lay["k"], None, None, 1, H, KV),
+        "v": lambda lay: ctx.Linear(v_, xt, lay["v"], None, None, 1, H, KV),
+        "o": lambda lay: ctx.Linear(o, q, lay["o"], None, None, 1, Q, H),
+        "gate": lambda lay: ctx.Linear(g, xt, lay["gate"], None, None, 1, H, I),
+        "up": lambda lay: ctx.Linear(u, xt, lay["up"], None, None, 1, H, I),
+        "geglu": lambda lay: ctx.Kernel(hip.GO_GEGLU, I, hh, g, u, None, [I, 0]),
+        "down": lambda lay: ctx.Linear(y, hh, lay["down"], None, None, 1, I, H),
     }
-    print(json.dumps(line))
+
+    def step():
+        for lay in layers:
+            for fn in ops.values():
+                fn(lay)
+
+    for _ in range(args.warmup):
+        step()
+    ms_step = timed_ms(ctx, step, args.steps)
+    us_layer = ms_step * 1000 / L
+    act = 4 * (H * 6 + Q * 2 + KV * 2 + I * 5 + H)  # activation reads and writes of the 8 ops
+    layer_b = sum(wbytes.values()) + act
+    per_op = {}
+    for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+        t = timed_ms(ctx, lambda: [ops[nm](lay) for lay in layers], max(3, args.steps // 5)) * 1000 / L
+        per_op[nm] = {"us": round(t, 2), "GBps": round(wbytes[nm] / (t * 1e-6) / 1e9, 1)}
+    head_us = timed_ms(ctx, lambda: ctx.Linear(logits, xt, head_b, None, None, 1, H, V), 20) * 1000
+    ctx.close()
+    dom = max(per_op, key=lambda nm: per_op[nm]["us"])
+    value = layer_b / (us_layer * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        pool = oracle.Pool(0)
+        encs = {hip.WE_Q4_K: oracle.ENC_Q4_K, hip.WE_Q3_K: oracle.ENC_Q3_K, hip.WE_Q2_K: oracle.ENC_Q2_K,
+                hip.WE_Q6_K: oracle.ENC_Q6_K}
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or n < 1:
+            outs = {}
+            for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+                e, nn, kk = shapes[nm]
+                src = x
+                if nm == "o":
+                    src = outs["q"]
+                elif nm == "down":
+                    gg, uu = outs["gate"], outs["up"]
+                    c = np.float32(0.7978845608)
+                    src = (0.5 * gg * (1 + np.tanh(c * (gg + np.float32(0.044715) * gg ** 3))) * uu).astype(np.float32)
+                outs[nm] = oracle.cpu_linear(data[nm], encs[e], src, kk, nn, pool)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu = {"value": round(layer_b * n / el / 1e9, 2), "unit": "GB/s", "cores": pool.threads, "kind": "port",
+               "sample": f"{n} Gemma layers ({el:.1f} s, {el / n * 1e6:.0f} us/layer): TCPUProjection.Linear "
+                         f"with the direct PackedDot paths (Q2_K block decode + VectorDot); nproc={os.cpu_count()}"}
+    return base_line(
+        args, "GGUF K-quant decode HBM GB/s + us/layer, Gemma-2-9B shape", value, "GB/s", ms_step, "gguf-w/fp32-acc",
+        "synthetic (N(0,0.02) fp32 encoded to GGML blocks; rows past 16384 repeat; x N(0,1)); "
+        f"{L} layer copies rotated ({L * sum(wbytes.values()) / 1e6:.0f} MB)",
+        {"workload": "configs[2]: Gemma-2-9B layer, hidden 3584, q/o Q4_K, k/v Q3_K, gate/up Q2_K + GEGLU, "
+                     "down Q6_K, batch 1; head Q6_K 256000x3584", "global_batch": 1},
+        us_per_layer=round(us_layer, 2), pct_of_hbm_peak=round(100 * value / HBM_PEAK_GBS, 2), per_op=per_op,
+        head={"us": round(head_us, 2), "GBps": round(head.size / (head_us * 1e-6) / 1e9, 1)},
+        roofline={"bound": "hbm", "achieved": per_op[dom]["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(per_op[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                  "kernel": f"k_gguf_matvec ({dom}: {shapes[dom][1]}x{shapes[dom][2]})",
+                  "kernel_us": per_op[dom]["us"], "bytes_per_launch": wbytes[dom],
+                  "timing": f"HIP events around {L}-launch runs of the op"},
+        cpu_baseline=cpu, setup_s=round(gen_s, 1))
+
+
+# ---------------------------------------------------------------------------
+# cfg4: Qwen3-30B-A3B MoE expert layer
+# ---------------------------------------------------------------------------
+def run_cfg4(args, hip) -> dict:
+    E, H, I, K, L = 128, 2048, 768, 8, 4
+    t0 = time.perf_counter()
+    rng = np.random.default_rng(17)
+
+    def mat(n, k):
+        w = rng.standard_normal((n, k), dtype=np.float32)
+        w *= np.float32(0.02)
+        return hip.quantize_int4(bf16_trunc(w))
+
+    gates = [mat(I, H) for _ in range(E)]
+    ups = [mat(I, H) for _ in range(E)]
+    downs = [mat(H, I) for _ in range(E)]
+    gen_s = time.perf_counter() - t0
+    per_expert = 2 * I * hip.int4_row_bytes(H) + H * hip.int4_row_bytes(I)
+    ctx = hip.GPUContext(0)
+    sets = [ctx.CreateExpertSet([hip.MemoryBlock.int4(w) for w in gates], [hip.MemoryBlock.int4(w) for w in ups],
+                                [hip.MemoryBlock.int4(w) for w in downs], H, I) for _ in range(L)]
+    res = {}
+    for rows in (1, 16):
+        x = rng.standard_normal((rows, H)).astype(np.float32)
+        xt = ctx.UploadRaw(x)
+        routes, distinct, first_logits = [], 0, None
+        for l in range(L):  # each layer copy gets its own router logits
+            lg = rng.standard_normal((rows, E)).astype(np.float32)
+            first_logits = lg if first_logits is None else first_logits
+            lt = ctx.UploadRaw(lg)
+            rt = ctx.NewTensor(2 * rows * K)
+            ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, rt, lt, None, None, [rows, E, K, 1])
+            routes.append(rt)
+            distinct += len(set(ctx.Download(rt)[:rows * K].view(np.uint32).tolist()))
+        out = ctx.NewTensor(rows * H)
+
+        def step():
+            for l in range(L):
+                ctx.MoEExperts(sets[l], out, xt, routes[l], rows, K)
+
+        for _ in range(args.warmup):
+            step()
+        ms = timed_ms(ctx, step, args.steps)
+        us_layer = ms * 1000 / L
+        nbytes = distinct / L * per_expert + 4 * rows * (2 * H + 2 * K)
+        res[rows] = {"ms_step": ms, "us_per_layer": round(us_layer, 2), "distinct_experts": round(distinct / L, 1),
+                     "GBps": round(nbytes / (us_layer * 1e-6) / 1e9, 1), "bytes": nbytes, "x": x,
+                     "logits": first_logits}
+    ctx.close()
+    r1 = res[1]
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        pool = oracle.Pool(0)
+        ids, probs = oracle.moe_route(r1["logits"], K, True)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or n < 3:
+            oracle.cpu_moe(gates, ups, downs, r1["x"], ids, probs, H, I, pool)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu = {"value": round(r1["bytes"] * n / el / 1e9, 2), "unit": "GB/s", "cores": pool.threads, "kind": "port",
+               "sample": f"{n} composed batch-1 MoE layers ({el:.1f} s, {el / n * 1e6:.0f} us each): 8 experts x "
+                         f"(gate, up, down) TCPUProjection.Linear + weighted sum; nproc={os.cpu_count()}"}
+    return base_line(
+        args, "MoE routed-expert HBM GB/s + us/layer, Qwen3-30B-A3B shape INT4", r1["GBps"], "GB/s", r1["ms_step"],
+        "int4-w/fp32-acc",
+        "synthetic (N(0,0.02) bf16 experts packed to INT4; router logits N(0,1), top-8 renormalised); "
+        f"{L} layer copies with their own routes rotated",
+        {"workload": "configs[3]: 128 experts, hidden 2048, expert inter 768, top-8, batch 1 (batch 16 below)",
+         "global_batch": 1},
+        us_per_layer=r1["us_per_layer"], distinct_experts=r1["distinct_experts"],
+        pct_of_hbm_peak=round(100 * r1["GBps"] / HBM_PEAK_GBS, 2),
+        batch16={k: v for k, v in res[16].items() if k in ("us_per_layer", "distinct_experts", "GBps")},
+        roofline={"bound": "hbm", "achieved": r1["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(r1["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                  "kernel": "k_moe gate/up + down (the two launches of one qnn_moe_experts call)",
+                  "kernel_us": r1["us_per_layer"], "bytes_per_launch": round(r1["bytes"]),
+                  "timing": f"HIP events around {args.steps}x{L} calls"},
+        cpu_baseline=cpu, setup_s=round(gen_s, 1))
+
+
+# ---------------------------------------------------------------------------
+# cfg5: Q8_0 prefill GEMM
+# ---------------------------------------------------------------------------
+def run_cfg5(args, hip) -> dict:
+    M, K, N, R = 512, 3072, 12288, 8  # 8 weight copies: 321 MB
+    wq = gguf_matrix(hip, hip.WE_Q8_0, N, K, 500)
+    rng = np.random.default_rng(19)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    ctx = hip.GPUContext(0)
+    ws = [hip.MemoryBlock.gguf(wq, N, K, hip.WE_Q8_0) for _ in range(R)]
+    ctx.PreloadWeights(ws)
+    at, ct = ctx.UploadRaw(a), ctx.NewTensor(M * N)
+
+    def step():
+        for w in ws:
+            ctx.Linear(ct, at, w, None, None, M, K, N)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    ms_step = timed_ms(ctx, step, args.steps)
+    ctx.close()
+    us = ms_step * 1000 / R
+    tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    nbytes = wq.size + 4 * M * K + 4 * M * N
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        pool = oracle.Pool(0)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or n < 4:
+            oracle.cpu_linear(wq, oracle.ENC_Q8_0, a[n % M], K, N, pool)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu = {"value": round(2.0 * N * K * n / el / 1e12, 4), "unit": "TFLOP/s", "cores": pool.threads,
+               "kind": "port",
+               "sample": f"{n} of the 512 rows as SIMD per-row PackedDotQ8 matvecs ({el:.1f} s); "
+                         f"nproc={os.cpu_count()}"}
+    return base_line(
+        args, "Q8_0 prefill GEMM TFLOP/s, 512x3072x12288", tflops, "TFLOP/s", ms_step, "fp16-mfma/fp32-acc",
+        f"synthetic (N(0,0.02) fp32 encoded to Q8_0; A N(0,1)); {R} weight copies rotated",
+        {"workload": "configs[4]: Q8_0 GEMM M 512, K 3072, N 12288", "global_batch": M},
+        us_per_gemm=round(us, 2), hbm_GBps=round(nbytes / (us * 1e-6) / 1e9, 1),
+        roofline={"bound": "mfma", "achieved": round(tflops, 1), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                  "kernel": "k_q8_gemm (+ activation preparation)", "kernel_us": round(us, 2),
+                  "flops_per_launch": 2 * M * N * K,
+                  "timing": f"HIP events around {args.steps}x{R} back-to-back calls"},
+        cpu_baseline=cpu)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(sharding the path over several GPUs is a design note, not built)", file=sys.stderr)
+        return 2
+
+    from quicknn_amd import hip
+
+    run = {1: run_cfg1, 2: run_cfg2, 3: run_cfg3, 4: run_cfg4, 5: run_cfg5}[args.config]
+    print(json.dumps(run(args, hip)))
     return 0
 
 

@@ -4,15 +4,17 @@
 // the repack and dequant kernels.  Format, layout and the fixed-point inner
 // product: qnn_int4_dev.h.
 //
-// A workgroup is 4 waves on 4 consecutive tiles (64-lane blocks; in SwiGLU
-// mode half a block of gate rows in lanes 0-31 and the same up rows in lanes
-// 32-63) and one K-slice; the activation slice is staged once in LDS for all
-// four.  Each lane accumulates its groups, the L lanes of a row are reduced
-// across the wave, and when the K-range is split over several workgroups the
-// last slice of a tile to finish (an atomic ticket per tile) sums the slices
-// in slice order, so results do not depend on timing.  At batch 1 the planner
-// keeps whole rows in one wave wherever the matrix has enough rows, so no
-// split is needed.
+// A workgroup is 4 waves: T consecutive tiles (64-lane blocks; in SwiGLU mode
+// half a block of gate rows in lanes 0-31 and the same up rows in lanes 32-63)
+// times P = 4/T parts of one K-slice, each part `steps_per_slice` steps long.
+// The workgroup's activation slice is staged once in LDS for all four waves.
+// Each lane accumulates its groups, the L lanes of a row are reduced across
+// the wave, the P parts of a tile are summed in LDS by part 0, and when the
+// K-range is split over several workgroups the last slice of a tile to finish
+// (an atomic ticket per tile) sums the slices in slice order, so results do not
+// depend on timing.  The planner (int4_plan) picks the largest power-of-two
+// steps per wave that splits the steps evenly and still gives enough waves to
+// fill the chip.
 #include "qnn_int4_dev.h"
 
 namespace qnn {

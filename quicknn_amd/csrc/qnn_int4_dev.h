@@ -1,6 +1,5 @@
 // qnn_int4_dev.h -- device building blocks of the native INT4 matvec kernels
-// (qnn_int4.hip: dense projections; qnn_moe.hip: routed experts; qnn_mlp.hip:
-// persistent layer stack).
+// (qnn_int4.hip: dense projections; qnn_moe.hip: routed experts).
 //
 // Format (src/core/QuickNN.Quantization.Int4.pas:10-94): per 32 weights an
 // fp32 scale s then 16 bytes of offset-binary nibbles n (element j in byte j/2,
@@ -25,9 +24,11 @@
 // (exact integer arithmetic inside a group; fp32 across groups; relative
 // error of the activation representation <= 2^-16 of the group's max|x|).
 //
-// Loads are issued without branches (out-of-range steps and tokens re-read a
-// valid address and are masked), so the compiler can wait for the activation
-// loads alone while the weight loads are still in flight.
+// Loads go through buffer resources (reads past the end return 0) and are
+// issued without per-lane branches (out-of-range steps and tokens re-read a
+// valid address and are masked when staged; only whole passes beyond the
+// slice are skipped, on a uniform condition), so the compiler can wait for
+// the activation loads alone while the weight loads are still in flight.
 #pragma once
 #include "qnn_internal.h"
 
