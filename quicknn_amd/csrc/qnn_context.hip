@@ -57,6 +57,14 @@ struct qnn_ctx_s {
   // upload staging
   void *staging = nullptr;
   size_t staging_bytes = 0;
+  // pinned host readback buffer (data + error word)
+  void *readback = nullptr;
+  size_t readback_bytes = 0;
+  // PreloadWeights pins until the next Flush/Download (Context.Implementation.inc:399-419);
+  // RetainWeight pins for the context's lifetime (:361-387).
+  std::vector<qnn::WeightEntry *> flush_pins;
+  std::vector<qnn::WeightEntry *> retained;
+  uint64_t retained_bytes = 0;
   hipEvent_t events[64] = {};
   bool capturing = false;
   std::vector<qnn::WeightEntry *> capture_pins;
@@ -110,6 +118,17 @@ void sync(qnn_ctx_s *ctx) {
   ctx->st.submissions++;
 }
 
+// XCD-local split-K exchange only for direct launches: kernels replayed from a
+// HIP graph are not dealt to XCDs in the probed blockIdx % 8 order, so captured
+// kernels exchange partial sums through device-coherent accesses.
+int xcd_local_launch(const qnn_ctx_s *ctx) { return ctx->xcd_local && !ctx->capturing ? 1 : 0; }
+
+// Flush releases the pins a synchronous preload took (Context.Implementation.inc:411-415).
+void release_flush_pins(qnn_ctx_s *ctx) {
+  for (auto *e : ctx->flush_pins) e->pins--;
+  ctx->flush_pins.clear();
+}
+
 // ---------------------------------------------------------------- tensors
 qnn_tensor_s *new_tensor(qnn_ctx_s *ctx, int count) {
   if (count < 1) fail(QNN_E_RANGE, "resident tensor size");
@@ -150,7 +169,11 @@ void ensure_splitk(qnn_ctx_s *ctx, size_t partial_floats, size_t counters) {
   ctx->counters = nullptr;
   hip_check(hipMalloc(&ctx->partial, std::max<size_t>(partial_floats, 1) * 4), "workspace allocation");
   hip_check(hipMalloc(&ctx->counters, std::max<size_t>(counters, 1) * 4), "workspace allocation");
-  hip_check(hipMemset(ctx->counters, 0, std::max<size_t>(counters, 1) * 4), "workspace clear");
+  // On the context stream and waited for: a plain hipMemset runs on the null
+  // stream, which a non-blocking stream does not wait for, so the next kernel
+  // could read tickets left in the recycled allocation.
+  hip_check(hipMemsetAsync(ctx->counters, 0, std::max<size_t>(counters, 1) * 4, ctx->stream), "workspace clear");
+  hip_check(hipStreamSynchronize(ctx->stream), "workspace clear");
   ctx->partial_floats = partial_floats;
   ctx->counter_count = counters;
 }
@@ -360,8 +383,12 @@ WeightEntry *acquire_raw(qnn_ctx_s *ctx, const qnn_weight *w, int64_t count) {
   e->source_bytes = bytes;
   try {
     e->dptr = alloc_weight(ctx, e->bytes);
-    hip_check(hipMemcpy(e->dptr, static_cast<const uint8_t *>(w->data) + w->offset * es, bytes, hipMemcpyHostToDevice),
+    // Ordered on the context stream (a plain hipMemcpy from pageable memory may
+    // return before its DMA lands, and the non-blocking stream would not wait).
+    hip_check(hipMemcpyAsync(e->dptr, static_cast<const uint8_t *>(w->data) + w->offset * es, bytes,
+                             hipMemcpyHostToDevice, ctx->stream),
               "vector upload");
+    sync(ctx);
   } catch (...) {
     if (e->dptr) (void)hipFree(e->dptr);
     delete e;
@@ -421,7 +448,7 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
     ensure_splitk(ctx, p.partial_floats, p.counters);
     a.partial = ctx->partial;
     a.counters = ctx->counters;
-    a.xcd_local = ctx->xcd_local ? 1 : 0;
+    a.xcd_local = xcd_local_launch(ctx);
     a.err = ctx->error_flag;
     int4_matvec_launch(a, p, ctx->stream);
   }
@@ -458,7 +485,7 @@ void run_gguf(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
   ensure_splitk(ctx, slices > 1 ? size_t(a.tiles) * slices * 64 : 0, size_t(a.tiles) * kCounterStride);
   a.partial = ctx->partial;
   a.counters = ctx->counters;
-  a.xcd_local = ctx->xcd_local ? 1 : 0;
+  a.xcd_local = xcd_local_launch(ctx);
   a.err = ctx->error_flag;
   gguf_matvec_launch(a, bw, slices, ctx->stream);
 }
@@ -499,7 +526,8 @@ int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out) {
     try {
       hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
       hip_check(hipMalloc(&ctx->error_flag, 256), "error word");
-      hip_check(hipMemset(ctx->error_flag, 0, 256), "error word");
+      hip_check(hipMemsetAsync(ctx->error_flag, 0, 256, ctx->stream), "error word");
+      hip_check(hipStreamSynchronize(ctx->stream), "error word");
       size_t free_b = 0, total_b = 0;
       hip_check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
       ctx->weight_limit = weight_cache_bytes ? weight_cache_bytes : uint64_t(double(free_b) * 0.85);
@@ -543,6 +571,7 @@ int qnn_ctx_destroy(qnn_ctx *ctx) {
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->staging) (void)hipFree(ctx->staging);
+    if (ctx->readback) (void)hipHostFree(ctx->readback);
     (void)hipFree(ctx->error_flag);
     (void)hipStreamDestroy(ctx->stream);
     std::lock_guard<std::mutex> g(g_lock);
@@ -613,23 +642,37 @@ int qnn_upload_raw(qnn_ctx *ctx, const void *data, int count, qnn_tensor **out) 
 int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count) {
   return guarded([&] {
     check_ctx(ctx);
-    if (count < 0) count = t ? t->count : 0;
+    if (count == -1) count = t ? t->count : 0;
+    if (count < 1) fail(QNN_E_ARGUMENT, "Empty resident download");
     check_tensor(ctx, t, count);
-    if (!dst) fail(QNN_E_ARGUMENT, "Download destination");
-    hip_check(hipMemcpyAsync(dst, t->ptr, size_t(count) * 4, hipMemcpyDeviceToHost, ctx->stream), "download");
-    int flag = 0;
-    hip_check(hipMemcpyAsync(&flag, ctx->error_flag, 4, hipMemcpyDeviceToHost, ctx->stream), "error word");
+    if (!dst) fail(QNN_E_ARGUMENT, "Resident download");
+    // Data and the error word land in one pinned buffer; the caller's memory is
+    // written only when no error was flagged (Context.Implementation.inc:745-756).
+    const size_t bytes = size_t(count) * 4;
+    if (ctx->readback_bytes < bytes + 4) {
+      if (ctx->readback) (void)hipHostFree(ctx->readback);
+      ctx->readback = nullptr;
+      ctx->readback_bytes = 0;
+      hip_check(hipHostMalloc(&ctx->readback, bytes + 4, hipHostMallocDefault), "readback buffer");
+      ctx->readback_bytes = bytes + 4;
+    }
+    auto *rb = static_cast<uint8_t *>(ctx->readback);
+    hip_check(hipMemcpyAsync(rb, t->ptr, bytes, hipMemcpyDeviceToHost, ctx->stream), "download");
+    hip_check(hipMemcpyAsync(rb + bytes, ctx->error_flag, 4, hipMemcpyDeviceToHost, ctx->stream), "error word");
     sync(ctx);
+    release_flush_pins(ctx);
     ctx->st.readbacks++;
-    if (flag) {  // Download raises on the non-finite flag (Context.Implementation.inc:747-756)
+    int flag = 0;
+    std::memcpy(&flag, rb + bytes, 4);
+    if (flag) {
       hip_check(hipMemsetAsync(ctx->error_flag, 0, 4, ctx->stream), "error word reset");
       sync(ctx);
-      if (flag & 2) fail(QNN_E_INVALID_OP, "persistent kernel dependency wait timed out");
       if (flag & 4) fail(QNN_E_INVALID_OP, "workgroup placement differs from the probed XCD mapping");
       if (flag & 8) fail(QNN_E_INVALID_OP, "Invalid GPU expert ID");  // LLM.MoE.pas:384-385
       if (flag & 16) fail(QNN_E_INVALID_OP, "MoE dispatch index outside its tensor");
-      fail(QNN_E_INVALID_OP, "GPU produced a non-finite value");
+      fail(QNN_E_INVALID_OP, "Resident GPU computation produced non-finite values");
     }
+    std::memcpy(dst, rb, bytes);
     return QNN_OK;
   });
 }
@@ -652,6 +695,7 @@ int qnn_flush(qnn_ctx *ctx) {
   return guarded([&] {
     check_ctx(ctx);
     sync(ctx);
+    release_flush_pins(ctx);
     return QNN_OK;
   });
 }
@@ -676,7 +720,12 @@ int qnn_retain_weight(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols) {
   return guarded([&] {
     check_ctx(ctx);
     WeightEntry *e = acquire_matrix(ctx, w, rows, cols);
-    e->pins++;  // RetainWeight: never evicted while the context lives (Context.Implementation.inc:361-387)
+    // RetainWeight (Context.Implementation.inc:361-387): pinned for the context's
+    // lifetime; retaining an entry twice keeps one pin.
+    if (std::find(ctx->retained.begin(), ctx->retained.end(), e) != ctx->retained.end()) return QNN_OK;
+    ctx->retained.push_back(e);
+    e->pins++;
+    ctx->retained_bytes += e->bytes;
     return QNN_OK;
   });
 }
@@ -686,8 +735,13 @@ int qnn_preload_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, uint64_t stag
     check_ctx(ctx);
     (void)staging_limit;
     if (n < 0 || (n > 0 && !ws)) fail(QNN_E_ARGUMENT, "PreloadWeights");
-    OpPins pin;
-    for (int i = 0; i < n; ++i) pin(acquire_matrix(ctx, &ws[i], int(ws[i].shape0), int(ws[i].shape1)));
+    // Every preloaded entry stays pinned until the next Flush or Download, so a
+    // later acquisition in the same batch cannot evict it (Context.API.inc:85-86).
+    for (int i = 0; i < n; ++i) {
+      WeightEntry *e = acquire_matrix(ctx, &ws[i], int(ws[i].shape0), int(ws[i].shape1));
+      e->pins++;
+      ctx->flush_pins.push_back(e);
+    }
     return QNN_OK;
   });
 }
@@ -709,10 +763,8 @@ int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes) {
   return guarded([&] {
     check_ctx(ctx);
     if (!bytes) fail(QNN_E_ARGUMENT, "out");
-    uint64_t pinned = 0;
-    for (auto &kv : ctx->weights)
-      if (kv.second->pins) pinned += kv.second->bytes;
-    *bytes = ctx->weight_limit > pinned ? ctx->weight_limit - pinned : 0;
+    // WeightBatchCapacity (Context.Implementation.inc:421-429): the cache limit less the retained bytes.
+    *bytes = ctx->weight_limit - std::min(ctx->weight_limit, ctx->retained_bytes);
     return QNN_OK;
   });
 }
@@ -1093,7 +1145,7 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     ensure_splitk(ctx, p.partial_floats, p.counters);
     a.partial = ctx->partial;
     a.counters = ctx->counters;
-    a.xcd_local = ctx->xcd_local ? 1 : 0;
+    a.xcd_local = xcd_local_launch(ctx);
     a.err = ctx->error_flag;
     moe_launch(a, p, ctx->stream);
     ctx->st.int4_calls += 3;

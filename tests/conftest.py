@@ -2,7 +2,7 @@
 
 `gpu` tests need an MI355X (libqnn_hip.so + a visible HIP device); everything
 else runs on the CPU.  One resident context per process is allowed (as in the
-reference), so GPU tests share the session-scoped `ctx` fixture.
+reference), so the GPU tests of a module share the module-scoped `ctx` fixture.
 """
 import os
 import sys
@@ -19,8 +19,10 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD GPU and the built HIP library")
 
 
-@pytest.fixture(scope="session")
+@pytest.fixture(scope="module")
 def ctx():
+    """One resident context per test module (closed before the next module
+    opens its own, so modules may also create contexts with other settings)."""
     from quicknn_amd import hip
 
     c = hip.GPUContext(0)
