@@ -93,6 +93,7 @@ typedef struct {
   uint64_t weight_uploads, weight_upload_bytes, weight_cache_hits, weight_cache_misses, weight_evictions;
   uint64_t readbacks, submissions;
   uint64_t weight_bytes, weight_limit, activation_bytes, activation_peak_bytes;
+  uint64_t mlp_fused; /* TrySwiGLUVector + Int4Linear pairs run as one launch (no reference counterpart) */
 } qnn_status;
 
 /* ---------------------------------------------------------------------------
@@ -149,7 +150,11 @@ int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_we
 /* TrySwiGLUVector (Context.API.inc:132-133, Implementation.inc:1003-1056):
  * dst[o] = silu(gate.x)[o] * (up.x)[o].  Returns QNN_OK, or QNN_NOT_HANDLED
  * where the reference returns False (unsupported dtype mix, or the pair does
- * not fit the weight budget and is not resident). */
+ * not fit the weight budget and is not resident).  A native-INT4 pair is
+ * recorded and launched by the next call on the context; when that call is
+ * the qnn_int4_linear that reads dst (the MLP's down projection, one row),
+ * both run as one launch with results identical to two (QNN_FUSE_MLP=0 turns
+ * this off). */
 int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *gate, const qnn_weight *up,
                       int in_dim, int out_dim);
 

@@ -65,6 +65,22 @@ struct qnn_ctx_s {
   std::vector<qnn::WeightEntry *> flush_pins;
   std::vector<qnn::WeightEntry *> retained;
   uint64_t retained_bytes = 0;
+  // An INT4 TrySwiGLUVector recorded but not launched yet: the next call
+  // either fuses it with the Int4Linear that reads its output (one launch for
+  // the MLP, qnn_mlp.hip) or launches it on its own first.
+  struct Pending {
+    bool on = false;
+    qnn::WeightEntry *g = nullptr, *u = nullptr;
+    const float *x = nullptr;
+    float *h = nullptr;
+    int in = 0, out = 0;
+  } pending;
+  // Per-block completion flags of the fused MLP (qnn_mlp.hip), owned by it
+  // alone: zeroed when allocated, then only ever set to launch epochs.
+  void *mlp_flags = nullptr;
+  size_t mlp_flag_bytes = 0;
+  unsigned mlp_epoch = 0;
+  int mlp_cap[9][9] = {};  // co-resident workgroups of the fused MLP kernel per (gate/up, down) steps (0: not asked yet, -1: none)
   hipEvent_t events[64] = {};
   bool capturing = false;
   std::vector<qnn::WeightEntry *> capture_pins;
@@ -97,11 +113,16 @@ int guarded(F &&f) {
   }
 }
 
-void check_ctx(qnn_ctx_s *ctx) {
+void settle_pending(qnn_ctx_s *ctx);
+
+// Every entry point starts here.  A recorded SwiGLU is launched first unless
+// the caller is the Int4Linear that may fuse with it (keep_pending).
+void check_ctx(qnn_ctx_s *ctx, bool keep_pending = false) {
   if (!ctx || ctx != g_ctx) fail(QNN_E_ARGUMENT, "invalid context");
   // Context.Implementation.inc:70-71: resident work stays on its creating thread.
   if (std::this_thread::get_id() != ctx->owner) fail(QNN_E_INVALID_OP, "context used from a thread other than its creator");
   hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+  if (!keep_pending && ctx->pending.on) settle_pending(ctx);
 }
 
 // Check (Context.Implementation.inc): a live tensor of at least `minimum` floats.
@@ -455,6 +476,80 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
   if (padded) padded->live = false;  // later users of the buffer are ordered after this launch
 }
 
+// ---------------------------------------------------------------- fused decode MLP
+void settle_pending(qnn_ctx_s *ctx) {
+  const qnn_ctx_s::Pending p = ctx->pending;
+  ctx->pending = {};
+  p.g->pins--;
+  p.u->pins--;
+  run_int4(ctx, p.g, p.u, I4_SWIGLU, p.x, p.h, 1, p.in, p.out, nullptr);
+}
+
+bool mlp_fusion_enabled() { return env_int("QNN_FUSE_MLP", 1) != 0; }
+
+// Launches the recorded SwiGLU and the down projection `d` (h -> y) as one
+// kernel when the per-op plans allow it; false leaves the pending
+// SwiGLU recorded.
+bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
+  qnn_ctx_s::Pending &p = ctx->pending;
+  const I4Layout &lg = p.g->i4, &ld = d->i4;
+  if (lg.lanes != 1 || ld.lanes != 1 || p.in % 4 || p.out % 4) return false;
+  const I4Plan pg = int4_plan(lg, 1, I4_SWIGLU), pd = int4_plan(ld, 1, I4_STORE);
+  if (pg.tiles_per_wg != 1 || pd.tiles_per_wg != 1 || pg.gsw > 8 || pd.gsw > 8) return false;
+  const int grid = std::max(pg.grid, pd.grid);
+  int &cap = ctx->mlp_cap[pg.gsw][pd.gsw];
+  if (cap == 0) cap = std::max(-1, mlp_capacity(pg.gsw, pd.gsw, ctx->device));
+  if (cap <= 0 || grid > cap) return false;
+  const size_t pf_gu = size_t(2 * lg.blocks) * pg.slices * 64, pf_dn = size_t(ld.blocks) * pd.slices * 64;
+  const size_t c_gu = size_t(lg.blocks) * kCounterStride, c_dn = size_t(ld.blocks) * kCounterStride;
+  ensure_splitk(ctx, pf_gu + pf_dn, c_gu + c_dn);
+  const size_t flag_bytes = size_t(lg.blocks) * 256;
+  if (flag_bytes > ctx->mlp_flag_bytes) {  // zeroed: epoch 0 is never a launch
+    sync(ctx);
+    if (ctx->mlp_flags) (void)hipFree(ctx->mlp_flags);
+    ctx->mlp_flags = nullptr;
+    ctx->mlp_flag_bytes = 0;
+    hip_check(hipMalloc(&ctx->mlp_flags, flag_bytes), "fused MLP flags");
+    hip_check(hipMemsetAsync(ctx->mlp_flags, 0, flag_bytes, ctx->stream), "fused MLP flags");
+    hip_check(hipStreamSynchronize(ctx->stream), "fused MLP flags");
+    ctx->mlp_flag_bytes = flag_bytes;
+  }
+  MlpLaunch a;
+  a.lg = lg;
+  a.ld = ld;
+  a.gnib = p.g->dptr;
+  a.gscl = static_cast<const uint8_t *>(p.g->dptr) + lg.nib_bytes();
+  a.unib = p.u->dptr;
+  a.uscl = static_cast<const uint8_t *>(p.u->dptr) + lg.nib_bytes();
+  a.dnib = d->dptr;
+  a.dscl = static_cast<const uint8_t *>(d->dptr) + ld.nib_bytes();
+  a.x = p.x;
+  a.h = p.h;
+  a.y = y;
+  a.hidden = p.in;
+  a.inter = p.out;
+  a.sps_gu = pg.steps_per_slice;
+  a.slices_gu = pg.slices;
+  a.sps_dn = pd.steps_per_slice;
+  a.slices_dn = pd.slices;
+  a.grid_dn = pd.grid;
+  a.partial_gu = ctx->partial;
+  a.partial_dn = ctx->partial + pf_gu;
+  a.counters_gu = ctx->counters;
+  a.counters_dn = ctx->counters + c_gu;
+  a.flags = static_cast<unsigned *>(ctx->mlp_flags);
+  if (++ctx->mlp_epoch == 0) ctx->mlp_epoch = 1;
+  a.epoch = ctx->mlp_epoch;
+  a.xcd_local = xcd_local_launch(ctx);
+  a.err = ctx->error_flag;
+  if (!mlp_launch(a, pg.gsw, pd.gsw, grid, ctx->stream)) return false;
+  p.g->pins--;
+  p.u->pins--;
+  ctx->pending = {};
+  ctx->st.mlp_fused++;
+  return true;
+}
+
 // ---------------------------------------------------------------- Q8_0 multi-row GEMM
 // Rows at which the MFMA GEMM replaces per-row matvecs (one weight pass per row).
 int q8_gemm_min_rows() { return std::max(2, env_int("QNN_Q8_GEMM_MIN_ROWS", 4)); }
@@ -572,6 +667,7 @@ int qnn_ctx_destroy(qnn_ctx *ctx) {
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->readback) (void)hipHostFree(ctx->readback);
+    if (ctx->mlp_flags) (void)hipFree(ctx->mlp_flags);
     (void)hipFree(ctx->error_flag);
     (void)hipStreamDestroy(ctx->stream);
     std::lock_guard<std::mutex> g(g_lock);
@@ -667,6 +763,7 @@ int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count) {
     if (flag) {
       hip_check(hipMemsetAsync(ctx->error_flag, 0, 4, ctx->stream), "error word reset");
       sync(ctx);
+      if (flag & 2) fail(QNN_E_INVALID_OP, "fused MLP: the wait for the gate/up output timed out");
       if (flag & 4) fail(QNN_E_INVALID_OP, "workgroup placement differs from the probed XCD mapping");
       if (flag & 8) fail(QNN_E_INVALID_OP, "Invalid GPU expert ID");  // LLM.MoE.pas:384-385
       if (flag & 16) fail(QNN_E_INVALID_OP, "MoE dispatch index outside its tensor");
@@ -773,15 +870,27 @@ int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes) {
 int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
                     int out_dim) {
   return guarded([&] {
-    check_ctx(ctx);
-    // Int4Linear validation (Context.Implementation.inc:1091-1104).
-    if (rows < 1 || rows > 128 || in_dim < 1 || out_dim < 1 || src == dst || int64_t(rows) * out_dim > 0x7fffffff)
-      fail(QNN_E_ARGUMENT, "Invalid packed INT4 projection");
-    check_tensor(ctx, src, int64_t(rows) * in_dim);
-    check_tensor(ctx, dst, int64_t(rows) * out_dim);
-    OpPins pin;
-    WeightEntry *e = pin(acquire_int4(ctx, w, out_dim, in_dim));
-    run_int4(ctx, e, nullptr, I4_STORE, src->ptr, dst->ptr, rows, in_dim, out_dim, nullptr);
+    check_ctx(ctx, true);
+    try {
+      // Int4Linear validation (Context.Implementation.inc:1091-1104).
+      if (rows < 1 || rows > 128 || in_dim < 1 || out_dim < 1 || src == dst || int64_t(rows) * out_dim > 0x7fffffff)
+        fail(QNN_E_ARGUMENT, "Invalid packed INT4 projection");
+      check_tensor(ctx, src, int64_t(rows) * in_dim);
+      check_tensor(ctx, dst, int64_t(rows) * out_dim);
+      OpPins pin;
+      WeightEntry *e = pin(acquire_int4(ctx, w, out_dim, in_dim));
+      const qnn_ctx_s::Pending &p = ctx->pending;
+      // The down projection of a recorded SwiGLU: one launch for the MLP.
+      const bool fused = p.on && rows == 1 && src->ptr == p.h && in_dim == p.out && out_dim == p.in &&
+                         dst->ptr != p.h && try_fused_mlp(ctx, e, dst->ptr);
+      if (!fused) {
+        if (ctx->pending.on) settle_pending(ctx);
+        run_int4(ctx, e, nullptr, I4_STORE, src->ptr, dst->ptr, rows, in_dim, out_dim, nullptr);
+      }
+    } catch (...) {
+      if (ctx->pending.on) settle_pending(ctx);
+      throw;
+    }
     ctx->st.gemm_calls++;
     ctx->st.int4_calls++;
     return QNN_OK;
@@ -837,7 +946,21 @@ int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_
     if (i4) {
       WeightEntry *eg = pin(acquire_int4(ctx, gate, out_dim, in_dim));
       WeightEntry *eu = pin(acquire_int4(ctx, up, out_dim, in_dim));
-      run_int4(ctx, eg, eu, I4_SWIGLU, src->ptr, dst->ptr, 1, in_dim, out_dim, nullptr);
+      if (mlp_fusion_enabled() && !ctx->capturing && eg->i4.lanes == 1 && in_dim % 4 == 0 && out_dim % 4 == 0) {
+        // Recorded: launched with the next call (fused if that is the down
+        // projection of this output).  Pinned until then.
+        eg->pins++;
+        eu->pins++;
+        ctx->pending.on = true;
+        ctx->pending.g = eg;
+        ctx->pending.u = eu;
+        ctx->pending.x = src->ptr;
+        ctx->pending.h = dst->ptr;
+        ctx->pending.in = in_dim;
+        ctx->pending.out = out_dim;
+      } else {
+        run_int4(ctx, eg, eu, I4_SWIGLU, src->ptr, dst->ptr, 1, in_dim, out_dim, nullptr);
+      }
       ctx->st.int4_calls += 2;
     } else {
       WeightEntry *eg = pin(acquire_gguf(ctx, gate, out_dim, in_dim));

@@ -27,7 +27,11 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   __shared__ float red[4][MT][64];
   constexpr int P = 4 / T;  // waves per tile: parts of the workgroup's K-slice
   const int wave = dev::wave_id(), tid = threadIdx.x, lane = tid & 63;
-  const int units = (a.tiles + T - 1) / T;
+  const bool swiglu = a.mode == I4_SWIGLU;
+  // I4_SWIGLU with one tile per workgroup: units are padded to groups of 16 so
+  // that the gate tile (unit u) and the up tile (unit u + 8) of a block land on
+  // one XCD; with T >= 2 they share the workgroup.
+  const int units = swiglu && T == 1 ? (a.tiles + 15) / 16 * 16 : (a.tiles + T - 1) / T;
   int unit, slice;
   if (!dev::map_tile(blockIdx.x, slices, units, unit, slice)) return;
   const I4Layout &l = a.l;
@@ -48,15 +52,19 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   dev::load_x<MT, GSW>(
       xr, dev::rsrc(a.x, size_t(a.m) * a.x_stride * 4), [&](int m) { return uint32_t(m) * uint32_t(a.x_stride) * 4u; },
       a.m, ws0 * L * 32, sgroups * 32, tid);
-  const int tile = unit * T + wave / P;
+  int tile = unit * T + wave / P;
+  if (swiglu && T == 1) tile = 2 * ((unit >> 4) * 8 + (unit & 7)) + ((unit >> 3) & 1);
   const bool active = tile < a.tiles;
   const int t = active ? tile : 0;
-  int b = t, wl = lane;
+  // I4_SWIGLU: tile 2b is the gate matrix's block b, tile 2b + 1 the up
+  // matrix's; the choice is uniform per wave, so the buffer resources stay
+  // scalar.
+  int b = t;
+  const int wl = lane;
   const void *nb = a.nib, *sb = a.scl;
-  if (a.mode == I4_SWIGLU) {
+  if (swiglu) {
     b = t >> 1;
-    wl = (t & 1) * 32 + (lane & 31);
-    if (lane >= 32) { nb = a.nib2; sb = a.scl2; }
+    if (t & 1) { nb = a.nib2; sb = a.scl2; }
   }
   uint4 w[GSW];
   float sc[GSW];
@@ -96,29 +104,35 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   if (!active) return;
 
   // 4) Split-K across workgroups: the last slice of a tile to finish sums all
-  //    slices in slice order.
-  if (slices > 1) {
+  //    slices in slice order.  I4_SWIGLU always meets here: the last of the
+  //    2 x slices arrivals of a block sums the gate slices and the up slices.
+  constexpr int PU = MT >= 8 ? 2 : (MT >= 4 ? 4 : 16);  // independent partial loads in flight
+  float accu[MT];
+  if (slices > 1 || swiglu) {
     float *part_p = a.partial + (size_t(tile) * slices + slice) * MT * 64 + lane;
     dev::check_xcd(a.xcd_local, a.err, lane);
 #pragma unroll
     for (int m = 0; m < MT; ++m) dev::xstore(part_p + m * 64, acc[m], a.xcd_local);
-    unsigned *ctr = &a.counters[size_t(tile) * kCounterStride];
-    if (!dev::last_arrival(ctr, unsigned(slices), lane)) return;
-    const float *pt = a.partial + size_t(tile) * slices * MT * 64 + lane;
-    constexpr int PU = MT >= 8 ? 2 : (MT >= 4 ? 4 : 16);  // independent partial loads in flight
+    unsigned *ctr = &a.counters[size_t(swiglu ? tile >> 1 : tile) * kCounterStride];
+    if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane)) return;
+    const int t0 = swiglu ? tile & ~1 : tile;
+    const float *pt = a.partial + size_t(t0) * slices * MT * 64 + lane;
     dev::sum_slices<MT, PU>(
         acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices, a.xcd_local);
+    if (swiglu) {
+      const float *pu = pt + size_t(slices) * MT * 64;
+      dev::sum_slices<MT, PU>(
+          accu, [&](int s, int m) { return pu + (size_t(s) * MT + m) * 64; }, slices, a.xcd_local);
+    }
     dev::reset_counter(ctr, lane);
   }
 
   // 5) Epilogue: the first lane of each row writes it.
-  if (a.mode == I4_SWIGLU) {
+  if (swiglu) {
     const int row = b * l.rpb + wl / L;
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float u = __shfl_down(acc[m], 32);
-      if (lane < 32 && j == 0 && row < a.n && m < a.m) a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * u;
-    }
+    for (int m = 0; m < MT; ++m)
+      if (j == 0 && row < a.n && m < a.m) a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * accu[m];
   } else {
     const int row = b * l.rpb + lane / L;
     if (j == 0 && row < a.n) {
@@ -270,8 +284,9 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   p.steps_per_slice = sps;
   p.slices = (l.steps + P * sps - 1) / (P * sps);
   p.lds = dev::xplanes_bytes(p.mt, P * sps * l.lanes);
-  p.grid = (units + 7) / 8 * 8 * p.slices;
-  p.partial_floats = p.slices > 1 ? size_t(tiles) * p.slices * p.mt * 64 : 0;
+  const int grid_units = mode == I4_SWIGLU && p.tiles_per_wg == 1 ? (tiles + 15) / 16 * 16 : (units + 7) / 8 * 8;
+  p.grid = grid_units * p.slices;
+  p.partial_floats = p.slices > 1 || mode == I4_SWIGLU ? size_t(tiles) * p.slices * p.mt * 64 : 0;
   p.counters = size_t(tiles) * kCounterStride;
   return p;
 }

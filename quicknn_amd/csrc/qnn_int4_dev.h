@@ -88,10 +88,14 @@ __device__ __forceinline__ Rsrc rsrc(const void *base, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(uint32_t(min(bytes, size_t(0xFFFFFFFFu)))),
                                            0x00020000);
 }
+// AUX = 16 sets SC1: the load is coherent at device (agent) scope, for data
+// another XCD wrote inside the same launch.
+template <int AUX = 0>
 __device__ __forceinline__ uint4 ld128(Rsrc r, uint32_t voff, uint32_t soff) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0);
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), AUX);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+constexpr int kCoherent = 16;
 __device__ __forceinline__ float ld32f(Rsrc r, uint32_t voff, uint32_t soff) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), 0));
 }
@@ -102,7 +106,7 @@ __device__ __forceinline__ float ld32f(Rsrc r, uint32_t voff, uint32_t soff) {
 // no load waits for another; stage_x zeroes the pieces outside the slice, the
 // row or the token count.
 // `ne` (uniform) bounds the passes to those the slice needs.
-template <int MT, int GSW, class OffF>
+template <int MT, int GSW, int AUX = 0, class OffF>
 __device__ __forceinline__ void load_x(float4 (&xr)[MT][x_iters<GSW>()], Rsrc src, OffF rowoff, int mt, int e0,
                                        int ne, int tid) {
   const int passes = (ne + 1023) >> 10;
@@ -113,7 +117,7 @@ __device__ __forceinline__ void load_x(float4 (&xr)[MT][x_iters<GSW>()], Rsrc sr
     for (int it = 0; it < x_iters<GSW>(); ++it) {
       float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
       if (it < passes) {
-        const uint4 v = ld128(src, base, uint32_t(it) * 4096u);
+        const uint4 v = ld128<AUX>(src, base, uint32_t(it) * 4096u);
         f = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
       }
       xr[m][it] = f;

@@ -156,6 +156,28 @@ void misc_pad_rows(float *dst, const float *src, int rows, int cols, int cols_pa
 // contiguous tiled INT4 matrix per projection at base + e * stride.
 constexpr int kMoEMaxExperts = 512;  // the route op's limit (moe.comp:13, 512-entry score array)
 constexpr int kMoEMaxRoutes = 2048;  // rows * topk per call
+// One decode MLP in a single launch (qnn_mlp.hip): gate/up items
+// of the I4_SWIGLU plan and down items of the I4_STORE plan.
+struct MlpLaunch {
+  I4Layout lg, ld;  // gate/up layout (both matrices), down layout; one lane per row
+  const void *gnib = nullptr, *gscl = nullptr, *unib = nullptr, *uscl = nullptr, *dnib = nullptr, *dscl = nullptr;
+  const float *x = nullptr;  // hidden floats
+  float *h = nullptr;        // inter floats (written, device-coherent)
+  float *y = nullptr;        // hidden floats
+  int hidden = 0, inter = 0;
+  int sps_gu = 0, slices_gu = 0;             // I4_SWIGLU plan of the pair
+  int sps_dn = 0, slices_dn = 0, grid_dn = 0;  // I4_STORE plan of the down matrix (its per-op grid)
+  float *partial_gu = nullptr, *partial_dn = nullptr;
+  unsigned *counters_gu = nullptr, *counters_dn = nullptr;
+  unsigned *flags = nullptr;  // per 64-row block of h, 256 B apart: epoch of the launch that completed it
+  unsigned epoch = 0;         // this launch's number (never 0)
+  int xcd_local = 0;          // split-K partial sums through the XCD's L2 (placement checked)
+  int *err = nullptr;         // bit 2: a wait for h timed out; bit 4: unexpected XCD placement
+};
+size_t mlp_lds_bytes(int gg, int gd);
+int mlp_capacity(int gg, int gd, int device);  // co-resident workgroups (0: variant not built)
+bool mlp_launch(const MlpLaunch &a, int gg, int gd, int grid, hipStream_t s);  // false: not launched
+
 struct MoELaunch {
   const uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
   size_t gu_stride = 0, dn_stride = 0;  // bytes per expert matrix
