@@ -2,9 +2,9 @@
 """Benchmark: QuickNN's quantized-weight decode path on one MI355X.
 
 Default (`--config 2`, the headline): Qwen3-4B-shaped native-INT4 decode-layer
-MLP.  hidden 2560, intermediate 9728; per layer the fused gate+up projection
-with SwiGLU (TrySwiGLUVector, one kernel) then the down projection
-(Int4Linear); 36 layers with independent seeds, batch 1.  A "step" is one token
+MLP.  hidden 2560, intermediate 9728; per layer the gate+up projection with
+SwiGLU (TrySwiGLUVector) then the down projection (Int4Linear), which the
+backend runs as one fused launch; 36 layers with independent seeds, batch 1.  A "step" is one token
 through the 36 layers, the output of layer l feeding layer l+1.  Weights are
 bf16 N(0, 0.02) (truncated from fp32 as SingleToBF16 does) packed with
 QuickNN's INT4 algorithm; activations fp32 N(0,1) RMS-normalised with unit
@@ -15,10 +15,10 @@ value = algorithmic bytes per step (packed weights + activations read once +
 outputs written once) / measured time per step, in GB/s.
 
 Also reported: us/layer and tokens/s; the dominant kernel's roofline (the
-fused gate/up SwiGLU matvec: algorithmic bytes per launch over its average
-launch time, from HIP events on the context stream around 36-launch runs of
-it); batch-8 figures; and the reference's CPU SIMD path (an AVX2 restatement in
-the CPU oracle) timed on this host on the same packed weights.
+fused decode MLP, one launch per layer: algorithmic bytes per launch over its
+average launch time, from HIP events on the context stream around 36-launch
+runs of it); batch-8 figures; and the reference's CPU SIMD path (an AVX2
+restatement in the CPU oracle) timed on this host on the same packed weights.
 
 The other workloads of the benchmark definition are measured with
 `--config 1|3|4|5` (one JSON line each, same fields):
@@ -173,19 +173,25 @@ def run_cfg2(args, hip) -> dict:
     us_layer = ms_step * 1000 / LAYERS
     value = (wbytes + abytes1) * LAYERS / (ms_step * 1e-3) / 1e9
 
-    # Dominant kernel (the fused gate/up SwiGLU matvec, 62% of the layer's
-    # bytes): HIP events on the context stream around its 36 launches over the
-    # 36 layers, back to back, repeated; average per launch.
+    # Dominant kernel: the fused decode MLP (k_int4_mlp, one launch per layer:
+    # the gate/up SwiGLU recorded by TrySwiGLUVector runs together with the
+    # Int4Linear that reads its output).  HIP events on the context stream
+    # around 36-launch runs over the 36 layers, back to back, repeated;
+    # average per launch.  With QNN_FUSE_MLP=0 the pair runs as two launches
+    # and the figure is per pair.
     reps = max(3, args.steps // 5)
+    fused0 = ctx.status().mlp_fused
     ctx.EventRecord(6)
     for _ in range(reps):
         for (g, u, d) in blocks:
             ctx.TrySwiGLUVector(h, x, g, u, HIDDEN, INTER)
+            ctx.Int4Linear(ya, h, d, 1, INTER, HIDDEN)
     ctx.EventRecord(7)
     ctx.Flush()
-    gu_us = ctx.EventElapsedMs(6, 7) * 1000 / (reps * LAYERS)
-    gu_bytes = 2 * INTER * hip.int4_row_bytes(HIDDEN) + 4 * (HIDDEN + INTER)  # weights + x in + h out
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    fused = ctx.status().mlp_fused - fused0 == reps * LAYERS
+    k_us = ctx.EventElapsedMs(6, 7) * 1000 / (reps * LAYERS)
+    k_bytes = wbytes + abytes1  # the layer's weights + x in, h out and in, y out
+    achieved = k_bytes / (k_us * 1e-6) / 1e9
 
     # Batch 8: gate and up as Int4Linear (8 rows), GO_SWIGLU, then down (the
     # engine's multi-row path, LLM.pas:594-601).
@@ -220,7 +226,7 @@ def run_cfg2(args, hip) -> dict:
     ctx.Flush()
 
     traffic = None  # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-    tpath = os.path.join(ROOT, "profiles", "int4_swiglu_gateup_qwen3_4b_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "int4_mlp_fused_qwen3_4b_traffic.json")
     if os.path.exists(tpath):
         try:
             traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
@@ -242,9 +248,11 @@ def run_cfg2(args, hip) -> dict:
                 "GBps": round((wbytes + abytes8) * LAYERS / (ms8 * 1e-3) / 1e9, 1),
                 "tokens_per_s": round(8000.0 / ms8, 1)},
         roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                  "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                  "kernel": "k_int4_matvec (I4_SWIGLU: fused gate+up SwiGLU, 9728x2560 pair)",
-                  "kernel_us": round(gu_us, 3), "bytes_per_launch": gu_bytes,
+                  "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic if fused else None,
+                  "kernel": ("k_int4_mlp (fused decode MLP: gate/up SwiGLU 2x9728x2560 + down 2560x9728, "
+                             "one launch per layer)") if fused else
+                            "k_int4_matvec I4_SWIGLU + I4_STORE (two launches per layer, fusion off)",
+                  "kernel_us": round(k_us, 3), "bytes_per_launch": k_bytes,
                   "timing": f"HIP events around {reps}x{LAYERS} back-to-back launches on the context stream"},
         cpu_baseline=cpu,
         setup_s=round(gen_s, 1))
