@@ -93,7 +93,8 @@ typedef struct {
   uint64_t weight_uploads, weight_upload_bytes, weight_cache_hits, weight_cache_misses, weight_evictions;
   uint64_t readbacks, submissions;
   uint64_t weight_bytes, weight_limit, activation_bytes, activation_peak_bytes;
-  uint64_t mlp_fused; /* TrySwiGLUVector + Int4Linear pairs run as one launch (no reference counterpart) */
+  uint64_t mlp_fused;      /* TrySwiGLUVector + Int4Linear pairs run as one launch (no reference counterpart) */
+  uint64_t linear_grouped; /* one-row GGUF Linear calls that ran in a shared launch (no reference counterpart) */
 } qnn_status;
 
 /* ---------------------------------------------------------------------------
@@ -136,7 +137,11 @@ int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /
  * ------------------------------------------------------------------------- */
 /* Linear (Context.API.inc:117-122, Implementation.inc:813-899).  GGUF weights:
  * rows == 1 runs the packed matvec (op 65), rows > 1 the multi-row product
- * (gemm.comp); Q8_0 with rows >= 4 runs the fp16-MFMA GEMM.  bias (optional,
+ * (gemm.comp); Q8_0 with rows >= 4 runs the fp16-MFMA GEMM.  One-row calls
+ * without bias are recorded and launched by the next call on the context;
+ * consecutive ones on the same src with the same encoding (up to 4) share one
+ * launch, each result identical to its own launch (QNN_GROUP_LINEAR=0 turns
+ * this off).  bias (optional,
  * F32 or BF16 [out]) is added afterwards.  scales must be NULL (INT8 ConvRot
  * weights are outside this backend). */
 int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,

@@ -80,7 +80,17 @@ struct qnn_ctx_s {
   void *mlp_flags = nullptr;
   size_t mlp_flag_bytes = 0;
   unsigned mlp_epoch = 0;
-  int mlp_cap[9][9] = {};  // co-resident workgroups of the fused MLP kernel per (gate/up, down) steps (0: not asked yet, -1: none)
+  int mlp_cap[9][9] = {};
+  // GGUF one-row Linear calls recorded for one grouped launch: consecutive
+  // calls on the same input (a layer's q/k/v or gate/up projections) with the
+  // same encoding and plan width, at most kGGMaxGroup, distinct outputs.
+  struct LinearGroup {
+    int count = 0, bw = 0, enc = 0;
+    const float *x = nullptr;
+    qnn::WeightEntry *e[qnn::kGGMaxGroup] = {};
+    float *y[qnn::kGGMaxGroup] = {};
+    int out[qnn::kGGMaxGroup] = {}, slices[qnn::kGGMaxGroup] = {};
+  } lgroup;  // co-resident workgroups of the fused MLP kernel per (gate/up, down) steps (0: not asked yet, -1: none)
   hipEvent_t events[64] = {};
   bool capturing = false;
   std::vector<qnn::WeightEntry *> capture_pins;
@@ -122,7 +132,7 @@ void check_ctx(qnn_ctx_s *ctx, bool keep_pending = false) {
   // Context.Implementation.inc:70-71: resident work stays on its creating thread.
   if (std::this_thread::get_id() != ctx->owner) fail(QNN_E_INVALID_OP, "context used from a thread other than its creator");
   hip_check(hipSetDevice(ctx->device), "hipSetDevice");
-  if (!keep_pending && ctx->pending.on) settle_pending(ctx);
+  if (!keep_pending && (ctx->pending.on || ctx->lgroup.count)) settle_pending(ctx);
 }
 
 // Check (Context.Implementation.inc): a live tensor of at least `minimum` floats.
@@ -476,8 +486,75 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
   if (padded) padded->live = false;  // later users of the buffer are ordered after this launch
 }
 
+// ---------------------------------------------------------------- recorded ops
+// Launches the recorded GGUF Linear group: one kernel, each member with its
+// own split-K workspace, computed exactly as on its own.
+void launch_linear_group(qnn_ctx_s *ctx) {
+  qnn_ctx_s::LinearGroup g = ctx->lgroup;
+  ctx->lgroup = {};
+  for (int i = 0; i < g.count; ++i) g.e[i]->pins--;
+  size_t pf = 0, nc = 0;
+  GGGroup grp;
+  grp.count = g.count;
+  for (int i = 0; i < g.count; ++i) {
+    const int tiles = g.e[i]->gg.tiles;
+    grp.start[i + 1] = grp.start[i] + (tiles + 7) / 8 * 8 * g.slices[i];
+    pf += g.slices[i] > 1 ? size_t(tiles) * g.slices[i] * 64 : 0;
+    nc += size_t(tiles) * kCounterStride;
+  }
+  ensure_splitk(ctx, pf, nc);
+  pf = nc = 0;
+  for (int i = 0; i < g.count; ++i) {
+    GGArgs &a = grp.m[i];
+    const WeightEntry *w = g.e[i];
+    a.l = w->gg;
+    a.w = w->dptr;
+    a.x = g.x;
+    a.x_vec4 = (w->gg.cols % 4 == 0) && (reinterpret_cast<uintptr_t>(g.x) % 16 == 0);
+    a.y = g.y[i];
+    a.n = g.out[i];
+    a.tiles = w->gg.tiles;
+    a.mode = GG_STORE;
+    a.partial = ctx->partial + pf;
+    a.counters = ctx->counters + nc;
+    a.xcd_local = xcd_local_launch(ctx);
+    a.err = ctx->error_flag;
+    grp.slices[i] = g.slices[i];
+    pf += g.slices[i] > 1 ? size_t(a.tiles) * g.slices[i] * 64 : 0;
+    nc += size_t(a.tiles) * kCounterStride;
+  }
+  gguf_group_launch(grp, g.bw, ctx->stream);
+  if (g.count > 1) ctx->st.linear_grouped += uint64_t(g.count);
+}
+
+bool linear_grouping_enabled() { return env_int("QNN_GROUP_LINEAR", 1) != 0; }
+
+// Records a one-row GGUF Linear into the group, launching what was recorded
+// first when it does not fit.
+void record_linear(qnn_ctx_s *ctx, WeightEntry *e, const float *x, float *y, int out_dim) {
+  int bw, slices;
+  gguf_plan(e->gg, e->gg.tiles, &bw, &slices);
+  qnn_ctx_s::LinearGroup &g = ctx->lgroup;
+  bool fits = g.count > 0 && g.count < kGGMaxGroup && g.x == x && g.enc == e->gg.enc && g.bw == bw;
+  for (int i = 0; fits && i < g.count; ++i) fits = g.y[i] != y;
+  if (!fits) settle_pending(ctx);
+  if (g.count == 0) {
+    g.x = x;
+    g.enc = e->gg.enc;
+    g.bw = bw;
+  }
+  e->pins++;
+  g.e[g.count] = e;
+  g.y[g.count] = y;
+  g.out[g.count] = out_dim;
+  g.slices[g.count] = slices;
+  g.count++;
+}
+
 // ---------------------------------------------------------------- fused decode MLP
 void settle_pending(qnn_ctx_s *ctx) {
+  if (ctx->lgroup.count) launch_linear_group(ctx);
+  if (!ctx->pending.on) return;
   const qnn_ctx_s::Pending p = ctx->pending;
   ctx->pending = {};
   p.g->pins--;
@@ -884,11 +961,11 @@ int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_we
       const bool fused = p.on && rows == 1 && src->ptr == p.h && in_dim == p.out && out_dim == p.in &&
                          dst->ptr != p.h && try_fused_mlp(ctx, e, dst->ptr);
       if (!fused) {
-        if (ctx->pending.on) settle_pending(ctx);
+        settle_pending(ctx);
         run_int4(ctx, e, nullptr, I4_STORE, src->ptr, dst->ptr, rows, in_dim, out_dim, nullptr);
       }
     } catch (...) {
-      if (ctx->pending.on) settle_pending(ctx);
+      settle_pending(ctx);
       throw;
     }
     ctx->st.gemm_calls++;
@@ -985,27 +1062,40 @@ int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_
 int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,
                const qnn_weight *bias, int rows, int in_dim, int out_dim) {
   return guarded([&] {
-    check_ctx(ctx);
-    check_tensor(ctx, src, int64_t(rows) * in_dim);
-    check_tensor(ctx, dst, int64_t(rows) * out_dim);
-    if (rows < 1 || in_dim < 1 || out_dim < 1 || src == dst)
-      fail(QNN_E_ARGUMENT, "Invalid resident linear dimensions/alias");
-    check_weight_desc(w);
-    if (scales && scales->data) fail(QNN_E_NOT_SUPPORTED, "INT8 ConvRot weights are not handled by the HIP backend");
-    if (!is_gguf(w->encoding))
-      fail(QNN_E_NOT_SUPPORTED, "Linear handles GGUF weights; native INT4 goes through Int4Linear");
-    OpPins pin;
-    WeightEntry *e = pin(acquire_gguf(ctx, w, out_dim, in_dim));
-    if (w->encoding != QNN_WE_Q8_0 || rows < q8_gemm_min_rows()) {
-      // Matvec per row (op 65); rows > 1 of K-quants reuse it row by row.
-      for (int r = 0; r < rows; ++r)
-        run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim, out_dim);
-    } else {
-      run_q8_gemm(ctx, e, src->ptr, dst->ptr, rows, in_dim, out_dim);
-    }
-    if (bias && bias->data) {
-      WeightEntry *b = pin(acquire_raw(ctx, bias, out_dim));
-      misc_bias_add(dst->ptr, b->dptr, b->raw_dtype == QNN_DT_BF16, rows, out_dim, ctx->stream);
+    check_ctx(ctx, true);
+    try {
+      check_tensor(ctx, src, int64_t(rows) * in_dim);
+      check_tensor(ctx, dst, int64_t(rows) * out_dim);
+      if (rows < 1 || in_dim < 1 || out_dim < 1 || src == dst)
+        fail(QNN_E_ARGUMENT, "Invalid resident linear dimensions/alias");
+      check_weight_desc(w);
+      if (scales && scales->data) fail(QNN_E_NOT_SUPPORTED, "INT8 ConvRot weights are not handled by the HIP backend");
+      if (!is_gguf(w->encoding))
+        fail(QNN_E_NOT_SUPPORTED, "Linear handles GGUF weights; native INT4 goes through Int4Linear");
+      OpPins pin;
+      WeightEntry *e = pin(acquire_gguf(ctx, w, out_dim, in_dim));
+      const bool has_bias = bias && bias->data;
+      if (rows == 1 && !has_bias && !ctx->capturing && linear_grouping_enabled()) {
+        // Recorded: launched with the next calls on the same input as one kernel.
+        record_linear(ctx, e, src->ptr, dst->ptr, out_dim);
+      } else {
+        settle_pending(ctx);
+        if (w->encoding != QNN_WE_Q8_0 || rows < q8_gemm_min_rows()) {
+          // Matvec per row (op 65); rows > 1 of K-quants reuse it row by row.
+          for (int r = 0; r < rows; ++r)
+            run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim,
+                     out_dim);
+        } else {
+          run_q8_gemm(ctx, e, src->ptr, dst->ptr, rows, in_dim, out_dim);
+        }
+        if (has_bias) {
+          WeightEntry *b = pin(acquire_raw(ctx, bias, out_dim));
+          misc_bias_add(dst->ptr, b->dptr, b->raw_dtype == QNN_DT_BF16, rows, out_dim, ctx->stream);
+        }
+      }
+    } catch (...) {
+      settle_pending(ctx);
+      throw;
     }
     ctx->st.gemm_calls++;
     ctx->st.gguf_calls++;

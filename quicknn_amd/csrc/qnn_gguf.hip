@@ -363,13 +363,21 @@ __device__ float unit_q2_k(const uint4 *mw, uint32_t side, const XSlice<NG> &xs,
 // Workgroup = 4 waves on one 64-row tile (SWIGLU: 32 gate rows in lanes
 // 0-31, the same 32 up rows in lanes 32-63); slice = 4*BW units, wave w
 // streams units [w*BW, (w+1)*BW) of it.
+// A launch carries up to kGGMaxGroup such matvecs (same encoding and BW, the
+// same input in practice: the q/k/v or gate/up projections of a layer); the
+// member is chosen by workgroup range and computed exactly as on its own.
 template <int ENC, int BW>
-__global__ __launch_bounds__(256) void k_gguf_matvec(const GGArgs a, const int slices) {
+__global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   using F = Fmt<ENC>;
   constexpr int U = 4 * BW;   // units per slice
   constexpr int NG = U * 8;   // 32-groups per slice
+  int mi = 0;
+  while (mi + 1 < grp.count && int(blockIdx.x) >= grp.start[mi + 1]) ++mi;
+  const GGArgs &a = grp.m[mi];
+  const int slices = grp.slices[mi];
+  const int bidx = int(blockIdx.x) - grp.start[mi];  // a multiple-of-8 offset keeps the XCD
   int tile, slice;
-  if (!map_tile_slice(blockIdx.x, slices, a.tiles, tile, slice)) return;
+  if (!map_tile_slice(bidx, slices, a.tiles, tile, slice)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const GGLayout &l = a.l;
   const int u0 = slice * U;
@@ -534,9 +542,10 @@ __global__ __launch_bounds__(256) void k_gguf_matvec(const GGArgs a, const int s
 }
 
 template <int ENC>
-void launch_enc(const GGArgs &a, int bw, int slices, int grid, hipStream_t st) {
-  if (bw == 2) hipLaunchKernelGGL((k_gguf_matvec<ENC, 2>), dim3(grid), dim3(256), 0, st, a, slices);
-  else hipLaunchKernelGGL((k_gguf_matvec<ENC, 1>), dim3(grid), dim3(256), 0, st, a, slices);
+void launch_enc(const GGGroup &g, int bw, hipStream_t st) {
+  const int grid = g.start[g.count];
+  if (bw == 2) hipLaunchKernelGGL((k_gguf_matvec<ENC, 2>), dim3(grid), dim3(256), 0, st, g);
+  else hipLaunchKernelGGL((k_gguf_matvec<ENC, 1>), dim3(grid), dim3(256), 0, st, g);
 }
 
 }  // namespace
@@ -592,17 +601,27 @@ void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {
   *slices = (l.units + 4 * pick - 1) / (4 * pick);
 }
 
-void gguf_matvec_launch(const GGArgs &a, int bw, int slices, hipStream_t s) {
-  const int grid = (a.tiles + 7) / 8 * 8 * slices;
-  switch (a.l.enc) {
-    case QNN_WE_Q4_K: launch_enc<QNN_WE_Q4_K>(a, bw, slices, grid, s); break;
-    case QNN_WE_Q6_K: launch_enc<QNN_WE_Q6_K>(a, bw, slices, grid, s); break;
-    case QNN_WE_Q3_K: launch_enc<QNN_WE_Q3_K>(a, bw, slices, grid, s); break;
-    case QNN_WE_Q2_K: launch_enc<QNN_WE_Q2_K>(a, bw, slices, grid, s); break;
-    case QNN_WE_Q8_0: launch_enc<QNN_WE_Q8_0>(a, bw, slices, grid, s); break;
+void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s) {
+  if (g.count < 1 || g.count > kGGMaxGroup) fail(QNN_E_INVALID_OP, "gguf group size");
+  switch (g.m[0].l.enc) {
+    case QNN_WE_Q4_K: launch_enc<QNN_WE_Q4_K>(g, bw, s); break;
+    case QNN_WE_Q6_K: launch_enc<QNN_WE_Q6_K>(g, bw, s); break;
+    case QNN_WE_Q3_K: launch_enc<QNN_WE_Q3_K>(g, bw, s); break;
+    case QNN_WE_Q2_K: launch_enc<QNN_WE_Q2_K>(g, bw, s); break;
+    case QNN_WE_Q8_0: launch_enc<QNN_WE_Q8_0>(g, bw, s); break;
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
   hip_check(hipGetLastError(), "gguf matvec launch");
+}
+
+void gguf_matvec_launch(const GGArgs &a, int bw, int slices, hipStream_t s) {
+  GGGroup g;
+  g.m[0] = a;
+  g.slices[0] = slices;
+  g.start[0] = 0;
+  g.start[1] = (a.tiles + 7) / 8 * 8 * slices;
+  g.count = 1;
+  gguf_group_launch(g, bw, s);
 }
 
 }  // namespace qnn

@@ -234,6 +234,17 @@ void gguf_repack_launch(const uint8_t *src, const GGLayout &l, void *dst, hipStr
 void gguf_dequant_launch(const GGLayout &l, const void *w, float *out, hipStream_t s);
 void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices);
 void gguf_matvec_launch(const GGArgs &a, int bw, int slices, hipStream_t s);
+// Up to kGGMaxGroup matvecs of one encoding and plan width in one launch:
+// member i owns workgroups [start[i], start[i+1]) (multiples of 8, so each
+// member keeps its XCD-aware tile map).
+constexpr int kGGMaxGroup = 4;
+struct GGGroup {
+  GGArgs m[kGGMaxGroup];
+  int slices[kGGMaxGroup] = {};
+  int start[kGGMaxGroup + 1] = {};
+  int count = 0;
+};
+void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s);
 
 // Q8_0 GEMM (qnn_gemm.hip).
 size_t q8_act_bytes(int m, int k);
