@@ -166,7 +166,9 @@ __global__ void k_int4_repack(const uint8_t *__restrict__ src, I4Layout l, uint4
     words = make_uint4(w32[1], w32[2], w32[3], w32[4]);
   }
   nib[idx] = words;
-  scl[idx] = sv;
+  scl[l.scale_at(b, s, lane)] = sv;
+  if (s == l.steps - 1)  // the last piece's slots past the last step hold 0
+    for (int p = s + 1; p < l.quads() * 4; ++p) scl[l.scale_at(b, p, lane)] = 0.0f;
 }
 
 // Bit-exact dequantisation fl32((n-8)*s) of the resident copy -> [rows][cols].
@@ -182,7 +184,7 @@ __global__ void k_int4_dequant(I4Layout l, const uint4 *__restrict__ nib, const 
   const size_t at = (size_t(b) * l.steps + s) * 64 + lane;
   const uint32_t word = sel4u(nib[at], e >> 3);
   const int n = int((word >> (4 * (e & 7))) & 15u);
-  out[idx] = float(n - 8) * scl[at];
+  out[idx] = float(n - 8) * scl[l.scale_at(b, s, lane)];
 }
 
 template <int MT, int GSW>
@@ -276,7 +278,10 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
     if (set0[i] <= cap && waves(set0[i]) >= size_t(target)) sps = set0[i];
   if (!sps) sps = 1;
   const int forced = env_int("QNN_I4_SPS", 0);
-  if (forced > 0) sps = std::min(forced, cap);
+  if (forced > 0) {  // a power of two: scale pieces hold 4 aligned steps
+    sps = 1;
+    while (sps * 2 <= std::min(forced, cap)) sps *= 2;
+  }
   const int *set = p.mt == 1 ? kGsw1 : (p.mt <= 4 ? kGswN : kGswBig);
   const int nset = p.mt == 1 ? int(sizeof kGsw1 / sizeof(int)) : 3;
   sps = std::min(sps, pick_template(sps, set, nset));

@@ -9,11 +9,11 @@
 // a power of two <= 16) and a 64-lane block holds R = 64/L rows.  Lane
 // l = r*L + j of block b carries groups j, j+L, j+2L, ... of row b*R + r; its
 // step-s group (group s*L + j) sits at
-//     nibbles: 16 B at ((b*S + s)*64 + l)          S = ceil(groups / L)
-//     scale:    4 B at ((b*S + s)*64 + l)
+//     nibbles: 16 B at ((b*S + s)*64 + l)               S = ceil(groups / L)
+//     scale:    4 B at ((b*Q + s/4)*64 + l)*4 + s%4       Q = ceil(S / 4)
 // so every step of a wave is one 16-byte load per lane over 1 KiB of
-// contiguous nibbles plus one 4-byte load over 256 B of scales.  Padding
-// groups/rows hold scale 0.
+// contiguous nibbles, and every 4 steps one more over 1 KiB of scales (a
+// lane's 4 scales side by side).  Padding groups/rows hold scale 0.
 //
 // A wave computes the rows of one block ("tile") over a K-range of steps; the
 // L partial sums of a row meet by cross-lane reduction.  The activation slice
@@ -128,14 +128,33 @@ __device__ __forceinline__ void load_x(float4 (&xr)[MT][x_iters<GSW>()], Rsrc sr
 // This wave's weight stream for GSW steps from step s0 of block b (lane wl of
 // the block): nibble pieces and scales.  Steps at or past the matrix's last
 // step read other blocks or zeros (masked in dot).
+// Scale pieces a GSW-step window needs: windows start at a multiple of their
+// (power-of-two) length, so steps s0..s0+GSW-1 lie in GSW/4 pieces, or in one
+// piece at offset s0 % 4 when GSW <= 2.
+template <int GSW>
+constexpr int scale_quads() { return GSW >= 4 ? GSW / 4 : 1; }
+template <int GSW>
+__device__ __forceinline__ void pick_scales(float (&sc)[GSW], const uint4 (&q)[scale_quads<GSW>()], int s0) {
+  if constexpr (GSW >= 4) {
+#pragma unroll
+    for (int g = 0; g < GSW; ++g) sc[g] = __uint_as_float(sel4u(q[g >> 2], g & 3));
+  } else {
+    const int o = s0 & 3;
+#pragma unroll
+    for (int g = 0; g < GSW; ++g) sc[g] = __uint_as_float(sel4u(q[0], (o + g) & 3));
+  }
+}
 template <int GSW>
 __device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc nib, Rsrc scl, const I4Layout &l, int b,
                                        int s0, int wl) {
   const uint32_t at = uint32_t((size_t(b) * l.steps + s0) * 64 + wl);
+  const uint32_t qat = uint32_t((size_t(b) * l.quads() + (s0 >> 2)) * 64 + wl);
+  uint4 q[scale_quads<GSW>()];
 #pragma unroll
-  for (int g = 0; g < GSW; ++g) sc[g] = ld32f(scl, at * 4u, uint32_t(g) * 256u);
+  for (int i = 0; i < scale_quads<GSW>(); ++i) q[i] = ld128(scl, qat * 16u, uint32_t(i) * 1024u);
 #pragma unroll
   for (int g = 0; g < GSW; ++g) w[g] = ld128(nib, at * 16u, uint32_t(g) * 1024u);
+  pick_scales<GSW>(sc, q, s0);
 }
 
 // Quantises the loaded slice per 32-element group to 16-bit fixed point,

@@ -53,8 +53,13 @@ struct I4Layout {
   int rpb = 64;    // R = 64 / L rows per block
   int steps = 0;   // S
   int blocks = 0;  // ceil(rows / R)
+  __host__ __device__ int quads() const { return (steps + 3) / 4; }  // scale pieces: 4 steps each
   __host__ __device__ size_t nib_bytes() const { return size_t(blocks) * steps * 64 * 16; }
-  __host__ __device__ size_t scale_bytes() const { return size_t(blocks) * steps * 64 * 4; }
+  __host__ __device__ size_t scale_bytes() const { return size_t(blocks) * quads() * 64 * 16; }
+  // Float index of the scale of step s, lane l, block b.
+  __host__ __device__ size_t scale_at(int b, int s, int l) const {
+    return ((size_t(b) * quads() + (s >> 2)) * 64 + l) * 4 + (s & 3);
+  }
   __host__ __device__ size_t bytes() const { return nib_bytes() + scale_bytes(); }
 };
 

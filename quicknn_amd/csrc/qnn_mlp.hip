@@ -33,7 +33,8 @@
 namespace qnn {
 namespace {
 
-constexpr int kNibStep = 1024, kSclStep = 256;  // bytes of one wave step
+constexpr int kNibStep = 1024;   // nibble bytes of one wave step
+constexpr int kSclPiece = 1024;  // scale bytes of one wave's 4-step piece
 
 template <int GG, int GD>
 __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
@@ -42,10 +43,11 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   const int wave = dev::wave_id(), tid = threadIdx.x, lane = tid & 63, part = wave;
   const int wg = blockIdx.x;
   uint8_t *lds = reinterpret_cast<uint8_t *>(dyn_lds);
-  uint8_t *dn_nib = lds + size_t(part) * GD * kNibStep;                              // this wave's down nibbles
-  uint8_t *dn_scl = lds + size_t(4) * GD * kNibStep + size_t(part) * GD * kSclStep;  // and scales
+  constexpr int QD = dev::scale_quads<GD>();
+  uint8_t *dn_nib = lds + size_t(part) * GD * kNibStep;                               // this wave's down nibbles
+  uint8_t *dn_scl = lds + size_t(4) * GD * kNibStep + size_t(part) * QD * kSclPiece;  // and scale pieces
   constexpr int XG = 4 * (GG > GD ? GG : GD);
-  const dev::XPlanes xs = dev::xplanes_at(lds + size_t(4) * GD * (kNibStep + kSclStep), 1, XG);
+  const dev::XPlanes xs = dev::xplanes_at(lds + size_t(4) * (GD * kNibStep + QD * kSclPiece), 1, XG);
   const I4Layout &lg = a.lg, &ld = a.ld;
   const int local = a.xcd_local;
 
@@ -81,12 +83,14 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   if (dn_on) {
     const dev::Rsrc dnib = dev::rsrc(a.dnib, ld.nib_bytes()), dscl = dev::rsrc(a.dscl, ld.scale_bytes());
     const uint32_t at = uint32_t((size_t(td) * ld.steps + s0d) * 64 + lane);
+    const uint32_t qat = uint32_t((size_t(td) * ld.quads() + (s0d >> 2)) * 64 + lane);
     typedef __attribute__((address_space(3))) void lds_t;
 #pragma unroll
-    for (int g = 0; g < GD; ++g) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dscl, (lds_t *)(dn_scl + g * kSclStep), 4, at * 4u, g * 256u, 0, 0);
+    for (int i = 0; i < QD; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dscl, (lds_t *)(dn_scl + i * kSclPiece), 16, qat * 16u, i * 1024u, 0, 0);
+#pragma unroll
+    for (int g = 0; g < GD; ++g)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(dnib, (lds_t *)(dn_nib + g * kNibStep), 16, at * 16u, g * 1024u, 0, 0);
-    }
   }
 
   // ---- 2) Gate/up item: stage x, integer dot, parts in LDS, split-K exchange;
@@ -153,11 +157,12 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   __syncthreads();
   uint4 wd[GD];
   float scd[GD];
+  uint4 qd[QD];
 #pragma unroll
-  for (int g = 0; g < GD; ++g) {
-    wd[g] = *reinterpret_cast<const uint4 *>(dn_nib + g * kNibStep + lane * 16);
-    scd[g] = *reinterpret_cast<const float *>(dn_scl + g * kSclStep + lane * 4);
-  }
+  for (int i = 0; i < QD; ++i) qd[i] = *reinterpret_cast<const uint4 *>(dn_scl + i * kSclPiece + lane * 16);
+#pragma unroll
+  for (int g = 0; g < GD; ++g) wd[g] = *reinterpret_cast<const uint4 *>(dn_nib + g * kNibStep + lane * 16);
+  dev::pick_scales<GD>(scd, qd, s0d);
   acc[0] = 0.0f;
   if (nsd > 0) {
     dev::XPlanes xp = xs;
@@ -214,7 +219,8 @@ int capacity_of(int device) {
 }  // namespace
 
 size_t mlp_lds_bytes(int gg, int gd) {
-  return size_t(4) * gd * (kNibStep + kSclStep) + dev::xplanes_bytes(1, 4 * std::max(gg, gd));
+  const int qd = gd >= 4 ? gd / 4 : 1;
+  return size_t(4) * (gd * kNibStep + qd * kSclPiece) + dev::xplanes_bytes(1, 4 * std::max(gg, gd));
 }
 
 int mlp_capacity(int gg, int gd, int device) {
