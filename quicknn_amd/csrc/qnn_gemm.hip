@@ -14,14 +14,19 @@
 // fp16 keeps 11 significant bits: the normwise error at the cfg5 shape is
 // ~3e-4 (an int8 activation pass would give ~5e-3, bf16 ~2e-3).
 //
-// Tiling.  A workgroup computes 256 x 96 of C with 4 waves of 64 x 96
-// (2 x 3 MFMA tiles of 32 x 32).  A is prepared once per call in MFMA
+// Tiling.  A workgroup computes (128 * MB) x 96 of C with 4 waves of
+// (32 * MB) x 96 (MB x 3 MFMA tiles of 32 x 32); MB = 1 keeps at least two
+// workgroups per CU at the prefill shapes.  A is prepared once per call in MFMA
 // fragment order (1 KiB per 32 rows x 16 k, one 16-byte piece per lane), so a
 // wave loads its A fragments straight from L2 with fully coalesced 16-byte
 // loads.  The 96 weight rows of a K-step are decoded once per workgroup into a
 // double-buffered LDS tile (fp16, rows padded by 16 bytes: conflict-free
-// ds_read_b128) that all four waves read.  Both M-tiles of an N-tile run on
-// one XCD, so the weight bytes are fetched from HBM once.
+// ds_read_b128) that all four waves read.  All M-tiles of an N-tile run on
+// one XCD, so the weight bytes are fetched from HBM once.  Loads run three
+// K-tiles deep (registers), since one K-tile of MFMA work is shorter than a
+// load's latency under load.
+#include <type_traits>
+
 #include "qnn_internal.h"
 
 namespace qnn {
@@ -30,7 +35,8 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256, BN = 96, BK = 64, LDB = BK + 8;  // LDB: halfs per LDS weight row
+constexpr int BN = 96, BK = 64, LDB = BK + 8;  // LDB: halfs per LDS weight row
+// Workgroup tile: 4 waves x MB 32-row blocks of C (BM = 128 * MB rows) by BN columns.
 
 __device__ __forceinline__ float half_bits_to_f(uint32_t h) {
   const uint16_t b = uint16_t(h);
@@ -54,18 +60,28 @@ __device__ __forceinline__ int range_exp(float amax) {
 }
 
 // ---- activation preparation ------------------------------------------------
-// One wave per row: ea[m] from max |A[m][.]|.
+// One workgroup per row: ea[m] from max |A[m][.]| (float4 loads, LDS reduction).
 __global__ __launch_bounds__(256) void k_act_rowexp(const float *__restrict__ a, int M, int K, int m_pad,
                                                     int *__restrict__ ea) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= m_pad) return;
+  __shared__ float red[4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   float amax = 0.0f;
   if (row < M) {
     const float *r = a + size_t(row) * K;
-    for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(r[k]));
+    if ((K & 3) == 0) {
+      const float4 *r4 = reinterpret_cast<const float4 *>(r);
+      for (int k = tid; k < K / 4; k += 256) {
+        const float4 v = r4[k];
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+      }
+    } else {
+      for (int k = tid; k < K; k += 256) amax = fmaxf(amax, fabsf(r[k]));
+    }
   }
   for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if (lane == 0) ea[row] = range_exp(amax);
+  if (lane == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  if (tid == 0) ea[row] = range_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
 }
 
 // Fragment order for v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane)
@@ -167,7 +183,9 @@ __device__ __forceinline__ void store_b(_Float16 (*bs)[LDB], const BRaw &b, floa
   for (int j = 0; j < 4; ++j) dst[j] = make_uint4(hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]);
 }
 
+template <int MB>
 __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
+  constexpr int BM = 128 * MB;
   const int b = blockIdx.x;
   // XCD-aware: the M-tiles of one N-tile share an XCD (workgroup b runs on XCD b % 8).
   const int xcd = b & 7, kq = b >> 3;
@@ -183,41 +201,45 @@ __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
     const int e = n < g.l.tiles * 64 ? reinterpret_cast<const int *>(g.w + g.l.rowexp_off)[n] : 0;
     wscale[tid] = ldexpf(1.0f, -e);
   }
-  const int m32 = (mtile * BM + wave * 64) >> 5;  // first 32-row block of this wave
-  const uint4 *ap0 = g.afrag + (size_t(m32) * g.ksteps) * 64 + lane;
-  const uint4 *ap1 = g.afrag + (size_t(m32 + 1) * g.ksteps) * 64 + lane;
-
-  f32x16 acc[2][3];
+  const int m32 = (mtile * BM + wave * 32 * MB) >> 5;  // first 32-row block of this wave
+  const uint4 *ap[MB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int mb = 0; mb < MB; ++mb) ap[mb] = g.afrag + (size_t(m32 + mb) * g.ksteps) * 64 + lane;
+
+  f32x16 acc[MB][3];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < 3; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  BRaw braw;
-  uint4 a[2][4], an[2][4];
-  load_b(braw, g, ntile, 0, tid);
+  // Software pipeline: the raw weights and the A fragments of K-tile kt + 2
+  // are requested while K-tile kt runs on the MFMAs and kt + 1 is decoded into
+  // the other LDS buffer, so each load has two K-tiles of work (~0.6 us) to
+  // arrive in.  Stages live in registers, indexed statically (kt % 3).
+  constexpr int D = 3;
+  BRaw braw[D];
+  uint4 a[D][MB][4];
+  auto load_stage = [&](auto S_, int kt) {
+    constexpr int S = decltype(S_)::value;
+    load_b(braw[S], g, ntile, kt, tid);
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    a[0][ks] = ap0[ks * 64];
-    a[1][ks] = ap1[ks * 64];
-  }
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) a[S][mb][ks] = ap[mb][(kt * 4 + ks) * 64];
+  };
+  load_stage(std::integral_constant<int, 0>(), 0);
+  if (g.ktiles > 1) load_stage(std::integral_constant<int, 1>(), 1);
   __syncthreads();  // wscale
-  store_b(bs[0], braw, tid < 2 * BN ? wscale[tid >> 1] : 0.0f, tid);
+  store_b(bs[0], braw[0], tid < 2 * BN ? wscale[tid >> 1] : 0.0f, tid);
   __syncthreads();
 
-  for (int kt = 0; kt < g.ktiles; ++kt) {
+  auto iter = [&](auto S_, int kt) {
+    constexpr int S = decltype(S_)::value;
+    constexpr int S1 = (S + 1) % D, S2 = (S + 2) % D;
     const int buf = kt & 1;
-    const bool more = kt + 1 < g.ktiles;
-    if (more) {
-      load_b(braw, g, ntile, kt + 1, tid);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        an[0][ks] = ap0[((kt + 1) * 4 + ks) * 64];
-        an[1][ks] = ap1[((kt + 1) * 4 + ks) * 64];
-      }
-    }
+    if (kt + 2 < g.ktiles) load_stage(std::integral_constant<int, S2>(), kt + 2);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       half8 bf[3];
@@ -227,22 +249,20 @@ __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
         __builtin_memcpy(&bf[nb], &v, 16);
       }
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         half8 af;
-        __builtin_memcpy(&af, &a[mb][ks], 16);
+        __builtin_memcpy(&af, &a[S][mb][ks], 16);
 #pragma unroll
         for (int nb = 0; nb < 3; ++nb) acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);
       }
     }
-    if (more) {
-      store_b(bs[buf ^ 1], braw, tid < 2 * BN ? wscale[tid >> 1] : 0.0f, tid);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        a[0][ks] = an[0][ks];
-        a[1][ks] = an[1][ks];
-      }
-    }
+    if (kt + 1 < g.ktiles) store_b(bs[buf ^ 1], braw[S1], tid < 2 * BN ? wscale[tid >> 1] : 0.0f, tid);
     __syncthreads();
+  };
+  for (int kt = 0; kt < g.ktiles; kt += D) {
+    iter(std::integral_constant<int, 0>(), kt);
+    if (kt + 1 < g.ktiles) iter(std::integral_constant<int, 1>(), kt + 1);
+    if (kt + 2 < g.ktiles) iter(std::integral_constant<int, 2>(), kt + 2);
   }
 
   // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32x32 tile.
@@ -252,10 +272,10 @@ __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
     if (col >= g.N) continue;
     const int ew = reinterpret_cast<const int *>(g.w + g.l.rowexp_off)[col];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int row = mtile * BM + wave * 64 + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const int row = mtile * BM + wave * 32 * MB + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
         if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], g.ea[row] + ew);
       }
     }
@@ -272,6 +292,11 @@ void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s) {
 
 Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
   Q8GemmPlan p;
+  // Two 32-row blocks per wave once the grid has >= 2 workgroups per CU anyway.
+  const int ntiles = (N + BN - 1) / BN;
+  p.mb = env_int("QNN_GEMM_MB", 0);
+  if (p.mb != 1 && p.mb != 2) p.mb = size_t((M + 255) / 256) * ntiles >= 512 ? 2 : 1;
+  const int BM = 128 * p.mb;
   p.m_pad = (M + BM - 1) / BM * BM;
   p.k_pad = (K + BK - 1) / BK * BK;
   p.ksteps = p.k_pad / 16;
@@ -284,7 +309,7 @@ Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
 
 void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
                     void *frag, int *ea, float *c, hipStream_t s) {
-  hipLaunchKernelGGL(k_act_rowexp, dim3(p.m_pad / 4), dim3(256), 0, s, a, M, K, p.m_pad, ea);
+  hipLaunchKernelGGL(k_act_rowexp, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.m_pad, ea);
   const size_t pieces = size_t(p.m_pad / 32) * p.ksteps * 64;
   hipLaunchKernelGGL(k_act_frag, dim3((pieces + 255) / 256), dim3(256), 0, s, a, ea, M, K, p.ksteps, pieces,
                      static_cast<uint4 *>(frag));
@@ -301,7 +326,8 @@ void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, co
   g.mtiles = p.mtiles;
   g.ntiles = p.ntiles;
   const int grid = (p.ntiles + 7) / 8 * 8 * p.mtiles;
-  hipLaunchKernelGGL(k_q8_gemm, dim3(grid), dim3(256), 0, s, g);
+  if (p.mb == 2) hipLaunchKernelGGL(k_q8_gemm<2>, dim3(grid), dim3(256), 0, s, g);
+  else hipLaunchKernelGGL(k_q8_gemm<1>, dim3(grid), dim3(256), 0, s, g);
   hip_check(hipGetLastError(), "q8 gemm launch");
 }
 
