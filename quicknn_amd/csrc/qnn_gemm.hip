@@ -150,20 +150,31 @@ struct BRaw {
   uint32_t d;
 };
 
-__device__ __forceinline__ void load_b(BRaw &b, const GemmArgs &g, int ntile, int kt, int tid) {
-  b.q0 = make_uint4(0u, 0u, 0u, 0u);
-  b.q1 = b.q0;
-  b.d = 0u;
-  if (tid >= 2 * BN) return;
+// Buffer loads without branches, so the compiler can count them across the
+// software pipeline: threads past the 96 rows and blocks past the matrix read
+// at an offset beyond the buffer, which returns zeros.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc rsrc(const void *base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(uint32_t(min(bytes, size_t(0xFFFFFFFFu)))),
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 ld128(Rsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+constexpr uint32_t kOutside = 0xFFFFFFF0u;
+
+__device__ __forceinline__ void load_b(BRaw &b, const GemmArgs &g, Rsrc wr, int ntile, int kt, int tid) {
   const int n = ntile * BN + (tid >> 1);
   const int kb = kt * 2 + (tid & 1);  // 32-element block
-  if (n >= g.l.tiles * 64 || kb >= g.l.units * 8) return;
+  const bool in = tid < 2 * BN && n < g.l.tiles * 64 && kb < g.l.units * 8;
   const int t = n >> 6, r = n & 63, u = kb >> 3, k8 = kb & 7;
   const size_t tu = size_t(t) * g.l.units + u;
-  const uint4 *mp = reinterpret_cast<const uint4 *>(g.w) + (tu * 16 + 2 * k8) * 64 + r;
-  b.q0 = mp[0];
-  b.q1 = mp[64];
-  b.d = *reinterpret_cast<const uint16_t *>(g.w + g.l.side1_off + (tu * 64 + r) * 16 + 2 * k8);
+  const uint32_t qoff = in ? uint32_t(((tu * 16 + 2 * k8) * 64 + r) * 16) : kOutside;
+  const uint32_t doff = in ? uint32_t(g.l.side1_off + (tu * 64 + r) * 16 + 2 * k8) : kOutside;
+  b.q0 = ld128(wr, qoff);
+  b.q1 = ld128(wr, qoff + (qoff == kOutside ? 0u : 1024u));
+  b.d = __builtin_amdgcn_raw_buffer_load_b16(wr, int(doff), 0, 0);
 }
 
 __device__ __forceinline__ void store_b(_Float16 (*bs)[LDB], const BRaw &b, float scale, int tid) {
@@ -202,9 +213,13 @@ __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
     wscale[tid] = ldexpf(1.0f, -e);
   }
   const int m32 = (mtile * BM + wave * 32 * MB) >> 5;  // first 32-row block of this wave
-  const uint4 *ap[MB];
+  // A fragments: piece (m32 + mb, ks) of this lane at byte ((m32 + mb) * ksteps + ks) * 1024 + lane * 16;
+  // pieces past the last K-step read zeros.
+  const Rsrc ar = rsrc(g.afrag, size_t(g.mtiles) * MB * 4 * g.ksteps * 1024);
+  const Rsrc wr = rsrc(g.w, g.l.total);
+  uint32_t aoff[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) ap[mb] = g.afrag + (size_t(m32 + mb) * g.ksteps) * 64 + lane;
+  for (int mb = 0; mb < MB; ++mb) aoff[mb] = uint32_t((size_t(m32 + mb) * g.ksteps) * 1024 + lane * 16);
 
   f32x16 acc[MB][3];
 #pragma unroll
@@ -223,14 +238,17 @@ __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
   uint4 a[D][MB][4];
   auto load_stage = [&](auto S_, int kt) {
     constexpr int S = decltype(S_)::value;
-    load_b(braw[S], g, ntile, kt, tid);
+    load_b(braw[S], g, wr, ntile, kt, tid);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) a[S][mb][ks] = ap[mb][(kt * 4 + ks) * 64];
+      for (int mb = 0; mb < MB; ++mb) {
+        const int kk = kt * 4 + ks;
+        a[S][mb][ks] = ld128(ar, kk < g.ksteps ? aoff[mb] + uint32_t(kk) * 1024u : kOutside);
+      }
   };
   load_stage(std::integral_constant<int, 0>(), 0);
-  if (g.ktiles > 1) load_stage(std::integral_constant<int, 1>(), 1);
+  load_stage(std::integral_constant<int, 1>(), 1);
   __syncthreads();  // wscale
   store_b(bs[0], braw[0], tid < 2 * BN ? wscale[tid >> 1] : 0.0f, tid);
   __syncthreads();
@@ -239,7 +257,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
     constexpr int S = decltype(S_)::value;
     constexpr int S1 = (S + 1) % D, S2 = (S + 2) % D;
     const int buf = kt & 1;
-    if (kt + 2 < g.ktiles) load_stage(std::integral_constant<int, S2>(), kt + 2);
+    load_stage(std::integral_constant<int, S2>(), kt + 2);  // past the end: zeros, unused
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       half8 bf[3];
@@ -295,7 +313,7 @@ Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
   // Two 32-row blocks per wave once the grid has >= 2 workgroups per CU anyway.
   const int ntiles = (N + BN - 1) / BN;
   p.mb = env_int("QNN_GEMM_MB", 0);
-  if (p.mb != 1 && p.mb != 2) p.mb = size_t((M + 255) / 256) * ntiles >= 512 ? 2 : 1;
+  if (p.mb != 1 && p.mb != 2) p.mb = M >= 256 ? 2 : 1;
   const int BM = 128 * p.mb;
   p.m_pad = (M + BM - 1) / BM * BM;
   p.k_pad = (K + BK - 1) / BK * BK;
