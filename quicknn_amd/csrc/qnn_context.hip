@@ -1282,7 +1282,7 @@ int qnn_expert_set_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight
       const size_t src_max = std::max(size_t(inter) * rbh, size_t(hidden) * rbi);
       for (int e = 0; e < experts; ++e) {
         const qnn_weight *ws[3] = {&gate[e], &up[e], &down[e]};
-        uint8_t *dst[3] = {base + size_t(e) * gub, base + size_t(experts + e) * gub,
+        uint8_t *dst[3] = {base + size_t(2 * e) * gub, base + size_t(2 * e + 1) * gub,
                            base + size_t(2 * experts) * gub + size_t(e) * dnb};
         for (int j = 0; j < 3; ++j) {
           const I4Layout &l = j < 2 ? set->gu : set->dn;
@@ -1336,8 +1336,7 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     const uint8_t *base = static_cast<const uint8_t *>(set->mem);
     a.gu_stride = set->gu.bytes();
     a.dn_stride = set->dn.bytes();
-    a.gate = base;
-    a.up = base + size_t(set->experts) * a.gu_stride;
+    a.gate_up = base;
     a.down = base + size_t(2 * set->experts) * a.gu_stride;
     a.gu = set->gu;
     a.dn = set->dn;

@@ -144,16 +144,19 @@ __device__ __forceinline__ void pick_scales(float (&sc)[GSW], const uint4 (&q)[s
     for (int g = 0; g < GSW; ++g) sc[g] = __uint_as_float(sel4u(q[0], (o + g) & 3));
   }
 }
+// nib_off / scl_off: per-lane byte offsets of the lane's matrix within the
+// resources (lets lanes of one wave read two matrices through one uniform
+// resource instead of a divergent one).
 template <int GSW>
 __device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc nib, Rsrc scl, const I4Layout &l, int b,
-                                       int s0, int wl) {
+                                       int s0, int wl, uint32_t nib_off = 0, uint32_t scl_off = 0) {
   const uint32_t at = uint32_t((size_t(b) * l.steps + s0) * 64 + wl);
   const uint32_t qat = uint32_t((size_t(b) * l.quads() + (s0 >> 2)) * 64 + wl);
   uint4 q[scale_quads<GSW>()];
 #pragma unroll
-  for (int i = 0; i < scale_quads<GSW>(); ++i) q[i] = ld128(scl, qat * 16u, uint32_t(i) * 1024u);
+  for (int i = 0; i < scale_quads<GSW>(); ++i) q[i] = ld128(scl, scl_off + qat * 16u, uint32_t(i) * 1024u);
 #pragma unroll
-  for (int g = 0; g < GSW; ++g) w[g] = ld128(nib, at * 16u, uint32_t(g) * 1024u);
+  for (int g = 0; g < GSW; ++g) w[g] = ld128(nib, nib_off + at * 16u, uint32_t(g) * 1024u);
   pick_scales<GSW>(sc, q, s0);
 }
 

@@ -184,7 +184,8 @@ int mlp_capacity(int gg, int gd, int device);  // co-resident workgroups (0: var
 bool mlp_launch(const MlpLaunch &a, int gg, int gd, int grid, hipStream_t s);  // false: not launched
 
 struct MoELaunch {
-  const uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+  const uint8_t *gate_up = nullptr;  // expert e: gate at gate_up + 2e*gu_stride, its up matrix gu_stride after it
+  const uint8_t *down = nullptr;     // expert e: down + e*dn_stride
   size_t gu_stride = 0, dn_stride = 0;  // bytes per expert matrix
   I4Layout gu, dn;                      // gate/up [inter, hidden]; down [hidden, inter]
   int experts = 0, hidden = 0, inter = 0, topk = 0, rows = 0;

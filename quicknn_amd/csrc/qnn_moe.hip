@@ -143,15 +143,22 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   const int sgroups = min(4 * sps * L, l.groups - ws0 * L);
   const int kin = DOWN ? a.inter : a.hidden;  // both multiples of 4 (checked by the host)
 
-  // weights of expert e: one contiguous matrix per expert
+  // weights of expert e: one contiguous matrix per expert; gate/up lanes
+  // 32-63 read the up matrix, which follows the gate matrix, through the same
+  // (workgroup-uniform) resources at a per-lane offset
   int b = tile, wl = lane;
   const uint8_t *wbase;
+  size_t wbytes;
+  uint32_t moff = 0;
   if (DOWN) {
     wbase = a.down + size_t(e) * a.dn_stride;
+    wbytes = a.dn_stride;
   } else {
     b = tile >> 1;
     wl = (tile & 1) * 32 + (lane & 31);
-    wbase = (lane < 32 ? a.gate : a.up) + size_t(e) * a.gu_stride;
+    wbase = a.gate_up + size_t(2 * e) * a.gu_stride;
+    wbytes = 2 * a.gu_stride;
+    moff = lane < 32 ? 0u : uint32_t(a.gu_stride);
   }
   // activation rows: h[R] (down) or x[token of R] (gate/up)
   const dev::Rsrc xsrc = DOWN ? dev::rsrc(a.h, size_t(n) * a.inter * 4) : dev::rsrc(a.x, size_t(a.rows) * a.hidden * 4);
@@ -163,8 +170,8 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   dev::load_x<MT, GSW>(xr, xsrc, xoff, min(c, MT), ws0 * L * 32, sgroups * 32, tid);
   uint4 w[GSW];
   float sc[GSW];
-  dev::load_w<GSW>(w, sc, dev::rsrc(wbase, l.nib_bytes()), dev::rsrc(wbase + l.nib_bytes(), l.scale_bytes()), l, b, s0,
-                   wl);
+  dev::load_w<GSW>(w, sc, dev::rsrc(wbase, wbytes), dev::rsrc(wbase + l.nib_bytes(), wbytes - l.nib_bytes()), l, b, s0,
+                   wl, moff, moff);
 
   const dev::XPlanes xs = dev::xplanes_at(dyn_lds, MT, 4 * sps * L);
   dev::XPlanes xw = xs;  // this wave's groups
