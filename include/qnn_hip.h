@@ -95,6 +95,7 @@ typedef struct {
   uint64_t weight_bytes, weight_limit, activation_bytes, activation_peak_bytes;
   uint64_t mlp_fused;      /* TrySwiGLUVector + Int4Linear pairs run as one launch (no reference counterpart) */
   uint64_t linear_grouped; /* one-row GGUF Linear calls that ran in a shared launch (no reference counterpart) */
+  uint64_t moe_fused;      /* one-token qnn_moe_experts calls run as a single launch (no reference counterpart) */
 } qnn_status;
 
 /* ---------------------------------------------------------------------------
@@ -203,7 +204,9 @@ int qnn_expert_set_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight
 int qnn_expert_set_destroy(qnn_ctx *ctx, qnn_expert_set *set);
 /* routes: output of GO_MOE_ROUTE ([rows*topk ids][rows*topk probabilities]).
  * dst[r] = sum over the token's routed experts in ascending id of
- *          p * down(silu(gate x_r) * (up x_r)). */
+ *          p * down(silu(gate x_r) * (up x_r)).
+ * One token (rows = 1) runs as a single launch outside graph capture
+ * (QNN_FUSE_MOE=0 keeps the two-launch path); results are identical. */
 int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tensor *src, qnn_tensor *routes,
                     int rows, int topk);
 

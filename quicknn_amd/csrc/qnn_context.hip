@@ -81,6 +81,7 @@ struct qnn_ctx_s {
   size_t mlp_flag_bytes = 0;
   unsigned mlp_epoch = 0;
   int mlp_cap[9][9] = {};
+  int moe_cap[9] = {};  // co-resident workgroups of the one-token MoE kernel per steps variant
   // GGUF one-row Linear calls recorded for one grouped launch: consecutive
   // calls on the same input (a layer's q/k/v or gate/up projections) with the
   // same encoding and plan width, at most kGGMaxGroup, distinct outputs.
@@ -96,7 +97,7 @@ struct qnn_ctx_s {
   std::vector<qnn::WeightEntry *> capture_pins;
   std::vector<qnn::GraphRec> graphs;
   std::vector<qnn_expert_set_s *> sets;
-  bool xcd_local = false;  // workgroup b runs on XCD b % 8 (probed at creation)
+  bool xcd_local = false;  // the device dealt workgroup b to XCD b % 8 when probed at creation
   qnn_status st{};
   uint64_t act_bytes = 0;
 };
@@ -149,10 +150,11 @@ void sync(qnn_ctx_s *ctx) {
   ctx->st.submissions++;
 }
 
-// XCD-local split-K exchange only for direct launches: kernels replayed from a
-// HIP graph are not dealt to XCDs in the probed blockIdx % 8 order, so captured
-// kernels exchange partial sums through device-coherent accesses.
-int xcd_local_launch(const qnn_ctx_s *ctx) { return ctx->xcd_local && !ctx->capturing ? 1 : 0; }
+// Split-K combines may read through the XCD's L2 when the workgroups ran where
+// the tile map intended; each kernel checks that per workgroup at run time
+// (qnn_exchange.h), since other GPU work in the process (and graph replays)
+// can change the dealing order that the creation-time probe saw.
+int xcd_local_launch(const qnn_ctx_s *ctx) { return ctx->xcd_local ? 1 : 0; }
 
 // Flush releases the pins a synchronous preload took (Context.Implementation.inc:411-415).
 void release_flush_pins(qnn_ctx_s *ctx) {
@@ -564,6 +566,25 @@ void settle_pending(qnn_ctx_s *ctx) {
 
 bool mlp_fusion_enabled() { return env_int("QNN_FUSE_MLP", 1) != 0; }
 
+// Completion flags of the single-launch kernels (fused MLP, one-token MoE):
+// words 256 B apart that hold the epoch of the launch that last completed the
+// block; zeroed when allocated, and epoch 0 is never a launch's.
+void ensure_flags(qnn_ctx_s *ctx, size_t bytes) {
+  if (bytes <= ctx->mlp_flag_bytes) return;
+  sync(ctx);
+  if (ctx->mlp_flags) (void)hipFree(ctx->mlp_flags);
+  ctx->mlp_flags = nullptr;
+  ctx->mlp_flag_bytes = 0;
+  hip_check(hipMalloc(&ctx->mlp_flags, bytes), "completion flags");
+  hip_check(hipMemsetAsync(ctx->mlp_flags, 0, bytes, ctx->stream), "completion flags");
+  hip_check(hipStreamSynchronize(ctx->stream), "completion flags");
+  ctx->mlp_flag_bytes = bytes;
+}
+unsigned next_epoch(qnn_ctx_s *ctx) {
+  if (++ctx->mlp_epoch == 0) ctx->mlp_epoch = 1;
+  return ctx->mlp_epoch;
+}
+
 // Launches the recorded SwiGLU and the down projection `d` (h -> y) as one
 // kernel when the per-op plans allow it; false leaves the pending
 // SwiGLU recorded.
@@ -580,17 +601,7 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
   const size_t pf_gu = size_t(2 * lg.blocks) * pg.slices * 64, pf_dn = size_t(ld.blocks) * pd.slices * 64;
   const size_t c_gu = size_t(lg.blocks) * kCounterStride, c_dn = size_t(ld.blocks) * kCounterStride;
   ensure_splitk(ctx, pf_gu + pf_dn, c_gu + c_dn);
-  const size_t flag_bytes = size_t(lg.blocks) * 256;
-  if (flag_bytes > ctx->mlp_flag_bytes) {  // zeroed: epoch 0 is never a launch
-    sync(ctx);
-    if (ctx->mlp_flags) (void)hipFree(ctx->mlp_flags);
-    ctx->mlp_flags = nullptr;
-    ctx->mlp_flag_bytes = 0;
-    hip_check(hipMalloc(&ctx->mlp_flags, flag_bytes), "fused MLP flags");
-    hip_check(hipMemsetAsync(ctx->mlp_flags, 0, flag_bytes, ctx->stream), "fused MLP flags");
-    hip_check(hipStreamSynchronize(ctx->stream), "fused MLP flags");
-    ctx->mlp_flag_bytes = flag_bytes;
-  }
+  ensure_flags(ctx, size_t(lg.blocks) * 256);
   MlpLaunch a;
   a.lg = lg;
   a.ld = ld;
@@ -615,8 +626,7 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
   a.counters_gu = ctx->counters;
   a.counters_dn = ctx->counters + c_gu;
   a.flags = static_cast<unsigned *>(ctx->mlp_flags);
-  if (++ctx->mlp_epoch == 0) ctx->mlp_epoch = 1;
-  a.epoch = ctx->mlp_epoch;
+  a.epoch = next_epoch(ctx);
   a.xcd_local = xcd_local_launch(ctx);
   a.err = ctx->error_flag;
   if (!mlp_launch(a, pg.gsw, pd.gsw, grid, ctx->stream)) return false;
@@ -840,8 +850,7 @@ int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count) {
     if (flag) {
       hip_check(hipMemsetAsync(ctx->error_flag, 0, 4, ctx->stream), "error word reset");
       sync(ctx);
-      if (flag & 2) fail(QNN_E_INVALID_OP, "fused MLP: the wait for the gate/up output timed out");
-      if (flag & 4) fail(QNN_E_INVALID_OP, "workgroup placement differs from the probed XCD mapping");
+      if (flag & 2) fail(QNN_E_INVALID_OP, "single-launch MLP/MoE: the wait for the gate/up output timed out");
       if (flag & 8) fail(QNN_E_INVALID_OP, "Invalid GPU expert ID");  // LLM.MoE.pas:384-385
       if (flag & 16) fail(QNN_E_INVALID_OP, "MoE dispatch index outside its tensor");
       fail(QNN_E_INVALID_OP, "Resident GPU computation produced non-finite values");
@@ -1359,8 +1368,33 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     a.counters = ctx->counters;
     a.xcd_local = xcd_local_launch(ctx);
     a.err = ctx->error_flag;
-    moe_launch(a, p, ctx->stream);
     ctx->st.int4_calls += 3;
+    // One token: one launch (bit-identical to the two below) when every
+    // workgroup of its grid can be resident; not under capture, where the
+    // epoch baked into the launch would repeat on every replay.
+    if (rows == 1 && !ctx->capturing && env_int("QNN_FUSE_MOE", 1) != 0) {
+      const MoEDecodePlan d = moe_decode_plan(a, p);
+      if (d.ok) {
+        int &cap = ctx->moe_cap[p.gsw];
+        if (cap == 0) cap = std::max(-1, moe_decode_capacity(p, ctx->device));
+        if (cap > 0 && d.grid <= cap) {
+          ensure_splitk(ctx, d.partial_gu + d.partial_dn, d.counters_gu + d.counters_dn);
+          ensure_flags(ctx, d.flag_bytes);
+          a.partial = ctx->partial;
+          a.partial_dn = ctx->partial + d.partial_gu;
+          a.counters = ctx->counters;
+          a.counters_dn = ctx->counters + d.counters_gu;
+          a.flags = static_cast<unsigned *>(ctx->mlp_flags);
+          a.epoch = next_epoch(ctx);
+          if (moe_decode_launch(a, p, d, ctx->stream)) {
+            ctx->st.moe_fused++;
+            return QNN_OK;
+          }
+          hip_check(hipGetLastError(), "moe decode launch");
+        }
+      }
+    }
+    moe_launch(a, p, ctx->stream);
     return QNN_OK;
   });
 }

@@ -28,7 +28,7 @@
 //   Q3_K: sum = s2 * d*(sc-32) * (dot(q3, X) - 4 sum(X))        (q3 = q + 4)
 //   Q8_0: sum = s2 * d * dot(q, X)
 // where X = 256 q1 + q2 and every dot is exact integer arithmetic.
-#include "qnn_internal.h"
+#include "qnn_exchange.h"
 
 namespace qnn {
 namespace {
@@ -495,40 +495,15 @@ __global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   if (wave > 0) return;
   acc = ((acc + red[0][lane]) + red[1][lane]) + red[2][lane];
   if (slices > 1) {
-    float *part = a.partial + (size_t(tile) * slices + slice) * 64;
-    if (a.xcd_local) {
-      if (lane == 0 && int(__builtin_amdgcn_s_getreg((3 << 11) | 20)) != int(blockIdx.x & 7)) atomicOr(a.err, 4);
-      part[lane] = acc;
-    } else {
-      __hip_atomic_store(part + lane, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    unsigned ticket = 0;
-    if (lane == 0)
-      ticket = __hip_atomic_fetch_add(&a.counters[tile * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ticket = __shfl(ticket, 0);
-    if (ticket != unsigned(slices - 1)) return;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    dev::xstore(a.partial + (size_t(tile) * slices + slice) * 64 + lane, acc);
+    unsigned *ctr = &a.counters[size_t(tile) * kCounterStride];
+    bool l2 = false;
+    if (!dev::last_arrival(ctr, unsigned(slices), lane, a.xcd_local, l2)) return;
     const float *pt = a.partial + size_t(tile) * slices * 64 + lane;
-    acc = 0.0f;
-    for (int s0 = 0; s0 < slices; s0 += 16) {
-      float v[16];
-      if (a.xcd_local) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (s0 + j < slices) v[j] = pt[size_t(s0 + j) * 64];
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (s0 + j < slices) v[j] = __hip_atomic_load(pt + size_t(s0 + j) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (s0 + j < slices) acc += v[j];
-    }
-    if (lane == 0) __hip_atomic_store(&a.counters[tile * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float s[1];
+    dev::sum_slices<1, 16>(s, [&](int sl, int) { return pt + size_t(sl) * 64; }, slices, l2);
+    acc = s[0];
+    dev::reset_counter(ctr, lane);
   }
   // 6) epilogue
   if (a.mode >= GG_SWIGLU) {

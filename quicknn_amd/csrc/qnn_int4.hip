@@ -110,19 +110,19 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   float accu[MT];
   if (slices > 1 || swiglu) {
     float *part_p = a.partial + (size_t(tile) * slices + slice) * MT * 64 + lane;
-    dev::check_xcd(a.xcd_local, a.err, lane);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) dev::xstore(part_p + m * 64, acc[m], a.xcd_local);
+    for (int m = 0; m < MT; ++m) dev::xstore(part_p + m * 64, acc[m]);
     unsigned *ctr = &a.counters[size_t(swiglu ? tile >> 1 : tile) * kCounterStride];
-    if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane)) return;
+    bool l2 = false;
+    if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane, a.xcd_local, l2)) return;
     const int t0 = swiglu ? tile & ~1 : tile;
     const float *pt = a.partial + size_t(t0) * slices * MT * 64 + lane;
     dev::sum_slices<MT, PU>(
-        acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices, a.xcd_local);
+        acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices, l2);
     if (swiglu) {
       const float *pu = pt + size_t(slices) * MT * 64;
       dev::sum_slices<MT, PU>(
-          accu, [&](int s, int m) { return pu + (size_t(s) * MT + m) * 64; }, slices, a.xcd_local);
+          accu, [&](int s, int m) { return pu + (size_t(s) * MT + m) * 64; }, slices, l2);
     }
     dev::reset_counter(ctr, lane);
   }

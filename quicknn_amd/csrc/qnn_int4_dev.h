@@ -30,7 +30,7 @@
 // slice are skipped, on a uniform condition), so the compiler can wait for
 // the activation loads alone while the weight loads are still in flight.
 #pragma once
-#include "qnn_internal.h"
+#include "qnn_exchange.h"
 
 namespace qnn {
 namespace dev {
@@ -43,9 +43,6 @@ __device__ __forceinline__ float silu(float g) {
 __device__ __forceinline__ uint32_t sel4u(const uint4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
-
-// Hardware XCC id of the executing wave (HW_REG_XCC_ID, bits 3:0).
-__device__ __forceinline__ int xcc_id() { return int(__builtin_amdgcn_s_getreg((3 << 11) | 20)) & 15; }
 
 // Wave index as a scalar (uniform) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -147,16 +144,25 @@ __device__ __forceinline__ void pick_scales(float (&sc)[GSW], const uint4 (&q)[s
 // nib_off / scl_off: per-lane byte offsets of the lane's matrix within the
 // resources (lets lanes of one wave read two matrices through one uniform
 // resource instead of a divergent one).
+// load_wq issues the loads only; pick_scales(sc, q, s0) then selects the
+// scales (for GSW < 4 a data-dependent select that waits for the scale load,
+// so callers that issue more loads do so before it).
 template <int GSW>
-__device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc nib, Rsrc scl, const I4Layout &l, int b,
-                                       int s0, int wl, uint32_t nib_off = 0, uint32_t scl_off = 0) {
+__device__ __forceinline__ void load_wq(uint4 (&w)[GSW], uint4 (&q)[scale_quads<GSW>()], Rsrc nib, Rsrc scl,
+                                        const I4Layout &l, int b, int s0, int wl, uint32_t nib_off = 0,
+                                        uint32_t scl_off = 0) {
   const uint32_t at = uint32_t((size_t(b) * l.steps + s0) * 64 + wl);
   const uint32_t qat = uint32_t((size_t(b) * l.quads() + (s0 >> 2)) * 64 + wl);
-  uint4 q[scale_quads<GSW>()];
 #pragma unroll
   for (int i = 0; i < scale_quads<GSW>(); ++i) q[i] = ld128(scl, scl_off + qat * 16u, uint32_t(i) * 1024u);
 #pragma unroll
   for (int g = 0; g < GSW; ++g) w[g] = ld128(nib, nib_off + at * 16u, uint32_t(g) * 1024u);
+}
+template <int GSW>
+__device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc nib, Rsrc scl, const I4Layout &l, int b,
+                                       int s0, int wl, uint32_t nib_off = 0, uint32_t scl_off = 0) {
+  uint4 q[scale_quads<GSW>()];
+  load_wq<GSW>(w, q, nib, scl, l, b, s0, wl, nib_off, scl_off);
   pick_scales<GSW>(sc, q, s0);
 }
 
@@ -282,73 +288,6 @@ __device__ __forceinline__ void reduce_lanes(float (&acc)[MT], int lanes) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] += __shfl_xor(acc[m], o);
   }
-}
-
-// ---- split-K exchange between workgroups of one tile --------------------
-// With `local` set, every workgroup of the tile runs on one XCD and the data
-// meet in that XCD's L2 through plain stores/loads; otherwise they travel as
-// device-scope atomic stores/loads, which are coherent across XCDs by
-// themselves (a device-scope fence would write back and invalidate the whole
-// L2).  The writer waits for its stores to complete before taking a ticket.
-__device__ __forceinline__ void xstore(float *p, float v, int local) {
-  if (local) *p = v;
-  else __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float xload(const float *p, int local) {
-  return local ? *p : __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Placement check for the XCD-local exchange: a workgroup that does not run on
-// XCD (blockIdx % 8) reports it (error bit 4) instead of combining silently.
-__device__ __forceinline__ void check_xcd(int local, int *err, int lane) {
-  if (local && lane == 0 && xcc_id() != int(blockIdx.x & 7)) atomicOr(err, 4);
-}
-// Completes this wave's exchange stores, then takes a ticket; true (uniform)
-// for the last of `arrivals` arrivals, which then owns the combine and resets
-// the counter for the next launch.
-__device__ __forceinline__ bool last_arrival(unsigned *counter, unsigned arrivals, int lane) {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  unsigned ticket = 0;
-  if (lane == 0) ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  ticket = __shfl(ticket, 0);
-  if (ticket != arrivals - 1) return false;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  return true;
-}
-__device__ __forceinline__ void reset_counter(unsigned *counter, int lane) {
-  if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// acc[m] = sum over s in slice order of part(s, m); PU independent loads per
-// token in flight.
-template <int MT, int PU, class AddrF>
-__device__ __forceinline__ void sum_slices(float (&acc)[MT], AddrF part, int slices, int local) {
-#pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-  for (int s0 = 0; s0 < slices; s0 += PU) {
-    float v[PU][MT];
-#pragma unroll
-    for (int j = 0; j < PU; ++j)
-      if (s0 + j < slices)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) v[j][m] = xload(part(s0 + j, m), local);
-#pragma unroll
-    for (int j = 0; j < PU; ++j)
-      if (s0 + j < slices)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] += v[j][m];
-  }
-}
-
-// blockIdx -> (unit, rest): every workgroup of a unit goes to the same XCD
-// (workgroups are dealt round-robin over the 8 XCDs), so the split-K partial
-// sums of a unit stay in one L2.  `per` = workgroups per unit.
-__device__ __forceinline__ bool map_tile(int b, int per, int units, int &unit, int &rest) {
-  const int xcd = b & 7, k = b >> 3;
-  const int q = k / per;
-  unit = q * 8 + xcd;
-  rest = k - q * per;
-  return unit < units;
 }
 
 }  // namespace dev

@@ -122,8 +122,8 @@ struct I4Launch {
   const float *prob = nullptr;  // I4_ACCUM: pointer to p
   float *partial = nullptr;     // split-K scratch
   unsigned *counters = nullptr;
-  int xcd_local = 0;            // combine slices through the XCD's L2 (placement verified)
-  int *err = nullptr;           // error word (bit 4: unexpected XCD placement)
+  int xcd_local = 0;            // combine slices through the XCD's L2 where placement allows (qnn_exchange.h)
+  int *err = nullptr;           // error word
 };
 struct I4Plan {
   int mt = 1, gsw = 1, slices = 1, grid = 0, steps_per_slice = 1, tiles_per_wg = 1;
@@ -176,8 +176,8 @@ struct MlpLaunch {
   unsigned *counters_gu = nullptr, *counters_dn = nullptr;
   unsigned *flags = nullptr;  // per 64-row block of h, 256 B apart: epoch of the launch that completed it
   unsigned epoch = 0;         // this launch's number (never 0)
-  int xcd_local = 0;          // split-K partial sums through the XCD's L2 (placement checked)
-  int *err = nullptr;         // bit 2: a wait for h timed out; bit 4: unexpected XCD placement
+  int xcd_local = 0;          // split-K partial sums through the XCD's L2 where placement allows (qnn_exchange.h)
+  int *err = nullptr;         // bit 2: a wait for h timed out
 };
 size_t mlp_lds_bytes(int gg, int gd);
 int mlp_capacity(int gg, int gd, int device);  // co-resident workgroups (0: variant not built)
@@ -197,13 +197,27 @@ struct MoELaunch {
   float *partial = nullptr;
   unsigned *counters = nullptr;
   int xcd_local = 0;
-  int *err = nullptr;  // bit 8: invalid route ids
+  int *err = nullptr;  // bit 8: invalid route ids; bit 2: a fused-launch wait for h timed out
+  // single-launch decode path (one token) only:
+  float *partial_dn = nullptr;
+  unsigned *counters_dn = nullptr;
+  unsigned *flags = nullptr;  // per (slot, 64-row block of h), 256 B apart: epoch of the launch that completed it
+  unsigned epoch = 0;
 };
 struct MoEPlanSizes {
   int slots = 0, mt = 1, gsw = 4, slices_gu = 1, slices_dn = 1, sps_gu = 1, sps_dn = 1;
   size_t lds_gu = 0, lds_dn = 0;  // dynamic LDS per launch
   size_t partial_floats = 0, counters = 0;
 };
+// One-token MoE as a single launch: sizes of its workspace and grid.
+struct MoEDecodePlan {
+  bool ok = false;  // shape and plan allow the single launch
+  int grid = 0, grid_dn = 0, units_gu = 0, bpad_dn = 0;
+  size_t partial_gu = 0, partial_dn = 0, counters_gu = 0, counters_dn = 0, flag_bytes = 0;  // floats / words / bytes
+};
+MoEDecodePlan moe_decode_plan(const MoELaunch &a, const MoEPlanSizes &p);
+int moe_decode_capacity(const MoEPlanSizes &p, int device);  // co-resident workgroups (0: variant not built)
+bool moe_decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, hipStream_t s);
 MoEPlanSizes moe_plan(const MoELaunch &a);
 void moe_launch(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s);
 

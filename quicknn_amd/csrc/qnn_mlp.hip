@@ -17,7 +17,7 @@
 // the same slice order, so h and y are bit-identical to the per-op path.
 // Workgroup w runs gate/up item w, then (for w below the down grid) down item
 // w, each placed with the per-op kernels' XCD-aware map, so split-K partial
-// sums meet in one XCD's L2 as there (placement checked, error bit 4).
+// sums meet in one XCD's L2 as there (qnn_exchange.h).
 //
 // Dataflow instead of a barrier: the workgroup that completes a block of h
 // (64 rows) writes it with device-coherent stores and then sets that block's
@@ -75,11 +75,11 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   // ---- 1) Loads: x slice and gate/up weights to registers, down weights to LDS.
   float4 xr[1][dev::x_iters<GG>()];
   uint4 w[GG];
-  float sc[GG];
+  uint4 q[dev::scale_quads<GG>()];
   dev::load_x<1, GG>(xr, dev::rsrc(a.x, size_t(a.hidden) * 4), [](int) { return 0u; }, 1, ws0 * 32, sgroups * 32,
                      tid);
-  dev::load_w<GG>(w, sc, dev::rsrc((tile & 1) ? a.unib : a.gnib, lg.nib_bytes()),
-                  dev::rsrc((tile & 1) ? a.uscl : a.gscl, lg.scale_bytes()), lg, tile >> 1, s0, lane);
+  dev::load_wq<GG>(w, q, dev::rsrc((tile & 1) ? a.unib : a.gnib, lg.nib_bytes()),
+                   dev::rsrc((tile & 1) ? a.uscl : a.gscl, lg.scale_bytes()), lg, tile >> 1, s0, lane);
   if (dn_on) {
     const dev::Rsrc dnib = dev::rsrc(a.dnib, ld.nib_bytes()), dscl = dev::rsrc(a.dscl, ld.scale_bytes());
     const uint32_t at = uint32_t((size_t(td) * ld.steps + s0d) * 64 + lane);
@@ -92,6 +92,8 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
     for (int g = 0; g < GD; ++g)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(dnib, (lds_t *)(dn_nib + g * kNibStep), 16, at * 16u, g * 1024u, 0, 0);
   }
+  float sc[GG];
+  dev::pick_scales<GG>(sc, q, s0);  // after every load is issued
 
   // ---- 2) Gate/up item: stage x, integer dot, parts in LDS, split-K exchange;
   //         the last of the 2 x slices arrivals of a block writes its h rows and
@@ -113,17 +115,17 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
     acc[0] += red[1][lane];
     acc[0] += red[2][lane];
     acc[0] += red[3][lane];
-    dev::check_xcd(local, a.err, lane);
-    dev::xstore(a.partial_gu + (size_t(tile) * a.slices_gu + slice) * 64 + lane, acc[0], local);
+    dev::xstore(a.partial_gu + (size_t(tile) * a.slices_gu + slice) * 64 + lane, acc[0]);
     unsigned *ctr = &a.counters_gu[size_t(tile >> 1) * kCounterStride];
-    if (dev::last_arrival(ctr, unsigned(2 * a.slices_gu), lane)) {
+    bool l2 = false;
+    if (dev::last_arrival(ctr, unsigned(2 * a.slices_gu), lane, local, l2)) {
       const float *pt = a.partial_gu + size_t(tile & ~1) * a.slices_gu * 64 + lane;
       float g[1], u[1];
-      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_gu, local);
-      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(a.slices_gu + s) * 64; }, a.slices_gu, local);
+      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_gu, l2);
+      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(a.slices_gu + s) * 64; }, a.slices_gu, l2);
       dev::reset_counter(ctr, lane);
       const int blk = tile >> 1, row = blk * 64 + lane;
-      if (row < a.inter) dev::xstore(a.h + row, dev::silu(g[0]) * u[0], 0);
+      if (row < a.inter) dev::xstore(a.h + row, dev::silu(g[0]) * u[0]);
       __builtin_amdgcn_s_waitcnt(0);  // the block's h is at the coherence point
       if (lane == 0)
         __hip_atomic_store(a.flags + size_t(blk) * 64, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -179,12 +181,12 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   acc[0] += red[2][lane];
   acc[0] += red[3][lane];
   if (a.slices_dn > 1) {
-    dev::check_xcd(local, a.err, lane);
-    dev::xstore(a.partial_dn + (size_t(td) * a.slices_dn + sld) * 64 + lane, acc[0], local);
+    dev::xstore(a.partial_dn + (size_t(td) * a.slices_dn + sld) * 64 + lane, acc[0]);
     unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
-    if (!dev::last_arrival(ctr, unsigned(a.slices_dn), lane)) return;
+    bool l2 = false;
+    if (!dev::last_arrival(ctr, unsigned(a.slices_dn), lane, local, l2)) return;
     const float *pt = a.partial_dn + size_t(td) * a.slices_dn * 64 + lane;
-    dev::sum_slices<1, 16>(acc, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_dn, local);
+    dev::sum_slices<1, 16>(acc, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_dn, l2);
     dev::reset_counter(ctr, lane);
   }
   const int row = td * 64 + lane;

@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   const int row = DOWN ? b * l.rpb + lane / L : b * l.rpb + wl / L;
   auto finish = [&](int R, float v) {  // final value of this lane's row for position R
     if (DOWN) {
-      if (j == 0 && row < nout) dev::xstore(a.y + size_t(R) * a.hidden + row, v, a.xcd_local);
+      if (j == 0 && row < nout) dev::xstore(a.y + size_t(R) * a.hidden + row, v);
     } else {
       const float u = __shfl_down(v, 32);
       if (lane < 32 && j == 0 && row < nout) a.h[size_t(R) * a.inter + row] = dev::silu(v) * u;
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
         acc[m] = ((acc[m] + red[0][m][lane]) + red[1][m][lane]) + red[2][m][lane];
         if (m0 + m < c) {
           const int R = pl.pos[m0 + m];
-          if (slices > 1) dev::xstore(part + size_t(R) * 64, acc[m], a.xcd_local);
+          if (slices > 1) dev::xstore(part + size_t(R) * 64, acc[m]);
           else finish(R, acc[m]);
         }
       }
@@ -225,15 +225,14 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
 
   // split-K: the last slice of (slot, tile) sums the slices in order
   if (slices > 1) {
-    dev::check_xcd(a.xcd_local, a.err, lane);
     unsigned *ctr = &a.counters[(size_t(tile) * slots + slot) * kCounterStride];
-    if (!dev::last_arrival(ctr, unsigned(slices), lane)) return;
+    bool l2 = false;
+    if (!dev::last_arrival(ctr, unsigned(slices), lane, a.xcd_local, l2)) return;
     const float *pt = a.partial + size_t(tile) * slices * n * 64 + lane;
     for (int m0 = 0; m0 < c; m0 += MT) {
       float acc[MT];
       dev::sum_slices<MT, 4>(
-          acc, [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices,
-          a.xcd_local);
+          acc, [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices, l2);
 #pragma unroll
       for (int m = 0; m < MT; ++m)
         if (m0 + m < c) finish(pl.pos[m0 + m], acc[m]);
@@ -244,9 +243,9 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
 
   // expert combine: the last (slot, tile) of this tile to finish; lane (r, j)
   // combines row r for tokens j, j+L, ...
-  dev::check_xcd(a.xcd_local, a.err, lane);
   unsigned *cctr = &a.counters[(size_t(tiles) * slots + tile) * kCounterStride];
-  if (!dev::last_arrival(cctr, unsigned(pl.active), lane)) return;
+  bool l2c = false;
+  if (!dev::last_arrival(cctr, unsigned(pl.active), lane, a.xcd_local, l2c)) return;
   if (row < nout) {
     for (int tk = j; tk < a.rows; tk += L) {
       float acc = 0.0f;
@@ -254,7 +253,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
         const int R = tk * a.topk + pl.ord[tk * a.topk + r];
         if (pl.ids[R] >= uint32_t(a.experts)) continue;
         const float p = a.routes[n + R];
-        const float v = dev::xload(a.y + size_t(R) * a.hidden + row, a.xcd_local);
+        const float v = dev::xload(a.y + size_t(R) * a.hidden + row, l2c);
         acc = add_mul_nofma(acc, v, p);  // moe.comp:70 / :126: out + y*p
       }
       a.out[size_t(tk) * a.hidden + row] = acc;
@@ -270,6 +269,243 @@ void launch_mt(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
   const int gdn = (tdn + 7) / 8 * 8 * p.slots * p.slices_dn;
   hipLaunchKernelGGL((k_moe<MT, GSW, false>), dim3(ggu), dim3(256), p.lds_gu, s, a, p.slices_gu, p.sps_gu, p.slots);
   hipLaunchKernelGGL((k_moe<MT, GSW, true>), dim3(gdn), dim3(256), p.lds_dn, s, a, p.slices_dn, p.sps_dn, p.slots);
+}
+
+// ---- one token, one launch -----------------------------------------------
+// With one token the k routed experts form a block-structured MLP: gate/up of
+// every expert reads the same x, and the down projections add up as
+//     out = sum_j p_j W_d[e_j] h_j  (j in ascending expert id),
+// i.e. a down matvec over the concatenated h whose K-segments use expert
+// e_j's weights.  So the layer runs as the fused decode MLP runs (qnn_mlp.hip):
+// workgroup w takes gate/up item w and down item w; the down weights go to
+// LDS together with the gate/up weights; a down item waits only for the
+// blocks of h its K-slice reads (per-(slot, block) epoch flags); and the
+// split-K combine of a down block, done by the last of its k * slices
+// arrivals, sums each expert's slices in order and then the experts in
+// ascending id with p, which is exactly the arithmetic of the two-launch path
+// (k_moe), so the results are bit-identical to it.
+//
+// Items: gate/up tiles are whole waves over one matrix (gate or up) of one
+// (slot, 64-row block) pair, numbered 2*pair + up over all slots and mapped
+// like the dense SwiGLU (units padded to 16: the gate tile u and the up tile
+// u + 8 share an XCD).  Down units are (slot, block) with blocks padded to 8
+// per slot, so every arrival of a down block runs on the XCD of block % 8.
+constexpr int kNibStep = 1024;   // nibble bytes of one wave step
+constexpr int kSclPiece = 1024;  // scale bytes of one wave's 4-step piece
+
+size_t moe_decode_lds(int g) {
+  return size_t(4) * (g * kNibStep + (g >= 4 ? g / 4 : 1) * kSclPiece) + dev::xplanes_bytes(1, 4 * g);
+}
+
+template <int GG, int GD>
+__global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int sps_gu, const int slices_gu,
+                                                    const int sps_dn, const int slices_dn, const int units_gu,
+                                                    const int bpad_dn, const int grid_dn) {
+  extern __shared__ uint4 dyn_lds[];
+  __shared__ float red[4][64];
+  const int wave = dev::wave_id(), tid = threadIdx.x, lane = tid & 63, part = wave;
+  const int wg = blockIdx.x;
+  const int k = a.topk;
+  uint8_t *lds = reinterpret_cast<uint8_t *>(dyn_lds);
+  constexpr int QD = dev::scale_quads<GD>();
+  uint8_t *dn_nib = lds + size_t(part) * GD * kNibStep;
+  uint8_t *dn_scl = lds + size_t(4) * GD * kNibStep + size_t(part) * QD * kSclPiece;
+  constexpr int XG = 4 * (GG > GD ? GG : GD);
+  const dev::XPlanes xs = dev::xplanes_at(lds + size_t(4) * (GD * kNibStep + QD * kSclPiece), 1, XG);
+  const I4Layout &lg = a.gu, &ld = a.dn;
+  const int local = a.xcd_local;
+
+  // ---- route ranks: lane i < k holds route i; rank = its position in
+  //      ascending expert id (ties: lower route index, reported as invalid).
+  const dev::Rsrc rr = dev::rsrc(a.routes, size_t(2 * k) * 4);  // branch-free loads (past the end: 0)
+  const uint32_t id0 = __float_as_uint(dev::ld32f(rr, uint32_t(lane) * 4u, 0));
+  const float prob0 = dev::ld32f(rr, uint32_t(k + lane) * 4u, 0);
+  const uint32_t id = lane < k ? id0 : 0xFFFFFFFFu;
+  const float prob = lane < k ? prob0 : 0.0f;
+  int rank = 0;
+  bool dup = false;
+  for (int i = 0; i < k; ++i) {
+    const uint32_t o = uint32_t(__builtin_amdgcn_readlane(int(id), i));
+    rank += (o < id) || (o == id && i < lane);
+    dup |= o == id && i != lane;
+  }
+  if (wg == 0 && wave == 0 && __ballot(lane < k && (dup || id >= uint32_t(a.experts))) != 0 && lane == 0)
+    atomicOr(a.err, 8);
+  auto src_of = [&](int slot) { return __ffsll((unsigned long long)__ballot(lane < k && rank == slot)) - 1; };
+  auto expert_of = [&](int slot) {  // clamped so addresses stay inside the set; scalar (uniform) for the resources
+    return __builtin_amdgcn_readfirstlane(int(min(uint32_t(__shfl(id, src_of(slot))), uint32_t(a.experts - 1))));
+  };
+
+  // ---- gate/up item
+  const int pairs = k * lg.blocks;
+  int unit = 0, slice = 0;
+  const bool mapped = dev::map_tile(wg, slices_gu, units_gu, unit, slice);
+  const int tile_m = 2 * ((unit >> 4) * 8 + (unit & 7)) + ((unit >> 3) & 1);
+  const bool gu_on = mapped && tile_m < 2 * pairs;
+  const int tile = gu_on ? tile_m : 0;
+  if (!gu_on) slice = 0;
+  const int pair = tile >> 1, slot = pair / lg.blocks, blk = pair - slot * lg.blocks;
+  const int ws0 = slice * 4 * sps_gu, s0 = ws0 + part * sps_gu;
+  const int ns = max(0, min(sps_gu, lg.steps - s0));
+  const int sgroups = min(4 * sps_gu, lg.groups - ws0);
+
+  // ---- down item
+  int ud = 0, sld = 0;
+  bool dn_on = wg < grid_dn && dev::map_tile(wg, slices_dn, k * bpad_dn, ud, sld);
+  int dslot = ud / bpad_dn, td = ud - dslot * bpad_dn;
+  dn_on = dn_on && td < ld.blocks;
+  if (!dn_on) dslot = td = sld = 0;
+  const int wsd = sld * 4 * sps_dn, s0d = wsd + part * sps_dn;
+  const int nsd = max(0, min(sps_dn, ld.steps - s0d));
+  const int sgd = min(4 * sps_dn, ld.groups - wsd);
+
+  const int eg = expert_of(slot), ed = expert_of(dslot);
+
+  // ---- 1) loads: x slice and gate/up weights to registers, down weights to LDS
+  float4 xr[1][dev::x_iters<GG>()];
+  uint4 w[GG];
+  uint4 q[dev::scale_quads<GG>()];
+  dev::load_x<1, GG>(xr, dev::rsrc(a.x, size_t(a.hidden) * 4), [](int) { return 0u; }, 1, ws0 * 32, sgroups * 32,
+                     tid);
+  {
+    const uint8_t *wb = a.gate_up + size_t(2 * eg + (tile & 1)) * a.gu_stride;
+    dev::load_wq<GG>(w, q, dev::rsrc(wb, lg.nib_bytes()), dev::rsrc(wb + lg.nib_bytes(), lg.scale_bytes()), lg, blk,
+                     s0, lane);
+  }
+  if (dn_on) {
+    const uint8_t *db = a.down + size_t(ed) * a.dn_stride;
+    const dev::Rsrc dnib = dev::rsrc(db, ld.nib_bytes()), dscl = dev::rsrc(db + ld.nib_bytes(), ld.scale_bytes());
+    const uint32_t at = uint32_t((size_t(td) * ld.steps + s0d) * 64 + lane);
+    const uint32_t qat = uint32_t((size_t(td) * ld.quads() + (s0d >> 2)) * 64 + lane);
+    typedef __attribute__((address_space(3))) void lds_t;
+#pragma unroll
+    for (int i = 0; i < QD; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dscl, (lds_t *)(dn_scl + i * kSclPiece), 16, qat * 16u, i * 1024u, 0, 0);
+#pragma unroll
+    for (int g = 0; g < GD; ++g)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dnib, (lds_t *)(dn_nib + g * kNibStep), 16, at * 16u, g * 1024u, 0, 0);
+  }
+  float sc[GG];
+  dev::pick_scales<GG>(sc, q, s0);
+
+  // ---- 2) gate/up: dot, parts in LDS, split-K exchange; the last of the
+  //         2 x slices arrivals of a pair writes its h rows and raises its flag.
+  dev::stage_x<1, GG>(xs, xr, 1, ws0 * 32, sgroups * 32, a.hidden, tid, lane);
+  __syncthreads();
+  float acc[1] = {0.0f};
+  if (ns > 0) {
+    dev::XPlanes xp = xs;
+    const int g0 = part * sps_gu;
+    xp.q = xs.q + size_t(g0) * dev::kXWords;
+    xp.s2 = xs.s2 + g0;
+    xp.off = xs.off + g0;
+    dev::dot<1, GG>(acc, w, sc, xp, 1, 0, ns);
+  }
+  if (part > 0) red[part][lane] = acc[0];
+  __syncthreads();
+  if (part == 0 && gu_on) {
+    acc[0] = ((acc[0] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    dev::xstore(a.partial + (size_t(tile) * slices_gu + slice) * 64 + lane, acc[0]);
+    unsigned *ctr = &a.counters[size_t(pair) * kCounterStride];
+    bool l2 = false;
+    if (dev::last_arrival(ctr, unsigned(2 * slices_gu), lane, local, l2)) {
+      const float *pt = a.partial + size_t(tile & ~1) * slices_gu * 64 + lane;
+      float g[1], u[1];
+      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, slices_gu, l2);
+      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(slices_gu + s) * 64; }, slices_gu, l2);
+      dev::reset_counter(ctr, lane);
+      const int row = blk * 64 + lane;
+      if (row < a.inter) dev::xstore(a.h + size_t(slot) * a.inter + row, dev::silu(g[0]) * u[0]);
+      __builtin_amdgcn_s_waitcnt(0);  // the block's h is at the coherence point
+      if (lane == 0)
+        __hip_atomic_store(a.flags + size_t(pair) * 64, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (!dn_on) return;
+
+  // ---- 3) down: wait for the blocks of h_slot in the K-slice, stage, dot
+  //         with the LDS weights, split-K exchange; the last arrival of the
+  //         block combines slices and experts.
+  __syncthreads();  // xs and red are reused
+  if (wave == 0) {
+    const int b0 = (wsd * 32) >> 6, nb = (sgd * 32 + 63) >> 6;  // h blocks of the slice (<= 64)
+    const unsigned *fl = a.flags + (size_t(dslot) * lg.blocks + b0) * 64;
+    unsigned spins = 0;
+    for (;;) {
+      const bool ready =
+          lane >= nb || __hip_atomic_load(fl + size_t(lane) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.epoch;
+      if (__ballot(!ready) == 0) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > (1u << 25)) {  // ~1 s: report and finish instead of hanging
+        if (lane == 0) atomicOr(a.err, 2);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  float4 hr[1][dev::x_iters<GD>()];
+  dev::load_x<1, GD, dev::kCoherent>(hr, dev::rsrc(a.h + size_t(dslot) * a.inter, size_t(a.inter) * 4),
+                                    [](int) { return 0u; }, 1, wsd * 32, sgd * 32, tid);
+  dev::stage_x<1, GD>(xs, hr, 1, wsd * 32, sgd * 32, a.inter, tid, lane);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's weights have landed in LDS
+  __syncthreads();
+  uint4 wd[GD];
+  float scd[GD];
+  uint4 qd[QD];
+#pragma unroll
+  for (int i = 0; i < QD; ++i) qd[i] = *reinterpret_cast<const uint4 *>(dn_scl + i * kSclPiece + lane * 16);
+#pragma unroll
+  for (int g = 0; g < GD; ++g) wd[g] = *reinterpret_cast<const uint4 *>(dn_nib + g * kNibStep + lane * 16);
+  dev::pick_scales<GD>(scd, qd, s0d);
+  acc[0] = 0.0f;
+  if (nsd > 0) {
+    dev::XPlanes xp = xs;
+    const int g0 = part * sps_dn;
+    xp.q = xs.q + size_t(g0) * dev::kXWords;
+    xp.s2 = xs.s2 + g0;
+    xp.off = xs.off + g0;
+    dev::dot<1, GD>(acc, wd, scd, xp, 1, 0, nsd);
+  }
+  if (part > 0) red[part][lane] = acc[0];
+  __syncthreads();
+  if (part > 0) return;
+  acc[0] = ((acc[0] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  dev::xstore(a.partial_dn + ((size_t(td) * k + dslot) * slices_dn + sld) * 64 + lane, acc[0]);
+  unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
+  bool l2 = false;
+  if (!dev::last_arrival(ctr, unsigned(k * slices_dn), lane, local, l2)) return;
+  const float *pt = a.partial_dn + size_t(td) * k * slices_dn * 64 + lane;
+  float out = 0.0f;
+  for (int j = 0; j < k; ++j) {  // ascending expert id
+    float y[1];
+    if (slices_dn > 1)
+      dev::sum_slices<1, 16>(y, [&](int s, int) { return pt + (size_t(j) * slices_dn + s) * 64; }, slices_dn, l2);
+    else
+      y[0] = dev::xload(pt + size_t(j) * 64, l2);
+    out = add_mul_nofma(out, y[0], __shfl(prob, src_of(j)));  // moe.comp:70 / :126: out + y*p
+  }
+  dev::reset_counter(ctr, lane);
+  const int row = td * 64 + lane;
+  if (row < a.hidden) a.out[row] = out;
+}
+
+template <int G>
+bool decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, hipStream_t s) {
+  hipLaunchKernelGGL((k_moe_decode<G, G>), dim3(d.grid), dim3(256), moe_decode_lds(G), s, a, p.sps_gu, p.slices_gu,
+                     p.sps_dn, p.slices_dn, d.units_gu, d.bpad_dn, d.grid_dn);
+  return hipGetLastError() == hipSuccess;
+}
+
+template <int G>
+int decode_capacity(int device) {
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&k_moe_decode<G, G>), 256,
+                                                   moe_decode_lds(G)) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return per_cu * cus;
 }
 
 }  // namespace
@@ -319,6 +555,45 @@ void moe_launch(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
     default: fail(QNN_E_INVALID_OP, "MoE launch plan");
   }
   hip_check(hipGetLastError(), "moe launch");
+}
+
+MoEDecodePlan moe_decode_plan(const MoELaunch &a, const MoEPlanSizes &p) {
+  MoEDecodePlan d;
+  if (a.rows != 1 || p.mt != 1 || a.gu.lanes != 1 || a.dn.lanes != 1 || p.sps_gu != p.sps_dn) return d;
+  if (p.gsw != 1 && p.gsw != 2 && p.gsw != 4 && p.gsw != 8) return d;
+  const int k = a.topk;
+  const int pairs = k * a.gu.blocks;
+  d.units_gu = (2 * pairs + 15) / 16 * 16;
+  d.bpad_dn = (a.dn.blocks + 7) / 8 * 8;
+  d.grid_dn = k * d.bpad_dn * p.slices_dn;
+  d.grid = std::max(d.units_gu * p.slices_gu, d.grid_dn);
+  d.partial_gu = size_t(2 * pairs) * p.slices_gu * 64;
+  d.partial_dn = size_t(a.dn.blocks) * k * p.slices_dn * 64;
+  d.counters_gu = size_t(pairs) * kCounterStride;
+  d.counters_dn = size_t(a.dn.blocks) * kCounterStride;
+  d.flag_bytes = size_t(pairs) * 256;
+  d.ok = true;
+  return d;
+}
+
+int moe_decode_capacity(const MoEPlanSizes &p, int device) {
+  switch (p.gsw) {
+    case 1: return decode_capacity<1>(device);
+    case 2: return decode_capacity<2>(device);
+    case 4: return decode_capacity<4>(device);
+    case 8: return decode_capacity<8>(device);
+    default: return 0;
+  }
+}
+
+bool moe_decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, hipStream_t s) {
+  switch (p.gsw) {
+    case 1: return decode_launch<1>(a, p, d, s);
+    case 2: return decode_launch<2>(a, p, d, s);
+    case 4: return decode_launch<4>(a, p, d, s);
+    case 8: return decode_launch<8>(a, p, d, s);
+    default: return false;
+  }
 }
 
 }  // namespace qnn

@@ -229,3 +229,68 @@ def test_moe_experts_argument_errors(ctx, rng):
     with pytest.raises(hip.EArgumentException):
         ctx.CreateExpertSet(ex.bg, ex.bu, ex.bd, 64, 96)  # shapes do not match
     ctx.DestroyExpertSet(s)
+
+
+def _run_moe(ctx, s, x, routes, rows, k, hidden):
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(rows * hidden)
+    ctx.MoEExperts(s, dst, src, routes, rows, k)
+    out = ctx.Download(dst).copy()
+    ctx.Recycle(src)
+    ctx.Recycle(dst)
+    return out
+
+
+@pytest.mark.parametrize("E,hidden,inter,k", [
+    (6, 100, 72, 2),     # ragged groups and tiles (blocks not a multiple of 8)
+    (1, 128, 64, 1),
+    (16, 512, 320, 8),   # h blocks of 64 rows in 5 per expert
+    (64, 1024, 256, 16),
+    (40, 192, 4100, 3),  # many gate/up blocks, ragged
+])
+def test_moe_decode_single_launch_equals_two_launch(ctx, rng, monkeypatch, E, hidden, inter, k):
+    """One token: the single-launch path and the two-launch path give the same bits."""
+    ex = Experts(rng, E, hidden, inter)
+    s = ctx.CreateExpertSet(ex.bg, ex.bu, ex.bd, hidden, inter)
+    x = rng.standard_normal((1, hidden)).astype(np.float32)
+    routes, ids, probs = route_on_gpu(ctx, rng.standard_normal((1, E)).astype(np.float32), k)
+    f0 = ctx.status().moe_fused
+    one = _run_moe(ctx, s, x, routes, 1, k, hidden)
+    again = _run_moe(ctx, s, x, routes, 1, k, hidden)
+    assert ctx.status().moe_fused - f0 == 2
+    monkeypatch.setenv("QNN_FUSE_MOE", "0")
+    two = _run_moe(ctx, s, x, routes, 1, k, hidden)
+    assert ctx.status().moe_fused - f0 == 2
+    ctx.DestroyExpertSet(s)
+    assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
+    assert np.array_equal(again.view(np.uint32), one.view(np.uint32))
+    assert normwise_rel_err(one.reshape(1, -1)[0], ex.oracle(x, ids, probs)[0]) <= TOL
+
+
+def test_moe_decode_qwen3_equals_two_launch(ctx, rng, monkeypatch, qwen3_moe):
+    ex, s = qwen3_moe
+    k = 8
+    for trial in range(3):  # fresh routes each time: other experts, other flags
+        x = rng.standard_normal((1, ex.hidden)).astype(np.float32)
+        routes, ids, probs = route_on_gpu(ctx, rng.standard_normal((1, ex.E)).astype(np.float32), k)
+        monkeypatch.delenv("QNN_FUSE_MOE", raising=False)
+        f0 = ctx.status().moe_fused
+        one = _run_moe(ctx, s, x, routes, 1, k, ex.hidden)
+        assert ctx.status().moe_fused - f0 == 1
+        monkeypatch.setenv("QNN_FUSE_MOE", "0")
+        two = _run_moe(ctx, s, x, routes, 1, k, ex.hidden)
+        assert np.array_equal(one.view(np.uint32), two.view(np.uint32)), trial
+        assert normwise_rel_err(one, ex.oracle(x, ids, probs)[0]) <= TOL
+
+
+@pytest.mark.parametrize("fuse", ["1", "0"])
+def test_moe_experts_duplicate_route_id(ctx, rng, monkeypatch, fuse):
+    """An expert twice in one token's routes is reported (bit 8), on either path."""
+    monkeypatch.setenv("QNN_FUSE_MOE", fuse)
+    ex = Experts(rng, 4, 64, 64)
+    s = ctx.CreateExpertSet(ex.bg, ex.bu, ex.bd, 64, 64)
+    plane = np.concatenate([np.array([2, 2], np.uint32).view(np.float32), np.array([0.5, 0.5], np.float32)])
+    routes, src, dst = ctx.UploadRaw(plane), ctx.UploadRaw(np.ones(64, np.float32)), ctx.NewTensor(64)
+    ctx.MoEExperts(s, dst, src, routes, 1, 2)
+    with pytest.raises(hip.EInvalidOp):
+        ctx.Download(dst)
+    ctx.DestroyExpertSet(s)
