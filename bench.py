@@ -430,7 +430,7 @@ def run_cfg4(args, hip) -> dict:
     for rows in (1, 16):
         x = rng.standard_normal((rows, H)).astype(np.float32)
         xt = ctx.UploadRaw(x)
-        routes, distinct, first_logits = [], 0, None
+        routes, logit_t, distinct, first_logits = [], [], 0, None
         for l in range(L):  # each layer copy gets its own router logits
             lg = rng.standard_normal((rows, E)).astype(np.float32)
             first_logits = lg if first_logits is None else first_logits
@@ -438,6 +438,7 @@ def run_cfg4(args, hip) -> dict:
             rt = ctx.NewTensor(2 * rows * K)
             ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, rt, lt, None, None, [rows, E, K, 1])
             routes.append(rt)
+            logit_t.append(lt)
             distinct += len(set(ctx.Download(rt)[:rows * K].view(np.uint32).tolist()))
         out = ctx.NewTensor(rows * H)
 
@@ -445,14 +446,26 @@ def run_cfg4(args, hip) -> dict:
             for l in range(L):
                 ctx.MoEExperts(sets[l], out, xt, routes[l], rows, K)
 
+        def route_step():  # GO_MOE_ROUTE again on the same logits: the same routes
+            for l in range(L):
+                ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, routes[l], logit_t[l], None, None, [rows, E, K, 1])
+
+        def layer_step():  # route then experts, as a decode layer issues them
+            for l in range(L):
+                ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, routes[l], logit_t[l], None, None, [rows, E, K, 1])
+                ctx.MoEExperts(sets[l], out, xt, routes[l], rows, K)
+
         for _ in range(args.warmup):
             step()
+            route_step()
         ms = timed_ms(ctx, step, args.steps)
+        us_route = timed_ms(ctx, route_step, args.steps) * 1000 / L
+        us_both = timed_ms(ctx, layer_step, args.steps) * 1000 / L
         us_layer = ms * 1000 / L
         nbytes = distinct / L * per_expert + 4 * rows * (2 * H + 2 * K)
         res[rows] = {"ms_step": ms, "us_per_layer": round(us_layer, 2), "distinct_experts": round(distinct / L, 1),
                      "GBps": round(nbytes / (us_layer * 1e-6) / 1e9, 1), "bytes": nbytes, "x": x,
-                     "logits": first_logits}
+                     "logits": first_logits, "route_us": round(us_route, 2), "route_plus_experts_us": round(us_both, 2)}
     ctx.close()
     r1 = res[1]
     cpu = None
@@ -477,11 +490,13 @@ def run_cfg4(args, hip) -> dict:
         {"workload": "configs[3]: 128 experts, hidden 2048, expert inter 768, top-8, batch 1 (batch 16 below)",
          "global_batch": 1},
         us_per_layer=r1["us_per_layer"], distinct_experts=r1["distinct_experts"],
+        route_us=r1["route_us"], route_plus_experts_us=r1["route_plus_experts_us"],
         pct_of_hbm_peak=round(100 * r1["GBps"] / HBM_PEAK_GBS, 2),
-        batch16={k: v for k, v in res[16].items() if k in ("us_per_layer", "distinct_experts", "GBps")},
+        batch16={k: v for k, v in res[16].items()
+                 if k in ("us_per_layer", "distinct_experts", "GBps", "route_us", "route_plus_experts_us")},
         roofline={"bound": "hbm", "achieved": r1["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": round(r1["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                  "kernel": "k_moe gate/up + down (the two launches of one qnn_moe_experts call)",
+                  "kernel": "k_moe_decode (one qnn_moe_experts call for one token: a single launch)",
                   "kernel_us": r1["us_per_layer"], "bytes_per_launch": round(r1["bytes"]),
                   "timing": f"HIP events around {args.steps}x{L} calls"},
         cpu_baseline=cpu, setup_s=round(gen_s, 1))

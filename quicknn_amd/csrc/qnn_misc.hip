@@ -95,89 +95,140 @@ __global__ __launch_bounds__(256) void k_norm(float *dst, const float *a, const 
 // GO_MOE_ROUTE (moe.comp:25-50): fp32 softmax, exact top-k with ties to the
 // lower id, optional renormalisation by the rank-ordered top-k sum.  Ranking
 // uses the logits (softmax is monotone), which keeps the selection identical
-// to the CPU oracle regardless of exp() rounding.  One block per token row.
-__global__ __launch_bounds__(256) void k_moe_route(float *routes, const float *logits, int rows, int experts, int k,
-                                                   int normalize) {
-  extern __shared__ float sh[];  // experts floats of probabilities + 2*256 scratch
-  float *prob = sh;
-  float *rv = sh + experts;
-  int *ri = reinterpret_cast<int *>(rv + 256);
-  __shared__ int top_ids[64];
-  __shared__ float top_p[64];
-  __shared__ float top_total;
+// to the CPU oracle regardless of exp() rounding.  One wave per token row; two
+// selection methods with the same result:
+//
+// * up to 1024 experts (k_moe_route_reg): a lane holds J = experts/64 keys in
+//   registers, key = (order-preserving bits of the logit) << 13 | (8191 - id),
+//   so larger key = larger logit, ties to the lower id, all keys distinct.  A
+//   45-step binary search with wave ballots finds the k-th largest key T
+//   (count(key >= T) >= k, maximal); the k keys >= T are compacted to LDS and
+//   ranked against each other.  No step depends on a cross-lane shuffle.
+// * more experts (k_moe_route): logits in LDS; each of the k rounds is a scan
+//   of the lane's experts plus a 6-step butterfly argmax over (logit desc, id
+//   asc), a strict total order, so every lane agrees on the winner.
+//
+// Both take max, then the denominator as each lane's experts in ascending id
+// and a butterfly sum broadcast from lane 0, and p = exp(l - max) / denominator,
+// so their probabilities are identical too.
+template <int J>
+__global__ __launch_bounds__(64) void k_moe_route_reg(float *routes, const float *logits, int rows, int experts, int k,
+                                                      int normalize) {
+  __shared__ unsigned long long sel[64];
+  __shared__ float pr[64];
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const float *l = logits + size_t(row) * experts;
+  float v[J];
+  unsigned long long key[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int e = j * 64 + lane;
+    v[j] = e < experts ? l[e] : 0.0f;
+    const uint32_t u = v[j] == 0.0f ? 0u : __float_as_uint(v[j]);  // -0 ties with +0, as the comparisons do
+    const uint32_t m = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    key[j] = e < experts ? (((unsigned long long)m << 13) | (unsigned long long)(8191 - e)) : 0ull;
+  }
+  unsigned long long t = 0;  // the k-th largest key (real keys are > 0, and k <= experts)
+  for (int b = 44; b >= 0; --b) {
+    const unsigned long long cand = t | (1ull << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+    if (cnt >= k) t = cand;
+  }
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const bool in = key[j] >= t;
+    const unsigned long long bm = __ballot(in);
+    if (in) sel[base + __popcll(bm & ((1ull << lane) - 1ull))] = key[j];
+    base += __popcll(bm);
+  }
+  __syncthreads();
+  const unsigned long long mine = lane < k ? sel[lane] : 0ull;
+  int rank = 0;
+  for (int m = 0; m < k; ++m) rank += sel[m] > mine;
+  const uint32_t mm = uint32_t(mine >> 13);
+  const float lv = __uint_as_float((mm & 0x80000000u) ? (mm & 0x7FFFFFFFu) : ~mm);
+  const int id = 8191 - int(mine & 0x1FFFu);
+  const int top = __ffsll((unsigned long long)__ballot(lane < k && rank == 0)) - 1;
+  const float mx = __shfl(lv, top);
+  float part = 0.0f;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (j * 64 + lane < experts) part += expf(v[j] - mx);
+  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+  const float denominator = __shfl(part, 0);
+  const float p = expf(lv - mx) / denominator;
+  if (lane < k) pr[rank] = p;
+  __syncthreads();
+  float total = 0.0f;
+  for (int r = 0; r < k; ++r) total += pr[r];  // rank order
+  if (lane < k) {
+    const int target = row * k + rank;
+    routes[target] = __uint_as_float(uint32_t(id));
+    routes[size_t(rows) * k + target] = normalize ? p / total : p;
+  }
+}
+
+constexpr int kRouteNone = 0x7fffffff;
+__device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) {
+  return i != kRouteNone && (bi == kRouteNone || v > bv || (v == bv && i < bi));
+}
+__global__ __launch_bounds__(64) void k_moe_route(float *routes, const float *logits, int rows, int experts, int k,
+                                                  int normalize) {
+  extern __shared__ float sh[];  // experts logits, then experts "taken" bytes
+  float *lg = sh;
+  uint8_t *taken = reinterpret_cast<uint8_t *>(sh + experts);
   const int row = blockIdx.x, lane = threadIdx.x;
   const float *l = logits + size_t(row) * experts;
   float mx = -3.402823466e38f;
-  for (int e = lane; e < experts; e += 256) mx = fmaxf(mx, l[e]);
-  rv[lane] = mx;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (lane < s) rv[lane] = fmaxf(rv[lane], rv[lane + s]);
-    __syncthreads();
+  for (int e = lane; e < experts; e += 64) {
+    const float v = l[e];
+    lg[e] = v;
+    taken[e] = 0;
+    mx = fmaxf(mx, v);
   }
-  const float maximum = rv[0];
-  __syncthreads();
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   float part = 0.0f;
-  for (int e = lane; e < experts; e += 256) {
-    float v = expf(l[e] - maximum);
-    prob[e] = v;
-    part += v;
-  }
-  rv[lane] = part;
+  for (int e = lane; e < experts; e += 64) part += expf(lg[e] - mx);  // the lane's own LDS entries
+  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+  const float denominator = __shfl(part, 0);
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (lane < s) rv[lane] += rv[lane + s];
-    __syncthreads();
-  }
-  const float denominator = rv[0];
-  __syncthreads();
-  for (int e = lane; e < experts; e += 256) prob[e] = prob[e] / denominator;
-  __syncthreads();
-  // k rounds of (logit desc, id asc) argmax over the not-yet-taken experts.
-  for (int rank = 0; rank < k; ++rank) {
+  int my_id = 0;
+  float my_p = 0.0f;
+  for (int r = 0; r < k; ++r) {
     float best = -INFINITY;
-    int best_id = 0x7fffffff;
-    for (int e = lane; e < experts; e += 256) {
-      bool taken = false;
-      for (int t = 0; t < rank; ++t) taken |= (top_ids[t] == e);
-      float v = l[e];
-      if (!taken && (best_id == 0x7fffffff || v > best || (v == best && e < best_id))) {
+    int bid = kRouteNone;
+    for (int e = lane; e < experts; e += 64) {
+      const float v = lg[e];
+      if (!taken[e] && route_better(v, e, best, bid)) {
         best = v;
-        best_id = e;
+        bid = e;
       }
     }
-    rv[lane] = best;
-    ri[lane] = best_id;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if (lane < s) {
-        float ov = rv[lane + s];
-        int oi = ri[lane + s];
-        bool better = (oi != 0x7fffffff) &&
-                      (ri[lane] == 0x7fffffff || ov > rv[lane] || (ov == rv[lane] && oi < ri[lane]));
-        if (better) {
-          rv[lane] = ov;
-          ri[lane] = oi;
-        }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(best, o);
+      const int oi = __shfl_xor(bid, o);
+      if (route_better(ov, oi, best, bid)) {
+        best = ov;
+        bid = oi;
       }
-      __syncthreads();
     }
-    if (lane == 0) {
-      top_ids[rank] = ri[0];
-      top_p[rank] = prob[ri[0]];
+    bid = __shfl(bid, 0);  // k <= experts: a candidate always exists
+    if (lane == 0) taken[bid] = 1;
+    if (lane == r) {
+      my_id = bid;
+      my_p = expf(lg[bid] - mx) / denominator;
     }
     __syncthreads();
   }
-  if (lane == 0) {
-    float total = 0.0f;
-    for (int r = 0; r < k; ++r) total += top_p[r];
-    top_total = total;
-  }
-  __syncthreads();
+  float total = 0.0f;
+  for (int r = 0; r < k; ++r) total += __shfl(my_p, r);  // rank order
   if (lane < k) {
     const int target = row * k + lane;
-    routes[target] = __uint_as_float(uint32_t(top_ids[lane]));
-    routes[size_t(rows) * k + target] = normalize ? top_p[lane] / top_total : top_p[lane];
+    routes[target] = __uint_as_float(uint32_t(my_id));
+    routes[size_t(rows) * k + target] = normalize ? my_p / total : my_p;
   }
 }
 
@@ -284,8 +335,13 @@ void misc_norm(float *dst, const float *a, const void *gamma, int gamma_bf16, co
 }
 void misc_moe_route(float *routes, const float *logits, int rows, int experts, int k, int normalize,
                     hipStream_t s) {
-  size_t shmem = size_t(experts) * 4 + 256 * 8;
-  hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(256), shmem, s, routes, logits, rows, experts, k, normalize);
+  const int j = (experts + 63) / 64;
+  if (j <= 1) hipLaunchKernelGGL(k_moe_route_reg<1>, dim3(rows), dim3(64), 0, s, routes, logits, rows, experts, k, normalize);
+  else if (j <= 2) hipLaunchKernelGGL(k_moe_route_reg<2>, dim3(rows), dim3(64), 0, s, routes, logits, rows, experts, k, normalize);
+  else if (j <= 4) hipLaunchKernelGGL(k_moe_route_reg<4>, dim3(rows), dim3(64), 0, s, routes, logits, rows, experts, k, normalize);
+  else if (j <= 8) hipLaunchKernelGGL(k_moe_route_reg<8>, dim3(rows), dim3(64), 0, s, routes, logits, rows, experts, k, normalize);
+  else if (j <= 16) hipLaunchKernelGGL(k_moe_route_reg<16>, dim3(rows), dim3(64), 0, s, routes, logits, rows, experts, k, normalize);
+  else hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(64), size_t(experts) * 5, s, routes, logits, rows, experts, k, normalize);
   hip_check(hipGetLastError(), "moe route");
 }
 void misc_moe_gather(float *dst, const float *src, size_t src_n, const float *indices, int n, int hidden, int topk,

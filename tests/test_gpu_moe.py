@@ -27,13 +27,24 @@ def route_on_gpu(ctx, logits, k, normalize=True):
     return routes, raw[:rows * k].view(np.uint32).reshape(rows, k), raw[rows * k:].reshape(rows, k)
 
 
-@pytest.mark.parametrize("rows,E,k", [(1, 128, 8), (16, 128, 8), (3, 512, 64), (2, 8, 8), (4, 1000, 4), (7, 60, 1)])
+@pytest.mark.parametrize("rows,E,k", [(1, 128, 8), (16, 128, 8), (3, 512, 64), (2, 8, 8), (4, 1000, 4), (7, 60, 1),
+                                      (2, 1024, 8), (2, 1025, 8), (1, 8192, 64), (1, 64, 64), (5, 65, 3)])
 @pytest.mark.parametrize("normalize", [True, False])
 def test_route_matches_oracle(ctx, rng, rows, E, k, normalize):
     logits = rng.standard_normal((rows, E)).astype(np.float32)
     _, ids, probs = route_on_gpu(ctx, logits, k, normalize)
     want_ids, want_p = oracle.moe_route(logits, k, normalize)
     assert np.array_equal(ids, want_ids)
+    assert np.allclose(probs, want_p, rtol=2e-6, atol=0)
+
+
+@pytest.mark.parametrize("E", [6, 2000])  # register and LDS selection
+def test_route_signed_zero_and_equal_logits_tie_to_lower_id(ctx, E):
+    logits = np.full((1, E), -1.0, np.float32)
+    logits[0, 3], logits[0, 1], logits[0, 5] = 0.0, -0.0, 0.0
+    _, ids, probs = route_on_gpu(ctx, logits, 3)
+    want_ids, want_p = oracle.moe_route(logits, 3)
+    assert ids[0].tolist() == [1, 3, 5] == want_ids[0].tolist()
     assert np.allclose(probs, want_p, rtol=2e-6, atol=0)
 
 
