@@ -311,7 +311,6 @@ void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s) {
 Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
   Q8GemmPlan p;
   // Two 32-row blocks per wave once the grid has >= 2 workgroups per CU anyway.
-  const int ntiles = (N + BN - 1) / BN;
   p.mb = env_int("QNN_GEMM_MB", 0);
   if (p.mb != 1 && p.mb != 2) p.mb = M >= 256 ? 2 : 1;
   const int BM = 128 * p.mb;
