@@ -97,7 +97,6 @@ struct qnn_ctx_s {
   std::vector<qnn::WeightEntry *> capture_pins;
   std::vector<qnn::GraphRec> graphs;
   std::vector<qnn_expert_set_s *> sets;
-  bool xcd_local = false;  // the device dealt workgroup b to XCD b % 8 when probed at creation
   qnn_status st{};
   uint64_t act_bytes = 0;
 };
@@ -150,11 +149,6 @@ void sync(qnn_ctx_s *ctx) {
   ctx->st.submissions++;
 }
 
-// Split-K combines may read through the XCD's L2 when the workgroups ran where
-// the tile map intended; each kernel checks that per workgroup at run time
-// (qnn_exchange.h), since other GPU work in the process (and graph replays)
-// can change the dealing order that the creation-time probe saw.
-int xcd_local_launch(const qnn_ctx_s *ctx) { return ctx->xcd_local ? 1 : 0; }
 
 // Flush releases the pins a synchronous preload took (Context.Implementation.inc:411-415).
 void release_flush_pins(qnn_ctx_s *ctx) {
@@ -481,7 +475,6 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
     ensure_splitk(ctx, p.partial_floats, p.counters);
     a.partial = ctx->partial;
     a.counters = ctx->counters;
-    a.xcd_local = xcd_local_launch(ctx);
     a.err = ctx->error_flag;
     int4_matvec_launch(a, p, ctx->stream);
   }
@@ -519,7 +512,6 @@ void launch_linear_group(qnn_ctx_s *ctx) {
     a.mode = GG_STORE;
     a.partial = ctx->partial + pf;
     a.counters = ctx->counters + nc;
-    a.xcd_local = xcd_local_launch(ctx);
     a.err = ctx->error_flag;
     grp.slices[i] = g.slices[i];
     pf += g.slices[i] > 1 ? size_t(a.tiles) * g.slices[i] * 64 : 0;
@@ -627,7 +619,6 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
   a.counters_dn = ctx->counters + c_gu;
   a.flags = static_cast<unsigned *>(ctx->mlp_flags);
   a.epoch = next_epoch(ctx);
-  a.xcd_local = xcd_local_launch(ctx);
   a.err = ctx->error_flag;
   if (!mlp_launch(a, pg.gsw, pd.gsw, grid, ctx->stream)) return false;
   p.g->pins--;
@@ -667,7 +658,6 @@ void run_gguf(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
   ensure_splitk(ctx, slices > 1 ? size_t(a.tiles) * slices * 64 : 0, size_t(a.tiles) * kCounterStride);
   a.partial = ctx->partial;
   a.counters = ctx->counters;
-  a.xcd_local = xcd_local_launch(ctx);
   a.err = ctx->error_flag;
   gguf_matvec_launch(a, bw, slices, ctx->stream);
 }
@@ -713,8 +703,6 @@ int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out) {
       size_t free_b = 0, total_b = 0;
       hip_check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
       ctx->weight_limit = weight_cache_bytes ? weight_cache_bytes : uint64_t(double(free_b) * 0.85);
-      const char *xl = getenv("QNN_XCD_LOCAL");
-      ctx->xcd_local = (xl && xl[0] == '0') ? false : xcd_probe(ctx->stream);
     } catch (...) {
       if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
       if (ctx->error_flag) (void)hipFree(ctx->error_flag);
@@ -1366,7 +1354,6 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     ensure_splitk(ctx, p.partial_floats, p.counters);
     a.partial = ctx->partial;
     a.counters = ctx->counters;
-    a.xcd_local = xcd_local_launch(ctx);
     a.err = ctx->error_flag;
     ctx->st.int4_calls += 3;
     // One token: one launch (bit-identical to the two below) when every

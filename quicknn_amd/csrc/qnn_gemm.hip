@@ -198,7 +198,8 @@ template <int MB>
 __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
   constexpr int BM = 128 * MB;
   const int b = blockIdx.x;
-  // XCD-aware: the M-tiles of one N-tile share an XCD (workgroup b runs on XCD b % 8).
+  // XCD-aware: the M-tiles of one N-tile have the same blockIdx % 8, so with the
+  // device's usual round-robin dealing they share an XCD and its L2.
   const int xcd = b & 7, kq = b >> 3;
   const int q = kq / g.mtiles;
   const int ntile = q * 8 + xcd, mtile = kq - q * g.mtiles;

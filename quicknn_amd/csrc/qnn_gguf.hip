@@ -497,11 +497,10 @@ __global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   if (slices > 1) {
     dev::xstore(a.partial + (size_t(tile) * slices + slice) * 64 + lane, acc);
     unsigned *ctr = &a.counters[size_t(tile) * kCounterStride];
-    bool l2 = false;
-    if (!dev::last_arrival(ctr, unsigned(slices), lane, a.xcd_local, l2)) return;
+    if (!dev::last_arrival(ctr, unsigned(slices), lane)) return;
     const float *pt = a.partial + size_t(tile) * slices * 64 + lane;
     float s[1];
-    dev::sum_slices<1, 16>(s, [&](int sl, int) { return pt + size_t(sl) * 64; }, slices, l2);
+    dev::sum_slices<1, 16>(s, [&](int sl, int) { return pt + size_t(sl) * 64; }, slices);
     acc = s[0];
     dev::reset_counter(ctr, lane);
   }

@@ -113,16 +113,15 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
 #pragma unroll
     for (int m = 0; m < MT; ++m) dev::xstore(part_p + m * 64, acc[m]);
     unsigned *ctr = &a.counters[size_t(swiglu ? tile >> 1 : tile) * kCounterStride];
-    bool l2 = false;
-    if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane, a.xcd_local, l2)) return;
+    if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane)) return;
     const int t0 = swiglu ? tile & ~1 : tile;
     const float *pt = a.partial + size_t(t0) * slices * MT * 64 + lane;
     dev::sum_slices<MT, PU>(
-        acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices, l2);
+        acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices);
     if (swiglu) {
       const float *pu = pt + size_t(slices) * MT * 64;
       dev::sum_slices<MT, PU>(
-          accu, [&](int s, int m) { return pu + (size_t(s) * MT + m) * 64; }, slices, l2);
+          accu, [&](int s, int m) { return pu + (size_t(s) * MT + m) * 64; }, slices);
     }
     dev::reset_counter(ctr, lane);
   }

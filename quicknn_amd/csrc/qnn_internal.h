@@ -122,7 +122,6 @@ struct I4Launch {
   const float *prob = nullptr;  // I4_ACCUM: pointer to p
   float *partial = nullptr;     // split-K scratch
   unsigned *counters = nullptr;
-  int xcd_local = 0;            // combine slices through the XCD's L2 where placement allows (qnn_exchange.h)
   int *err = nullptr;           // error word
 };
 struct I4Plan {
@@ -131,7 +130,6 @@ struct I4Plan {
   size_t partial_floats = 0;  // split-K scratch
   size_t counters = 0;
 };
-bool xcd_probe(hipStream_t s);  // true when workgroup b runs on XCD b % 8
 // Launch geometry for m tokens (at most 16 per launch) in the given mode.
 I4Plan int4_plan(const I4Layout &l, int m, int mode);
 void int4_matvec_launch(const I4Launch &a, const I4Plan &p, hipStream_t s);
@@ -176,7 +174,6 @@ struct MlpLaunch {
   unsigned *counters_gu = nullptr, *counters_dn = nullptr;
   unsigned *flags = nullptr;  // per 64-row block of h, 256 B apart: epoch of the launch that completed it
   unsigned epoch = 0;         // this launch's number (never 0)
-  int xcd_local = 0;          // split-K partial sums through the XCD's L2 where placement allows (qnn_exchange.h)
   int *err = nullptr;         // bit 2: a wait for h timed out
 };
 size_t mlp_lds_bytes(int gg, int gd);
@@ -196,7 +193,6 @@ struct MoELaunch {
   float *y = nullptr;             // workspace [rows*topk][hidden]
   float *partial = nullptr;
   unsigned *counters = nullptr;
-  int xcd_local = 0;
   int *err = nullptr;  // bit 8: invalid route ids; bit 2: a fused-launch wait for h timed out
   // single-launch decode path (one token) only:
   float *partial_dn = nullptr;
@@ -247,7 +243,6 @@ struct GGArgs {
   int mode = GG_STORE;
   float *partial = nullptr;
   unsigned *counters = nullptr;
-  int xcd_local = 0;
   int *err = nullptr;
 };
 GGLayout gguf_layout(int enc, int rows, int cols);

@@ -282,31 +282,9 @@ __global__ void k_pad_rows(float *dst, const float *src, int rows, int cols, int
 }
 
 // Records the hardware XCC id (HW_REG_XCC_ID) of each workgroup.
-__global__ void k_xcc_probe(int *out) {
-  if (threadIdx.x == 0) out[blockIdx.x] = int(__builtin_amdgcn_s_getreg((3 << 11) | 20));
-}
-
 inline int blocks(long long n, int t) { return int((n + t - 1) / t); }
 
 }  // namespace
-
-bool xcd_probe(hipStream_t s) {
-  constexpr int n = 2048;
-  int *d = nullptr;
-  std::vector<int> h(n, -1);
-  hip_check(hipMalloc(&d, n * sizeof(int)), "xcd probe");
-  hipLaunchKernelGGL(k_xcc_probe, dim3(n), dim3(64), 0, s, d);
-  const hipError_t e1 = hipGetLastError();
-  const hipError_t e2 = hipMemcpyAsync(h.data(), d, n * sizeof(int), hipMemcpyDeviceToHost, s);
-  const hipError_t e3 = hipStreamSynchronize(s);
-  (void)hipFree(d);
-  hip_check(e1, "xcd probe launch");
-  hip_check(e2, "xcd probe copy");
-  hip_check(e3, "xcd probe sync");
-  for (int i = 0; i < n; ++i)
-    if (h[i] != (i & 7)) return false;
-  return true;
-}
 
 void misc_fill(float *dst, int n, uint32_t bits, hipStream_t s) {
   hipLaunchKernelGGL(k_fill, dim3(blocks(n, 256)), dim3(256), 0, s, dst, n, bits);

@@ -16,8 +16,7 @@
 // I4_STORE plan, with the same per-wave steps, the same in-workgroup order and
 // the same slice order, so h and y are bit-identical to the per-op path.
 // Workgroup w runs gate/up item w, then (for w below the down grid) down item
-// w, each placed with the per-op kernels' XCD-aware map, so split-K partial
-// sums meet in one XCD's L2 as there (qnn_exchange.h).
+// w, each placed with the per-op kernels' tile map (qnn_exchange.h).
 //
 // Dataflow instead of a barrier: the workgroup that completes a block of h
 // (64 rows) writes it with device-coherent stores and then sets that block's
@@ -49,7 +48,6 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   constexpr int XG = 4 * (GG > GD ? GG : GD);
   const dev::XPlanes xs = dev::xplanes_at(lds + size_t(4) * (GD * kNibStep + QD * kSclPiece), 1, XG);
   const I4Layout &lg = a.lg, &ld = a.ld;
-  const int local = a.xcd_local;
 
   // ---- gate/up item of this workgroup (qnn_int4.hip I4_SWIGLU, T = 1: units
   //      padded to 16 so the gate tile u and the up tile u + 8 share an XCD).
@@ -117,12 +115,11 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
     acc[0] += red[3][lane];
     dev::xstore(a.partial_gu + (size_t(tile) * a.slices_gu + slice) * 64 + lane, acc[0]);
     unsigned *ctr = &a.counters_gu[size_t(tile >> 1) * kCounterStride];
-    bool l2 = false;
-    if (dev::last_arrival(ctr, unsigned(2 * a.slices_gu), lane, local, l2)) {
+    if (dev::last_arrival(ctr, unsigned(2 * a.slices_gu), lane)) {
       const float *pt = a.partial_gu + size_t(tile & ~1) * a.slices_gu * 64 + lane;
       float g[1], u[1];
-      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_gu, l2);
-      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(a.slices_gu + s) * 64; }, a.slices_gu, l2);
+      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_gu);
+      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(a.slices_gu + s) * 64; }, a.slices_gu);
       dev::reset_counter(ctr, lane);
       const int blk = tile >> 1, row = blk * 64 + lane;
       if (row < a.inter) dev::xstore(a.h + row, dev::silu(g[0]) * u[0]);
@@ -183,10 +180,9 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   if (a.slices_dn > 1) {
     dev::xstore(a.partial_dn + (size_t(td) * a.slices_dn + sld) * 64 + lane, acc[0]);
     unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
-    bool l2 = false;
-    if (!dev::last_arrival(ctr, unsigned(a.slices_dn), lane, local, l2)) return;
+    if (!dev::last_arrival(ctr, unsigned(a.slices_dn), lane)) return;
     const float *pt = a.partial_dn + size_t(td) * a.slices_dn * 64 + lane;
-    dev::sum_slices<1, 16>(acc, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_dn, l2);
+    dev::sum_slices<1, 16>(acc, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_dn);
     dev::reset_counter(ctr, lane);
   }
   const int row = td * 64 + lane;
@@ -197,9 +193,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
 // checks it against mlp_capacity): on an otherwise idle device every
 // workgroup is placed at once, and the bounded waits turn anything else into
 // an error instead of a hang.  (A cooperative launch would guarantee the
-// residency, but after one the device no longer deals the workgroups of
-// later ordinary launches to XCDs in blockIdx % 8 order, which the XCD-local
-// exchanges rely on.)
+// residency; it was measured slower.)
 template <int GG, int GD>
 bool launch_mlp(const MlpLaunch &a, int grid, hipStream_t st) {
   hipLaunchKernelGGL((k_int4_mlp<GG, GD>), dim3(grid), dim3(256), mlp_lds_bytes(GG, GD), st, a);

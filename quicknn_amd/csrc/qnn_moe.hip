@@ -226,13 +226,12 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   // split-K: the last slice of (slot, tile) sums the slices in order
   if (slices > 1) {
     unsigned *ctr = &a.counters[(size_t(tile) * slots + slot) * kCounterStride];
-    bool l2 = false;
-    if (!dev::last_arrival(ctr, unsigned(slices), lane, a.xcd_local, l2)) return;
+    if (!dev::last_arrival(ctr, unsigned(slices), lane)) return;
     const float *pt = a.partial + size_t(tile) * slices * n * 64 + lane;
     for (int m0 = 0; m0 < c; m0 += MT) {
       float acc[MT];
       dev::sum_slices<MT, 4>(
-          acc, [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices, l2);
+          acc, [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices);
 #pragma unroll
       for (int m = 0; m < MT; ++m)
         if (m0 + m < c) finish(pl.pos[m0 + m], acc[m]);
@@ -244,8 +243,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   // expert combine: the last (slot, tile) of this tile to finish; lane (r, j)
   // combines row r for tokens j, j+L, ...
   unsigned *cctr = &a.counters[(size_t(tiles) * slots + tile) * kCounterStride];
-  bool l2c = false;
-  if (!dev::last_arrival(cctr, unsigned(pl.active), lane, a.xcd_local, l2c)) return;
+  if (!dev::last_arrival(cctr, unsigned(pl.active), lane)) return;
   if (row < nout) {
     for (int tk = j; tk < a.rows; tk += L) {
       float acc = 0.0f;
@@ -253,7 +251,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
         const int R = tk * a.topk + pl.ord[tk * a.topk + r];
         if (pl.ids[R] >= uint32_t(a.experts)) continue;
         const float p = a.routes[n + R];
-        const float v = dev::xload(a.y + size_t(R) * a.hidden + row, l2c);
+        const float v = dev::xload(a.y + size_t(R) * a.hidden + row);
         acc = add_mul_nofma(acc, v, p);  // moe.comp:70 / :126: out + y*p
       }
       a.out[size_t(tk) * a.hidden + row] = acc;
@@ -289,7 +287,7 @@ void launch_mt(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
 // (slot, 64-row block) pair, numbered 2*pair + up over all slots and mapped
 // like the dense SwiGLU (units padded to 16: the gate tile u and the up tile
 // u + 8 share an XCD).  Down units are (slot, block) with blocks padded to 8
-// per slot, so every arrival of a down block runs on the XCD of block % 8.
+// per slot, so every arrival of a down block has the same blockIdx % 8.
 constexpr int kNibStep = 1024;   // nibble bytes of one wave step
 constexpr int kSclPiece = 1024;  // scale bytes of one wave's 4-step piece
 
@@ -313,7 +311,6 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   constexpr int XG = 4 * (GG > GD ? GG : GD);
   const dev::XPlanes xs = dev::xplanes_at(lds + size_t(4) * (GD * kNibStep + QD * kSclPiece), 1, XG);
   const I4Layout &lg = a.gu, &ld = a.dn;
-  const int local = a.xcd_local;
 
   // ---- route ranks: lane i < k holds route i; rank = its position in
   //      ascending expert id (ties: lower route index, reported as invalid).
@@ -407,12 +404,11 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
     acc[0] = ((acc[0] + red[1][lane]) + red[2][lane]) + red[3][lane];
     dev::xstore(a.partial + (size_t(tile) * slices_gu + slice) * 64 + lane, acc[0]);
     unsigned *ctr = &a.counters[size_t(pair) * kCounterStride];
-    bool l2 = false;
-    if (dev::last_arrival(ctr, unsigned(2 * slices_gu), lane, local, l2)) {
+    if (dev::last_arrival(ctr, unsigned(2 * slices_gu), lane)) {
       const float *pt = a.partial + size_t(tile & ~1) * slices_gu * 64 + lane;
       float g[1], u[1];
-      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, slices_gu, l2);
-      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(slices_gu + s) * 64; }, slices_gu, l2);
+      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, slices_gu);
+      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(slices_gu + s) * 64; }, slices_gu);
       dev::reset_counter(ctr, lane);
       const int row = blk * 64 + lane;
       if (row < a.inter) dev::xstore(a.h + size_t(slot) * a.inter + row, dev::silu(g[0]) * u[0]);
@@ -472,16 +468,15 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   acc[0] = ((acc[0] + red[1][lane]) + red[2][lane]) + red[3][lane];
   dev::xstore(a.partial_dn + ((size_t(td) * k + dslot) * slices_dn + sld) * 64 + lane, acc[0]);
   unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
-  bool l2 = false;
-  if (!dev::last_arrival(ctr, unsigned(k * slices_dn), lane, local, l2)) return;
+  if (!dev::last_arrival(ctr, unsigned(k * slices_dn), lane)) return;
   const float *pt = a.partial_dn + size_t(td) * k * slices_dn * 64 + lane;
   float out = 0.0f;
   for (int j = 0; j < k; ++j) {  // ascending expert id
     float y[1];
     if (slices_dn > 1)
-      dev::sum_slices<1, 16>(y, [&](int s, int) { return pt + (size_t(j) * slices_dn + s) * 64; }, slices_dn, l2);
+      dev::sum_slices<1, 16>(y, [&](int s, int) { return pt + (size_t(j) * slices_dn + s) * 64; }, slices_dn);
     else
-      y[0] = dev::xload(pt + size_t(j) * 64, l2);
+      y[0] = dev::xload(pt + size_t(j) * 64);
     out = add_mul_nofma(out, y[0], __shfl(prob, src_of(j)));  // moe.comp:70 / :126: out + y*p
   }
   dev::reset_counter(ctr, lane);
