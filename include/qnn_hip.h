@@ -96,6 +96,7 @@ typedef struct {
   uint64_t mlp_fused;      /* TrySwiGLUVector + Int4Linear pairs run as one launch (no reference counterpart) */
   uint64_t linear_grouped; /* one-row GGUF Linear calls that ran in a shared launch (no reference counterpart) */
   uint64_t moe_fused;      /* one-token qnn_moe_experts calls run as a single launch (no reference counterpart) */
+  uint64_t moe_route_fused; /* of those, with the preceding GO_MOE_ROUTE computed in the launch (no reference counterpart) */
 } qnn_status;
 
 /* ---------------------------------------------------------------------------

@@ -81,7 +81,15 @@ struct qnn_ctx_s {
   size_t mlp_flag_bytes = 0;
   unsigned mlp_epoch = 0;
   int mlp_cap[9][9] = {};
-  int moe_cap[9] = {};  // co-resident workgroups of the one-token MoE kernel per steps variant
+  int moe_cap[9][17] = {};  // co-resident workgroups of the one-token MoE kernel per (steps, route) variant
+  // A one-token GO_MOE_ROUTE recorded instead of launched: when the next call
+  // is qnn_moe_experts on its output, that launch computes the routes itself.
+  struct PendingRoute {
+    bool on = false;
+    const float *logits = nullptr;
+    float *routes = nullptr;
+    int experts = 0, k = 0, normalize = 0;
+  } proute;
   // GGUF one-row Linear calls recorded for one grouped launch: consecutive
   // calls on the same input (a layer's q/k/v or gate/up projections) with the
   // same encoding and plan width, at most kGGMaxGroup, distinct outputs.
@@ -132,7 +140,7 @@ void check_ctx(qnn_ctx_s *ctx, bool keep_pending = false) {
   // Context.Implementation.inc:70-71: resident work stays on its creating thread.
   if (std::this_thread::get_id() != ctx->owner) fail(QNN_E_INVALID_OP, "context used from a thread other than its creator");
   hip_check(hipSetDevice(ctx->device), "hipSetDevice");
-  if (!keep_pending && (ctx->pending.on || ctx->lgroup.count)) settle_pending(ctx);
+  if (!keep_pending && (ctx->pending.on || ctx->lgroup.count || ctx->proute.on)) settle_pending(ctx);
 }
 
 // Check (Context.Implementation.inc): a live tensor of at least `minimum` floats.
@@ -547,6 +555,11 @@ void record_linear(qnn_ctx_s *ctx, WeightEntry *e, const float *x, float *y, int
 
 // ---------------------------------------------------------------- fused decode MLP
 void settle_pending(qnn_ctx_s *ctx) {
+  if (ctx->proute.on) {
+    const qnn_ctx_s::PendingRoute r = ctx->proute;
+    ctx->proute = {};
+    misc_moe_route(r.routes, r.logits, 1, r.experts, r.k, r.normalize, ctx->stream);
+  }
   if (ctx->lgroup.count) launch_linear_group(ctx);
   if (!ctx->pending.on) return;
   const qnn_ctx_s::Pending p = ctx->pending;
@@ -1147,8 +1160,12 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
           fail(QNN_E_ARGUMENT, "GO_MOE_ROUTE geometry");
         check_tensor(ctx, a, int64_t(rows) * experts);
         check_tensor(ctx, dst, int64_t(rows) * k * 2);
-        misc_moe_route(dst->ptr, a->ptr, rows, experts, k, norm, ctx->stream);
         ctx->st.moe_calls++;
+        if (rows == 1 && moe_route_j(experts) && !ctx->capturing && env_int("QNN_FUSE_MOE", 1) != 0 && dst != a) {
+          ctx->proute = {true, a->ptr, dst->ptr, experts, k, norm};  // launched with the next call
+          return QNN_OK;
+        }
+        misc_moe_route(dst->ptr, a->ptr, rows, experts, k, norm, ctx->stream);
         return QNN_OK;
       }
       case QNN_GO_MOE_GATHER: {
@@ -1317,7 +1334,29 @@ int qnn_expert_set_destroy(qnn_ctx *ctx, qnn_expert_set *set) {
 int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tensor *src, qnn_tensor *routes, int rows,
                     int topk) {
   return guarded([&] {
-    check_ctx(ctx);
+    check_ctx(ctx, true);
+    // The route op recorded just before, for these routes: computed in the
+    // one-token launch below if that launch happens; settled otherwise.
+    qnn_ctx_s::PendingRoute fr = {};
+    if (ctx->proute.on && routes && routes->ptr == ctx->proute.routes && rows == 1 &&
+        std::find(ctx->sets.begin(), ctx->sets.end(), set) != ctx->sets.end() &&
+        set->experts == ctx->proute.experts && topk == ctx->proute.k && src && src->ptr != ctx->proute.routes &&
+        dst && dst->ptr != ctx->proute.logits) {
+      fr = ctx->proute;
+      ctx->proute = {};
+    }
+    if (ctx->pending.on || ctx->lgroup.count || ctx->proute.on) settle_pending(ctx);
+    struct RouteGuard {  // an error below still runs the recorded route op
+      qnn_ctx_s *ctx;
+      qnn_ctx_s::PendingRoute &r;
+      ~RouteGuard() {
+        if (!r.on) return;
+        try {
+          misc_moe_route(r.routes, r.logits, 1, r.experts, r.k, r.normalize, ctx->stream);
+        } catch (...) {  // a launch error surfaces at the next synchronising call
+        }
+      }
+    } route_guard{ctx, fr};
     if (std::find(ctx->sets.begin(), ctx->sets.end(), set) == ctx->sets.end())
       fail(QNN_E_ARGUMENT, "unknown expert set");
     // TLLMMoE.forward geometry (LLM.MoE.pas:376-377) and the route op's limits.
@@ -1361,9 +1400,10 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     // epoch baked into the launch would repeat on every replay.
     if (rows == 1 && !ctx->capturing && env_int("QNN_FUSE_MOE", 1) != 0) {
       const MoEDecodePlan d = moe_decode_plan(a, p);
+      const int rj = fr.on && p.gsw == 8 ? moe_route_j(set->experts) : 0;
       if (d.ok) {
-        int &cap = ctx->moe_cap[p.gsw];
-        if (cap == 0) cap = std::max(-1, moe_decode_capacity(p, ctx->device));
+        int &cap = ctx->moe_cap[p.gsw][rj];
+        if (cap == 0) cap = std::max(-1, moe_decode_capacity(p, rj, ctx->device));
         if (cap > 0 && d.grid <= cap) {
           ensure_splitk(ctx, d.partial_gu + d.partial_dn, d.counters_gu + d.counters_dn);
           ensure_flags(ctx, d.flag_bytes);
@@ -1373,13 +1413,26 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
           a.counters_dn = ctx->counters + d.counters_gu;
           a.flags = static_cast<unsigned *>(ctx->mlp_flags);
           a.epoch = next_epoch(ctx);
-          if (moe_decode_launch(a, p, d, ctx->stream)) {
+          if (rj) {
+            a.logits = fr.logits;
+            a.routes_out = fr.routes;
+            a.normalize = fr.normalize;
+          }
+          if (moe_decode_launch(a, p, d, rj, ctx->stream)) {
+            if (rj) {
+              fr.on = false;  // computed by this launch
+              ctx->st.moe_route_fused++;
+            }
             ctx->st.moe_fused++;
             return QNN_OK;
           }
           hip_check(hipGetLastError(), "moe decode launch");
         }
       }
+    }
+    if (fr.on) {  // the routes first, then the two launches that read them
+      fr.on = false;
+      misc_moe_route(fr.routes, fr.logits, 1, fr.experts, fr.k, fr.normalize, ctx->stream);
     }
     moe_launch(a, p, ctx->stream);
     return QNN_OK;

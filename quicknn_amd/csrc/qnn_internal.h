@@ -199,6 +199,10 @@ struct MoELaunch {
   unsigned *counters_dn = nullptr;
   unsigned *flags = nullptr;  // per (slot, 64-row block of h), 256 B apart: epoch of the launch that completed it
   unsigned epoch = 0;
+  // computing the routes in the launch (moe_decode_launch with route_j > 0):
+  const float *logits = nullptr;  // [experts] router logits of the token
+  float *routes_out = nullptr;    // the route tensor, written as GO_MOE_ROUTE would
+  int normalize = 0;
 };
 struct MoEPlanSizes {
   int slots = 0, mt = 1, gsw = 4, slices_gu = 1, slices_dn = 1, sps_gu = 1, sps_dn = 1;
@@ -212,8 +216,9 @@ struct MoEDecodePlan {
   size_t partial_gu = 0, partial_dn = 0, counters_gu = 0, counters_dn = 0, flag_bytes = 0;  // floats / words / bytes
 };
 MoEDecodePlan moe_decode_plan(const MoELaunch &a, const MoEPlanSizes &p);
-int moe_decode_capacity(const MoEPlanSizes &p, int device);  // co-resident workgroups (0: variant not built)
-bool moe_decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, hipStream_t s);
+int moe_route_j(int experts);  // route-computing variant for this expert count (0: none)
+int moe_decode_capacity(const MoEPlanSizes &p, int route_j, int device);  // co-resident workgroups (0: not built)
+bool moe_decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, int route_j, hipStream_t s);
 MoEPlanSizes moe_plan(const MoELaunch &a);
 void moe_launch(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s);
 

@@ -1,7 +1,7 @@
 // qnn_misc.hip -- small ops on the decode path: fill, add, SwiGLU/GEGLU,
 // finite check, RMS/LayerNorm, MoE route, gather and scatter.  Semantics
 // follow the Vulkan shaders cited per kernel.
-#include "qnn_internal.h"
+#include "qnn_route_dev.h"
 
 namespace qnn {
 namespace {
@@ -98,12 +98,9 @@ __global__ __launch_bounds__(256) void k_norm(float *dst, const float *a, const 
 // to the CPU oracle regardless of exp() rounding.  One wave per token row; two
 // selection methods with the same result:
 //
-// * up to 1024 experts (k_moe_route_reg): a lane holds J = experts/64 keys in
-//   registers, key = (order-preserving bits of the logit) << 13 | (8191 - id),
-//   so larger key = larger logit, ties to the lower id, all keys distinct.  A
-//   45-step binary search with wave ballots finds the k-th largest key T
-//   (count(key >= T) >= k, maximal); the k keys >= T are compacted to LDS and
-//   ranked against each other.  No step depends on a cross-lane shuffle.
+// * up to 1024 experts (k_moe_route_reg): keys in registers and a ballot
+//   radix select (dev::route_row, qnn_route_dev.h).  No step depends on a
+//   cross-lane shuffle chain.
 // * more experts (k_moe_route): logits in LDS; each of the k rounds is a scan
 //   of the lane's experts plus a 6-step butterfly argmax over (logit desc, id
 //   asc), a strict total order, so every lane agrees on the winner.
@@ -115,59 +112,16 @@ template <int J>
 __global__ __launch_bounds__(64) void k_moe_route_reg(float *routes, const float *logits, int rows, int experts, int k,
                                                       int normalize) {
   __shared__ unsigned long long sel[64];
-  __shared__ float pr[64];
+  __shared__ int ids[64];
+  __shared__ float lvs[64];
   const int row = blockIdx.x, lane = threadIdx.x;
-  const float *l = logits + size_t(row) * experts;
-  float v[J];
-  unsigned long long key[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int e = j * 64 + lane;
-    v[j] = e < experts ? l[e] : 0.0f;
-    const uint32_t u = v[j] == 0.0f ? 0u : __float_as_uint(v[j]);  // -0 ties with +0, as the comparisons do
-    const uint32_t m = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    key[j] = e < experts ? (((unsigned long long)m << 13) | (unsigned long long)(8191 - e)) : 0ull;
-  }
-  unsigned long long t = 0;  // the k-th largest key (real keys are > 0, and k <= experts)
-  for (int b = 44; b >= 0; --b) {
-    const unsigned long long cand = t | (1ull << b);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= cand));
-    if (cnt >= k) t = cand;
-  }
-  int base = 0;
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const bool in = key[j] >= t;
-    const unsigned long long bm = __ballot(in);
-    if (in) sel[base + __popcll(bm & ((1ull << lane) - 1ull))] = key[j];
-    base += __popcll(bm);
-  }
-  __syncthreads();
-  const unsigned long long mine = lane < k ? sel[lane] : 0ull;
-  int rank = 0;
-  for (int m = 0; m < k; ++m) rank += sel[m] > mine;
-  const uint32_t mm = uint32_t(mine >> 13);
-  const float lv = __uint_as_float((mm & 0x80000000u) ? (mm & 0x7FFFFFFFu) : ~mm);
-  const int id = 8191 - int(mine & 0x1FFFu);
-  const int top = __ffsll((unsigned long long)__ballot(lane < k && rank == 0)) - 1;
-  const float mx = __shfl(lv, top);
-  float part = 0.0f;
-#pragma unroll
-  for (int j = 0; j < J; ++j)
-    if (j * 64 + lane < experts) part += expf(v[j] - mx);
-  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
-  const float denominator = __shfl(part, 0);
-  const float p = expf(lv - mx) / denominator;
-  if (lane < k) pr[rank] = p;
-  __syncthreads();
-  float total = 0.0f;
-  for (int r = 0; r < k; ++r) total += pr[r];  // rank order
+  dev::RouteRow<J> r;
+  dev::route_select<J>(r, logits + size_t(row) * experts, experts, k, lane, sel, ids, lvs);
+  const float p = dev::route_probs<J>(r, experts, k, normalize, lane);
   if (lane < k) {
-    const int target = row * k + rank;
-    routes[target] = __uint_as_float(uint32_t(id));
-    routes[size_t(rows) * k + target] = normalize ? p / total : p;
+    const int target = row * k + lane;
+    routes[target] = __uint_as_float(uint32_t(r.id));
+    routes[size_t(rows) * k + target] = p;
   }
 }
 

@@ -22,6 +22,7 @@
 // last (slot, tile) of a tile to finish combines the experts, both in a fixed
 // order, so results do not depend on timing.
 #include "qnn_int4_dev.h"
+#include "qnn_route_dev.h"
 
 namespace qnn {
 namespace {
@@ -295,7 +296,11 @@ size_t moe_decode_lds(int g) {
   return size_t(4) * (g * kNibStep + (g >= 4 ? g / 4 : 1) * kSclPiece) + dev::xplanes_bytes(1, 4 * g);
 }
 
-template <int GG, int GD>
+// J > 0: the token's routes are computed here from a.logits (GO_MOE_ROUTE
+// recorded just before, J = experts/64 rounded up to a power of two), by every
+// wave with the route op's own code, and workgroup 0 writes them to the
+// route tensor as the route op would.
+template <int GG, int GD, int J>
 __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int sps_gu, const int slices_gu,
                                                     const int sps_dn, const int slices_dn, const int units_gu,
                                                     const int bpad_dn, const int grid_dn) {
@@ -314,11 +319,22 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
 
   // ---- route ranks: lane i < k holds route i; rank = its position in
   //      ascending expert id (ties: lower route index, reported as invalid).
-  const dev::Rsrc rr = dev::rsrc(a.routes, size_t(2 * k) * 4);  // branch-free loads (past the end: 0)
-  const uint32_t id0 = __float_as_uint(dev::ld32f(rr, uint32_t(lane) * 4u, 0));
-  const float prob0 = dev::ld32f(rr, uint32_t(k + lane) * 4u, 0);
-  const uint32_t id = lane < k ? id0 : 0xFFFFFFFFu;
-  const float prob = lane < k ? prob0 : 0.0f;
+  uint32_t id;
+  float prob = 0.0f;  // J > 0: computed once the weight loads are issued
+  dev::RouteRow<(J > 0 ? J : 1)> rr_;
+  if constexpr (J == 0) {
+    const dev::Rsrc rr = dev::rsrc(a.routes, size_t(2 * k) * 4);  // branch-free loads (past the end: 0)
+    const uint32_t id0 = __float_as_uint(dev::ld32f(rr, uint32_t(lane) * 4u, 0));
+    const float prob0 = dev::ld32f(rr, uint32_t(k + lane) * 4u, 0);
+    id = lane < k ? id0 : 0xFFFFFFFFu;
+    prob = lane < k ? prob0 : 0.0f;
+  } else {
+    __shared__ unsigned long long rsel[4][64];
+    __shared__ int rids[4][64];
+    __shared__ float rlv[4][64];
+    dev::route_select<J>(rr_, a.logits, a.experts, k, lane, rsel[wave], rids[wave], rlv[wave]);
+    id = lane < k ? uint32_t(rr_.id) : 0xFFFFFFFFu;
+  }
   int rank = 0;
   bool dup = false;
   for (int i = 0; i < k; ++i) {
@@ -384,6 +400,13 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   }
   float sc[GG];
   dev::pick_scales<GG>(sc, q, s0);
+  if constexpr (J > 0) {  // the probabilities, while the loads are in flight
+    prob = dev::route_probs<J>(rr_, a.experts, k, a.normalize, lane);
+    if (wg == 0 && wave == 0 && lane < k) {
+      a.routes_out[lane] = __uint_as_float(uint32_t(rr_.id));
+      a.routes_out[k + lane] = prob;
+    }
+  }
 
   // ---- 2) gate/up: dot, parts in LDS, split-K exchange; the last of the
   //         2 x slices arrivals of a pair writes its h rows and raises its flag.
@@ -484,18 +507,18 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   if (row < a.hidden) a.out[row] = out;
 }
 
-template <int G>
+template <int G, int J>
 bool decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, hipStream_t s) {
-  hipLaunchKernelGGL((k_moe_decode<G, G>), dim3(d.grid), dim3(256), moe_decode_lds(G), s, a, p.sps_gu, p.slices_gu,
-                     p.sps_dn, p.slices_dn, d.units_gu, d.bpad_dn, d.grid_dn);
+  hipLaunchKernelGGL((k_moe_decode<G, G, J>), dim3(d.grid), dim3(256), moe_decode_lds(G), s, a, p.sps_gu,
+                     p.slices_gu, p.sps_dn, p.slices_dn, d.units_gu, d.bpad_dn, d.grid_dn);
   return hipGetLastError() == hipSuccess;
 }
 
-template <int G>
+template <int G, int J>
 int decode_capacity(int device) {
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&k_moe_decode<G, G>), 256,
-                                                   moe_decode_lds(G)) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&k_moe_decode<G, G, J>),
+                                                   256, moe_decode_lds(G)) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
     (void)hipGetLastError();
     return 0;
@@ -572,22 +595,51 @@ MoEDecodePlan moe_decode_plan(const MoELaunch &a, const MoEPlanSizes &p) {
   return d;
 }
 
-int moe_decode_capacity(const MoEPlanSizes &p, int device) {
+// Route-computing variants exist for the default one-token plan (8 steps per
+// wave); a forced plan uses the route op and the plain variant.
+int moe_route_j(int experts) {
+  const int j = (experts + 63) / 64;
+  return j <= 1 ? 1 : (j <= 2 ? 2 : (j <= 4 ? 4 : (j <= 8 ? 8 : (j <= 16 ? 16 : 0))));
+}
+
+int moe_decode_capacity(const MoEPlanSizes &p, int route_j, int device) {
+  if (route_j) {
+    if (p.gsw != 8) return 0;
+    switch (route_j) {
+      case 1: return decode_capacity<8, 1>(device);
+      case 2: return decode_capacity<8, 2>(device);
+      case 4: return decode_capacity<8, 4>(device);
+      case 8: return decode_capacity<8, 8>(device);
+      case 16: return decode_capacity<8, 16>(device);
+      default: return 0;
+    }
+  }
   switch (p.gsw) {
-    case 1: return decode_capacity<1>(device);
-    case 2: return decode_capacity<2>(device);
-    case 4: return decode_capacity<4>(device);
-    case 8: return decode_capacity<8>(device);
+    case 1: return decode_capacity<1, 0>(device);
+    case 2: return decode_capacity<2, 0>(device);
+    case 4: return decode_capacity<4, 0>(device);
+    case 8: return decode_capacity<8, 0>(device);
     default: return 0;
   }
 }
 
-bool moe_decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, hipStream_t s) {
+bool moe_decode_launch(const MoELaunch &a, const MoEPlanSizes &p, const MoEDecodePlan &d, int route_j, hipStream_t s) {
+  if (route_j) {
+    if (p.gsw != 8) return false;
+    switch (route_j) {
+      case 1: return decode_launch<8, 1>(a, p, d, s);
+      case 2: return decode_launch<8, 2>(a, p, d, s);
+      case 4: return decode_launch<8, 4>(a, p, d, s);
+      case 8: return decode_launch<8, 8>(a, p, d, s);
+      case 16: return decode_launch<8, 16>(a, p, d, s);
+      default: return false;
+    }
+  }
   switch (p.gsw) {
-    case 1: return decode_launch<1>(a, p, d, s);
-    case 2: return decode_launch<2>(a, p, d, s);
-    case 4: return decode_launch<4>(a, p, d, s);
-    case 8: return decode_launch<8>(a, p, d, s);
+    case 1: return decode_launch<1, 0>(a, p, d, s);
+    case 2: return decode_launch<2, 0>(a, p, d, s);
+    case 4: return decode_launch<4, 0>(a, p, d, s);
+    case 8: return decode_launch<8, 0>(a, p, d, s);
     default: return false;
   }
 }

@@ -305,3 +305,80 @@ def test_moe_experts_duplicate_route_id(ctx, rng, monkeypatch, fuse):
     with pytest.raises(hip.EInvalidOp):
         ctx.Download(dst)
     ctx.DestroyExpertSet(s)
+
+
+@pytest.mark.parametrize("E,hidden,inter,k", [(128, 512, 256, 8), (64, 256, 128, 4), (512, 128, 64, 8), (8, 128, 64, 8)])
+def test_moe_route_then_experts_one_launch(ctx, rng, E, hidden, inter, k):
+    """A one-token GO_MOE_ROUTE followed by qnn_moe_experts on its output runs
+    as one launch that computes the routes itself: the output and the route
+    tensor are bit-identical to the route op followed by the experts."""
+    ex = Experts(rng, E, hidden, inter)
+    s = ctx.CreateExpertSet(ex.bg, ex.bu, ex.bd, hidden, inter)
+    x = rng.standard_normal((1, hidden)).astype(np.float32)
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    lt, src = ctx.UploadRaw(logits), ctx.UploadRaw(x)
+    st0 = ctx.status()
+
+    rt1, out1 = ctx.NewTensor(2 * k), ctx.NewTensor(hidden)
+    ctx.Kernel(hip.GO_MOE_ROUTE, 2 * k, rt1, lt, None, None, [1, E, k, 1])
+    ctx.MoEExperts(s, out1, src, rt1, 1, k)  # fused with the recorded route
+    got, got_routes = ctx.Download(out1), ctx.Download(rt1)
+    st1 = ctx.status()
+    assert st1.moe_route_fused - st0.moe_route_fused == 1
+
+    rt2, out2 = ctx.NewTensor(2 * k), ctx.NewTensor(hidden)
+    ctx.Kernel(hip.GO_MOE_ROUTE, 2 * k, rt2, lt, None, None, [1, E, k, 1])
+    want_routes = ctx.Download(rt2)  # settles the route op on its own
+    ctx.MoEExperts(s, out2, src, rt2, 1, k)
+    want = ctx.Download(out2)
+    assert ctx.status().moe_route_fused == st1.moe_route_fused
+    assert np.array_equal(got_routes.view(np.uint32), want_routes.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ids, probs = oracle.moe_route(logits, k, True)
+    assert np.array_equal(got_routes[:k].view(np.uint32), ids[0])
+    assert normwise_rel_err(got, ex.oracle(x, ids, probs)[0]) <= TOL
+    for t in (lt, src, rt1, rt2, out1, out2):
+        ctx.Recycle(t)
+    ctx.DestroyExpertSet(s)
+
+
+def test_recorded_route_settles_on_other_calls(ctx, rng):
+    """A recorded route op runs before any call that could observe it, and a
+    MoE call on other routes does not consume it."""
+    E, k, hidden, inter = 32, 4, 128, 64
+    ex = Experts(rng, E, hidden, inter)
+    s = ctx.CreateExpertSet(ex.bg, ex.bu, ex.bd, hidden, inter)
+    logits = rng.standard_normal((2, E)).astype(np.float32)
+    l0, l1 = ctx.UploadRaw(logits[:1]), ctx.UploadRaw(logits[1:])
+    r0, r1 = ctx.NewTensor(2 * k), ctx.NewTensor(2 * k)
+    ctx.Kernel(hip.GO_MOE_ROUTE, 2 * k, r1, l1, None, None, [1, E, k, 1])
+    want1 = ctx.Download(r1)
+    f0 = ctx.status().moe_route_fused
+    ctx.Kernel(hip.GO_MOE_ROUTE, 2 * k, r0, l0, None, None, [1, E, k, 0])  # recorded
+    src, out = ctx.UploadRaw(rng.standard_normal(hidden).astype(np.float32)), ctx.NewTensor(hidden)
+    ctx.MoEExperts(s, out, src, r1, 1, k)  # other routes: the recorded op runs first, unfused
+    assert ctx.status().moe_route_fused == f0
+    ids, p = oracle.moe_route(logits[:1], k, False)
+    got0 = ctx.Download(r0)
+    assert np.array_equal(got0[:k].view(np.uint32), ids[0])
+    assert np.allclose(got0[k:], p[0], rtol=2e-6, atol=0)
+    assert np.array_equal(ctx.Download(r1).view(np.uint32), want1.view(np.uint32))
+    # recorded, then a different op: settled by it
+    ctx.Kernel(hip.GO_MOE_ROUTE, 2 * k, r0, l1, None, None, [1, E, k, 1])
+    ctx.Kernel(hip.GO_FILL, hidden, out, None, None, None, [0])
+    assert np.array_equal(ctx.Download(r0).view(np.uint32), want1.view(np.uint32))
+    for t in (l0, l1, r0, r1, src, out):
+        ctx.Recycle(t)
+    ctx.DestroyExpertSet(s)
+
+
+def test_route_over_1024_experts_is_not_recorded(ctx, rng):
+    E, k = 2000, 8
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    lt, rt = ctx.UploadRaw(logits), ctx.NewTensor(2 * k)
+    ctx.Kernel(hip.GO_MOE_ROUTE, 2 * k, rt, lt, None, None, [1, E, k, 1])
+    ids, p = oracle.moe_route(logits, k, True)
+    got = ctx.Download(rt)
+    assert np.array_equal(got[:k].view(np.uint32), ids[0])
+    ctx.Recycle(lt)
+    ctx.Recycle(rt)
