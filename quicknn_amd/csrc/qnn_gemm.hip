@@ -14,9 +14,9 @@
 // fp16 keeps 11 significant bits: the normwise error at the cfg5 shape is
 // ~3e-4 (an int8 activation pass would give ~5e-3, bf16 ~2e-3).
 //
-// Tiling.  A workgroup computes (128 * MB) x 96 of C with 4 waves of
-// (32 * MB) x 96 (MB x 3 MFMA tiles of 32 x 32); MB = 1 keeps at least two
-// workgroups per CU at the prefill shapes.  A is prepared once per call in MFMA
+// Tiling.  A workgroup computes (32 * MB * NW) x 96 of C with NW waves of
+// (32 * MB) x 96 (MB x 3 MFMA tiles of 32 x 32): 256 x 96 as 8 waves of one
+// block at prefill shapes, 128 x 96 as 4 waves below.  A is prepared once per call in MFMA
 // fragment order (1 KiB per 32 rows x 16 k, one 16-byte piece per lane), so a
 // wave loads its A fragments straight from L2 with fully coalesced 16-byte
 // loads.  The 96 weight rows of a K-step are decoded once per workgroup into a
@@ -36,7 +36,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BN = 96, BK = 64, LDB = BK + 8;  // LDB: halfs per LDS weight row
-// Workgroup tile: 4 waves x MB 32-row blocks of C (BM = 128 * MB rows) by BN columns.
+// Workgroup tile: NW waves x MB 32-row blocks of C (BM = 32 * MB * NW rows) by BN columns.
 
 __device__ __forceinline__ float half_bits_to_f(uint32_t h) {
   const uint16_t b = uint16_t(h);
@@ -177,26 +177,49 @@ __device__ __forceinline__ void load_b(BRaw &b, const GemmArgs &g, Rsrc wr, int 
   b.d = __builtin_amdgcn_raw_buffer_load_b16(wr, int(doff), 0, 0);
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void store_b(_Float16 (*bs)[LDB], const BRaw &b, float scale, int tid) {
   if (tid >= 2 * BN) return;
   const float ds = half_bits_to_f(b.d) * scale;  // d * 2^-ew (exact)
   const uint32_t qw[8] = {b.q0.x, b.q0.y, b.q0.z, b.q0.w, b.q1.x, b.q1.y, b.q1.z, b.q1.w};
   uint32_t hw[16];
+  if (fabsf(ds) >= 6.103515625e-05f) {
+    // ds is an fp16 normal, so fp16 arithmetic gives the same single rounding
+    // RNE(q * ds) as the fp32 product below: each byte q goes under the fp16
+    // exponent of 1024 as (q + 128) (v_perm), x - 1152 = q exactly, and one
+    // packed fp16 multiply rounds q * ds.
+    const _Float16 dh = _Float16(ds);  // exact
+    const half2v dsh = {dh, dh}, off = {_Float16(1152.0f), _Float16(1152.0f)};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int q0 = int(int8_t(qw[i] & 255u)), q1 = int(int8_t((qw[i] >> 8) & 255u));
-    const int q2 = int(int8_t((qw[i] >> 16) & 255u)), q3 = int(int8_t(qw[i] >> 24));
-    hw[2 * i] = pack_h2(float(q0) * ds, float(q1) * ds);
-    hw[2 * i + 1] = pack_h2(float(q2) * ds, float(q3) * ds);
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t u = qw[i] ^ 0x80808080u;
+      const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // q0 + 1152, q1 + 1152
+      const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // q2 + 1152, q3 + 1152
+      half2v a, c;
+      __builtin_memcpy(&a, &lo, 4);
+      __builtin_memcpy(&c, &hi, 4);
+      a = (a - off) * dsh;
+      c = (c - off) * dsh;
+      __builtin_memcpy(&hw[2 * i], &a, 4);
+      __builtin_memcpy(&hw[2 * i + 1], &c, 4);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q0 = int(int8_t(qw[i] & 255u)), q1 = int(int8_t((qw[i] >> 8) & 255u));
+      const int q2 = int(int8_t((qw[i] >> 16) & 255u)), q3 = int(int8_t(qw[i] >> 24));
+      hw[2 * i] = pack_h2(float(q0) * ds, float(q1) * ds);
+      hw[2 * i + 1] = pack_h2(float(q2) * ds, float(q3) * ds);
+    }
   }
   uint4 *dst = reinterpret_cast<uint4 *>(&bs[tid >> 1][(tid & 1) * 32]);
 #pragma unroll
   for (int j = 0; j < 4; ++j) dst[j] = make_uint4(hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]);
 }
 
-template <int MB>
-__global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
-  constexpr int BM = 128 * MB;
+template <int MB, int NW>
+__global__ __launch_bounds__(NW * 64) void k_q8_gemm(const GemmArgs g) {
+  constexpr int BM = 32 * MB * NW;
   const int b = blockIdx.x;
   // XCD-aware: the M-tiles of one N-tile have the same blockIdx % 8, so with the
   // device's usual round-robin dealing they share an XCD and its L2.
@@ -216,7 +239,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm(const GemmArgs g) {
   const int m32 = (mtile * BM + wave * 32 * MB) >> 5;  // first 32-row block of this wave
   // A fragments: piece (m32 + mb, ks) of this lane at byte ((m32 + mb) * ksteps + ks) * 1024 + lane * 16;
   // pieces past the last K-step read zeros.
-  const Rsrc ar = rsrc(g.afrag, size_t(g.mtiles) * MB * 4 * g.ksteps * 1024);
+  const Rsrc ar = rsrc(g.afrag, size_t(g.mtiles) * MB * NW * g.ksteps * 1024);
   const Rsrc wr = rsrc(g.w, g.l.total);
   uint32_t aoff[MB];
 #pragma unroll
@@ -311,10 +334,16 @@ void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s) {
 
 Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
   Q8GemmPlan p;
-  // Two 32-row blocks per wave once the grid has >= 2 workgroups per CU anyway.
+  // Prefill shapes (M >= 256): workgroup tile 256 x 96 as 8 waves of one
+  // 32-row block, so two waves per SIMD hide each other's waits (cfg5: 71.6 us
+  // against 76.8 for 4 waves of two blocks, the same tile; the weight decode
+  // per tile is shared by all of them).  Fewer rows: 128 x 96 as 4 waves.
+  // QNN_GEMM_NW / QNN_GEMM_MB override.
+  p.nw = env_int("QNN_GEMM_NW", 0);
+  if (p.nw != 4 && p.nw != 8) p.nw = M >= 256 ? 8 : 4;
   p.mb = env_int("QNN_GEMM_MB", 0);
-  if (p.mb != 1 && p.mb != 2) p.mb = M >= 256 ? 2 : 1;
-  const int BM = 128 * p.mb;
+  if (p.mb != 1 && p.mb != 2) p.mb = 1;
+  const int BM = 32 * p.mb * p.nw;
   p.m_pad = (M + BM - 1) / BM * BM;
   p.k_pad = (K + BK - 1) / BK * BK;
   p.ksteps = p.k_pad / 16;
@@ -344,8 +373,13 @@ void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, co
   g.mtiles = p.mtiles;
   g.ntiles = p.ntiles;
   const int grid = (p.ntiles + 7) / 8 * 8 * p.mtiles;
-  if (p.mb == 2) hipLaunchKernelGGL(k_q8_gemm<2>, dim3(grid), dim3(256), 0, s, g);
-  else hipLaunchKernelGGL(k_q8_gemm<1>, dim3(grid), dim3(256), 0, s, g);
+  if (p.nw == 8) {
+    if (p.mb == 2) hipLaunchKernelGGL((k_q8_gemm<2, 8>), dim3(grid), dim3(512), 0, s, g);
+    else hipLaunchKernelGGL((k_q8_gemm<1, 8>), dim3(grid), dim3(512), 0, s, g);
+  } else {
+    if (p.mb == 2) hipLaunchKernelGGL((k_q8_gemm<2, 4>), dim3(grid), dim3(256), 0, s, g);
+    else hipLaunchKernelGGL((k_q8_gemm<1, 4>), dim3(grid), dim3(256), 0, s, g);
+  }
   hip_check(hipGetLastError(), "q8 gemm launch");
 }
 

@@ -224,7 +224,8 @@ void moe_launch(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s);
 
 // Multi-row Q8_0 projection on fp16 MFMA (qnn_gemm.hip).
 struct Q8GemmPlan {
-  int mb = 1;  // 32-row blocks of C per wave (workgroup tile 128 * mb rows)
+  int mb = 1;  // 32-row blocks of C per wave
+  int nw = 4;  // waves per workgroup (workgroup tile 32 * mb * nw rows)
   int m_pad = 0, k_pad = 0, ksteps = 0, mtiles = 0, ntiles = 0;
   size_t frag_bytes = 0, exp_bytes = 0;  // workspace: fp16 A fragments, per-row exponents
 };
