@@ -75,8 +75,9 @@ struct qnn_ctx_s {
     float *h = nullptr;
     int in = 0, out = 0;
   } pending;
-  // Per-block completion flags of the fused MLP (qnn_mlp.hip), owned by it
-  // alone: zeroed when allocated, then only ever set to launch epochs.
+  // Completion flags of the single-launch kernels (fused MLP, one-token MoE):
+  // zeroed when allocated, then only ever set to launch epochs, which are
+  // unique per context, so both share it.
   void *mlp_flags = nullptr;
   size_t mlp_flag_bytes = 0;
   unsigned mlp_epoch = 0;
@@ -851,7 +852,7 @@ int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count) {
     if (flag) {
       hip_check(hipMemsetAsync(ctx->error_flag, 0, 4, ctx->stream), "error word reset");
       sync(ctx);
-      if (flag & 2) fail(QNN_E_INVALID_OP, "single-launch MLP/MoE: the wait for the gate/up output timed out");
+      if (flag & 2) fail(QNN_E_INVALID_OP, "single-launch kernel: a wait for data of the same launch timed out");
       if (flag & 8) fail(QNN_E_INVALID_OP, "Invalid GPU expert ID");  // LLM.MoE.pas:384-385
       if (flag & 16) fail(QNN_E_INVALID_OP, "MoE dispatch index outside its tensor");
       fail(QNN_E_INVALID_OP, "Resident GPU computation produced non-finite values");

@@ -268,9 +268,4 @@ struct GGGroup {
 };
 void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s);
 
-// Q8_0 GEMM (qnn_gemm.hip).
-size_t q8_act_bytes(int m, int k);
-void q8_act_quant_launch(const float *a, int m, int k, void *act, hipStream_t s);
-void q8_gemm_launch(const GGLayout &l, const void *w, const void *act, int m, float *c, hipStream_t s);
-
 }  // namespace qnn
