@@ -532,7 +532,14 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
   MoEPlanSizes p;
   const int n = a.rows * a.topk;
   p.slots = std::min(a.experts, n);
-  p.mt = a.rows == 1 ? 1 : (a.rows * a.topk <= 2 * a.experts ? 2 : 4);
+  // One token per pass: fewer registers (101 against 126 at 2 tokens), so
+  // five workgroups per CU instead of four; measured faster at 4, 16 and 32
+  // tokens (16: 159 against 167 us) even though an expert with several tokens
+  // makes several passes over its weights in registers.  QNN_MOE_MT (1, 2, 4)
+  // overrides.
+  p.mt = 1;
+  const int fmt = env_int("QNN_MOE_MT", 0);
+  if (fmt == 1 || fmt == 2 || fmt == 4) p.mt = fmt;
   // Steps per wave: 8 for one token (the single launch), 4 otherwise,
   // measured fastest for 128 experts of 768 x 2048 (1 token: 16.0 us against
   // 17.9 at 2 steps; 2-32 tokens: 14-16% faster than 2 steps, and than 8);
