@@ -242,20 +242,49 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   if (!DOWN) return;
 
   // expert combine: the last (slot, tile) of this tile to finish; lane (r, j)
-  // combines row r for tokens j, j+L, ...
+  // combines row r for tokens j, j+L, ...  The y values and probabilities of
+  // up to CT tokens x CR routes are loaded in one batch (independent loads in
+  // flight together), then summed in route order.
   unsigned *cctr = &a.counters[(size_t(tiles) * slots + tile) * kCounterStride];
   if (!dev::last_arrival(cctr, unsigned(pl.active), lane)) return;
   if (row < nout) {
-    for (int tk = j; tk < a.rows; tk += L) {
-      float acc = 0.0f;
-      for (int r = 0; r < a.topk; ++r) {
-        const int R = tk * a.topk + pl.ord[tk * a.topk + r];
-        if (pl.ids[R] >= uint32_t(a.experts)) continue;
-        const float p = a.routes[n + R];
-        const float v = dev::xload(a.y + size_t(R) * a.hidden + row);
-        acc = add_mul_nofma(acc, v, p);  // moe.comp:70 / :126: out + y*p
+    constexpr int CT = 4, CR = 8;
+    for (int t0 = j; t0 < a.rows; t0 += CT * L) {
+      float acc[CT];
+#pragma unroll
+      for (int c = 0; c < CT; ++c) acc[c] = 0.0f;
+      for (int r0 = 0; r0 < a.topk; r0 += CR) {
+        float v[CT][CR], pv[CT][CR];
+#pragma unroll
+        for (int c = 0; c < CT; ++c)
+#pragma unroll
+          for (int q = 0; q < CR; ++q) {
+            const int tk = t0 + c * L, r = r0 + q;
+            v[c][q] = pv[c][q] = 0.0f;
+            if (tk < a.rows && r < a.topk) {
+              const int R = tk * a.topk + pl.ord[tk * a.topk + r];
+              if (pl.ids[R] < uint32_t(a.experts)) {
+                pv[c][q] = a.routes[n + R];
+                v[c][q] = dev::xload(a.y + size_t(R) * a.hidden + row);
+              }
+            }
+          }
+#pragma unroll
+        for (int c = 0; c < CT; ++c)
+#pragma unroll
+          for (int q = 0; q < CR; ++q) {
+            const int tk = t0 + c * L, r = r0 + q;
+            if (tk < a.rows && r < a.topk) {
+              const int R = tk * a.topk + pl.ord[tk * a.topk + r];
+              if (pl.ids[R] < uint32_t(a.experts)) acc[c] = add_mul_nofma(acc[c], v[c][q], pv[c][q]);  // moe.comp:70 / :126
+            }
+          }
       }
-      a.out[size_t(tk) * a.hidden + row] = acc;
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const int tk = t0 + c * L;
+        if (tk < a.rows) a.out[size_t(tk) * a.hidden + row] = acc[c];
+      }
     }
   }
   dev::reset_counter(cctr, lane);
