@@ -222,72 +222,81 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
       }
     }
   }
-  if (wave > 0) return;
+  if (!DOWN && wave > 0) return;
 
-  // split-K: the last slice of (slot, tile) sums the slices in order
-  if (slices > 1) {
-    unsigned *ctr = &a.counters[(size_t(tile) * slots + slot) * kCounterStride];
-    if (!dev::last_arrival(ctr, unsigned(slices), lane)) return;
-    const float *pt = a.partial + size_t(tile) * slices * n * 64 + lane;
-    for (int m0 = 0; m0 < c; m0 += MT) {
-      float acc[MT];
-      dev::sum_slices<MT, 4>(
-          acc, [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices);
+  // split-K: the last slice of (slot, tile) sums the slices in order.  Down
+  // launch: the last (slot, tile) of a tile to finish then owns that tile's
+  // expert combine, which all four waves share.
+  __shared__ int owner;
+  if (wave == 0) {
+    bool last = true;
+    if (slices > 1) {
+      unsigned *ctr = &a.counters[(size_t(tile) * slots + slot) * kCounterStride];
+      last = dev::last_arrival(ctr, unsigned(slices), lane);
+      if (last) {
+        const float *pt = a.partial + size_t(tile) * slices * n * 64 + lane;
+        for (int m0 = 0; m0 < c; m0 += MT) {
+          float acc[MT];
+          dev::sum_slices<MT, 4>(
+              acc, [&](int s, int m) { return pt + (size_t(s) * n + pl.pos[min(m0 + m, c - 1)]) * 64; }, slices);
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
-        if (m0 + m < c) finish(pl.pos[m0 + m], acc[m]);
+          for (int m = 0; m < MT; ++m)
+            if (m0 + m < c) finish(pl.pos[m0 + m], acc[m]);
+        }
+        dev::reset_counter(ctr, lane);
+      }
     }
-    dev::reset_counter(ctr, lane);
+    if (!DOWN) return;
+    if (last) last = dev::last_arrival(&a.counters[(size_t(tiles) * slots + tile) * kCounterStride],
+                                       unsigned(pl.active), lane);
+    if (lane == 0) owner = last;
   }
   if (!DOWN) return;
+  __syncthreads();
+  if (!owner) return;
 
-  // expert combine: the last (slot, tile) of this tile to finish; lane (r, j)
-  // combines row r for tokens j, j+L, ...  The y values and probabilities of
-  // up to CT tokens x CR routes are loaded in one batch (independent loads in
-  // flight together), then summed in route order.
-  unsigned *cctr = &a.counters[(size_t(tiles) * slots + tile) * kCounterStride];
-  if (!dev::last_arrival(cctr, unsigned(pl.active), lane)) return;
+  // expert combine: lane (r, j) of wave w sums row r for tokens w*L + j,
+  // (w+4)*L + j, ...  The y values and probabilities of CT tokens x CR routes
+  // load in one branch-free batch (indices clamped in range, out-of-range
+  // entries dropped when summing), then add up in route order.
   if (row < nout) {
     constexpr int CT = 4, CR = 8;
-    for (int t0 = j; t0 < a.rows; t0 += CT * L) {
+    const int T = 4 * L;
+    for (int t0 = wave * L + j; t0 < a.rows; t0 += CT * T) {
       float acc[CT];
 #pragma unroll
-      for (int c = 0; c < CT; ++c) acc[c] = 0.0f;
+      for (int q = 0; q < CT; ++q) acc[q] = 0.0f;
       for (int r0 = 0; r0 < a.topk; r0 += CR) {
+        int R[CT][CR];
         float v[CT][CR], pv[CT][CR];
 #pragma unroll
-        for (int c = 0; c < CT; ++c)
+        for (int q = 0; q < CT; ++q)
 #pragma unroll
-          for (int q = 0; q < CR; ++q) {
-            const int tk = t0 + c * L, r = r0 + q;
-            v[c][q] = pv[c][q] = 0.0f;
-            if (tk < a.rows && r < a.topk) {
-              const int R = tk * a.topk + pl.ord[tk * a.topk + r];
-              if (pl.ids[R] < uint32_t(a.experts)) {
-                pv[c][q] = a.routes[n + R];
-                v[c][q] = dev::xload(a.y + size_t(R) * a.hidden + row);
-              }
-            }
+          for (int u = 0; u < CR; ++u) {
+            const int tk = min(t0 + q * T, a.rows - 1), r = min(r0 + u, a.topk - 1);
+            R[q][u] = tk * a.topk + pl.ord[tk * a.topk + r];
           }
 #pragma unroll
-        for (int c = 0; c < CT; ++c)
+        for (int q = 0; q < CT; ++q)
 #pragma unroll
-          for (int q = 0; q < CR; ++q) {
-            const int tk = t0 + c * L, r = r0 + q;
-            if (tk < a.rows && r < a.topk) {
-              const int R = tk * a.topk + pl.ord[tk * a.topk + r];
-              if (pl.ids[R] < uint32_t(a.experts)) acc[c] = add_mul_nofma(acc[c], v[c][q], pv[c][q]);  // moe.comp:70 / :126
-            }
+          for (int u = 0; u < CR; ++u) {
+            pv[q][u] = a.routes[n + R[q][u]];
+            v[q][u] = dev::xload(a.y + size_t(R[q][u]) * a.hidden + row);
+          }
+#pragma unroll
+        for (int q = 0; q < CT; ++q)
+#pragma unroll
+          for (int u = 0; u < CR; ++u) {
+            const bool ok = t0 + q * T < a.rows && r0 + u < a.topk && pl.ids[R[q][u]] < uint32_t(a.experts);
+            if (ok) acc[q] = add_mul_nofma(acc[q], v[q][u], pv[q][u]);  // moe.comp:70 / :126: out + y*p
           }
       }
 #pragma unroll
-      for (int c = 0; c < CT; ++c) {
-        const int tk = t0 + c * L;
-        if (tk < a.rows) a.out[size_t(tk) * a.hidden + row] = acc[c];
-      }
+      for (int q = 0; q < CT; ++q)
+        if (t0 + q * T < a.rows) a.out[size_t(t0 + q * T) * a.hidden + row] = acc[q];
     }
   }
-  dev::reset_counter(cctr, lane);
+  if (wave == 0) dev::reset_counter(&a.counters[(size_t(tiles) * slots + tile) * kCounterStride], lane);
 }
 
 template <int MT, int GSW>
