@@ -7,9 +7,10 @@
 // projection cannot start streaming its weights before the gate/up launch has
 // drained, and each launch pays its own ramp-up and split-K tail while HBM
 // idles.  Here every workgroup issues its down-projection weights straight
-// into LDS (buffer_load ... lds) together with its gate/up weights, so the
-// layer's weights stream as one, and each down item starts as soon as the
-// part of h it reads exists.
+// into LDS (buffer_load ... lds) as soon as its gate/up item is done, so the
+// layer's weights stream as one with every gate/up weight requested first
+// (h completes sooner), and each down item starts as soon as the part of h
+// it reads exists.
 //
 // Work items are exactly those of the two per-op launches (qnn_int4.hip):
 // gate/up items (tile, slice) of the I4_SWIGLU plan and down items of the
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   const int nsd = max(0, min(a.sps_dn, ld.steps - s0d));
   const int sgd = min(4 * a.sps_dn, ld.groups - wsd);
 
-  // ---- 1) Loads: x slice and gate/up weights to registers, down weights to LDS.
+  // ---- 1) Loads: x slice and gate/up weights to registers.
   float4 xr[1][dev::x_iters<GG>()];
   uint4 w[GG];
   uint4 q[dev::scale_quads<GG>()];
@@ -78,18 +79,6 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
                      tid);
   dev::load_wq<GG>(w, q, dev::rsrc((tile & 1) ? a.unib : a.gnib, lg.nib_bytes()),
                    dev::rsrc((tile & 1) ? a.uscl : a.gscl, lg.scale_bytes()), lg, tile >> 1, s0, lane);
-  if (dn_on) {
-    const dev::Rsrc dnib = dev::rsrc(a.dnib, ld.nib_bytes()), dscl = dev::rsrc(a.dscl, ld.scale_bytes());
-    const uint32_t at = uint32_t((size_t(td) * ld.steps + s0d) * 64 + lane);
-    const uint32_t qat = uint32_t((size_t(td) * ld.quads() + (s0d >> 2)) * 64 + lane);
-    typedef __attribute__((address_space(3))) void lds_t;
-#pragma unroll
-    for (int i = 0; i < QD; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dscl, (lds_t *)(dn_scl + i * kSclPiece), 16, qat * 16u, i * 1024u, 0, 0);
-#pragma unroll
-    for (int g = 0; g < GD; ++g)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dnib, (lds_t *)(dn_nib + g * kNibStep), 16, at * 16u, g * 1024u, 0, 0);
-  }
   float sc[GG];
   dev::pick_scales<GG>(sc, q, s0);  // after every load is issued
 
@@ -129,6 +118,21 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
     }
   }
   if (!dn_on) return;
+
+  // ---- Down weights into LDS, issued only now, so that the gate/up weights
+  //      of every workgroup are requested first and h is complete sooner.
+  {
+    const dev::Rsrc dnib = dev::rsrc(a.dnib, ld.nib_bytes()), dscl = dev::rsrc(a.dscl, ld.scale_bytes());
+    const uint32_t at = uint32_t((size_t(td) * ld.steps + s0d) * 64 + lane);
+    const uint32_t qat = uint32_t((size_t(td) * ld.quads() + (s0d >> 2)) * 64 + lane);
+    typedef __attribute__((address_space(3))) void lds_t;
+#pragma unroll
+    for (int i = 0; i < QD; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dscl, (lds_t *)(dn_scl + i * kSclPiece), 16, qat * 16u, i * 1024u, 0, 0);
+#pragma unroll
+    for (int g = 0; g < GD; ++g)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dnib, (lds_t *)(dn_nib + g * kNibStep), 16, at * 16u, g * 1024u, 0, 0);
+  }
 
   // ---- 3) Down item: wait for the blocks of h in its K-slice, stage them, dot
   //         with the weights already in LDS, split-K exchange, y.
