@@ -106,12 +106,11 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
     unsigned *ctr = &a.counters_gu[size_t(tile >> 1) * kCounterStride];
     if (dev::last_arrival(ctr, unsigned(2 * a.slices_gu), lane)) {
       const float *pt = a.partial_gu + size_t(tile & ~1) * a.slices_gu * 64 + lane;
-      float g[1], u[1];
-      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_gu);
-      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(a.slices_gu + s) * 64; }, a.slices_gu);
+      float gu[2];  // gate and up, their slices loaded in one batch
+      dev::sum_slices<2, 16>(gu, [&](int s, int m) { return pt + size_t(m * a.slices_gu + s) * 64; }, a.slices_gu);
       dev::reset_counter(ctr, lane);
       const int blk = tile >> 1, row = blk * 64 + lane;
-      if (row < a.inter) dev::xstore(a.h + row, dev::silu(g[0]) * u[0]);
+      if (row < a.inter) dev::xstore(a.h + row, dev::silu(gu[0]) * gu[1]);
       __builtin_amdgcn_s_waitcnt(0);  // the block's h is at the coherence point
       if (lane == 0)
         __hip_atomic_store(a.flags + size_t(blk) * 64, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -186,7 +185,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
     unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
     if (!dev::last_arrival(ctr, unsigned(a.slices_dn), lane)) return;
     const float *pt = a.partial_dn + size_t(td) * a.slices_dn * 64 + lane;
-    dev::sum_slices<1, 16>(acc, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_dn);
+    dev::sum_slices<1, 32>(acc, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_dn);
     dev::reset_counter(ctr, lane);
   }
   const int row = td * 64 + lane;

@@ -467,12 +467,11 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
     unsigned *ctr = &a.counters[size_t(pair) * kCounterStride];
     if (dev::last_arrival(ctr, unsigned(2 * slices_gu), lane)) {
       const float *pt = a.partial + size_t(tile & ~1) * slices_gu * 64 + lane;
-      float g[1], u[1];
-      dev::sum_slices<1, 16>(g, [&](int s, int) { return pt + size_t(s) * 64; }, slices_gu);
-      dev::sum_slices<1, 16>(u, [&](int s, int) { return pt + size_t(slices_gu + s) * 64; }, slices_gu);
+      float gu[2];  // gate and up, their slices loaded in one batch
+      dev::sum_slices<2, 16>(gu, [&](int s, int m) { return pt + size_t(m * slices_gu + s) * 64; }, slices_gu);
       dev::reset_counter(ctr, lane);
       const int row = blk * 64 + lane;
-      if (row < a.inter) dev::xstore(a.h + size_t(slot) * a.inter + row, dev::silu(g[0]) * u[0]);
+      if (row < a.inter) dev::xstore(a.h + size_t(slot) * a.inter + row, dev::silu(gu[0]) * gu[1]);
       __builtin_amdgcn_s_waitcnt(0);  // the block's h is at the coherence point
       if (lane == 0)
         __hip_atomic_store(a.flags + size_t(pair) * 64, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
