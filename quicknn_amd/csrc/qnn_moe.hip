@@ -530,14 +530,23 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
   if (!dev::last_arrival(ctr, unsigned(k * slices_dn), lane)) return;
   const float *pt = a.partial_dn + size_t(td) * k * slices_dn * 64 + lane;
-  float out = 0.0f;
-  for (int j = 0; j < k; ++j) {  // ascending expert id
-    float y[1];
-    if (slices_dn > 1)
-      dev::sum_slices<1, 16>(y, [&](int s, int) { return pt + (size_t(j) * slices_dn + s) * 64; }, slices_dn);
-    else
-      y[0] = dev::xload(pt + size_t(j) * 64);
-    out = add_mul_nofma(out, y[0], __shfl(prob, src_of(j)));  // moe.comp:70 / :126: out + y*p
+  // The k x slices partial sums (expert-major) load 32 at a time; each
+  // expert's y sums its slices in slice order, and out adds the experts in
+  // ascending id order.
+  float out = 0.0f, y = 0.0f;
+  const int total = k * slices_dn;
+  for (int i0 = 0; i0 < total; i0 += 32) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (i0 + i < total) v[i] = dev::xload(pt + size_t(i0 + i) * 64);
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (i0 + i < total) {
+        const int j = (i0 + i) / slices_dn, s = i0 + i - j * slices_dn;
+        y = s == 0 ? v[i] : y + v[i];
+        if (s == slices_dn - 1) out = add_mul_nofma(out, y, __shfl(prob, src_of(j)));  // moe.comp:70 / :126: out + y*p
+      }
   }
   dev::reset_counter(ctr, lane);
   const int row = td * 64 + lane;
