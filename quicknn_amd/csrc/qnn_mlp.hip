@@ -6,11 +6,10 @@
 // 238-248 is the same composition on the CPU).  As two launches, the down
 // projection cannot start streaming its weights before the gate/up launch has
 // drained, and each launch pays its own ramp-up and split-K tail while HBM
-// idles.  Here every workgroup issues its down-projection weights straight
-// into LDS (buffer_load ... lds) as soon as its gate/up item is done, so the
-// layer's weights stream as one with every gate/up weight requested first
-// (h completes sooner), and each down item starts as soon as the part of h
-// it reads exists.
+// idles.  Here every workgroup issues its down-projection weight loads as
+// soon as its gate/up item is done, so the layer's weights stream as one with
+// every gate/up weight requested first (h completes sooner), and each down
+// item starts as soon as the part of h it reads exists.
 //
 // Work items are exactly those of the two per-op launches (qnn_int4.hip):
 // gate/up items (tile, slice) of the I4_SWIGLU plan and down items of the
@@ -33,21 +32,15 @@
 namespace qnn {
 namespace {
 
-constexpr int kNibStep = 1024;   // nibble bytes of one wave step
-constexpr int kSclPiece = 1024;  // scale bytes of one wave's 4-step piece
-
 template <int GG, int GD>
 __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   extern __shared__ uint4 dyn_lds[];
   __shared__ float red[4][64];
   const int wave = dev::wave_id(), tid = threadIdx.x, lane = tid & 63, part = wave;
   const int wg = blockIdx.x;
-  uint8_t *lds = reinterpret_cast<uint8_t *>(dyn_lds);
   constexpr int QD = dev::scale_quads<GD>();
-  uint8_t *dn_nib = lds + size_t(part) * GD * kNibStep;                               // this wave's down nibbles
-  uint8_t *dn_scl = lds + size_t(4) * GD * kNibStep + size_t(part) * QD * kSclPiece;  // and scale pieces
   constexpr int XG = 4 * (GG > GD ? GG : GD);
-  const dev::XPlanes xs = dev::xplanes_at(lds + size_t(4) * (GD * kNibStep + QD * kSclPiece), 1, XG);
+  const dev::XPlanes xs = dev::xplanes_at(dyn_lds, 1, XG);
   const I4Layout &lg = a.lg, &ld = a.ld;
 
   // ---- gate/up item of this workgroup (qnn_int4.hip I4_SWIGLU, T = 1: units
@@ -118,23 +111,15 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   }
   if (!dn_on) return;
 
-  // ---- Down weights into LDS, issued only now, so that the gate/up weights
-  //      of every workgroup are requested first and h is complete sooner.
-  {
-    const dev::Rsrc dnib = dev::rsrc(a.dnib, ld.nib_bytes()), dscl = dev::rsrc(a.dscl, ld.scale_bytes());
-    const uint32_t at = uint32_t((size_t(td) * ld.steps + s0d) * 64 + lane);
-    const uint32_t qat = uint32_t((size_t(td) * ld.quads() + (s0d >> 2)) * 64 + lane);
-    typedef __attribute__((address_space(3))) void lds_t;
-#pragma unroll
-    for (int i = 0; i < QD; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dscl, (lds_t *)(dn_scl + i * kSclPiece), 16, qat * 16u, i * 1024u, 0, 0);
-#pragma unroll
-    for (int g = 0; g < GD; ++g)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dnib, (lds_t *)(dn_nib + g * kNibStep), 16, at * 16u, g * 1024u, 0, 0);
-  }
+  // ---- Down weights to registers, issued only now, so that the gate/up
+  //      weights of every workgroup are requested first and h is complete
+  //      sooner.
+  uint4 wd[GD];
+  uint4 qd[QD];
+  dev::load_wq<GD>(wd, qd, dev::rsrc(a.dnib, ld.nib_bytes()), dev::rsrc(a.dscl, ld.scale_bytes()), ld, td, s0d, lane);
 
   // ---- 3) Down item: wait for the blocks of h in its K-slice, stage them, dot
-  //         with the weights already in LDS, split-K exchange, y.
+  //         with the weights already in registers, split-K exchange, y.
   __syncthreads();  // xs and red are reused
   if (wave == 0) {
     const int b0 = (wsd * 32) >> 6, nb = (sgd * 32 + 63) >> 6;  // h blocks of the slice (<= 64)
@@ -155,15 +140,8 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   dev::load_x<1, GD, dev::kCoherent>(hr, dev::rsrc(a.h, size_t(a.inter) * 4), [](int) { return 0u; }, 1, wsd * 32,
                                     sgd * 32, tid);
   dev::stage_x<1, GD>(xs, hr, 1, wsd * 32, sgd * 32, a.inter, tid, lane);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's weights have landed in LDS
   __syncthreads();
-  uint4 wd[GD];
   float scd[GD];
-  uint4 qd[QD];
-#pragma unroll
-  for (int i = 0; i < QD; ++i) qd[i] = *reinterpret_cast<const uint4 *>(dn_scl + i * kSclPiece + lane * 16);
-#pragma unroll
-  for (int g = 0; g < GD; ++g) wd[g] = *reinterpret_cast<const uint4 *>(dn_nib + g * kNibStep + lane * 16);
   dev::pick_scales<GD>(scd, qd, s0d);
   acc[0] = 0.0f;
   if (nsd > 0) {
@@ -217,10 +195,7 @@ int capacity_of(int device) {
 
 }  // namespace
 
-size_t mlp_lds_bytes(int gg, int gd) {
-  const int qd = gd >= 4 ? gd / 4 : 1;
-  return size_t(4) * (gd * kNibStep + qd * kSclPiece) + dev::xplanes_bytes(1, 4 * std::max(gg, gd));
-}
+size_t mlp_lds_bytes(int gg, int gd) { return dev::xplanes_bytes(1, 4 * std::max(gg, gd)); }
 
 int mlp_capacity(int gg, int gd, int device) {
   if (gg == 4 && gd == 4) return capacity_of<4, 4>(device);
