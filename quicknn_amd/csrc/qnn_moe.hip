@@ -327,12 +327,7 @@ void launch_mt(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
 // like the dense SwiGLU (units padded to 16: the gate tile u and the up tile
 // u + 8 share an XCD).  Down units are (slot, block) with blocks padded to 8
 // per slot, so every arrival of a down block has the same blockIdx % 8.
-constexpr int kNibStep = 1024;   // nibble bytes of one wave step
-constexpr int kSclPiece = 1024;  // scale bytes of one wave's 4-step piece
-
-size_t moe_decode_lds(int g) {
-  return size_t(4) * (g * kNibStep + (g >= 4 ? g / 4 : 1) * kSclPiece) + dev::xplanes_bytes(1, 4 * g);
-}
+size_t moe_decode_lds(int g) { return dev::xplanes_bytes(1, 4 * g); }
 
 // J > 0: the token's routes are computed here from a.logits (GO_MOE_ROUTE
 // recorded just before, J = experts/64 rounded up to a power of two), by every
@@ -347,12 +342,9 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   const int wave = dev::wave_id(), tid = threadIdx.x, lane = tid & 63, part = wave;
   const int wg = blockIdx.x;
   const int k = a.topk;
-  uint8_t *lds = reinterpret_cast<uint8_t *>(dyn_lds);
   constexpr int QD = dev::scale_quads<GD>();
-  uint8_t *dn_nib = lds + size_t(part) * GD * kNibStep;
-  uint8_t *dn_scl = lds + size_t(4) * GD * kNibStep + size_t(part) * QD * kSclPiece;
   constexpr int XG = 4 * (GG > GD ? GG : GD);
-  const dev::XPlanes xs = dev::xplanes_at(lds + size_t(4) * (GD * kNibStep + QD * kSclPiece), 1, XG);
+  const dev::XPlanes xs = dev::xplanes_at(dyn_lds, 1, XG);
   const I4Layout &lg = a.gu, &ld = a.dn;
 
   // ---- route ranks: lane i < k holds route i; rank = its position in
@@ -412,7 +404,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
 
   const int eg = expert_of(slot), ed = expert_of(dslot);
 
-  // ---- 1) loads: x slice and gate/up weights to registers, down weights to LDS
+  // ---- 1) loads: x slice and gate/up weights to registers
   float4 xr[1][dev::x_iters<GG>()];
   uint4 w[GG];
   uint4 q[dev::scale_quads<GG>()];
@@ -422,19 +414,6 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
     const uint8_t *wb = a.gate_up + size_t(2 * eg + (tile & 1)) * a.gu_stride;
     dev::load_wq<GG>(w, q, dev::rsrc(wb, lg.nib_bytes()), dev::rsrc(wb + lg.nib_bytes(), lg.scale_bytes()), lg, blk,
                      s0, lane);
-  }
-  if (dn_on) {
-    const uint8_t *db = a.down + size_t(ed) * a.dn_stride;
-    const dev::Rsrc dnib = dev::rsrc(db, ld.nib_bytes()), dscl = dev::rsrc(db + ld.nib_bytes(), ld.scale_bytes());
-    const uint32_t at = uint32_t((size_t(td) * ld.steps + s0d) * 64 + lane);
-    const uint32_t qat = uint32_t((size_t(td) * ld.quads() + (s0d >> 2)) * 64 + lane);
-    typedef __attribute__((address_space(3))) void lds_t;
-#pragma unroll
-    for (int i = 0; i < QD; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dscl, (lds_t *)(dn_scl + i * kSclPiece), 16, qat * 16u, i * 1024u, 0, 0);
-#pragma unroll
-    for (int g = 0; g < GD; ++g)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dnib, (lds_t *)(dn_nib + g * kNibStep), 16, at * 16u, g * 1024u, 0, 0);
   }
   float sc[GG];
   dev::pick_scales<GG>(sc, q, s0);
@@ -479,9 +458,20 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   }
   if (!dn_on) return;
 
+  // ---- down weights to registers, issued only now, so that the gate/up
+  //      weights of every workgroup are requested first and h is complete
+  //      sooner.
+  uint4 wd[GD];
+  uint4 qd[QD];
+  {
+    const uint8_t *db = a.down + size_t(ed) * a.dn_stride;
+    dev::load_wq<GD>(wd, qd, dev::rsrc(db, ld.nib_bytes()), dev::rsrc(db + ld.nib_bytes(), ld.scale_bytes()), ld, td,
+                     s0d, lane);
+  }
+
   // ---- 3) down: wait for the blocks of h_slot in the K-slice, stage, dot
-  //         with the LDS weights, split-K exchange; the last arrival of the
-  //         block combines slices and experts.
+  //         with the weights in registers, split-K exchange; the last arrival
+  //         of the block combines slices and experts.
   __syncthreads();  // xs and red are reused
   if (wave == 0) {
     const int b0 = (wsd * 32) >> 6, nb = (sgd * 32 + 63) >> 6;  // h blocks of the slice (<= 64)
@@ -503,15 +493,8 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   dev::load_x<1, GD, dev::kCoherent>(hr, dev::rsrc(a.h + size_t(dslot) * a.inter, size_t(a.inter) * 4),
                                     [](int) { return 0u; }, 1, wsd * 32, sgd * 32, tid);
   dev::stage_x<1, GD>(xs, hr, 1, wsd * 32, sgd * 32, a.inter, tid, lane);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's weights have landed in LDS
   __syncthreads();
-  uint4 wd[GD];
   float scd[GD];
-  uint4 qd[QD];
-#pragma unroll
-  for (int i = 0; i < QD; ++i) qd[i] = *reinterpret_cast<const uint4 *>(dn_scl + i * kSclPiece + lane * 16);
-#pragma unroll
-  for (int g = 0; g < GD; ++g) wd[g] = *reinterpret_cast<const uint4 *>(dn_nib + g * kNibStep + lane * 16);
   dev::pick_scales<GD>(scd, qd, s0d);
   acc[0] = 0.0f;
   if (nsd > 0) {

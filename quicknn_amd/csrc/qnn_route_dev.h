@@ -28,8 +28,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Selection, then probabilities: the one-token MoE launch addresses its
 // weights with the ids alone and computes the probabilities while its loads
-// are in flight.  The probability phase uses no LDS (the launch's LDS-DMA
-// loads would otherwise make every LDS read wait for them).
+// are in flight.  The probability phase uses no LDS and no barrier, so it
+// does not hold up the waves that stage activations meanwhile.
 template <int J>
 struct RouteRow {
   float v[J];   // this lane's logits (experts j*64 + lane)
