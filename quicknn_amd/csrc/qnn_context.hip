@@ -606,7 +606,10 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
   if (cap <= 0 || grid > cap) return false;
   const size_t pf_gu = size_t(2 * lg.blocks) * pg.slices * 64, pf_dn = size_t(ld.blocks) * pd.slices * 64;
   const size_t c_gu = size_t(lg.blocks) * kCounterStride, c_dn = size_t(ld.blocks) * kCounterStride;
-  ensure_splitk(ctx, pf_gu + pf_dn, c_gu + c_dn);
+  // Sized for the per-op pair too: a graph capture of the same sequence runs
+  // it unfused, and a capture cannot grow the workspace.
+  ensure_splitk(ctx, std::max({pf_gu + pf_dn, pg.partial_floats, pd.partial_floats}),
+                std::max({c_gu + c_dn, pg.counters, pd.counters}));
   ensure_flags(ctx, size_t(lg.blocks) * 256);
   MlpLaunch a;
   a.lg = lg;

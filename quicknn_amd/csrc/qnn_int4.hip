@@ -258,14 +258,19 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   while (p.tiles_per_wg < 4 && (4 / p.tiles_per_wg) * l.lanes > 16) p.tiles_per_wg *= 2;  // slice fits x_iters
   const int P = 4 / p.tiles_per_wg;
   // Steps per wave: bounded by the template set (registers) and by the LDS of
-  // the workgroup's activation slice (at most 48 KiB).
-  const int set_max = p.mt == 1 ? 8 : (p.mt <= 8 ? 4 : 2);
+  // the workgroup's activation slice (at most 48 KiB).  One token: 4 steps
+  // per wave whatever the wave count.  Fewer steps give more waves but more
+  // split-K arrivals per tile, and at batch 1 the exchange costs more than
+  // the waves gain: 4 against the 1-2 a 3000-wave target picks was 5-16%
+  // faster at every measured decode shape (6144x2048 6.58 -> 6.18 us,
+  // 2560x2560 6.42 -> 5.38, 1024x2560 5.83 -> 4.97), and 8 was slower.
+  const int set_max = p.mt == 1 ? 4 : (p.mt <= 8 ? 4 : 2);
   const int lds_max = int((48 << 10) / (size_t(p.mt) * P * l.lanes * (dev::kXWords * 4 + 8)));
   const int cap = std::max(1, std::min(set_max, lds_max));
   // Steps per wave: the largest that splits the K-range into equal workgroup
   // slices (an uneven last slice was measured up to 40% slower) while giving
   // at least `target` waves; failing that, the largest that gives the waves.
-  const int target = env_int("QNN_I4_TARGET_WAVES", 3000);
+  const int target = env_int("QNN_I4_TARGET_WAVES", p.mt == 1 ? 1 : 3000);
   const int units = (tiles + p.tiles_per_wg - 1) / p.tiles_per_wg;
   auto waves = [&](int sps) { return size_t(units) * 4 * ((l.steps + P * sps - 1) / (P * sps)); };
   const int *set0 = p.mt == 1 ? kGsw1 : (p.mt <= 4 ? kGswN : kGswBig);
