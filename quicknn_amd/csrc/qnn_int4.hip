@@ -21,7 +21,9 @@ namespace qnn {
 namespace {
 using dev::sel4u;
 
-template <int MT, int GSW, int T>
+// MF: the inner product on the int8 matrix cores (dot_mf; L = 1, MT >= 4,
+// GSW a multiple of 4), bit-identical to the v_dot4 path.
+template <int MT, int GSW, int T, bool MF>
 __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int slices) {
   extern __shared__ uint4 dyn_lds[];
   __shared__ float red[4][MT][64];
@@ -66,9 +68,13 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
     b = t >> 1;
     if (t & 1) { nb = a.nib2; sb = a.scl2; }
   }
-  uint4 w[GSW];
-  float sc[GSW];
-  dev::load_w<GSW>(w, sc, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, wl);
+  uint4 w[MF ? 1 : GSW];
+  float sc[MF ? 1 : GSW];
+  dev::MfWeights<MF ? GSW : 4> mw;
+  if constexpr (MF)
+    dev::load_w_mf<GSW>(mw, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, lane);
+  else
+    dev::load_w<GSW>(w, sc, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, wl);
 
   // 2) Fixed-point activation planes in LDS.
   const dev::XPlanes xs = dev::xplanes_at(dyn_lds, MT, P * sps * L);
@@ -86,8 +92,18 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
     xp.q = xs.q + size_t(g0) * dev::kXWords;
     xp.s2 = xs.s2 + g0;
     xp.off = xs.off + g0;
-    dev::dot<MT, GSW>(acc, w, sc, xp, L, j, ns);
-    dev::reduce_lanes<MT>(acc, L);
+    if constexpr (MF) {
+      float accm[4][4];
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) accm[rq][r] = 0.0f;
+      dev::dot_mf<MT, GSW>(accm, mw, xp, ns, lane);
+      dev::mf_to_rows<MT>(acc, accm, &red[wave][0][0], lane);
+    } else {
+      dev::dot<MT, GSW>(acc, w, sc, xp, L, j, ns);
+      dev::reduce_lanes<MT>(acc, L);
+    }
   }
   if (P > 1) {
     if (part > 0) {
@@ -186,13 +202,25 @@ __global__ void k_int4_dequant(I4Layout l, const uint4 *__restrict__ nib, const 
   out[idx] = float(n - 8) * scl[l.scale_at(b, s, lane)];
 }
 
+template <int MT, int GSW, bool MF>
+void launch_tpw(const I4Launch &a, const I4Plan &p, hipStream_t st) {
+  switch (p.tiles_per_wg) {
+    case 1: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 1, MF>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
+    case 2: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 2, MF>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
+    default: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 4, MF>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
+  }
+}
+// Several tokens over one-lane rows with 4 steps per wave: the matrix-core
+// inner product (QNN_I4_MFMA=0 keeps v_dot4).
 template <int MT, int GSW>
 void launch_one(const I4Launch &a, const I4Plan &p, hipStream_t st) {
-  switch (p.tiles_per_wg) {
-    case 1: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 1>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
-    case 2: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 2>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
-    default: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 4>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
+  if constexpr (MT >= 4 && GSW == 4) {
+    if (a.l.lanes == 1 && env_int("QNN_I4_MFMA", 1) != 0) {
+      launch_tpw<MT, GSW, true>(a, p, st);
+      return;
+    }
   }
+  launch_tpw<MT, GSW, false>(a, p, st);
 }
 
 // Steps-per-wave templates by token count (register budget).

@@ -280,6 +280,105 @@ __device__ __forceinline__ void dot(float (&acc)[MT], const uint4 (&w)[GSW], con
   }
 }
 
+// ---- Several tokens on the int8 matrix cores (L = 1, MT >= 4, GSW >= 4).
+// Per group and 16-row quarter rq of the block, one v_mfma_i32_16x16x32_i8
+// per activation plane: A = the plane (16 tokens x 32 elements; lane l gives
+// token l%16, elements 8c..8c+7 of the group, c = l/16, as plane words 2c and
+// 2c+1), B = the nibbles (32 elements x 16 rows; lane l gives row 16rq + l%16,
+// the same elements: the low then the high nibbles of its dword c).  Both
+// orders are [8c+0,2,4,6, 8c+1,3,5,7], so D[token][row] is the group's exact
+// integer dot of that plane, the sum dot() forms with v_dot4; the fp32 step
+// (isum, then fma with s*s2) is the same, so results are bit-identical to
+// dot().  Lane l holds D[4c + r][l%16], r = 0..3: tokens 4c..4c+3 of row
+// 16rq + l%16.  Token rows >= MT read token 0's plane and are discarded.
+//
+// The weights are loaded straight into that pattern: lane l takes dword c of
+// row 16rq + l%16 (per step four 4-byte loads, each over 256 contiguous bytes
+// of the step's 1 KiB), and the scales of those rows (one 16-byte scale piece
+// per quarter and 4 steps).
+template <int GSW>
+struct MfWeights {
+  uint32_t w[GSW][4];  // [step][quarter]: dword c of row 16*quarter + l%16
+  float sc[GSW][4];    // [step][quarter]: its scale
+};
+template <int GSW>
+__device__ __forceinline__ void load_w_mf(MfWeights<GSW> &mw, Rsrc nib, Rsrc scl, const I4Layout &l, int b, int s0,
+                                          int lane) {
+  static_assert(GSW % 4 == 0, "scale pieces hold 4 aligned steps");
+  const int p = lane & 15, c = lane >> 4;
+  const uint32_t at = uint32_t(size_t(b) * l.steps + s0) * 1024u + uint32_t(p * 16 + c * 4);
+  const uint32_t qat = uint32_t((size_t(b) * l.quads() + (s0 >> 2)) * 64 + p) * 16u;
+  uint4 q[GSW / 4][4];
+#pragma unroll
+  for (int i = 0; i < GSW / 4; ++i)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) q[i][rq] = ld128(scl, qat + uint32_t(rq) * 256u, uint32_t(i) * 1024u);
+#pragma unroll
+  for (int g = 0; g < GSW; ++g)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq)
+      mw.w[g][rq] = __builtin_amdgcn_raw_buffer_load_b32(nib, int(at + uint32_t(rq) * 256u), int(g * 1024), 0);
+#pragma unroll
+  for (int g = 0; g < GSW; ++g)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) mw.sc[g][rq] = __uint_as_float(sel4u(q[g >> 2][rq], g & 3));
+}
+
+typedef int mf_i32x4 __attribute__((ext_vector_type(4)));
+
+// acc[rq][r] += the group sums of steps 0..ns-1 for token 4c + r, row
+// 16rq + l%16 (the layout above), in step order.
+template <int MT, int GSW>
+__device__ __forceinline__ void dot_mf(float (&acc)[4][4], const MfWeights<GSW> &mw, const XPlanes &xs, int ns,
+                                       int lane) {
+  const int p = lane & 15, c = lane >> 4;
+  const int ta = p < MT ? p : 0;  // A row token
+#pragma unroll
+  for (int g = 0; g < GSW; ++g) {
+    if (g < ns) {
+      const uint32_t *qa = xs.q + (size_t(ta) * xs.groups + g) * kXWords;
+      const long ah = *reinterpret_cast<const long *>(qa + 2 * c);
+      const long al = *reinterpret_cast<const long *>(qa + 8 + 2 * c);
+      float s2[4];
+      int off[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * c + r < MT ? 4 * c + r : 0;
+        s2[r] = xs.s2[size_t(m) * xs.groups + g];
+        off[r] = xs.off[size_t(m) * xs.groups + g];
+      }
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const uint32_t wd = mw.w[g][rq];
+        const long bw = long(wd & 0x0F0F0F0Fu) | (long((wd >> 4) & 0x0F0F0F0Fu) << 32);
+        const mf_i32x4 z = {0, 0, 0, 0};
+        const mf_i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
+        const mf_i32x4 dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bw, z, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int isum = (dh[r] << 8) + dl[r] + off[r];
+          acc[rq][r] = fmaf(float(isum), mw.sc[g][rq] * s2[r], acc[rq][r]);
+        }
+      }
+    }
+  }
+}
+
+// The MFMA layout -> one row per lane (acc[m] = token m of row `lane`),
+// through this wave's [MT][64] LDS slot.
+template <int MT>
+__device__ __forceinline__ void mf_to_rows(float (&acc)[MT], const float (&accm)[4][4], float *slot, int lane) {
+  const int p = lane & 15, c = lane >> 4;
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (4 * c + r < MT) slot[(4 * c + r) * 64 + 16 * rq + p] = accm[rq][r];
+  wave_lds_sync();
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = slot[m * 64 + lane];
+}
+
 // Sum over the L lanes of each row (L a power of two): afterwards every lane
 // of a row holds the row total.  Pairwise order, identical in every launch.
 template <int MT>

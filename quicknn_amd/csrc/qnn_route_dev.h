@@ -13,18 +13,10 @@
 // taken as each lane's experts in ascending id, then a butterfly sum broadcast
 // from lane 0; renormalisation divides by the top-k sum in rank order.
 #pragma once
-#include "qnn_internal.h"
+#include "qnn_exchange.h"
 
 namespace qnn {
 namespace dev {
-
-// LDS ordering between the lanes of one wave (LDS operations of a wave run in
-// order; this keeps the compiler from moving them across).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Selection, then probabilities: the one-token MoE launch addresses its
 // weights with the ids alone and computes the probabilities while its loads

@@ -195,3 +195,27 @@ def test_lane_layouts_and_tile_groupings(ctx, rng, monkeypatch, lanes, tpw):
     got8 = ctx.Download(dst8).reshape(8, 768)
     for r in range(8):
         assert normwise_rel_err(got8[r], oracle.cpu_linear(pg, oracle.ENC_INT4, x8[r], 2048, 768)) <= TOL, r
+
+
+@pytest.mark.parametrize("rows", [4, 5, 8])
+def test_multi_token_matrix_cores_match_dot4(ctx, rng, monkeypatch, rows):
+    """4-8 tokens over one-lane rows with 4 steps per wave run the inner product on the int8
+    matrix cores: bit-identical to the v_dot4 path (QNN_I4_MFMA=0) and within tolerance of the
+    CPU path, including a partial last block of rows and a slice shorter than a wave's steps."""
+    monkeypatch.setenv("QNN_I4_SPS", "4")
+    for n, k in [(2560, 9728), (1000, 2560), (200, 96)]:
+        p = make_int4(rng, n, k)
+        w = hip.MemoryBlock.int4(p)
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        src, dst = ctx.UploadRaw(x), ctx.NewTensor(rows * n)
+        got = {}
+        for mf in ("1", "0"):
+            monkeypatch.setenv("QNN_I4_MFMA", mf)
+            ctx.Int4Linear(dst, src, w, rows, k, n)
+            got[mf] = ctx.Download(dst).reshape(rows, n)
+        assert np.array_equal(got["1"].view(np.uint32), got["0"].view(np.uint32)), (n, k)
+        for r in range(rows):
+            want = oracle.cpu_linear(p, oracle.ENC_INT4, x[r], k, n)
+            assert normwise_rel_err(got["1"][r], want) <= TOL, (n, k, r)
+        ctx.Recycle(src)
+        ctx.Recycle(dst)
