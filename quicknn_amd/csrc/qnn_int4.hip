@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   // 4) Split-K across workgroups: the last slice of a tile to finish sums all
   //    slices in slice order.  I4_SWIGLU always meets here: the last of the
   //    2 x slices arrivals of a block sums the gate slices and the up slices.
-  constexpr int PU = MT >= 8 ? 2 : (MT >= 4 ? 4 : 16);  // independent partial loads in flight
+  constexpr int PU = MT >= 16 ? 2 : (MT >= 8 ? 4 : (MT >= 4 ? 8 : 16));  // independent partial loads in flight
   float accu[MT];
   if (slices > 1 || swiglu) {
     float *part_p = a.partial + (size_t(tile) * slices + slice) * MT * 64 + lane;
