@@ -97,6 +97,7 @@ typedef struct {
   uint64_t linear_grouped; /* one-row GGUF Linear calls that ran in a shared launch (no reference counterpart) */
   uint64_t moe_fused;      /* one-token qnn_moe_experts calls run as a single launch (no reference counterpart) */
   uint64_t moe_route_fused; /* of those, with the preceding GO_MOE_ROUTE computed in the launch (no reference counterpart) */
+  uint64_t glu_fused;      /* multi-row Int4Linear gate + up + GO_SWIGLU triples run as one launch (no reference counterpart) */
 } qnn_status;
 
 /* ---------------------------------------------------------------------------
@@ -150,7 +151,11 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
                const qnn_weight *bias, int rows, int in_dim, int out_dim);
 
 /* Int4Linear (Context.API.inc:138-142, Implementation.inc:1080-1135):
- * 1 <= rows <= 128; weight U8/NATIVE [out_dim, Int4RowBytes(in_dim)], offset 0. */
+ * 1 <= rows <= 128; weight U8/NATIVE [out_dim, Int4RowBytes(in_dim)], offset 0.
+ * A multi-row call may be recorded and launched with the next call: two on
+ * the same input followed by QNN_GO_SWIGLU of their outputs (the engine's
+ * multi-row MLP) run as one gate/up SwiGLU launch that also writes both
+ * outputs, bit-identical to the three separate operations. */
 int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
                     int out_dim);
 

@@ -101,6 +101,16 @@ struct qnn_ctx_s {
     float *y[qnn::kGGMaxGroup] = {};
     int out[qnn::kGGMaxGroup] = {}, slices[qnn::kGGMaxGroup] = {};
   } lgroup;  // co-resident workgroups of the fused MLP kernel per (gate/up, down) steps (0: not asked yet, -1: none)
+  // Multi-row Int4Linear calls recorded to meet a GO_SWIGLU: the first, then
+  // a second on the same input and shape; when the next call is GO_SWIGLU of
+  // their two outputs, the three run as one gate/up SwiGLU launch.
+  struct PendingRows {
+    int count = 0;
+    qnn::WeightEntry *e[2] = {};
+    float *y[2] = {};
+    const float *x = nullptr;
+    int rows = 0, in = 0, out = 0;
+  } prows;
   hipEvent_t events[64] = {};
   bool capturing = false;
   std::vector<qnn::WeightEntry *> capture_pins;
@@ -141,7 +151,7 @@ void check_ctx(qnn_ctx_s *ctx, bool keep_pending = false) {
   // Context.Implementation.inc:70-71: resident work stays on its creating thread.
   if (std::this_thread::get_id() != ctx->owner) fail(QNN_E_INVALID_OP, "context used from a thread other than its creator");
   hip_check(hipSetDevice(ctx->device), "hipSetDevice");
-  if (!keep_pending && (ctx->pending.on || ctx->lgroup.count || ctx->proute.on)) settle_pending(ctx);
+  if (!keep_pending && (ctx->pending.on || ctx->lgroup.count || ctx->proute.on || ctx->prows.count)) settle_pending(ctx);
 }
 
 // Check (Context.Implementation.inc): a live tensor of at least `minimum` floats.
@@ -448,7 +458,7 @@ struct OpPins {
 
 // ---------------------------------------------------------------- INT4 projection
 void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
-              int rows, int in_dim, int out_dim, const float *prob) {
+              int rows, int in_dim, int out_dim, const float *prob, float *g_out = nullptr, float *u_out = nullptr) {
   const I4Layout &l = w->i4;
   // The kernels read activation rows as aligned 4-float pieces: a row length
   // that is not a multiple of 4 goes through a zero-padded copy.
@@ -480,6 +490,10 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
     a.tiles = mode == I4_SWIGLU ? 2 * l.blocks : l.blocks;
     a.mode = mode;
     a.prob = prob;
+    if (g_out) {
+      a.g_out = g_out + size_t(r0) * out_dim;
+      a.u_out = u_out + size_t(r0) * out_dim;
+    }
     const I4Plan p = int4_plan(l, m, mode);
     ensure_splitk(ctx, p.partial_floats, p.counters);
     a.partial = ctx->partial;
@@ -562,6 +576,14 @@ void settle_pending(qnn_ctx_s *ctx) {
     misc_moe_route(r.routes, r.logits, 1, r.experts, r.k, r.normalize, ctx->stream);
   }
   if (ctx->lgroup.count) launch_linear_group(ctx);
+  if (ctx->prows.count) {
+    const qnn_ctx_s::PendingRows q = ctx->prows;
+    ctx->prows = {};
+    for (int i = 0; i < q.count; ++i) {
+      q.e[i]->pins--;
+      run_int4(ctx, q.e[i], nullptr, I4_STORE, q.x, q.y[i], q.rows, q.in, q.out, nullptr);
+    }
+  }
   if (!ctx->pending.on) return;
   const qnn_ctx_s::Pending p = ctx->pending;
   ctx->pending = {};
@@ -571,6 +593,20 @@ void settle_pending(qnn_ctx_s *ctx) {
 }
 
 bool mlp_fusion_enabled() { return env_int("QNN_FUSE_MLP", 1) != 0; }
+
+// A gate/up SwiGLU launch gives each row the sums the two I4_STORE launches
+// would (same steps per wave, slices and parts for every 16-row chunk), so
+// the recorded triple stays bit-identical to the separate operations.
+bool glu_plans_match(const I4Layout &l, int rows) {
+  for (int r0 = 0; r0 < rows; r0 += 16) {
+    const int m = std::min(16, rows - r0);
+    const I4Plan a = int4_plan(l, m, I4_STORE), b = int4_plan(l, m, I4_SWIGLU);
+    if (a.mt != b.mt || a.gsw != b.gsw || a.steps_per_slice != b.steps_per_slice || a.slices != b.slices ||
+        a.tiles_per_wg != b.tiles_per_wg)
+      return false;
+  }
+  return true;
+}
 
 // Completion flags of the single-launch kernels (fused MLP, one-token MoE):
 // words 256 B apart that hold the epoch of the launch that last completed the
@@ -974,7 +1010,28 @@ int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_we
       // The down projection of a recorded SwiGLU: one launch for the MLP.
       const bool fused = p.on && rows == 1 && src->ptr == p.h && in_dim == p.out && out_dim == p.in &&
                          dst->ptr != p.h && try_fused_mlp(ctx, e, dst->ptr);
-      if (!fused) {
+      // Several rows: recorded to meet a following GO_SWIGLU (gate, up).
+      qnn_ctx_s::PendingRows &q = ctx->prows;
+      if (!fused && rows >= 2 && !ctx->capturing && mlp_fusion_enabled() && glu_plans_match(e->i4, rows)) {
+        if (q.count == 1 && q.x == src->ptr && q.rows == rows && q.in == in_dim && q.out == out_dim &&
+            dst->ptr != q.y[0] && e->i4.rows == q.e[0]->i4.rows && e->i4.cols == q.e[0]->i4.cols &&
+            e->i4.lanes == q.e[0]->i4.lanes) {
+          e->pins++;
+          q.e[1] = e;
+          q.y[1] = dst->ptr;
+          q.count = 2;
+        } else {
+          settle_pending(ctx);
+          e->pins++;
+          q.count = 1;
+          q.e[0] = e;
+          q.y[0] = dst->ptr;
+          q.x = src->ptr;
+          q.rows = rows;
+          q.in = in_dim;
+          q.out = out_dim;
+        }
+      } else if (!fused) {
         settle_pending(ctx);
         run_int4(ctx, e, nullptr, I4_STORE, src->ptr, dst->ptr, rows, in_dim, out_dim, nullptr);
       }
@@ -1120,7 +1177,9 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
 int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_tensor *b, qnn_tensor *c,
                const int *args, int nargs) {
   return guarded([&] {
-    check_ctx(ctx);
+    // A GO_SWIGLU may complete a recorded gate/up pair (checked below).
+    const bool glu_pair = op == QNN_GO_SWIGLU && ctx && ctx == g_ctx && ctx->prows.count == 2;
+    check_ctx(ctx, glu_pair);
     auto arg = [&](int i) -> int {
       if (i >= nargs || !args) fail(QNN_E_ARGUMENT, "missing kernel argument");
       return args[i];
@@ -1150,6 +1209,19 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
         check_tensor(ctx, dst, n);
         check_tensor(ctx, a, inter_leaved ? int64_t(n) * 2 : n);
         if (!inter_leaved) check_tensor(ctx, b, n);
+        if (glu_pair) {
+          const qnn_ctx_s::PendingRows q = ctx->prows;
+          if (!inter_leaved && a->ptr == q.y[0] && b->ptr == q.y[1] && inter == q.out &&
+              int64_t(n) == int64_t(q.rows) * q.out && dst->ptr != q.x) {
+            ctx->prows = {};
+            q.e[0]->pins--;
+            q.e[1]->pins--;
+            run_int4(ctx, q.e[0], q.e[1], I4_SWIGLU, q.x, dst->ptr, q.rows, q.in, q.out, nullptr, q.y[0], q.y[1]);
+            ctx->st.glu_fused++;
+            return QNN_OK;
+          }
+          settle_pending(ctx);
+        }
         if (n) misc_glu(dst->ptr, a->ptr, inter_leaved ? nullptr : b->ptr, n, inter, inter_leaved,
                         op == QNN_GO_GEGLU, ctx->stream);
         return QNN_OK;

@@ -147,7 +147,13 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
     const int row = b * l.rpb + wl / L;
 #pragma unroll
     for (int m = 0; m < MT; ++m)
-      if (j == 0 && row < a.n && m < a.m) a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * accu[m];
+      if (j == 0 && row < a.n && m < a.m) {
+        if (a.g_out) {
+          a.g_out[size_t(m) * a.y_stride + row] = acc[m];
+          a.u_out[size_t(m) * a.y_stride + row] = accu[m];
+        }
+        a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * accu[m];
+      }
   } else {
     const int row = b * l.rpb + lane / L;
     if (j == 0 && row < a.n) {

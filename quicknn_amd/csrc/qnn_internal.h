@@ -120,6 +120,8 @@ struct I4Launch {
   int steps_per_slice = 0;  // steps per wave (a workgroup slice is 4/T times that)
   int mode = I4_STORE;
   const float *prob = nullptr;  // I4_ACCUM: pointer to p
+  float *g_out = nullptr;       // I4_SWIGLU, optional: the gate and up sums too (y_stride apart)
+  float *u_out = nullptr;
   float *partial = nullptr;     // split-K scratch
   unsigned *counters = nullptr;
   int *err = nullptr;           // error word

@@ -73,7 +73,8 @@ class Status(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in (
         "gemm_calls", "gguf_calls", "int4_calls", "moe_calls", "weight_uploads", "weight_upload_bytes",
         "weight_cache_hits", "weight_cache_misses", "weight_evictions", "readbacks", "submissions",
-        "weight_bytes", "weight_limit", "activation_bytes", "activation_peak_bytes", "mlp_fused", "linear_grouped", "moe_fused", "moe_route_fused")]
+        "weight_bytes", "weight_limit", "activation_bytes", "activation_peak_bytes", "mlp_fused", "linear_grouped", "moe_fused", "moe_route_fused",
+        "glu_fused")]
 
 
 _lib = None
