@@ -569,15 +569,16 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
   p.mt = 1;
   const int fmt = env_int("QNN_MOE_MT", 0);
   if (fmt == 1 || fmt == 2 || fmt == 4) p.mt = fmt;
-  // Steps per wave: 8 for one token (the single launch), 4 otherwise,
-  // measured fastest for 128 experts of 768 x 2048 (1 token: 16.0 us against
-  // 17.9 at 2 steps; 2-32 tokens: 14-16% faster than 2 steps, and than 8);
-  // QNN_MOE_SPS overrides.  Bounded by the activation-slice LDS budget.
+  // Steps per wave: 8 with one token per pass, 4 with several, measured
+  // fastest for 128 experts of 768 x 2048 (one token per pass, 2-64 rows: 8
+  // steps 4-17% faster than 4, e.g. 16 rows 129 -> 114 us; 2 tokens per pass:
+  // 4 steps 14-16% faster than 2 and than 8); QNN_MOE_SPS overrides.  Bounded
+  // by the activation-slice LDS budget.
   const int forced = env_int("QNN_MOE_SPS", 0);
   auto steps = [&](const I4Layout &l, int) {
     const int lds_cap = int((48 << 10) / (size_t(p.mt) * 4 * l.lanes * (dev::kXWords * 4 + 8)));
     const int cap = std::max(1, std::min(8, lds_cap));
-    return std::min(forced > 0 ? forced : (a.rows == 1 ? 8 : 4), cap);
+    return std::min(forced > 0 ? forced : (p.mt == 1 ? 8 : 4), cap);
   };
   p.sps_gu = steps(a.gu, 2 * a.gu.blocks);
   p.sps_dn = steps(a.dn, a.dn.blocks);
