@@ -28,7 +28,7 @@
 //   Q3_K: sum = s2 * d*(sc-32) * (dot(q3, X) - 4 sum(X))        (q3 = q + 4)
 //   Q8_0: sum = s2 * d * dot(q, X)
 // where X = 256 q1 + q2 and every dot is exact integer arithmetic.
-#include "qnn_exchange.h"
+#include "qnn_int4_dev.h"  // buffer-load helpers (rsrc, ld128, ld32f) and the exchange
 
 namespace qnn {
 namespace {
@@ -385,23 +385,23 @@ __global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   const int uw0 = wave * BW;
   const int nuw = max(0, min(BW, nu - uw0));
 
-  // 1) activation slice (elements [u0*256, (u0+nu)*256) of token 0)
+  // 1) activation slice (elements [u0*256, (u0+nu)*256) of token 0).  Loads
+  //    are issued without per-lane branches (buffer loads past the row return
+  //    0; pieces past the slice are zeroed when quantised), so the compiler
+  //    can wait for them alone while the weight loads below are in flight.
   constexpr int XIT = (U * 256 + 1023) / 1024;
   float4 xr[XIT];
+  const dev::Rsrc xsrc = dev::rsrc(a.x, size_t(l.cols) * 4);
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
-    const int e = (it * 256 + tid) * 4, kk = u0 * 256 + e;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (e < nu * 256) {
-      if (kk + 3 < l.cols && a.x_vec4) v = *reinterpret_cast<const float4 *>(a.x + kk);
-      else {
-        if (kk < l.cols) v.x = a.x[kk];
-        if (kk + 1 < l.cols) v.y = a.x[kk + 1];
-        if (kk + 2 < l.cols) v.z = a.x[kk + 2];
-        if (kk + 3 < l.cols) v.w = a.x[kk + 3];
-      }
+    const uint32_t kb = uint32_t(u0 * 256 + (it * 256 + tid) * 4) * 4u;
+    if (a.x_vec4) {  // uniform
+      const uint4 v = dev::ld128(xsrc, kb, 0);
+      xr[it] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    } else {
+      xr[it] = make_float4(dev::ld32f(xsrc, kb, 0), dev::ld32f(xsrc, kb + 4, 0), dev::ld32f(xsrc, kb + 8, 0),
+                           dev::ld32f(xsrc, kb + 12, 0));
     }
-    xr[it] = v;
   }
   // 2) weights of this wave's units
   int stile = tile, srow = lane;
@@ -415,30 +415,31 @@ __global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   uint4 mw[BW][F::C];
   uint4 s1v[BW];
   uint32_t s1w[BW], s2w[BW];
+  // Units past this wave's share re-read the slice's last unit (no per-unit
+  // branch, so no load waits for another) and are skipped by the dot.
 #pragma unroll
   for (int b = 0; b < BW; ++b) {
-    if (b < nuw) {
-      const size_t tu = size_t(stile) * l.units + (u0 + uw0 + b);
-      const uint4 *mp = reinterpret_cast<const uint4 *>(P.main) + (tu * F::C) * 64 + srow;
+    const size_t tu = size_t(stile) * l.units + (u0 + min(uw0 + b, nu - 1));
+    const uint4 *mp = reinterpret_cast<const uint4 *>(P.main) + (tu * F::C) * 64 + srow;
 #pragma unroll
-      for (int c = 0; c < F::C; ++c) mw[b][c] = mp[c * 64];
-      if (F::S1 == 16) s1v[b] = reinterpret_cast<const uint4 *>(P.side1)[tu * 64 + srow];
-      if (F::S1 == 12) {
-        const uint32_t *q = reinterpret_cast<const uint32_t *>(P.side1 + (tu * 64 + srow) * 12);
-        s1v[b] = make_uint4(q[0], q[1], q[2], 0u);
-      }
-      if (F::S1 == 4) s1w[b] = reinterpret_cast<const uint32_t *>(P.side1)[tu * 64 + srow];
-      if (F::S1 == 2) s1w[b] = reinterpret_cast<const uint16_t *>(P.side1)[tu * 64 + srow];
-      if (F::S2 == 2) s2w[b] = reinterpret_cast<const uint16_t *>(P.side2)[tu * 64 + srow];
+    for (int c = 0; c < F::C; ++c) mw[b][c] = mp[c * 64];
+    if (F::S1 == 16) s1v[b] = reinterpret_cast<const uint4 *>(P.side1)[tu * 64 + srow];
+    if (F::S1 == 12) {
+      const uint32_t *q = reinterpret_cast<const uint32_t *>(P.side1 + (tu * 64 + srow) * 12);
+      s1v[b] = make_uint4(q[0], q[1], q[2], 0u);
     }
+    if (F::S1 == 4) s1w[b] = reinterpret_cast<const uint32_t *>(P.side1)[tu * 64 + srow];
+    if (F::S1 == 2) s1w[b] = reinterpret_cast<const uint16_t *>(P.side1)[tu * 64 + srow];
+    if (F::S2 == 2) s2w[b] = reinterpret_cast<const uint16_t *>(P.side2)[tu * 64 + srow];
   }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the quantisation below waits for x
   // 3) quantise the activation slice (natural element order)
   __shared__ XSlice<NG> xs;
   __shared__ float red[3][64];
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
     const int e = (it * 256 + tid) * 4;
-    const float4 v = xr[it];
+    const float4 v = e < nu * 256 ? xr[it] : make_float4(0.f, 0.f, 0.f, 0.f);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1));
     amax = fmaxf(amax, __shfl_xor(amax, 2));
