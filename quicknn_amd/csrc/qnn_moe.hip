@@ -44,11 +44,19 @@ __device__ void build_plan(MoEPlan &pl, const MoELaunch &a, int n, int slot, int
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   bool bad = false;
-  for (int i = lane; i < n; i += 64) {
-    const uint32_t id = __float_as_uint(a.routes[i]);
-    pl.ids[i] = id;
-    if (id < uint32_t(a.experts)) atomicOr(&pl.mask[id >> 5], 1u << (id & 31));
-    else bad = true;
+  for (int i0 = 0; i0 < n; i0 += 256) {  // 4 route ids per lane in flight together
+    uint32_t idv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) idv[r] = __float_as_uint(a.routes[min(i0 + r * 64 + lane, n - 1)]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = i0 + r * 64 + lane;
+      if (i < n) {
+        pl.ids[i] = idv[r];
+        if (idv[r] < uint32_t(a.experts)) atomicOr(&pl.mask[idv[r] >> 5], 1u << (idv[r] & 31));
+        else bad = true;
+      }
+    }
   }
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
