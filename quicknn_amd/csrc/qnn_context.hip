@@ -143,6 +143,8 @@ int guarded(F &&f) {
 }
 
 void settle_pending(qnn_ctx_s *ctx);
+void run_gguf(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
+              int out_dim, float *g_out = nullptr, float *u_out = nullptr);
 
 // Every entry point starts here.  A recorded SwiGLU is launched first unless
 // the caller is the Int4Linear that may fuse with it (keep_pending).
@@ -546,6 +548,30 @@ void launch_linear_group(qnn_ctx_s *ctx) {
 
 bool linear_grouping_enabled() { return env_int("QNN_GROUP_LINEAR", 1) != 0; }
 
+// A recorded one-row GGUF group of exactly a gate and an up projection of one
+// shape, completed by a GLU of their two outputs: one gate/up pair launch
+// (GG_SWIGLU / GG_GEGLU) that also writes both outputs.  Only where the pair
+// launch's plan has the group's units per wave and slices, so every output
+// is bit-identical to the grouped launch followed by the GLU.
+bool try_glu_group(qnn_ctx_s *ctx, int op, int n, int interleaved, qnn_tensor_s *dst, qnn_tensor_s *a,
+                   qnn_tensor_s *b) {
+  const qnn_ctx_s::LinearGroup &g = ctx->lgroup;
+  if (g.count != 2 || interleaved || !b || a->ptr != g.y[0] || b->ptr != g.y[1] || dst->ptr == g.x) return false;
+  const GGLayout &l0 = g.e[0]->gg, &l1 = g.e[1]->gg;
+  if (l0.enc != l1.enc || l0.rows != l1.rows || l0.cols != l1.cols || g.out[0] != g.out[1] || n != g.out[0])
+    return false;
+  int bw = 0, slices = 0;
+  gguf_plan(l0, (g.out[0] + 31) / 32, &bw, &slices);
+  if (bw != g.bw || slices != g.slices[0] || slices != g.slices[1]) return false;
+  const qnn_ctx_s::LinearGroup q = g;
+  ctx->lgroup = {};
+  q.e[0]->pins--;
+  q.e[1]->pins--;
+  run_gguf(ctx, q.e[0], q.e[1], op == QNN_GO_GEGLU ? GG_GEGLU : GG_SWIGLU, q.x, dst->ptr, q.out[0], q.y[0], q.y[1]);
+  ctx->st.glu_fused++;
+  return true;
+}
+
 // Records a one-row GGUF Linear into the group, launching what was recorded
 // first when it does not fit.
 void record_linear(qnn_ctx_s *ctx, WeightEntry *e, const float *x, float *y, int out_dim) {
@@ -695,7 +721,7 @@ void run_q8_gemm(qnn_ctx_s *ctx, const WeightEntry *w, const float *x, float *y,
 
 // ---------------------------------------------------------------- GGUF projection
 void run_gguf(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
-              int out_dim) {
+              int out_dim, float *g_out, float *u_out) {
   GGArgs a;
   a.l = w->gg;
   a.w = w->dptr;
@@ -706,6 +732,8 @@ void run_gguf(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
   a.n = out_dim;
   a.tiles = mode >= GG_SWIGLU ? (out_dim + 31) / 32 : w->gg.tiles;
   a.mode = mode;
+  a.g_out = g_out;
+  a.u_out = u_out;
   int bw, slices;
   gguf_plan(w->gg, a.tiles, &bw, &slices);
   ensure_splitk(ctx, slices > 1 ? size_t(a.tiles) * slices * 64 : 0, size_t(a.tiles) * kCounterStride);
@@ -1177,8 +1205,9 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
 int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_tensor *b, qnn_tensor *c,
                const int *args, int nargs) {
   return guarded([&] {
-    // A GO_SWIGLU may complete a recorded gate/up pair (checked below).
-    const bool glu_pair = op == QNN_GO_SWIGLU && ctx && ctx == g_ctx && ctx->prows.count == 2;
+    // A GLU may complete a recorded gate/up pair (checked below).
+    const bool glu_pair = (op == QNN_GO_SWIGLU || op == QNN_GO_GEGLU) && ctx && ctx == g_ctx &&
+                          (ctx->prows.count == 2 || ctx->lgroup.count == 2);
     check_ctx(ctx, glu_pair);
     auto arg = [&](int i) -> int {
       if (i >= nargs || !args) fail(QNN_E_ARGUMENT, "missing kernel argument");
@@ -1209,10 +1238,11 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
         check_tensor(ctx, dst, n);
         check_tensor(ctx, a, inter_leaved ? int64_t(n) * 2 : n);
         if (!inter_leaved) check_tensor(ctx, b, n);
+        if (glu_pair && try_glu_group(ctx, op, n, inter_leaved, dst, a, b)) return QNN_OK;
         if (glu_pair) {
           const qnn_ctx_s::PendingRows q = ctx->prows;
-          if (!inter_leaved && a->ptr == q.y[0] && b->ptr == q.y[1] && inter == q.out &&
-              int64_t(n) == int64_t(q.rows) * q.out && dst->ptr != q.x) {
+          if (op == QNN_GO_SWIGLU && q.count == 2 && !inter_leaved && a->ptr == q.y[0] && b->ptr == q.y[1] &&
+              inter == q.out && int64_t(n) == int64_t(q.rows) * q.out && dst->ptr != q.x) {
             ctx->prows = {};
             q.e[0]->pins--;
             q.e[1]->pins--;

@@ -33,8 +33,11 @@
 namespace qnn {
 namespace {
 
-__device__ __forceinline__ float silu_dev(float g) {
+__device__ __forceinline__ float silu_dev(float g) {  // tensor.comp:22, as GO_SWIGLU
   return g >= 20.0f ? g : (g <= -20.0f ? 0.0f : g / (1.0f + expf(-g)));
+}
+__device__ __forceinline__ float gelu_dev(float x) {  // tensor.comp:23 (tanh approximation), as GO_GEGLU
+  return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
 }
 __device__ __forceinline__ uint32_t sel4u(const uint4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
@@ -509,7 +512,13 @@ __global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   if (a.mode >= GG_SWIGLU) {
     const float u = __shfl_down(acc, 32);
     const int row = tile * 32 + lane;
-    if (lane < 32 && row < a.n) a.y[row] = silu_dev(acc) * u;
+    if (lane < 32 && row < a.n) {
+      if (a.g_out) {
+        a.g_out[row] = acc;
+        a.u_out[row] = u;
+      }
+      a.y[row] = (a.mode == GG_GEGLU ? gelu_dev(acc) : silu_dev(acc)) * u;
+    }
   } else {
     const int row = tile * 64 + lane;
     if (row < a.n) a.y[row] = acc;

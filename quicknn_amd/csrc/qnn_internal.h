@@ -238,7 +238,7 @@ void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
 
 
 // GGUF (qnn_gguf.hip).
-enum GGMode { GG_STORE = 0, GG_SWIGLU = 2 };
+enum GGMode { GG_STORE = 0, GG_SWIGLU = 2, GG_GEGLU = 3 };
 struct GGArgs {
   GGLayout l;
   const void *w = nullptr;   // tiled weight (gate in pair modes)
@@ -249,6 +249,8 @@ struct GGArgs {
   int n = 0;       // valid output rows
   int tiles = 0;   // wave tiles (64 rows; 32 in pair modes)
   int mode = GG_STORE;
+  float *g_out = nullptr;  // pair modes, optional: the gate and up sums too
+  float *u_out = nullptr;
   float *partial = nullptr;
   unsigned *counters = nullptr;
   int *err = nullptr;

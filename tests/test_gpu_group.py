@@ -91,3 +91,48 @@ def test_group_limits_and_interleaving(ctx, rng):
     assert not ctx.Download(ys[3]).any()
     for t in ys + [x]:
         ctx.Recycle(t)
+
+
+@pytest.mark.parametrize("op_name,enc_name,inter,hidden", [("GO_GEGLU", "WE_Q2_K", 14336, 3584),
+                                                             ("GO_GEGLU", "WE_Q4_K", 2816, 1024),
+                                                             ("GO_SWIGLU", "WE_Q6_K", 1536, 512),
+                                                             ("GO_SWIGLU", "WE_Q8_0", 1000, 768)])
+def test_gate_up_glu_one_launch(ctx, rng, monkeypatch, op_name, enc_name, inter, hidden):
+    """One-row GGUF Linear gate + up on the same input followed by a GLU of their two outputs
+    run as one gate/up pair launch (qnn_status.glu_fused) that still writes both outputs; all
+    three outputs are bit-identical to the grouped launch followed by the GLU kernel, and the
+    projections (and the SwiGLU) are within 1e-3 of the CPU path."""
+    from quicknn_amd import hip
+
+    enc, op = getattr(hip, enc_name), getattr(hip, op_name)
+    ws = mats(rng, hip, [("gate", enc, inter, hidden), ("up", enc, inter, hidden)])
+    x0 = rng.standard_normal(hidden).astype(np.float32)
+
+    def run():
+        x = ctx.UploadRaw(x0)
+        g, u, hh = ctx.NewTensor(inter), ctx.NewTensor(inter), ctx.NewTensor(inter)
+        ctx.Linear(g, x, ws["gate"][0], None, None, 1, hidden, inter)
+        ctx.Linear(u, x, ws["up"][0], None, None, 1, hidden, inter)
+        ctx.Kernel(op, inter, hh, g, u, None, [inter, 0] if op_name == "GO_SWIGLU" else [inter])
+        out = [ctx.Download(t).view(np.uint32).copy() for t in (g, u, hh)]
+        for t in (x, g, u, hh):
+            ctx.Recycle(t)
+        return out
+
+    n0 = ctx.status().glu_fused
+    fused = run()
+    n1 = ctx.status().glu_fused
+    monkeypatch.setenv("QNN_GROUP_LINEAR", "0")
+    sep = run()
+    assert ctx.status().glu_fused == n1
+    for a, b, nm in zip(fused, sep, ("gate", "up", "glu")):
+        assert np.array_equal(a, b), nm
+    if (enc_name, inter) == ("WE_Q2_K", 14336):  # the Gemma-2 layer shape: plans agree
+        assert n1 - n0 == 1
+    gw = oracle.cpu_linear(ws["gate"][0].data, enc, x0, hidden, inter)
+    uw = oracle.cpu_linear(ws["up"][0].data, enc, x0, hidden, inter)
+    assert normwise_rel_err(fused[0].view(np.float32), gw) < 1e-3
+    assert normwise_rel_err(fused[1].view(np.float32), uw) < 1e-3
+    if op_name == "GO_SWIGLU":
+        silu = np.vectorize(oracle.silu, otypes=[np.float32])
+        assert normwise_rel_err(fused[2].view(np.float32), silu(gw) * uw) < 1e-3
