@@ -144,7 +144,9 @@ int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /
  * without bias are recorded and launched by the next call on the context;
  * consecutive ones on the same src with the same encoding (up to 4) share one
  * launch, each result identical to its own launch (QNN_GROUP_LINEAR=0 turns
- * this off).  bias (optional,
+ * this off); a group of exactly a gate and an up projection followed by
+ * QNN_GO_GEGLU / QNN_GO_SWIGLU of their outputs runs as one gate/up launch
+ * that also writes both outputs, identical to the separate ops.  bias (optional,
  * F32 or BF16 [out]) is added afterwards.  scales must be NULL (INT8 ConvRot
  * weights are outside this backend). */
 int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,
