@@ -50,10 +50,15 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
   //    return 0); a wave past the last tile reads tile 0 and stops after the
   //    barrier.
   // The slice is P*sps*L <= 16*GSW groups (the planner keeps P*L <= 16).
-  float4 xr[MT][dev::x_iters<GSW>()];
-  dev::load_x<MT, GSW>(
-      xr, dev::rsrc(a.x, size_t(a.m) * a.x_stride * 4), [&](int m) { return uint32_t(m) * uint32_t(a.x_stride) * 4u; },
-      a.m, ws0 * L * 32, sgroups * 32, tid);
+  // MF: slices of at most 4 x 4 x 32 = 512 elements, staged two tokens per pass.
+  float4 xr[MF ? 1 : MT][MF ? 1 : dev::x_iters<GSW>()];
+  float4 xr2[MF ? MT / 2 : 1];
+  const dev::Rsrc xsrc = dev::rsrc(a.x, size_t(a.m) * a.x_stride * 4);
+  auto xrow = [&](int m) { return uint32_t(m) * uint32_t(a.x_stride) * 4u; };
+  if constexpr (MF)
+    dev::load_x_pairs<MT>(xr2, xsrc, xrow, a.m, ws0 * L * 32, tid);
+  else
+    dev::load_x<MT, GSW>(xr, xsrc, xrow, a.m, ws0 * L * 32, sgroups * 32, tid);
   int tile = unit * T + wave / P;
   if (swiglu && T == 1) tile = 2 * ((unit >> 4) * 8 + (unit & 7)) + ((unit >> 3) & 1);
   const bool active = tile < a.tiles;
@@ -78,7 +83,10 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
 
   // 2) Fixed-point activation planes in LDS.
   const dev::XPlanes xs = dev::xplanes_at(dyn_lds, MT, P * sps * L);
-  dev::stage_x<MT, GSW>(xs, xr, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
+  if constexpr (MF)
+    dev::stage_x_pairs<MT>(xs, xr2, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
+  else
+    dev::stage_x<MT, GSW>(xs, xr, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
   __syncthreads();
 
   // 3) Integer dot per group and token, the L lanes of each row, then the P

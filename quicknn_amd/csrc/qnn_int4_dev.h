@@ -176,6 +176,53 @@ __device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc n
 // an entry are the high plane, 8-15 the low plane.
 // Pieces of token m >= mt, of element >= ne within the slice or of row
 // element >= k are zero (e0 = first element of the slice).
+// One 4-element piece: elements e..e+3 (within the slice) of token m; the 8
+// lanes of a 32-group meet through shuffles, so every lane of the wave runs it.
+__device__ __forceinline__ void stage_piece(const XPlanes &xs, const float4 v, int m, int e, int lane) {
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  const float s1 = amax / 127.0f;
+  const float inv = s1 > 0.0f ? 1.0f / s1 : 0.0f;
+  const float inv2 = inv * 256.0f;
+  int h[4], l[4];
+  const float xv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float q1 = fminf(127.0f, fmaxf(-127.0f, rintf(xv[j] * inv)));
+    const float r = fmaf(-q1, s1, xv[j]);
+    const float q2 = fminf(127.0f, fmaxf(-127.0f, rintf(r * inv2)));
+    h[j] = int(q1);
+    l[j] = int(q2);
+  }
+  int sumq = (256 * h[0] + l[0]) + (256 * h[1] + l[1]) + (256 * h[2] + l[2]) + (256 * h[3] + l[3]);
+  sumq += __shfl_xor(sumq, 1);
+  sumq += __shfl_xor(sumq, 2);
+  sumq += __shfl_xor(sumq, 4);
+  const int g = e >> 5;
+  if (g < xs.groups) {
+    const int i0 = e & 31;  // element 8c + (i0 & 7) of group g
+    const int c = i0 >> 3, half = (i0 >> 2) & 1;
+    // bytes for even slots (elements +0, +2) and odd slots (+1, +3) of this half dword
+    const uint32_t he = (uint32_t(h[0]) & 255u) | ((uint32_t(h[2]) & 255u) << 8);
+    const uint32_t ho = (uint32_t(h[1]) & 255u) | ((uint32_t(h[3]) & 255u) << 8);
+    const uint32_t le = (uint32_t(l[0]) & 255u) | ((uint32_t(l[2]) & 255u) << 8);
+    const uint32_t lo = (uint32_t(l[1]) & 255u) | ((uint32_t(l[3]) & 255u) << 8);
+    const size_t mg = size_t(m) * xs.groups + g;
+    uint16_t *ph = reinterpret_cast<uint16_t *>(xs.q + mg * kXWords);
+    uint16_t *pl = ph + 16;
+    ph[(2 * c) * 2 + half] = uint16_t(he);
+    ph[(2 * c + 1) * 2 + half] = uint16_t(ho);
+    pl[(2 * c) * 2 + half] = uint16_t(le);
+    pl[(2 * c + 1) * 2 + half] = uint16_t(lo);
+    if ((lane & 7) == 0) {
+      xs.s2[mg] = s1 * 0.00390625f;
+      xs.off[mg] = -8 * sumq;
+    }
+  }
+}
+
 template <int MT, int GSW>
 __device__ __forceinline__ void stage_x(const XPlanes &xs, const float4 (&xr)[MT][x_iters<GSW>()], int mt, int e0,
                                         int ne, int k, int tid, int lane) {
@@ -186,50 +233,31 @@ __device__ __forceinline__ void stage_x(const XPlanes &xs, const float4 (&xr)[MT
       if (it * 1024 >= ne) break;  // uniform: passes past the slice
       const int e = (it * 256 + tid) * 4;  // first element of this thread, within the slice
       const bool ok = m < mt && e < ne && e0 + e < k;
-      const float4 v = ok ? xr[m][it] : make_float4(0.f, 0.f, 0.f, 0.f);
-      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
-      amax = fmaxf(amax, __shfl_xor(amax, 4));
-      const float s1 = amax / 127.0f;
-      const float inv = s1 > 0.0f ? 1.0f / s1 : 0.0f;
-      const float inv2 = inv * 256.0f;
-      int h[4], l[4];
-      const float xv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float q1 = fminf(127.0f, fmaxf(-127.0f, rintf(xv[j] * inv)));
-        const float r = fmaf(-q1, s1, xv[j]);
-        const float q2 = fminf(127.0f, fmaxf(-127.0f, rintf(r * inv2)));
-        h[j] = int(q1);
-        l[j] = int(q2);
-      }
-      int sumq = (256 * h[0] + l[0]) + (256 * h[1] + l[1]) + (256 * h[2] + l[2]) + (256 * h[3] + l[3]);
-      sumq += __shfl_xor(sumq, 1);
-      sumq += __shfl_xor(sumq, 2);
-      sumq += __shfl_xor(sumq, 4);
-      const int g = e >> 5;
-      if (g < xs.groups) {
-        const int i0 = e & 31;  // element 8c + (i0 & 7) of group g
-        const int c = i0 >> 3, half = (i0 >> 2) & 1;
-        // bytes for even slots (elements +0, +2) and odd slots (+1, +3) of this half dword
-        const uint32_t he = (uint32_t(h[0]) & 255u) | ((uint32_t(h[2]) & 255u) << 8);
-        const uint32_t ho = (uint32_t(h[1]) & 255u) | ((uint32_t(h[3]) & 255u) << 8);
-        const uint32_t le = (uint32_t(l[0]) & 255u) | ((uint32_t(l[2]) & 255u) << 8);
-        const uint32_t lo = (uint32_t(l[1]) & 255u) | ((uint32_t(l[3]) & 255u) << 8);
-        const size_t mg = size_t(m) * xs.groups + g;
-        uint16_t *ph = reinterpret_cast<uint16_t *>(xs.q + mg * kXWords);
-        uint16_t *pl = ph + 16;
-        ph[(2 * c) * 2 + half] = uint16_t(he);
-        ph[(2 * c + 1) * 2 + half] = uint16_t(ho);
-        pl[(2 * c) * 2 + half] = uint16_t(le);
-        pl[(2 * c + 1) * 2 + half] = uint16_t(lo);
-        if ((lane & 7) == 0) {
-          xs.s2[mg] = s1 * 0.00390625f;
-          xs.off[mg] = -8 * sumq;
-        }
-      }
+      stage_piece(xs, ok ? xr[m][it] : make_float4(0.f, 0.f, 0.f, 0.f), m, e, lane);
     }
+  }
+}
+
+// Slices of at most 512 elements, an even number of tokens: two tokens per
+// pass, so no thread idles (threads t < 128 take token 2p, the others token
+// 2p + 1, elements 4(t % 128) ..).  The planes are those stage_x writes.
+template <int MT, class OffF>
+__device__ __forceinline__ void load_x_pairs(float4 (&xr)[MT / 2], Rsrc src, OffF rowoff, int mt, int e0, int tid) {
+#pragma unroll
+  for (int p = 0; p < MT / 2; ++p) {
+    const int m = 2 * p + (tid >> 7);
+    const uint4 v = ld128(src, rowoff(m < mt ? m : 0) + uint32_t(e0 + (tid & 127) * 4) * 4u, 0);
+    xr[p] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  }
+}
+template <int MT>
+__device__ __forceinline__ void stage_x_pairs(const XPlanes &xs, const float4 (&xr)[MT / 2], int mt, int e0, int ne,
+                                              int k, int tid, int lane) {
+#pragma unroll
+  for (int p = 0; p < MT / 2; ++p) {
+    const int m = 2 * p + (tid >> 7), e = (tid & 127) * 4;
+    const bool ok = m < mt && e < ne && e0 + e < k;
+    stage_piece(xs, ok ? xr[p] : make_float4(0.f, 0.f, 0.f, 0.f), m, e, lane);
   }
 }
 
