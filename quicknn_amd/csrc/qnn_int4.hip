@@ -226,15 +226,20 @@ void launch_tpw(const I4Launch &a, const I4Plan &p, hipStream_t st) {
 }
 // Several tokens over one-lane rows with 4 steps per wave: the matrix-core
 // inner product (QNN_I4_MFMA=0 keeps v_dot4).
+bool mfma_enabled() { return env_int("QNN_I4_MFMA", 1) != 0; }
+
 template <int MT, int GSW>
 void launch_one(const I4Launch &a, const I4Plan &p, hipStream_t st) {
   if constexpr (MT >= 4 && GSW == 4) {
-    if (a.l.lanes == 1 && env_int("QNN_I4_MFMA", 1) != 0) {
+    if (a.l.lanes == 1 && mfma_enabled()) {
       launch_tpw<MT, GSW, true>(a, p, st);
       return;
     }
   }
-  launch_tpw<MT, GSW, false>(a, p, st);
+  if constexpr (MT == 16 && GSW == 4)  // planned only for the matrix-core path
+    fail(QNN_E_INVALID_OP, "int4 plan: 16 tokens at 4 steps per wave without the matrix cores");
+  else
+    launch_tpw<MT, GSW, false>(a, p, st);
 }
 
 // Steps-per-wave templates by token count (register budget).
@@ -249,11 +254,9 @@ void launch_mt(const I4Launch &a, const I4Plan &p, hipStream_t st) {
     case 2: launch_one<MT, 2>(a, p, st); return;
     default: break;
   }
-  if constexpr (MT <= 8) {
-    if (p.gsw == 4) {
-      launch_one<MT, 4>(a, p, st);
-      return;
-    }
+  if (p.gsw == 4) {  // 16 tokens: matrix cores only
+    launch_one<MT, 4>(a, p, st);
+    return;
   }
   if constexpr (MT == 1) {
     if (p.gsw == 8) {
@@ -306,7 +309,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   // the waves gain: 4 against the 1-2 a 3000-wave target picks was 5-16%
   // faster at every measured decode shape (6144x2048 6.58 -> 6.18 us,
   // 2560x2560 6.42 -> 5.38, 1024x2560 5.83 -> 4.97), and 8 was slower.
-  const int set_max = p.mt == 1 ? 4 : (p.mt <= 8 ? 4 : 2);
+  const int set_max = p.mt <= 8 || (l.lanes == 1 && mfma_enabled()) ? 4 : 2;  // 16 tokens: 4 on the matrix cores
   const int lds_max = int((48 << 10) / (size_t(p.mt) * P * l.lanes * (dev::kXWords * 4 + 8)));
   const int cap = std::max(1, std::min(set_max, lds_max));
   // Steps per wave: the largest that splits the K-range into equal workgroup

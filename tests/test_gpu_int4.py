@@ -219,3 +219,28 @@ def test_multi_token_matrix_cores_match_dot4(ctx, rng, monkeypatch, rows):
             assert normwise_rel_err(got["1"][r], want) <= TOL, (n, k, r)
         ctx.Recycle(src)
         ctx.Recycle(dst)
+
+
+def test_sixteen_token_chunks_on_matrix_cores(ctx, rng):
+    """Rows in 16-token chunks run on the matrix cores too (4 steps per wave at shapes that fill
+    the chip): each row is bit-identical to the same rows computed as two 8-token calls, and
+    within tolerance of the CPU path."""
+    n, k, rows = 9728, 2560, 16
+    p = make_int4(rng, n, k)
+    w = hip.MemoryBlock.int4(p)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(rows * n)
+    ctx.Int4Linear(dst, src, w, rows, k, n)
+    got16 = ctx.Download(dst).reshape(rows, n)
+    halves = []
+    for h in range(2):
+        s8, d8 = ctx.UploadRaw(x[8 * h:8 * h + 8]), ctx.NewTensor(8 * n)
+        ctx.Int4Linear(d8, s8, w, 8, k, n)
+        halves.append(ctx.Download(d8).reshape(8, n))
+        ctx.Recycle(s8)
+        ctx.Recycle(d8)
+    assert np.array_equal(got16.view(np.uint32), np.concatenate(halves).view(np.uint32))
+    for r in (0, 7, 15):
+        assert normwise_rel_err(got16[r], oracle.cpu_linear(p, oracle.ENC_INT4, x[r], k, n)) <= TOL, r
+    ctx.Recycle(src)
+    ctx.Recycle(dst)
