@@ -187,3 +187,34 @@ def test_multi_row_pair_settles_on_other_calls(ctx, rng):
     assert ctx.status().glu_fused == n0
     for t in (x, g8, u8, hh):
         ctx.Recycle(t)
+
+
+def test_multi_row_triple_under_graph_capture(ctx, rng):
+    """Captured, the multi-row gate + up + GO_SWIGLU run as three launches (nothing is recorded
+    during capture); every replay is bit-identical to the eager, fused run."""
+    from quicknn_amd import hip
+
+    rows, hidden, inter = 8, 1024, 3072
+    g, u = hip.MemoryBlock.int4(rand_int4(rng, inter, hidden)), hip.MemoryBlock.int4(rand_int4(rng, inter, hidden))
+    x = ctx.UploadRaw(rng.standard_normal((rows, hidden)).astype(np.float32))
+    g8, u8, hh = ctx.NewTensor(rows * inter), ctx.NewTensor(rows * inter), ctx.NewTensor(rows * inter)
+
+    def triple():
+        ctx.Int4Linear(g8, x, g, rows, hidden, inter)
+        ctx.Int4Linear(u8, x, u, rows, hidden, inter)
+        ctx.Kernel(hip.GO_SWIGLU, rows * inter, hh, g8, u8, None, [inter, 0])
+
+    triple()  # eager (fused where the plans agree); also sizes the workspace
+    want = [ctx.Download(t).view(np.uint32).copy() for t in (g8, u8, hh)]
+    ctx.GraphBegin()
+    triple()
+    gid = ctx.GraphEnd()
+    for rep in range(3):
+        for t in (g8, u8, hh):
+            ctx.Kernel(hip.GO_FILL, rows * inter, t, None, None, None, [0])
+        ctx.GraphLaunch(gid)
+        got = [ctx.Download(t).view(np.uint32) for t in (g8, u8, hh)]
+        for a, b, nm in zip(got, want, ("gate", "up", "glu")):
+            assert np.array_equal(a, b), (rep, nm)
+    for t in (x, g8, u8, hh):
+        ctx.Recycle(t)
