@@ -140,12 +140,20 @@ __global__ __launch_bounds__(256) void k_int4_matvec(const I4Launch a, const int
     if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane)) return;
     const int t0 = swiglu ? tile & ~1 : tile;
     const float *pt = a.partial + size_t(t0) * slices * MT * 64 + lane;
-    dev::sum_slices<MT, PU>(
-        acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices);
-    if (swiglu) {
+    if (swiglu) {  // gate and up partials in one batch of loads
       const float *pu = pt + size_t(slices) * MT * 64;
+      float gu[2 * MT];
+      dev::sum_slices<2 * MT, (PU > 1 ? PU / 2 : 1)>(  // as many loads in flight as one matrix at PU
+          gu, [&](int s, int m) { return (m < MT ? pt : pu) + (size_t(s) * MT + (m < MT ? m : m - MT)) * 64; },
+          slices);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        acc[m] = gu[m];
+        accu[m] = gu[MT + m];
+      }
+    } else {
       dev::sum_slices<MT, PU>(
-          accu, [&](int s, int m) { return pu + (size_t(s) * MT + m) * 64; }, slices);
+          acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices);
     }
     dev::reset_counter(ctr, lane);
   }
