@@ -12,9 +12,11 @@
 // the wave, the P parts of a tile are summed in LDS by part 0, and when the
 // K-range is split over several workgroups the last slice of a tile to finish
 // (an atomic ticket per tile) sums the slices in slice order, so results do not
-// depend on timing.  The planner (int4_plan) picks the largest power-of-two
-// steps per wave that splits the steps evenly and still gives enough waves to
-// fill the chip.
+// depend on timing.  The planner (int4_plan) picks 4 steps per wave for one
+// token; for several, the largest power-of-two that splits the steps evenly
+// and still gives enough waves to fill the chip.  With 4-16 tokens over
+// one-lane rows at 4 steps per wave the group dots run on the int8 matrix
+// cores (dot_mf), bit-identical to the v_dot4 path.
 #include "qnn_int4_dev.h"
 
 namespace qnn {
