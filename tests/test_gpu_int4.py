@@ -197,12 +197,14 @@ def test_lane_layouts_and_tile_groupings(ctx, rng, monkeypatch, lanes, tpw):
         assert normwise_rel_err(got8[r], oracle.cpu_linear(pg, oracle.ENC_INT4, x8[r], 2048, 768)) <= TOL, r
 
 
-@pytest.mark.parametrize("rows", [4, 5, 8])
-def test_multi_token_matrix_cores_match_dot4(ctx, rng, monkeypatch, rows):
+@pytest.mark.parametrize("rows,tpw", [(4, 1), (5, 1), (8, 1), (8, 2), (6, 4)])
+def test_multi_token_matrix_cores_match_dot4(ctx, rng, monkeypatch, rows, tpw):
     """4-8 tokens over one-lane rows with 4 steps per wave run the inner product on the int8
     matrix cores: bit-identical to the v_dot4 path (QNN_I4_MFMA=0) and within tolerance of the
-    CPU path, including a partial last block of rows and a slice shorter than a wave's steps."""
+    CPU path, including a partial last block of rows, a slice shorter than a wave's steps and
+    2 or 4 tiles per workgroup (QNN_I4_TPW)."""
     monkeypatch.setenv("QNN_I4_SPS", "4")
+    monkeypatch.setenv("QNN_I4_TPW", str(tpw))
     for n, k in [(2560, 9728), (1000, 2560), (200, 96)]:
         p = make_int4(rng, n, k)
         w = hip.MemoryBlock.int4(p)
