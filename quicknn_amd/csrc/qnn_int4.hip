@@ -26,7 +26,7 @@ using dev::sel4u;
 // MF: the inner product on the int8 matrix cores (dot_mf; L = 1, MT >= 4,
 // GSW a multiple of 4), bit-identical to the v_dot4 path.
 template <int MT, int GSW, int T, bool MF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MF && MT <= 8 ? 6 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MF ? (MT <= 8 ? 6 : 5) : 1)))
 void k_int4_matvec(const I4Launch a, const int slices) {
   extern __shared__ uint4 dyn_lds[];
   __shared__ float red[4][MT][64];
