@@ -142,8 +142,8 @@ int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /
  * rows == 1 runs the packed matvec (op 65), rows > 1 the multi-row product
  * (gemm.comp); Q8_0 with rows >= 4 runs the fp16-MFMA GEMM.  One-row calls
  * without bias are recorded and launched by the next call on the context;
- * consecutive ones on the same src with the same encoding (up to 4) share one
- * launch, each result identical to its own launch (QNN_GROUP_LINEAR=0 turns
+ * consecutive ones on the same src (up to 4; one encoding, or two K-quant
+ * encodings) share one launch, each result identical to its own launch (QNN_GROUP_LINEAR=0 turns
  * this off); a group of exactly a gate and an up projection followed by
  * QNN_GO_GEGLU / QNN_GO_SWIGLU of their outputs runs as one gate/up launch
  * that also writes both outputs, identical to the separate ops.  bias (optional,

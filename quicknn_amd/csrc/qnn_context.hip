@@ -95,7 +95,7 @@ struct qnn_ctx_s {
   // calls on the same input (a layer's q/k/v or gate/up projections) with the
   // same encoding and plan width, at most kGGMaxGroup, distinct outputs.
   struct LinearGroup {
-    int count = 0, bw = 0, enc = 0;
+    int count = 0, bw = 0, enc = 0, enc2 = -1;  // enc2: a second K-quant encoding (one unit per wave), or -1
     const float *x = nullptr;
     qnn::WeightEntry *e[qnn::kGGMaxGroup] = {};
     float *y[qnn::kGGMaxGroup] = {};
@@ -578,13 +578,21 @@ void record_linear(qnn_ctx_s *ctx, WeightEntry *e, const float *x, float *y, int
   int bw, slices;
   gguf_plan(e->gg, e->gg.tiles, &bw, &slices);
   qnn_ctx_s::LinearGroup &g = ctx->lgroup;
-  bool fits = g.count > 0 && g.count < kGGMaxGroup && g.x == x && g.enc == e->gg.enc && g.bw == bw;
+  // A second encoding may join (a layer's q/k/v often mix quant types): K-quants
+  // at one unit per wave, at most two encodings per launch.
+  const int enc = e->gg.enc;
+  const bool enc_ok = g.enc == enc || (bw == 1 && enc != QNN_WE_Q8_0 && g.enc != QNN_WE_Q8_0 &&
+                                       (g.enc2 < 0 || g.enc2 == enc));
+  bool fits = g.count > 0 && g.count < kGGMaxGroup && g.x == x && enc_ok && g.bw == bw;
   for (int i = 0; fits && i < g.count; ++i) fits = g.y[i] != y;
   if (!fits) settle_pending(ctx);
   if (g.count == 0) {
     g.x = x;
-    g.enc = e->gg.enc;
+    g.enc = enc;
+    g.enc2 = -1;
     g.bw = bw;
+  } else if (enc != g.enc) {
+    g.enc2 = enc;
   }
   e->pins++;
   g.e[g.count] = e;

@@ -366,16 +366,19 @@ __device__ float unit_q2_k(const uint4 *mw, uint32_t side, const XSlice<NG> &xs,
 // Workgroup = 4 waves on one 64-row tile (SWIGLU: 32 gate rows in lanes
 // 0-31, the same 32 up rows in lanes 32-63); slice = 4*BW units, wave w
 // streams units [w*BW, (w+1)*BW) of it.
-// A launch carries up to kGGMaxGroup such matvecs (same encoding and BW, the
-// same input in practice: the q/k/v or gate/up projections of a layer); the
-// member is chosen by workgroup range and computed exactly as on its own.
+// A launch carries up to kGGMaxGroup such matvecs (the same input in
+// practice: the q/k/v or gate/up projections of a layer); the member is
+// chosen by workgroup range and computed exactly as on its own.
+__device__ __forceinline__ int group_member(const GGGroup &grp) {
+  int mi = 0;
+  while (mi + 1 < grp.count && int(blockIdx.x) >= grp.start[mi + 1]) ++mi;
+  return mi;
+}
 template <int ENC, int BW>
-__global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
+__device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
   using F = Fmt<ENC>;
   constexpr int U = 4 * BW;   // units per slice
   constexpr int NG = U * 8;   // 32-groups per slice
-  int mi = 0;
-  while (mi + 1 < grp.count && int(blockIdx.x) >= grp.start[mi + 1]) ++mi;
   const GGArgs &a = grp.m[mi];
   const int slices = grp.slices[mi];
   const int bidx = int(blockIdx.x) - grp.start[mi];  // a multiple-of-8 offset keeps the XCD
@@ -525,6 +528,52 @@ __global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   }
 }
 
+template <int ENC, int BW>
+__global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
+  gguf_item<ENC, BW>(grp, group_member(grp));
+}
+// Members of two K-quant encodings in one launch (a layer's q/k/v often mix
+// quant types), one unit per wave; each workgroup runs its member's own code.
+template <int E0, int E1>
+__global__ __launch_bounds__(256) void k_gguf_matvec_mixed(const GGGroup grp) {
+  const int mi = group_member(grp);
+  if (grp.m[mi].l.enc == E0) gguf_item<E0, 1>(grp, mi);
+  else gguf_item<E1, 1>(grp, mi);
+}
+
+template <int E0>
+void launch_mixed(const GGGroup &g, int e1, hipStream_t st) {
+  const int grid = g.start[g.count];
+  switch (e1) {
+    case QNN_WE_Q4_K:
+      if constexpr (E0 != QNN_WE_Q4_K) {
+        hipLaunchKernelGGL((k_gguf_matvec_mixed<E0, QNN_WE_Q4_K>), dim3(grid), dim3(256), 0, st, g);
+        return;
+      }
+      break;
+    case QNN_WE_Q6_K:
+      if constexpr (E0 != QNN_WE_Q6_K) {
+        hipLaunchKernelGGL((k_gguf_matvec_mixed<E0, QNN_WE_Q6_K>), dim3(grid), dim3(256), 0, st, g);
+        return;
+      }
+      break;
+    case QNN_WE_Q3_K:
+      if constexpr (E0 != QNN_WE_Q3_K) {
+        hipLaunchKernelGGL((k_gguf_matvec_mixed<E0, QNN_WE_Q3_K>), dim3(grid), dim3(256), 0, st, g);
+        return;
+      }
+      break;
+    case QNN_WE_Q2_K:
+      if constexpr (E0 != QNN_WE_Q2_K) {
+        hipLaunchKernelGGL((k_gguf_matvec_mixed<E0, QNN_WE_Q2_K>), dim3(grid), dim3(256), 0, st, g);
+        return;
+      }
+      break;
+    default: break;
+  }
+  fail(QNN_E_INVALID_OP, "gguf mixed group encodings");
+}
+
 template <int ENC>
 void launch_enc(const GGGroup &g, int bw, hipStream_t st) {
   const int grid = g.start[g.count];
@@ -587,6 +636,21 @@ void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {
 
 void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s) {
   if (g.count < 1 || g.count > kGGMaxGroup) fail(QNN_E_INVALID_OP, "gguf group size");
+  int e1 = g.m[0].l.enc;
+  for (int i = 1; i < g.count; ++i)
+    if (g.m[i].l.enc != g.m[0].l.enc) e1 = g.m[i].l.enc;
+  if (e1 != g.m[0].l.enc) {  // two encodings (the recorder allows at most two K-quants, one unit per wave)
+    if (bw != 1) fail(QNN_E_INVALID_OP, "gguf mixed group width");
+    switch (g.m[0].l.enc) {
+      case QNN_WE_Q4_K: launch_mixed<QNN_WE_Q4_K>(g, e1, s); break;
+      case QNN_WE_Q6_K: launch_mixed<QNN_WE_Q6_K>(g, e1, s); break;
+      case QNN_WE_Q3_K: launch_mixed<QNN_WE_Q3_K>(g, e1, s); break;
+      case QNN_WE_Q2_K: launch_mixed<QNN_WE_Q2_K>(g, e1, s); break;
+      default: fail(QNN_E_INVALID_OP, "gguf mixed group encodings");
+    }
+    hip_check(hipGetLastError(), "gguf matvec launch");
+    return;
+  }
   switch (g.m[0].l.enc) {
     case QNN_WE_Q4_K: launch_enc<QNN_WE_Q4_K>(g, bw, s); break;
     case QNN_WE_Q6_K: launch_enc<QNN_WE_Q6_K>(g, bw, s); break;

@@ -48,10 +48,10 @@ def test_grouped_equals_single(ctx, rng, monkeypatch):
     x0 = rng.standard_normal(H).astype(np.float32)
     g0 = ctx.status().linear_grouped
     grouped = gemma_like(ctx, hip, ws, x0)
-    assert ctx.status().linear_grouped - g0 == 4  # k+v and gate+up
+    assert ctx.status().linear_grouped - g0 == 5  # q+k+v (two encodings) and gate+up
     monkeypatch.setenv("QNN_GROUP_LINEAR", "0")
     single = gemma_like(ctx, hip, ws, x0)
-    assert ctx.status().linear_grouped - g0 == 4
+    assert ctx.status().linear_grouped - g0 == 5
     for name in grouped:
         assert np.array_equal(grouped[name], single[name]), name
     for name in ("k", "gate"):
