@@ -68,6 +68,12 @@ extern "C" {
 #define QNN_GO_MOE_SCATTER 54
 #define QNN_GO_GEGLU 75
 
+/* OnWeightEvicted (Context.API.inc:164, TProc<IInterface>): called with the
+ * evicted entry's WeightIdentity before its device memory is released
+ * (QuickNN.Vulkan.pas:568-569).  It runs on the context's thread inside the
+ * call that needed the room and must not call back into the context. */
+typedef void (*qnn_weight_evicted_fn)(uint64_t identity, void *user);
+
 typedef struct qnn_ctx_s qnn_ctx;       /* TQNNGPUContext */
 typedef struct qnn_tensor_s qnn_tensor; /* TQNNGPUTensor: fp32 device buffer */
 typedef struct qnn_expert_set_s qnn_expert_set;
@@ -121,6 +127,9 @@ int qnn_tensor_new(qnn_ctx *ctx, int count, qnn_tensor **out);                 /
 int qnn_recycle(qnn_ctx *ctx, qnn_tensor **tensor);                            /* Recycle */
 int qnn_scratch(qnn_ctx *ctx, int slot, int count, qnn_tensor **out);          /* Scratch */
 int qnn_upload_raw(qnn_ctx *ctx, const void *data, int count, qnn_tensor **out); /* UploadRaw */
+/* Upload(TMemoryBlock) (Context.Implementation.inc:700-705): F32 storage only
+ * (else QNN_E_ARGUMENT); Size floats starting at element Offset. */
+int qnn_upload(qnn_ctx *ctx, const qnn_weight *data, qnn_tensor **out);
 int qnn_download(qnn_ctx *ctx, qnn_tensor *t, void *dst, int count);           /* Download (-1 = all) */
 int qnn_copy(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, int count, int dst_offset, int src_offset); /* Copy */
 int qnn_flush(qnn_ctx *ctx);                                                   /* Flush */
@@ -134,13 +143,17 @@ int qnn_retain_weight(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols);  /
 int qnn_preload_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, uint64_t staging_limit); /* PreloadWeights */
 int qnn_is_weight_resident(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols, int *resident); /* IsWeightResident */
 int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /* WeightBatchCapacity */
+/* OnWeightEvicted setter (Context.API.inc:164); fn = NULL clears it. */
+int qnn_set_weight_evicted(qnn_ctx *ctx, qnn_weight_evicted_fn fn, void *user);
 
 /* ---------------------------------------------------------------------------
  * Hot-path ops
  * ------------------------------------------------------------------------- */
 /* Linear (Context.API.inc:117-122, Implementation.inc:813-899).  GGUF weights:
  * rows == 1 runs the packed matvec (op 65), rows > 1 the multi-row product
- * (gemm.comp); Q8_0 with rows >= 4 runs the fp16-MFMA GEMM.  One-row calls
+ * (gemm.comp); Q8_0 with rows >= 4 runs the fp16-MFMA GEMM.  F32 and BF16
+ * weights [out_dim, in_dim] (the router and native-precision layers) run an
+ * fp32 matvec (rows == 1) or fp32 GEMM (rows > 1); bf16 widens exactly.  One-row calls
  * without bias are recorded and launched by the next call on the context;
  * consecutive ones on the same src (up to 4; one encoding, or two K-quant
  * encodings) share one launch, each result identical to its own launch (QNN_GROUP_LINEAR=0 turns
@@ -151,6 +164,13 @@ int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /
  * weights are outside this backend). */
 int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,
                const qnn_weight *bias, int rows, int in_dim, int out_dim);
+
+/* VectorLinear (Context.API.inc:130, Implementation.inc:969-1001): dst = W src for
+ * an F32 or BF16 weight [out_dim, in_dim]; any other dtype is QNN_E_ARGUMENT.
+ * The engine's router projection for one token (LLM.MoE.pas:363) and the
+ * native-precision projections of LLM.pas:471, QwenHybrid.pas:548 and
+ * Gemma2.pas:146. */
+int qnn_vector_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int in_dim, int out_dim);
 
 /* Int4Linear (Context.API.inc:138-142, Implementation.inc:1080-1135):
  * 1 <= rows <= 128; weight U8/NATIVE [out_dim, Int4RowBytes(in_dim)], offset 0.

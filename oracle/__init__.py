@@ -240,8 +240,9 @@ def cpu_mlp(gate, up, down, enc, x, hidden, inter, pool: Pool | None = None) -> 
     return out
 
 
-def moe_route(logits: np.ndarray, k: int, normalize: bool = True, select_on_logits: bool = True):
-    """GO_MOE_ROUTE (moe.comp:25-50). Returns (ids uint32 [rows,k], probs f32 [rows,k])."""
+def moe_route(logits: np.ndarray, k: int, normalize: bool = True, select_on_logits: bool = False):
+    """GO_MOE_ROUTE (moe.comp:25-50): ranked by fp32 probability, ties to the lower id.
+    Returns (ids uint32 [rows,k], probs f32 [rows,k])."""
     logits = np.ascontiguousarray(logits, np.float32)
     rows, experts = logits.shape
     ids = np.zeros((rows, k), np.uint32)

@@ -736,10 +736,19 @@ int qo_cpu_mlp(void *pool, const uint8_t *gate, const uint8_t *up, const uint8_t
 // ===========================================================================
 
 // GO_MOE_ROUTE (src/backends/vulkan/shaders/moe.comp:25-50): softmax over the
-// experts, k rounds of argmax with ties to the lower id, the selected entry
-// set to -1, optional renormalisation by the rank-ordered sum of the top-k.
-// select_on_logits=1 ranks by logit (softmax is monotone, so the order is the
-// same except where rounding makes two distinct probabilities equal).
+// experts, k rounds of argmax over the probabilities with ties to the lower id
+// (:36-46), the selected entry set to -1, optional renormalisation by the
+// rank-ordered sum of the top-k (:47-48).
+//  - v_e = exp(l_e - max) (:31): the shader's exp has implementation-defined
+//    precision; here it is the correctly rounded fp32 exponential (double exp,
+//    rounded once).
+//  - The denominator follows sumGroup (:20, :32): 256 partial sums, partial L
+//    over experts L, L+256, ... in ascending id (:31), then the LDS tree
+//    partial[L] += partial[L+s] for s = 128 .. 1.
+//  - p_e = v_e / denominator (:33), so distinct logits whose probabilities
+//    round equal tie, and the lower id wins.
+// select_on_logits=1 ranks by logit instead (the same order wherever no two
+// distinct probabilities round equal).
 int qo_moe_route(const float *logits, int rows, int experts, int k, int normalize, int select_on_logits,
                  uint32_t *ids, float *probs) {
   if (!logits || !ids || !probs || rows < 1 || experts < 1 || k < 1 || k > experts || k > 64) return -1;
@@ -748,8 +757,14 @@ int qo_moe_route(const float *logits, int rows, int experts, int k, int normaliz
     const float *l = logits + (size_t)row * experts;
     float maximum = -3.402823466e38f;
     for (int e = 0; e < experts; ++e) maximum = std::max(maximum, l[e]);
-    float denominator = 0;
-    for (int e = 0; e < experts; ++e) { p[e] = std::exp(l[e] - maximum); denominator += p[e]; }
+    float partial[256] = {};
+    for (int e = 0; e < experts; ++e) {
+      p[e] = (float)std::exp((double)(l[e] - maximum));
+      partial[e % 256] += p[e];
+    }
+    for (int s = 128; s > 0; s >>= 1)
+      for (int lane = 0; lane < s; ++lane) partial[lane] += partial[lane + s];
+    const float denominator = partial[0];
     for (int e = 0; e < experts; ++e) p[e] /= denominator;
     for (int e = 0; e < experts; ++e) key[e] = select_on_logits ? l[e] : p[e];
     std::vector<uint32_t> top_ids(k);

@@ -118,6 +118,10 @@ struct qnn_ctx_s {
   std::vector<qnn_expert_set_s *> sets;
   qnn_status st{};
   uint64_t act_bytes = 0;
+  // OnWeightEvicted (Context.API.inc:164): told the identity of every entry
+  // the cache evicts, before its memory is released (QuickNN.Vulkan.pas:568-569).
+  qnn_weight_evicted_fn on_evicted = nullptr;
+  void *on_evicted_user = nullptr;
 };
 
 namespace qnn {
@@ -300,6 +304,7 @@ void evict_one_or_fail(qnn_ctx_s *ctx) {  // EvictOne (QuickNN.Vulkan.pas:551-57
     if (e->pins == 0 && e->op_pins == 0 && (!oldest || e->last_use < oldest->last_use)) oldest = e;
   }
   if (!oldest) fail(QNN_E_RANGE, "VRAM cache cannot hold the active chain");
+  if (ctx->on_evicted) ctx->on_evicted(oldest->identity, ctx->on_evicted_user);
   ctx->weights.erase(oldest->key);
   ctx->weight_bytes -= oldest->bytes;
   (void)hipFree(oldest->dptr);
@@ -362,6 +367,7 @@ WeightEntry *acquire_int4(qnn_ctx_s *ctx, const qnn_weight *w, int rows, int col
   begin_miss(ctx);
   auto *e = new WeightEntry();
   e->key = key;
+  e->identity = w->identity;
   e->kind = WKind::Int4;
   e->i4 = int4_layout(rows, cols);
   e->bytes = e->i4.bytes();
@@ -389,6 +395,7 @@ WeightEntry *acquire_gguf(qnn_ctx_s *ctx, const qnn_weight *w, int rows, int col
   begin_miss(ctx);
   auto *e = new WeightEntry();
   e->key = key;
+  e->identity = w->identity;
   e->kind = WKind::Gguf;
   e->gg = gguf_layout(w->encoding, rows, cols);
   e->bytes = e->gg.bytes();
@@ -425,6 +432,7 @@ WeightEntry *acquire_raw(qnn_ctx_s *ctx, const qnn_weight *w, int64_t count) {
   begin_miss(ctx);
   auto *e = new WeightEntry();
   e->key = key;
+  e->identity = w->identity;
   e->kind = WKind::Raw;
   e->raw_dtype = w->dtype;
   e->bytes = (bytes + 255) & ~uint64_t(255);
@@ -843,7 +851,7 @@ int qnn_ctx_destroy(qnn_ctx *ctx) {
 
 int qnn_get_status(qnn_ctx *ctx, qnn_status *out) {
   return guarded([&] {
-    check_ctx(ctx);
+    check_ctx(ctx, true);  // a query: recorded ops stay recorded
     if (!out) fail(QNN_E_ARGUMENT, "out");
     ctx->st.weight_bytes = ctx->weight_bytes;
     ctx->st.weight_limit = ctx->weight_limit;
@@ -855,7 +863,10 @@ int qnn_get_status(qnn_ctx *ctx, qnn_status *out) {
 // ---------------------------------------------------------------- tensors
 int qnn_tensor_new(qnn_ctx *ctx, int count, qnn_tensor **out) {
   return guarded([&] {
-    check_ctx(ctx);
+    // Recorded ops stay recorded: the engine creates each output right before
+    // the projection that writes it (Work.New, QwenHybrid.pas:542, :700), and a
+    // new tensor cannot alias a recorded op's buffers (Recycle settles them).
+    check_ctx(ctx, true);
     if (!out) fail(QNN_E_ARGUMENT, "out");
     *out = new_tensor(ctx, count);
     return QNN_OK;
@@ -973,7 +984,9 @@ static WeightEntry *acquire_matrix(qnn_ctx_s *ctx, const qnn_weight *w, int rows
     if (qnn_int4_row_bytes(k) != cols) fail(QNN_E_ARGUMENT, "INT4 row width is not a multiple of 20 bytes");
     return acquire_int4(ctx, w, rows, k);
   }
-  fail(QNN_E_NOT_SUPPORTED, "only packed INT4 and GGUF matrices are resident in the HIP backend");
+  // F32 / BF16 matrices [rows, cols] (the router, RetainRouters LLM.MoE.pas:190-194).
+  if (w->dtype == QNN_DT_F32 || w->dtype == QNN_DT_BF16) return acquire_raw(ctx, w, int64_t(rows) * cols);
+  fail(QNN_E_NOT_SUPPORTED, "only packed INT4, GGUF, F32 and BF16 matrices are resident in the HIP backend");
 }
 
 int qnn_retain_weight(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols) {
@@ -1008,11 +1021,13 @@ int qnn_preload_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, uint64_t stag
 
 int qnn_is_weight_resident(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols, int *resident) {
   return guarded([&] {
-    check_ctx(ctx);
+    check_ctx(ctx, true);  // a query: recorded ops stay recorded
     check_weight_desc(w);
     if (!resident) fail(QNN_E_ARGUMENT, "out");
     std::string key;
     if (is_gguf(w->encoding)) key = weight_key("gg", w, gguf_weight_bytes(w, rows, cols));
+    else if (w->dtype == QNN_DT_F32 || w->dtype == QNN_DT_BF16)
+      key = weight_key("raw", w, uint64_t(rows) * cols * (w->dtype == QNN_DT_F32 ? 4 : 2));
     else key = weight_key("i4", w, uint64_t(rows) * cols);
     *resident = ctx->weights.count(key) ? 1 : 0;
     return QNN_OK;
@@ -1021,7 +1036,7 @@ int qnn_is_weight_resident(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols
 
 int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes) {
   return guarded([&] {
-    check_ctx(ctx);
+    check_ctx(ctx, true);  // a query: recorded ops stay recorded
     if (!bytes) fail(QNN_E_ARGUMENT, "out");
     // WeightBatchCapacity (Context.Implementation.inc:421-429): the cache limit less the retained bytes.
     *bytes = ctx->weight_limit - std::min(ctx->weight_limit, ctx->retained_bytes);
@@ -1177,11 +1192,26 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
         fail(QNN_E_ARGUMENT, "Invalid resident linear dimensions/alias");
       check_weight_desc(w);
       if (scales && scales->data) fail(QNN_E_NOT_SUPPORTED, "INT8 ConvRot weights are not handled by the HIP backend");
-      if (!is_gguf(w->encoding))
-        fail(QNN_E_NOT_SUPPORTED, "Linear handles GGUF weights; native INT4 goes through Int4Linear");
+      const bool has_bias = bias && bias->data;
+      if (!is_gguf(w->encoding)) {
+        // F32 / BF16 weights (the gemm pipeline with the bf16 flag, Implementation.inc:852-883).
+        if (w->dtype != QNN_DT_F32 && w->dtype != QNN_DT_BF16)
+          fail(QNN_E_NOT_SUPPORTED, "Linear handles GGUF, F32 and BF16 weights; native INT4 goes through Int4Linear");
+        settle_pending(ctx);
+        OpPins pin;
+        WeightEntry *e = pin(acquire_raw(ctx, w, int64_t(out_dim) * in_dim));
+        const int bf = e->raw_dtype == QNN_DT_BF16;
+        if (rows == 1) dense_matvec_launch(e->dptr, bf, src->ptr, dst->ptr, out_dim, in_dim, ctx->stream);
+        else dense_gemm_launch(e->dptr, bf, src->ptr, dst->ptr, rows, out_dim, in_dim, ctx->stream);
+        if (has_bias) {
+          WeightEntry *b = pin(acquire_raw(ctx, bias, out_dim));
+          misc_bias_add(dst->ptr, b->dptr, b->raw_dtype == QNN_DT_BF16, rows, out_dim, ctx->stream);
+        }
+        ctx->st.gemm_calls++;
+        return QNN_OK;
+      }
       OpPins pin;
       WeightEntry *e = pin(acquire_gguf(ctx, w, out_dim, in_dim));
-      const bool has_bias = bias && bias->data;
       if (rows == 1 && !has_bias && !ctx->capturing && linear_grouping_enabled()) {
         // Recorded: launched with the next calls on the same input as one kernel.
         record_linear(ctx, e, src->ptr, dst->ptr, out_dim);
@@ -1206,6 +1236,52 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
     }
     ctx->st.gemm_calls++;
     ctx->st.gguf_calls++;
+    return QNN_OK;
+  });
+}
+
+int qnn_vector_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int in_dim, int out_dim) {
+  return guarded([&] {
+    check_ctx(ctx);
+    // VectorLinear validation (Context.Implementation.inc:982-985).
+    check_tensor(ctx, src, in_dim);
+    check_tensor(ctx, dst, out_dim);
+    check_weight_desc(w);
+    if (in_dim < 1 || out_dim < 1 || src == dst || (w->dtype != QNN_DT_F32 && w->dtype != QNN_DT_BF16))
+      fail(QNN_E_ARGUMENT, "Invalid resident vector projection");
+    OpPins pin;
+    WeightEntry *e = pin(acquire_raw(ctx, w, int64_t(out_dim) * in_dim));
+    dense_matvec_launch(e->dptr, e->raw_dtype == QNN_DT_BF16, src->ptr, dst->ptr, out_dim, in_dim, ctx->stream);
+    ctx->st.gemm_calls++;
+    return QNN_OK;
+  });
+}
+
+int qnn_upload(qnn_ctx *ctx, const qnn_weight *data, qnn_tensor **out) {
+  return guarded([&] {
+    check_ctx(ctx);
+    // Upload(TMemoryBlock) (Context.Implementation.inc:700-705): F32 storage
+    // only; Count = Size floats from element Offset (Common.pas:1234-1237, :1597-1605).
+    if (!data || !out) fail(QNN_E_ARGUMENT, "Resident upload");
+    if (data->dtype != QNN_DT_F32) fail(QNN_E_ARGUMENT, "Resident upload requires F32 storage");
+    if (!data->data || data->offset < 0) fail(QNN_E_ARGUMENT, "Resident upload");
+    if (data->size < 1 || data->size > 0x7fffffff) fail(QNN_E_RANGE, "resident tensor size");
+    if (ctx->capturing) fail(QNN_E_INVALID_OP, "upload during graph capture");
+    auto *t = new_tensor(ctx, int(data->size));
+    hip_check(hipMemcpyAsync(t->ptr, static_cast<const float *>(data->data) + data->offset, size_t(data->size) * 4,
+                             hipMemcpyHostToDevice, ctx->stream),
+              "upload");
+    sync(ctx);
+    *out = t;
+    return QNN_OK;
+  });
+}
+
+int qnn_set_weight_evicted(qnn_ctx *ctx, qnn_weight_evicted_fn fn, void *user) {
+  return guarded([&] {
+    check_ctx(ctx, true);
+    ctx->on_evicted = fn;
+    ctx->on_evicted_user = user;
     return QNN_OK;
   });
 }
@@ -1459,7 +1535,7 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
       fr = ctx->proute;
       ctx->proute = {};
     }
-    if (ctx->pending.on || ctx->lgroup.count || ctx->proute.on) settle_pending(ctx);
+    settle_pending(ctx);  // every other recorded op runs before the experts read or write
     struct RouteGuard {  // an error below still runs the recorded route op
       qnn_ctx_s *ctx;
       qnn_ctx_s::PendingRoute &r;

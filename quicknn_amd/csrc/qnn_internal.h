@@ -77,6 +77,7 @@ enum class WKind { Int4, Gguf, Raw };
 
 struct WeightEntry {
   std::string key;
+  uint64_t identity = 0;   // WeightIdentity of the source block (reported on eviction)
   WKind kind = WKind::Raw;
   void *dptr = nullptr;
   size_t bytes = 0;        // device bytes held
@@ -236,6 +237,11 @@ void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, co
                     void *frag, int *ea, float *c, hipStream_t s);
 void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
 
+
+// F32 / BF16 weights, row-major [n, k] (qnn_dense.hip): y = W x for one row,
+// Y[m, n] = X[m, k] W^T for several.
+void dense_matvec_launch(const void *w, int bf16, const float *x, float *y, int n, int k, hipStream_t s);
+void dense_gemm_launch(const void *w, int bf16, const float *x, float *y, int m, int n, int k, hipStream_t s);
 
 // GGUF (qnn_gguf.hip).
 enum GGMode { GG_STORE = 0, GG_SWIGLU = 2, GG_GEGLU = 3 };

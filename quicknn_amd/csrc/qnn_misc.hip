@@ -92,22 +92,19 @@ __global__ __launch_bounds__(256) void k_norm(float *dst, const float *a, const 
   }
 }
 
-// GO_MOE_ROUTE (moe.comp:25-50): fp32 softmax, exact top-k with ties to the
-// lower id, optional renormalisation by the rank-ordered top-k sum.  Ranking
-// uses the logits (softmax is monotone), which keeps the selection identical
-// to the CPU oracle regardless of exp() rounding.  One wave per token row; two
-// selection methods with the same result:
+// GO_MOE_ROUTE (moe.comp:25-50): fp32 softmax, exact top-k by probability
+// with ties to the lower id, optional renormalisation by the rank-ordered
+// top-k sum.  exp is rounded once from double and the denominator is summed in
+// the reference's 256-partial order (qnn_route_dev.h), so ids and
+// probabilities match the CPU oracle bit for bit.  One wave per token row;
+// two selection methods with the same result:
 //
 // * up to 1024 experts (k_moe_route_reg): keys in registers and a ballot
-//   radix select (dev::route_row, qnn_route_dev.h).  No step depends on a
-//   cross-lane shuffle chain.
-// * more experts (k_moe_route): logits in LDS; each of the k rounds is a scan
-//   of the lane's experts plus a 6-step butterfly argmax over (logit desc, id
-//   asc), a strict total order, so every lane agrees on the winner.
-//
-// Both take max, then the denominator as each lane's experts in ascending id
-// and a butterfly sum broadcast from lane 0, and p = exp(l - max) / denominator,
-// so their probabilities are identical too.
+//   radix select (dev::route_select, qnn_route_dev.h).
+// * more experts (k_moe_route): probabilities in LDS; each of the k rounds is
+//   a scan of the lane's experts plus a 6-step butterfly argmax over
+//   (probability desc, id asc), a strict total order, so every lane agrees on
+//   the winner.
 template <int J>
 __global__ __launch_bounds__(64) void k_moe_route_reg(float *routes, const float *logits, int rows, int experts, int k,
                                                       int normalize) {
@@ -131,23 +128,29 @@ __device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) {
 }
 __global__ __launch_bounds__(64) void k_moe_route(float *routes, const float *logits, int rows, int experts, int k,
                                                   int normalize) {
-  extern __shared__ float sh[];  // experts logits, then experts "taken" bytes
-  float *lg = sh;
+  extern __shared__ float sh[];  // experts probabilities, then experts "taken" bytes
+  float *pr = sh;
   uint8_t *taken = reinterpret_cast<uint8_t *>(sh + experts);
   const int row = blockIdx.x, lane = threadIdx.x;
   const float *l = logits + size_t(row) * experts;
   float mx = -3.402823466e38f;
   for (int e = lane; e < experts; e += 64) {
     const float v = l[e];
-    lg[e] = v;
+    pr[e] = v;
     taken[e] = 0;
     mx = fmaxf(mx, v);
   }
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  float part = 0.0f;
-  for (int e = lane; e < experts; e += 64) part += expf(lg[e] - mx);  // the lane's own LDS entries
-  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
-  const float denominator = __shfl(part, 0);
+  // The lane's own LDS entries: partial lane + 64*i sums experts lane + 64*i + 256*m, ascending m.
+  float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int i = 0; i < 4; ++i)
+    for (int e = lane + 64 * i; e < experts; e += 256) {
+      const float v = dev::route_exp(pr[e] - mx);
+      pr[e] = v;
+      q[i] = q[i] + v;
+    }
+  const float den = dev::route_denominator(q[0], q[1], q[2], q[3]);
+  for (int e = lane; e < experts; e += 64) pr[e] = pr[e] / den;
   __syncthreads();
   int my_id = 0;
   float my_p = 0.0f;
@@ -155,7 +158,7 @@ __global__ __launch_bounds__(64) void k_moe_route(float *routes, const float *lo
     float best = -INFINITY;
     int bid = kRouteNone;
     for (int e = lane; e < experts; e += 64) {
-      const float v = lg[e];
+      const float v = pr[e];
       if (!taken[e] && route_better(v, e, best, bid)) {
         best = v;
         bid = e;
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(64) void k_moe_route(float *routes, const float *lo
     if (lane == 0) taken[bid] = 1;
     if (lane == r) {
       my_id = bid;
-      my_p = expf(lg[bid] - mx) / denominator;
+      my_p = pr[bid];
     }
     __syncthreads();
   }

@@ -11,6 +11,7 @@ of this module raises -- there is no CPU fallback.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import itertools
 import os
@@ -80,6 +81,7 @@ class Status(ctypes.Structure):
 _lib = None
 _vp = ctypes.c_void_p
 _ip = ctypes.POINTER(ctypes.c_int)
+_EVICTED = ctypes.CFUNCTYPE(None, ctypes.c_uint64, ctypes.c_void_p)  # qnn_weight_evicted_fn
 
 
 def lib():
@@ -108,6 +110,9 @@ def lib():
             "qnn_preload_weights": (ctypes.c_int, [_vp, W, ctypes.c_int, ctypes.c_uint64]),
             "qnn_is_weight_resident": (ctypes.c_int, [_vp, W, ctypes.c_int, ctypes.c_int, _ip]),
             "qnn_weight_batch_capacity": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
+            "qnn_set_weight_evicted": (ctypes.c_int, [_vp, _EVICTED, _vp]),
+            "qnn_upload": (ctypes.c_int, [_vp, W, ctypes.POINTER(_vp)]),
+            "qnn_vector_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int]),
             "qnn_linear": (ctypes.c_int, [_vp, _vp, _vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_int4_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_swiglu_vector": (ctypes.c_int, [_vp, _vp, _vp, W, W, ctypes.c_int, ctypes.c_int]),
@@ -145,7 +150,7 @@ EXPORTED = (
     "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_tensor_new", "qnn_recycle",
     "qnn_scratch", "qnn_upload_raw", "qnn_download", "qnn_copy", "qnn_flush", "qnn_tensor_count",
     "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
-    "qnn_weight_batch_capacity", "qnn_linear", "qnn_int4_linear", "qnn_swiglu_vector",
+    "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_int4_linear", "qnn_swiglu_vector",
     "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
     "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
@@ -205,6 +210,15 @@ class MemoryBlock:
         """GGUF tensor: dtU8 with element shape [N, K] (SafeTensors.pas:874-890)."""
         blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
         return MemoryBlock(blocks, (rows, cols), DT_U8, encoding, 0, rows * cols, **kw)
+
+    @staticmethod
+    def matrix(values: np.ndarray, **kw) -> "MemoryBlock":
+        """F32 [N, K] (float32) or BF16 [N, K] (uint16 bits) weight, e.g. the MoE router."""
+        v = np.ascontiguousarray(values)
+        dt = DT_BF16 if v.dtype == np.uint16 else DT_F32
+        if dt == DT_F32:
+            v = v.astype(np.float32, copy=False)
+        return MemoryBlock(v, v.shape, dt, WE_NATIVE, 0, v.size, **kw)
 
     @staticmethod
     def vector(values: np.ndarray, **kw) -> "MemoryBlock":
@@ -273,6 +287,22 @@ def _th(t: Tensor | None):
     return None if t is None else t.handle
 
 
+# Contexts still open when the interpreter exits are destroyed by an atexit
+# hook, before the HIP runtime's own teardown (a context left alive into
+# process exit races that teardown: its stream, events, graphs and pinned
+# readback buffer would be released by a runtime that is shutting down).
+_open_contexts: set = set()
+
+
+@atexit.register
+def _close_open_contexts() -> None:
+    for c in list(_open_contexts):
+        try:
+            c.close()
+        except Exception:  # created on another thread, or the runtime already failed
+            _open_contexts.discard(c)
+
+
 class GPUContext:
     """TQNNGPUContext over libqnn_hip.so (one per process, bound to its creating thread)."""
 
@@ -280,12 +310,15 @@ class GPUContext:
         h = _vp()
         _raise(lib().qnn_ctx_create(device, weight_cache_bytes, ctypes.byref(h)))
         self.h = h.value
+        self._evicted_cb = self._evicted_fn = None
+        _open_contexts.add(self)
 
     # -- lifetime
     def close(self) -> None:
         if self.h:
             _raise(lib().qnn_ctx_destroy(self.h))
             self.h = None
+        _open_contexts.discard(self)
 
     def __enter__(self):
         return self
@@ -321,7 +354,11 @@ class GPUContext:
         _raise(lib().qnn_upload_raw(self.h, a.ctypes.data, a.size, ctypes.byref(h)))
         return Tensor(self, h.value)
 
-    Upload = UploadRaw
+    def Upload(self, data: MemoryBlock) -> Tensor:
+        """Upload(TMemoryBlock) (Context.Implementation.inc:700-705): F32 storage only."""
+        h = _vp()
+        _raise(lib().qnn_upload(self.h, _wd(data), ctypes.byref(h)))
+        return Tensor(self, h.value)
 
     def Download(self, t: Tensor, count: int = -1, dtype=np.float32) -> np.ndarray:
         n = t.count if count < 0 else count
@@ -348,6 +385,17 @@ class GPUContext:
         _raise(lib().qnn_is_weight_resident(self.h, _wd(w), rows, cols, ctypes.byref(r)))
         return bool(r.value)
 
+    @property
+    def OnWeightEvicted(self):
+        """OnWeightEvicted (Context.API.inc:164): fn(identity) per evicted cache entry, or None."""
+        return self._evicted_fn
+
+    @OnWeightEvicted.setter
+    def OnWeightEvicted(self, fn) -> None:
+        cb = None if fn is None else _EVICTED(lambda ident, _user: fn(int(ident)))
+        _raise(lib().qnn_set_weight_evicted(self.h, cb if cb is not None else _EVICTED(), None))
+        self._evicted_cb, self._evicted_fn = cb, fn  # the C side keeps the pointer: hold the thunk
+
     def WeightBatchCapacity(self) -> int:
         v = ctypes.c_uint64()
         _raise(lib().qnn_weight_batch_capacity(self.h, ctypes.byref(v)))
@@ -358,6 +406,9 @@ class GPUContext:
                bias: MemoryBlock | None, rows: int, input_dim: int, output_dim: int) -> None:
         _raise(lib().qnn_linear(self.h, dst.handle, src.handle, _wd(weight), _wd(scales), _wd(bias), rows,
                                 input_dim, output_dim))
+
+    def VectorLinear(self, dst: Tensor, src: Tensor, weight: MemoryBlock, input_dim: int, output_dim: int) -> None:
+        _raise(lib().qnn_vector_linear(self.h, dst.handle, src.handle, _wd(weight), input_dim, output_dim))
 
     def Int4Linear(self, dst: Tensor, src: Tensor, weight: MemoryBlock, rows: int, input_dim: int,
                    output_dim: int) -> None:

@@ -66,6 +66,6 @@ def test_moe_route(ctx):
     raw = ctx.Download(routes)
     assert raw[:rows * k].view(np.uint32).reshape(rows, k).astype(int).tolist() == r["ids"]
     want = f32(r["probs_hex"])
-    assert np.allclose(raw[rows * k:], want, rtol=2e-6, atol=0)
+    assert np.array_equal(raw[rows * k:].view(np.uint32), want.view(np.uint32))
     ctx.Recycle(lt)
     ctx.Recycle(routes)

@@ -39,19 +39,37 @@ def gemma_like(ctx, hip, ws, x0):
     return res
 
 
-def test_grouped_equals_single(ctx, rng, monkeypatch):
+def recorded_groups(encs):
+    """Calls that share a launch when one-row K-quant Linear calls on one input
+    (one unit per wave) are recorded in this order: a group takes up to four
+    members of at most two encodings."""
+    groups, cur = [], []
+    for e in encs:
+        if cur and (len(cur) == 4 or (e not in cur and len(set(cur)) == 2)):
+            groups.append(cur)
+            cur = []
+        cur.append(e)
+    groups.append(cur)
+    return sum(len(g) for g in groups if len(g) > 1)
+
+
+# q's encoding and k/v's: two K-quant encodings share one launch (k_gguf_matvec_mixed).
+@pytest.mark.parametrize("eq,ekv", [(2, 4), (2, 3), (3, 9), (4, 2), (9, 3), (3, 2)],
+                         ids=["q4k+q3k", "q4k+q6k", "q6k+q2k", "q3k+q4k", "q2k+q6k", "q6k+q4k"])
+def test_grouped_equals_single(ctx, rng, monkeypatch, eq, ekv):
     from quicknn_amd import hip
 
     H = 1024
-    ws = mats(rng, hip, [("q", hip.WE_Q4_K, 1024, H), ("k", hip.WE_Q3_K, 512, H), ("v", hip.WE_Q3_K, 512, H),
+    ws = mats(rng, hip, [("q", eq, 1024, H), ("k", ekv, 512, H), ("v", ekv, 512, H),
                          ("o", hip.WE_Q4_K, H, 1024), ("gate", hip.WE_Q2_K, 2816, H), ("up", hip.WE_Q2_K, 2816, H)])
     x0 = rng.standard_normal(H).astype(np.float32)
     g0 = ctx.status().linear_grouped
     grouped = gemma_like(ctx, hip, ws, x0)
-    assert ctx.status().linear_grouped - g0 == 5  # q+k+v (two encodings) and gate+up
+    want = recorded_groups([eq, ekv, ekv, hip.WE_Q2_K, hip.WE_Q2_K])
+    assert ctx.status().linear_grouped - g0 == want  # e.g. q+k+v (two encodings) and gate+up
     monkeypatch.setenv("QNN_GROUP_LINEAR", "0")
     single = gemma_like(ctx, hip, ws, x0)
-    assert ctx.status().linear_grouped - g0 == 5
+    assert ctx.status().linear_grouped - g0 == want
     for name in grouped:
         assert np.array_equal(grouped[name], single[name]), name
     for name in ("k", "gate"):

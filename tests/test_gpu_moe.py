@@ -1,7 +1,8 @@
 """GPU parity of the MoE path (native INT4 experts) against the CPU oracle.
 
-* GO_MOE_ROUTE (moe.comp:25-50): expert ids identical to the oracle; routing
-  weights within 2e-6 relative (device expf vs the host's).
+* GO_MOE_ROUTE (moe.comp:25-50): expert ids and routing weights identical to
+  the oracle bit for bit (both rank by fp32 probability with a correctly
+  rounded exp and the reference's summation order).
 * GO_MOE_GATHER / GO_MOE_SCATTER (moe.comp:124-126): exact.
 * TLLMMoE.forward (LLM.MoE.pas:376-448) replayed op by op on this backend,
   and the device-routed qnn_moe_experts: within a normwise relative error of
@@ -35,7 +36,22 @@ def test_route_matches_oracle(ctx, rng, rows, E, k, normalize):
     _, ids, probs = route_on_gpu(ctx, logits, k, normalize)
     want_ids, want_p = oracle.moe_route(logits, k, normalize)
     assert np.array_equal(ids, want_ids)
-    assert np.allclose(probs, want_p, rtol=2e-6, atol=0)
+    assert np.array_equal(probs.view(np.uint32), want_p.view(np.uint32))
+
+
+@pytest.mark.parametrize("E,k", [(128, 1), (128, 2), (2000, 2)])  # register and LDS selection
+def test_route_equal_probabilities_of_distinct_logits_tie_to_lower_id(ctx, E, k):
+    """moe.comp:36-46 ranks by probability: logits 0 (id 7) and -1e-8 (id 3)
+    give exp values that both round to 1.0f, so their probabilities are equal
+    and the lower id ranks first although its logit is smaller."""
+    logits = np.full((1, E), -4.0, np.float32)
+    logits[0, 7], logits[0, 3] = 0.0, -1e-8
+    _, ids, probs = route_on_gpu(ctx, logits, k)
+    want_ids, want_p = oracle.moe_route(logits, k)
+    assert ids[0].tolist() == [3, 7][:k] == want_ids[0].tolist()
+    assert np.array_equal(probs.view(np.uint32), want_p.view(np.uint32))
+    by_logit, _ = oracle.moe_route(logits, k, select_on_logits=True)
+    assert by_logit[0, 0] == 7  # the logit rule would rank id 7 first
 
 
 @pytest.mark.parametrize("E", [6, 2000])  # register and LDS selection
@@ -45,7 +61,7 @@ def test_route_signed_zero_and_equal_logits_tie_to_lower_id(ctx, E):
     _, ids, probs = route_on_gpu(ctx, logits, 3)
     want_ids, want_p = oracle.moe_route(logits, 3)
     assert ids[0].tolist() == [1, 3, 5] == want_ids[0].tolist()
-    assert np.allclose(probs, want_p, rtol=2e-6, atol=0)
+    assert np.array_equal(probs.view(np.uint32), want_p.view(np.uint32))
 
 
 def test_route_ties_take_lower_id(ctx):

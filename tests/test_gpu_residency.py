@@ -100,3 +100,46 @@ def test_retain_and_capacity(small, rng):
         ctx.Int4Linear(ctx.NewTensor(4 * N), xt, big, 1, K, 4 * N)
     ctx.Recycle(xt)
     ctx.Recycle(yt)
+
+
+def test_on_weight_evicted_reports_each_evicted_identity(small, rng):
+    """OnWeightEvicted (Context.API.inc:164) hears the identity of every entry
+    the cache evicts, in LRU order (QuickNN.Vulkan.pas:568-569); the MoE layer
+    uses it to hand the native bytes back to its cache (LLM.MoE.pas:196-203).
+    Streams six matrices through the three-matrix cache (less what earlier
+    tests retained), so each new one evicts the oldest."""
+    ctx = small
+    ctx.Flush()
+    ws = mats(rng, 6)
+    ids = [w.identity for w in ws]
+    xt, yt = ctx.UploadRaw(rng.standard_normal(K).astype(np.float32)), ctx.NewTensor(N)
+    heard = []
+    ctx.OnWeightEvicted = heard.append
+    e0 = ctx.status().weight_evictions
+    for w in ws:
+        run(ctx, w, xt, yt)
+    assert len(heard) == ctx.status().weight_evictions - e0 >= 3
+    ours = [i for i in heard if i in ids]
+    assert ours == ids[:len(ours)] and len(ours) >= 3  # ours leave oldest first
+    for w in ws[:len(ours)]:
+        assert not ctx.IsWeightResident(w, N, w.shape[1])
+    ctx.OnWeightEvicted = None
+    n = len(heard)
+    run(ctx, ws[0], xt, yt)  # evicts again; nobody is told
+    assert len(heard) == n
+    ctx.Recycle(xt)
+    ctx.Recycle(yt)
+
+
+def test_upload_memory_block(small, rng):
+    """Upload(TMemoryBlock) (Context.Implementation.inc:700-705): F32 storage only,
+    Size floats from element Offset (Common.pas:1597-1605)."""
+    from quicknn_amd import hip
+
+    ctx = small
+    v = rng.standard_normal(100).astype(np.float32)
+    t = ctx.Upload(hip.MemoryBlock(v, (100,), hip.DT_F32, offset=10, size=60))
+    assert t.count == 60 and np.array_equal(ctx.Download(t), v[10:70])
+    with pytest.raises(hip.EArgumentException):
+        ctx.Upload(hip.MemoryBlock(v.view(np.uint16)[:100], (100,), hip.DT_BF16))
+    ctx.Recycle(t)

@@ -1,8 +1,9 @@
 """Pins the MoE part of the oracle.
 
 The reference has no CPU MoE; the oracle restates the route op (moe.comp:25-50:
-fp32 softmax, k rounds of argmax with ties to the lower id, optional
-renormalisation by the top-k sum) and the expert accumulation of
+fp32 softmax, k rounds of argmax over the probabilities with ties to the
+lower id, optional renormalisation by the top-k sum; exp correctly rounded,
+the denominator in the shader's 256-partial order) and the expert accumulation of
 TLLMMoE.forward (LLM.MoE.pas:376-448: experts in ascending id, out += y*p,
 moe.comp:70 and :125-126).  Pins: route invariants, a brute-force stable sort
 on small and tied inputs, and a float64 brute-force composition of the expert
@@ -43,6 +44,40 @@ def test_route_ties_take_lower_id():
     ids, probs = oracle.moe_route(logits, 4, True)
     assert ids[0].tolist() == [1, 2, 4, 0]
     assert probs[0][0] == probs[0][1] == probs[0][2]
+
+
+def test_route_exp_is_correctly_rounded_and_sum_is_close():
+    """v = exp(l - max) rounded once: p * denominator reproduces the float64
+    exponential to within half an ulp plus the division's rounding, and the
+    denominator is within the float32 summation bound of the float64 sum."""
+    logits = np.linspace(-30, 3, 300).astype(np.float32)[None, :]
+    ids, probs = oracle.moe_route(logits, 64, False)
+    e64 = np.exp(logits[0].astype(np.float64) - float(logits.max()))
+    den = e64.sum()
+    rel = np.abs(probs[0].astype(np.float64) * den - e64[ids[0]]) / e64[ids[0]]
+    assert np.all(rel < 3 * 2.0 ** -24 + 300 * 2.0 ** -24)
+
+
+def test_route_equal_probabilities_of_distinct_logits_tie_to_lower_id():
+    """moe.comp:36-46 compares probabilities: exp(-1e-8) rounds to 1.0f, so ids
+    3 (logit -1e-8) and 7 (logit 0) have equal probability and 3 ranks first.
+    Ranking by logit would put 7 first."""
+    logits = np.full((1, 128), -4.0, np.float32)
+    logits[0, 7], logits[0, 3] = 0.0, -1e-8
+    assert np.float32(np.exp(np.float64(np.float32(-1e-8)))) == np.float32(1.0)
+    ids, probs = oracle.moe_route(logits, 2, True)
+    assert ids[0].tolist() == [3, 7] and probs[0, 0] == probs[0, 1] == np.float32(0.5)
+    by_logit, _ = oracle.moe_route(logits, 2, True, select_on_logits=True)
+    assert by_logit[0].tolist() == [7, 3]
+
+
+def test_route_denominator_equal_terms():
+    """All experts equal: every v is 1, the partial sums and the tree are exact,
+    so p = 1/E exactly, whatever E (here beyond the 256 partials)."""
+    for E in (5, 256, 300, 1000):
+        ids, probs = oracle.moe_route(np.zeros((1, E), np.float32), 4, False)
+        assert ids[0].tolist() == [0, 1, 2, 3]
+        assert np.all(probs == np.float32(1.0) / np.float32(E))
 
 
 def test_route_logit_and_probability_selection_agree_without_ties(rng):
