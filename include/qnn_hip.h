@@ -181,6 +181,23 @@ int qnn_vector_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_
 int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
                     int out_dim);
 
+/* No counterpart in the reference.  Int4Linear for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): same arguments and results as
+ * qnn_int4_linear (bit for bit), but it never uploads, records or allocates.
+ *  - The weight must already be resident (RetainWeight / PreloadWeights /
+ *    an earlier call); otherwise QNN_E_INVALID_OP.
+ *  - in_dim must be a multiple of 4 (QNN_E_ARGUMENT), and the projection's
+ *    split-K workspace must fit the library's fixed device scratch of 8 MiB
+ *    per GPU (7 MiB partial sums, 1 MiB tickets), else QNN_E_RANGE.
+ *  - Every call on a GPU shares that scratch; calls are ordered on the
+ *    context's stream, so two of them that overlap on one GPU (for example a
+ *    captured graph replayed on another stream during an eager call) race.
+ *  - Calls recorded before it are launched first; they sized their own
+ *    workspace when they were recorded. */
+int qnn_int4_linear_noalloc(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows,
+                            int in_dim, int out_dim);
+
 /* TrySwiGLUVector (Context.API.inc:132-133, Implementation.inc:1003-1056):
  * dst[o] = silu(gate.x)[o] * (up.x)[o].  Returns QNN_OK, or QNN_NOT_HANDLED
  * where the reference returns False (unsupported dtype mix, or the pair does

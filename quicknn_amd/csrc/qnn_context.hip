@@ -467,8 +467,16 @@ struct OpPins {
 };
 
 // ---------------------------------------------------------------- INT4 projection
+// Caller-provided split-K workspace (the no-allocation entry point's static
+// scratch): its tickets are cleared by a fill kernel before every launch.
+struct FixedWs {
+  float *partial = nullptr;
+  unsigned *counters = nullptr;
+};
+
 void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
-              int rows, int in_dim, int out_dim, const float *prob, float *g_out = nullptr, float *u_out = nullptr) {
+              int rows, int in_dim, int out_dim, const float *prob, float *g_out = nullptr, float *u_out = nullptr,
+              const FixedWs *fixed = nullptr) {
   const I4Layout &l = w->i4;
   // The kernels read activation rows as aligned 4-float pieces: a row length
   // that is not a multiple of 4 goes through a zero-padded copy.
@@ -505,9 +513,15 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
       a.u_out = u_out + size_t(r0) * out_dim;
     }
     const I4Plan p = int4_plan(l, m, mode);
-    ensure_splitk(ctx, p.partial_floats, p.counters);
-    a.partial = ctx->partial;
-    a.counters = ctx->counters;
+    if (fixed) {
+      misc_fill(reinterpret_cast<float *>(fixed->counters), int(p.counters), 0u, ctx->stream);
+      a.partial = fixed->partial;
+      a.counters = fixed->counters;
+    } else {
+      ensure_splitk(ctx, p.partial_floats, p.counters);
+      a.partial = ctx->partial;
+      a.counters = ctx->counters;
+    }
     a.err = ctx->error_flag;
     int4_matvec_launch(a, p, ctx->stream);
   }
@@ -608,6 +622,13 @@ void record_linear(qnn_ctx_s *ctx, WeightEntry *e, const float *x, float *y, int
   g.out[g.count] = out_dim;
   g.slices[g.count] = slices;
   g.count++;
+  // The group's launch workspace, sized now so that launching it never allocates.
+  size_t pf = 0, nc = 0;
+  for (int i = 0; i < g.count; ++i) {
+    pf += g.slices[i] > 1 ? size_t(g.e[i]->gg.tiles) * g.slices[i] * 64 : 0;
+    nc += size_t(g.e[i]->gg.tiles) * kCounterStride;
+  }
+  ensure_splitk(ctx, pf, nc);
 }
 
 // ---------------------------------------------------------------- fused decode MLP
@@ -789,6 +810,11 @@ int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out) {
     }
     if (device < 0 || device >= n) fail(QNN_E_ARGUMENT, "device index");
     hip_check(hipSetDevice(device), "hipSetDevice");
+    try {
+      noalloc_scratch_init(device);  // the static scratch's address on this device, once
+    } catch (const Error &) {
+      // only qnn_int4_linear_noalloc needs it; that call reports the failure
+    }
     auto *ctx = new qnn_ctx_s();
     ctx->device = device;
     ctx->owner = std::this_thread::get_id();
@@ -1063,7 +1089,18 @@ int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_we
                          dst->ptr != p.h && try_fused_mlp(ctx, e, dst->ptr);
       // Several rows: recorded to meet a following GO_SWIGLU (gate, up).
       qnn_ctx_s::PendingRows &q = ctx->prows;
-      if (!fused && rows >= 2 && !ctx->capturing && mlp_fusion_enabled() && glu_plans_match(e->i4, rows)) {
+      if (!fused && rows >= 2 && !ctx->capturing && mlp_fusion_enabled() && in_dim % 4 == 0 &&
+          glu_plans_match(e->i4, rows)) {
+        // Sized now (its own launch and the gate/up SwiGLU launch it may join),
+        // so that launching it never allocates.
+        size_t pf = 0, nc = 0;
+        for (int r0 = 0; r0 < rows; r0 += 16) {
+          const I4Plan a = int4_plan(e->i4, std::min(16, rows - r0), I4_STORE);
+          const I4Plan b = int4_plan(e->i4, std::min(16, rows - r0), I4_SWIGLU);
+          pf = std::max({pf, a.partial_floats, b.partial_floats});
+          nc = std::max({nc, a.counters, b.counters});
+        }
+        ensure_splitk(ctx, pf, nc);
         if (q.count == 1 && q.x == src->ptr && q.rows == rows && q.in == in_dim && q.out == out_dim &&
             dst->ptr != q.y[0] && e->i4.rows == q.e[0]->i4.rows && e->i4.cols == q.e[0]->i4.cols &&
             e->i4.lanes == q.e[0]->i4.lanes) {
@@ -1090,6 +1127,50 @@ int qnn_int4_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_we
       settle_pending(ctx);
       throw;
     }
+    ctx->st.gemm_calls++;
+    ctx->st.int4_calls++;
+    return QNN_OK;
+  });
+}
+
+int qnn_int4_linear_noalloc(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
+                            int out_dim) {
+  return guarded([&] {
+    check_ctx(ctx, true);
+    // Recorded calls sized their workspace when they were recorded, so
+    // launching them here allocates nothing either.
+    settle_pending(ctx);
+    // Int4Linear validation (Context.Implementation.inc:1091-1104), plus the
+    // limits of this variant.
+    if (rows < 1 || rows > 128 || in_dim < 1 || out_dim < 1 || src == dst || int64_t(rows) * out_dim > 0x7fffffff)
+      fail(QNN_E_ARGUMENT, "Invalid packed INT4 projection");
+    if (in_dim % 4 != 0)
+      fail(QNN_E_ARGUMENT, "the no-allocation INT4 projection needs an input width that is a multiple of 4");
+    check_tensor(ctx, src, int64_t(rows) * in_dim);
+    check_tensor(ctx, dst, int64_t(rows) * out_dim);
+    check_weight_desc(w);
+    const int rb = qnn_int4_row_bytes(in_dim);
+    if (w->dtype != QNN_DT_U8 || w->encoding != QNN_WE_NATIVE || w->offset != 0 || rb < 0 || w->shape0 != out_dim ||
+        w->shape1 != rb || int64_t(out_dim) * rb > w->size)
+      fail(QNN_E_ARGUMENT, "Invalid packed INT4 projection");
+    WeightEntry *e = lookup(ctx, weight_key("i4", w, uint64_t(out_dim) * rb));
+    if (!e)
+      fail(QNN_E_INVALID_OP,
+           "weight not resident: the no-allocation projection does not upload (RetainWeight or PreloadWeights it first)");
+    auto *base = static_cast<uint8_t *>(noalloc_scratch(ctx->device));
+    if (!base) fail(QNN_E_INVALID_OP, "the static scratch of the no-allocation projection is not available on this device");
+    for (int r0 = 0; r0 < rows; r0 += 16) {
+      const I4Plan p = int4_plan(e->i4, std::min(16, rows - r0), I4_STORE);
+      if (p.partial_floats * 4 > kNoAllocPartialBytes || p.counters * 4 > kNoAllocCounterBytes)
+        fail(QNN_E_RANGE, "INT4 projection too large for the no-allocation scratch (7 MiB of partial sums, "
+                          "1 MiB of tickets); use qnn_int4_linear");
+    }
+    FixedWs ws;
+    ws.partial = reinterpret_cast<float *>(base);
+    ws.counters = reinterpret_cast<unsigned *>(base + kNoAllocPartialBytes);
+    OpPins pin;
+    pin(e);
+    run_int4(ctx, e, nullptr, I4_STORE, src->ptr, dst->ptr, rows, in_dim, out_dim, nullptr, nullptr, nullptr, &ws);
     ctx->st.gemm_calls++;
     ctx->st.int4_calls++;
     return QNN_OK;
@@ -1147,7 +1228,10 @@ int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_
       WeightEntry *eu = pin(acquire_int4(ctx, up, out_dim, in_dim));
       if (mlp_fusion_enabled() && !ctx->capturing && eg->i4.lanes == 1 && in_dim % 4 == 0 && out_dim % 4 == 0) {
         // Recorded: launched with the next call (fused if that is the down
-        // projection of this output).  Pinned until then.
+        // projection of this output).  Pinned until then; the workspace of
+        // its own launch is sized now, so launching it never allocates.
+        const I4Plan pp = int4_plan(eg->i4, 1, I4_SWIGLU);
+        ensure_splitk(ctx, pp.partial_floats, pp.counters);
         eg->pins++;
         eu->pins++;
         ctx->pending.on = true;

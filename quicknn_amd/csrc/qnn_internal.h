@@ -238,6 +238,14 @@ void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, co
 void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
 
 
+// Fixed device scratch of the no-allocation INT4 projection (qnn_noalloc.hip):
+// [split-K partial sums: 7 MiB][arrival tickets: 1 MiB], one copy per GPU.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+constexpr size_t kNoAllocCounterBytes = size_t(1) << 20;
+constexpr size_t kNoAllocPartialBytes = kNoAllocScratchBytes - kNoAllocCounterBytes;
+void noalloc_scratch_init(int device);  // with `device` current: resolves and keeps its copy's address
+void *noalloc_scratch(int device);      // that address, or null if set-up failed
+
 // F32 / BF16 weights, row-major [n, k] (qnn_dense.hip): y = W x for one row,
 // Y[m, n] = X[m, k] W^T for several.
 void dense_matvec_launch(const void *w, int bf16, const float *x, float *y, int n, int k, hipStream_t s);

@@ -115,6 +115,7 @@ def lib():
             "qnn_vector_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int]),
             "qnn_linear": (ctypes.c_int, [_vp, _vp, _vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_int4_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "qnn_int4_linear_noalloc": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_swiglu_vector": (ctypes.c_int, [_vp, _vp, _vp, W, W, ctypes.c_int, ctypes.c_int]),
             "qnn_int4_linear_accumulate": (ctypes.c_int, [_vp, _vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int,
                                                           ctypes.c_int]),
@@ -150,7 +151,7 @@ EXPORTED = (
     "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_tensor_new", "qnn_recycle",
     "qnn_scratch", "qnn_upload_raw", "qnn_download", "qnn_copy", "qnn_flush", "qnn_tensor_count",
     "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
-    "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_int4_linear", "qnn_swiglu_vector",
+    "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_int4_linear", "qnn_int4_linear_noalloc", "qnn_swiglu_vector",
     "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
     "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
@@ -419,6 +420,12 @@ class GPUContext:
         rc = _raise(lib().qnn_swiglu_vector(self.h, dst.handle, src.handle, _wd(gate), _wd(up), input_dim,
                                             output_dim))
         return rc == QNN_OK
+
+    def Int4LinearNoAlloc(self, dst: Tensor, src: Tensor, weight: MemoryBlock, rows: int, input_dim: int,
+                          output_dim: int) -> None:
+        """qnn_int4_linear_noalloc: Int4Linear without device allocation (resident weight, fixed scratch)."""
+        _raise(lib().qnn_int4_linear_noalloc(self.h, dst.handle, src.handle, _wd(weight), rows, input_dim,
+                                             output_dim))
 
     def Int4LinearAccumulate(self, dst: Tensor, src: Tensor, probabilities: Tensor, weight: MemoryBlock,
                              input_dim: int, output_dim: int, probability_index: int) -> None:
