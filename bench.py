@@ -21,7 +21,8 @@ runs of it); batch-8 figures; and the reference's CPU SIMD path (an AVX2
 restatement in the CPU oracle) timed on this host on the same packed weights.
 
 The other workloads of the benchmark definition are measured with
-`--config 1|3|4|5` (one JSON line each, same fields):
+`--config 1|3|4|5` (one JSON line each, same fields), and the default run
+also times each of them briefly and reports them under `other_configs`:
   1  one INT4 matvec 6144x2048 (Qwen3-1.7B gate shape), batch 1;
   3  Gemma-2-9B-shaped GGUF K-quant decode layer (Q4_K q/o, Q3_K k/v, Q2_K
      gate/up + GEGLU, Q6_K down) and the Q6_K output head;
@@ -96,6 +97,26 @@ def gguf_matrix(hip, enc: int, n: int, k: int, seed: int, max_rows: int = 16384)
     return np.ascontiguousarray(b).reshape(-1)
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def traffic_calibration_copy(ctx) -> None:
+    """For rocprofv3 --pmc runs: one device-to-device copy of a known 64 MiB
+    (its FETCH_SIZE / WRITE_SIZE give the counters' bytes-per-KiB factors)."""
+    a, b = ctx.NewTensor(16 << 20), ctx.NewTensor(16 << 20)
+    ctx.Copy(b, a, 16 << 20)
+    ctx.Flush()
+    ctx.Recycle(a)
+    ctx.Recycle(b)
+
+
 def base_line(args, metric, value, unit, ms_step, dtype, data, config, **extra) -> dict:
     line = {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
@@ -113,21 +134,29 @@ def cpu_baseline_mlp(packed, x0: np.ndarray, budget_s: float, wbytes: int, abyte
     the oracle, at the reference default of min(8, nproc) worker threads."""
     import oracle
 
-    pool = oracle.Pool(0)
-    layers_done, t0 = 0, time.perf_counter()
-    x = x0.copy()
-    while True:
-        g, u, d = packed[layers_done % LAYERS]
-        x = oracle.cpu_mlp(g, u, d, oracle.ENC_INT4, x, HIDDEN, INTER, pool)[0]
-        layers_done += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s and layers_done >= LAYERS:
-            break
-    us_layer = el / layers_done * 1e6
-    return {"value": round((wbytes + abytes) / (us_layer * 1e-6) / 1e9, 2), "unit": "GB/s",
-            "cores": pool.threads, "kind": "port",
-            "sample": f"{layers_done} INT4 MLP layers at batch 1 ({el:.1f} s), same packed weights; "
-                      f"{us_layer:.0f} us/layer; nproc={os.cpu_count()}"}
+    def timed(pool, budget):
+        layers_done, t0 = 0, time.perf_counter()
+        x = x0.copy()
+        while True:
+            g, u, d = packed[layers_done % LAYERS]
+            x = oracle.cpu_mlp(g, u, d, oracle.ENC_INT4, x, HIDDEN, INTER, pool)[0]
+            layers_done += 1
+            el = time.perf_counter() - t0
+            if el >= budget and layers_done >= LAYERS:
+                return layers_done, el
+
+    pool = oracle.Pool(0)  # the reference default: min(8, nproc) threads (CPU.Inference.pas:112-115)
+    n8, el8 = timed(pool, budget_s)
+    us8 = el8 / n8 * 1e6
+    allc = oracle.Pool(min(64, os.cpu_count() or 1))  # every core this process may use (the pool's cap is 64)
+    na, ela = timed(allc, budget_s / 2)
+    usa = ela / na * 1e6
+    gbs = lambda us: round((wbytes + abytes) / (us * 1e-6) / 1e9, 2)
+    return {"value": gbs(us8), "unit": "GB/s", "cores": pool.threads, "kind": "port",
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "all_cores": {"value": gbs(usa), "cores": allc.threads, "us_per_layer": round(usa, 1)},
+            "sample": f"{n8} INT4 MLP layers at batch 1 ({el8:.1f} s) with {pool.threads} threads, {us8:.0f} us/layer; "
+                      f"{na} layers ({ela:.1f} s) with {allc.threads} threads; same packed weights"}
 
 
 def run_cfg2(args, hip) -> dict:
@@ -218,12 +247,35 @@ def run_cfg2(args, hip) -> dict:
     ctx.EventRecord(5)
     ms8 = ctx.EventElapsedMs(4, 5) / n8
 
-    # Traffic calibration for rocprofv3 --pmc runs: one device-to-device copy
-    # of a known 64 MiB (FETCH_SIZE / WRITE_SIZE of this copy give the
-    # counter's bytes-per-KiB factor).
-    cal_a, cal_b = ctx.NewTensor(16 << 20), ctx.NewTensor(16 << 20)
-    ctx.Copy(cal_b, cal_a, 16 << 20)
+    # The engine's call order (LLM.pas:588-598, QwenHybrid.pas:692-702): each
+    # layer's outputs are created right before the projection that writes them
+    # and released afterwards (its TGPUWorkspace).  Same launches (the fused
+    # MLP per layer); the figure adds this host's per-call overhead.
+    def step_engine():
+        src = x
+        for (g, u, d) in blocks:
+            hh = ctx.NewTensor(INTER)
+            ctx.TrySwiGLUVector(hh, src, g, u, HIDDEN, INTER)
+            yy = ctx.NewTensor(HIDDEN)
+            ctx.Int4Linear(yy, hh, d, 1, INTER, HIDDEN)
+            ctx.Recycle(hh)
+            if src is not x:
+                ctx.Recycle(src)
+            src = yy
+        ctx.Recycle(src)
+
+    step_engine()
     ctx.Flush()
+    fused1 = ctx.status().mlp_fused
+    ne = max(5, args.steps // 5)
+    ctx.EventRecord(8)
+    for _ in range(ne):
+        step_engine()
+    ctx.EventRecord(9)
+    engine_us = ctx.EventElapsedMs(8, 9) * 1000 / (ne * LAYERS)
+    engine_fused = ctx.status().mlp_fused - fused1 == ne * LAYERS
+
+    traffic_calibration_copy(ctx)
 
     traffic = None  # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     tpath = os.path.join(ROOT, "profiles", "int4_mlp_fused_qwen3_4b_traffic.json")
@@ -236,7 +288,7 @@ def run_cfg2(args, hip) -> dict:
 
     cpu = None if args.no_cpu else cpu_baseline_mlp(packed, x1, args.cpu_seconds, wbytes, abytes1)
     return base_line(
-        args, METRIC, value, "GB/s", ms_step, "int4-w/fp32-acc",
+        args, METRIC, value, "GB/s", ms_step, "int4-w/x16-fixed-act/fp32-acc",
         "synthetic (seeded N(0,0.02) bf16 weights packed to QuickNN INT4; N(0,1) RMS-normalised activations)",
         {"workload": "configs[1]: Qwen3-4B MLP, hidden 2560, intermediate 9728, fused gate+up SwiGLU "
                      "then down, native INT4, 36 layers, batch 1",
@@ -244,6 +296,10 @@ def run_cfg2(args, hip) -> dict:
         pct_of_hbm_peak=round(100 * value / HBM_PEAK_GBS, 2),
         us_per_layer=round(us_layer, 3),
         tokens_per_s=round(1000.0 / ms_step, 1),
+        engine_order={"us_per_layer": round(engine_us, 3), "fused_every_layer": engine_fused,
+                      "note": "NewTensor before and Recycle after each projection, as the engine's workspace does"},
+        arithmetic="weights INT4 exact; activations per 32-group 16-bit fixed point (two int8 planes) into "
+                   "v_dot4_i32_i8, exact integer group sums, fp32 scale and accumulation",
         batch8={"us_per_layer": round(ms8 * 1000 / LAYERS, 3),
                 "GBps": round((wbytes + abytes8) * LAYERS / (ms8 * 1e-3) / 1e9, 1),
                 "tokens_per_s": round(8000.0 / ms8, 1)},
@@ -280,6 +336,7 @@ def run_cfg1(args, hip) -> dict:
     for _ in range(args.warmup):
         step()
     ms_step = timed_ms(ctx, step, args.steps)
+    traffic_calibration_copy(ctx)
     ctx.close()
     nbytes = packed.size + 4 * (K + N)
     us = ms_step * 1000 / R
@@ -297,7 +354,7 @@ def run_cfg1(args, hip) -> dict:
         cpu = {"value": round(nbytes * n / el / 1e9, 2), "unit": "GB/s", "cores": pool.threads, "kind": "port",
                "sample": f"{n} matvecs ({el:.1f} s), {el / n * 1e6:.0f} us each; nproc={os.cpu_count()}"}
     return base_line(
-        args, "INT4 matvec HBM GB/s, 6144x2048", achieved, "GB/s", ms_step, "int4-w/fp32-acc",
+        args, "INT4 matvec HBM GB/s, 6144x2048", achieved, "GB/s", ms_step, "int4-w/x16-fixed-act/fp32-acc",
         f"synthetic (seeded N(0,0.02) bf16 packed to QuickNN INT4; x N(0,1)); {R} distinct weight copies rotated",
         {"workload": "configs[0]: native INT4 matvec, N 6144, K 2048, batch 1", "global_batch": 1},
         us_per_matvec=round(us, 3), pct_of_hbm_peak=round(100 * achieved / HBM_PEAK_GBS, 2),
@@ -361,6 +418,7 @@ def run_cfg3(args, hip) -> dict:
         t = timed_ms(ctx, lambda: [ops[nm](lay) for lay in layers], max(3, args.steps // 5)) * 1000 / L
         per_op[nm] = {"us": round(t, 2), "GBps": round(wbytes[nm] / (t * 1e-6) / 1e9, 1)}
     head_us = timed_ms(ctx, lambda: ctx.Linear(logits, xt, head_b, None, None, 1, H, V), 20) * 1000
+    traffic_calibration_copy(ctx)
     ctx.close()
     dom = max(per_op, key=lambda nm: per_op[nm]["us"])
     value = layer_b / (us_layer * 1e-6) / 1e9
@@ -390,7 +448,8 @@ def run_cfg3(args, hip) -> dict:
                "sample": f"{n} Gemma layers ({el:.1f} s, {el / n * 1e6:.0f} us/layer): TCPUProjection.Linear "
                          f"with the direct PackedDot paths (Q2_K block decode + VectorDot); nproc={os.cpu_count()}"}
     return base_line(
-        args, "GGUF K-quant decode HBM GB/s + us/layer, Gemma-2-9B shape", value, "GB/s", ms_step, "gguf-w/fp32-acc",
+        args, "GGUF K-quant decode HBM GB/s + us/layer, Gemma-2-9B shape", value, "GB/s", ms_step,
+        "gguf-w/x16-fixed-act/fp32-acc",
         "synthetic (N(0,0.02) fp32 encoded to GGML blocks; rows past 16384 repeat; x N(0,1)); "
         f"{L} layer copies rotated ({L * sum(wbytes.values()) / 1e6:.0f} MB)",
         {"workload": "configs[2]: Gemma-2-9B layer, hidden 3584, q/o Q4_K, k/v Q3_K, gate/up Q2_K + GEGLU, "
@@ -466,6 +525,7 @@ def run_cfg4(args, hip) -> dict:
         res[rows] = {"ms_step": ms, "us_per_layer": round(us_layer, 2), "distinct_experts": round(distinct / L, 1),
                      "GBps": round(nbytes / (us_layer * 1e-6) / 1e9, 1), "bytes": nbytes, "x": x,
                      "logits": first_logits, "route_us": round(us_route, 2), "route_plus_experts_us": round(us_both, 2)}
+    traffic_calibration_copy(ctx)
     ctx.close()
     r1 = res[1]
     cpu = None
@@ -484,7 +544,7 @@ def run_cfg4(args, hip) -> dict:
                          f"(gate, up, down) TCPUProjection.Linear + weighted sum; nproc={os.cpu_count()}"}
     return base_line(
         args, "MoE routed-expert HBM GB/s + us/layer, Qwen3-30B-A3B shape INT4", r1["GBps"], "GB/s", r1["ms_step"],
-        "int4-w/fp32-acc",
+        "int4-w/x16-fixed-act/fp32-acc",
         "synthetic (N(0,0.02) bf16 experts packed to INT4; router logits N(0,1), top-8 renormalised); "
         f"{L} layer copies with their own routes rotated",
         {"workload": "configs[3]: 128 experts, hidden 2048, expert inter 768, top-8, batch 1 (batch 16 below)",
@@ -522,6 +582,7 @@ def run_cfg5(args, hip) -> dict:
     for _ in range(max(1, args.warmup)):
         step()
     ms_step = timed_ms(ctx, step, args.steps)
+    traffic_calibration_copy(ctx)
     ctx.close()
     us = ms_step * 1000 / R
     tflops = 2.0 * M * N * K / (us * 1e-6) / 1e12
@@ -561,6 +622,7 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-others", action="store_true", help="config 2 only: skip the other configs' summaries")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -569,8 +631,27 @@ def main() -> int:
 
     from quicknn_amd import hip
 
-    run = {1: run_cfg1, 2: run_cfg2, 3: run_cfg3, 4: run_cfg4, 5: run_cfg5}[args.config]
-    print(json.dumps(run(args, hip)))
+    runs = {1: run_cfg1, 2: run_cfg2, 3: run_cfg3, 4: run_cfg4, 5: run_cfg5}
+    line = runs[args.config](args, hip)
+    if args.config == 2 and not args.no_others:
+        # The other workloads of the benchmark definition, in the same run (so
+        # the driver's clock covers them): short timings, no CPU legs.
+        sub = argparse.Namespace(**vars(args))
+        sub.steps, sub.warmup, sub.no_cpu = max(5, args.steps // 5), 2, True
+        others = {}
+        for c in (1, 3, 4, 5):
+            t0 = time.perf_counter()
+            r = runs[c](sub, hip)
+            rf = r["roofline"]
+            others[f"cfg{c}"] = {
+                "workload": r["config"]["workload"], "metric": r["metric"], "value": r["value"], "unit": r["unit"],
+                "dtype": r["dtype"], "kernel": rf["kernel"], "kernel_us": rf["kernel_us"],
+                "roofline_frac": rf["frac"], "roofline_bound": rf["bound"], "roofline_peak": rf["peak"],
+                **{k: r[k] for k in ("us_per_matvec", "us_per_layer", "us_per_gemm", "head", "batch16", "per_op",
+                                     "route_plus_experts_us", "hbm_GBps") if k in r},
+                "steps": sub.steps, "wall_s": round(time.perf_counter() - t0, 1)}
+        line["other_configs"] = others
+    print(json.dumps(line))
     return 0
 
 
