@@ -165,6 +165,17 @@ int qnn_set_weight_evicted(qnn_ctx *ctx, qnn_weight_evicted_fn fn, void *user);
 int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, const qnn_weight *scales,
                const qnn_weight *bias, int rows, int in_dim, int out_dim);
 
+/* No counterpart in the reference: the benchmark's prefill GEMM for a Q8_0
+ * weight [out_dim, in_dim], dst[r] = W src[r] for rows r, with the
+ * activations quantised per 32-element block to int8 (d = max|x|/127 in fp32,
+ * q = roundf(x / d)) and the products on the int8 matrix cores.  Block b adds
+ * fma(float(S_b), dx * dw, acc) in ascending b, S_b the exact int32 block dot,
+ * so results are reproducible bit for bit.  The quantisation moves results
+ * about 5e-3 (normwise, N(0,1) activations) from the reference's fp32-
+ * activation product; qnn_linear stays within 1e-3 of it. */
+int qnn_q8_gemm_int8(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
+                     int out_dim);
+
 /* VectorLinear (Context.API.inc:130, Implementation.inc:969-1001): dst = W src for
  * an F32 or BF16 weight [out_dim, in_dim]; any other dtype is QNN_E_ARGUMENT.
  * The engine's router projection for one token (LLM.MoE.pas:363) and the

@@ -33,6 +33,7 @@ _lib = None
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
+_i8p = ctypes.POINTER(ctypes.c_int8)
 _vp = ctypes.c_void_p
 
 
@@ -74,6 +75,8 @@ def lib():
             "qo_cpu_moe": (ctypes.c_int, [_vp, ctypes.POINTER(_u8p), ctypes.POINTER(_u8p), ctypes.POINTER(_u8p),
                                           _f32p, _u32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, _f32p]),
+            "qo_q8_act_quant": (ctypes.c_int, [_f32p, ctypes.c_int, ctypes.c_int, _i8p, _f32p]),
+            "qo_q8_gemm_i8": (ctypes.c_int, [_u8p, _i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]),
             "qo_gguf_gemm_scalar": (ctypes.c_int, [_u8p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int,
                                                    ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int]),
             "qo_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
@@ -274,6 +277,27 @@ def gguf_gemm_scalar(w, enc, a, n, row_begin=0, row_end=None) -> np.ndarray:
     c = np.zeros((m, n), np.float32)
     _check(lib().qo_gguf_gemm_scalar(_p(w, _u8p), enc, _p(a, _f32p), m, k, n, _p(c, _f32p), row_begin, row_end),
            "gguf_gemm_scalar")
+    return c
+
+
+def q8_act_quant(a):
+    """Activations [m, k] -> (int8 q [m, k], fp32 d [m, k/32]): per 32-element block, GGML's Q8_0 rule."""
+    a = np.ascontiguousarray(a, np.float32)
+    m, k = a.shape
+    q = np.zeros((m, k), np.int8)
+    d = np.zeros((m, k // 32), np.float32)
+    _check(lib().qo_q8_act_quant(_p(a, _f32p), m, k, _p(q, _i8p), _p(d, _f32p)), "q8_act_quant")
+    return q, d
+
+
+def q8_gemm_i8(w, q, d, n) -> np.ndarray:
+    """The int8-activation Q8_0 GEMM: acc = fma(float(S_b), dx * dw, acc) over blocks in order."""
+    q = np.ascontiguousarray(q, np.int8)
+    d = np.ascontiguousarray(d, np.float32)
+    m, k = q.shape
+    c = np.zeros((m, n), np.float32)
+    _check(lib().qo_q8_gemm_i8(_p(np.ascontiguousarray(w, np.uint8), _u8p), _p(q, _i8p), _p(d, _f32p), m, k, n,
+                               _p(c, _f32p)), "q8_gemm_i8")
     return c
 
 

@@ -841,4 +841,60 @@ int qo_gguf_gemm_scalar(const uint8_t *w, int enc, const float *a, int m, int k,
   return 0;
 }
 
+// ===========================================================================
+// The benchmark's int8-activation prefill GEMM (configs[4]: "activations ...
+// quantized per 32-element block to int8 for the MFMA path").  The reference
+// has no such path (its multi-row GGUF product is the fp32/double one above);
+// these restate the rule the HIP kernel applies, so it can be checked bit for
+// bit, and the fp32 path above measures what the quantisation costs.
+// ===========================================================================
+
+// Per row and 32-element block: the public GGML Q8_0 reference rule
+// (quantize_row_q8_0_reference: amax = max|x|, d = amax / 127,
+// id = d ? 1/d : 0, q = roundf(x * id)), with d kept in fp32.
+// q: [m][k] int8; d: [m][k/32].
+int qo_q8_act_quant(const float *a, int m, int k, int8_t *q, float *d) {
+  if (!a || !q || !d || m < 1 || k < 32 || k % 32) return -1;
+  const int kb = k / 32;
+  for (int r = 0; r < m; ++r)
+    for (int b = 0; b < kb; ++b) {
+      const float *x = a + (size_t)r * k + (size_t)b * 32;
+      float amax = 0.0f;
+      for (int i = 0; i < 32; ++i) amax = std::max(amax, std::fabs(x[i]));
+      const float dd = amax / 127.0f;
+      const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+      for (int i = 0; i < 32; ++i) q[(size_t)r * k + (size_t)b * 32 + i] = int8_t(int(std::roundf(x[i] * id)));
+      d[(size_t)r * kb + b] = dd;
+    }
+  return 0;
+}
+
+// C[r][o] = sum over blocks b in ascending order of
+//   acc = fma(float(S_b), dx[r][b] * dw[o][b], acc),
+// S_b = the exact integer dot of the block's int8 activations and Q8_0 quants,
+// dw = the block's fp16 scale (GGUF.Quantization.pas:180-181).  w: Q8_0 rows
+// [n][k/32 blocks of 34 B].
+int qo_q8_gemm_i8(const uint8_t *w, const int8_t *q, const float *d, int m, int k, int n, float *c) {
+  if (!w || !q || !d || !c || m < 1 || n < 1 || k < 32 || k % 32) return -1;
+  const int kb = k / 32;
+  const size_t rb = (size_t)kb * 34;
+  for (int o = 0; o < n; ++o) {
+    const uint8_t *wr = w + (size_t)o * rb;
+    for (int r = 0; r < m; ++r) {
+      float acc = 0.0f;
+      for (int b = 0; b < kb; ++b) {
+        const uint8_t *blk = wr + (size_t)b * 34;
+        const float dw = half_to_float(uint16_t(blk[0] | (blk[1] << 8)));
+        const int8_t *xq = q + (size_t)r * k + (size_t)b * 32;
+        int32_t s = 0;
+        for (int i = 0; i < 32; ++i) s += int32_t(xq[i]) * int32_t(int8_t(blk[2 + i]));
+        const float t = d[(size_t)r * kb + b] * dw;
+        acc = std::fma(float(s), t, acc);
+      }
+      c[(size_t)r * n + o] = acc;
+    }
+  }
+  return 0;
+}
+
 }  // extern "C"

@@ -77,6 +77,10 @@ int qo_cpu_moe(void *pool, const uint8_t *const *gate, const uint8_t *const *up,
 int qo_gguf_gemm_scalar(const uint8_t *w, int enc, const float *a, int m, int k, int n,
                         float *c, int row_begin, int row_end);
 
+/* ---- int8-activation prefill GEMM (the benchmark's configs[4] path; no reference counterpart) ---- */
+int qo_q8_act_quant(const float *a, int m, int k, int8_t *q, float *d);          /* GGML Q8_0 rule, fp32 d */
+int qo_q8_gemm_i8(const uint8_t *w, const int8_t *q, const float *d, int m, int k, int n, float *c);
+
 /* ---- numerics helpers ---- */
 float qo_half_to_float(uint16_t h);            /* src/core/QuickNN.Common.pas:1799+ */
 uint16_t qo_float_to_half(float f);            /* round-to-nearest-even (test helper) */

@@ -1370,6 +1370,27 @@ int qnn_set_weight_evicted(qnn_ctx *ctx, qnn_weight_evicted_fn fn, void *user) {
   });
 }
 
+int qnn_q8_gemm_int8(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight *w, int rows, int in_dim,
+                     int out_dim) {
+  return guarded([&] {
+    check_ctx(ctx);
+    // Linear's validation (Context.Implementation.inc:826-829) for a Q8_0 weight.
+    check_tensor(ctx, src, int64_t(rows) * in_dim);
+    check_tensor(ctx, dst, int64_t(rows) * out_dim);
+    if (rows < 1 || in_dim < 1 || out_dim < 1 || src == dst)
+      fail(QNN_E_ARGUMENT, "Invalid resident linear dimensions/alias");
+    check_weight_desc(w);
+    if (w->encoding != QNN_WE_Q8_0) fail(QNN_E_NOT_SUPPORTED, "the int8-activation GEMM takes Q8_0 weights");
+    OpPins pin;
+    WeightEntry *e = pin(acquire_gguf(ctx, w, out_dim, in_dim));
+    void *ws = ensure_work(ctx, q8_i8_workspace(rows, in_dim));
+    q8_gemm_i8_launch(src->ptr, rows, in_dim, out_dim, e->gg, e->dptr, ws, dst->ptr, ctx->stream);
+    ctx->st.gemm_calls++;
+    ctx->st.gguf_calls++;
+    return QNN_OK;
+  });
+}
+
 int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_tensor *b, qnn_tensor *c,
                const int *args, int nargs) {
   return guarded([&] {

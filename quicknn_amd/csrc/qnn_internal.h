@@ -236,6 +236,11 @@ Q8GemmPlan q8_gemm_plan(int M, int K, int N);
 void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
                     void *frag, int *ea, float *c, hipStream_t s);
 void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
+// Multi-row Q8_0 projection with activations quantised per 32-element block to
+// int8, on the int8 matrix cores (qnn_gemm_i8.hip).  K % 32 == 0.
+size_t q8_i8_workspace(int M, int K);
+void q8_gemm_i8_launch(const float *a, int M, int K, int N, const GGLayout &l, const void *w, void *ws, float *c,
+                       hipStream_t s);
 
 
 // Fixed device scratch of the no-allocation INT4 projection (qnn_noalloc.hip):

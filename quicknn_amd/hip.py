@@ -115,6 +115,7 @@ def lib():
             "qnn_vector_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int]),
             "qnn_linear": (ctypes.c_int, [_vp, _vp, _vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_int4_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "qnn_q8_gemm_int8": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_int4_linear_noalloc": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_swiglu_vector": (ctypes.c_int, [_vp, _vp, _vp, W, W, ctypes.c_int, ctypes.c_int]),
             "qnn_int4_linear_accumulate": (ctypes.c_int, [_vp, _vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int,
@@ -151,7 +152,7 @@ EXPORTED = (
     "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_tensor_new", "qnn_recycle",
     "qnn_scratch", "qnn_upload_raw", "qnn_download", "qnn_copy", "qnn_flush", "qnn_tensor_count",
     "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
-    "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_int4_linear", "qnn_int4_linear_noalloc", "qnn_swiglu_vector",
+    "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_q8_gemm_int8", "qnn_int4_linear", "qnn_int4_linear_noalloc", "qnn_swiglu_vector",
     "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
     "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
@@ -407,6 +408,11 @@ class GPUContext:
                bias: MemoryBlock | None, rows: int, input_dim: int, output_dim: int) -> None:
         _raise(lib().qnn_linear(self.h, dst.handle, src.handle, _wd(weight), _wd(scales), _wd(bias), rows,
                                 input_dim, output_dim))
+
+    def Q8GemmInt8(self, dst: Tensor, src: Tensor, weight: MemoryBlock, rows: int, input_dim: int,
+                   output_dim: int) -> None:
+        """qnn_q8_gemm_int8: Q8_0 projection with per-32 int8 activations on the int8 matrix cores."""
+        _raise(lib().qnn_q8_gemm_int8(self.h, dst.handle, src.handle, _wd(weight), rows, input_dim, output_dim))
 
     def VectorLinear(self, dst: Tensor, src: Tensor, weight: MemoryBlock, input_dim: int, output_dim: int) -> None:
         _raise(lib().qnn_vector_linear(self.h, dst.handle, src.handle, _wd(weight), input_dim, output_dim))

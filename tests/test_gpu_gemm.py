@@ -107,3 +107,49 @@ def test_small_rows_use_matvec_and_agree(ctx, rng):
     two = run_linear(ctx, w, a[:2], n)     # matvec per row
     for r in range(2):
         assert normwise_rel_err(full[r], two[r]) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# The int8-activation GEMM (qnn_q8_gemm_int8): activations quantised per
+# 32-element block to int8 (K7), int32 block sums on the int8 matrix cores,
+# fma(float(S_b), dx * dw, acc) in block order (K8).  Bit-identical to the
+# oracle's restatement of the same rule; its distance from the reference's
+# fp32-activation product is the quantisation's (about 5e-3 normwise).
+# ---------------------------------------------------------------------------
+def run_int8(ctx, w, a, n):
+    m, k = a.shape
+    src, dst = ctx.UploadRaw(a), ctx.NewTensor(m * n)
+    ctx.Q8GemmInt8(dst, src, hip.MemoryBlock.gguf(w, n, k, ENC_Q8_0), m, k, n)
+    out = ctx.Download(dst).reshape(m, n)
+    ctx.Recycle(src)
+    ctx.Recycle(dst)
+    return out
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 32, 32), (3, 96, 100), (33, 256, 257), (64, 288, 64), (100, 1024, 130),
+                                   (130, 3072, 128)])
+def test_int8_gemm_bit_identical_to_oracle(ctx, rng, m, k, n):
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    a[0, :32] = 0.0  # a zero block: d = 0
+    w = q8(rng, n, k)
+    got = run_int8(ctx, w, a, n)
+    q, d = oracle.q8_act_quant(a)
+    want = oracle.q8_gemm_i8(w, q, d, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_int8_gemm_prefill_shape(ctx, rng):
+    """cfg5: A [512, 3072] x Q8_0 W [12288, 3072]; 12 rows spread over A (its
+    quantisation is per row) checked bit for bit against the oracle, and the
+    whole product against the fp32 path."""
+    m, k, n = 512, 3072, 12288
+    w = q8(rng, n, k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    got = run_int8(ctx, w, a, n)
+    rows = np.array([0, 1, 31, 32, 63, 64, 200, 255, 256, 384, 510, 511])
+    q, d = oracle.q8_act_quant(a[rows])
+    want = oracle.q8_gemm_i8(w, q, d, n)
+    assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
+    fp = run_linear(ctx, w, a, n)  # the fp32-level path (fp16 MFMA, within 1e-3 of the reference)
+    e = normwise_rel_err(got, fp)
+    assert 1e-4 < e < 1e-2, e
