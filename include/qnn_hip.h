@@ -104,6 +104,7 @@ typedef struct {
   uint64_t moe_fused;      /* one-token qnn_moe_experts calls run as a single launch (no reference counterpart) */
   uint64_t moe_route_fused; /* of those, with the preceding GO_MOE_ROUTE computed in the launch (no reference counterpart) */
   uint64_t glu_fused;      /* multi-row Int4Linear gate + up + GO_SWIGLU triples run as one launch (no reference counterpart) */
+  uint64_t async_weight_batches, async_weight_bytes; /* PrefetchWeights batches copied on the copy stream, and their bytes */
 } qnn_status;
 
 /* ---------------------------------------------------------------------------
@@ -145,6 +146,34 @@ int qnn_is_weight_resident(qnn_ctx *ctx, const qnn_weight *w, int rows, int cols
 int qnn_weight_batch_capacity(qnn_ctx *ctx, uint64_t *bytes);                  /* WeightBatchCapacity */
 /* OnWeightEvicted setter (Context.API.inc:164); fn = NULL clears it. */
 int qnn_set_weight_evicted(qnn_ctx *ctx, qnn_weight_evicted_fn fn, void *user);
+
+/* ---------------------------------------------------------------------------
+ * Asynchronous layer prefetch (Context.API.inc:88-95, Context.Prefetch.inc:92-456).
+ * Two slots, each a pinned host staging buffer and a device staging buffer of
+ * max_layer_bytes; uploads run on a copy stream (host -> device copy, then the
+ * repack into the weight cache) while the compute stream works.  The weights
+ * of a PrefetchWeights batch are complete 2-D matrices (offset 0, size =
+ * shape0 * shape1), pinned until the batch is released.  Any op that reads a
+ * prefetched entry first makes the compute stream wait for its slot.
+ * ------------------------------------------------------------------------- */
+/* EnableWeightPrefetch: *enabled = 0 when max_layer_bytes is 0, above 512 MiB,
+ * or above half the weight batch capacity (nothing is allocated then). */
+int qnn_enable_weight_prefetch(qnn_ctx *ctx, uint64_t max_layer_bytes, int *enabled);
+int qnn_begin_weight_prefetch(qnn_ctx *ctx);   /* BeginWeightPrefetch: launches recorded work */
+/* PrefetchWeights: QNN_E_INVALID_OP unless enabled with no batch queued;
+ * QNN_E_RANGE above the double-buffer budget.  defer_join = 0 also completes
+ * (CompleteWeightPrefetch). */
+int qnn_prefetch_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, int defer_join);
+/* StageWeightPrefetch: copies the next batch's host bytes into the free
+ * slot's staging buffer now, so the following PrefetchWeights of the same
+ * weights only starts the device copy. */
+int qnn_stage_weight_prefetch(qnn_ctx *ctx, const qnn_weight *ws, int n);
+int qnn_complete_weight_prefetch(qnn_ctx *ctx); /* CompleteWeightPrefetch: waits for compute, releases the active batch */
+/* ActivatePrefetchedWeights: *activated = 1 when the queued batch holds
+ * exactly these weights; it becomes the active batch and compute waits for it. */
+int qnn_activate_prefetched_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, int *activated);
+int qnn_seal_weight_prefetch(qnn_ctx *ctx);    /* SealWeightPrefetch: active pins move to the next Flush */
+int qnn_end_weight_prefetch(qnn_ctx *ctx);     /* EndWeightPrefetch: waits and releases both slots */
 
 /* ---------------------------------------------------------------------------
  * Hot-path ops

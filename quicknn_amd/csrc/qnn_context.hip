@@ -122,6 +122,26 @@ struct qnn_ctx_s {
   // the cache evicts, before its memory is released (QuickNN.Vulkan.pas:568-569).
   qnn_weight_evicted_fn on_evicted = nullptr;
   void *on_evicted_user = nullptr;
+  // Asynchronous layer prefetch (Context.Prefetch.inc): two slots, each with a
+  // pinned host staging buffer, a raw device staging buffer and an event that
+  // the copy stream records after the slot's copies and repacks.
+  struct PrefetchSlot {
+    void *host = nullptr;
+    void *dev = nullptr;
+    hipEvent_t ready = nullptr;
+    bool submitted = false;
+    std::vector<std::string> keys;
+    std::vector<qnn::WeightEntry *> entries;  // one pin each while queued or active
+    std::vector<std::string> prepared_keys;   // host staging filled by StageWeightPrefetch
+    std::vector<uint64_t> prepared_offsets;
+  };
+  struct Prefetch {
+    bool enabled = false;
+    uint64_t bytes = 0;
+    hipStream_t copy = nullptr;
+    PrefetchSlot slot[2];
+    int active = -1, queued = -1, next = 0;
+  } pf;
 };
 
 namespace qnn {
@@ -322,6 +342,11 @@ WeightEntry *lookup(qnn_ctx_s *ctx, const std::string &key) {
   if (it == ctx->weights.end()) return nullptr;
   it->second->last_use = ++ctx->clock;
   ctx->st.weight_cache_hits++;
+  if (it->second->ready) {  // written by a prefetch: compute waits for its copy stream first
+    if (ctx->capturing) hip_check(hipEventSynchronize(it->second->ready), "prefetch join");
+    else hip_check(hipStreamWaitEvent(ctx->stream, it->second->ready, 0), "prefetch join");
+    it->second->ready = nullptr;
+  }
   if (ctx->capturing) {
     it->second->pins++;
     ctx->capture_pins.push_back(it->second);
@@ -451,6 +476,116 @@ WeightEntry *acquire_raw(qnn_ctx_s *ctx, const qnn_weight *w, int64_t count) {
     throw;
   }
   return insert(ctx, e);
+}
+
+// ---------------------------------------------------------------- asynchronous prefetch
+// PrefetchWeights / StageWeightPrefetch accept complete 2-D matrices only
+// (Context.Prefetch.inc:186-191, :328-333).
+void check_prefetch_matrix(const qnn_weight *w) {
+  check_weight_desc(w);
+  if (w->offset != 0 || w->shape0 < 1 || w->shape0 > 0x7fffffff || w->shape1 < 1 || w->shape1 > 0x7fffffff ||
+      w->size != w->shape0 * w->shape1)
+    fail(QNN_E_ARGUMENT, "Layer prefetch requires complete immutable matrices");
+}
+// Source bytes of a matrix and the cache key its acquisition uses.
+uint64_t matrix_source_bytes(const qnn_weight *w) {
+  const int rows = int(w->shape0), cols = int(w->shape1);
+  if (is_gguf(w->encoding)) return gguf_weight_bytes(w, rows, cols);
+  if (w->dtype == QNN_DT_U8) return uint64_t(rows) * cols;
+  if (w->dtype == QNN_DT_F32 || w->dtype == QNN_DT_BF16) return uint64_t(rows) * cols * (w->dtype == QNN_DT_F32 ? 4 : 2);
+  fail(QNN_E_NOT_SUPPORTED, "only packed INT4, GGUF, F32 and BF16 matrices are resident in the HIP backend");
+}
+std::string matrix_key(const qnn_weight *w) {
+  const uint64_t bytes = matrix_source_bytes(w);
+  if (is_gguf(w->encoding)) return weight_key("gg", w, bytes);
+  if (w->dtype == QNN_DT_U8) return weight_key("i4", w, bytes);
+  return weight_key("raw", w, bytes);
+}
+
+// Waits for the slot's copies, unpins its entries and forgets its batch.
+void release_slot(qnn_ctx_s *ctx, int i) {
+  if (i < 0) return;
+  qnn_ctx_s::PrefetchSlot &s = ctx->pf.slot[i];
+  if (s.submitted) {
+    hip_check(hipEventSynchronize(s.ready), "prefetch slot");
+    s.submitted = false;
+  }
+  for (auto *e : s.entries) {
+    if (e->ready == s.ready) e->ready = nullptr;  // complete; the event will be recorded again
+    e->pins--;
+  }
+  s.entries.clear();
+  s.keys.clear();
+}
+
+// A cache entry for matrix w, uploaded on the copy stream from the slot's
+// staging at byte `off` (the host bytes are copied there first unless
+// StageWeightPrefetch already did).
+WeightEntry *prefetch_entry(qnn_ctx_s *ctx, qnn_ctx_s::PrefetchSlot &s, const qnn_weight *w, const std::string &key,
+                            uint64_t bytes, uint64_t off, bool staged) {
+  auto *e = new WeightEntry();
+  e->key = key;
+  e->identity = w->identity;
+  e->source_bytes = bytes;
+  const int rows = int(w->shape0), cols = int(w->shape1);
+  if (is_gguf(w->encoding)) {
+    e->kind = WKind::Gguf;
+    e->gg = gguf_layout(w->encoding, rows, cols);
+    e->bytes = e->gg.bytes();
+  } else if (w->dtype == QNN_DT_U8) {
+    const int k = (cols / 20) * 32;
+    if (w->encoding != QNN_WE_NATIVE || qnn_int4_row_bytes(k) != cols) fail(QNN_E_ARGUMENT, "Invalid packed INT4 projection");
+    e->kind = WKind::Int4;
+    e->i4 = int4_layout(rows, k);
+    e->bytes = e->i4.bytes();
+  } else {
+    e->kind = WKind::Raw;
+    e->raw_dtype = w->dtype;
+    e->bytes = (bytes + 255) & ~uint64_t(255);
+  }
+  try {
+    e->dptr = alloc_weight(ctx, e->bytes);
+    uint8_t *host = static_cast<uint8_t *>(s.host) + off;
+    uint8_t *dev = static_cast<uint8_t *>(s.dev) + off;
+    if (!staged) std::memcpy(host, w->data, bytes);
+    hipStream_t cs = ctx->pf.copy;
+    if (e->kind == WKind::Raw) {
+      hip_check(hipMemcpyAsync(e->dptr, host, bytes, hipMemcpyHostToDevice, cs), "prefetch copy");
+    } else {
+      hip_check(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, cs), "prefetch copy");
+      if (e->kind == WKind::Int4) {
+        int4_repack_launch(dev, e->i4, e->dptr, cs);
+      } else {
+        gguf_repack_launch(dev, e->gg, e->dptr, cs);
+        if (e->gg.rowexp_off) q8_rowexp_launch(e->gg, e->dptr, cs);
+      }
+    }
+  } catch (...) {
+    if (e->dptr) (void)hipFree(e->dptr);
+    delete e;
+    throw;
+  }
+  e->ready = s.ready;
+  e->pins++;  // the slot's
+  ctx->st.weight_cache_misses++;
+  return insert(ctx, e);
+}
+
+void destroy_prefetch(qnn_ctx_s *ctx) {
+  qnn_ctx_s::Prefetch &pf = ctx->pf;
+  if (pf.copy) (void)hipStreamSynchronize(pf.copy);
+  for (auto &s : pf.slot) {
+    for (auto *e : s.entries) {
+      if (e->ready == s.ready) e->ready = nullptr;
+      e->pins--;
+    }
+    if (s.host) (void)hipHostFree(s.host);
+    if (s.dev) (void)hipFree(s.dev);
+    if (s.ready) (void)hipEventDestroy(s.ready);
+    s = qnn_ctx_s::PrefetchSlot();
+  }
+  if (pf.copy) (void)hipStreamDestroy(pf.copy);
+  pf = qnn_ctx_s::Prefetch();
 }
 
 // Holds entries against eviction for the duration of one call.
@@ -842,6 +977,7 @@ int qnn_ctx_destroy(qnn_ctx *ctx) {
   return guarded([&] {
     check_ctx(ctx);
     (void)hipStreamSynchronize(ctx->stream);
+    destroy_prefetch(ctx);
     for (auto &g : ctx->graphs) {
       if (g.exec) (void)hipGraphExecDestroy(g.exec);
       if (g.graph) (void)hipGraphDestroy(g.graph);
@@ -1387,6 +1523,241 @@ int qnn_q8_gemm_int8(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_w
     q8_gemm_i8_launch(src->ptr, rows, in_dim, out_dim, e->gg, e->dptr, ws, dst->ptr, ctx->stream);
     ctx->st.gemm_calls++;
     ctx->st.gguf_calls++;
+    return QNN_OK;
+  });
+}
+
+// ---------------------------------------------------------------- asynchronous prefetch
+int qnn_enable_weight_prefetch(qnn_ctx *ctx, uint64_t max_layer_bytes, int *enabled) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!enabled) fail(QNN_E_ARGUMENT, "out");
+    *enabled = 0;
+    qnn_ctx_s::Prefetch &pf = ctx->pf;
+    if (pf.enabled) {
+      *enabled = max_layer_bytes <= pf.bytes;
+      return QNN_OK;
+    }
+    // EnableWeightPrefetch (Context.Prefetch.inc:106-110).
+    uint64_t capacity = 0;
+    qnn_weight_batch_capacity(ctx, &capacity);
+    const uint64_t padded = (max_layer_bytes + 255) & ~uint64_t(255);
+    if (max_layer_bytes == 0 || max_layer_bytes > (uint64_t(512) << 20) || padded > capacity / 2) return QNN_OK;
+    if (ctx->capturing) fail(QNN_E_INVALID_OP, "prefetch set-up during graph capture");
+    sync(ctx);
+    try {
+      hip_check(hipStreamCreateWithFlags(&pf.copy, hipStreamNonBlocking), "copy stream");
+      for (auto &s : pf.slot) {
+        hip_check(hipHostMalloc(&s.host, padded, hipHostMallocDefault), "prefetch host staging");
+        hip_check(hipMalloc(&s.dev, padded), "prefetch device staging");
+        hip_check(hipEventCreateWithFlags(&s.ready, hipEventDisableTiming), "prefetch event");
+      }
+    } catch (const Error &) {
+      (void)hipGetLastError();
+      destroy_prefetch(ctx);  // resource pressure changes scheduling, never results
+      return QNN_OK;
+    }
+    pf.bytes = padded;
+    pf.enabled = true;
+    *enabled = 1;
+    return QNN_OK;
+  });
+}
+
+int qnn_begin_weight_prefetch(qnn_ctx *ctx) {
+  return guarded([&] {
+    check_ctx(ctx);  // launches what was recorded (Context.Prefetch.inc:153-161)
+    if (!ctx->pf.enabled) fail(QNN_E_INVALID_OP, "Layer prefetch is disabled");
+    return QNN_OK;
+  });
+}
+
+int qnn_complete_weight_prefetch(qnn_ctx *ctx) {
+  return guarded([&] {
+    check_ctx(ctx);
+    qnn_ctx_s::Prefetch &pf = ctx->pf;
+    // CompleteWeightPrefetch (Context.Prefetch.inc:388-405): wait for compute,
+    // then release the batch it was using.
+    sync(ctx);
+    release_flush_pins(ctx);
+    release_slot(ctx, pf.active);
+    pf.active = -1;
+    return QNN_OK;
+  });
+}
+
+int qnn_prefetch_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, int defer_join) {
+  return guarded([&] {
+    check_ctx(ctx);
+    qnn_ctx_s::Prefetch &pf = ctx->pf;
+    if (!pf.enabled || pf.queued >= 0 || n < 1 || !ws) fail(QNN_E_INVALID_OP, "Invalid layer prefetch state");
+    if (ctx->capturing) fail(QNN_E_INVALID_OP, "prefetch during graph capture");
+    std::vector<std::string> keys(n);
+    std::vector<uint64_t> sizes(n);
+    std::unordered_map<std::string, int> unique;
+    uint64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+      check_prefetch_matrix(&ws[i]);
+      keys[i] = matrix_key(&ws[i]);
+      sizes[i] = matrix_source_bytes(&ws[i]);
+      if (unique.emplace(keys[i], i).second) total += (sizes[i] + 255) & ~uint64_t(255);
+    }
+    uint64_t capacity = 0;
+    qnn_weight_batch_capacity(ctx, &capacity);
+    if (total > pf.bytes || total > capacity / 2) fail(QNN_E_RANGE, "Layer prefetch exceeds the double-buffer budget");
+    const int si = pf.next;
+    qnn_ctx_s::PrefetchSlot &s = pf.slot[si];
+    release_slot(ctx, si);
+    const bool prepared = s.prepared_keys == keys;
+    s.keys = keys;
+    std::vector<bool> created(n, false);
+    try {
+      // Cache hits are pinned before any eviction (duplicates included).
+      for (int i = 0; i < n; ++i) {
+        auto it = ctx->weights.find(keys[i]);
+        if (it == ctx->weights.end()) continue;
+        WeightEntry *e = lookup(ctx, keys[i]);
+        e->pins++;
+        s.entries.push_back(e);
+        created[i] = true;  // handled
+      }
+      uint64_t used = 0;
+      std::unordered_map<std::string, bool> made;
+      for (int i = 0; i < n; ++i) {
+        if (created[i] || made.count(keys[i])) continue;
+        const uint64_t off = prepared ? s.prepared_offsets[i] : used;
+        WeightEntry *e = prefetch_entry(ctx, s, &ws[i], keys[i], sizes[i], off, prepared);
+        s.entries.push_back(e);
+        made[keys[i]] = true;
+        used += (sizes[i] + 255) & ~uint64_t(255);
+        ctx->st.weight_uploads++;
+        ctx->st.weight_upload_bytes += sizes[i];
+        ctx->st.async_weight_bytes += sizes[i];
+      }
+      hip_check(hipEventRecord(s.ready, pf.copy), "prefetch event");
+      s.submitted = true;
+    } catch (...) {
+      (void)hipStreamSynchronize(pf.copy);
+      s.submitted = false;
+      // entries made here hold no valid data until the copies finish: drop them
+      for (auto *e : s.entries) {
+        e->pins--;
+        if (e->ready == s.ready) {
+          ctx->weights.erase(e->key);
+          ctx->weight_bytes -= e->bytes;
+          (void)hipFree(e->dptr);
+          delete e;
+        }
+      }
+      s.entries.clear();
+      s.keys.clear();
+      throw;
+    }
+    ctx->st.async_weight_batches++;
+    s.prepared_keys.clear();
+    s.prepared_offsets.clear();
+    pf.queued = si;
+    pf.next = 1 - si;
+    if (!defer_join) return qnn_complete_weight_prefetch(ctx);
+    return QNN_OK;
+  });
+}
+
+int qnn_stage_weight_prefetch(qnn_ctx *ctx, const qnn_weight *ws, int n) {
+  return guarded([&] {
+    check_ctx(ctx, true);
+    qnn_ctx_s::Prefetch &pf = ctx->pf;
+    if (!pf.enabled || pf.queued < 0) fail(QNN_E_INVALID_OP, "Host staging requires an uploaded next layer");
+    if (n < 1 || !ws) fail(QNN_E_ARGUMENT, "StageWeightPrefetch");
+    qnn_ctx_s::PrefetchSlot &s = pf.slot[pf.next];
+    // Only the host buffer is reused here; its previous device weights stay
+    // pinned until CompleteWeightPrefetch (Context.Prefetch.inc:322-327).
+    if (s.submitted) {
+      hip_check(hipEventSynchronize(s.ready), "prefetch slot");
+      s.submitted = false;
+    }
+    s.prepared_keys.clear();
+    s.prepared_offsets.clear();
+    std::vector<std::string> keys(n);
+    std::vector<uint64_t> offsets(n), sizes(n);
+    std::unordered_map<std::string, int> unique;
+    uint64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+      check_prefetch_matrix(&ws[i]);
+      keys[i] = matrix_key(&ws[i]);
+      sizes[i] = matrix_source_bytes(&ws[i]);
+      auto it = unique.find(keys[i]);
+      if (it != unique.end()) {
+        offsets[i] = offsets[it->second];
+      } else {
+        unique.emplace(keys[i], i);
+        offsets[i] = total;
+        total += (sizes[i] + 255) & ~uint64_t(255);
+      }
+    }
+    if (total > pf.bytes) fail(QNN_E_RANGE, "Host-staged layer exceeds its buffer");
+    for (auto &kv : unique)
+      std::memcpy(static_cast<uint8_t *>(s.host) + offsets[kv.second], ws[kv.second].data, sizes[kv.second]);
+    s.prepared_keys = keys;
+    s.prepared_offsets = offsets;
+    return QNN_OK;
+  });
+}
+
+int qnn_activate_prefetched_weights(qnn_ctx *ctx, const qnn_weight *ws, int n, int *activated) {
+  return guarded([&] {
+    check_ctx(ctx, true);
+    qnn_ctx_s::Prefetch &pf = ctx->pf;
+    if (!activated) fail(QNN_E_ARGUMENT, "out");
+    *activated = 0;
+    if (pf.queued < 0 || !ws) return QNN_OK;
+    qnn_ctx_s::PrefetchSlot &s = pf.slot[pf.queued];
+    if (n != int(s.keys.size())) return QNN_OK;
+    for (int i = 0; i < n; ++i) {
+      check_weight_desc(&ws[i]);
+      if (matrix_key(&ws[i]) != s.keys[i]) return QNN_OK;
+    }
+    if (pf.active >= 0) fail(QNN_E_INVALID_OP, "Previous prefetched layer is still active");
+    // Compute waits for the batch's copies (the reference's semaphore wait).
+    hip_check(hipStreamWaitEvent(ctx->stream, s.ready, 0), "prefetch join");
+    for (auto *e : s.entries)
+      if (e->ready == s.ready) e->ready = nullptr;
+    pf.active = pf.queued;
+    pf.queued = -1;
+    *activated = 1;
+    return QNN_OK;
+  });
+}
+
+int qnn_seal_weight_prefetch(qnn_ctx *ctx) {
+  return guarded([&] {
+    check_ctx(ctx, true);
+    qnn_ctx_s::Prefetch &pf = ctx->pf;
+    if (pf.queued >= 0) fail(QNN_E_INVALID_OP, "Unused prefetched layer at forward completion");
+    if (pf.active < 0) return QNN_OK;
+    // The last layer's pins move to the next Flush/Download, as PreloadWeights'
+    // do (Context.Prefetch.inc:421-438).
+    qnn_ctx_s::PrefetchSlot &s = pf.slot[pf.active];
+    for (auto *e : s.entries) ctx->flush_pins.push_back(e);
+    s.entries.clear();
+    s.keys.clear();
+    pf.active = -1;
+    return QNN_OK;
+  });
+}
+
+int qnn_end_weight_prefetch(qnn_ctx *ctx) {
+  return guarded([&] {
+    check_ctx(ctx);
+    qnn_ctx_s::Prefetch &pf = ctx->pf;
+    sync(ctx);
+    release_flush_pins(ctx);
+    for (int i = 0; i < 2; ++i) {
+      release_slot(ctx, i);
+      pf.slot[i].prepared_keys.clear();
+      pf.slot[i].prepared_offsets.clear();
+    }
+    pf.active = pf.queued = -1;
     return QNN_OK;
   });
 }

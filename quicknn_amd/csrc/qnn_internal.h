@@ -86,6 +86,7 @@ struct WeightEntry {
   int op_pins = 0;         // held during one call's acquisitions
   uint64_t last_use = 0;
   int raw_dtype = 0;       // Raw: dtype of the copied vector
+  hipEvent_t ready = nullptr;  // written by an asynchronous prefetch: the compute stream waits for it first
   I4Layout i4;
   GGLayout gg;
 };

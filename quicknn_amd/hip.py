@@ -75,7 +75,7 @@ class Status(ctypes.Structure):
         "gemm_calls", "gguf_calls", "int4_calls", "moe_calls", "weight_uploads", "weight_upload_bytes",
         "weight_cache_hits", "weight_cache_misses", "weight_evictions", "readbacks", "submissions",
         "weight_bytes", "weight_limit", "activation_bytes", "activation_peak_bytes", "mlp_fused", "linear_grouped", "moe_fused", "moe_route_fused",
-        "glu_fused")]
+        "glu_fused", "async_weight_batches", "async_weight_bytes")]
 
 
 _lib = None
@@ -111,6 +111,14 @@ def lib():
             "qnn_is_weight_resident": (ctypes.c_int, [_vp, W, ctypes.c_int, ctypes.c_int, _ip]),
             "qnn_weight_batch_capacity": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
             "qnn_set_weight_evicted": (ctypes.c_int, [_vp, _EVICTED, _vp]),
+            "qnn_enable_weight_prefetch": (ctypes.c_int, [_vp, ctypes.c_uint64, _ip]),
+            "qnn_begin_weight_prefetch": (ctypes.c_int, [_vp]),
+            "qnn_prefetch_weights": (ctypes.c_int, [_vp, W, ctypes.c_int, ctypes.c_int]),
+            "qnn_stage_weight_prefetch": (ctypes.c_int, [_vp, W, ctypes.c_int]),
+            "qnn_complete_weight_prefetch": (ctypes.c_int, [_vp]),
+            "qnn_activate_prefetched_weights": (ctypes.c_int, [_vp, W, ctypes.c_int, _ip]),
+            "qnn_seal_weight_prefetch": (ctypes.c_int, [_vp]),
+            "qnn_end_weight_prefetch": (ctypes.c_int, [_vp]),
             "qnn_upload": (ctypes.c_int, [_vp, W, ctypes.POINTER(_vp)]),
             "qnn_vector_linear": (ctypes.c_int, [_vp, _vp, _vp, W, ctypes.c_int, ctypes.c_int]),
             "qnn_linear": (ctypes.c_int, [_vp, _vp, _vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
@@ -152,7 +160,9 @@ EXPORTED = (
     "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_tensor_new", "qnn_recycle",
     "qnn_scratch", "qnn_upload_raw", "qnn_download", "qnn_copy", "qnn_flush", "qnn_tensor_count",
     "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
-    "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_q8_gemm_int8", "qnn_int4_linear", "qnn_int4_linear_noalloc", "qnn_swiglu_vector",
+    "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_enable_weight_prefetch", "qnn_begin_weight_prefetch",
+    "qnn_prefetch_weights", "qnn_stage_weight_prefetch", "qnn_complete_weight_prefetch",
+    "qnn_activate_prefetched_weights", "qnn_seal_weight_prefetch", "qnn_end_weight_prefetch", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_q8_gemm_int8", "qnn_int4_linear", "qnn_int4_linear_noalloc", "qnn_swiglu_vector",
     "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
     "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
@@ -397,6 +407,42 @@ class GPUContext:
         cb = None if fn is None else _EVICTED(lambda ident, _user: fn(int(ident)))
         _raise(lib().qnn_set_weight_evicted(self.h, cb if cb is not None else _EVICTED(), None))
         self._evicted_cb, self._evicted_fn = cb, fn  # the C side keeps the pointer: hold the thunk
+
+    # -- asynchronous layer prefetch (Context.API.inc:88-95)
+    @staticmethod
+    def _wlist(ws):
+        return (_Weight * len(ws))(*[w.desc() for w in ws]), len(ws)
+
+    def EnableWeightPrefetch(self, max_layer_bytes: int) -> bool:
+        r = ctypes.c_int()
+        _raise(lib().qnn_enable_weight_prefetch(self.h, max_layer_bytes, ctypes.byref(r)))
+        return bool(r.value)
+
+    def BeginWeightPrefetch(self) -> None:
+        _raise(lib().qnn_begin_weight_prefetch(self.h))
+
+    def PrefetchWeights(self, ws, defer_join: bool = False) -> None:
+        arr, n = self._wlist(ws)
+        _raise(lib().qnn_prefetch_weights(self.h, arr, n, int(defer_join)))
+
+    def StageWeightPrefetch(self, ws) -> None:
+        arr, n = self._wlist(ws)
+        _raise(lib().qnn_stage_weight_prefetch(self.h, arr, n))
+
+    def CompleteWeightPrefetch(self) -> None:
+        _raise(lib().qnn_complete_weight_prefetch(self.h))
+
+    def ActivatePrefetchedWeights(self, ws) -> bool:
+        arr, n = self._wlist(ws)
+        r = ctypes.c_int()
+        _raise(lib().qnn_activate_prefetched_weights(self.h, arr, n, ctypes.byref(r)))
+        return bool(r.value)
+
+    def SealWeightPrefetch(self) -> None:
+        _raise(lib().qnn_seal_weight_prefetch(self.h))
+
+    def EndWeightPrefetch(self) -> None:
+        _raise(lib().qnn_end_weight_prefetch(self.h))
 
     def WeightBatchCapacity(self) -> int:
         v = ctypes.c_uint64()
