@@ -36,17 +36,30 @@ extern "C" {
 /* ---- status codes: exception classes of the reference ---- */
 #define QNN_OK 0
 #define QNN_NOT_HANDLED 1        /* TrySwiGLUVector returned False (caller falls back) */
+#define QNN_NOT_FOUND 2          /* GetTensor returned nil (no tensor of that name) */
 #define QNN_E_ARGUMENT (-1)      /* EArgumentException */
 #define QNN_E_RANGE (-2)         /* ERangeError (budgets, device limits) */
 #define QNN_E_NOT_SUPPORTED (-3) /* ENotSupportedException */
 #define QNN_E_INVALID_OP (-4)    /* EInvalidOp (wrong thread, non-finite results, device failure) */
+#define QNN_E_FORMAT (-5)        /* ESafeTensorError, EGGUFError (malformed or stale files) */
+#define QNN_E_IO (-6)            /* EFOpenError / EFCreateError / EInOutError */
 
 /* ---- TQNNDataType ordinals (src/core/QuickNN.Common.pas:71-90) ---- */
+#define QNN_DT_UNDEF 0
 #define QNN_DT_F16 1
 #define QNN_DT_BF16 2
 #define QNN_DT_F32 3
+#define QNN_DT_S32 4
 #define QNN_DT_S8 5
 #define QNN_DT_U8 6
+#define QNN_DT_F64 7
+#define QNN_DT_BOOLEAN 8
+#define QNN_DT_F8E5M2 9
+#define QNN_DT_F8E4M3 10
+#define QNN_DT_S4 11
+#define QNN_DT_F4E2M1 14
+#define QNN_DT_S16 16
+#define QNN_DT_U16 17
 
 /* ---- TQNNWeightEncoding ordinals (src/core/QuickNN.Common.pas:130-131) ---- */
 #define QNN_WE_NATIVE 0
@@ -54,7 +67,39 @@ extern "C" {
 #define QNN_WE_Q4_K 2
 #define QNN_WE_Q6_K 3
 #define QNN_WE_Q3_K 4
+#define QNN_WE_Q5_K 5      /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ4_NL 6    /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ3_S 7     /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ4_XS 8    /* read from GGUF tables; no kernel here */
 #define QNN_WE_Q2_K 9
+#define QNN_WE_IQ2_XXS 10  /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ2_S 11    /* read from GGUF tables; no kernel here */
+#define QNN_WE_Q2_0 12     /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ3_XXS 13  /* read from GGUF tables; no kernel here */
+
+/* ---- TSafeTensorType ordinals (src/io/QuickNN.SafeTensors.pas:34-77) ---- */
+#define QNN_ST_UNKNOWN (-1)
+#define QNN_ST_BOOL 0
+#define QNN_ST_F4 1
+#define QNN_ST_F6_E2M3 2
+#define QNN_ST_F6_E3M2 3
+#define QNN_ST_U8 4
+#define QNN_ST_I8 5
+#define QNN_ST_F8_E5M2 6
+#define QNN_ST_F8_E4M3 7
+#define QNN_ST_F8_E8M0 8
+#define QNN_ST_I16 9
+#define QNN_ST_U16 10
+#define QNN_ST_F16 11
+#define QNN_ST_BF16 12
+#define QNN_ST_I32 13
+#define QNN_ST_U32 14
+#define QNN_ST_F32 15
+#define QNN_ST_C64 16
+#define QNN_ST_F64 17
+#define QNN_ST_I64 18
+#define QNN_ST_U64 19
+#define QNN_ST_I4 20
 
 /* ---- op codes accepted by qnn_kernel / qnn_kernel_weights
         (Context.API.inc:167-258) ---- */
@@ -309,6 +354,117 @@ int qnn_graph_begin(qnn_ctx *ctx);
 int qnn_graph_end(qnn_ctx *ctx, int *graph_id);
 int qnn_graph_launch(qnn_ctx *ctx, int graph_id);
 void *qnn_stream(qnn_ctx *ctx);
+
+/* ---------------------------------------------------------------------------
+ * Checkpoint files (host side; no context needed).  They turn safetensors and
+ * GGUF checkpoints, and the INT4 cache built from them, into qnn_weight views
+ * of the mapped bytes that the context's entry points take.
+ * ------------------------------------------------------------------------- */
+typedef struct qnn_tensor_files_s qnn_tensor_files; /* TSafeTensorFiles (SafeTensors.pas:207-222) */
+typedef struct qnn_gguf_header_s qnn_gguf_header;   /* TGGUFHeader (GGUF.pas:26-34) */
+typedef struct qnn_int4_cache_s qnn_int4_cache;     /* TLLMInt4Cache (LLM.Quantization.pas:13-28) */
+
+/* TSafeTensor (SafeTensors.pas:149-180).  Pointers stay valid while the files are open. */
+typedef struct {
+  const char *name;       /* UTF-8, NUL-terminated */
+  const void *data;       /* the mapped bytes */
+  const int64_t *shape;   /* ndim dimensions, row-major (GGUF: reversed from ne[]) */
+  uint64_t identity;      /* WeightIdentity: fresh per tensor per open, top bit set */
+  int64_t data_offset;    /* DataOffset: absolute file offset */
+  int64_t data_size;      /* DataSize: bytes */
+  int32_t ndim;           /* Ndim */
+  int32_t st_dtype;       /* DType: QNN_ST_* */
+  int32_t dtype;          /* DType.ToDataType: QNN_DT_* (QNN_DT_UNDEF if none) */
+  int32_t encoding;       /* Encoding: QNN_WE_* (packed GGUF blocks: not NATIVE) */
+  int32_t file;           /* index of the file within the set */
+  uint32_t storage_type;  /* GGML type of a GGUF tensor; 0xFFFFFFFF for safetensors */
+} qnn_tensor_info;
+
+/* TSafeTensorFile fields (SafeTensors.pas:184-197). */
+typedef struct {
+  const char *path;
+  const char *architecture; /* GGUF general.architecture, else "" */
+  const char *header_json;  /* HeaderJson: the raw safetensors header, "" for GGUF */
+  const void *data;         /* Data: the mapping of the whole file */
+  int64_t file_size, header_size, data_size, offset;
+  int32_t is_gguf, tensor_count;
+} qnn_tensor_file_info;
+
+/* TSafeTensorFile.Open (SafeTensors.pas:522-690): a safetensors file, or a
+ * GGUF file when its first four bytes are the GGUF magic (:480-520).  The
+ * header is validated as the reference does (UTF-8, dtype sizes, contiguous
+ * buffer with no gaps, overlaps or trailing bytes, unique names) and the file
+ * is mapped read-only.  QNN_E_FORMAT on malformed files, QNN_E_IO if unreadable. */
+int qnn_tensor_files_open(const char *path, qnn_tensor_files **out);
+/* LoadSafeTensorShards (SafeTensors.pas:777-837): the shards named by
+ * dir/index_file's weight_map, in order of first appearance, or dir/single_file
+ * when there is no index. */
+int qnn_tensor_files_open_shards(const char *dir, const char *index_file, const char *single_file,
+                                 qnn_tensor_files **out);
+int qnn_tensor_files_close(qnn_tensor_files *files);
+int qnn_tensor_files_count(const qnn_tensor_files *files, int *count);
+int qnn_tensor_files_file(const qnn_tensor_files *files, int file, qnn_tensor_file_info *out);
+/* Tensors[index] of one file, in descriptor order. */
+int qnn_tensor_files_tensor(const qnn_tensor_files *files, int file, int index, qnn_tensor_info *out);
+/* GetTensor (SafeTensors.pas:900-912): the first file holding `name`; QNN_NOT_FOUND if none. */
+int qnn_tensor_files_find(const qnn_tensor_files *files, const char *name, qnn_tensor_info *out);
+/* GetLinearWeight(Name, UseMMAP = True) (SafeTensors.pas:874-898): packed GGUF
+ * -> U8 view with its encoding and logical [N, K] shape; BF16 and F32 -> views
+ * of the mapped data; F16 -> an F32 copy held until the files close.  A 1-D
+ * tensor has shape1 = 1.  Missing tensor or other dtypes -> QNN_E_FORMAT. */
+int qnn_tensor_files_linear_weight(qnn_tensor_files *files, const char *name, qnn_weight *out);
+
+/* TGGUFHeader fields (GGUF.pas:26-34). */
+typedef struct {
+  uint32_t version, alignment;
+  int64_t data_offset;
+  int32_t vocabulary_size, tensor_count;
+  const char *architecture;
+  const char *metadata_json; /* the metadata object when requested, else "" */
+} qnn_gguf_header_info;
+/* TGGUFTensor (GGUF.pas:18-23). */
+typedef struct {
+  const char *name;
+  const int64_t *shape; /* row-major, reversed from GGML ne[] */
+  int64_t offset;       /* from the start of the data section */
+  int64_t byte_size;
+  int32_t ndim;
+  uint32_t storage_type;
+  int32_t encoding; /* GGUFEncoding(storage_type) */
+} qnn_gguf_tensor;
+/* TGGUFHeader.ReadFile (GGUF.pas:206-337): GGUF v2/v3 header and tensor table.
+ * with_metadata != 0 collects the metadata as a JSON object (Metadata <> nil);
+ * include_vocabulary = 0 skips the tokenizer vocabulary, merges, token types
+ * and scores.  QNN_E_FORMAT on malformed headers, QNN_E_IO if unreadable. */
+int qnn_gguf_read_file(const char *path, int with_metadata, int include_vocabulary, qnn_gguf_header **out);
+int qnn_gguf_header_free(qnn_gguf_header *header);
+int qnn_gguf_header_get(const qnn_gguf_header *header, qnn_gguf_header_info *out);
+int qnn_gguf_header_tensor(const qnn_gguf_header *header, int index, qnn_gguf_tensor *out);
+
+/* TLLMInt4Scope (LLM.Quantization.pas:11). */
+#define QNN_IQ_EXPERTS 0
+#define QNN_IQ_DENSE 1
+/* TProc<Integer, Integer>: shards written so far and the shard count. */
+typedef void (*qnn_progress_fn)(int done, int total, void *user);
+/* TLLMInt4Cache.Create (LLM.Quantization.pas:79-125): opens the cache for
+ * `sources` under directory/<format>-<fingerprint>, building it first when its
+ * index is absent (:164-297: weight selection, QuantizeInt4 per matrix, shards
+ * of 384 expert or 32 dense matrices, written as *.part and renamed, the index
+ * last), then validates the index and every shard's metadata (:137-162).
+ * A second builder of the same cache fails with QNN_E_IO while the first holds
+ * its build.lock.  `sources` must stay open while the cache is built. */
+int qnn_int4_cache_create(const qnn_tensor_files *sources, const char *directory, qnn_progress_fn progress,
+                          void *user, int scope, qnn_int4_cache **out);
+int qnn_int4_cache_destroy(qnn_int4_cache *cache);
+/* Weight (LLM.Quantization.pas:299-317): U8 [rows, Int4RowBytes(columns)] of
+ * the mapped shard; QNN_E_FORMAT if missing or of another shape. */
+int qnn_int4_cache_weight(const qnn_int4_cache *cache, const char *name, int rows, int columns, qnn_weight *out);
+/* MappedBytes (:319-325). */
+int qnn_int4_cache_mapped_bytes(const qnn_int4_cache *cache, uint64_t *bytes);
+/* Directory: NUL-terminated, valid while the cache is open. */
+const char *qnn_int4_cache_directory(const qnn_int4_cache *cache);
+/* SourceFingerprint (:70-73): 64 lowercase hex digits of SHA-256 plus NUL into out[65]. */
+int qnn_int4_source_fingerprint(const qnn_tensor_files *sources, char *out);
 
 /* ---------------------------------------------------------------------------
  * Host utilities

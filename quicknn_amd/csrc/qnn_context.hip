@@ -16,6 +16,7 @@
 namespace qnn {
 
 thread_local std::string t_last_error;
+void set_last_error(const std::string &msg) { t_last_error = msg; }
 
 struct GraphRec {
   hipGraph_t graph = nullptr;

@@ -25,10 +25,13 @@ LIB_PATH = os.path.join(_HERE, "libqnn_hip.so")
 # ---- status codes -> the reference's exception classes ----
 QNN_OK = 0
 QNN_NOT_HANDLED = 1
+QNN_NOT_FOUND = 2
 QNN_E_ARGUMENT = -1
 QNN_E_RANGE = -2
 QNN_E_NOT_SUPPORTED = -3
 QNN_E_INVALID_OP = -4
+QNN_E_FORMAT = -5
+QNN_E_IO = -6
 
 
 class QNNError(RuntimeError):
@@ -51,7 +54,18 @@ class EInvalidOp(QNNError):
     code = QNN_E_INVALID_OP
 
 
-_ERRORS = {c.code: c for c in (EArgumentException, ERangeError, ENotSupportedException, EInvalidOp)}
+class ESafeTensorError(QNNError):
+    """ESafeTensorError / EGGUFError: a malformed, stale or missing checkpoint entry."""
+    code = QNN_E_FORMAT
+
+
+class EInOutError(QNNError, OSError):
+    """EFOpenError / EFCreateError / EInOutError: a file that cannot be opened or written."""
+    code = QNN_E_IO
+
+
+_ERRORS = {c.code: c for c in (EArgumentException, ERangeError, ENotSupportedException, EInvalidOp,
+                               ESafeTensorError, EInOutError)}
 
 # ---- TQNNDataType / TQNNWeightEncoding ordinals ----
 DT_F16, DT_BF16, DT_F32, DT_S8, DT_U8 = 1, 2, 3, 5, 6
@@ -82,6 +96,7 @@ _lib = None
 _vp = ctypes.c_void_p
 _ip = ctypes.POINTER(ctypes.c_int)
 _EVICTED = ctypes.CFUNCTYPE(None, ctypes.c_uint64, ctypes.c_void_p)  # qnn_weight_evicted_fn
+_PROGRESS = ctypes.CFUNCTYPE(None, ctypes.c_int, ctypes.c_int, ctypes.c_void_p)  # qnn_progress_fn
 
 
 def lib():
@@ -147,6 +162,26 @@ def lib():
             "qnn_int4_row_bytes": (ctypes.c_int, [ctypes.c_int]),
             "qnn_quantize_int4": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]),
             "qnn_gguf_quantize": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_int64, _vp]),
+            "qnn_tensor_files_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+            "qnn_tensor_files_open_shards": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                                            ctypes.POINTER(_vp)]),
+            "qnn_tensor_files_close": (ctypes.c_int, [_vp]),
+            "qnn_tensor_files_count": (ctypes.c_int, [_vp, _ip]),
+            "qnn_tensor_files_file": (ctypes.c_int, [_vp, ctypes.c_int, _vp]),
+            "qnn_tensor_files_tensor": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp]),
+            "qnn_tensor_files_find": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp]),
+            "qnn_tensor_files_linear_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, W]),
+            "qnn_gguf_read_file": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+            "qnn_gguf_header_free": (ctypes.c_int, [_vp]),
+            "qnn_gguf_header_get": (ctypes.c_int, [_vp, _vp]),
+            "qnn_gguf_header_tensor": (ctypes.c_int, [_vp, ctypes.c_int, _vp]),
+            "qnn_int4_cache_create": (ctypes.c_int, [_vp, ctypes.c_char_p, _PROGRESS, _vp, ctypes.c_int,
+                                                     ctypes.POINTER(_vp)]),
+            "qnn_int4_cache_destroy": (ctypes.c_int, [_vp]),
+            "qnn_int4_cache_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.c_int, W]),
+            "qnn_int4_cache_mapped_bytes": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
+            "qnn_int4_cache_directory": (ctypes.c_char_p, [_vp]),
+            "qnn_int4_source_fingerprint": (ctypes.c_int, [_vp, ctypes.c_char_p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -167,6 +202,11 @@ EXPORTED = (
     "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
     "qnn_stream", "qnn_int4_row_bytes", "qnn_quantize_int4", "qnn_gguf_quantize",
+    "qnn_tensor_files_open", "qnn_tensor_files_open_shards", "qnn_tensor_files_close", "qnn_tensor_files_count",
+    "qnn_tensor_files_file", "qnn_tensor_files_tensor", "qnn_tensor_files_find", "qnn_tensor_files_linear_weight",
+    "qnn_gguf_read_file", "qnn_gguf_header_free", "qnn_gguf_header_get", "qnn_gguf_header_tensor",
+    "qnn_int4_cache_create", "qnn_int4_cache_destroy", "qnn_int4_cache_weight", "qnn_int4_cache_mapped_bytes",
+    "qnn_int4_cache_directory", "qnn_int4_source_fingerprint",
 )
 
 
@@ -210,6 +250,16 @@ class MemoryBlock:
     def desc(self) -> _Weight:
         return _Weight(self.identity, self.data.ctypes.data, self.offset, self.size, self.shape[0],
                        self.shape[1] if len(self.shape) > 1 else 1, self.dtype, self.encoding)
+
+    @staticmethod
+    def mapped(ptr: int, nbytes: int, shape, dtype: int, encoding: int, size: int, identity: int,
+               owner) -> "MemoryBlock":
+        """A view of ``nbytes`` at ``ptr`` inside a mapping that ``owner`` keeps open (DataPtr of a
+        TMemoryBlock returned with UseMMAP = True)."""
+        view = np.ctypeslib.as_array((ctypes.c_uint8 * max(int(nbytes), 1)).from_address(ptr))
+        b = MemoryBlock(view, shape, dtype, encoding, 0, size, identity)
+        b.owner = owner
+        return b
 
     @staticmethod
     def int4(packed: np.ndarray, **kw) -> "MemoryBlock":
