@@ -108,10 +108,15 @@ extern "C" {
 #define QNN_GO_ADD 4
 #define QNN_GO_SWIGLU 9
 #define QNN_GO_FINITE 13
+#define QNN_GO_SCALE 43
+#define QNN_GO_LLM_CACHE_WRITE 44
+#define QNN_GO_LLM_ROPE 45
+#define QNN_GO_LLM_SEEN 48
 #define QNN_GO_MOE_ROUTE 52
 #define QNN_GO_MOE_GATHER 53
 #define QNN_GO_MOE_SCATTER 54
 #define QNN_GO_GEGLU 75
+#define QNN_GO_SOFTCAP 76
 
 /* OnWeightEvicted (Context.API.inc:164, TProc<IInterface>): called with the
  * evicted entry's WeightIdentity before its device memory is released
@@ -308,6 +313,15 @@ int qnn_int4_linear_accumulate(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, q
  *   QNN_GO_MOE_ROUTE   args [rows, experts, topk, normalize]   (moe.comp:25-50)
  *   QNN_GO_MOE_GATHER  args [hidden, topk, offset]             (moe.comp:124)
  *   QNN_GO_MOE_SCATTER args [hidden, topk, offset, route_index, single_row, prob_base] (moe.comp:125-126)
+ *   QNN_GO_SCALE       args [mul_bits, add_bits = 0]     dst = a * mul + add (tensor.comp:309)
+ *   QNN_GO_SOFTCAP     args [cap_bits]                   dst = cap * tanh(clamp(a / cap, -20, 20)) (tensor.comp:308)
+ *   QNN_GO_LLM_ROPE    args [heads, dim, position, theta_bits]; n = rows * heads * dim / 2;
+ *                      pairs (j, j + dim/2) of each head row rotated by
+ *                      (position + row) * theta^(-2j/dim) (tensor.comp:318-327)
+ *   QNN_GO_LLM_CACHE_WRITE args [rows, kv_heads, dim, capacity, position]; n = rows * kv_heads * dim;
+ *                      dst = cache, a = K, b = V: K transposed [kv_heads][dim][capacity],
+ *                      then V [kv_heads][capacity][dim] (tensor.comp:313-317)
+ *   QNN_GO_LLM_SEEN    args [vocab]: dst[a[i]] |= 1 (token ids as raw bits) (tensor.comp:328)
  * a, b, c may be NULL where the op does not read them. */
 int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_tensor *b, qnn_tensor *c,
                const int *args, int nargs);
@@ -316,6 +330,27 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
  *   args [rows, dim, flags, 0, 0, src_offset, unit_gamma, eps_bits]; b = gamma (F32/BF16 [dim]). */
 int qnn_kernel_weights(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, const qnn_weight *b,
                        const qnn_weight *c, const int *args, int nargs);
+
+/* CachedAttention (Context.API.inc:142-146, Implementation.inc:1189-1226;
+ * attention.comp): for query row r at absolute position position + r, softmax
+ * attention over cache keys [start, position + r], start = end - window when
+ * window > 0, of each head against its KV head (heads / kv_heads query heads
+ * per KV head).  Scores are scaled by `scale` (0: 1/sqrt(dim)) and, when
+ * softcap > 0, capped as softcap * tanh(score / softcap).  masked != 0 reads a
+ * [query_rows][capacity] word mask after the cache; keys with a zero word are
+ * skipped.  q, dst: [query_rows][heads][dim]; cache as GO_LLM_CACHE_WRITE. */
+int qnn_cached_attention(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *q, qnn_tensor *cache, int query_rows, int capacity,
+                         int heads, int kv_heads, int dim, int position, int window, float softcap, float scale,
+                         int masked);
+
+/* SampleToken (Context.API.inc:136-140, Implementation.inc:1137-1187;
+ * tensor.comp:123-199): exact top-k (k = min(vocab, top_k), 1 at temperature
+ * 0) of the logits after the repetition penalty (seen flag != 0: score * penalty
+ * below zero, score / penalty above; flag 0xffffffff: token excluded), ranked
+ * by score then lower id; then nucleus sampling with `uniform` in [0, 1).
+ * dst[0] receives the token id as raw bits.  One launch for any vocabulary. */
+int qnn_sample_token(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *logits, qnn_tensor *seen, int vocab, int top_k,
+                     float temperature, float top_p, float penalty, float uniform);
 
 /* CheckFinite (Context.API.inc:158): a later qnn_download fails with
  * QNN_E_INVALID_OP if any checked value was NaN or infinite. */

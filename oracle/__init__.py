@@ -79,6 +79,16 @@ def lib():
             "qo_q8_gemm_i8": (ctypes.c_int, [_u8p, _i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]),
             "qo_gguf_gemm_scalar": (ctypes.c_int, [_u8p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int,
                                                    ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int]),
+            "qo_rope": (ctypes.c_int, [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float]),
+            "qo_cache_write": (ctypes.c_int, [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_int]),
+            "qo_cached_attention": (ctypes.c_int, [_f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                   ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                   ctypes.c_float, ctypes.c_float, ctypes.c_int, _f32p]),
+            "qo_sample_topk": (ctypes.c_int, [_f32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f32p,
+                                              _u32p]),
+            "qo_sample_token": (ctypes.c_uint32, [_f32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                                  ctypes.c_float, ctypes.c_float, ctypes.c_float]),
             "qo_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
             "qo_float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
         }
@@ -307,3 +317,52 @@ def half_to_float(h: int) -> float:
 
 def float_to_half(f: float) -> int:
     return lib().qo_float_to_half(f)
+
+
+# ---------------------------------------------------------------------------
+# The rest of a decode layer
+# ---------------------------------------------------------------------------
+def rope(x: np.ndarray, rows: int, heads: int, dim: int, position: int, theta: float) -> np.ndarray:
+    """QwenCPUApplyRoPE (QwenHybrid.CPU.pas:51-67), rows at position + row; returns a rotated copy."""
+    y = np.array(x, np.float32, copy=True).reshape(-1)
+    _check(lib().qo_rope(_p(y, _f32p), rows, heads, dim, position, theta), "rope")
+    return y
+
+
+def cache_write(cache: np.ndarray, k: np.ndarray, v: np.ndarray, rows: int, kv_heads: int, dim: int, cap: int,
+                position: int) -> None:
+    """KV-cache append (QwenHybrid.CPU.pas:198-204, tensor.comp:313-317), in place."""
+    k = np.ascontiguousarray(k, np.float32).reshape(-1)
+    v = np.ascontiguousarray(v, np.float32).reshape(-1)
+    _check(lib().qo_cache_write(_p(cache, _f32p), _p(k, _f32p), _p(v, _f32p), rows, kv_heads, dim, cap, position),
+           "cache_write")
+
+
+def cached_attention(q, cache, rows, cap, heads, kv_heads, dim, position, window=0, softcap=0.0, scale=0.0,
+                     masked=False) -> np.ndarray:
+    """CachedAttention (attention.comp mask modes 2 and 4) in double."""
+    q = np.ascontiguousarray(q, np.float32).reshape(-1)
+    cache = np.ascontiguousarray(cache, np.float32).reshape(-1)
+    out = np.empty(rows * heads * dim, np.float32)
+    _check(lib().qo_cached_attention(_p(q, _f32p), _p(cache, _f32p), rows, cap, heads, kv_heads, dim, position, window,
+                                     softcap, scale, int(masked), _p(out, _f32p)), "cached_attention")
+    return out
+
+
+def sample_topk(logits, seen, k: int, penalty: float = 1.0):
+    """SampleToken's ranked top-k: (scores, ids)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    seen = np.ascontiguousarray(seen, np.uint32)
+    s = np.empty(k, np.float32)
+    i = np.empty(k, np.uint32)
+    _check(lib().qo_sample_topk(_p(logits, _f32p), _p(seen, _u32p), logits.size, k, penalty, _p(s, _f32p),
+                                _p(i, _u32p)), "sample_topk")
+    return s, i
+
+
+def sample_token(logits, seen, top_k: int, temperature: float, top_p: float, penalty: float, uniform: float) -> int:
+    """SampleToken (Context.Implementation.inc:1137-1187, tensor.comp:177-197)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    seen = np.ascontiguousarray(seen, np.uint32)
+    return int(lib().qo_sample_token(_p(logits, _f32p), _p(seen, _u32p), logits.size, top_k, temperature, top_p,
+                                     penalty, uniform))

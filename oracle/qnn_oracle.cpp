@@ -897,4 +897,164 @@ int qo_q8_gemm_i8(const uint8_t *w, const int8_t *q, const float *d, int m, int 
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// The rest of a decode layer
+// ---------------------------------------------------------------------------
+
+// QwenCPUApplyRoPE (src/models/QuickNN.Models.QwenHybrid.CPU.pas:51-67) with
+// RotaryDim = Dim and one position axis: Angle := Pos * Power(Theta, -2*J/Dim)
+// in double; X[First] := A*Cos(Angle) - B*Sin(Angle), X[Second] := A*Sin(Angle)
+// + B*Cos(Angle) in double, stored as Single.  The rows of a multi-row call sit
+// at Position + row (tensor.comp:320).
+int qo_rope(float *x, int rows, int heads, int dim, int position, float theta) {
+  if (!x || rows < 1 || heads < 1 || dim < 2 || dim % 2 || position < 0 || !(theta > 0.0f)) return -1;
+  const int half = dim / 2;
+  for (int r = 0; r < rows; ++r)
+    for (int h = 0; h < heads; ++h)
+      for (int j = 0; j < half; ++j) {
+        const double angle = double(position + r) * std::pow(double(theta), -2.0 * double(j) / double(dim));
+        float *row = x + ((size_t)r * heads + h) * dim;
+        const double a = row[j], b = row[j + half];
+        const double c = std::cos(angle), s = std::sin(angle);
+        row[j] = float(a * c - b * s);
+        row[j + half] = float(a * s + b * c);
+      }
+  return 0;
+}
+
+// The cache layout written by QwenHybrid.CPU.pas:198-204 (and tensor.comp:313-317).
+int qo_cache_write(float *cache, const float *k, const float *v, int rows, int kv_heads, int dim, int cap,
+                   int position) {
+  if (!cache || !k || !v || rows < 1 || kv_heads < 1 || dim < 1 || position < 0 || position + rows > cap) return -1;
+  const size_t width = (size_t)kv_heads * dim;
+  for (int r = 0; r < rows; ++r)
+    for (int h = 0; h < kv_heads; ++h)
+      for (int j = 0; j < dim; ++j) {
+        const size_t src = (size_t)r * width + (size_t)h * dim + j;
+        const size_t t = (size_t)position + r;
+        cache[((size_t)h * dim + j) * cap + t] = k[src];
+        cache[(size_t)cap * width + ((size_t)h * cap + t) * dim + j] = v[src];
+      }
+  return 0;
+}
+
+// attention.comp:17-44 with mask mode 2 (4 when masked): query row r attends
+// to keys [start, position + r] (start = end - window when window > 0 and the
+// range is longer), skipping keys whose mask word is zero; scores scaled by
+// `scale` or 1/sqrt(dim), optionally capped by softcap * tanh(s / softcap)
+// (arguments clamped to +-20); softmax; weighted sum of V.  All in double.
+int qo_cached_attention(const float *q, const float *cache, int rows, int cap, int heads, int kv_heads, int dim,
+                        int position, int window, float softcap, float scale, int masked, float *out) {
+  if (!q || !cache || !out || rows < 1 || cap < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads || dim < 1 ||
+      position < 0 || position + rows > cap || window < 0)
+    return -1;
+  const size_t width = (size_t)kv_heads * dim;
+  const float *vbase = cache + (size_t)cap * width;
+  const uint32_t *mask = reinterpret_cast<const uint32_t *>(cache + 2 * (size_t)cap * width);
+  const int group = heads / kv_heads;
+  const double mul = scale > 0.0f ? double(scale) : 1.0 / std::sqrt(double(dim));
+  std::vector<double> sc(cap), acc(dim);
+  for (int r = 0; r < rows; ++r) {
+    const int end = position + r + 1;
+    const int start = (window > 0 && end > window) ? end - window : 0;
+    for (int h = 0; h < heads; ++h) {
+      const int kh = h / group;
+      const float *qr = q + ((size_t)r * heads + h) * dim;
+      double mx = -INFINITY;
+      for (int j = start; j < end; ++j) {
+        if (masked && mask[(size_t)r * cap + j] == 0u) {
+          sc[j] = -INFINITY;
+          continue;
+        }
+        double s = 0.0;
+        for (int d = 0; d < dim; ++d) s += double(qr[d]) * double(cache[((size_t)kh * dim + d) * cap + j]);
+        s *= mul;
+        if (softcap > 0.0f) s = double(softcap) * std::tanh(std::min(std::max(s / double(softcap), -20.0), 20.0));
+        sc[j] = s;
+        mx = std::max(mx, s);
+      }
+      double den = 0.0;
+      std::fill(acc.begin(), acc.end(), 0.0);
+      for (int j = start; j < end; ++j) {
+        if (sc[j] == -INFINITY) continue;
+        const double p = std::exp(sc[j] - mx);
+        den += p;
+        const float *vr = vbase + ((size_t)kh * cap + j) * dim;
+        for (int d = 0; d < dim; ++d) acc[d] += p * double(vr[d]);
+      }
+      float *o = out + ((size_t)r * heads + h) * dim;
+      for (int d = 0; d < dim; ++d) o[d] = float(acc[d] / den);
+    }
+  }
+  return 0;
+}
+
+namespace {
+const float kLowestF = -3.402823466e38f;
+bool ranks_before(float s, uint32_t id, float bs, uint32_t bid) { return s > bs || (s == bs && id < bid); }
+}  // namespace
+
+// tensor.comp:160-176: k ranks, each the best remaining (score, id) with
+// best = -FLT_MAX, id = 0xffffffff to start, penalty applied to seen tokens.
+int qo_sample_topk(const float *logits, const uint32_t *seen, int vocab, int k, float penalty, float *scores,
+                   uint32_t *ids) {
+  if (!logits || !seen || !scores || !ids || vocab < 1 || k < 1 || k > 64) return -1;
+  std::vector<uint8_t> used(vocab, 0);
+  for (int rank = 0; rank < k; ++rank) {
+    float best = kLowestF;
+    uint32_t best_id = 0xffffffffu;
+    for (int t = 0; t < vocab; ++t) {
+      if (seen[t] == 0xffffffffu || used[t]) continue;
+      float s = logits[t];
+      if (seen[t] != 0u) s = s < 0.0f ? s * penalty : s / penalty;
+      if (ranks_before(s, uint32_t(t), best, best_id)) {
+        best = s;
+        best_id = uint32_t(t);
+      }
+    }
+    if (best_id != 0xffffffffu) used[best_id] = 1;
+    scores[rank] = best;
+    ids[rank] = best_id;
+  }
+  return 0;
+}
+
+// tensor.comp:177-197: weights exp((v_j - v_0) / T) (fp32, exp correctly
+// rounded), the nucleus as the shortest prefix whose running sum reaches
+// top_p * total, then the first rank whose running sum exceeds uniform * kept.
+uint32_t qo_sample_token(const float *logits, const uint32_t *seen, int vocab, int top_k, float temperature,
+                         float top_p, float penalty, float uniform) {
+  if (vocab < 1 || top_k < 1 || top_k > 64) return 0xffffffffu;
+  const int k = temperature <= 0.0f ? 1 : std::min(vocab, top_k);
+  float sc[64];
+  uint32_t id[64];
+  if (qo_sample_topk(logits, seen, vocab, k, penalty, sc, id)) return 0xffffffffu;
+  uint32_t selected = id[0];
+  if (temperature > 0.0f && k > 1) {
+    float total = 0.0f;
+    const float maximum = sc[0];
+    for (int j = 0; j < k; ++j) {
+      sc[j] = float(std::exp(double((sc[j] - maximum) / temperature)));
+      total += sc[j];
+    }
+    float retained = 0.0f;
+    int count = 0;
+    do {
+      retained += sc[count];
+      ++count;
+    } while (count < k && retained < top_p * total);
+    const float target = uniform * retained;
+    float accumulated = 0.0f;
+    selected = id[count - 1];
+    for (int j = 0; j < count; ++j) {
+      accumulated += sc[j];
+      if (target < accumulated) {
+        selected = id[j];
+        break;
+      }
+    }
+  }
+  return selected;
+}
+
 }  // extern "C"

@@ -81,6 +81,26 @@ int qo_gguf_gemm_scalar(const uint8_t *w, int enc, const float *a, int m, int k,
 int qo_q8_act_quant(const float *a, int m, int k, int8_t *q, float *d);          /* GGML Q8_0 rule, fp32 d */
 int qo_q8_gemm_i8(const uint8_t *w, const int8_t *q, const float *d, int m, int k, int n, float *c);
 
+/* ---- the rest of a decode layer ---- */
+/* RoPE as the reference's CPU statement (src/models/QuickNN.Models.QwenHybrid.CPU.pas:51-67, RotaryDim = dim):
+ * pairs (j, j + dim/2) of each of rows*heads head rows rotated by (position + row) * theta^(-2j/dim),
+ * angle, sine, cosine and rotation in double, rounded once.  In place. */
+int qo_rope(float *x, int rows, int heads, int dim, int position, float theta);
+/* KV-cache append (tensor.comp:313-317; CPU statement QwenHybrid.CPU.pas:198-204):
+ * K transposed [kv_heads][dim][cap], then V [kv_heads][cap][dim]. */
+int qo_cache_write(float *cache, const float *k, const float *v, int rows, int kv_heads, int dim, int cap,
+                   int position);
+/* CachedAttention (attention.comp, mask modes 2 and 4) in double: out fp32 [rows][heads][dim]. */
+int qo_cached_attention(const float *q, const float *cache, int rows, int cap, int heads, int kv_heads, int dim,
+                        int position, int window, float softcap, float scale, int masked, float *out);
+/* SampleToken's top-k (tensor.comp:123-176): k best (score after penalty, id) ranked by score then id;
+ * tokens with seen == 0xffffffff excluded; unfilled ranks are (-FLT_MAX, 0xffffffff). */
+int qo_sample_topk(const float *logits, const uint32_t *seen, int vocab, int k, float penalty, float *scores,
+                   uint32_t *ids);
+/* SampleToken (Context.Implementation.inc:1137-1187, tensor.comp:177-197): the selected token id. */
+uint32_t qo_sample_token(const float *logits, const uint32_t *seen, int vocab, int top_k, float temperature,
+                         float top_p, float penalty, float uniform);
+
 /* ---- numerics helpers ---- */
 float qo_half_to_float(uint16_t h);            /* src/core/QuickNN.Common.pas:1799+ */
 uint16_t qo_float_to_half(float f);            /* round-to-nearest-even (test helper) */

@@ -1857,6 +1857,61 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
                            n, hidden, topk, offset, route, single, pbase, ctx->error_flag, ctx->stream);
         return QNN_OK;
       }
+      case QNN_GO_SCALE: {
+        // tensor.comp:309: dst = a * v0 + v1 (v1 defaults to 0, as an unset push constant).
+        float mul, add = 0.0f;
+        const int mb = arg(0), ab = nargs > 1 ? args[1] : 0;
+        std::memcpy(&mul, &mb, 4);
+        std::memcpy(&add, &ab, 4);
+        check_tensor(ctx, a, n);
+        check_tensor(ctx, dst, n);
+        if (n) decode_scale(dst->ptr, a->ptr, n, mul, add, ctx->stream);
+        return QNN_OK;
+      }
+      case QNN_GO_SOFTCAP: {
+        float cap;
+        const int cb = arg(0);
+        std::memcpy(&cap, &cb, 4);
+        check_tensor(ctx, a, n);
+        check_tensor(ctx, dst, n);
+        if (n) decode_softcap(dst->ptr, a->ptr, n, cap, ctx->stream);
+        return QNN_OK;
+      }
+      case QNN_GO_LLM_CACHE_WRITE: {
+        // Args [Rows, KvHeads, HeadDim, Capacity, Position] (LLM.pas:556-563).
+        const int kvh = arg(1), dim = arg(2), cap = arg(3), pos = arg(4);
+        if (kvh < 1 || dim < 1 || cap < 1 || pos < 0 || n % (int64_t(kvh) * dim) != 0)
+          fail(QNN_E_ARGUMENT, "GO_LLM_CACHE_WRITE geometry");
+        const int64_t rows = n / (int64_t(kvh) * dim);
+        if (pos + rows > cap) fail(QNN_E_ARGUMENT, "GO_LLM_CACHE_WRITE: rows past the cache capacity");
+        check_tensor(ctx, a, n);
+        check_tensor(ctx, b, n);
+        check_tensor(ctx, dst, 2 * int64_t(cap) * kvh * dim);
+        if (n) decode_cache_write(dst->ptr, a->ptr, b->ptr, n, kvh, dim, cap, pos, ctx->stream);
+        return QNN_OK;
+      }
+      case QNN_GO_LLM_ROPE: {
+        // Args [Heads, HeadDim, Position, Theta bits] (LLM.pas:538-546); N = rows * heads * dim / 2.
+        const int heads = arg(0), dim = arg(1), pos = arg(2), tb = arg(3);
+        float theta;
+        std::memcpy(&theta, &tb, 4);
+        if (heads < 1 || dim < 2 || dim % 2 || pos < 0 || n % (int64_t(heads) * (dim / 2)) != 0 ||
+            !(theta > 0.0f) || std::isinf(theta))
+          fail(QNN_E_ARGUMENT, "GO_LLM_ROPE geometry");
+        check_tensor(ctx, a, 2 * int64_t(n));
+        check_tensor(ctx, dst, 2 * int64_t(n));
+        if (n) decode_rope(dst->ptr, a->ptr, n, heads, dim, pos, theta, ctx->stream);
+        return QNN_OK;
+      }
+      case QNN_GO_LLM_SEEN: {
+        // Args [Vocab] (LLM.pas:643): flags[a[i]] |= 1 for ids below Vocab.
+        const int vocab = arg(0);
+        if (vocab < 1) fail(QNN_E_ARGUMENT, "GO_LLM_SEEN vocabulary");
+        check_tensor(ctx, a, n);
+        check_tensor(ctx, dst, vocab);
+        if (n) decode_seen(dst->ptr, a->ptr, n, vocab, ctx->stream);
+        return QNN_OK;
+      }
     }
     fail(QNN_E_NOT_SUPPORTED, "op code not implemented by the HIP backend");
     return QNN_OK;
@@ -1890,6 +1945,50 @@ int qnn_kernel_weights(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor 
       bbf = be->raw_dtype == QNN_DT_BF16;
     }
     misc_norm(dst->ptr, a->ptr, gp, gbf, bp, bbf, rows, dim, flags, soff, unit, eps, ctx->stream);
+    return QNN_OK;
+  });
+}
+
+int qnn_cached_attention(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *q, qnn_tensor *cache, int query_rows, int capacity,
+                         int heads, int kv_heads, int dim, int position, int window, float softcap, float scale,
+                         int masked) {
+  return guarded([&] {
+    check_ctx(ctx);
+    // The argument rules of CachedAttention (Context.Implementation.inc:1194-1207).
+    if (query_rows < 1 || query_rows > 65535 || capacity < 1 || position < 0 ||
+        int64_t(position) + query_rows > capacity || heads < 1 || kv_heads < 1 || heads % kv_heads != 0 ||
+        dim < 1 || dim > 1152 || window < 0 || !(softcap >= 0.0f) || std::isinf(softcap) || !(scale >= 0.0f) ||
+        std::isinf(scale))
+      fail(QNN_E_ARGUMENT, "Invalid resident cached attention");
+    check_tensor(ctx, q, int64_t(query_rows) * heads * dim);
+    check_tensor(ctx, dst, int64_t(query_rows) * heads * dim);
+    check_tensor(ctx, cache, 2 * int64_t(capacity) * kv_heads * dim + (masked ? int64_t(query_rows) * capacity : 0));
+    const AttnPlan p = attn_plan(query_rows, heads, kv_heads, dim, position, window);
+    float *ws = p.part_floats ? static_cast<float *>(ensure_work(ctx, p.part_floats * 4)) : nullptr;
+    attn_launch(q->ptr, cache->ptr, dst->ptr, ws, p, query_rows, capacity, heads, kv_heads, dim, position, window,
+                softcap, scale, masked ? 1 : 0, ctx->stream);
+    return QNN_OK;
+  });
+}
+
+int qnn_sample_token(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *logits, qnn_tensor *seen, int vocab, int top_k,
+                     float temperature, float top_p, float penalty, float uniform) {
+  return guarded([&] {
+    check_ctx(ctx);
+    // The argument rules of SampleToken (Context.Implementation.inc:1143-1168).
+    check_tensor(ctx, dst, 1);
+    check_tensor(ctx, logits, vocab > 0 ? vocab : 1);
+    check_tensor(ctx, seen, vocab > 0 ? vocab : 1);
+    if (vocab < 1 || top_k < 1 || top_k > 64 || std::isnan(temperature) || std::isinf(temperature) ||
+        temperature < 0 || std::isnan(top_p) || top_p <= 0 || top_p > 1 || std::isnan(penalty) ||
+        std::isinf(penalty) || penalty <= 0 || std::isnan(uniform) || uniform < 0 || uniform >= 1 || dst == logits ||
+        dst == seen)
+      fail(QNN_E_ARGUMENT, "Invalid GPU token sampling arguments");
+    const int k = temperature == 0.0f ? 1 : std::min(vocab, top_k);
+    ensure_splitk(ctx, 0, 1);
+    float *cand = static_cast<float *>(ensure_work(ctx, sample_workspace_floats(vocab, k) * 4));
+    sample_launch(dst->ptr, logits->ptr, seen->ptr, cand, ctx->counters, vocab, k, temperature, top_p, penalty, uniform,
+                  ctx->stream);
     return QNN_OK;
   });
 }

@@ -1,0 +1,720 @@
+// qnn_decode.hip -- the rest of a resident decode layer: RoPE, KV-cache
+// append, cached attention, seen-token flags and token sampling.
+//
+// Semantics follow the Vulkan shaders cited per kernel
+// (src/backends/vulkan/shaders/tensor.comp, attention.comp) and the host
+// methods that drive them (QuickNN.Vulkan.Context.Implementation.inc).
+//
+// Cached attention is split over keys (flash-decoding): a workgroup owns one
+// query row, a batch of the query heads that share one KV head (so K and V are
+// read once for all of them), and a chunk of keys; it writes the chunk's
+// running max, sum and unnormalised output, and a second launch merges the
+// chunks.  The KV cache is fp32 in the reference's layout: K transposed
+// [kv_heads][dim][capacity] (keys contiguous, coalesced score loads), then V
+// [kv_heads][capacity][dim] (channels contiguous).
+//
+// Sampling is one launch: workgroups take exact local top-k of 4096-token
+// tiles, and the last workgroup to arrive merges the tiles' candidates, takes
+// the global top-k and draws the token, as tensor.comp:123-199 does in two.
+#include <cmath>
+
+#include "qnn_exchange.h"
+
+namespace qnn {
+namespace {
+
+// ---------------------------------------------------------------------------
+// GO_LLM_ROPE (tensor.comp:318-327): rotate the pairs (j, j + dim/2) of each
+// head row by angle (position + row) * theta^(-2j/dim).  The angle, its sine
+// and cosine and the rotation are evaluated in double and rounded once, as the
+// reference's CPU statement of the same rotation does
+// (src/models/QuickNN.Models.QwenHybrid.CPU.pas:51-67).
+__global__ void k_rope(float *dst, const float *src, int n, int heads, int dim, int position, float theta) {
+#pragma clang fp contract(off)
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  const int half = dim / 2, j = id % half, hr = id / half, r = hr / heads;
+  const double angle = double(position + r) * pow(double(theta), -2.0 * double(j) / double(dim));
+  double s, c;
+  sincos(angle, &s, &c);
+  const size_t x = size_t(hr) * dim + j, y = x + half;
+  const double a = src[x], b = src[y];
+  dst[x] = float(a * c - b * s);
+  dst[y] = float(a * s + b * c);
+}
+
+// GO_LLM_CACHE_WRITE (tensor.comp:313-317): append rows of K and V at
+// position + row: K transposed, V head-major.
+__global__ void k_cache_write(float *cache, const float *k, const float *v, int n, int kv_heads, int dim, int cap,
+                              int position) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  const int width = kv_heads * dim, r = id / width, h = (id % width) / dim, j = id % dim, t = position + r;
+  cache[(size_t(h) * dim + j) * cap + t] = k[id];
+  cache[size_t(cap) * width + (size_t(h) * cap + t) * dim + j] = v[id];
+}
+
+// GO_LLM_SEEN (tensor.comp:328): flag[token] |= 1 for each token id below vocab.
+__global__ void k_seen(unsigned *flags, const unsigned *ids, int n, unsigned vocab) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  const unsigned token = ids[id];
+  if (token < vocab) atomicOr(&flags[token], 1u);
+}
+
+// GO_SCALE (tensor.comp:309): x * a + b.  GO_SOFTCAP (tensor.comp:308):
+// cap * tanh(clamp(x / cap, -20, 20)).
+__global__ void k_scale(float *dst, const float *src, int n, float a, float b) {
+#pragma clang fp contract(off)
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id < n) dst[id] = src[id] * a + b;
+}
+__global__ void k_softcap(float *dst, const float *src, int n, float cap) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id < n) dst[id] = cap * tanhf(fminf(fmaxf(src[id] / cap, -20.0f), 20.0f));
+}
+
+// ---------------------------------------------------------------------------
+// Cached attention (attention.comp, the online path the resident context
+// dispatches with mask mode 2, or 4 with a per-row key mask).
+//
+// A workgroup owns (query row, GB heads of one KV head, a chunk of keys).  It
+// walks the chunk in sub-chunks of up to 256 keys with an online softmax.
+// Score pass: P = 256 / sub-chunk threads per key, each over dim / P channels
+// with up to 32 independent K loads in flight (K^T rows are contiguous in the
+// key, so a wave's load covers 64 consecutive keys).  Value pass: float4
+// channel groups, dim / 4 lanes per key and 256 / (dim / 4) keys at a time,
+// four or eight keys' loads in flight per lane.
+constexpr int kAttnThreads = 256;
+constexpr int kAttnSub = 256;  // keys per sub-chunk at most
+
+struct AttnArgs {
+  int rows, cap, heads, kv_heads, dim, position, window, masked;
+  float softcap, scale;
+  int group, gpk, splits, chunk, sub, parts, lpk, kl, nd4;
+};
+
+__device__ __forceinline__ void key_range(const AttnArgs &a, int r, int &start, int &end) {
+  end = a.position + r + 1;
+  start = (a.window > 0 && end > a.window) ? end - a.window : 0;
+}
+
+// Four channels c .. c+3 of a row of `dim` floats: one 16-byte access when
+// rows are 16-byte aligned (dim % 4 == 0), else element by element within dim.
+__device__ __forceinline__ float4 load4(const float *row, int c, int dim) {
+  if ((dim & 3) == 0) return *reinterpret_cast<const float4 *>(row + c);
+  return make_float4(row[c], c + 1 < dim ? row[c + 1] : 0.f, c + 2 < dim ? row[c + 2] : 0.f,
+                     c + 3 < dim ? row[c + 3] : 0.f);
+}
+__device__ __forceinline__ void store4(float *row, int c, int dim, float4 v) {
+  if ((dim & 3) == 0) {
+    *reinterpret_cast<float4 *>(row + c) = v;
+    return;
+  }
+  row[c] = v.x;
+  if (c + 1 < dim) row[c + 1] = v.y;
+  if (c + 2 < dim) row[c + 2] = v.z;
+  if (c + 3 < dim) row[c + 3] = v.w;
+}
+
+template <int GB>
+__device__ __forceinline__ void block_max_sum(float (&v)[GB], float *red, bool is_max) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    float x = v[g];
+    for (int off = 32; off > 0; off >>= 1) {
+      const float o = __shfl_xor(x, off);
+      x = is_max ? fmaxf(x, o) : x + o;
+    }
+    if (lane == 0) red[g * 4 + wave] = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < GB; ++g)
+    v[g] = is_max ? fmaxf(fmaxf(red[g * 4], red[g * 4 + 1]), fmaxf(red[g * 4 + 2], red[g * 4 + 3]))
+                  : (red[g * 4] + red[g * 4 + 1]) + (red[g * 4 + 2] + red[g * 4 + 3]);
+  __syncthreads();
+}
+
+template <int GB, int ND4>
+__global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__ q, const float *__restrict__ cache,
+                                                       float *__restrict__ out, float *__restrict__ opart,
+                                                       float *__restrict__ mlpart, AttnArgs a) {
+  extern __shared__ float lds[];
+  float *qs = lds;                        // [GB][dim]
+  float *ps = qs + GB * a.dim;            // [GB][sub]
+  float *red = ps + GB * kAttnSub;        // [GB][4]
+  float *xred = red + GB * 4;             // score parts [parts][GB][sub], then value lanes [kl][GB][dim]
+  const int tid = threadIdx.x;
+  const int kh = blockIdx.x / a.gpk, h0 = kh * a.group + (blockIdx.x % a.gpk) * GB;
+  const int r = blockIdx.y, s = blockIdx.z;
+  int start, end;
+  key_range(a, r, start, end);
+  const int k0 = start + s * a.chunk, k1 = min(end, k0 + a.chunk);
+  const size_t width = size_t(a.kv_heads) * a.dim;
+  const float *kt = cache + size_t(kh) * a.dim * a.cap;
+  const float *vb = cache + size_t(a.cap) * width + size_t(kh) * a.cap * a.dim;
+  const unsigned *mask = reinterpret_cast<const unsigned *>(cache + 2 * size_t(a.cap) * width) + size_t(r) * a.cap;
+
+  for (int i = tid; i < GB * a.dim; i += kAttnThreads) {
+    const int g = i / a.dim, d = i % a.dim;
+    qs[i] = q[(size_t(r) * a.heads + h0 + g) * a.dim + d];
+  }
+  __syncthreads();
+
+  const float mul = a.scale > 0.0f ? a.scale : 1.0f / sqrtf(float(a.dim));
+  float m_run[GB], l_run[GB];
+  float4 acc[GB][ND4];
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ND4; ++i) acc[g][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const int key_t = tid % a.sub, part = tid / a.sub;
+  const int dp = (a.dim + a.parts - 1) / a.parts, d0 = part * dp, d1 = min(a.dim, d0 + dp);
+  const int kk = tid / a.lpk, c4 = tid % a.lpk;  // value pass: key lane, float4 channel group
+
+  for (int c0 = k0; c0 < k1; c0 += a.sub) {
+    const int c1 = min(k1, c0 + a.sub);
+    // ---- scores (part of the channels per thread)
+    const int j = c0 + key_t;
+    bool valid = j < c1 && part < a.parts;
+    if (valid && a.masked) valid = mask[j] != 0u;
+    float sc[GB];
+#pragma unroll
+    for (int g = 0; g < GB; ++g) sc[g] = 0.0f;
+    if (valid) {
+      const float *kc = kt + j;
+      int d = d0;
+      for (; d + 32 <= d1; d += 32) {
+        float kv[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) kv[u] = kc[size_t(d + u) * a.cap];
+#pragma unroll
+        for (int u = 0; u < 32; ++u)
+#pragma unroll
+          for (int g = 0; g < GB; ++g) sc[g] += qs[g * a.dim + d + u] * kv[u];
+      }
+      for (; d + 8 <= d1; d += 8) {
+        float kv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) kv[u] = kc[size_t(d + u) * a.cap];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int g = 0; g < GB; ++g) sc[g] += qs[g * a.dim + d + u] * kv[u];
+      }
+      for (; d < d1; ++d) {
+        const float kv = kc[size_t(d) * a.cap];
+#pragma unroll
+        for (int g = 0; g < GB; ++g) sc[g] += qs[g * a.dim + d] * kv;
+      }
+    }
+    if (a.parts > 1) {
+#pragma unroll
+      for (int g = 0; g < GB; ++g) xred[(part * GB + g) * a.sub + key_t] = sc[g];
+      __syncthreads();
+      if (part == 0)
+#pragma unroll
+        for (int g = 0; g < GB; ++g) {
+          float v = sc[g];
+          for (int p = 1; p < a.parts; ++p) v += xred[(p * GB + g) * a.sub + key_t];
+          sc[g] = v;
+        }
+      __syncthreads();
+      valid = valid && part == 0;
+    }
+    float cm[GB];
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      float v = sc[g] * mul;
+      if (a.softcap > 0.0f) v = a.softcap * tanhf(fminf(fmaxf(v / a.softcap, -20.0f), 20.0f));
+      sc[g] = v;
+      cm[g] = valid ? v : -INFINITY;
+    }
+    block_max_sum<GB>(cm, red, true);
+    float m_new[GB], keep[GB], ls[GB];
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      m_new[g] = fmaxf(m_run[g], cm[g]);
+      keep[g] = m_new[g] == -INFINITY ? 1.0f : expf(m_run[g] - m_new[g]);
+      const float p = (valid && m_new[g] > -INFINITY) ? expf(sc[g] - m_new[g]) : 0.0f;
+      if (part == 0) ps[g * kAttnSub + key_t] = p;
+      ls[g] = p;
+    }
+    block_max_sum<GB>(ls, red, false);  // its barriers also publish ps
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      l_run[g] = l_run[g] * keep[g] + ls[g];
+      m_run[g] = m_new[g];
+#pragma unroll
+      for (int i = 0; i < ND4; ++i) {
+        acc[g][i].x *= keep[g];
+        acc[g][i].y *= keep[g];
+        acc[g][i].z *= keep[g];
+        acc[g][i].w *= keep[g];
+      }
+    }
+    // ---- values: lane group kk walks keys kk, kk + kl, ..., U at a time
+    constexpr int U = GB * ND4 >= 8 ? 4 : 8;
+    if (kk < a.kl) {
+      const int nkeys = c1 - c0;
+      for (int key0 = kk; key0 < nkeys; key0 += U * a.kl) {
+        float4 vv[U][ND4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int key = key0 + u * a.kl;
+#pragma unroll
+          for (int i = 0; i < ND4; ++i) {
+            const int cg = c4 + i * a.lpk;
+            vv[u][i] = (key < nkeys && i < a.nd4 && cg * 4 < a.dim)
+                           ? load4(vb + size_t(c0 + key) * a.dim, cg * 4, a.dim)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int key = key0 + u * a.kl;
+          if (key < nkeys)
+#pragma unroll
+            for (int g = 0; g < GB; ++g) {
+              const float w = ps[g * kAttnSub + key];
+#pragma unroll
+              for (int i = 0; i < ND4; ++i) {
+                acc[g][i].x += w * vv[u][i].x;
+                acc[g][i].y += w * vv[u][i].y;
+                acc[g][i].z += w * vv[u][i].z;
+                acc[g][i].w += w * vv[u][i].w;
+              }
+            }
+        }
+      }
+    }
+    __syncthreads();  // ps is rewritten by the next sub-chunk
+  }
+
+  // Sum the key lanes.
+  if (a.kl > 1) {
+    if (kk < a.kl)
+#pragma unroll
+      for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int i = 0; i < ND4; ++i) {
+          const int cg = c4 + i * a.lpk;
+          if (i < a.nd4 && cg * 4 < a.dim) store4(xred + (size_t(kk) * GB + g) * a.dim, cg * 4, a.dim, acc[g][i]);
+        }
+    __syncthreads();
+    if (kk == 0)
+#pragma unroll
+      for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int i = 0; i < ND4; ++i) {
+          const int cg = c4 + i * a.lpk;
+          if (i < a.nd4 && cg * 4 < a.dim)
+            for (int l = 1; l < a.kl; ++l) {
+              const float4 o = load4(xred + (size_t(l) * GB + g) * a.dim, cg * 4, a.dim);
+              acc[g][i].x += o.x;
+              acc[g][i].y += o.y;
+              acc[g][i].z += o.z;
+              acc[g][i].w += o.w;
+            }
+        }
+  }
+  if (kk != 0) return;
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    const size_t row_head = size_t(r) * a.heads + h0 + g;
+#pragma unroll
+    for (int i = 0; i < ND4; ++i) {
+      const int cg = c4 + i * a.lpk;
+      if (i < a.nd4 && cg * 4 < a.dim) {
+        float4 o = acc[g][i];
+        if (a.splits == 1) {
+          const float l = l_run[g];
+          o = make_float4(o.x / l, o.y / l, o.z / l, o.w / l);
+          store4(out + row_head * a.dim, cg * 4, a.dim, o);
+        } else {
+          store4(opart + (size_t(s) * a.rows * a.heads + row_head) * a.dim, cg * 4, a.dim, o);
+        }
+      }
+    }
+    if (a.splits > 1 && tid == 0) {
+      float *ml = mlpart + (size_t(s) * a.rows * a.heads + row_head) * 2;
+      ml[0] = m_run[g];
+      ml[1] = l_run[g];
+    }
+  }
+}
+
+// Merge the key chunks: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+// One workgroup per (row, head) and 256 channels; `sg` split groups of
+// threads share a channel and walk the chunks sixteen loads at a time.
+constexpr int kMergeMaxSplits = 4096;
+__global__ __launch_bounds__(256) void k_attn_merge(float *out, const float *opart, const float *mlpart, int splits,
+                                                    int row_heads, int dim, int dspan, int sg) {
+  __shared__ float wsh[kMergeMaxSplits];
+  __shared__ float red[256];
+  const int rh = blockIdx.x, tid = threadIdx.x;
+  float m = -INFINITY;
+  for (int s = tid; s < splits; s += 256) m = fmaxf(m, mlpart[(size_t(s) * row_heads + rh) * 2]);
+  red[tid] = m;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (tid < st) red[tid] = fmaxf(red[tid], red[tid + st]);
+    __syncthreads();
+  }
+  m = red[0];
+  __syncthreads();
+  float l = 0.0f;
+  for (int s = tid; s < splits; s += 256) {
+    const float *ml = mlpart + (size_t(s) * row_heads + rh) * 2;
+    const float w = ml[0] > -INFINITY ? expf(ml[0] - m) : 0.0f;
+    wsh[s] = w;
+    l += ml[1] * w;
+  }
+  red[tid] = l;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (tid < st) red[tid] += red[tid + st];
+    __syncthreads();
+  }
+  l = red[0];
+  __syncthreads();
+  const int g = tid / dspan, d = blockIdx.y * dspan + tid % dspan;
+  float v = 0.0f;
+  if (g < sg && d < dim) {
+    const float *base = opart + size_t(rh) * dim + d;
+    const size_t stride = size_t(row_heads) * dim;
+    int s = g;
+    for (; s + 15 * sg < splits; s += 16 * sg) {
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = base[size_t(s + u * sg) * stride];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v += x[u] * wsh[s + u * sg];
+    }
+    for (; s < splits; s += sg) v += base[size_t(s) * stride] * wsh[s];
+  }
+  red[tid] = v;
+  __syncthreads();
+  if (g == 0 && d < dim) {
+    for (int j = 1; j < sg; ++j) v += red[j * dspan + tid];
+    out[size_t(rh) * dim + d] = v / l;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// SampleToken (Context.Implementation.inc:1137-1187; tensor.comp:123-199).
+//
+// Level 0 reads the logits and seen flags; a workgroup takes the exact top-k
+// of its 4096 tokens (tensor.comp:123-156 does 512).  Each wave first ranks
+// its own 1024 tokens by k wave-wide arg-max rounds (no workgroup barrier),
+// then wave 0 ranks the four waves' lists.  Levels above read the previous
+// level's (score, id) candidates.  When a level's candidates fit one
+// workgroup (tiles * k <= 4096) the last workgroup to finish merges them and
+// draws the token (tensor.comp:160-197), so one launch serves vocabularies up
+// to 4096 * 4096 / k tokens.
+constexpr int kSampleThreads = 256;
+constexpr int kSamplePerThread = 16;
+constexpr int kSampleTile = kSampleThreads * kSamplePerThread;
+constexpr unsigned kNoToken = 0xffffffffu;
+constexpr float kLowest = -3.402823466e38f;
+
+// (s, id) ranks before (bs, bid): higher score, then lower id.
+__device__ __forceinline__ bool ranks_before(float s, unsigned id, float bs, unsigned bid) {
+  return s > bs || (s == bs && id < bid);
+}
+
+struct SampleArgs {
+  int count, k, tiles, level0, merge;
+  float temperature, top_p, penalty, uniform;
+};
+
+// k rounds over the lane's items: each round's pick is the wave-wide best
+// item ranked after the previous pick; lane 0 appends it to out_s / out_i.
+template <int N>
+__device__ __forceinline__ void wave_topk(const float (&vs)[N], const unsigned (&vi)[N], int k, float *out_s,
+                                          unsigned *out_i) {
+  const int lane = threadIdx.x & 63;
+  float ps = INFINITY;
+  unsigned pi = 0;
+  for (int rank = 0; rank < k; ++rank) {
+    float bs = kLowest;
+    unsigned bi = kNoToken;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (vi[i] != kNoToken && (rank == 0 || ranks_before(ps, pi, vs[i], vi[i])) &&
+          ranks_before(vs[i], vi[i], bs, bi)) {
+        bs = vs[i];
+        bi = vi[i];
+      }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float os = __shfl_xor(bs, off);
+      const unsigned oi = __shfl_xor(bi, off);
+      if (ranks_before(os, oi, bs, bi)) {
+        bs = os;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      out_s[rank] = bs;
+      out_i[rank] = bi;
+    }
+    ps = bs;
+    pi = bi;
+  }
+}
+
+__global__ __launch_bounds__(kSampleThreads) void k_sample(unsigned *dst, const float *logits, const unsigned *seen,
+                                                           const float *in_s, const unsigned *in_i, float *out_s,
+                                                           unsigned *out_i, unsigned *counter, SampleArgs a) {
+  __shared__ float ws[4][64];
+  __shared__ unsigned wi[4][64];
+  __shared__ float top_s[64];
+  __shared__ unsigned top_i[64];
+  __shared__ unsigned last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, tile = blockIdx.x;
+  float vs[kSamplePerThread];
+  unsigned vi[kSamplePerThread];
+  // Wave w holds tokens [w*1024, (w+1)*1024) of the tile, lane-strided.
+#pragma unroll
+  for (int i = 0; i < kSamplePerThread; ++i) {
+    const unsigned item = unsigned(tile) * kSampleTile + unsigned(wave) * 1024 + unsigned(i) * 64 + lane;
+    vs[i] = kLowest;
+    vi[i] = kNoToken;
+    if (item < unsigned(a.count)) {
+      if (a.level0) {
+        const unsigned flag = seen[item];
+        if (flag != kNoToken) {
+          float score = logits[item];
+          if (flag != 0u) score = score < 0.0f ? score * a.penalty : score / a.penalty;
+          vs[i] = score;
+          vi[i] = item;
+        }
+      } else {
+        vi[i] = __hip_atomic_load(&in_i[item], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        vs[i] = dev::xload(&in_s[item]);
+      }
+    }
+  }
+  wave_topk<kSamplePerThread>(vs, vi, a.k, ws[wave], wi[wave]);
+  __syncthreads();
+  if (wave == 0) {
+    float s4[4];
+    unsigned i4[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      s4[w] = lane < a.k ? ws[w][lane] : kLowest;
+      i4[w] = lane < a.k ? wi[w][lane] : kNoToken;
+    }
+    wave_topk<4>(s4, i4, a.k, top_s, top_i);
+  }
+  __syncthreads();
+  if (tid < a.k) {
+    dev::xstore(&out_s[size_t(tile) * a.k + tid], top_s[tid]);
+    __hip_atomic_store(&out_i[size_t(tile) * a.k + tid], top_i[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!a.merge) return;
+  // One ticket per workgroup once its candidates are stored.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == unsigned(a.tiles - 1);
+  __syncthreads();
+  if (!last) return;
+
+  // The last workgroup ranks every tile's candidates (at most 4096).
+  const int count = a.tiles * a.k;
+#pragma unroll
+  for (int i = 0; i < kSamplePerThread; ++i) {
+    const int c = wave * 1024 + i * 64 + lane;
+    vs[i] = kLowest;
+    vi[i] = kNoToken;
+    if (c < count) {
+      vi[i] = __hip_atomic_load(&out_i[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      vs[i] = dev::xload(&out_s[c]);
+    }
+  }
+  __syncthreads();
+  wave_topk<kSamplePerThread>(vs, vi, a.k, ws[wave], wi[wave]);
+  __syncthreads();
+  if (wave == 0) {
+    float s4[4];
+    unsigned i4[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      s4[w] = lane < a.k ? ws[w][lane] : kLowest;
+      i4[w] = lane < a.k ? wi[w][lane] : kNoToken;
+    }
+    wave_topk<4>(s4, i4, a.k, top_s, top_i);
+  }
+  __syncthreads();
+  if (tid == 0) {
+#pragma clang fp contract(off)
+    unsigned selected = top_i[0];
+    if (a.temperature > 0.0f && a.k > 1) {
+      float total = 0.0f;
+      const float maximum = top_s[0];
+      for (int j = 0; j < a.k; ++j) {
+        top_s[j] = expf((top_s[j] - maximum) / a.temperature);
+        total += top_s[j];
+      }
+      float retained = 0.0f;
+      int n = 0;
+      do {
+        retained += top_s[n];
+        ++n;
+      } while (n < a.k && retained < a.top_p * total);
+      const float target = a.uniform * retained;
+      float accumulated = 0.0f;
+      selected = top_i[n - 1];
+      for (int j = 0; j < n; ++j) {
+        accumulated += top_s[j];
+        if (target < accumulated) {
+          selected = top_i[j];
+          break;
+        }
+      }
+    }
+    dst[0] = selected;
+    dev::reset_counter(counter, 0);
+  }
+}
+
+int grid_of(int64_t n, int block) { return int((n + block - 1) / block); }
+
+}  // namespace
+
+void decode_rope(float *dst, const float *src, int n, int heads, int dim, int position, float theta, hipStream_t s) {
+  k_rope<<<grid_of(n, 256), 256, 0, s>>>(dst, src, n, heads, dim, position, theta);
+}
+
+void decode_cache_write(float *cache, const float *k, const float *v, int n, int kv_heads, int dim, int cap,
+                        int position, hipStream_t s) {
+  k_cache_write<<<grid_of(n, 256), 256, 0, s>>>(cache, k, v, n, kv_heads, dim, cap, position);
+}
+
+void decode_seen(float *flags, const float *ids, int n, int vocab, hipStream_t s) {
+  k_seen<<<grid_of(n, 256), 256, 0, s>>>(reinterpret_cast<unsigned *>(flags), reinterpret_cast<const unsigned *>(ids),
+                                         n, unsigned(vocab));
+}
+
+void decode_scale(float *dst, const float *src, int n, float a, float b, hipStream_t s) {
+  k_scale<<<grid_of(n, 256), 256, 0, s>>>(dst, src, n, a, b);
+}
+
+void decode_softcap(float *dst, const float *src, int n, float cap, hipStream_t s) {
+  k_softcap<<<grid_of(n, 256), 256, 0, s>>>(dst, src, n, cap);
+}
+
+AttnPlan attn_plan(int rows, int heads, int kv_heads, int dim, int position, int window) {
+  AttnPlan p;
+  const int group = heads / kv_heads;
+  p.gb = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+  const int wgs = kv_heads * (group / p.gb) * rows;
+  const int last_end = position + rows;
+  const int longest = window > 0 ? std::min(window, last_end) : last_end;
+  // About one workgroup per CU, chunks of at least 128 keys (the chunk
+  // partials' merge reads splits * heads * dim floats).
+  const int target = env_int("QNN_ATTN_WGS", 256);
+  const int min_chunk = env_int("QNN_ATTN_MIN_CHUNK", 128);
+  int splits = std::max(1, std::min((target + wgs - 1) / wgs, (longest + min_chunk - 1) / min_chunk));
+  splits = std::min(splits, kMergeMaxSplits);
+  p.chunk = ((longest + splits - 1) / splits + 63) / 64 * 64;
+  p.splits = (longest + p.chunk - 1) / p.chunk;
+  p.part_floats = p.splits > 1 ? size_t(p.splits) * rows * heads * (size_t(dim) + 2) : 0;
+  return p;
+}
+
+void attn_launch(const float *q, const float *cache, float *out, float *ws, const AttnPlan &p, int rows, int cap,
+                 int heads, int kv_heads, int dim, int position, int window, float softcap, float scale, int masked,
+                 hipStream_t s) {
+  AttnArgs a;
+  a.rows = rows;
+  a.cap = cap;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.dim = dim;
+  a.position = position;
+  a.window = window;
+  a.masked = masked;
+  a.softcap = softcap;
+  a.scale = scale;
+  a.group = heads / kv_heads;
+  a.gpk = a.group / p.gb;
+  a.splits = p.splits;
+  a.chunk = p.chunk;
+  a.sub = std::min(p.chunk, kAttnSub);
+  a.parts = kAttnThreads / a.sub;
+  const int groups4 = (dim + 3) / 4;
+  a.lpk = std::min(groups4, kAttnThreads);
+  a.kl = kAttnThreads / a.lpk;
+  a.nd4 = (groups4 + a.lpk - 1) / a.lpk;
+  float *opart = ws, *ml = ws ? ws + size_t(p.splits) * rows * heads * dim : nullptr;
+  const size_t xred = std::max(size_t(a.parts > 1 ? a.parts : 0) * p.gb * a.sub,
+                               size_t(a.kl > 1 ? a.kl : 0) * p.gb * dim);
+  const size_t lds = (size_t(p.gb) * dim + size_t(p.gb) * kAttnSub + p.gb * 4 + xred) * 4;
+  dim3 grid(kv_heads * a.gpk, rows, p.splits);
+#define QNN_ATTN(G, N) k_attn<G, N><<<grid, kAttnThreads, lds, s>>>(q, cache, out, opart, ml, a)
+  if (a.nd4 == 1) {
+    switch (p.gb) {
+      case 8: QNN_ATTN(8, 1); break;
+      case 4: QNN_ATTN(4, 1); break;
+      case 2: QNN_ATTN(2, 1); break;
+      default: QNN_ATTN(1, 1); break;
+    }
+  } else {
+    switch (p.gb) {
+      case 8: QNN_ATTN(8, 2); break;
+      case 4: QNN_ATTN(4, 2); break;
+      case 2: QNN_ATTN(2, 2); break;
+      default: QNN_ATTN(1, 2); break;
+    }
+  }
+#undef QNN_ATTN
+  if (p.splits > 1) {
+    const int dspan = dim >= 256 ? 256 : dim > 128 ? 256 : dim > 64 ? 128 : 64;
+    const int sg = 256 / dspan;
+    dim3 mg(rows * heads, (dim + dspan - 1) / dspan);
+    k_attn_merge<<<mg, 256, 0, s>>>(out, opart, ml, p.splits, rows * heads, dim, dspan, sg);
+  }
+}
+
+size_t sample_workspace_floats(int vocab, int k) {
+  size_t total = 0;
+  for (int count = vocab;;) {
+    const int tiles = (count + kSampleTile - 1) / kSampleTile;
+    total += 2 * size_t(tiles) * k;
+    if (size_t(tiles) * k <= size_t(kSampleTile)) break;
+    count = tiles * k;
+  }
+  return total;
+}
+
+void sample_launch(float *dst, const float *logits, const float *seen, float *ws, unsigned *counter, int vocab, int k,
+                   float temperature, float top_p, float penalty, float uniform, hipStream_t s) {
+  const float *in_s = nullptr;
+  const unsigned *in_i = nullptr;
+  int count = vocab, level0 = 1;
+  for (;;) {
+    const int tiles = (count + kSampleTile - 1) / kSampleTile;
+    const int merge = size_t(tiles) * k <= size_t(kSampleTile) ? 1 : 0;
+    float *out_s = ws;
+    unsigned *out_i = reinterpret_cast<unsigned *>(ws + size_t(tiles) * k);
+    SampleArgs a{count, k, tiles, level0, merge, temperature, top_p, penalty, uniform};
+    k_sample<<<tiles, kSampleThreads, 0, s>>>(reinterpret_cast<unsigned *>(dst), logits,
+                                              reinterpret_cast<const unsigned *>(seen), in_s, in_i, out_s, out_i,
+                                              counter, a);
+    if (merge) break;
+    in_s = out_s;
+    in_i = out_i;
+    ws += 2 * size_t(tiles) * k;
+    count = tiles * k;
+    level0 = 0;
+  }
+}
+
+}  // namespace qnn

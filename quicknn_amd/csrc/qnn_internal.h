@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <list>
@@ -158,6 +159,29 @@ void misc_moe_scatter(float *dst, size_t dst_n, const float *y, const float *ind
                       int prob_base, int *err, hipStream_t s);
 void misc_bias_add(float *dst, const void *bias, int bias_bf16, int rows, int cols, hipStream_t s);
 void misc_pad_rows(float *dst, const float *src, int rows, int cols, int cols_pad, hipStream_t s);
+
+// Decode-layer ops (qnn_decode.hip).
+void decode_rope(float *dst, const float *src, int n, int heads, int dim, int position, float theta, hipStream_t s);
+void decode_cache_write(float *cache, const float *k, const float *v, int n, int kv_heads, int dim, int cap,
+                        int position, hipStream_t s);
+void decode_seen(float *flags, const float *ids, int n, int vocab, hipStream_t s);
+void decode_scale(float *dst, const float *src, int n, float a, float b, hipStream_t s);
+void decode_softcap(float *dst, const float *src, int n, float cap, hipStream_t s);
+// Cached attention: query heads per workgroup (gb), key chunks (splits) and
+// the chunk partials' workspace in floats (0 when one chunk covers the keys).
+struct AttnPlan {
+  int gb = 1, splits = 1, chunk = 64;
+  size_t part_floats = 0;
+};
+AttnPlan attn_plan(int rows, int heads, int kv_heads, int dim, int position, int window);
+void attn_launch(const float *q, const float *cache, float *out, float *ws, const AttnPlan &p, int rows, int cap,
+                 int heads, int kv_heads, int dim, int position, int window, float softcap, float scale, int masked,
+                 hipStream_t s);
+// Token sampling: tiles of 4096 tokens per level; the candidates of every
+// level take sample_workspace_floats words.
+size_t sample_workspace_floats(int vocab, int k);
+void sample_launch(float *dst, const float *logits, const float *seen, float *ws, unsigned *counter, int vocab, int k,
+                   float temperature, float top_p, float penalty, float uniform, hipStream_t s);
 
 // Device-side routed experts (qnn_moe.hip).  Every expert of a set is one
 // contiguous tiled INT4 matrix per projection at base + e * stride.

@@ -75,7 +75,8 @@ GGUF_BLOCK = {WE_Q8_0: (32, 34), WE_Q4_K: (256, 144), WE_Q6_K: (256, 210), WE_Q3
 
 # ---- op codes (Context.API.inc:167-258) ----
 GO_FILL, GO_NORM, GO_ADD, GO_SWIGLU, GO_FINITE = 0, 2, 4, 9, 13
-GO_MOE_ROUTE, GO_MOE_GATHER, GO_MOE_SCATTER, GO_GEGLU = 52, 53, 54, 75
+GO_SCALE, GO_LLM_CACHE_WRITE, GO_LLM_ROPE, GO_LLM_SEEN = 43, 44, 45, 48
+GO_MOE_ROUTE, GO_MOE_GATHER, GO_MOE_SCATTER, GO_GEGLU, GO_SOFTCAP = 52, 53, 54, 75, 76
 
 
 class _Weight(ctypes.Structure):
@@ -147,6 +148,10 @@ def lib():
             "qnn_kernel_weights": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp, W, W, _ip,
                                                   ctypes.c_int]),
             "qnn_check_finite": (ctypes.c_int, [_vp, _vp, ctypes.c_int]),
+            "qnn_cached_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp] + [ctypes.c_int] * 7 +
+                                     [ctypes.c_float, ctypes.c_float, ctypes.c_int]),
+            "qnn_sample_token": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int] +
+                                 [ctypes.c_float] * 4),
             "qnn_expert_set_create": (ctypes.c_int, [_vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                      ctypes.POINTER(_vp)]),
             "qnn_expert_set_destroy": (ctypes.c_int, [_vp, _vp]),
@@ -199,6 +204,7 @@ EXPORTED = (
     "qnn_prefetch_weights", "qnn_stage_weight_prefetch", "qnn_complete_weight_prefetch",
     "qnn_activate_prefetched_weights", "qnn_seal_weight_prefetch", "qnn_end_weight_prefetch", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_q8_gemm_int8", "qnn_int4_linear", "qnn_int4_linear_noalloc", "qnn_swiglu_vector",
     "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
+    "qnn_cached_attention", "qnn_sample_token",
     "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
     "qnn_stream", "qnn_int4_row_bytes", "qnn_quantize_int4", "qnn_gguf_quantize",
@@ -543,6 +549,19 @@ class GPUContext:
                       c: MemoryBlock | None, args) -> None:
         arr = (ctypes.c_int * max(1, len(args)))(*args)
         _raise(lib().qnn_kernel_weights(self.h, op, n, dst.handle, a.handle, _wd(b), _wd(c), arr, len(args)))
+
+    def CachedAttention(self, dst: Tensor, q: Tensor, cache: Tensor, query_rows: int, capacity: int, heads: int,
+                        kv_heads: int, dim: int, position: int, window: int = 0, softcap: float = 0.0,
+                        scale: float = 0.0, masked: bool = False) -> None:
+        """CachedAttention (Context.API.inc:142-146)."""
+        _raise(lib().qnn_cached_attention(self.h, dst.handle, q.handle, cache.handle, query_rows, capacity, heads,
+                                          kv_heads, dim, position, window, softcap, scale, int(masked)))
+
+    def SampleToken(self, dst: Tensor, logits: Tensor, seen: Tensor, vocab: int, top_k: int, temperature: float,
+                    top_p: float, penalty: float, uniform: float) -> None:
+        """SampleToken (Context.API.inc:136-140): dst[0] receives the token id as raw bits."""
+        _raise(lib().qnn_sample_token(self.h, dst.handle, logits.handle, seen.handle, vocab, top_k, temperature, top_p,
+                                      penalty, uniform))
 
     def CheckFinite(self, t: Tensor, count: int = -1) -> None:
         _raise(lib().qnn_check_finite(self.h, t.handle, count))
