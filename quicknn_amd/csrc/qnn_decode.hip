@@ -409,23 +409,199 @@ __global__ __launch_bounds__(256) void k_attn_merge(float *out, const float *opa
 // ---------------------------------------------------------------------------
 // SampleToken (Context.Implementation.inc:1137-1187; tensor.comp:123-199).
 //
+// Tokens are ranked by a 64-bit key: the order-preserving bits of the score
+// (after the repetition penalty; -0 taken as +0) above the inverted token id,
+// so a larger key is a higher score or, on equal scores, a lower id -- the
+// order of tensor.comp:135-136 and :169.  Key 0 is "no token" (excluded by a
+// 0xffffffff seen flag, NaN, or past the vocabulary); keys at or below that of
+// (-FLT_MAX, 0xffffffff) are never picked, as the reference's rank loop never
+// picks them (its running best starts there).
+//
 // Level 0 reads the logits and seen flags; a workgroup takes the exact top-k
-// of its 4096 tokens (tensor.comp:123-156 does 512).  Each wave first ranks
-// its own 1024 tokens by k wave-wide arg-max rounds (no workgroup barrier),
-// then wave 0 ranks the four waves' lists.  Levels above read the previous
-// level's (score, id) candidates.  When a level's candidates fit one
-// workgroup (tiles * k <= 4096) the last workgroup to finish merges them and
-// draws the token (tensor.comp:160-197), so one launch serves vocabularies up
-// to 4096 * 4096 / k tokens.
+// of its 4096 tokens.  Each wave ranks its own 1024: a threshold found by
+// bisection over ballot counts keeps only the tokens that can be in the
+// wave's top-k (at least k half-lane maxima reach it), those are compacted,
+// and k rounds of a DPP wave-wide maximum rank them; wave 0 then ranks the
+// four waves' lists.  Levels above read the previous level's keys.  When a
+// level's keys fit one workgroup (tiles * k <= 4096) the last workgroup to
+// finish ranks them and draws the token (tensor.comp:177-197).
 constexpr int kSampleThreads = 256;
 constexpr int kSamplePerThread = 16;
 constexpr int kSampleTile = kSampleThreads * kSamplePerThread;
 constexpr unsigned kNoToken = 0xffffffffu;
 constexpr float kLowest = -3.402823466e38f;
 
-// (s, id) ranks before (bs, bid): higher score, then lower id.
-__device__ __forceinline__ bool ranks_before(float s, unsigned id, float bs, unsigned bid) {
-  return s > bs || (s == bs && id < bid);
+__device__ __forceinline__ uint32_t order_bits(float s) {
+  const uint32_t u = __float_as_uint(s == 0.0f ? 0.0f : s);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_order_bits(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+__device__ __forceinline__ uint64_t rank_key(float s, unsigned id) {
+  return isnan(s) ? 0ull : (uint64_t(order_bits(s)) << 32) | uint32_t(~id);
+}
+// The key of the reference's starting best (-FLT_MAX, 0xffffffff).
+__device__ __forceinline__ uint64_t floor_key() { return uint64_t(order_bits(kLowest)) << 32; }
+
+// Wave-wide maximum of an unsigned word (all 64 lanes active), uniform
+// result: row_shr 1, 2, 4, 8 leave each row's maximum in its lane 15,
+// row_bcast 15 and 31 carry it to lane 63.  Lanes without a source read 0,
+// the identity of the maximum.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x111, 0xf, 0xf, true)));  // row_shr:1
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x112, 0xf, 0xf, true)));  // row_shr:2
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x114, 0xf, 0xf, true)));  // row_shr:4
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x118, 0xf, 0xf, true)));  // row_shr:8
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x142, 0xa, 0xf, false)));  // row_bcast:15
+  x = max(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x143, 0xc, 0xf, false)));  // row_bcast:31
+  return uint32_t(__builtin_amdgcn_readlane(int(x), 63));
+}
+
+// Wave-wide maximum of 64-bit keys: the high words first; the low words only
+// among the lanes that hold the highest high word.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+  const uint32_t hi = uint32_t(v >> 32), lo = uint32_t(v);
+  const uint32_t mh = wave_max_u32(hi);
+  const uint64_t at = __ballot(hi == mh);
+  uint32_t ml;
+  if (__popcll(at) == 1)
+    ml = uint32_t(__builtin_amdgcn_readlane(int(lo), __ffsll(static_cast<long long>(at)) - 1));
+  else
+    ml = wave_max_u32(hi == mh ? lo : 0u);
+  return (uint64_t(mh) << 32) | ml;
+}
+
+// k rounds over J candidate keys per lane: each takes the wave-wide best key
+// below the previous pick; keys at or below the floor are never picked.
+template <int J>
+__device__ __forceinline__ void rank_rounds(const uint64_t (&c)[J], int k, uint64_t *out) {
+  const uint64_t floor = floor_key();
+  uint64_t prev = ~0ull;
+  for (int rank = 0; rank < k; ++rank) {
+    uint64_t b = 0ull;
+#pragma unroll
+    for (int i = 0; i < J; ++i) {
+      const uint64_t v = c[i] < prev ? c[i] : 0ull;
+      b = v > b ? v : b;
+    }
+    uint64_t best = wave_max_key(b);
+    if (best < floor) best = floor;
+    if ((threadIdx.x & 63) == 0) out[rank] = best;
+    prev = best;
+  }
+}
+
+template <int J>
+__device__ __forceinline__ void rank_from(const uint64_t *scratch, int count, int k, uint64_t *out) {
+  const int lane = threadIdx.x & 63;
+  uint64_t c[J];
+#pragma unroll
+  for (int i = 0; i < J; ++i) c[i] = i * 64 + lane < count ? scratch[i * 64 + lane] : 0ull;
+  rank_rounds<J>(c, k, out);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_key(uint64_t v, int m) {
+  const int lo = __shfl_xor(int(uint32_t(v)), m), hi = __shfl_xor(int(uint32_t(v >> 32)), m);
+  return (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo);
+}
+
+// Sorts the wave's 64*J keys (element j*64 + lane in c[j]) into descending
+// order with a bitonic network, then writes ranks 0..k-1 (keys at or below the
+// floor become the floor).
+template <int J>
+__device__ __forceinline__ void sort_from(const uint64_t *scratch, int count, int k, uint64_t *out) {
+  const int lane = threadIdx.x & 63;
+  uint64_t c[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) c[j] = j * 64 + lane < count ? scratch[j * 64 + lane] : 0ull;
+#pragma unroll
+  for (int size = 2; size <= 64 * J; size <<= 1) {
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride >>= 1) {
+      if (stride >= 64) {
+        const int rs = stride / 64;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          if ((j & rs) == 0) {
+            const int e = j * 64 + lane;
+            const bool desc = (e & size) == 0;
+            const uint64_t a = c[j], b = c[j | rs];
+            const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+            c[j] = desc ? hi : lo;
+            c[j | rs] = desc ? lo : hi;
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const int e = j * 64 + lane;
+          const uint64_t other = shfl_xor_key(c[j], stride);
+          const bool desc = (e & size) == 0, first = (lane & stride) == 0;
+          const uint64_t hi = c[j] > other ? c[j] : other, lo = c[j] > other ? other : c[j];
+          c[j] = (first == desc) ? hi : lo;
+        }
+      }
+    }
+  }
+  const uint64_t floor = floor_key();
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int e = j * 64 + lane;
+    if (e < k) out[e] = c[j] > floor ? c[j] : floor;
+  }
+  if (lane == 0)
+    for (int e = 64 * J; e < k; ++e) out[e] = floor;
+}
+
+// Ranked top-k (k <= 64) of the wave's keys, N per lane, into out[0..k)
+// (unfilled ranks get floor_key()).  scratch: 64 * N keys of LDS.
+template <int N>
+__device__ __forceinline__ void wave_topk(const uint64_t (&key)[N], int k, uint64_t *scratch, uint64_t *out) {
+  const int lane = threadIdx.x & 63;
+  if (k <= 2) {  // a round or two of the wave-wide maximum beats filtering
+    rank_rounds<N>(key, k, out);
+    return;
+  }
+  // Threshold: the largest T with at least k half-lane maxima whose score
+  // bits reach T; every key of the top-k has score bits >= T.
+  uint32_t hm0 = 0, hm1 = 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const uint32_t h = uint32_t(key[i] >> 32);
+    if (i < (N + 1) / 2) hm0 = max(hm0, h);
+    else hm1 = max(hm1, h);
+  }
+  uint32_t t = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t c = t | (1u << bit);
+    const int n = __popcll(__ballot(hm0 >= c)) + (N > 1 ? __popcll(__ballot(hm1 >= c)) : 0);
+    if (n >= k) t = c;
+  }
+  // Compact the keys that reach it.
+  int count = 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const bool keep = key[i] != 0ull && uint32_t(key[i] >> 32) >= t;
+    const uint64_t mask = __ballot(keep);
+    if (keep) scratch[count + __popcll(mask & ((1ull << lane) - 1ull))] = key[i];
+    count += __popcll(mask);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // Few survivors (the usual case): sort them.  Many (ties, flat logits):
+  // k rounds of the wave-wide maximum.
+  const int per_lane = (count + 63) / 64;
+  if (per_lane <= 1)
+    sort_from<1>(scratch, count, k, out);
+  else if (per_lane <= 2)
+    sort_from<2>(scratch, count, k, out);
+  else if (per_lane <= 4 || N <= 4)
+    sort_from<(N < 4 ? N : 4)>(scratch, count, k, out);
+  else if (per_lane <= 8 || N <= 8)
+    rank_from<(N < 8 ? N : 8)>(scratch, count, k, out);
+  else
+    rank_from<N>(scratch, count, k, out);
 }
 
 struct SampleArgs {
@@ -433,92 +609,53 @@ struct SampleArgs {
   float temperature, top_p, penalty, uniform;
 };
 
-// k rounds over the lane's items: each round's pick is the wave-wide best
-// item ranked after the previous pick; lane 0 appends it to out_s / out_i.
-template <int N>
-__device__ __forceinline__ void wave_topk(const float (&vs)[N], const unsigned (&vi)[N], int k, float *out_s,
-                                          unsigned *out_i) {
-  const int lane = threadIdx.x & 63;
-  float ps = INFINITY;
-  unsigned pi = 0;
-  for (int rank = 0; rank < k; ++rank) {
-    float bs = kLowest;
-    unsigned bi = kNoToken;
+// The workgroup's ranked top-k of its 4096 keys (16 per lane) into top[0..k).
+__device__ __forceinline__ void group_topk(const uint64_t (&key)[kSamplePerThread], int k, uint64_t *scratch,
+                                           uint64_t (*lists)[64], uint64_t *top) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  wave_topk<kSamplePerThread>(key, k, scratch + wave * 64 * kSamplePerThread, lists[wave]);
+  __syncthreads();
+  if (wave == 0) {
+    uint64_t c4[4];
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-      if (vi[i] != kNoToken && (rank == 0 || ranks_before(ps, pi, vs[i], vi[i])) &&
-          ranks_before(vs[i], vi[i], bs, bi)) {
-        bs = vs[i];
-        bi = vi[i];
-      }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float os = __shfl_xor(bs, off);
-      const unsigned oi = __shfl_xor(bi, off);
-      if (ranks_before(os, oi, bs, bi)) {
-        bs = os;
-        bi = oi;
-      }
-    }
-    if (lane == 0) {
-      out_s[rank] = bs;
-      out_i[rank] = bi;
-    }
-    ps = bs;
-    pi = bi;
+    for (int w = 0; w < 4; ++w) c4[w] = lane < k ? lists[w][lane] : 0ull;
+    wave_topk<4>(c4, k, scratch, top);
   }
+  __syncthreads();
 }
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(unsigned *dst, const float *logits, const unsigned *seen,
-                                                           const float *in_s, const unsigned *in_i, float *out_s,
-                                                           unsigned *out_i, unsigned *counter, SampleArgs a) {
-  __shared__ float ws[4][64];
-  __shared__ unsigned wi[4][64];
-  __shared__ float top_s[64];
-  __shared__ unsigned top_i[64];
+                                                           const uint64_t *in_keys, uint64_t *out_keys,
+                                                           unsigned *counter, SampleArgs a) {
+  __shared__ uint64_t scratch[4 * 64 * kSamplePerThread];
+  __shared__ uint64_t lists[4][64];
+  __shared__ uint64_t top[64];
+  __shared__ float top_w[64];
+  __shared__ unsigned ids[64];
   __shared__ unsigned last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, tile = blockIdx.x;
-  float vs[kSamplePerThread];
-  unsigned vi[kSamplePerThread];
-  // Wave w holds tokens [w*1024, (w+1)*1024) of the tile, lane-strided.
+  uint64_t key[kSamplePerThread];
+  // Wave w holds items [w*1024, (w+1)*1024) of the tile, lane-strided.
 #pragma unroll
   for (int i = 0; i < kSamplePerThread; ++i) {
     const unsigned item = unsigned(tile) * kSampleTile + unsigned(wave) * 1024 + unsigned(i) * 64 + lane;
-    vs[i] = kLowest;
-    vi[i] = kNoToken;
+    key[i] = 0ull;
     if (item < unsigned(a.count)) {
       if (a.level0) {
         const unsigned flag = seen[item];
-        if (flag != kNoToken) {
-          float score = logits[item];
-          if (flag != 0u) score = score < 0.0f ? score * a.penalty : score / a.penalty;
-          vs[i] = score;
-          vi[i] = item;
-        }
+        float score = logits[item];
+        if (flag != 0u) score = score < 0.0f ? score * a.penalty : score / a.penalty;
+        key[i] = flag != kNoToken ? rank_key(score, item) : 0ull;
       } else {
-        vi[i] = __hip_atomic_load(&in_i[item], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        vs[i] = dev::xload(&in_s[item]);
+        key[i] = __hip_atomic_load(&in_keys[item], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
-  wave_topk<kSamplePerThread>(vs, vi, a.k, ws[wave], wi[wave]);
-  __syncthreads();
-  if (wave == 0) {
-    float s4[4];
-    unsigned i4[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      s4[w] = lane < a.k ? ws[w][lane] : kLowest;
-      i4[w] = lane < a.k ? wi[w][lane] : kNoToken;
-    }
-    wave_topk<4>(s4, i4, a.k, top_s, top_i);
-  }
-  __syncthreads();
-  if (tid < a.k) {
-    dev::xstore(&out_s[size_t(tile) * a.k + tid], top_s[tid]);
-    __hip_atomic_store(&out_i[size_t(tile) * a.k + tid], top_i[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  group_topk(key, a.k, scratch, lists, top);
+  if (tid < a.k) __hip_atomic_store(&out_keys[size_t(tile) * a.k + tid], top[tid], __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
   if (!a.merge) return;
-  // One ticket per workgroup once its candidates are stored.
+  // One ticket per workgroup once its keys are stored.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0)
@@ -526,55 +663,43 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(unsigned *dst, const 
   __syncthreads();
   if (!last) return;
 
-  // The last workgroup ranks every tile's candidates (at most 4096).
+  // The last workgroup ranks every tile's keys (at most 4096).
   const int count = a.tiles * a.k;
 #pragma unroll
   for (int i = 0; i < kSamplePerThread; ++i) {
     const int c = wave * 1024 + i * 64 + lane;
-    vs[i] = kLowest;
-    vi[i] = kNoToken;
-    if (c < count) {
-      vi[i] = __hip_atomic_load(&out_i[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      vs[i] = dev::xload(&out_s[c]);
-    }
+    key[i] = c < count ? __hip_atomic_load(&out_keys[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
   }
-  __syncthreads();
-  wave_topk<kSamplePerThread>(vs, vi, a.k, ws[wave], wi[wave]);
-  __syncthreads();
-  if (wave == 0) {
-    float s4[4];
-    unsigned i4[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      s4[w] = lane < a.k ? ws[w][lane] : kLowest;
-      i4[w] = lane < a.k ? wi[w][lane] : kNoToken;
-    }
-    wave_topk<4>(s4, i4, a.k, top_s, top_i);
-  }
-  __syncthreads();
+  group_topk(key, a.k, scratch, lists, top);
   if (tid == 0) {
 #pragma clang fp contract(off)
-    unsigned selected = top_i[0];
+    const uint64_t floor = floor_key();
+    for (int j = 0; j < a.k; ++j) {
+      const bool none = top[j] <= floor;
+      top_w[j] = none ? kLowest : from_order_bits(uint32_t(top[j] >> 32));
+      ids[j] = none ? kNoToken : ~uint32_t(top[j]);
+    }
+    unsigned selected = ids[0];
     if (a.temperature > 0.0f && a.k > 1) {
       float total = 0.0f;
-      const float maximum = top_s[0];
+      const float maximum = top_w[0];
       for (int j = 0; j < a.k; ++j) {
-        top_s[j] = expf((top_s[j] - maximum) / a.temperature);
-        total += top_s[j];
+        top_w[j] = expf((top_w[j] - maximum) / a.temperature);
+        total += top_w[j];
       }
       float retained = 0.0f;
       int n = 0;
       do {
-        retained += top_s[n];
+        retained += top_w[n];
         ++n;
       } while (n < a.k && retained < a.top_p * total);
       const float target = a.uniform * retained;
       float accumulated = 0.0f;
-      selected = top_i[n - 1];
+      selected = ids[n - 1];
       for (int j = 0; j < n; ++j) {
-        accumulated += top_s[j];
+        accumulated += top_w[j];
         if (target < accumulated) {
-          selected = top_i[j];
+          selected = ids[j];
           break;
         }
       }
@@ -617,10 +742,10 @@ AttnPlan attn_plan(int rows, int heads, int kv_heads, int dim, int position, int
   const int wgs = kv_heads * (group / p.gb) * rows;
   const int last_end = position + rows;
   const int longest = window > 0 ? std::min(window, last_end) : last_end;
-  // About one workgroup per CU, chunks of at least 128 keys (the chunk
-  // partials' merge reads splits * heads * dim floats).
-  const int target = env_int("QNN_ATTN_WGS", 256);
-  const int min_chunk = env_int("QNN_ATTN_MIN_CHUNK", 128);
+  // About two workgroups per CU, chunks of at least 64 keys (measured on
+  // MI355X: 512 / 64 beat 256 / 128 and 128 / 256 at 4k and 32k keys).
+  const int target = env_int("QNN_ATTN_WGS", 512);
+  const int min_chunk = std::max(64, env_int("QNN_ATTN_MIN_CHUNK", 64)) / 64 * 64;
   int splits = std::max(1, std::min((target + wgs - 1) / wgs, (longest + min_chunk - 1) / min_chunk));
   splits = std::min(splits, kMergeMaxSplits);
   p.chunk = ((longest + splits - 1) / splits + 63) / 64 * 64;
@@ -687,7 +812,7 @@ size_t sample_workspace_floats(int vocab, int k) {
   size_t total = 0;
   for (int count = vocab;;) {
     const int tiles = (count + kSampleTile - 1) / kSampleTile;
-    total += 2 * size_t(tiles) * k;
+    total += 2 * size_t(tiles) * k;  // 64-bit keys
     if (size_t(tiles) * k <= size_t(kSampleTile)) break;
     count = tiles * k;
   }
@@ -696,22 +821,18 @@ size_t sample_workspace_floats(int vocab, int k) {
 
 void sample_launch(float *dst, const float *logits, const float *seen, float *ws, unsigned *counter, int vocab, int k,
                    float temperature, float top_p, float penalty, float uniform, hipStream_t s) {
-  const float *in_s = nullptr;
-  const unsigned *in_i = nullptr;
+  const uint64_t *in_keys = nullptr;
+  uint64_t *keys = reinterpret_cast<uint64_t *>(ws);
   int count = vocab, level0 = 1;
   for (;;) {
     const int tiles = (count + kSampleTile - 1) / kSampleTile;
     const int merge = size_t(tiles) * k <= size_t(kSampleTile) ? 1 : 0;
-    float *out_s = ws;
-    unsigned *out_i = reinterpret_cast<unsigned *>(ws + size_t(tiles) * k);
     SampleArgs a{count, k, tiles, level0, merge, temperature, top_p, penalty, uniform};
     k_sample<<<tiles, kSampleThreads, 0, s>>>(reinterpret_cast<unsigned *>(dst), logits,
-                                              reinterpret_cast<const unsigned *>(seen), in_s, in_i, out_s, out_i,
-                                              counter, a);
+                                              reinterpret_cast<const unsigned *>(seen), in_keys, keys, counter, a);
     if (merge) break;
-    in_s = out_s;
-    in_i = out_i;
-    ws += 2 * size_t(tiles) * k;
+    in_keys = keys;
+    keys += size_t(tiles) * k;
     count = tiles * k;
     level0 = 0;
   }
