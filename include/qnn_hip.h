@@ -331,6 +331,14 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
 int qnn_kernel_weights(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, const qnn_weight *b,
                        const qnn_weight *c, const int *args, int nargs);
 
+/* Gather (Context.API.inc:147-151, Implementation.inc:1228-1267; tensor.comp:245-251):
+ * dst[r][j] = row ids[r] (token id as raw bits) of the [vocab, dim] table w,
+ * column j; 0 for ids at or past vocab.  w: F32, BF16, a packed GGUF
+ * encoding, or S8 with `scales` = F32 [vocab] per-row scales.  rotation != 0
+ * (ConvRot) -> QNN_E_NOT_SUPPORTED. */
+int qnn_gather(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *ids, const qnn_weight *w, const qnn_weight *scales, int rows,
+               int dim, int vocab, int rotation);
+
 /* CachedAttention (Context.API.inc:142-146, Implementation.inc:1189-1226;
  * attention.comp): for query row r at absolute position position + r, softmax
  * attention over cache keys [start, position + r], start = end - window when

@@ -446,12 +446,12 @@ WeightEntry *acquire_gguf(qnn_ctx_s *ctx, const qnn_weight *w, int rows, int col
 }
 
 // F32/BF16 vector (norm gamma, bias) copied as is.
-WeightEntry *acquire_raw(qnn_ctx_s *ctx, const qnn_weight *w, int64_t count) {
+WeightEntry *acquire_raw(qnn_ctx_s *ctx, const qnn_weight *w, int64_t count, bool allow_s8 = false) {
   check_weight_desc(w);
-  if ((w->dtype != QNN_DT_F32 && w->dtype != QNN_DT_BF16) || w->encoding != QNN_WE_NATIVE || w->offset < 0 ||
-      count > w->size - w->offset)
+  if ((w->dtype != QNN_DT_F32 && w->dtype != QNN_DT_BF16 && !(allow_s8 && w->dtype == QNN_DT_S8)) ||
+      w->encoding != QNN_WE_NATIVE || w->offset < 0 || count > w->size - w->offset)
     fail(QNN_E_ARGUMENT, "vector weight must be F32 or BF16 with enough elements");
-  const int es = w->dtype == QNN_DT_F32 ? 4 : 2;
+  const int es = w->dtype == QNN_DT_F32 ? 4 : w->dtype == QNN_DT_BF16 ? 2 : 1;
   const uint64_t bytes = uint64_t(count) * es;
   const std::string key = weight_key("raw", w, bytes);
   if (auto *e = lookup(ctx, key)) return e;
@@ -1945,6 +1945,38 @@ int qnn_kernel_weights(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor 
       bbf = be->raw_dtype == QNN_DT_BF16;
     }
     misc_norm(dst->ptr, a->ptr, gp, gbf, bp, bbf, rows, dim, flags, soff, unit, eps, ctx->stream);
+    return QNN_OK;
+  });
+}
+
+int qnn_gather(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *ids, const qnn_weight *w, const qnn_weight *scales, int rows,
+               int dim, int vocab, int rotation) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (rows < 1 || dim < 1 || vocab < 1) fail(QNN_E_ARGUMENT, "Gather geometry");
+    check_tensor(ctx, dst, int64_t(rows) * dim);
+    check_tensor(ctx, ids, rows);
+    if (!w) fail(QNN_E_ARGUMENT, "Gather weight");
+    if (rotation != 0) fail(QNN_E_NOT_SUPPORTED, "ConvRot weights are not handled by the HIP backend");
+    OpPins pin;
+    if (is_gguf(w->encoding)) {
+      WeightEntry *e = pin(acquire_gguf(ctx, w, vocab, dim));
+      gguf_gather_launch(e->gg, e->dptr, ids->ptr, dst->ptr, rows, vocab, ctx->stream);
+      return QNN_OK;
+    }
+    if (w->dtype == QNN_DT_S8) {
+      // Int8 rows with one F32 scale per row (AcquireInt8Weight).
+      if (!scales) fail(QNN_E_ARGUMENT, "Gather: int8 rows need their scales");
+      WeightEntry *e = pin(acquire_raw(ctx, w, int64_t(vocab) * dim, true));
+      WeightEntry *sc = pin(acquire_raw(ctx, scales, vocab));
+      if (sc->raw_dtype != QNN_DT_F32) fail(QNN_E_ARGUMENT, "Gather: int8 row scales must be F32");
+      decode_gather(dst->ptr, ids->ptr, e->dptr, 2, static_cast<const float *>(sc->dptr), rows, dim, vocab,
+                    ctx->stream);
+      return QNN_OK;
+    }
+    WeightEntry *e = pin(acquire_raw(ctx, w, int64_t(vocab) * dim));
+    decode_gather(dst->ptr, ids->ptr, e->dptr, e->raw_dtype == QNN_DT_BF16 ? 1 : 0, nullptr, rows, dim, vocab,
+                  ctx->stream);
     return QNN_OK;
   });
 }

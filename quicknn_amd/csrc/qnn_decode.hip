@@ -74,6 +74,30 @@ __global__ void k_softcap(float *dst, const float *src, int n, float cap) {
   if (id < n) dst[id] = cap * tanhf(fminf(fmaxf(src[id] / cap, -20.0f), 20.0f));
 }
 
+// Gather (Context.Implementation.inc:1228-1267; tensor.comp:245-251): rows
+// of an F32, BF16 or int8 (times a per-row F32 scale) table by token id (raw
+// bits); ids at or past the vocabulary give zeros.
+__global__ void k_gather(float *out, const unsigned *ids, const void *w, int kind, const float *scales, int n, int dim,
+                         int vocab) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= n) return;
+  const int r = id / dim, j = id % dim;
+  const unsigned token = ids[r];
+  if (token >= unsigned(vocab)) {
+    out[id] = 0.0f;
+    return;
+  }
+  const size_t index = size_t(token) * dim + j;
+  float x;
+  if (kind == 1)
+    x = __uint_as_float(uint32_t(static_cast<const uint16_t *>(w)[index]) << 16);
+  else if (kind == 2)
+    x = float(static_cast<const int8_t *>(w)[index]) * scales[token];
+  else
+    x = static_cast<const float *>(w)[index];
+  out[id] = x;
+}
+
 // ---------------------------------------------------------------------------
 // Cached attention (attention.comp, the online path the resident context
 // dispatches with mask mode 2, or 4 with a per-row key mask).
@@ -725,6 +749,13 @@ void decode_cache_write(float *cache, const float *k, const float *v, int n, int
 void decode_seen(float *flags, const float *ids, int n, int vocab, hipStream_t s) {
   k_seen<<<grid_of(n, 256), 256, 0, s>>>(reinterpret_cast<unsigned *>(flags), reinterpret_cast<const unsigned *>(ids),
                                          n, unsigned(vocab));
+}
+
+void decode_gather(float *dst, const float *ids, const void *w, int kind, const float *scales, int rows, int dim,
+                   int vocab, hipStream_t s) {
+  const int n = rows * dim;
+  k_gather<<<grid_of(n, 256), 256, 0, s>>>(dst, reinterpret_cast<const unsigned *>(ids), w, kind, scales, n, dim,
+                                           vocab);
 }
 
 void decode_scale(float *dst, const float *src, int n, float a, float b, hipStream_t s) {

@@ -191,6 +191,23 @@ __global__ void k_gguf_dequant(GGLayout l, const uint8_t *__restrict__ w, float 
   out[idx] = gguf_value_tiled(l.enc, l, p, row / 64, k / 256, row & 63, k % 256);
 }
 
+// Gather (Context.Implementation.inc:1228-1267, tensor.comp:245-251 with a
+// GGUF weight): out[r][k] = value of row ids[r] (raw token bits) column k, or 0
+// for ids at or past the vocabulary.
+__global__ void k_gguf_gather(GGLayout l, const uint8_t *__restrict__ w, const unsigned *__restrict__ ids,
+                              float *__restrict__ out, int rows, int vocab) {
+  const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= size_t(rows) * l.cols) return;
+  const int r = int(idx / l.cols), k = int(idx % l.cols);
+  const unsigned token = ids[r];
+  if (token >= unsigned(vocab)) {
+    out[idx] = 0.0f;
+    return;
+  }
+  const Planes p = planes_of(l, w);
+  out[idx] = gguf_value_tiled(l.enc, l, p, int(token / 64), k / 256, int(token & 63), k % 256);
+}
+
 // ---------------------------------------------------------------- matvec
 // Fixed-point activation slice of one token, in LDS: per 32-group 8 words of
 // q1 and q2 bytes (element order), s2, and the sums of X = 256 q1 + q2 over
@@ -622,6 +639,14 @@ void gguf_dequant_launch(const GGLayout &l, const void *w, float *out, hipStream
   hipLaunchKernelGGL(k_gguf_dequant, dim3((total + 255) / 256), dim3(256), 0, s, l,
                      static_cast<const uint8_t *>(w), out);
   hip_check(hipGetLastError(), "gguf dequant launch");
+}
+
+void gguf_gather_launch(const GGLayout &l, const void *w, const float *ids, float *out, int rows, int vocab,
+                        hipStream_t s) {
+  const size_t total = size_t(rows) * l.cols;
+  hipLaunchKernelGGL(k_gguf_gather, dim3((total + 255) / 256), dim3(256), 0, s, l, static_cast<const uint8_t *>(w),
+                     reinterpret_cast<const unsigned *>(ids), out, rows, vocab);
+  hip_check(hipGetLastError(), "gguf gather launch");
 }
 
 void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {

@@ -166,6 +166,11 @@ void decode_cache_write(float *cache, const float *k, const float *v, int n, int
                         int position, hipStream_t s);
 void decode_seen(float *flags, const float *ids, int n, int vocab, hipStream_t s);
 void decode_scale(float *dst, const float *src, int n, float a, float b, hipStream_t s);
+// kind: 0 F32, 1 BF16, 2 int8 with per-row F32 scales.
+void decode_gather(float *dst, const float *ids, const void *w, int kind, const float *scales, int rows, int dim,
+                   int vocab, hipStream_t s);
+void gguf_gather_launch(const GGLayout &l, const void *w, const float *ids, float *out, int rows, int vocab,
+                        hipStream_t s);
 void decode_softcap(float *dst, const float *src, int n, float cap, hipStream_t s);
 // Cached attention: query heads per workgroup (gb), key chunks (splits) and
 // the chunk partials' workspace in floats (0 when one chunk covers the keys).

@@ -150,6 +150,7 @@ def lib():
             "qnn_check_finite": (ctypes.c_int, [_vp, _vp, ctypes.c_int]),
             "qnn_cached_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp] + [ctypes.c_int] * 7 +
                                      [ctypes.c_float, ctypes.c_float, ctypes.c_int]),
+            "qnn_gather": (ctypes.c_int, [_vp, _vp, _vp, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
             "qnn_sample_token": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int] +
                                  [ctypes.c_float] * 4),
             "qnn_expert_set_create": (ctypes.c_int, [_vp, W, W, W, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -204,7 +205,7 @@ EXPORTED = (
     "qnn_prefetch_weights", "qnn_stage_weight_prefetch", "qnn_complete_weight_prefetch",
     "qnn_activate_prefetched_weights", "qnn_seal_weight_prefetch", "qnn_end_weight_prefetch", "qnn_upload", "qnn_vector_linear", "qnn_linear", "qnn_q8_gemm_int8", "qnn_int4_linear", "qnn_int4_linear_noalloc", "qnn_swiglu_vector",
     "qnn_int4_linear_accumulate", "qnn_kernel", "qnn_kernel_weights", "qnn_check_finite",
-    "qnn_cached_attention", "qnn_sample_token",
+    "qnn_cached_attention", "qnn_sample_token", "qnn_gather",
     "qnn_expert_set_create", "qnn_expert_set_destroy", "qnn_moe_experts", "qnn_dequantize",
     "qnn_event_record", "qnn_event_elapsed_ms", "qnn_graph_begin", "qnn_graph_end", "qnn_graph_launch",
     "qnn_stream", "qnn_int4_row_bytes", "qnn_quantize_int4", "qnn_gguf_quantize",
@@ -556,6 +557,11 @@ class GPUContext:
         """CachedAttention (Context.API.inc:142-146)."""
         _raise(lib().qnn_cached_attention(self.h, dst.handle, q.handle, cache.handle, query_rows, capacity, heads,
                                           kv_heads, dim, position, window, softcap, scale, int(masked)))
+
+    def Gather(self, dst: Tensor, ids: Tensor, weight: MemoryBlock, scales: MemoryBlock | None, rows: int, dim: int,
+               vocab: int, rotation: int = 0) -> None:
+        """Gather (Context.API.inc:147-151): embedding rows by token id."""
+        _raise(lib().qnn_gather(self.h, dst.handle, ids.handle, _wd(weight), _wd(scales), rows, dim, vocab, rotation))
 
     def SampleToken(self, dst: Tensor, logits: Tensor, seen: Tensor, vocab: int, top_k: int, temperature: float,
                     top_p: float, penalty: float, uniform: float) -> None:

@@ -259,3 +259,39 @@ def test_sampling_excluded_tokens_and_errors(ctx):
         ctx.SampleToken(tl, tl, ts, vocab, 10, 1.0, 1.0, 1.0, 0.5)
     for z in (tl, ts, td):
         ctx.Recycle(z)
+
+
+# ---------------------------------------------------------------- gather
+@pytest.mark.parametrize("kind", ["f32", "bf16", "s8", "q4_k", "q6_k", "q8_0"])
+def test_gather_embedding_rows(ctx, rng, kind):
+    """Gather: token rows of the table, bit-exact; ids at or past the vocabulary give zeros."""
+    vocab, dim = 1000, 512
+    table = (rng.standard_normal((vocab, dim)) * 0.05).astype(np.float32)
+    scales = None
+    if kind == "f32":
+        w, rows_f = hip.MemoryBlock.matrix(table), table
+    elif kind == "bf16":
+        bits = (table.view(np.uint32) >> 16).astype(np.uint16)
+        w, rows_f = hip.MemoryBlock.matrix(bits), (bits.astype(np.uint32) << 16).view(np.float32)
+    elif kind == "s8":
+        q = rng.integers(-127, 128, (vocab, dim)).astype(np.int8)
+        s = (rng.random(vocab) * 0.01).astype(np.float32)
+        w = hip.MemoryBlock(q, q.shape, hip.DT_S8)
+        scales = hip.MemoryBlock.vector(s)
+        rows_f = q.astype(np.float32) * s[:, None]
+    else:
+        enc = {"q4_k": hip.WE_Q4_K, "q6_k": hip.WE_Q6_K, "q8_0": hip.WE_Q8_0}[kind]
+        blocks = hip.gguf_quantize(enc, table)
+        w = hip.MemoryBlock.gguf(blocks, vocab, dim, enc)
+        rows_f = oracle.gguf_dequant_scalar(blocks, enc, vocab * dim).reshape(vocab, dim)
+    ids = np.array([0, 999, 5, 1000, 123, 0xFFFFFFFF, 5], np.uint32)
+    ti, td = up(ctx, ids), ctx.NewTensor(ids.size * dim)
+    ctx.Gather(td, ti, w, scales, ids.size, dim, vocab)
+    got = ctx.Download(td).reshape(ids.size, dim)
+    for r, t in enumerate(ids):
+        want = rows_f[t] if t < vocab else np.zeros(dim, np.float32)
+        assert np.array_equal(got[r], want), (kind, r)
+    with pytest.raises(hip.ENotSupportedException):
+        ctx.Gather(td, ti, w, scales, ids.size, dim, vocab, 1)
+    ctx.Recycle(ti)
+    ctx.Recycle(td)
