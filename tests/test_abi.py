@@ -58,3 +58,39 @@ def test_no_device_is_reported_not_faked():
         pytest.skip("a GPU is visible")
     with pytest.raises(hip.ENotSupportedException):
         hip.GPUContext(0)
+
+
+def pascal_externals() -> dict[str, int]:
+    """Name -> parameter count of every `external QNN_LIB` routine in the Pascal unit."""
+    text = open(os.path.join(ROOT, "src/backends/hip/QuickNN.HIP.pas")).read()
+    out = {}
+    for m in re.finditer(r"(?:function|procedure)\s+(qnn_\w+)\s*(\((.*?)\))?[^;]*;\s*cdecl;\s*external QNN_LIB;",
+                         text, flags=re.S):
+        params = m.group(3) or ""
+        names = 0
+        for group in params.split(";"):
+            if ":" in group:
+                names += len(group.split(":")[0].replace("out ", "").replace("var ", "").replace("const ", "")
+                             .split(","))
+        out[m.group(1)] = names
+    return out
+
+
+def c_param_counts() -> dict[str, int]:
+    text = open(os.path.join(ROOT, "include/qnn_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^(?:int|void \*|const char \*|uint64_t)\s*(qnn_\w+)\(([^;]*)\);", text, flags=re.M):
+        args = " ".join(m.group(2).split())
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_pascal_unit_binds_every_entry_point():
+    """src/backends/hip/QuickNN.HIP.pas declares each C entry point with the same parameter count."""
+    pas, c = pascal_externals(), c_param_counts()
+    assert set(c) == declared("include/qnn_hip.h", "qnn_")
+    missing = sorted(set(c) - set(pas))
+    assert not missing, missing
+    wrong = {n: (pas[n], c[n]) for n in c if pas[n] != c[n]}
+    assert not wrong, wrong
