@@ -21,14 +21,16 @@ runs of it); batch-8 figures; and the reference's CPU SIMD path (an AVX2
 restatement in the CPU oracle) timed on this host on the same packed weights.
 
 The other workloads of the benchmark definition are measured with
-`--config 1|3|4|5` (one JSON line each, same fields), and the default run
+`--config 1|3|4|5|6` (one JSON line each, same fields), and the default run
 also times each of them briefly and reports them under `other_configs`:
   1  one INT4 matvec 6144x2048 (Qwen3-1.7B gate shape), batch 1;
   3  Gemma-2-9B-shaped GGUF K-quant decode layer (Q4_K q/o, Q3_K k/v, Q2_K
      gate/up + GEGLU, Q6_K down) and the Q6_K output head;
   4  Qwen3-30B-A3B-shaped MoE expert layer (128 INT4 experts, top-8) at batch
      1 and 16, routed on the device;
-  5  Q8_0 prefill GEMM 512x3072x12288.
+  5  Q8_0 prefill GEMM 512x3072x12288;
+  6  the rest of the decode layer at the Qwen3-4B shape: cached attention
+     over 4096 and 32768 keys, token sampling over 151936 tokens, RoPE.
 Each rotates over enough distinct weight copies (> 256 MB) that the weights
 come from HBM, not from the MALL.
 """
@@ -636,12 +638,104 @@ def run_cfg5(args, hip) -> dict:
         cpu_baseline=cpu)
 
 
+# ---------------------------------------------------------------------------
+# cfg6: the rest of the decode layer (cached attention, sampling, RoPE)
+# ---------------------------------------------------------------------------
+def run_cfg6(args, hip) -> dict:
+    """Decode-layer ops around the quantized matvecs, at the Qwen3-4B shape
+    (32 query heads, 8 KV heads, head dim 128, vocabulary 151936):
+    CachedAttention for one query row over 4096 keys (one cache per layer,
+    36 layers: 1.21 GB, so the caches come from HBM) and over 32768 keys
+    (4 caches of 268 MB), SampleToken (top-k 1 and 40) and GO_LLM_ROPE on
+    the query heads.  value = K and V bytes read per 4096-key call over its
+    average time."""
+    heads, kvh, dim, vocab = 32, 8, 128, 151936
+    rng = np.random.default_rng(23)
+    ctx = hip.GPUContext(0)
+
+    def cache_set(keys, count):
+        one = rng.standard_normal(2 * keys * kvh * dim).astype(np.float32)
+        return [ctx.UploadRaw(one) for _ in range(count)]
+
+    def attn_us(keys, caches):
+        def step():
+            for c in caches:
+                ctx.CachedAttention(o, q, c, 1, keys, heads, kvh, dim, keys - 1)
+        for _ in range(max(1, args.warmup)):
+            step()
+        return timed_ms(ctx, step, args.steps) * 1000 / len(caches)
+
+    q = ctx.UploadRaw(rng.standard_normal(heads * dim).astype(np.float32))
+    o = ctx.NewTensor(heads * dim)
+    t0 = time.perf_counter()
+    caches = cache_set(4096, LAYERS)
+    us4k = attn_us(4096, caches)
+    for c in caches:
+        ctx.Recycle(c)
+    caches = cache_set(32768, 4)
+    us32k = attn_us(32768, caches)
+    for c in caches:
+        ctx.Recycle(c)
+    gen_s = time.perf_counter() - t0
+    bytes4k = 2 * 4096 * kvh * dim * 4
+    bytes32k = 2 * 32768 * kvh * dim * 4
+    gbs = bytes4k / (us4k * 1e-6) / 1e9
+
+    logits = ctx.UploadRaw(rng.standard_normal(vocab).astype(np.float32))
+    seen = ctx.UploadRaw(np.zeros(vocab, np.float32))
+    tok = ctx.NewTensor(1)
+    sample = {}
+    for k, temp in ((1, 0.0), (40, 0.7)):
+        def s_step(k=k, temp=temp):
+            ctx.SampleToken(tok, logits, seen, vocab, k, temp, 0.9, 1.1, 0.5)
+        for _ in range(max(1, args.warmup)):
+            s_step()
+        sample[f"top_k_{k}_us"] = round(timed_ms(ctx, s_step, args.steps * 4) * 1000, 2)
+
+    def r_step():
+        ctx.Kernel(hip.GO_LLM_ROPE, heads * dim // 2, q, q, None, None, [heads, dim, 4000, hip.float_bits(1e6)])
+    for _ in range(max(1, args.warmup)):
+        r_step()
+    rope_us = timed_ms(ctx, r_step, args.steps * 4) * 1000
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        qh = rng.standard_normal(heads * dim).astype(np.float32)
+        ch = rng.standard_normal(2 * 4096 * kvh * dim).astype(np.float32)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds or n < 2:
+            oracle.cached_attention(qh, ch, 1, 4096, heads, kvh, dim, 4095)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu = {"value": round(bytes4k * n / el / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+               "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+               "sample": f"{n} CachedAttention calls over 4096 keys, the oracle's scalar restatement "
+                         f"in double ({el:.1f} s)"}
+    return base_line(
+        args, "cached attention GB/s (K and V read once), Qwen3-4B shape, 4096 keys", gbs, "GB/s", us4k / 1000,
+        "f32", "synthetic (N(0,1) queries and caches); one cache per layer, 36 layers",
+        {"workload": "decode-layer ops: CachedAttention 32x8 heads dim 128 over 4096 and 32768 keys, "
+                     "SampleToken over 151936 tokens, GO_LLM_ROPE", "global_batch": 1},
+        attention_32k={"us": round(us32k, 2), "GBps": round(bytes32k / (us32k * 1e-6) / 1e9, 1),
+                       "frac_of_hbm_peak": round(bytes32k / (us32k * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        sample=sample, rope_us=round(rope_us, 2), setup_s=round(gen_s, 1),
+        roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                  "kernel": "k_attn + k_attn_merge (one qnn_cached_attention call)",
+                  "kernel_us": round(us4k, 2), "bytes_per_launch": bytes4k,
+                  "timing": f"HIP events around {args.steps}x{LAYERS} calls"},
+        cpu_baseline=cpu)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true", help="config 2 only: skip the other configs' summaries")
@@ -653,7 +747,7 @@ def main() -> int:
 
     from quicknn_amd import hip
 
-    runs = {1: run_cfg1, 2: run_cfg2, 3: run_cfg3, 4: run_cfg4, 5: run_cfg5}
+    runs = {1: run_cfg1, 2: run_cfg2, 3: run_cfg3, 4: run_cfg4, 5: run_cfg5, 6: run_cfg6}
     line = runs[args.config](args, hip)
     if args.config == 2 and not args.no_others:
         # The other workloads of the benchmark definition, in the same run (so
@@ -661,7 +755,7 @@ def main() -> int:
         sub = argparse.Namespace(**vars(args))
         sub.steps, sub.warmup, sub.no_cpu = max(5, args.steps // 5), 2, True
         others = {}
-        for c in (1, 3, 4, 5):
+        for c in (1, 3, 4, 5, 6):
             t0 = time.perf_counter()
             r = runs[c](sub, hip)
             rf = r["roofline"]
@@ -670,7 +764,8 @@ def main() -> int:
                 "dtype": r["dtype"], "kernel": rf["kernel"], "kernel_us": rf["kernel_us"],
                 "roofline_frac": rf["frac"], "roofline_bound": rf["bound"], "roofline_peak": rf["peak"],
                 **{k: r[k] for k in ("us_per_matvec", "us_per_layer", "us_per_gemm", "head", "batch16", "per_op",
-                                     "route_plus_experts_us", "hbm_GBps", "fp16_linear") if k in r},
+                                     "route_plus_experts_us", "hbm_GBps", "fp16_linear", "attention_32k", "sample",
+                                     "rope_us") if k in r},
                 "steps": sub.steps, "wall_s": round(time.perf_counter() - t0, 1)}
         line["other_configs"] = others
     print(json.dumps(line))

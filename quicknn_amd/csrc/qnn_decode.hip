@@ -181,9 +181,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
   const float *vb = cache + size_t(a.cap) * width + size_t(kh) * a.cap * a.dim;
   const unsigned *mask = reinterpret_cast<const unsigned *>(cache + 2 * size_t(a.cap) * width) + size_t(r) * a.cap;
 
-  for (int i = tid; i < GB * a.dim; i += kAttnThreads) {
-    const int g = i / a.dim, d = i % a.dim;
-    qs[i] = q[(size_t(r) * a.heads + h0 + g) * a.dim + d];
+  // q rows of the batch: GB * dim <= 8 * 1152 floats, at most 36 per thread,
+  // loaded before any is stored so they are in flight together.
+  {
+    constexpr int QMAX = (GB * 1152 + kAttnThreads - 1) / kAttnThreads;
+    float qv[QMAX];
+#pragma unroll
+    for (int u = 0; u < QMAX; ++u) {
+      const int i = tid + u * kAttnThreads;
+      qv[u] = i < GB * a.dim ? q[(size_t(r) * a.heads + h0 + i / a.dim) * a.dim + i % a.dim] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < QMAX; ++u) {
+      const int i = tid + u * kAttnThreads;
+      if (i < GB * a.dim) qs[i] = qv[u];
+    }
   }
   __syncthreads();
 
@@ -201,8 +213,26 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
   const int dp = (a.dim + a.parts - 1) / a.parts, d0 = part * dp, d1 = min(a.dim, d0 + dp);
   const int kk = tid / a.lpk, c4 = tid % a.lpk;  // value pass: key lane, float4 channel group
 
+  constexpr int U = GB * ND4 >= 8 ? 4 : 8;
+  auto load_values = [&](float4 (&vv)[U][ND4], int c0, int nkeys, int key0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = key0 + u * a.kl;
+#pragma unroll
+      for (int i = 0; i < ND4; ++i) {
+        const int cg = c4 + i * a.lpk;
+        vv[u][i] = (kk < a.kl && key < nkeys && i < a.nd4 && cg * 4 < a.dim)
+                       ? load4(vb + size_t(c0 + key) * a.dim, cg * 4, a.dim)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
   for (int c0 = k0; c0 < k1; c0 += a.sub) {
     const int c1 = min(k1, c0 + a.sub);
+    // The first batch of V rows does not depend on the scores: request it
+    // now, so it travels with the K loads below.
+    float4 vfirst[U][ND4];
+    load_values(vfirst, c0, c1 - c0, kk);
     // ---- scores (part of the channels per thread)
     const int j = c0 + key_t;
     bool valid = j < c1 && part < a.parts;
@@ -283,21 +313,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
       }
     }
     // ---- values: lane group kk walks keys kk, kk + kl, ..., U at a time
-    constexpr int U = GB * ND4 >= 8 ? 4 : 8;
     if (kk < a.kl) {
       const int nkeys = c1 - c0;
       for (int key0 = kk; key0 < nkeys; key0 += U * a.kl) {
         float4 vv[U][ND4];
+        if (key0 == kk) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int key = key0 + u * a.kl;
+          for (int u = 0; u < U; ++u)
 #pragma unroll
-          for (int i = 0; i < ND4; ++i) {
-            const int cg = c4 + i * a.lpk;
-            vv[u][i] = (key < nkeys && i < a.nd4 && cg * 4 < a.dim)
-                           ? load4(vb + size_t(c0 + key) * a.dim, cg * 4, a.dim)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-          }
+            for (int i = 0; i < ND4; ++i) vv[u][i] = vfirst[u][i];
+        } else {
+          load_values(vv, c0, nkeys, key0);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
