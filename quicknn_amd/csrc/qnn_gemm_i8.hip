@@ -29,6 +29,14 @@
 // 16 quants of half l / 32 of the block: 512 contiguous bytes per half).  All
 // M-tiles of an N-tile share blockIdx % 8, so they run on one XCD and the
 // weights come from HBM once.
+//
+// VALU economy (the bound): the MFMA results land in VGPRs (this file is
+// built with the VGPR form of MFMA, so no accumulator-register reads), every
+// block-dependent load offset is a scalar offset (no per-block address
+// arithmetic), a block's fp16 weight scale arrives in a 4-byte word (one
+// conversion, selecting the half), and the activation scales reach each lane
+// through LDS.  About 51 VALU instructions per MFMA remain, against the 48
+// of the epilogue itself.
 #include "qnn_internal.h"
 
 namespace qnn {
@@ -42,7 +50,6 @@ __device__ __forceinline__ Rsrc rsrc(const void *base, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(uint32_t(min(bytes, size_t(0xFFFFFFFFu)))),
                                            0x00020000);
 }
-constexpr uint32_t kOutside = 0xFFFFFFF0u;  // a buffer offset past the end: loads return 0
 
 __device__ __forceinline__ float half_to_f(uint32_t h) {
   const uint16_t b = uint16_t(h);
@@ -52,44 +59,37 @@ __device__ __forceinline__ float half_to_f(uint32_t h) {
 }
 
 // ---- K7 ----------------------------------------------------------------------
-// One thread per (row, block): the block's 32 values, its scale and its two
-// 16-byte fragment pieces.  Rows past M (padding to 32) quantise to zeros.
+// Eight lanes per (row, block), four values each; a wave covers 8 consecutive
+// rows of one block, so it reads 8 x 128 contiguous bytes and writes two
+// 128-byte runs of fragment pieces.  The block maximum is exchanged among the
+// eight lanes; each lane packs its 4 quants into one word of the row's piece.
+// Rows past M (padding to 64) quantise to zeros.
 __global__ __launch_bounds__(256) void k_q8_act_quant(const float *__restrict__ a, int M, int K, int m_pad,
-                                                      uint4 *__restrict__ afrag, float *__restrict__ dx) {
+                                                      uint32_t *__restrict__ afrag, float *__restrict__ dx) {
   const int kb_n = K / 32;
   const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (id >= (long long)m_pad * kb_n) return;
-  const int row = int(id / kb_n), kb = int(id % kb_n);
-  float v[32];
-  if (row < M) {
-    const float4 *p = reinterpret_cast<const float4 *>(a + size_t(row) * K + size_t(kb) * 32);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 f = p[i];
-      v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = 0.0f;
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  if (id >= (long long)m_pad * kb_n * 8) return;
+  const int p = int(id & 7);
+  const long long g = id >> 3;  // ((m32 * kb_n + kb) * 32 + r32)
+  const int r32 = int(g & 31);
+  const long long mk = g >> 5;
+  const int kb = int(mk % kb_n), m32 = int(mk / kb_n);
+  const int row = m32 * 32 + r32;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (row < M) v = *reinterpret_cast<const float4 *>(a + size_t(row) * K + size_t(kb) * 32 + 4 * p);
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
   const float d = amax / 127.0f;
   const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-  uint32_t w[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) word |= (uint32_t(int(roundf(v[4 * j + e] * inv))) & 255u) << (8 * e);
-    w[j] = word;
-  }
+  const uint32_t word = (uint32_t(int(roundf(v.x * inv))) & 255u) | (uint32_t(int(roundf(v.y * inv))) & 255u) << 8 |
+                        (uint32_t(int(roundf(v.z * inv))) & 255u) << 16 |
+                        (uint32_t(int(roundf(v.w * inv))) & 255u) << 24;
   // piece (m32, kb, lane): 16 bytes of row m32*32 + lane%32, elements 16*(lane/32) ..
-  const size_t base = (size_t(row >> 5) * kb_n + kb) * 64 + (row & 31);
-  afrag[base] = make_uint4(w[0], w[1], w[2], w[3]);
-  afrag[base + 32] = make_uint4(w[4], w[5], w[6], w[7]);
-  dx[size_t(kb) * m_pad + row] = d;
+  const size_t piece = (size_t(m32) * kb_n + kb) * 64 + r32 + 32 * (p >> 2);
+  afrag[piece * 4 + (p & 3)] = word;
+  if (p == 0) dx[size_t(kb) * m_pad + row] = d;
 }
 
 // ---- K8 ----------------------------------------------------------------------
@@ -102,63 +102,81 @@ struct I8GemmArgs {
   int M, N, m_pad, kb_n, mtiles, ntiles;
 };
 
-constexpr int TM = 64, TN = 128;
+constexpr int TM = 64;
+constexpr int NJ = 2;      // 32-column MFMA tiles per wave (one tile per wave ran 10% slower: more A and
+                           // scale traffic per MFMA outweighs the extra waves)
+constexpr int kDepth = 4;  // blocks of A and B fragments in flight per wave
 
-// This lane's operands for block kb: A fragment, the B fragments and scales of
-// its two column tiles, and the activation scales of its 16 rows.
+// This lane's matrix operands for one block: the A fragment, the B fragments
+// of its NJ column tiles and the 4-byte words holding their fp16 scales (low
+// half for even blocks).
 struct I8Stage {
   v4i a;
-  v4i b[2];
-  float dw[2];
-  float4 dxq[4];
+  v4i b[NJ];
+  uint32_t dw[NJ];
+};
+// Per-lane parts of the buffer offsets; the block-dependent parts are wave
+// uniform and go in the scalar offset.  Every offset stays inside its buffer
+// (columns past the layout are clamped, blocks past the end are clamped by
+// the caller), so no load relies on the range check.
+struct I8Offsets {
+  uint32_t a, b[NJ], d[NJ];
 };
 
-__device__ __forceinline__ void load_stage(I8Stage &s, const I8GemmArgs &g, Rsrc ar, Rsrc wr, Rsrc dr, int m32,
-                                           int n0, int kb, int lane) {
-  const bool in = kb < g.kb_n;
-  {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-        ar, int(in ? uint32_t(((size_t(m32) * g.kb_n + kb) * 64 + lane) * 16) : kOutside), 0, 0);
-    s.a = v4i{int(v[0]), int(v[1]), int(v[2]), int(v[3])};
-  }
-  const int u = kb >> 3, k8 = kb & 7, hi = lane >> 5;
+__device__ __forceinline__ void load_ab(I8Stage &s, Rsrc ar, Rsrc wr, const I8Offsets &o, int kb) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(ar, int(o.a), kb * 1024, 0);
+  s.a = v4i{int(v[0]), int(v[1]), int(v[2]), int(v[3])};
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + 32 * j + (lane & 31);
-    const bool ok = in && n < g.l.tiles * 64;
-    const size_t tu = size_t(n >> 6) * g.l.units + u;
-    const uint32_t qoff = ok ? uint32_t(((tu * 16 + 2 * k8 + hi) * 64 + (n & 63)) * 16) : kOutside;
-    const uint32_t doff = ok ? uint32_t(g.l.side1_off + (tu * 64 + (n & 63)) * 16 + 2 * k8) : kOutside;
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(wr, int(qoff), 0, 0);
-    s.b[j] = v4i{int(v[0]), int(v[1]), int(v[2]), int(v[3])};
-    s.dw[j] = half_to_f(__builtin_amdgcn_raw_buffer_load_b16(wr, int(doff), 0, 0));
-  }
-  // rows 8q + 4*hi + 0..3 of the 32-row block: four consecutive scales
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t off = in ? uint32_t((size_t(kb) * g.m_pad + m32 * 32 + 8 * q + 4 * hi) * 4) : kOutside;
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(dr, int(off), 0, 0);
-    s.dxq[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+  for (int j = 0; j < NJ; ++j) {
+    const auto w = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o.b[j]), kb * 2048, 0);
+    s.b[j] = v4i{int(w[0]), int(w[1]), int(w[2]), int(w[3])};
+    s.dw[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, int(o.d[j]), (kb >> 3) * 1024 + (kb & 6) * 2, 0);
   }
 }
 
-__device__ __forceinline__ void block_step(float (&acc)[2][16], const I8Stage &s) {
+// Activation scales go through LDS, per wave: the wave's 32 rows x kDepth
+// blocks are one 8-byte load per lane, issued a group of blocks ahead and
+// written to the wave's own LDS slot at the top of the group that uses them
+// (a wave's own LDS write and reads stay in order: no barrier).  Each lane
+// then reads its 16 rows per block as 4 x 16 bytes (broadcast within each
+// half-wave).  Held as registers, the same scales would take 16 VGPRs per
+// block in flight.
+static_assert(kDepth == 4, "a group's scales are 32 rows x 4 blocks, two floats per lane");
+
+__device__ __forceinline__ float2 load_scales(Rsrc dr, uint32_t vx, int m_pad, int kb0, int last, int lane) {
+  kb0 = min(kb0, last);
+  const int blk = min(lane >> 4, last - kb0);  // blocks past the end reload the last one (never used)
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(dr, int(vx + uint32_t(blk * m_pad * 4)), kb0 * m_pad * 4, 0);
+  return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+
+__device__ __forceinline__ void block_step(float (&acc)[NJ][16], const I8Stage &s, const float4 *xs, int hi,
+                                           bool odd) {
+  float dw[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(s.a, s.b[j], v16i{}, 0, 0, 0);
+  for (int j = 0; j < NJ; ++j) dw[j] = half_to_f(odd ? s.dw[j] >> 16 : s.dw[j]);
+  v16i d[NJ];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float dq[4] = {s.dxq[q].x, s.dxq[q].y, s.dxq[q].z, s.dxq[q].w};
+  for (int j = 0; j < NJ; ++j) d[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(s.a, s.b[j], v16i{}, 0, 0, 0);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 x = xs[2 * q + hi];  // rows 8q + 4*hi + 0..3 of the wave's 32
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float dq[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 4 * q + r;  // lane holds C[8q + 4*(lane/32) + r][lane%32]
-        acc[j][i] = fmaf(float(d[i]), dq[r] * s.dw[j], acc[j][i]);
+        acc[j][i] = fmaf(float(d[j][i]), dq[r] * dw[j], acc[j][i]);
       }
     }
   }
 }
 
+// A workgroup computes 64 rows x 64*NJ columns: wave w takes rows 32*(w & 1)
+// and NJ column tiles of 32 from 32*NJ*(w >> 1).
 __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
+  __shared__ float4 xs_all[4][2][kDepth][8];  // [wave][slot][block][32 rows / 4]
   const int b = blockIdx.x;
   const int xcd = b & 7, kq = b >> 3;
   const int qn = kq / g.mtiles;
@@ -166,33 +184,74 @@ __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
   if (ntile >= g.ntiles) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m32 = mtile * (TM / 32) + (wave & 1);
-  const int n0 = ntile * TN + 64 * (wave >> 1);
+  const int n0 = ntile * 64 * NJ + 32 * NJ * (wave >> 1);
+  const int hi = lane >> 5;
   const Rsrc ar = rsrc(g.afrag, size_t(g.m_pad) * g.kb_n * 32);
   const Rsrc wr = rsrc(g.w, g.l.total);
   const Rsrc dr = rsrc(g.dx, size_t(g.kb_n) * g.m_pad * 4);
+  float2 *xw = reinterpret_cast<float2 *>(&xs_all[wave][0][0][0]);  // this wave's two slots
 
-  float acc[2][16];
+  I8Offsets o;
+  o.a = uint32_t((size_t(m32) * g.kb_n * 64 + lane) * 16);
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < NJ; ++j) {
+    const int n = min(n0 + 32 * j + (lane & 31), g.l.tiles * 64 - 1);
+    const size_t t0 = size_t(n >> 6) * g.l.units;  // tile's first unit
+    o.b[j] = uint32_t(((t0 * 16 + hi) * 64 + (n & 63)) * 16);
+    o.d[j] = uint32_t(g.l.side1_off + (t0 * 64 + (n & 63)) * 16);
+  }
+  // lane l loads rows 2 * (l % 16) .. + 1 of block l / 16 of a group
+  const uint32_t vx = uint32_t((m32 * 32 + 2 * (lane & 15)) * 4);
+
+  float acc[NJ][16];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
-  // Two stages in flight: block kb + 1 loads while block kb computes.
-  I8Stage s0, s1;
-  load_stage(s0, g, ar, wr, dr, m32, n0, 0, lane);
-  for (int kb = 0; kb < g.kb_n; kb += 2) {
-    load_stage(s1, g, ar, wr, dr, m32, n0, kb + 1, lane);
-    block_step(acc, s0);
-    if (kb + 1 >= g.kb_n) break;
-    load_stage(s0, g, ar, wr, dr, m32, n0, kb + 2, lane);
-    block_step(acc, s1);
+  const int last = g.kb_n - 1;
+  // In flight at the top of each group: that group's scales, then its kDepth
+  // blocks of A and B (the same order as the loop leaves them; the
+  // scheduling barriers keep it, so the wait counts at the loop head need not
+  // be conservative).
+  float2 hx = load_scales(dr, vx, g.m_pad, 0, last, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  I8Stage s[kDepth];
+#pragma unroll
+  for (int p = 0; p < kDepth; ++p) {
+    load_ab(s[p], ar, wr, o, min(p, last));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  const int kb_main = g.kb_n - g.kb_n % kDepth;
+  int slot = 0;
+  for (int kb = 0; kb < kb_main; kb += kDepth) {
+    xw[slot * 64 + lane] = hx;  // [block lane/16][rows 2*(lane%16) ..]
+    hx = load_scales(dr, vx, g.m_pad, kb + kDepth, last, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    const float4 *xc = &xs_all[wave][slot][0][0];
+#pragma unroll
+    for (int p = 0; p < kDepth; ++p) {
+      block_step(acc, s[p], xc + p * 8, hi, p & 1);
+      load_ab(s[p], ar, wr, o, min(kb + p + kDepth, last));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    slot ^= 1;
+  }
+  // The last kb_n % kDepth blocks sit in s[0 ..], their scales in hx.
+  if (kb_main < g.kb_n) {
+    xw[slot * 64 + lane] = hx;
+    const float4 *xc = &xs_all[wave][slot][0][0];
+#pragma unroll
+    for (int p = 0; p < kDepth - 1; ++p)
+      if (kb_main + p < g.kb_n) block_step(acc, s[p], xc + p * 8, hi, p & 1);
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int col = n0 + 32 * j + (lane & 31);
     if (col >= g.N) continue;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int row = m32 * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      const int row = m32 * 32 + 8 * (i >> 2) + 4 * hi + (i & 3);
       if (row < g.M) g.c[size_t(row) * g.N + col] = acc[j][i];
     }
   }
@@ -210,9 +269,12 @@ void q8_gemm_i8_launch(const float *a, int M, int K, int N, const GGLayout &l, c
   const int m_pad = (M + 63) / 64 * 64, kb_n = K / 32;
   auto *afrag = static_cast<uint4 *>(ws);
   auto *dx = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((size_t(m_pad) * K + 255) & ~size_t(255)));
-  const long long threads = (long long)m_pad * kb_n;
-  hipLaunchKernelGGL(k_q8_act_quant, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, a, M, K, m_pad, afrag,
-                     dx);
+  // Every buffer offset of the GEMM is a 32-bit byte offset.
+  if (l.total > 0xFFFFFFFFull || size_t(m_pad) * K > 0xFFFFFFFFull)
+    fail(QNN_E_NOT_SUPPORTED, "the int8-activation GEMM takes weights and activations below 4 GiB");
+  const long long threads = (long long)m_pad * kb_n * 8;
+  hipLaunchKernelGGL(k_q8_act_quant, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, a, M, K, m_pad,
+                     reinterpret_cast<uint32_t *>(afrag), dx);
   I8GemmArgs g;
   g.afrag = afrag;
   g.dx = dx;
@@ -224,7 +286,7 @@ void q8_gemm_i8_launch(const float *a, int M, int K, int N, const GGLayout &l, c
   g.m_pad = m_pad;
   g.kb_n = kb_n;
   g.mtiles = m_pad / TM;
-  g.ntiles = (N + TN - 1) / TN;
+  g.ntiles = (N + 64 * NJ - 1) / (64 * NJ);
   const int grid = (g.ntiles + 7) / 8 * 8 * g.mtiles;
   hipLaunchKernelGGL(k_q8_gemm_i8, dim3(grid), dim3(256), 0, s, g);
   hip_check(hipGetLastError(), "q8 int8 gemm launch");

@@ -126,8 +126,8 @@ def run_int8(ctx, w, a, n):
     return out
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 32, 32), (3, 96, 100), (33, 256, 257), (64, 288, 64), (100, 1024, 130),
-                                   (130, 3072, 128)])
+@pytest.mark.parametrize("m,k,n", [(1, 32, 32), (3, 96, 100), (5, 160, 70), (7, 224, 64), (33, 256, 257),
+                                   (64, 288, 64), (100, 1024, 130), (130, 3072, 128)])
 def test_int8_gemm_bit_identical_to_oracle(ctx, rng, m, k, n):
     a = rng.standard_normal((m, k)).astype(np.float32)
     a[0, :32] = 0.0  # a zero block: d = 0
