@@ -39,6 +39,16 @@ __device__ __forceinline__ float silu_dev(float g) {  // tensor.comp:22, as GO_S
 __device__ __forceinline__ float gelu_dev(float x) {  // tensor.comp:23 (tanh approximation), as GO_GEGLU
   return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
 }
+// Weight loads: each weight byte is read once per launch, so they stream
+// (non-temporal) and leave the L2 to the activations and the exchange
+// (measured: Gemma-2 layer 43.2 -> 41.4 us).
+typedef unsigned wl_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 wload(const uint4 *p) {
+  const wl_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const wl_u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <class T> __device__ __forceinline__ T wload(const T *p) { return __builtin_nontemporal_load(p); }
+
 __device__ __forceinline__ uint32_t sel4u(const uint4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
@@ -445,15 +455,15 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
     const size_t tu = size_t(stile) * l.units + (u0 + min(uw0 + b, nu - 1));
     const uint4 *mp = reinterpret_cast<const uint4 *>(P.main) + (tu * F::C) * 64 + srow;
 #pragma unroll
-    for (int c = 0; c < F::C; ++c) mw[b][c] = mp[c * 64];
-    if (F::S1 == 16) s1v[b] = reinterpret_cast<const uint4 *>(P.side1)[tu * 64 + srow];
+    for (int c = 0; c < F::C; ++c) mw[b][c] = wload(mp + c * 64);
+    if (F::S1 == 16) s1v[b] = wload(reinterpret_cast<const uint4 *>(P.side1) + tu * 64 + srow);
     if (F::S1 == 12) {
       const uint32_t *q = reinterpret_cast<const uint32_t *>(P.side1 + (tu * 64 + srow) * 12);
-      s1v[b] = make_uint4(q[0], q[1], q[2], 0u);
+      s1v[b] = make_uint4(wload(q), wload(q + 1), wload(q + 2), 0u);
     }
-    if (F::S1 == 4) s1w[b] = reinterpret_cast<const uint32_t *>(P.side1)[tu * 64 + srow];
-    if (F::S1 == 2) s1w[b] = reinterpret_cast<const uint16_t *>(P.side1)[tu * 64 + srow];
-    if (F::S2 == 2) s2w[b] = reinterpret_cast<const uint16_t *>(P.side2)[tu * 64 + srow];
+    if (F::S1 == 4) s1w[b] = wload(reinterpret_cast<const uint32_t *>(P.side1) + tu * 64 + srow);
+    if (F::S1 == 2) s1w[b] = wload(reinterpret_cast<const uint16_t *>(P.side1) + tu * 64 + srow);
+    if (F::S2 == 2) s2w[b] = wload(reinterpret_cast<const uint16_t *>(P.side2) + tu * 64 + srow);
   }
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the quantisation below waits for x
   // 3) quantise the activation slice (natural element order)

@@ -93,6 +93,11 @@ __device__ __forceinline__ uint4 ld128(Rsrc r, uint32_t voff, uint32_t soff) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 constexpr int kCoherent = 16;
+// AUX = 2 sets NT: a streaming (non-temporal) load.  Weight bytes are read
+// once per launch, so they stream and leave the L2 to the activation slices
+// and the split-K exchange (measured: Qwen3-4B decode MLP 16.3 -> 15.9 us,
+// 6144 x 2048 matvec 6.1 -> 5.8 us).
+constexpr int kStream = 2;
 __device__ __forceinline__ float ld32f(Rsrc r, uint32_t voff, uint32_t soff) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), 0));
 }
@@ -154,9 +159,9 @@ __device__ __forceinline__ void load_wq(uint4 (&w)[GSW], uint4 (&q)[scale_quads<
   const uint32_t at = uint32_t((size_t(b) * l.steps + s0) * 64 + wl);
   const uint32_t qat = uint32_t((size_t(b) * l.quads() + (s0 >> 2)) * 64 + wl);
 #pragma unroll
-  for (int i = 0; i < scale_quads<GSW>(); ++i) q[i] = ld128(scl, scl_off + qat * 16u, uint32_t(i) * 1024u);
+  for (int i = 0; i < scale_quads<GSW>(); ++i) q[i] = ld128<kStream>(scl, scl_off + qat * 16u, uint32_t(i) * 1024u);
 #pragma unroll
-  for (int g = 0; g < GSW; ++g) w[g] = ld128(nib, nib_off + at * 16u, uint32_t(g) * 1024u);
+  for (int g = 0; g < GSW; ++g) w[g] = ld128<kStream>(nib, nib_off + at * 16u, uint32_t(g) * 1024u);
 }
 template <int GSW>
 __device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc nib, Rsrc scl, const I4Layout &l, int b,
@@ -320,32 +325,42 @@ __device__ __forceinline__ void dot(float (&acc)[MT], const uint4 (&w)[GSW], con
 // dot().  Lane l holds D[4c + r][l%16], r = 0..3: tokens 4c..4c+3 of row
 // 16rq + l%16.  Token rows >= MT read token 0's plane and are discarded.
 //
-// The weights are loaded straight into that pattern: lane l takes dword c of
-// row 16rq + l%16 (per step four 4-byte loads, each over 256 contiguous bytes
-// of the step's 1 KiB), and the scales of those rows (one 16-byte scale piece
-// per quarter and 4 steps).
+// The weights arrive as the layout stores them, lane l holding row l's 16
+// bytes of each step (one 16-byte load per lane and step: 4-byte loads in that
+// pattern streamed 30% slower), and are put in that pattern at use: dword c of
+// row 16rq + l%16 is a 4 x 4 transpose across the four 16-lane rows (two
+// 32-lane and two 16-lane swaps per step).  The scales of those rows come as
+// one 16-byte scale piece per quarter and 4 steps.
 template <int GSW>
 struct MfWeights {
-  uint32_t w[GSW][4];  // [step][quarter]: dword c of row 16*quarter + l%16
-  float sc[GSW][4];    // [step][quarter]: its scale
+  uint4 w[GSW];        // [step]: row l's 16 bytes
+  float sc[GSW][4];    // [step][quarter]: the scale of row 16*quarter + l%16
 };
+// (dword c of row 16rq + l%16 for rq = 0..3) from (row l's dwords 0..3).
+__device__ __forceinline__ void mf_transpose(uint32_t (&o)[4], const uint4 &v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  o[0] = c[0];
+  o[1] = c[1];
+  o[2] = d[0];
+  o[3] = d[1];
+}
 template <int GSW>
 __device__ __forceinline__ void load_w_mf(MfWeights<GSW> &mw, Rsrc nib, Rsrc scl, const I4Layout &l, int b, int s0,
                                           int lane) {
   static_assert(GSW % 4 == 0, "scale pieces hold 4 aligned steps");
-  const int p = lane & 15, c = lane >> 4;
-  const uint32_t at = uint32_t(size_t(b) * l.steps + s0) * 1024u + uint32_t(p * 16 + c * 4);
+  const int p = lane & 15;
+  const uint32_t at = uint32_t(size_t(b) * l.steps + s0) * 1024u + uint32_t(lane * 16);
   const uint32_t qat = uint32_t((size_t(b) * l.quads() + (s0 >> 2)) * 64 + p) * 16u;
   uint4 q[GSW / 4][4];
 #pragma unroll
   for (int i = 0; i < GSW / 4; ++i)
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) q[i][rq] = ld128(scl, qat + uint32_t(rq) * 256u, uint32_t(i) * 1024u);
+    for (int rq = 0; rq < 4; ++rq) q[i][rq] = ld128<kStream>(scl, qat + uint32_t(rq) * 256u, uint32_t(i) * 1024u);
 #pragma unroll
-  for (int g = 0; g < GSW; ++g)
-#pragma unroll
-    for (int rq = 0; rq < 4; ++rq)
-      mw.w[g][rq] = __builtin_amdgcn_raw_buffer_load_b32(nib, int(at + uint32_t(rq) * 256u), int(g * 1024), 0);
+  for (int g = 0; g < GSW; ++g) mw.w[g] = ld128<kStream>(nib, at, uint32_t(g) * 1024u);
 #pragma unroll
   for (int g = 0; g < GSW; ++g)
 #pragma unroll
@@ -375,9 +390,11 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][4], const MfWeights<GSW> 
         s2[r] = xs.s2[size_t(m) * xs.groups + g];
         off[r] = xs.off[size_t(m) * xs.groups + g];
       }
+      uint32_t wq[4];
+      mf_transpose(wq, mw.w[g]);
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const uint32_t wd = mw.w[g][rq];
+        const uint32_t wd = wq[rq];
         const long bw = long(wd & 0x0F0F0F0Fu) | (long((wd >> 4) & 0x0F0F0F0Fu) << 32);
         const mf_i32x4 z = {0, 0, 0, 0};
         const mf_i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
