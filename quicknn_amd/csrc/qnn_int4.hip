@@ -79,17 +79,21 @@ void k_int4_matvec(const I4Launch a, const int slices) {
   uint4 w[MF ? 1 : GSW];
   float sc[MF ? 1 : GSW];
   dev::MfWeights<MF ? GSW : 4> mw;
-  if constexpr (MF)
-    dev::load_w_mf<GSW>(mw, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, lane);
-  else
-    dev::load_w<GSW>(w, sc, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, wl);
-
-  // 2) Fixed-point activation planes in LDS.
   const dev::XPlanes xs = dev::xplanes_at(dyn_lds, MT, P * sps * L);
-  if constexpr (MF)
+  // 2) Fixed-point activation planes in LDS.  On the matrix-core path (4-16
+  //    tokens) the slice is staged before the weight loads are issued: a
+  //    wave cannot pass its weight loads until the memory pipeline accepts
+  //    them, which under the whole grid's stream took microseconds (batch-8
+  //    gate/up 18.8 -> 17.5 us, down 13.1 -> 12.2 us).  With one token the
+  //    staging is short and issuing the weights first is faster (6144 x 2048
+  //    5.9 against 6.3 us).
+  if constexpr (MF) {
     dev::stage_x_pairs<MT>(xs, xr2, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
-  else
+    dev::load_w_mf<GSW>(mw, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, lane);
+  } else {
+    dev::load_w<GSW>(w, sc, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, wl);
     dev::stage_x<MT, GSW>(xs, xr, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
+  }
   __syncthreads();
 
   // 3) Integer dot per group and token, the L lanes of each row, then the P
