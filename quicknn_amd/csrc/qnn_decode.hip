@@ -130,6 +130,18 @@ __device__ __forceinline__ float4 load4(const float *row, int c, int dim) {
   return make_float4(row[c], c + 1 < dim ? row[c + 1] : 0.f, c + 2 < dim ? row[c + 2] : 0.f,
                      c + 3 < dim ? row[c + 3] : 0.f);
 }
+// Cache reads: each K and V element is read once per call, so they stream
+// (non-temporal; 32k keys 60.8 -> 57.0 us) and leave the L2 to q and the
+// chunk partials.
+__device__ __forceinline__ float kvload(const float *p) { return __builtin_nontemporal_load(p); }
+typedef float kv_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load4v(const float *row, int c, int dim) {
+  if ((dim & 3) == 0) {
+    const kv_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const kv_f32x4 *>(row + c));
+    return make_float4(v.x, v.y, v.z, v.w);
+  }
+  return load4(row, c, dim);
+}
 __device__ __forceinline__ void store4(float *row, int c, int dim, float4 v) {
   if ((dim & 3) == 0) {
     *reinterpret_cast<float4 *>(row + c) = v;
@@ -222,7 +234,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
       for (int i = 0; i < ND4; ++i) {
         const int cg = c4 + i * a.lpk;
         vv[u][i] = (kk < a.kl && key < nkeys && i < a.nd4 && cg * 4 < a.dim)
-                       ? load4(vb + size_t(c0 + key) * a.dim, cg * 4, a.dim)
+                       ? load4v(vb + size_t(c0 + key) * a.dim, cg * 4, a.dim)
                        : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
@@ -246,7 +258,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
       for (; d + 32 <= d1; d += 32) {
         float kv[32];
 #pragma unroll
-        for (int u = 0; u < 32; ++u) kv[u] = kc[size_t(d + u) * a.cap];
+        for (int u = 0; u < 32; ++u) kv[u] = kvload(kc + size_t(d + u) * a.cap);
 #pragma unroll
         for (int u = 0; u < 32; ++u)
 #pragma unroll
@@ -255,14 +267,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
       for (; d + 8 <= d1; d += 8) {
         float kv[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) kv[u] = kc[size_t(d + u) * a.cap];
+        for (int u = 0; u < 8; ++u) kv[u] = kvload(kc + size_t(d + u) * a.cap);
 #pragma unroll
         for (int u = 0; u < 8; ++u)
 #pragma unroll
           for (int g = 0; g < GB; ++g) sc[g] += qs[g * a.dim + d + u] * kv[u];
       }
       for (; d < d1; ++d) {
-        const float kv = kc[size_t(d) * a.cap];
+        const float kv = kvload(kc + size_t(d) * a.cap);
 #pragma unroll
         for (int g = 0; g < GB; ++g) sc[g] += qs[g * a.dim + d] * kv;
       }
