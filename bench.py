@@ -753,7 +753,7 @@ def main() -> int:
         # The other workloads of the benchmark definition, in the same run (so
         # the driver's clock covers them): short timings, no CPU legs.
         sub = argparse.Namespace(**vars(args))
-        sub.steps, sub.warmup, sub.no_cpu = max(5, args.steps // 5), 2, True
+        sub.steps, sub.warmup, sub.no_cpu = max(5, args.steps // 5), max(2, args.warmup), True
         others = {}
         for c in (1, 3, 4, 5, 6):
             t0 = time.perf_counter()
