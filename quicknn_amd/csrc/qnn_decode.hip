@@ -412,11 +412,81 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
 }
 
 // Merge the key chunks: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
-// One workgroup per (row, head) and 256 channels; `sg` split groups of
-// threads share a channel and walk the chunks sixteen loads at a time.
-constexpr int kMergeMaxSplits = 4096;
+// One workgroup per (row, head).  Thread t owns float4 channel group t % G
+// (G = dim / 4 groups, dim % 4 == 0) and every (256 / G)-th chunk from t / G;
+// it requests all of its chunks' outputs first (up to kMergeLoads float4 in
+// flight), then the (max, sum) pairs; the head's maximum and denominator come
+// from wave reductions, and the chunk groups meet in LDS in a fixed order.
+// Other shapes (dim % 4 != 0, more chunks than fit the loads) take
+// k_attn_merge_general.
+constexpr int kMergeLoads = 8;
 __global__ __launch_bounds__(256) void k_attn_merge(float *out, const float *opart, const float *mlpart, int splits,
-                                                    int row_heads, int dim, int dspan, int sg) {
+                                                    int row_heads, int dim) {
+  __shared__ float wsh[256];
+  __shared__ float red[2][4];
+  __shared__ float4 acc4[256];
+  const int rh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int groups = dim / 4, sg = 256 / groups;  // chunk groups
+  const int c = tid % groups, gi = tid / groups;
+  float4 x[kMergeLoads];
+  const float4 *ob = reinterpret_cast<const float4 *>(opart + size_t(rh) * dim) + c;
+  const size_t stride4 = size_t(row_heads) * groups;
+#pragma unroll
+  for (int u = 0; u < kMergeLoads; ++u) {
+    const int sidx = gi + u * sg;
+    x[u] = (gi < sg && sidx < splits) ? ob[size_t(sidx) * stride4] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // (max, sum) of chunk tid (splits <= 256)
+  float m = -INFINITY, l = 0.0f;
+  if (tid < splits) {
+    const float2 ml = *reinterpret_cast<const float2 *>(mlpart + (size_t(tid) * row_heads + rh) * 2);
+    m = ml.x;
+    l = ml.y;
+  }
+  float M = m;
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+  if (lane == 0) red[0][wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  const float w = m > -INFINITY ? expf(m - M) : 0.0f;
+  wsh[tid] = w;
+  float L = l * w;
+  for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+  if (lane == 0) red[1][wave] = L;
+  __syncthreads();
+  L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int u = 0; u < kMergeLoads; ++u) {
+    const int sidx = gi + u * sg;
+    if (gi < sg && sidx < splits) {
+      const float ww = wsh[sidx];
+      v.x += x[u].x * ww;
+      v.y += x[u].y * ww;
+      v.z += x[u].z * ww;
+      v.w += x[u].w * ww;
+    }
+  }
+  acc4[tid] = v;
+  __syncthreads();
+  if (gi == 0) {
+    for (int j = 1; j < sg; ++j) {
+      const float4 o = acc4[j * groups + c];
+      v.x += o.x;
+      v.y += o.y;
+      v.z += o.z;
+      v.w += o.w;
+    }
+    reinterpret_cast<float4 *>(out + size_t(rh) * dim)[c] = make_float4(v.x / L, v.y / L, v.z / L, v.w / L);
+  }
+}
+
+constexpr int kMergeMaxSplits = 4096;
+// Any shape: one workgroup per (row, head) and 256 channels; `sg` split
+// groups of threads share a channel and walk the chunks sixteen loads at a
+// time.
+__global__ __launch_bounds__(256) void k_attn_merge_general(float *out, const float *opart, const float *mlpart,
+                                                            int splits, int row_heads, int dim, int dspan, int sg) {
   __shared__ float wsh[kMergeMaxSplits];
   __shared__ float red[256];
   const int rh = blockIdx.x, tid = threadIdx.x;
@@ -870,10 +940,15 @@ void attn_launch(const float *q, const float *cache, float *out, float *ws, cons
   }
 #undef QNN_ATTN
   if (p.splits > 1) {
-    const int dspan = dim >= 256 ? 256 : dim > 128 ? 256 : dim > 64 ? 128 : 64;
-    const int sg = 256 / dspan;
-    dim3 mg(rows * heads, (dim + dspan - 1) / dspan);
-    k_attn_merge<<<mg, 256, 0, s>>>(out, opart, ml, p.splits, rows * heads, dim, dspan, sg);
+    const int groups = dim / 4;
+    if (dim % 4 == 0 && groups <= 256 && p.splits <= 256 && p.splits <= kMergeLoads * (256 / groups)) {
+      k_attn_merge<<<rows * heads, 256, 0, s>>>(out, opart, ml, p.splits, rows * heads, dim);
+    } else {
+      const int dspan = dim >= 256 ? 256 : dim > 128 ? 256 : dim > 64 ? 128 : 64;
+      const int sg = 256 / dspan;
+      dim3 mg(rows * heads, (dim + dspan - 1) / dspan);
+      k_attn_merge_general<<<mg, 256, 0, s>>>(out, opart, ml, p.splits, rows * heads, dim, dspan, sg);
+    }
   }
 }
 
