@@ -290,32 +290,70 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
           for (int p = 1; p < a.parts; ++p) v += xred[(p * GB + g) * a.sub + key_t];
           sc[g] = v;
         }
-      __syncthreads();
+      if (a.sub != 64) __syncthreads();
       valid = valid && part == 0;
     }
-    float cm[GB];
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
       float v = sc[g] * mul;
       if (a.softcap > 0.0f) v = a.softcap * tanhf(fminf(fmaxf(v / a.softcap, -20.0f), 20.0f));
       sc[g] = v;
-      cm[g] = valid ? v : -INFINITY;
     }
-    block_max_sum<GB>(cm, red, true);
-    float m_new[GB], keep[GB], ls[GB];
+    float keep[GB];
+    if (a.sub == 64) {
+      // A 64-key sub-chunk: after the channel parts meet, wave 0 holds every
+      // score (one key per lane) and runs the online softmax with wave
+      // reductions; the other waves read the rescale factors from LDS.
+      if (part == 0) {
+#pragma unroll
+        for (int g = 0; g < GB; ++g) {
+          float mx = valid ? sc[g] : -INFINITY;
+          for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+          const float m_new = fmaxf(m_run[g], mx);
+          keep[g] = m_new == -INFINITY ? 1.0f : expf(m_run[g] - m_new);
+          const float p = (valid && m_new > -INFINITY) ? expf(sc[g] - m_new) : 0.0f;
+          ps[g * kAttnSub + key_t] = p;
+          float ls = p;
+          for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off);
+          l_run[g] = l_run[g] * keep[g] + ls;
+          m_run[g] = m_new;
+          if (key_t == 0) {
+            red[g] = keep[g];
+            red[GB + g] = l_run[g];
+            red[2 * GB + g] = m_run[g];
+          }
+        }
+      }
+      __syncthreads();  // publishes ps and the running state
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        keep[g] = red[g];
+        l_run[g] = red[GB + g];
+        m_run[g] = red[2 * GB + g];
+      }
+    } else {
+      float cm[GB];
+#pragma unroll
+      for (int g = 0; g < GB; ++g) cm[g] = valid ? sc[g] : -INFINITY;
+      block_max_sum<GB>(cm, red, true);
+      float m_new[GB], ls[GB];
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        m_new[g] = fmaxf(m_run[g], cm[g]);
+        keep[g] = m_new[g] == -INFINITY ? 1.0f : expf(m_run[g] - m_new[g]);
+        const float p = (valid && m_new[g] > -INFINITY) ? expf(sc[g] - m_new[g]) : 0.0f;
+        if (part == 0) ps[g * kAttnSub + key_t] = p;
+        ls[g] = p;
+      }
+      block_max_sum<GB>(ls, red, false);  // its barriers also publish ps
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        l_run[g] = l_run[g] * keep[g] + ls[g];
+        m_run[g] = m_new[g];
+      }
+    }
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
-      m_new[g] = fmaxf(m_run[g], cm[g]);
-      keep[g] = m_new[g] == -INFINITY ? 1.0f : expf(m_run[g] - m_new[g]);
-      const float p = (valid && m_new[g] > -INFINITY) ? expf(sc[g] - m_new[g]) : 0.0f;
-      if (part == 0) ps[g * kAttnSub + key_t] = p;
-      ls[g] = p;
-    }
-    block_max_sum<GB>(ls, red, false);  // its barriers also publish ps
-#pragma unroll
-    for (int g = 0; g < GB; ++g) {
-      l_run[g] = l_run[g] * keep[g] + ls[g];
-      m_run[g] = m_new[g];
 #pragma unroll
       for (int i = 0; i < ND4; ++i) {
         acc[g][i].x *= keep[g];
@@ -359,7 +397,44 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
   }
 
   // Sum the key lanes.
-  if (a.kl > 1) {
+  if (a.kl > 1 && a.lpk == 32) {
+    // Two key lanes per wave (lanes 0-31 and 32-63): they meet by a lane
+    // shuffle, then the four waves' sums in LDS.
+#pragma unroll
+    for (int g = 0; g < GB; ++g)
+#pragma unroll
+      for (int i = 0; i < ND4; ++i) {
+        acc[g][i].x += __shfl_down(acc[g][i].x, 32);
+        acc[g][i].y += __shfl_down(acc[g][i].y, 32);
+        acc[g][i].z += __shfl_down(acc[g][i].z, 32);
+        acc[g][i].w += __shfl_down(acc[g][i].w, 32);
+      }
+    const int w = tid >> 6, ln = tid & 63;
+    if (w > 0 && ln < 32)
+#pragma unroll
+      for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int i = 0; i < ND4; ++i) {
+          const int cg = c4 + i * a.lpk;
+          if (i < a.nd4 && cg * 4 < a.dim) store4(xred + (size_t(w - 1) * GB + g) * a.dim, cg * 4, a.dim, acc[g][i]);
+        }
+    __syncthreads();
+    if (tid < 32)
+#pragma unroll
+      for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int i = 0; i < ND4; ++i) {
+          const int cg = c4 + i * a.lpk;
+          if (i < a.nd4 && cg * 4 < a.dim)
+            for (int l = 0; l < 3; ++l) {
+              const float4 o = load4(xred + (size_t(l) * GB + g) * a.dim, cg * 4, a.dim);
+              acc[g][i].x += o.x;
+              acc[g][i].y += o.y;
+              acc[g][i].z += o.z;
+              acc[g][i].w += o.w;
+            }
+        }
+  } else if (a.kl > 1) {
     if (kk < a.kl)
 #pragma unroll
       for (int g = 0; g < GB; ++g)
