@@ -108,11 +108,11 @@ void k_int4_matvec(const I4Launch a, const int slices) {
     xp.s2 = xs.s2 + g0;
     xp.off = xs.off + g0;
     if constexpr (MF) {
-      float accm[4][4];
+      float accm[4][dev::mf_per_lane<MT>()];
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) accm[rq][r] = 0.0f;
+        for (int r = 0; r < dev::mf_per_lane<MT>(); ++r) accm[rq][r] = 0.0f;
       dev::dot_mf<MT, GSW>(accm, mw, xp, ns, lane);
       dev::mf_to_rows<MT>(acc, accm, &red[wave][0][0], lane);
     } else {

@@ -314,8 +314,9 @@ __device__ __forceinline__ void dot(float (&acc)[MT], const uint4 (&w)[GSW], con
 }
 
 // ---- Several tokens on the int8 matrix cores (L = 1, MT >= 4, GSW >= 4).
-// Per group and 16-row quarter rq of the block, one v_mfma_i32_16x16x32_i8
-// per activation plane: A = the plane (16 tokens x 32 elements; lane l gives
+// Per group and 16-row quarter rq of the block, with 9-16 tokens one
+// v_mfma_i32_16x16x32_i8 per activation plane (up to 8 tokens: one for both,
+// below): A = the plane (16 tokens x 32 elements; lane l gives
 // token l%16, elements 8c..8c+7 of the group, c = l/16, as plane words 2c and
 // 2c+1), B = the nibbles (32 elements x 16 rows; lane l gives row 16rq + l%16,
 // the same elements: the low then the high nibbles of its dword c).  Both
@@ -369,26 +370,47 @@ __device__ __forceinline__ void load_w_mf(MfWeights<GSW> &mw, Rsrc nib, Rsrc scl
 
 typedef int mf_i32x4 __attribute__((ext_vector_type(4)));
 
-// acc[rq][r] += the group sums of steps 0..ns-1 for token 4c + r, row
-// 16rq + l%16 (the layout above), in step order.
+// Up to 8 tokens: both planes in one product.  A row p = 8 * plane + token
+// (plane 0 the high plane), so lane l holds D[4c + r][l%16] = plane c/2, token
+// 4(c%2) + r, and lanes l and l + 32 hold the two planes of the same tokens.
+// A 32-lane swap of D[r] with D[r + 2] (r = 0, 1) leaves every lane with both
+// planes of one token: lanes 0-31 those of tokens 4c + r, lanes 32-63 those of
+// 4(c-2) + 2 + r.  Each lane then finishes 2 (row, token) sums per quarter
+// and step instead of 4, with half the products.
+template <int MT>
+constexpr int mf_per_lane() { return MT <= 8 ? 2 : 4; }
+template <int MT>
+__device__ __forceinline__ int mf_token(int lane, int r) {
+  if constexpr (MT <= 8)
+    return 4 * ((lane >> 4) & 1) + 2 * (lane >> 5) + r;
+  else
+    return 4 * (lane >> 4) + r;
+}
+
+// acc[rq][r] += the group sums of steps 0..ns-1 for token mf_token(lane, r),
+// row 16rq + l%16 (the layouts above), in step order.
 template <int MT, int GSW>
-__device__ __forceinline__ void dot_mf(float (&acc)[4][4], const MfWeights<GSW> &mw, const XPlanes &xs, int ns,
-                                       int lane) {
+__device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const MfWeights<GSW> &mw,
+                                       const XPlanes &xs, int ns, int lane) {
+  constexpr int R = mf_per_lane<MT>();
   const int p = lane & 15, c = lane >> 4;
-  const int ta = p < MT ? p : 0;  // A row token
+  const int tp = MT <= 8 ? (p & 7) : p;  // A row token
+  const int ta = tp < MT ? tp : 0;
+  const int aw = MT <= 8 ? 8 * (p >> 3) + 2 * c : 2 * c;  // A words within the entry
+  int tk[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) tk[r] = mf_token<MT>(lane, r) < MT ? mf_token<MT>(lane, r) : 0;
 #pragma unroll
   for (int g = 0; g < GSW; ++g) {
     if (g < ns) {
       const uint32_t *qa = xs.q + (size_t(ta) * xs.groups + g) * kXWords;
-      const long ah = *reinterpret_cast<const long *>(qa + 2 * c);
-      const long al = *reinterpret_cast<const long *>(qa + 8 + 2 * c);
-      float s2[4];
-      int off[4];
+      const long ah = *reinterpret_cast<const long *>(qa + aw);
+      float s2[R];
+      int off[R];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 4 * c + r < MT ? 4 * c + r : 0;
-        s2[r] = xs.s2[size_t(m) * xs.groups + g];
-        off[r] = xs.off[size_t(m) * xs.groups + g];
+      for (int r = 0; r < R; ++r) {
+        s2[r] = xs.s2[size_t(tk[r]) * xs.groups + g];
+        off[r] = xs.off[size_t(tk[r]) * xs.groups + g];
       }
       uint32_t wq[4];
       mf_transpose(wq, mw.w[g]);
@@ -398,10 +420,26 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][4], const MfWeights<GSW> 
         const long bw = long(wd & 0x0F0F0F0Fu) | (long((wd >> 4) & 0x0F0F0F0Fu) << 32);
         const mf_i32x4 z = {0, 0, 0, 0};
         const mf_i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
-        const mf_i32x4 dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bw, z, 0, 0, 0);
+        int hi[R], lo[R];
+        if constexpr (MT <= 8) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int isum = (dh[r] << 8) + dl[r] + off[r];
+          for (int r = 0; r < 2; ++r) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(dh[r], dh[r + 2], false, false);
+            hi[r] = int(sw[0]);
+            lo[r] = int(sw[1]);
+          }
+        } else {
+          const long al = *reinterpret_cast<const long *>(qa + 8 + 2 * c);
+          const mf_i32x4 dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bw, z, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            hi[r] = dh[r];
+            lo[r] = dl[r];
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int isum = (hi[r] << 8) + lo[r] + off[r];
           acc[rq][r] = fmaf(float(isum), mw.sc[g][rq] * s2[r], acc[rq][r]);
         }
       }
@@ -412,13 +450,14 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][4], const MfWeights<GSW> 
 // The MFMA layout -> one row per lane (acc[m] = token m of row `lane`),
 // through this wave's [MT][64] LDS slot.
 template <int MT>
-__device__ __forceinline__ void mf_to_rows(float (&acc)[MT], const float (&accm)[4][4], float *slot, int lane) {
-  const int p = lane & 15, c = lane >> 4;
+__device__ __forceinline__ void mf_to_rows(float (&acc)[MT], const float (&accm)[4][mf_per_lane<MT>()], float *slot,
+                                           int lane) {
+  const int p = lane & 15;
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (4 * c + r < MT) slot[(4 * c + r) * 64 + 16 * rq + p] = accm[rq][r];
+    for (int r = 0; r < mf_per_lane<MT>(); ++r)
+      if (mf_token<MT>(lane, r) < MT) slot[mf_token<MT>(lane, r) * 64 + 16 * rq + p] = accm[rq][r];
   wave_lds_sync();
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = slot[m * 64 + lane];
