@@ -53,13 +53,13 @@ void k_int4_matvec(const I4Launch a, const int slices) {
   //    return 0); a wave past the last tile reads tile 0 and stops after the
   //    barrier.
   // The slice is P*sps*L <= 16*GSW groups (the planner keeps P*L <= 16).
-  // MF: slices of at most 4 x 4 x 32 = 512 elements, staged two tokens per pass.
+  // MF: slices of at most 4 x 4 x 32 = 512 elements, staged four tokens per pass.
   float4 xr[MF ? 1 : MT][MF ? 1 : dev::x_iters<GSW>()];
-  float4 xr2[MF ? MT / 2 : 1];
+  float4 xr4[MF ? MT / 4 : 1][2];
   const dev::Rsrc xsrc = dev::rsrc(a.x, size_t(a.m) * a.x_stride * 4);
   auto xrow = [&](int m) { return uint32_t(m) * uint32_t(a.x_stride) * 4u; };
   if constexpr (MF)
-    dev::load_x_pairs<MT>(xr2, xsrc, xrow, a.m, ws0 * L * 32, tid);
+    dev::load_x_quads<MT>(xr4, xsrc, xrow, a.m, ws0 * L * 32, wave, lane);
   else
     dev::load_x<MT, GSW>(xr, xsrc, xrow, a.m, ws0 * L * 32, sgroups * 32, tid);
   int tile = unit * T + wave / P;
@@ -88,7 +88,7 @@ void k_int4_matvec(const I4Launch a, const int slices) {
   //    staging is short and issuing the weights first is faster (6144 x 2048
   //    5.9 against 6.3 us).
   if constexpr (MF) {
-    dev::stage_x_pairs<MT>(xs, xr2, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
+    dev::stage_x_quads<MT>(xs, xr4, a.m, ws0 * L * 32, sgroups * 32, a.k, wave, lane);
     dev::load_w_mf<GSW>(mw, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, lane);
   } else {
     dev::load_w<GSW>(w, sc, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, wl);

@@ -174,55 +174,103 @@ __device__ __forceinline__ void load_w(uint4 (&w)[GSW], float (&sc)[GSW], Rsrc n
 // Quantises the loaded slice per 32-element group to 16-bit fixed point,
 // x ~= s2 * (256*q1 + q2) with q1, q2 in [-127, 127]:
 //   s1 = amax/127, q1 = rint(x/s1), r = x - q1*s1, s2 = s1/256, q2 = rint(r/s2)
-// (|x - s2(256 q1 + q2)| <= s2/2 = amax/65024).  The int8 planes match the
-// nibble bytes of a weight dword: dword c of a group holds elements 8c..8c+7,
-// its low nibbles are the even elements and its high nibbles the odd ones, so
-// plane word 2c packs x[8c+0,2,4,6] and word 2c+1 x[8c+1,3,5,7].  Words 0-7 of
-// an entry are the high plane, 8-15 the low plane.
+// (|x - s2(256 q1 + q2)| <= s2/2 = amax/65024, up to s2 where the clamp of
+// q2 to 127 bites).  1/s1 is the hardware reciprocal, and the rounding is
+// fma(v, 1/s, 1.5 * 2^23): the sum rounds v/s to the nearest integer (ties
+// to even) inside the float, whose low mantissa bits then hold it in two's
+// complement, so byte 0 of the float's bits is the int8 and the float minus
+// 1.5 * 2^23 is the exact q as a float.  Every kernel stages through these
+// helpers, so all paths see the same planes.
+// The int8 planes match the nibble bytes of a weight dword: dword c of a group
+// holds elements 8c..8c+7, its low nibbles are the even elements and its high
+// nibbles the odd ones, so plane word 2c packs x[8c+0,2,4,6] and word 2c+1
+// x[8c+1,3,5,7].  Words 0-7 of an entry are the high plane, 8-15 the low plane.
 // Pieces of token m >= mt, of element >= ne within the slice or of row
 // element >= k are zero (e0 = first element of the slice).
-// One 4-element piece: elements e..e+3 (within the slice) of token m; the 8
-// lanes of a 32-group meet through shuffles, so every lane of the wave runs it.
-__device__ __forceinline__ void stage_piece(const XPlanes &xs, const float4 v, int m, int e, int lane) {
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
-  const float s1 = amax / 127.0f;
-  const float inv = s1 > 0.0f ? 1.0f / s1 : 0.0f;
-  const float inv2 = inv * 256.0f;
-  int h[4], l[4];
-  const float xv[4] = {v.x, v.y, v.z, v.w};
+constexpr float kRound = 12582912.0f;      // 1.5 * 2^23
+constexpr uint32_t kRoundBits = 0x4B400000u;  // its bits
+struct GroupScale {
+  float s1, inv, inv2;
+};
+__device__ __forceinline__ GroupScale group_scale(float amax) {
+  GroupScale g;
+  g.s1 = amax * (1.0f / 127.0f);
+  g.inv = g.s1 > 1e-30f ? __builtin_amdgcn_rcpf(g.s1) : 0.0f;  // groups below 1e-28 stage as zeros
+  g.inv2 = g.inv * 256.0f;
+  return g;
+}
+// One element: the rounded floats whose bits carry q1 (b1) and q2 (b2).
+__device__ __forceinline__ void quant_elem(float x, const GroupScale &g, uint32_t &b1, uint32_t &b2) {
+  const float f1 = fmaf(x, g.inv, kRound);
+  const float r = fmaf(kRound - f1, g.s1, x);  // x - q1 * s1
+  const float f2 = __builtin_amdgcn_fmed3f(fmaf(r, g.inv2, kRound), kRound - 127.0f, kRound + 127.0f);
+  b1 = __float_as_uint(f1);
+  b2 = __float_as_uint(f2);
+}
+// sum(256 q1 + q2) over N elements from their bits (exact: the true sum is small).
+template <int N>
+__device__ __forceinline__ int quant_sum(const uint32_t (&b1)[N], const uint32_t (&b2)[N]) {
+  uint32_t s1 = 0, s2 = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float q1 = fminf(127.0f, fmaxf(-127.0f, rintf(xv[j] * inv)));
-    const float r = fmaf(-q1, s1, xv[j]);
-    const float q2 = fminf(127.0f, fmaxf(-127.0f, rintf(r * inv2)));
-    h[j] = int(q1);
-    l[j] = int(q2);
+  for (int i = 0; i < N; ++i) {
+    s1 += b1[i];
+    s2 += b2[i];
   }
-  int sumq = (256 * h[0] + l[0]) + (256 * h[1] + l[1]) + (256 * h[2] + l[2]) + (256 * h[3] + l[3]);
-  sumq += __shfl_xor(sumq, 1);
-  sumq += __shfl_xor(sumq, 2);
-  sumq += __shfl_xor(sumq, 4);
+  return int((s1 << 8) + s2 - uint32_t(N) * 257u * kRoundBits);
+}
+// Byte 0 of a and of b -> bytes 0 and 1 (bytes 2, 3 zero).
+__device__ __forceinline__ uint32_t pack2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x0C0C0400u); }
+// The low halves of a and b -> one word.
+__device__ __forceinline__ uint32_t join2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+
+// Cross-lane reductions over aligned groups of 4 or 8 lanes (DPP, within a
+// 16-lane row): quad swaps of 1 and 2, then the other half of 8.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float max_lanes4(float v) {
+  v = fmaxf(v, __uint_as_float(dpp<0xB1>(__float_as_uint(v))));  // quad_perm [1,0,3,2]
+  return fmaxf(v, __uint_as_float(dpp<0x4E>(__float_as_uint(v))));  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ float max_lanes8(float v) {
+  v = max_lanes4(v);
+  return fmaxf(v, __uint_as_float(dpp<0x141>(__float_as_uint(v))));  // row_half_mirror
+}
+__device__ __forceinline__ int sum_lanes4(int v) {
+  v += int(dpp<0xB1>(uint32_t(v)));
+  return v + int(dpp<0x4E>(uint32_t(v)));
+}
+__device__ __forceinline__ int sum_lanes8(int v) {
+  v = sum_lanes4(v);
+  return v + int(dpp<0x141>(uint32_t(v)));
+}
+
+// One 4-element piece: elements e..e+3 (within the slice) of token m; the 8
+// lanes of a 32-group meet through DPP, so every lane of the wave runs it.
+__device__ __forceinline__ void stage_piece(const XPlanes &xs, const float4 v, int m, int e, int lane) {
+  const float amax = max_lanes8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  const GroupScale gs = group_scale(amax);
+  uint32_t b1[4], b2[4];
+  quant_elem(v.x, gs, b1[0], b2[0]);
+  quant_elem(v.y, gs, b1[1], b2[1]);
+  quant_elem(v.z, gs, b1[2], b2[2]);
+  quant_elem(v.w, gs, b1[3], b2[3]);
+  const int sumq = sum_lanes8(quant_sum<4>(b1, b2));
   const int g = e >> 5;
   if (g < xs.groups) {
     const int i0 = e & 31;  // element 8c + (i0 & 7) of group g
     const int c = i0 >> 3, half = (i0 >> 2) & 1;
-    // bytes for even slots (elements +0, +2) and odd slots (+1, +3) of this half dword
-    const uint32_t he = (uint32_t(h[0]) & 255u) | ((uint32_t(h[2]) & 255u) << 8);
-    const uint32_t ho = (uint32_t(h[1]) & 255u) | ((uint32_t(h[3]) & 255u) << 8);
-    const uint32_t le = (uint32_t(l[0]) & 255u) | ((uint32_t(l[2]) & 255u) << 8);
-    const uint32_t lo = (uint32_t(l[1]) & 255u) | ((uint32_t(l[3]) & 255u) << 8);
     const size_t mg = size_t(m) * xs.groups + g;
     uint16_t *ph = reinterpret_cast<uint16_t *>(xs.q + mg * kXWords);
     uint16_t *pl = ph + 16;
-    ph[(2 * c) * 2 + half] = uint16_t(he);
-    ph[(2 * c + 1) * 2 + half] = uint16_t(ho);
-    pl[(2 * c) * 2 + half] = uint16_t(le);
-    pl[(2 * c + 1) * 2 + half] = uint16_t(lo);
+    // bytes for even slots (elements +0, +2) and odd slots (+1, +3) of this half dword
+    ph[(2 * c) * 2 + half] = uint16_t(pack2(b1[0], b1[2]));
+    ph[(2 * c + 1) * 2 + half] = uint16_t(pack2(b1[1], b1[3]));
+    pl[(2 * c) * 2 + half] = uint16_t(pack2(b2[0], b2[2]));
+    pl[(2 * c + 1) * 2 + half] = uint16_t(pack2(b2[1], b2[3]));
     if ((lane & 7) == 0) {
-      xs.s2[mg] = s1 * 0.00390625f;
+      xs.s2[mg] = gs.s1 * 0.00390625f;
       xs.off[mg] = -8 * sumq;
     }
   }
@@ -243,26 +291,60 @@ __device__ __forceinline__ void stage_x(const XPlanes &xs, const float4 (&xr)[MT
   }
 }
 
-// Slices of at most 512 elements, an even number of tokens: two tokens per
-// pass, so no thread idles (threads t < 128 take token 2p, the others token
-// 2p + 1, elements 4(t % 128) ..).  The planes are those stage_x writes.
+// Slices of at most 512 elements, MT a multiple of 4: in pass p wave w stages
+// token 4p + w, lane l elements 8l..8l+7 of the slice (dword l%4 of group
+// l/4), so no thread idles and a lane writes whole plane words.  The planes
+// are those stage_x writes.
 template <int MT, class OffF>
-__device__ __forceinline__ void load_x_pairs(float4 (&xr)[MT / 2], Rsrc src, OffF rowoff, int mt, int e0, int tid) {
+__device__ __forceinline__ void load_x_quads(float4 (&xr)[MT / 4][2], Rsrc src, OffF rowoff, int mt, int e0, int wave,
+                                             int lane) {
 #pragma unroll
-  for (int p = 0; p < MT / 2; ++p) {
-    const int m = 2 * p + (tid >> 7);
-    const uint4 v = ld128(src, rowoff(m < mt ? m : 0) + uint32_t(e0 + (tid & 127) * 4) * 4u, 0);
-    xr[p] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  for (int p = 0; p < MT / 4; ++p) {
+    const int m = 4 * p + wave;
+    const uint32_t base = rowoff(m < mt ? m : 0) + uint32_t(e0 + lane * 8) * 4u;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint4 v = ld128(src, base, uint32_t(h) * 16u);
+      xr[p][h] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    }
   }
 }
 template <int MT>
-__device__ __forceinline__ void stage_x_pairs(const XPlanes &xs, const float4 (&xr)[MT / 2], int mt, int e0, int ne,
-                                              int k, int tid, int lane) {
+__device__ __forceinline__ void stage_x_quads(const XPlanes &xs, const float4 (&xr)[MT / 4][2], int mt, int e0, int ne,
+                                              int k, int wave, int lane) {
 #pragma unroll
-  for (int p = 0; p < MT / 2; ++p) {
-    const int m = 2 * p + (tid >> 7), e = (tid & 127) * 4;
-    const bool ok = m < mt && e < ne && e0 + e < k;
-    stage_piece(xs, ok ? xr[p] : make_float4(0.f, 0.f, 0.f, 0.f), m, e, lane);
+  for (int p = 0; p < MT / 4; ++p) {
+    const int m = 4 * p + wave, e = lane * 8;
+    float v[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool ok = m < mt && e + 4 * h < ne && e0 + e + 4 * h < k;
+      const float4 f = ok ? xr[p][h] : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[4 * h] = f.x;
+      v[4 * h + 1] = f.y;
+      v[4 * h + 2] = f.z;
+      v[4 * h + 3] = f.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    const GroupScale gs = group_scale(max_lanes4(amax));
+    uint32_t b1[8], b2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) quant_elem(v[i], gs, b1[i], b2[i]);
+    const int sumq = sum_lanes4(quant_sum<8>(b1, b2));
+    const int g = lane >> 2, c = lane & 3;
+    if (g < xs.groups) {
+      const size_t mg = size_t(m) * xs.groups + g;
+      uint2 *pq = reinterpret_cast<uint2 *>(xs.q + mg * kXWords);
+      pq[c] = make_uint2(join2(pack2(b1[0], b1[2]), pack2(b1[4], b1[6])), join2(pack2(b1[1], b1[3]), pack2(b1[5], b1[7])));
+      pq[4 + c] =
+          make_uint2(join2(pack2(b2[0], b2[2]), pack2(b2[4], b2[6])), join2(pack2(b2[1], b2[3]), pack2(b2[5], b2[7])));
+      if (c == 0) {
+        xs.s2[mg] = gs.s1 * 0.00390625f;
+        xs.off[mg] = -8 * sumq;
+      }
+    }
   }
 }
 
