@@ -23,6 +23,85 @@ namespace qnn {
 namespace {
 using dev::sel4u;
 
+// The P parts of a tile meet in LDS (part 0 sums them in order 0+1+2+3),
+// then the split-K exchange and the epilogue.
+template <int MT, int P>
+__device__ __forceinline__ void finish_tile(const I4Launch &a, float (&acc)[MT], float (*red)[MT][64], int wave,
+                                            int part, int lane, int tile, int slice, int slices, int b, bool active) {
+  const I4Layout &l = a.l;
+  const bool swiglu = a.mode == I4_SWIGLU;
+  const int L = l.lanes, j = lane & (L - 1), wl = lane;
+  if (P > 1) {
+    if (part > 0) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) red[wave][m][lane] = acc[m];
+    }
+    __syncthreads();
+    if (part > 0) return;
+#pragma unroll
+    for (int q = 1; q < P; ++q)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[m] += red[wave + q][m][lane];
+  }
+  if (!active) return;
+
+  // 4) Split-K across workgroups: the last slice of a tile to finish sums all
+  //    slices in slice order.  I4_SWIGLU always meets here: the last of the
+  //    2 x slices arrivals of a block sums the gate slices and the up slices.
+  constexpr int PU = MT >= 16 ? 2 : (MT >= 8 ? 4 : (MT >= 4 ? 8 : 16));  // independent partial loads in flight
+  float accu[MT];
+  if (slices > 1 || swiglu) {
+    float *part_p = a.partial + (size_t(tile) * slices + slice) * MT * 64 + lane;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) dev::xstore(part_p + m * 64, acc[m]);
+    unsigned *ctr = &a.counters[size_t(swiglu ? tile >> 1 : tile) * kCounterStride];
+    if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane)) return;
+    const int t0 = swiglu ? tile & ~1 : tile;
+    const float *pt = a.partial + size_t(t0) * slices * MT * 64 + lane;
+    if (swiglu) {  // gate and up partials in one batch of loads
+      const float *pu = pt + size_t(slices) * MT * 64;
+      float gu[2 * MT];
+      dev::sum_slices<2 * MT, (PU > 1 ? PU / 2 : 1)>(  // as many loads in flight as one matrix at PU
+          gu, [&](int s, int m) { return (m < MT ? pt : pu) + (size_t(s) * MT + (m < MT ? m : m - MT)) * 64; },
+          slices);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        acc[m] = gu[m];
+        accu[m] = gu[MT + m];
+      }
+    } else {
+      dev::sum_slices<MT, PU>(
+          acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices);
+    }
+    dev::reset_counter(ctr, lane);
+  }
+
+  // 5) Epilogue: the first lane of each row writes it.
+  if (swiglu) {
+    const int row = b * l.rpb + wl / L;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      if (j == 0 && row < a.n && m < a.m) {
+        if (a.g_out) {
+          a.g_out[size_t(m) * a.y_stride + row] = acc[m];
+          a.u_out[size_t(m) * a.y_stride + row] = accu[m];
+        }
+        a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * accu[m];
+      }
+  } else {
+    const int row = b * l.rpb + lane / L;
+    if (j == 0 && row < a.n) {
+      if (a.mode == I4_ACCUM) {
+        a.y[row] = add_mul_nofma(a.y[row], acc[0], a.prob[0]);  // moe.comp:70
+      } else {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          if (m < a.m) a.y[size_t(m) * a.y_stride + row] = acc[m];
+      }
+    }
+  }
+}
+
 // MF: the inner product on the int8 matrix cores (dot_mf; L = 1, MT >= 4,
 // GSW a multiple of 4), bit-identical to the v_dot4 path.
 template <int MT, int GSW, int T, bool MF>
@@ -120,75 +199,7 @@ void k_int4_matvec(const I4Launch a, const int slices) {
       dev::reduce_lanes<MT>(acc, L);
     }
   }
-  if (P > 1) {
-    if (part > 0) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m) red[wave][m][lane] = acc[m];
-    }
-    __syncthreads();
-    if (part > 0) return;
-#pragma unroll
-    for (int q = 1; q < P; ++q)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) acc[m] += red[wave + q][m][lane];
-  }
-  if (!active) return;
-
-  // 4) Split-K across workgroups: the last slice of a tile to finish sums all
-  //    slices in slice order.  I4_SWIGLU always meets here: the last of the
-  //    2 x slices arrivals of a block sums the gate slices and the up slices.
-  constexpr int PU = MT >= 16 ? 2 : (MT >= 8 ? 4 : (MT >= 4 ? 8 : 16));  // independent partial loads in flight
-  float accu[MT];
-  if (slices > 1 || swiglu) {
-    float *part_p = a.partial + (size_t(tile) * slices + slice) * MT * 64 + lane;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) dev::xstore(part_p + m * 64, acc[m]);
-    unsigned *ctr = &a.counters[size_t(swiglu ? tile >> 1 : tile) * kCounterStride];
-    if (!dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane)) return;
-    const int t0 = swiglu ? tile & ~1 : tile;
-    const float *pt = a.partial + size_t(t0) * slices * MT * 64 + lane;
-    if (swiglu) {  // gate and up partials in one batch of loads
-      const float *pu = pt + size_t(slices) * MT * 64;
-      float gu[2 * MT];
-      dev::sum_slices<2 * MT, (PU > 1 ? PU / 2 : 1)>(  // as many loads in flight as one matrix at PU
-          gu, [&](int s, int m) { return (m < MT ? pt : pu) + (size_t(s) * MT + (m < MT ? m : m - MT)) * 64; },
-          slices);
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        acc[m] = gu[m];
-        accu[m] = gu[MT + m];
-      }
-    } else {
-      dev::sum_slices<MT, PU>(
-          acc, [&](int s, int m) { return pt + (size_t(s) * MT + m) * 64; }, slices);
-    }
-    dev::reset_counter(ctr, lane);
-  }
-
-  // 5) Epilogue: the first lane of each row writes it.
-  if (swiglu) {
-    const int row = b * l.rpb + wl / L;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-      if (j == 0 && row < a.n && m < a.m) {
-        if (a.g_out) {
-          a.g_out[size_t(m) * a.y_stride + row] = acc[m];
-          a.u_out[size_t(m) * a.y_stride + row] = accu[m];
-        }
-        a.y[size_t(m) * a.y_stride + row] = dev::silu(acc[m]) * accu[m];
-      }
-  } else {
-    const int row = b * l.rpb + lane / L;
-    if (j == 0 && row < a.n) {
-      if (a.mode == I4_ACCUM) {
-        a.y[row] = add_mul_nofma(a.y[row], acc[0], a.prob[0]);  // moe.comp:70
-      } else {
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-          if (m < a.m) a.y[size_t(m) * a.y_stride + row] = acc[m];
-      }
-    }
-  }
+  finish_tile<MT, P>(a, acc, red, wave, part, lane, tile, slice, slices, b, active);
 }
 
 // Raw packed rows -> device layout.  One thread per (block, step, lane).

@@ -291,6 +291,30 @@ __device__ __forceinline__ void stage_x(const XPlanes &xs, const float4 (&xr)[MT
   }
 }
 
+// Planes of one (token, group) dword from 8 elements held by this lane; the
+// 4 lanes of the group (aligned, adjacent) meet through DPP.
+__device__ __forceinline__ void stage_dword(const XPlanes &xs, const float (&v)[8], int m, int g, int c) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const GroupScale gs = group_scale(max_lanes4(amax));
+  uint32_t b1[8], b2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) quant_elem(v[i], gs, b1[i], b2[i]);
+  const int sumq = sum_lanes4(quant_sum<8>(b1, b2));
+  if (g < xs.groups) {
+    const size_t mg = size_t(m) * xs.groups + g;
+    uint2 *pq = reinterpret_cast<uint2 *>(xs.q + mg * kXWords);
+    pq[c] = make_uint2(join2(pack2(b1[0], b1[2]), pack2(b1[4], b1[6])), join2(pack2(b1[1], b1[3]), pack2(b1[5], b1[7])));
+    pq[4 + c] =
+        make_uint2(join2(pack2(b2[0], b2[2]), pack2(b2[4], b2[6])), join2(pack2(b2[1], b2[3]), pack2(b2[5], b2[7])));
+    if (c == 0) {
+      xs.s2[mg] = gs.s1 * 0.00390625f;
+      xs.off[mg] = -8 * sumq;
+    }
+  }
+}
+
 // Slices of at most 512 elements, MT a multiple of 4: in pass p wave w stages
 // token 4p + w, lane l elements 8l..8l+7 of the slice (dword l%4 of group
 // l/4), so no thread idles and a lane writes whole plane words.  The planes
@@ -325,26 +349,7 @@ __device__ __forceinline__ void stage_x_quads(const XPlanes &xs, const float4 (&
       v[4 * h + 2] = f.z;
       v[4 * h + 3] = f.w;
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    const GroupScale gs = group_scale(max_lanes4(amax));
-    uint32_t b1[8], b2[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) quant_elem(v[i], gs, b1[i], b2[i]);
-    const int sumq = sum_lanes4(quant_sum<8>(b1, b2));
-    const int g = lane >> 2, c = lane & 3;
-    if (g < xs.groups) {
-      const size_t mg = size_t(m) * xs.groups + g;
-      uint2 *pq = reinterpret_cast<uint2 *>(xs.q + mg * kXWords);
-      pq[c] = make_uint2(join2(pack2(b1[0], b1[2]), pack2(b1[4], b1[6])), join2(pack2(b1[1], b1[3]), pack2(b1[5], b1[7])));
-      pq[4 + c] =
-          make_uint2(join2(pack2(b2[0], b2[2]), pack2(b2[4], b2[6])), join2(pack2(b2[1], b2[3]), pack2(b2[5], b2[7])));
-      if (c == 0) {
-        xs.s2[mg] = gs.s1 * 0.00390625f;
-        xs.off[mg] = -8 * sumq;
-      }
-    }
+    stage_dword(xs, v, m, lane >> 2, lane & 3);
   }
 }
 
