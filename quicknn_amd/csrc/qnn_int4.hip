@@ -23,6 +23,87 @@ namespace qnn {
 namespace {
 using dev::sel4u;
 
+// One tile per workgroup (four parts) and 4-16 tokens: the same sums as
+// below, spread over the four waves.  Every part goes to LDS; wave w then
+// owns tokens w*MT/4 .. (w+1)*MT/4-1: it sums their four parts (order
+// 0+1+2+3), stores their partials, and, when the workgroup's ticket is the
+// last, sums their slices (slice order) and writes their outputs.  The
+// combine's loads are spread over four waves instead of one, so they go out
+// in one or two batches instead of up to five.
+template <int MT>
+__device__ __forceinline__ void finish_tile_wide(const I4Launch &a, float (&acc)[MT], float (*red)[MT][64], int wave,
+                                                 int lane, int tile, int slice, int slices, int b, bool active) {
+  constexpr int TW = MT / 4;                                  // tokens per wave
+  constexpr int PS = TW == 1 ? 32 : (TW == 2 ? 20 : 8);       // slices per batch of loads, one matrix
+  constexpr int PG = TW == 1 ? 16 : (TW == 2 ? 8 : 4);        // slices per batch, gate and up
+  __shared__ int last_wg;
+  const I4Layout &l = a.l;
+  const bool swiglu = a.mode == I4_SWIGLU;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) red[wave][m][lane] = acc[m];
+  __syncthreads();
+  if (!active) return;  // uniform: one tile per workgroup
+  const int m0 = wave * TW;
+  float v[TW], vu[TW];
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    v[i] = red[0][m0 + i][lane];
+    v[i] += red[1][m0 + i][lane];
+    v[i] += red[2][m0 + i][lane];
+    v[i] += red[3][m0 + i][lane];
+  }
+  if (slices > 1 || swiglu) {
+    float *part_p = a.partial + (size_t(tile) * slices + slice) * MT * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < TW; ++i) dev::xstore(part_p + (m0 + i) * 64, v[i]);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partials are at the coherence point
+    __syncthreads();
+    unsigned *ctr = &a.counters[size_t(swiglu ? tile >> 1 : tile) * kCounterStride];
+    if (wave == 0) {
+      const bool last = dev::last_arrival(ctr, unsigned(swiglu ? 2 * slices : slices), lane);
+      if (lane == 0) last_wg = last ? 1 : 0;
+    }
+    __syncthreads();
+    if (!last_wg) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const int t0 = swiglu ? tile & ~1 : tile;
+    const float *pt = a.partial + size_t(t0) * slices * MT * 64 + lane;
+    if (swiglu) {  // gate and up partials of this wave's tokens in one batch
+      const float *pu = pt + size_t(slices) * MT * 64;
+      float gu[2 * TW];
+      dev::sum_slices<2 * TW, PG>(
+          gu, [&](int s, int i) { return (i < TW ? pt : pu) + (size_t(s) * MT + m0 + (i < TW ? i : i - TW)) * 64; },
+          slices);
+#pragma unroll
+      for (int i = 0; i < TW; ++i) {
+        v[i] = gu[i];
+        vu[i] = gu[TW + i];
+      }
+    } else {
+      dev::sum_slices<TW, PS>(
+          v, [&](int s, int i) { return pt + (size_t(s) * MT + m0 + i) * 64; }, slices);
+    }
+    if (wave == 0) dev::reset_counter(ctr, lane);
+  }
+  // Epilogue: the first lane of each row writes this wave's tokens of it.
+  const int row = b * l.rpb + lane / l.lanes;
+  if ((lane & (l.lanes - 1)) != 0 || row >= a.n) return;
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    const int m = m0 + i;
+    if (m >= a.m) continue;
+    if (swiglu) {
+      if (a.g_out) {
+        a.g_out[size_t(m) * a.y_stride + row] = v[i];
+        a.u_out[size_t(m) * a.y_stride + row] = vu[i];
+      }
+      a.y[size_t(m) * a.y_stride + row] = dev::silu(v[i]) * vu[i];
+    } else {
+      a.y[size_t(m) * a.y_stride + row] = v[i];
+    }
+  }
+}
+
 // The P parts of a tile meet in LDS (part 0 sums them in order 0+1+2+3),
 // then the split-K exchange and the epilogue.
 template <int MT, int P>
@@ -31,6 +112,12 @@ __device__ __forceinline__ void finish_tile(const I4Launch &a, float (&acc)[MT],
   const I4Layout &l = a.l;
   const bool swiglu = a.mode == I4_SWIGLU;
   const int L = l.lanes, j = lane & (L - 1), wl = lane;
+  if constexpr (P == 4 && MT >= 4) {
+    if (a.mode != I4_ACCUM) {
+      finish_tile_wide<MT>(a, acc, red, wave, lane, tile, slice, slices, b, active);
+      return;
+    }
+  }
   if (P > 1) {
     if (part > 0) {
 #pragma unroll
