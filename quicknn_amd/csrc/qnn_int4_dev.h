@@ -501,14 +501,26 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
       }
       uint32_t wq[4];
       mf_transpose(wq, mw.w[g]);
+      // Up to 8 tokens: the step's four products first, so that each one's
+      // latency is covered by the others before its swaps read it.
+      mf_i32x4 d4[MT <= 8 ? 4 : 1];
+      if constexpr (MT <= 8) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const uint32_t wd = wq[rq];
+          const long bw = long(wd & 0x0F0F0F0Fu) | (long((wd >> 4) & 0x0F0F0F0Fu) << 32);
+          const mf_i32x4 z = {0, 0, 0, 0};
+          d4[rq] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const uint32_t wd = wq[rq];
         const long bw = long(wd & 0x0F0F0F0Fu) | (long((wd >> 4) & 0x0F0F0F0Fu) << 32);
         const mf_i32x4 z = {0, 0, 0, 0};
-        const mf_i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
         int hi[R], lo[R];
         if constexpr (MT <= 8) {
+          const mf_i32x4 dh = d4[rq];
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
             const auto sw = __builtin_amdgcn_permlane32_swap(dh[r], dh[r + 2], false, false);
@@ -516,6 +528,7 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
             lo[r] = int(sw[1]);
           }
         } else {
+          const mf_i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
           const long al = *reinterpret_cast<const long *>(qa + 8 + 2 * c);
           const mf_i32x4 dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bw, z, 0, 0, 0);
 #pragma unroll
