@@ -292,7 +292,9 @@ __device__ __forceinline__ void stage_x(const XPlanes &xs, const float4 (&xr)[MT
 }
 
 // Planes of one (token, group) dword from 8 elements held by this lane; the
-// 4 lanes of the group (aligned, adjacent) meet through DPP.
+// 4 lanes of the group (aligned, adjacent) meet through DPP.  For the
+// matrix-core dot, which multiplies signed nibbles scaled by 16 (dot_mf), the
+// entry holds s2/16 and no offset.
 __device__ __forceinline__ void stage_dword(const XPlanes &xs, const float (&v)[8], int m, int g, int c) {
   float amax = 0.0f;
 #pragma unroll
@@ -301,17 +303,13 @@ __device__ __forceinline__ void stage_dword(const XPlanes &xs, const float (&v)[
   uint32_t b1[8], b2[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) quant_elem(v[i], gs, b1[i], b2[i]);
-  const int sumq = sum_lanes4(quant_sum<8>(b1, b2));
   if (g < xs.groups) {
     const size_t mg = size_t(m) * xs.groups + g;
     uint2 *pq = reinterpret_cast<uint2 *>(xs.q + mg * kXWords);
     pq[c] = make_uint2(join2(pack2(b1[0], b1[2]), pack2(b1[4], b1[6])), join2(pack2(b1[1], b1[3]), pack2(b1[5], b1[7])));
     pq[4 + c] =
         make_uint2(join2(pack2(b2[0], b2[2]), pack2(b2[4], b2[6])), join2(pack2(b2[1], b2[3]), pack2(b2[5], b2[7])));
-    if (c == 0) {
-      xs.s2[mg] = gs.s1 * 0.00390625f;
-      xs.off[mg] = -8 * sumq;
-    }
+    if (c == 0) xs.s2[mg] = gs.s1 * (0.00390625f * 0.0625f);
   }
 }
 
@@ -405,13 +403,20 @@ __device__ __forceinline__ void dot(float (&acc)[MT], const uint4 (&w)[GSW], con
 // v_mfma_i32_16x16x32_i8 per activation plane (up to 8 tokens: one for both,
 // below): A = the plane (16 tokens x 32 elements; lane l gives
 // token l%16, elements 8c..8c+7 of the group, c = l/16, as plane words 2c and
-// 2c+1), B = the nibbles (32 elements x 16 rows; lane l gives row 16rq + l%16,
-// the same elements: the low then the high nibbles of its dword c).  Both
-// orders are [8c+0,2,4,6, 8c+1,3,5,7], so D[token][row] is the group's exact
-// integer dot of that plane, the sum dot() forms with v_dot4; the fp32 step
-// (isum, then fma with s*s2) is the same, so results are bit-identical to
-// dot().  Lane l holds D[4c + r][l%16], r = 0..3: tokens 4c..4c+3 of row
-// 16rq + l%16.  Token rows >= MT read token 0's plane and are discarded.
+// 2c+1), B = the weights (32 elements x 16 rows; lane l gives row 16rq + l%16,
+// the same elements: the low then the high nibbles of its dword c) as the
+// signed bytes 16 (n - 8): after n ^ 8 a nibble read as signed 4 bits is
+// n - 8, and with the nibble in the high half of its byte the byte is 16 (n -
+// 8), so the -8 needs no offset term and no masking of signs.  Both orders
+// are [8c+0,2,4,6, 8c+1,3,5,7], so 256 D_high + D_low is 16 times the group's
+// exact sum 256 dot(n, q1) + dot(n, q2) - 8 sum(256 q1 + q2) that dot()
+// forms with v_dot4 (an integer below 2^28 with four zero low bits, so its
+// float is exact and 16 times dot()'s), and the planes hold s2 / 16, so
+// s * s2 / 16 is dot()'s scale product over 16 exactly: the fma gives the
+// same float, and results are bit-identical to dot() (while s * s2 / 16 stays
+// a normal float).  Lane l holds D[4c + r][l%16], r = 0..3: tokens 4c..4c+3
+// of row 16rq + l%16.  Token rows >= MT read token 0's plane and are
+// discarded.
 //
 // The weights arrive as the layout stores them, lane l holding row l's 16
 // bytes of each step (one 16-byte load per lane and step: 4-byte loads in that
@@ -493,14 +498,12 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
       const uint32_t *qa = xs.q + (size_t(ta) * xs.groups + g) * kXWords;
       const long ah = *reinterpret_cast<const long *>(qa + aw);
       float s2[R];
-      int off[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        s2[r] = xs.s2[size_t(tk[r]) * xs.groups + g];
-        off[r] = xs.off[size_t(tk[r]) * xs.groups + g];
-      }
+      for (int r = 0; r < R; ++r) s2[r] = xs.s2[size_t(tk[r]) * xs.groups + g];
       uint32_t wq[4];
-      mf_transpose(wq, mw.w[g]);
+      const uint4 ws = make_uint4(mw.w[g].x ^ 0x88888888u, mw.w[g].y ^ 0x88888888u, mw.w[g].z ^ 0x88888888u,
+                                  mw.w[g].w ^ 0x88888888u);  // nibbles n ^ 8: n - 8 as signed nibbles
+      mf_transpose(wq, ws);
       // Up to 8 tokens: the step's four products first, so that each one's
       // latency is covered by the others before its swaps read it.
       mf_i32x4 d4[MT <= 8 ? 4 : 1];
@@ -508,7 +511,7 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
           const uint32_t wd = wq[rq];
-          const long bw = long(wd & 0x0F0F0F0Fu) | (long((wd >> 4) & 0x0F0F0F0Fu) << 32);
+          const long bw = long((wd << 4) & 0xF0F0F0F0u) | (long(wd & 0xF0F0F0F0u) << 32);  // 16 (n - 8)
           const mf_i32x4 z = {0, 0, 0, 0};
           d4[rq] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
         }
@@ -516,7 +519,7 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const uint32_t wd = wq[rq];
-        const long bw = long(wd & 0x0F0F0F0Fu) | (long((wd >> 4) & 0x0F0F0F0Fu) << 32);
+        const long bw = long((wd << 4) & 0xF0F0F0F0u) | (long(wd & 0xF0F0F0F0u) << 32);  // 16 (n - 8)
         const mf_i32x4 z = {0, 0, 0, 0};
         int hi[R], lo[R];
         if constexpr (MT <= 8) {
@@ -539,8 +542,8 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const int isum = (hi[r] << 8) + lo[r] + off[r];
-          acc[rq][r] = fmaf(float(isum), mw.sc[g][rq] * s2[r], acc[rq][r]);
+          const int isum16 = (hi[r] << 8) + lo[r];  // 16 x the exact group sum
+          acc[rq][r] = fmaf(float(isum16), mw.sc[g][rq] * s2[r], acc[rq][r]);
         }
       }
     }
