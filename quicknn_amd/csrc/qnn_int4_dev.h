@@ -462,19 +462,17 @@ __device__ __forceinline__ void load_w_mf(MfWeights<GSW> &mw, Rsrc nib, Rsrc scl
 
 typedef int mf_i32x4 __attribute__((ext_vector_type(4)));
 
-// Up to 8 tokens: both planes in one product.  A row p = 8 * plane + token
-// (plane 0 the high plane), so lane l holds D[4c + r][l%16] = plane c/2, token
-// 4(c%2) + r, and lanes l and l + 32 hold the two planes of the same tokens.
-// A 32-lane swap of D[r] with D[r + 2] (r = 0, 1) leaves every lane with both
-// planes of one token: lanes 0-31 those of tokens 4c + r, lanes 32-63 those of
-// 4(c-2) + 2 + r.  Each lane then finishes 2 (row, token) sums per quarter
-// and step instead of 4, with half the products.
+// Up to 8 tokens: both planes in one product.  A row p = 2 * token + plane
+// (plane 0 the high plane), so lane l holds D[4c + r][l%16] = token 2c + r/2,
+// plane r%2: the high and the low sum of tokens 2c and 2c + 1 sit in the
+// lane's own result registers.  Each lane finishes 2 (row, token) sums per
+// quarter and step instead of 4, with half the products and no lane swaps.
 template <int MT>
 constexpr int mf_per_lane() { return MT <= 8 ? 2 : 4; }
 template <int MT>
 __device__ __forceinline__ int mf_token(int lane, int r) {
   if constexpr (MT <= 8)
-    return 4 * ((lane >> 4) & 1) + 2 * (lane >> 5) + r;
+    return 2 * (lane >> 4) + r;
   else
     return 4 * (lane >> 4) + r;
 }
@@ -486,9 +484,9 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
                                        const XPlanes &xs, int ns, int lane) {
   constexpr int R = mf_per_lane<MT>();
   const int p = lane & 15, c = lane >> 4;
-  const int tp = MT <= 8 ? (p & 7) : p;  // A row token
+  const int tp = MT <= 8 ? (p >> 1) : p;  // A row token
   const int ta = tp < MT ? tp : 0;
-  const int aw = MT <= 8 ? 8 * (p >> 3) + 2 * c : 2 * c;  // A words within the entry
+  const int aw = MT <= 8 ? 8 * (p & 1) + 2 * c : 2 * c;  // A words within the entry
   int tk[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) tk[r] = mf_token<MT>(lane, r) < MT ? mf_token<MT>(lane, r) : 0;
@@ -526,9 +524,8 @@ __device__ __forceinline__ void dot_mf(float (&acc)[4][mf_per_lane<MT>()], const
           const mf_i32x4 dh = d4[rq];
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(dh[r], dh[r + 2], false, false);
-            hi[r] = int(sw[0]);
-            lo[r] = int(sw[1]);
+            hi[r] = dh[2 * r];
+            lo[r] = dh[2 * r + 1];
           }
         } else {
           const mf_i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw, z, 0, 0, 0);
