@@ -473,36 +473,26 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
   for (int it = 0; it < XIT; ++it) {
     const int e = (it * 256 + tid) * 4;
     const float4 v = e < nu * 256 ? xr[it] : make_float4(0.f, 0.f, 0.f, 0.f);
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    const float s1 = amax / 127.0f;
-    const float inv = s1 > 0.0f ? 1.0f / s1 : 0.0f;
-    const float inv2 = inv * 256.0f;
-    const float vv[4] = {v.x, v.y, v.z, v.w};
-    uint32_t hw = 0, lw = 0;
-    int sumq = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float q1 = fminf(127.0f, fmaxf(-127.0f, rintf(vv[j] * inv)));
-      const float r = fmaf(-q1, s1, vv[j]);
-      const float q2 = fminf(127.0f, fmaxf(-127.0f, rintf(r * inv2)));
-      hw |= (uint32_t(int(q1)) & 255u) << (8 * j);
-      lw |= (uint32_t(int(q2)) & 255u) << (8 * j);
-      sumq += 256 * int(q1) + int(q2);
-    }
-    sumq += __shfl_xor(sumq, 1);
-    sumq += __shfl_xor(sumq, 2);  // 16-element sum
-    const int s16 = sumq;
-    const int s32 = s16 + __shfl_xor(s16, 4);
+    // the INT4 kernels' fixed-point staging arithmetic (qnn_int4_dev.h); the
+    // 8 lanes of a 32-group meet through DPP
+    const dev::GroupScale gs =
+        dev::group_scale(dev::max_lanes8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)))));
+    uint32_t b1[4], b2[4];
+    dev::quant_elem(v.x, gs, b1[0], b2[0]);
+    dev::quant_elem(v.y, gs, b1[1], b2[1]);
+    dev::quant_elem(v.z, gs, b1[2], b2[2]);
+    dev::quant_elem(v.w, gs, b1[3], b2[3]);
+    const uint32_t hw = dev::join2(dev::pack2(b1[0], b1[1]), dev::pack2(b1[2], b1[3]));
+    const uint32_t lw = dev::join2(dev::pack2(b2[0], b2[1]), dev::pack2(b2[2], b2[3]));
+    const int s16 = dev::sum_lanes4(dev::quant_sum<4>(b1, b2));  // 16-element sum
+    const int s32 = s16 + int(dev::dpp<0x141>(uint32_t(s16)));
     if (e < U * 256) {
       const int g = e >> 5, k = (e >> 2) & 7;
       xs.h[g][k] = hw;
       xs.l[g][k] = lw;
       if ((lane & 3) == 0) xs.sum16[g][(lane >> 2) & 1] = s16;
       if ((lane & 7) == 0) {
-        xs.s2[g] = s1 * 0.00390625f;
+        xs.s2[g] = gs.s1 * 0.00390625f;
         xs.sum32[g] = s32;
       }
     }
