@@ -204,12 +204,16 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
 
   for (int m0 = 0; m0 < c; m0 += MT) {
     if (m0 > 0) {
-      dev::load_x<MT, GSW>(xr, xsrc, [&](int m) { return xoff(m0 + m); }, min(c - m0, MT), ws0 * L * 32, sgroups * 32,
-                           tid);
       __syncthreads();  // the previous chunk's LDS reads are done
+      dev::stage_x<MT, GSW>(xs, xr, min(c - m0, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
     }
-    if (m0 > 0) dev::stage_x<MT, GSW>(xs, xr, min(c - m0, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
     __syncthreads();
+    // The next chunk's activations are requested now (its staging is done
+    // with these registers), so their latency overlaps this chunk's products
+    // and part sums instead of following them (batch 16: 101.5 -> 100.9 us).
+    if (m0 + MT < c)
+      dev::load_x<MT, GSW>(xr, xsrc, [&](int m) { return xoff(m0 + MT + m); }, min(c - m0 - MT, MT), ws0 * L * 32,
+                           sgroups * 32, tid);
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
@@ -573,19 +577,23 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
   MoEPlanSizes p;
   const int n = a.rows * a.topk;
   p.slots = std::min(a.experts, n);
-  // One token per pass: fewer registers (101 against 126 at 2 tokens), so
-  // five workgroups per CU instead of four; measured faster at 4, 16 and 32
-  // tokens (16: 159 against 167 us) even though an expert with several tokens
-  // makes several passes over its weights in registers.  QNN_MOE_MT (1, 2, 4)
-  // overrides.
+  // One token per pass: fewer registers (at 4 steps per wave 97-114 VGPRs
+  // against 123-126 at 2 tokens); measured faster at 4, 16 and 32 tokens (16:
+  // 159 against 167 us, 100.7 against 123.2 us with the current kernels) even
+  // though an expert with several tokens makes several passes over its
+  // weights in registers.  QNN_MOE_MT (1, 2, 4) overrides.
   p.mt = 1;
   const int fmt = env_int("QNN_MOE_MT", 0);
   if (fmt == 1 || fmt == 2 || fmt == 4) p.mt = fmt;
   // Steps per wave: 8 with one token per pass, 4 with several, measured
   // fastest for 128 experts of 768 x 2048 (one token per pass, 2-64 rows: 8
-  // steps 4-17% faster than 4, e.g. 16 rows 129 -> 114 us; 2 tokens per pass:
-  // 4 steps 14-16% faster than 2 and than 8); QNN_MOE_SPS overrides.  Bounded
-  // by the activation-slice LDS budget.
+  // steps 4-17% faster than 4, e.g. 16 rows 129 -> 114 us, 100.7 against
+  // 118.3 us with the current kernels; 2 tokens per pass: 4 steps 14-16%
+  // faster than 2 and than 8).  One row with its routes given would take 4
+  // (13.36 against 13.63 us), but the launch that computes the routes itself
+  // is faster at 8 (16.55 against 17.91 us) and must sum in the same order as
+  // the routes-given launch, so one row keeps 8.  QNN_MOE_SPS overrides.
+  // Bounded by the activation-slice LDS budget.
   const int forced = env_int("QNN_MOE_SPS", 0);
   auto steps = [&](const I4Layout &l, int) {
     const int lds_cap = int((48 << 10) / (size_t(p.mt) * 4 * l.lanes * (dev::kXWords * 4 + 8)));
