@@ -2188,9 +2188,10 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     float *w = static_cast<float *>(ensure_work(ctx, (hfl + n * set->hidden) * 4));
     a.h = w;
     a.y = w + hfl;
-    ensure_splitk(ctx, p.partial_floats, p.counters);
+    ensure_splitk(ctx, p.partial_floats + p.plan_words, p.counters);
     a.partial = ctx->partial;
     a.counters = ctx->counters;
+    a.plan = reinterpret_cast<int *>(ctx->partial + p.partial_floats);
     a.err = ctx->error_flag;
     ctx->st.int4_calls += 3;
     // One token: one launch (bit-identical to the two below) when every

@@ -226,7 +226,8 @@ struct MoELaunch {
   float *y = nullptr;             // workspace [rows*topk][hidden]
   float *partial = nullptr;
   unsigned *counters = nullptr;
-  int *err = nullptr;  // bit 8: invalid route ids; bit 2: a fused-launch wait for h timed out
+  int *plan = nullptr;  // multi-token launches: slot plans written by k_moe_plan (plan_words words)
+  int *err = nullptr;   // bit 8: invalid route ids; bit 2: a fused-launch wait for h timed out
   // single-launch decode path (one token) only:
   float *partial_dn = nullptr;
   unsigned *counters_dn = nullptr;
@@ -241,6 +242,7 @@ struct MoEPlanSizes {
   int slots = 0, mt = 1, gsw = 4, slices_gu = 1, slices_dn = 1, sps_gu = 1, sps_dn = 1;
   size_t lds_gu = 0, lds_dn = 0;  // dynamic LDS per launch
   size_t partial_floats = 0, counters = 0;
+  size_t plan_words = 0;  // slot plans of the multi-token launches (k_moe_plan)
 };
 // One-token MoE as a single launch: sizes of its workspace and grid.
 struct MoEDecodePlan {

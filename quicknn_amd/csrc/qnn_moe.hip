@@ -7,7 +7,10 @@
 // accumulated as out += p * y in ascending expert id (op 69 for one token,
 // GO_MOE_SCATTER otherwise, moe.comp:70 and :125-126).
 //
-// Here the routes stay on the GPU and a layer's experts take two launches:
+// Here the routes stay on the GPU and a layer's experts take two launches
+// after a small planning launch:
+//   0. plan:    per slot, its expert and the route positions routed to it
+//      (k_moe_plan, from the route ids; no host readback);
 //   1. gate/up: h[R] = silu(W_g[e] x_t) * (W_u[e] x_t) for every route
 //      position R = t*topk + j (token t, expert e = id[R]);
 //   2. down:    y[R] = W_d[e] h[R], then out[t] = sum over the token's routes in
@@ -15,9 +18,7 @@
 //      GO_FILL + accumulate order).
 // The grid is (4 tiles, slot, K-slice); slot s is the s-th smallest expert id
 // present in the routes, so only routed experts' weights are read, each once
-// per launch for all of its tokens.  Every workgroup derives its slot's expert
-// and token positions from the route ids itself (a few LDS operations), so no
-// planning launch or host readback is needed.  Split-K slices of a
+// per launch for all of its tokens.  Split-K slices of a
 // (slot, tile) are combined by the last to finish, and in the down launch the
 // last (slot, tile) of a tile to finish combines the experts, both in a fixed
 // order, so results do not depend on timing.
@@ -118,6 +119,73 @@ __device__ void build_order(MoEPlan &pl, int n, int k, int lane) {
   }
 }
 
+// Multi-token launches: every slot's plan is built once per call by
+// k_moe_plan (the same build_plan / build_order that each workgroup ran
+// itself before) and stored as a record per slot -- expert, position count,
+// active experts, positions -- followed by the route ids and the per-token
+// order.  A k_moe workgroup then loads its slot's record in one batch of
+// loads instead of rebuilding the plan (batch 16: building it twice per
+// workgroup cost 16 us per layer).
+constexpr int kSlotWords = 4 + kMaxPos;
+__global__ __launch_bounds__(64) void k_moe_plan(const MoELaunch a) {
+  __shared__ MoEPlan pl;
+  const int n = a.rows * a.topk, slot = blockIdx.x, lane = threadIdx.x;
+  build_plan(pl, a, n, slot, lane);
+  if (slot == 0) build_order(pl, n, a.topk, lane);
+  dev::wave_lds_sync();
+  int *rec = a.plan + size_t(slot) * kSlotWords;
+  if (lane == 0) {
+    rec[0] = pl.e;
+    rec[1] = pl.c;
+    rec[2] = pl.active;
+    rec[3] = 0;
+  }
+  for (int i = lane; i < kMaxPos; i += 64) rec[4 + i] = i < pl.c ? pl.pos[i] : 0;
+  if (slot == 0) {
+    int *ids = a.plan + size_t(gridDim.x) * kSlotWords;
+    for (int i = lane; i < n; i += 64) {
+      ids[i] = int(pl.ids[i]);
+      ids[n + i] = int(pl.ord[i]);
+    }
+  }
+}
+// Wave 0 loads `slot`'s plan record (and, with IDS, the route ids and the
+// order) into LDS; the caller synchronises.
+template <bool IDS>
+__device__ void load_plan(MoEPlan &pl, const MoELaunch &a, int n, int slot, int slots, int lane) {
+  const int *rec = a.plan + size_t(slot) * kSlotWords;
+  const int r0 = rec[lane], r1 = rec[64 + lane], r2 = rec[128 + min(lane, kSlotWords - 129)];
+  const int c = __shfl(r0, 1), active = __shfl(r0, 2);
+  if (lane == 0) {
+    pl.e = r0;
+    pl.c = c;
+    pl.active = active;
+  }
+  if (lane >= 4) pl.pos[lane - 4] = r0;
+  pl.pos[60 + lane] = r1;
+  if (lane < kSlotWords - 128) pl.pos[124 + lane] = r2;
+  if (IDS) {
+    const int *ids = a.plan + size_t(slots) * kSlotWords;
+    for (int i0 = 0; i0 < n; i0 += 256) {  // 4 ids and orders per lane in flight together
+      int iv[4], ov[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = min(i0 + r * 64 + lane, n - 1);
+        iv[r] = ids[i];
+        ov[r] = ids[n + i];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + r * 64 + lane;
+        if (i < n) {
+          pl.ids[i] = uint32_t(iv[r]);
+          pl.ord[i] = uint8_t(ov[r]);
+        }
+      }
+    }
+  }
+}
+
 // DOWN = false: gate/up launch (a tile is half a 64-lane block: its gate rows
 // in lanes 0-31 and the same up rows in lanes 32-63).  DOWN = true: down
 // launch (a tile is one block) + expert combine.  A workgroup is one tile of
@@ -137,10 +205,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   const int tid = threadIdx.x, lane = tid & 63, wave = dev::wave_id();
 
   __shared__ MoEPlan pl;
-  if (wave == 0) {
-    build_plan(pl, a, n, slot, lane);
-    if (DOWN) build_order(pl, n, a.topk, lane);
-  }
+  if (wave == 0) load_plan<DOWN>(pl, a, n, slot, slots, lane);
   __syncthreads();
   const int e = pl.e, c = pl.c;
   if (e < 0) return;  // fewer routed experts than slots
@@ -320,6 +385,7 @@ void launch_mt(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
   const int tgu = 2 * a.gu.blocks, tdn = a.dn.blocks;
   const int ggu = (tgu + 7) / 8 * 8 * p.slots * p.slices_gu;
   const int gdn = (tdn + 7) / 8 * 8 * p.slots * p.slices_dn;
+  hipLaunchKernelGGL(k_moe_plan, dim3(p.slots), dim3(64), 0, s, a);
   hipLaunchKernelGGL((k_moe<MT, GSW, false>), dim3(ggu), dim3(256), p.lds_gu, s, a, p.slices_gu, p.sps_gu, p.slots);
   hipLaunchKernelGGL((k_moe<MT, GSW, true>), dim3(gdn), dim3(256), p.lds_dn, s, a, p.slices_dn, p.sps_dn, p.slots);
 }
@@ -611,6 +677,7 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
   const int tgu = 2 * a.gu.blocks, tdn = a.dn.blocks;
   p.partial_floats = std::max(size_t(tgu) * p.slices_gu, size_t(tdn) * p.slices_dn) * n * 64;
   p.counters = (size_t(std::max(tgu, tdn)) * p.slots + tdn) * kCounterStride;
+  p.plan_words = size_t(p.slots) * kSlotWords + 2 * size_t(n);
   return p;
 }
 
