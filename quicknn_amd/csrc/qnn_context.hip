@@ -2079,8 +2079,8 @@ int qnn_expert_set_create(qnn_ctx *ctx, const qnn_weight *gate, const qnn_weight
     set->experts = experts;
     set->hidden = hidden;
     set->inter = inter;
-    set->gu = int4_layout(inter, hidden);
-    set->dn = int4_layout(hidden, inter);
+    set->gu = int4_layout(inter, hidden, true);
+    set->dn = int4_layout(hidden, inter, true);
     const size_t gub = set->gu.bytes(), dnb = set->dn.bytes();
     set->bytes = size_t(experts) * (2 * gub + dnb);
     set->source_bytes = size_t(experts) * (2 * size_t(inter) * rbh + size_t(hidden) * rbi);

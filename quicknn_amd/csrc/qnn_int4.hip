@@ -388,7 +388,7 @@ int pick_template(int sps, const int *set, int n) {
 
 }  // namespace
 
-I4Layout int4_layout(int rows, int cols) {
+I4Layout int4_layout(int rows, int cols, bool one_lane) {
   I4Layout l;
   l.rows = rows;
   l.cols = cols;
@@ -398,7 +398,7 @@ I4Layout int4_layout(int rows, int cols) {
   // QNN_I4_LANES selects 2..16 lanes per row instead.
   l.lanes = 1;
   const int forced = env_int("QNN_I4_LANES", 0);
-  if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) l.lanes = forced;
+  if (!one_lane && (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16)) l.lanes = forced;
   l.rpb = 64 / l.lanes;
   l.steps = (l.groups + l.lanes - 1) / l.lanes;
   l.blocks = (rows + l.rpb - 1) / l.rpb;

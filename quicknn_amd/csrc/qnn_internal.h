@@ -139,7 +139,8 @@ struct I4Plan {
 I4Plan int4_plan(const I4Layout &l, int m, int mode);
 void int4_matvec_launch(const I4Launch &a, const I4Plan &p, hipStream_t s);
 void int4_repack_launch(const uint8_t *src, const I4Layout &l, void *dst, hipStream_t s);
-I4Layout int4_layout(int rows, int cols);
+// one_lane: one lane per row whatever QNN_I4_LANES says (the MoE expert kernels assume it).
+I4Layout int4_layout(int rows, int cols, bool one_lane = false);
 void int4_dequant_launch(const I4Layout &l, const void *w, float *out, hipStream_t s);
 
 void misc_fill(float *dst, int n, uint32_t bits, hipStream_t s);

@@ -195,6 +195,10 @@ template <int MT, int GSW, bool DOWN>
 __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices, const int sps, const int slots) {
   extern __shared__ uint4 dyn_lds[];
   __shared__ float red[3][MT][64];
+  // Expert layouts have one lane per row (int4_layout(.., true)), so a
+  // slice is at most 4 x 8 x 32 elements: one pass of activation loads
+  // (x_iters<2>), 12 fewer VGPRs than the lanes-per-row general form.
+  constexpr int XG = GSW <= 8 ? 2 : GSW;
   const int n = a.rows * a.topk;
   const I4Layout &l = DOWN ? a.dn : a.gu;
   const int tiles = DOWN ? l.blocks : 2 * l.blocks;
@@ -240,8 +244,8 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
     const int R = pl.pos[min(m, c - 1)];
     return DOWN ? uint32_t(R) * uint32_t(a.inter) * 4u : uint32_t(R / a.topk) * uint32_t(a.hidden) * 4u;
   };
-  float4 xr[MT][dev::x_iters<GSW>()];
-  dev::load_x<MT, GSW>(xr, xsrc, xoff, min(c, MT), ws0 * L * 32, sgroups * 32, tid);
+  float4 xr[MT][dev::x_iters<XG>()];
+  dev::load_x<MT, XG>(xr, xsrc, xoff, min(c, MT), ws0 * L * 32, sgroups * 32, tid);
   const dev::XPlanes xs = dev::xplanes_at(dyn_lds, MT, 4 * sps * L);
   // The first chunk's activations are requested, then the weights, then the
   // activations are staged (waiting for them alone).  With the plan loaded
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   dev::load_w<GSW>(w, sc, dev::rsrc(wbase, wbytes), dev::rsrc(wbase + l.nib_bytes(), wbytes - l.nib_bytes()), l, b, s0,
                    wl, moff, moff);
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the staging waits for x
-  dev::stage_x<MT, GSW>(xs, xr, min(c, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
+  dev::stage_x<MT, XG>(xs, xr, min(c, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
 
   dev::XPlanes xw = xs;  // this wave's groups
   xw.q = xs.q + size_t(wave) * sps * L * dev::kXWords;
@@ -273,14 +277,14 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   for (int m0 = 0; m0 < c; m0 += MT) {
     if (m0 > 0) {
       __syncthreads();  // the previous chunk's LDS reads are done
-      dev::stage_x<MT, GSW>(xs, xr, min(c - m0, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
+      dev::stage_x<MT, XG>(xs, xr, min(c - m0, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
     }
     __syncthreads();
     // The next chunk's activations are requested now (its staging is done
     // with these registers), so their latency overlaps this chunk's products
     // and part sums instead of following them (batch 16: 101.5 -> 100.9 us).
     if (m0 + MT < c)
-      dev::load_x<MT, GSW>(xr, xsrc, [&](int m) { return xoff(m0 + MT + m); }, min(c - m0 - MT, MT), ws0 * L * 32,
+      dev::load_x<MT, XG>(xr, xsrc, [&](int m) { return xoff(m0 + MT + m); }, min(c - m0 - MT, MT), ws0 * L * 32,
                            sgroups * 32, tid);
     float acc[MT];
 #pragma unroll
@@ -643,6 +647,7 @@ int decode_capacity(int device) {
 }  // namespace
 
 MoEPlanSizes moe_plan(const MoELaunch &a) {
+  if (a.gu.lanes != 1 || a.dn.lanes != 1) fail(QNN_E_INVALID_OP, "MoE expert layouts need one lane per row");
   MoEPlanSizes p;
   const int n = a.rows * a.topk;
   p.slots = std::min(a.experts, n);
