@@ -254,8 +254,16 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   // 92.1 us).
   uint4 w[GSW];
   float sc[GSW];
-  dev::load_w<GSW>(w, sc, dev::rsrc(wbase, wbytes), dev::rsrc(wbase + l.nib_bytes(), wbytes - l.nib_bytes()), l, b, s0,
-                   wl, moff, moff);
+  // Down: the resources end with this block, so steps of a wave past the
+  // block's last step (K = 768 is 24 steps: the fourth wave of an 8-step
+  // slice has none) read zeros instead of the next block's weights (down
+  // traffic was 1.38x the weight bytes).  Gate/up: both matrices through one
+  // resource at a per-lane offset, whose K-slices cover the steps exactly at
+  // the shapes measured.
+  const size_t nib_end = DOWN ? size_t(b + 1) * l.steps * 1024 : l.nib_bytes();
+  const size_t scl_end = DOWN ? size_t(b + 1) * l.quads() * 1024 : wbytes - l.nib_bytes();
+  dev::load_w<GSW>(w, sc, dev::rsrc(wbase, DOWN ? nib_end : wbytes), dev::rsrc(wbase + l.nib_bytes(), scl_end), l, b,
+                   s0, wl, moff, moff);
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the staging waits for x
   dev::stage_x<MT, XG>(xs, xr, min(c, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
 
