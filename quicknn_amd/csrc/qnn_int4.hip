@@ -255,9 +255,9 @@ void k_int4_matvec(const I4Launch a, const int slices) {
   //    5.9 against 6.3 us).
   if constexpr (MF) {
     dev::stage_x_quads<MT>(xs, xr4, a.m, ws0 * L * 32, sgroups * 32, a.k, wave, lane);
-    dev::load_w_mf<GSW>(mw, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, lane);
+    dev::load_w_mf<GSW>(mw, dev::block_nib_rsrc(nb, l, b), dev::block_scl_rsrc(sb, l, b), l, b, s0, lane);
   } else {
-    dev::load_w<GSW>(w, sc, dev::rsrc(nb, l.nib_bytes()), dev::rsrc(sb, l.scale_bytes()), l, b, s0, wl);
+    dev::load_w<GSW>(w, sc, dev::block_nib_rsrc(nb, l, b), dev::block_scl_rsrc(sb, l, b), l, b, s0, wl);
     dev::stage_x<MT, GSW>(xs, xr, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
   }
   __syncthreads();

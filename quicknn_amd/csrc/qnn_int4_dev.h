@@ -85,6 +85,15 @@ __device__ __forceinline__ Rsrc rsrc(const void *base, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(uint32_t(min(bytes, size_t(0xFFFFFFFFu)))),
                                            0x00020000);
 }
+// Resources that end with block b's weights (its nibbles, its scale pieces),
+// so a wave's steps past the block's last step read zeros rather than the
+// next block's bytes (a K-slice longer than the steps left in the block).
+__device__ __forceinline__ Rsrc block_nib_rsrc(const void *nib, const I4Layout &l, int b) {
+  return rsrc(nib, size_t(b + 1) * l.steps * 1024);
+}
+__device__ __forceinline__ Rsrc block_scl_rsrc(const void *scl, const I4Layout &l, int b) {
+  return rsrc(scl, size_t(b + 1) * l.quads() * 1024);
+}
 // AUX = 16 sets SC1: the load is coherent at device (agent) scope, for data
 // another XCD wrote inside the same launch.
 template <int AUX = 0>

@@ -254,16 +254,17 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
   // 92.1 us).
   uint4 w[GSW];
   float sc[GSW];
-  // Down: the resources end with this block, so steps of a wave past the
-  // block's last step (K = 768 is 24 steps: the fourth wave of an 8-step
-  // slice has none) read zeros instead of the next block's weights (down
-  // traffic was 1.38x the weight bytes).  Gate/up: both matrices through one
-  // resource at a per-lane offset, whose K-slices cover the steps exactly at
-  // the shapes measured.
-  const size_t nib_end = DOWN ? size_t(b + 1) * l.steps * 1024 : l.nib_bytes();
-  const size_t scl_end = DOWN ? size_t(b + 1) * l.quads() * 1024 : wbytes - l.nib_bytes();
-  dev::load_w<GSW>(w, sc, dev::rsrc(wbase, DOWN ? nib_end : wbytes), dev::rsrc(wbase + l.nib_bytes(), scl_end), l, b,
-                   s0, wl, moff, moff);
+  // Down: resources that end with this block (K = 768 is 24 steps, so the
+  // fourth wave of an 8-step slice has none and reads zeros instead of the
+  // next block's weights; down traffic was 1.38x the weight bytes).  Gate/up:
+  // both matrices through one resource at a per-lane offset, whose K-slices
+  // cover the steps exactly at the shapes measured.
+  if (DOWN)
+    dev::load_w<GSW>(w, sc, dev::block_nib_rsrc(wbase, l, b), dev::block_scl_rsrc(wbase + l.nib_bytes(), l, b), l, b, s0,
+                     wl);
+  else
+    dev::load_w<GSW>(w, sc, dev::rsrc(wbase, wbytes), dev::rsrc(wbase + l.nib_bytes(), wbytes - l.nib_bytes()), l, b,
+                     s0, wl, moff, moff);
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the staging waits for x
   dev::stage_x<MT, XG>(xs, xr, min(c, MT), ws0 * L * 32, sgroups * 32, kin, tid, lane);
 
@@ -509,8 +510,8 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
                      tid);
   {
     const uint8_t *wb = a.gate_up + size_t(2 * eg + (tile & 1)) * a.gu_stride;
-    dev::load_wq<GG>(w, q, dev::rsrc(wb, lg.nib_bytes()), dev::rsrc(wb + lg.nib_bytes(), lg.scale_bytes()), lg, blk,
-                     s0, lane);
+    dev::load_wq<GG>(w, q, dev::block_nib_rsrc(wb, lg, blk), dev::block_scl_rsrc(wb + lg.nib_bytes(), lg, blk), lg,
+                     blk, s0, lane);
   }
   float sc[GG];
   dev::pick_scales<GG>(sc, q, s0);
@@ -562,8 +563,8 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   uint4 qd[QD];
   {
     const uint8_t *db = a.down + size_t(ed) * a.dn_stride;
-    dev::load_wq<GD>(wd, qd, dev::rsrc(db, ld.nib_bytes()), dev::rsrc(db + ld.nib_bytes(), ld.scale_bytes()), ld, td,
-                     s0d, lane);
+    dev::load_wq<GD>(wd, qd, dev::block_nib_rsrc(db, ld, td), dev::block_scl_rsrc(db + ld.nib_bytes(), ld, td), ld,
+                     td, s0d, lane);
   }
 
   // ---- 3) down: wait for the blocks of h_slot in the K-slice, stage, dot
