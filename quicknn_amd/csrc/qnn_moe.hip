@@ -127,11 +127,25 @@ __device__ void build_order(MoEPlan &pl, int n, int k, int lane) {
 // loads instead of rebuilding the plan (batch 16: building it twice per
 // workgroup cost 16 us per layer).
 constexpr int kSlotWords = 4 + kMaxPos;
-__global__ __launch_bounds__(64) void k_moe_plan(const MoELaunch a) {
+// Workgroups 0 .. slots-1 build one slot's record each; the last one (slot
+// == slots) writes the route ids and the per-token order, in parallel with
+// them.
+__global__ __launch_bounds__(64) void k_moe_plan(const MoELaunch a, const int slots) {
   __shared__ MoEPlan pl;
   const int n = a.rows * a.topk, slot = blockIdx.x, lane = threadIdx.x;
+  if (slot == slots) {
+    for (int i = lane; i < n; i += 64) pl.ids[i] = __float_as_uint(a.routes[i]);
+    dev::wave_lds_sync();
+    build_order(pl, n, a.topk, lane);
+    dev::wave_lds_sync();
+    int *ids = a.plan + size_t(slots) * kSlotWords;
+    for (int i = lane; i < n; i += 64) {
+      ids[i] = int(pl.ids[i]);
+      ids[n + i] = int(pl.ord[i]);
+    }
+    return;
+  }
   build_plan(pl, a, n, slot, lane);
-  if (slot == 0) build_order(pl, n, a.topk, lane);
   dev::wave_lds_sync();
   int *rec = a.plan + size_t(slot) * kSlotWords;
   if (lane == 0) {
@@ -141,13 +155,6 @@ __global__ __launch_bounds__(64) void k_moe_plan(const MoELaunch a) {
     rec[3] = 0;
   }
   for (int i = lane; i < kMaxPos; i += 64) rec[4 + i] = i < pl.c ? pl.pos[i] : 0;
-  if (slot == 0) {
-    int *ids = a.plan + size_t(gridDim.x) * kSlotWords;
-    for (int i = lane; i < n; i += 64) {
-      ids[i] = int(pl.ids[i]);
-      ids[n + i] = int(pl.ord[i]);
-    }
-  }
 }
 // Wave 0 loads `slot`'s plan record (and, with IDS, the route ids and the
 // order) into LDS; the caller synchronises.
@@ -401,7 +408,7 @@ void launch_mt(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
   const int tgu = 2 * a.gu.blocks, tdn = a.dn.blocks;
   const int ggu = (tgu + 7) / 8 * 8 * p.slots * p.slices_gu;
   const int gdn = (tdn + 7) / 8 * 8 * p.slots * p.slices_dn;
-  hipLaunchKernelGGL(k_moe_plan, dim3(p.slots), dim3(64), 0, s, a);
+  hipLaunchKernelGGL(k_moe_plan, dim3(p.slots + 1), dim3(64), 0, s, a, p.slots);
   hipLaunchKernelGGL((k_moe<MT, GSW, false>), dim3(ggu), dim3(256), p.lds_gu, s, a, p.slices_gu, p.sps_gu, p.slots);
   hipLaunchKernelGGL((k_moe<MT, GSW, true>), dim3(gdn), dim3(256), p.lds_dn, s, a, p.slices_dn, p.sps_dn, p.slots);
 }
