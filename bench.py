@@ -632,8 +632,8 @@ def run_cfg5(args, hip) -> dict:
                   "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4), "traffic": None,
                   "kernel": "k_q8_gemm_i8 (+ k_q8_act_quant, the per-32 int8 activation quantiser)",
                   "kernel_us": round(us, 2), "ops_per_launch": int(ops),
-                  "bound_note": "per output and 32-element block: convert, scale product, fma on the VALU "
-                                "(1.8 G lane-ops at this shape)",
+                  "bound_note": "per output and 32-element block: convert and fma on the VALU (1.2 G "
+                                "lane-ops at this shape); the scale products on the fp32 matrix cores",
                   "timing": f"HIP events around {args.steps}x{R} back-to-back calls"},
         cpu_baseline=cpu)
 

@@ -16,10 +16,12 @@
 // 247-258) by the activation quantisation (about 5e-3 normwise for N(0, 1)
 // activations); Linear (qnn_gemm.hip) keeps fp32-level agreement instead.
 //
-// Each block needs its own pair of scales, so the epilogue costs three VALU
-// operations per output per block (convert, scale product, fma): at the cfg5
-// shape 512 x 12288 x 96 blocks that is 1.8 G lane-operations, against 7.7 us
-// of int8 MFMA work -- this kernel is bound by the VALU, not the matrix cores.
+// Each block needs its own pair of scales per output, so the epilogue, not the
+// int8 matrix work, is the cost: at the cfg5 shape 512 x 12288 x 96 blocks
+// there are 604 M (output, block) pairs against 7.7 us of int8 MFMA work.  The
+// scale products dx[m] * dw[n] go to the fp32 matrix cores as outer products,
+// two blocks per instruction (v_mfma_f32_32x32x1_2b_f32), which leaves the
+// VALU two operations per output and block (convert, fma).
 //
 // Tiling: a 256-thread workgroup computes 64 rows x 128 columns; wave w takes
 // rows 32 * (w & 1) and columns 64 * (w >> 1) as two 32 x 32 MFMA tiles.
@@ -30,13 +32,12 @@
 // M-tiles of an N-tile share blockIdx % 8, so they run on one XCD and the
 // weights come from HBM once.
 //
-// VALU economy (the bound): the MFMA results land in VGPRs (this file is
-// built with the VGPR form of MFMA, so no accumulator-register reads), every
-// block-dependent load offset is a scalar offset (no per-block address
-// arithmetic), a block's fp16 weight scale arrives in a 4-byte word (one
-// conversion, selecting the half), and the activation scales reach each lane
-// through LDS.  About 51 VALU instructions per MFMA remain, against the 48
-// of the epilogue itself.
+// VALU economy: the MFMA results land in VGPRs (this file is built with the
+// VGPR form of MFMA, so no accumulator-register reads), every block-dependent
+// load offset is a scalar offset (no per-block address arithmetic), and a
+// block pair's fp16 weight scales arrive in one 4-byte word (each half-wave
+// converts its half).  About 33 VALU instructions per int8 MFMA remain,
+// against the 32 of the convert-and-fma epilogue itself.
 #include "qnn_internal.h"
 
 namespace qnn {
@@ -44,6 +45,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 __device__ __forceinline__ Rsrc rsrc(const void *base, size_t bytes) {
@@ -108,67 +110,61 @@ constexpr int NJ = 2;      // 32-column MFMA tiles per wave (one tile per wave r
 constexpr int kDepth = 4;  // blocks of A and B fragments in flight per wave
 
 // This lane's matrix operands for one block: the A fragment, the B fragments
-// of its NJ column tiles and the 4-byte words holding their fp16 scales (low
-// half for even blocks).
+// of its NJ column tiles, the 4-byte words holding their fp16 scales (low
+// half for even blocks) and the activation scale of its row (lane % 32).
 struct I8Stage {
   v4i a;
   v4i b[NJ];
   uint32_t dw[NJ];
+  float dx;
 };
 // Per-lane parts of the buffer offsets; the block-dependent parts are wave
 // uniform and go in the scalar offset.  Every offset stays inside its buffer
 // (columns past the layout are clamped, blocks past the end are clamped by
 // the caller), so no load relies on the range check.
 struct I8Offsets {
-  uint32_t a, b[NJ], d[NJ];
+  uint32_t a, b[NJ], d[NJ], x;
 };
 
-__device__ __forceinline__ void load_ab(I8Stage &s, Rsrc ar, Rsrc wr, const I8Offsets &o, int kb) {
+// Even stages also load the pair's scales: the word with blocks kb, kb + 1's
+// fp16 weight scales and, per lane, the activation scale of row lane % 32 in
+// block kb + lane / 32.
+template <bool SCALES>
+__device__ __forceinline__ void load_ab(I8Stage &s, Rsrc ar, Rsrc wr, Rsrc dr, const I8Offsets &o, int kb,
+                                        int m_pad) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(ar, int(o.a), kb * 1024, 0);
   s.a = v4i{int(v[0]), int(v[1]), int(v[2]), int(v[3])};
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const auto w = __builtin_amdgcn_raw_buffer_load_b128(wr, int(o.b[j]), kb * 2048, 0);
     s.b[j] = v4i{int(w[0]), int(w[1]), int(w[2]), int(w[3])};
-    s.dw[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, int(o.d[j]), (kb >> 3) * 1024 + (kb & 6) * 2, 0);
+    if (SCALES) s.dw[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, int(o.d[j]), (kb >> 3) * 1024 + (kb & 6) * 2, 0);
   }
+  if (SCALES) s.dx = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(dr, int(o.x), kb * m_pad * 4, 0));
 }
 
-// Activation scales go through LDS, per wave: the wave's 32 rows x kDepth
-// blocks are one 8-byte load per lane, issued a group of blocks ahead and
-// written to the wave's own LDS slot at the top of the group that uses them
-// (a wave's own LDS write and reads stay in order: no barrier).  Each lane
-// then reads its 16 rows per block as 4 x 16 bytes (broadcast within each
-// half-wave).  Held as registers, the same scales would take 16 VGPRs per
-// block in flight.
-static_assert(kDepth == 4, "a group's scales are 32 rows x 4 blocks, two floats per lane");
-
-__device__ __forceinline__ float2 load_scales(Rsrc dr, uint32_t vx, int m_pad, int kb0, int last, int lane) {
-  kb0 = min(kb0, last);
-  const int blk = min(lane >> 4, last - kb0);  // blocks past the end reload the last one (never used)
-  const auto v = __builtin_amdgcn_raw_buffer_load_b64(dr, int(vx + uint32_t(blk * m_pad * 4)), kb0 * m_pad * 4, 0);
-  return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
-}
-
-__device__ __forceinline__ void block_step(float (&acc)[NJ][16], const I8Stage &s, const float4 *xs, int hi,
-                                           bool odd) {
-  float dw[NJ];
+// Two consecutive blocks (kb even, kb + 1): the scale products dx[m] * dw[n]
+// of both 32 x 32 tiles are formed on the fp32 matrix cores as one
+// two-block outer product (v_mfma_f32_32x32x1_2b_f32: lanes 0..31 hold block
+// kb's scales, lanes 32..63 block kb + 1's, and each product is one rounded
+// multiply, the value a VALU multiply gives), in the register layout of the
+// int32 tiles.  The VALU is left with the conversion and the fma: two
+// operations per output and block instead of three.  With `second` false
+// (an odd block count's last block) only block kb is accumulated.
+__device__ __forceinline__ void block_pair(float (&acc)[NJ][16], const I8Stage &s0, const I8Stage &s1, int hi,
+                                           bool second) {
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) dw[j] = half_to_f(odd ? s.dw[j] >> 16 : s.dw[j]);
-  v16i d[NJ];
+  for (int j = 0; j < NJ; ++j) {
+    const float wb = half_to_f(s0.dw[j] >> (16 * hi));  // the word holds blocks kb (low) and kb + 1
+    const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(s0.dx, wb, v32f{}, 0, 0, 0);
+    const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(s0.a, s0.b[j], v16i{}, 0, 0, 0);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) d[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(s.a, s.b[j], v16i{}, 0, 0, 0);
+    for (int i = 0; i < 16; ++i)  // lane holds C[8 (i / 4) + 4 (lane / 32) + i % 4][lane % 32]
+      acc[j][i] = fmaf(float(d0[i]), pr[i], acc[j][i]);
+    if (second) {
+      const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(s1.a, s1.b[j], v16i{}, 0, 0, 0);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float4 x = xs[2 * q + hi];  // rows 8q + 4*hi + 0..3 of the wave's 32
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const float dq[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 4 * q + r;  // lane holds C[8q + 4*(lane/32) + r][lane%32]
-        acc[j][i] = fmaf(float(d[j][i]), dq[r] * dw[j], acc[j][i]);
-      }
+      for (int i = 0; i < 16; ++i) acc[j][i] = fmaf(float(d1[i]), pr[16 + i], acc[j][i]);
     }
   }
 }
@@ -176,7 +172,6 @@ __device__ __forceinline__ void block_step(float (&acc)[NJ][16], const I8Stage &
 // A workgroup computes 64 rows x 64*NJ columns: wave w takes rows 32*(w & 1)
 // and NJ column tiles of 32 from 32*NJ*(w >> 1).
 __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
-  __shared__ float4 xs_all[4][2][kDepth][8];  // [wave][slot][block][32 rows / 4]
   const int b = blockIdx.x;
   const int xcd = b & 7, kq = b >> 3;
   const int qn = kq / g.mtiles;
@@ -188,8 +183,9 @@ __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
   const int hi = lane >> 5;
   const Rsrc ar = rsrc(g.afrag, size_t(g.m_pad) * g.kb_n * 32);
   const Rsrc wr = rsrc(g.w, g.l.total);
-  const Rsrc dr = rsrc(g.dx, size_t(g.kb_n) * g.m_pad * 4);
-  float2 *xw = reinterpret_cast<float2 *>(&xs_all[wave][0][0][0]);  // this wave's two slots
+  // One block past the last is part of the workspace: a pair that starts at
+  // the last block reads its (unused) second scales there.
+  const Rsrc dr = rsrc(g.dx, size_t(g.kb_n + 1) * g.m_pad * 4);
 
   I8Offsets o;
   o.a = uint32_t((size_t(m32) * g.kb_n * 64 + lane) * 16);
@@ -200,8 +196,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
     o.b[j] = uint32_t(((t0 * 16 + hi) * 64 + (n & 63)) * 16);
     o.d[j] = uint32_t(g.l.side1_off + (t0 * 64 + (n & 63)) * 16);
   }
-  // lane l loads rows 2 * (l % 16) .. + 1 of block l / 16 of a group
-  const uint32_t vx = uint32_t((m32 * 32 + 2 * (lane & 15)) * 4);
+  o.x = uint32_t((m32 * 32 + (lane & 31) + hi * g.m_pad) * 4);
 
   float acc[NJ][16];
 #pragma unroll
@@ -209,42 +204,31 @@ __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
   const int last = g.kb_n - 1;
-  // In flight at the top of each group: that group's scales, then its kDepth
-  // blocks of A and B (the same order as the loop leaves them; the
-  // scheduling barriers keep it, so the wait counts at the loop head need not
-  // be conservative).
-  float2 hx = load_scales(dr, vx, g.m_pad, 0, last, lane);
-  __builtin_amdgcn_sched_barrier(0);
+  // kDepth blocks of operands in flight at the top of each group (the
+  // scheduling barriers keep the issue order, so the wait counts at the loop
+  // head need not be conservative).
   I8Stage s[kDepth];
 #pragma unroll
-  for (int p = 0; p < kDepth; ++p) {
-    load_ab(s[p], ar, wr, o, min(p, last));
+  for (int p = 0; p < kDepth; p += 2) {
+    load_ab<true>(s[p], ar, wr, dr, o, min(p, last), g.m_pad);
+    load_ab<false>(s[p + 1], ar, wr, dr, o, min(p + 1, last), g.m_pad);
     __builtin_amdgcn_sched_barrier(0);
   }
 
   const int kb_main = g.kb_n - g.kb_n % kDepth;
-  int slot = 0;
   for (int kb = 0; kb < kb_main; kb += kDepth) {
-    xw[slot * 64 + lane] = hx;  // [block lane/16][rows 2*(lane%16) ..]
-    hx = load_scales(dr, vx, g.m_pad, kb + kDepth, last, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    const float4 *xc = &xs_all[wave][slot][0][0];
 #pragma unroll
-    for (int p = 0; p < kDepth; ++p) {
-      block_step(acc, s[p], xc + p * 8, hi, p & 1);
-      load_ab(s[p], ar, wr, o, min(kb + p + kDepth, last));
+    for (int p = 0; p < kDepth; p += 2) {
+      block_pair(acc, s[p], s[p + 1], hi, true);
+      load_ab<true>(s[p], ar, wr, dr, o, min(kb + p + kDepth, last), g.m_pad);
+      load_ab<false>(s[p + 1], ar, wr, dr, o, min(kb + p + 1 + kDepth, last), g.m_pad);
       __builtin_amdgcn_sched_barrier(0);
     }
-    slot ^= 1;
   }
-  // The last kb_n % kDepth blocks sit in s[0 ..], their scales in hx.
-  if (kb_main < g.kb_n) {
-    xw[slot * 64 + lane] = hx;
-    const float4 *xc = &xs_all[wave][slot][0][0];
+  // The last kb_n % kDepth blocks sit in s[0 ..].
 #pragma unroll
-    for (int p = 0; p < kDepth - 1; ++p)
-      if (kb_main + p < g.kb_n) block_step(acc, s[p], xc + p * 8, hi, p & 1);
-  }
+  for (int p = 0; p < kDepth; p += 2)
+    if (kb_main + p < g.kb_n) block_pair(acc, s[p], s[p + 1], hi, kb_main + p + 1 < g.kb_n);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int col = n0 + 32 * j + (lane & 31);
@@ -261,7 +245,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
 
 size_t q8_i8_workspace(int M, int K) {
   const int m_pad = (M + 63) / 64 * 64;
-  return ((size_t(m_pad) * K + 255) & ~size_t(255)) + size_t(m_pad) * (K / 32) * 4;
+  return ((size_t(m_pad) * K + 255) & ~size_t(255)) + size_t(m_pad) * (K / 32 + 1) * 4;
 }
 
 void q8_gemm_i8_launch(const float *a, int M, int K, int N, const GGLayout &l, const void *w, void *ws, float *c,

@@ -126,8 +126,11 @@ def run_int8(ctx, w, a, n):
     return out
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 32, 32), (3, 96, 100), (5, 160, 70), (7, 224, 64), (33, 256, 257),
-                                   (64, 288, 64), (100, 1024, 130), (130, 3072, 128)])
+# K = 32 .. 3072: block counts 1, 2, 3, 5, 7, 8, 9, 10, 32 and 96 (the kernel
+# takes blocks in pairs and groups of four, so every remainder is covered).
+@pytest.mark.parametrize("m,k,n", [(1, 32, 32), (9, 64, 96), (3, 96, 100), (5, 160, 70), (7, 224, 64),
+                                   (33, 256, 257), (64, 288, 64), (2, 320, 33), (100, 1024, 130),
+                                   (130, 3072, 128)])
 def test_int8_gemm_bit_identical_to_oracle(ctx, rng, m, k, n):
     a = rng.standard_normal((m, k)).astype(np.float32)
     a[0, :32] = 0.0  # a zero block: d = 0
