@@ -125,10 +125,31 @@ __device__ __forceinline__ void finish_tile(const I4Launch &a, float (&acc)[MT],
     }
     __syncthreads();
     if (part > 0) return;
+    if constexpr (P <= 4) {
 #pragma unroll
-    for (int q = 1; q < P; ++q)
+      for (int q = 1; q < P; ++q)
 #pragma unroll
-      for (int m = 0; m < MT; ++m) acc[m] += red[wave + q][m][lane];
+        for (int m = 0; m < MT; ++m) acc[m] += red[wave + q][m][lane];
+    } else {
+      // An 8- or 16-wave workgroup over the whole K-range: its parts are
+      // summed as P / 4 four-wave slices and their split-K combine would sum
+      // them (four parts in order, then the slices in order from zero), so
+      // the result is the same bit for bit.
+      float tot[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) tot[m] = 0.0f;
+#pragma unroll
+      for (int g = 0; g < P / 4; ++g)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          float q = g == 0 ? acc[m] : red[wave + 4 * g][m][lane];
+#pragma unroll
+          for (int r = 1; r < 4; ++r) q += red[wave + 4 * g + r][m][lane];
+          tot[m] += q;
+        }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[m] = tot[m];
+    }
   }
   if (!active) return;
 
@@ -191,12 +212,16 @@ __device__ __forceinline__ void finish_tile(const I4Launch &a, float (&acc)[MT],
 
 // MF: the inner product on the int8 matrix cores (dot_mf; L = 1, MT >= 4,
 // GSW a multiple of 4), bit-identical to the v_dot4 path.
-template <int MT, int GSW, int T, bool MF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MF ? (MT <= 8 ? 6 : 5) : 1)))
+// W = 4 waves per workgroup, or (one token, one tile, I4_STORE) 8 or 16: one
+// workgroup over a K-range that two or four four-wave slices would split, so
+// its parts meet in LDS instead of in a cross-workgroup exchange.
+template <int MT, int GSW, int T, bool MF, int W = 4>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(MF ? (MT <= 8 ? 6 : 5) : 1)))
 void k_int4_matvec(const I4Launch a, const int slices) {
+  static_assert(W == 4 || (MT == 1 && T == 1 && !MF && (W == 8 || W == 16)), "wide workgroups: one token, one tile");
   extern __shared__ uint4 dyn_lds[];
-  __shared__ float red[4][MT][64];
-  constexpr int P = 4 / T;  // waves per tile: parts of the workgroup's K-slice
+  __shared__ float red[W][MT][64];
+  constexpr int P = W / T;  // waves per tile: parts of the workgroup's K-slice
   const int wave = dev::wave_id(), tid = threadIdx.x, lane = tid & 63;
   const bool swiglu = a.mode == I4_SWIGLU;
   // I4_SWIGLU with one tile per workgroup: units are padded to groups of 16 so
@@ -224,9 +249,12 @@ void k_int4_matvec(const I4Launch a, const int slices) {
   float4 xr4[MF ? MT / 4 : 1][2];
   const dev::Rsrc xsrc = dev::rsrc(a.x, size_t(a.m) * a.x_stride * 4);
   auto xrow = [&](int m) { return uint32_t(m) * uint32_t(a.x_stride) * 4u; };
+  // (Wide workgroups: the first four waves load and stage the slice, which
+  // the planner keeps within their x_iters passes.)
+  const bool xstager = W == 4 || tid < 256;
   if constexpr (MF)
     dev::load_x_quads<MT>(xr4, xsrc, xrow, a.m, ws0 * L * 32, wave, lane);
-  else
+  else if (xstager)
     dev::load_x<MT, GSW>(xr, xsrc, xrow, a.m, ws0 * L * 32, sgroups * 32, tid);
   int tile = unit * T + wave / P;
   if (swiglu && T == 1) tile = 2 * ((unit >> 4) * 8 + (unit & 7)) + ((unit >> 3) & 1);
@@ -258,7 +286,7 @@ void k_int4_matvec(const I4Launch a, const int slices) {
     dev::load_w_mf<GSW>(mw, dev::block_nib_rsrc(nb, l, b), dev::block_scl_rsrc(sb, l, b), l, b, s0, lane);
   } else {
     dev::load_w<GSW>(w, sc, dev::block_nib_rsrc(nb, l, b), dev::block_scl_rsrc(sb, l, b), l, b, s0, wl);
-    dev::stage_x<MT, GSW>(xs, xr, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
+    if (xstager) dev::stage_x<MT, GSW>(xs, xr, a.m, ws0 * L * 32, sgroups * 32, a.k, tid, lane);
   }
   __syncthreads();
 
@@ -331,6 +359,17 @@ __global__ void k_int4_dequant(I4Layout l, const uint4 *__restrict__ nib, const 
 
 template <int MT, int GSW, bool MF>
 void launch_tpw(const I4Launch &a, const I4Plan &p, hipStream_t st) {
+  if constexpr (MT == 1 && !MF) {
+    if (p.wg_waves == 16) {
+      hipLaunchKernelGGL((k_int4_matvec<1, GSW, 1, false, 16>), dim3(p.grid), dim3(1024), p.lds, st, a, p.slices);
+      return;
+    }
+    if (p.wg_waves == 8) {
+      hipLaunchKernelGGL((k_int4_matvec<1, GSW, 1, false, 8>), dim3(p.grid), dim3(512), p.lds, st, a, p.slices);
+      return;
+    }
+  }
+  if (p.wg_waves != 4) fail(QNN_E_INVALID_OP, "int4 plan: wide workgroups take one token");
   switch (p.tiles_per_wg) {
     case 1: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 1, MF>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
     case 2: hipLaunchKernelGGL((k_int4_matvec<MT, GSW, 2, MF>), dim3(p.grid), dim3(256), p.lds, st, a, p.slices); break;
@@ -453,6 +492,16 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   p.lds = dev::xplanes_bytes(p.mt, P * sps * l.lanes);
   const int grid_units = mode == I4_SWIGLU && p.tiles_per_wg == 1 ? (tiles + 15) / 16 * 16 : (units + 7) / 8 * 8;
   p.grid = grid_units * p.slices;
+  // One token over one-lane rows whose K-range splits evenly into 2 or 4
+  // four-wave slices: one 8- or 16-wave workgroup per tile instead, with no
+  // cross-workgroup exchange (QNN_I4_WIDE=0 keeps the slices).
+  if (mode == I4_STORE && p.mt == 1 && p.tiles_per_wg == 1 && l.lanes == 1 && (p.slices == 2 || p.slices == 4) &&
+      l.steps == P * sps * p.slices && env_int("QNN_I4_WIDE", 1) != 0) {
+    p.wg_waves = 4 * p.slices;
+    p.slices = 1;
+    p.lds = dev::xplanes_bytes(p.mt, p.wg_waves * sps * l.lanes);
+    p.grid = grid_units;
+  }
   p.partial_floats = p.slices > 1 || mode == I4_SWIGLU ? size_t(tiles) * p.slices * p.mt * 64 : 0;
   p.counters = size_t(tiles) * kCounterStride;
   return p;

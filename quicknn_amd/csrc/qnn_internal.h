@@ -131,6 +131,7 @@ struct I4Launch {
 };
 struct I4Plan {
   int mt = 1, gsw = 1, slices = 1, grid = 0, steps_per_slice = 1, tiles_per_wg = 1;
+  int wg_waves = 4;           // 8 or 16: one workgroup takes what 2 or 4 four-wave slices would
   size_t lds = 0;             // dynamic LDS bytes
   size_t partial_floats = 0;  // split-K scratch
   size_t counters = 0;

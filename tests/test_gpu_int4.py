@@ -197,6 +197,28 @@ def test_lane_layouts_and_tile_groupings(ctx, rng, monkeypatch, lanes, tpw):
         assert normwise_rel_err(got8[r], oracle.cpu_linear(pg, oracle.ENC_INT4, x8[r], 2048, 768)) <= TOL, r
 
 
+@pytest.mark.parametrize("n,k", [(6144, 2048), (1000, 1024), (130, 2040), (70, 2048), (300, 2560)])
+def test_one_token_wide_workgroups_match_slices(ctx, rng, monkeypatch, n, k):
+    """One token whose K-range splits evenly into 2 or 4 four-wave slices runs as one 8- or
+    16-wave workgroup per tile (no cross-workgroup exchange): bit-identical to the split-K
+    launch (QNN_I4_WIDE=0) and within tolerance of the CPU path, including a ragged last
+    group (K = 2040), a partial last block of rows and a K-range (2560: five slices) that
+    keeps the split-K launch."""
+    p = make_int4(rng, n, k)
+    w = hip.MemoryBlock.int4(p)
+    x = rng.standard_normal(k).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
+    got = {}
+    for wide in ("1", "0"):
+        monkeypatch.setenv("QNN_I4_WIDE", wide)
+        ctx.Int4Linear(dst, src, w, 1, k, n)
+        got[wide] = ctx.Download(dst)
+    assert np.array_equal(got["1"].view(np.uint32), got["0"].view(np.uint32)), (n, k)
+    assert normwise_rel_err(got["1"], oracle.cpu_linear(p, oracle.ENC_INT4, x, k, n)) <= TOL
+    ctx.Recycle(src)
+    ctx.Recycle(dst)
+
+
 @pytest.mark.parametrize("rows,tpw", [(4, 1), (5, 1), (8, 1), (8, 2), (6, 4)])
 def test_multi_token_matrix_cores_match_dot4(ctx, rng, monkeypatch, rows, tpw):
     """4-8 tokens over one-lane rows with 4 steps per wave run the inner product on the int8
