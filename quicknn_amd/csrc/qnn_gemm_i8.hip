@@ -23,8 +23,8 @@
 // two blocks per instruction (v_mfma_f32_32x32x1_2b_f32), which leaves the
 // VALU two operations per output and block (convert, fma).
 //
-// Tiling: a 256-thread workgroup computes 64 rows x 128 columns; wave w takes
-// rows 32 * (w & 1) and columns 64 * (w >> 1) as two 32 x 32 MFMA tiles.
+// Tiling: a 256-thread workgroup computes 64 rows x 192 columns; wave w takes
+// rows 32 * (w & 1) and columns 96 * (w >> 1) as three 32 x 32 MFMA tiles.
 // Activations come pre-arranged in MFMA fragment order (16 bytes per lane and
 // block, one coalesced 1 KiB load per 32 rows); weight fragments are read
 // straight from the tiled Q8_0 layout (lane l: row l % 32 of the tile, the
@@ -105,8 +105,8 @@ struct I8GemmArgs {
 };
 
 constexpr int TM = 64;
-constexpr int NJ = 2;      // 32-column MFMA tiles per wave (one tile per wave ran 10% slower: more A and
-                           // scale traffic per MFMA outweighs the extra waves)
+constexpr int NJ = 3;      // 32-column MFMA tiles per wave: fewer A and scale bytes per MFMA (1 -> 2 -> 3
+                           // tiles: 87 -> 65 -> 61 us at cfg5) outweigh the waves lost (5 -> 3 -> 2 per SIMD)
 constexpr int kDepth = 4;  // blocks of A and B fragments in flight per wave
 
 // This lane's matrix operands for one block: the A fragment, the B fragments
