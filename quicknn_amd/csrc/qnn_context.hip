@@ -648,7 +648,7 @@ void run_int4(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int m
       a.g_out = g_out + size_t(r0) * out_dim;
       a.u_out = u_out + size_t(r0) * out_dim;
     }
-    const I4Plan p = int4_plan(l, m, mode);
+    const I4Plan p = int4_plan(l, m, mode, true);
     if (fixed) {
       misc_fill(reinterpret_cast<float *>(fixed->counters), int(p.counters), 0u, ctx->stream);
       a.partial = fixed->partial;

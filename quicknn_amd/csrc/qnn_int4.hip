@@ -444,7 +444,7 @@ I4Layout int4_layout(int rows, int cols, bool one_lane) {
   return l;
 }
 
-I4Plan int4_plan(const I4Layout &l, int m, int mode) {
+I4Plan int4_plan(const I4Layout &l, int m, int mode, bool wide) {
   I4Plan p;
   p.mt = m <= 1 ? 1 : (m <= 2 ? 2 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16)));
   const int tiles = mode == I4_SWIGLU ? 2 * l.blocks : l.blocks;
@@ -494,8 +494,10 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode) {
   p.grid = grid_units * p.slices;
   // One token over one-lane rows whose K-range splits evenly into 2 or 4
   // four-wave slices: one 8- or 16-wave workgroup per tile instead, with no
-  // cross-workgroup exchange (QNN_I4_WIDE=0 keeps the slices).
-  if (mode == I4_STORE && p.mt == 1 && p.tiles_per_wg == 1 && l.lanes == 1 && (p.slices == 2 || p.slices == 4) &&
+  // cross-workgroup exchange (QNN_I4_WIDE=0 keeps the slices).  Only where
+  // the caller launches k_int4_matvec (`wide`): the fused MLP builds its down
+  // items from the four-wave slices.
+  if (wide && mode == I4_STORE && p.mt == 1 && p.tiles_per_wg == 1 && l.lanes == 1 && (p.slices == 2 || p.slices == 4) &&
       l.steps == P * sps * p.slices && env_int("QNN_I4_WIDE", 1) != 0) {
     p.wg_waves = 4 * p.slices;
     p.slices = 1;

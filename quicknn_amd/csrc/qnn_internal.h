@@ -137,7 +137,9 @@ struct I4Plan {
   size_t counters = 0;
 };
 // Launch geometry for m tokens (at most 16 per launch) in the given mode.
-I4Plan int4_plan(const I4Layout &l, int m, int mode);
+// wide: the plan may take 8- or 16-wave workgroups (k_int4_matvec only; the
+// fused kernels build their items from the four-wave plan).
+I4Plan int4_plan(const I4Layout &l, int m, int mode, bool wide = false);
 void int4_matvec_launch(const I4Launch &a, const I4Plan &p, hipStream_t s);
 void int4_repack_launch(const uint8_t *src, const I4Layout &l, void *dst, hipStream_t s);
 // one_lane: one lane per row whatever QNN_I4_LANES says (the MoE expert kernels assume it).

@@ -33,7 +33,11 @@ def mlp(ctx, hip, layers, x0, hidden, inter):
     return hs, outs
 
 
-@pytest.mark.parametrize("hidden,inter,nl", [(2560, 9728, 3), (1024, 3072, 2), (2048, 768, 2), (512, 1536, 1)])
+# inter 2048 and 1024: down K-ranges of 64 and 32 steps, which the per-op
+# one-token matvec runs as 16- and 8-wave workgroups while the fused kernel
+# keeps its four-wave slices.
+@pytest.mark.parametrize("hidden,inter,nl", [(2560, 9728, 3), (1024, 3072, 2), (2048, 768, 2), (512, 1536, 1),
+                                             (1024, 2048, 2), (768, 1024, 1)])
 def test_fused_equals_per_op(ctx, rng, monkeypatch, hidden, inter, nl):
     from quicknn_amd import hip
 
@@ -52,8 +56,8 @@ def test_fused_equals_per_op(ctx, rng, monkeypatch, hidden, inter, nl):
     g, u, d = layers[0]
     want = oracle.cpu_mlp(g.data, u.data, d.data, oracle.ENC_INT4, x0, hidden, inter)[0]
     assert normwise_rel_err(y_f[0], want) < 1e-3
-    if (hidden, inter) == (2560, 9728):
-        assert fused == nl  # the benchmark shape runs fused
+    if (hidden, inter) in ((2560, 9728), (1024, 2048), (768, 1024)):
+        assert fused == nl  # the benchmark shape and the short down K-ranges run fused
 
 
 def test_recorded_swiglu_settles_on_other_calls(ctx, rng):
