@@ -170,6 +170,11 @@ int qnn_last_error(char *buf, int len);
 int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out);
 int qnn_ctx_destroy(qnn_ctx *ctx);
 int qnn_get_status(qnn_ctx *ctx, qnn_status *out);
+/* Re-reads the QNN_* tuning switches (INTEGRATION.md lists them) from the
+ * environment.  They are read once when a context is created, not per call;
+ * this picks up a change made afterwards (tests and sweeps).  No reference
+ * counterpart. */
+int qnn_reload_tuning(void);
 
 /* ---------------------------------------------------------------------------
  * Resident tensors (Context.API.inc:79-106)
@@ -289,9 +294,11 @@ int qnn_int4_linear_noalloc(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, cons
                             int in_dim, int out_dim);
 
 /* TrySwiGLUVector (Context.API.inc:132-133, Implementation.inc:1003-1056):
- * dst[o] = silu(gate.x)[o] * (up.x)[o].  Returns QNN_OK, or QNN_NOT_HANDLED
- * where the reference returns False (unsupported dtype mix, or the pair does
- * not fit the weight budget and is not resident).  A native-INT4 pair is
+ * dst[o] = silu(gate.x)[o] * (up.x)[o].  Handles two GGUF weights (op 67),
+ * two native INT4 weights (op 68) and two native F32/BF16 weights in any mix
+ * (op 66, one pass over both rows).  Returns QNN_OK, or QNN_NOT_HANDLED
+ * where the reference returns False (any other mix, or the pair does not fit
+ * the weight budget and is not resident).  A native-INT4 pair is
  * recorded and launched by the next call on the context; when that call is
  * the qnn_int4_linear that reads dst (the MLP's down projection, one row),
  * both run as one launch with results identical to two (QNN_FUSE_MLP=0 turns

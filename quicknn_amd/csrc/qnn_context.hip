@@ -147,6 +147,37 @@ struct qnn_ctx_s {
 
 namespace qnn {
 namespace {
+Tuning g_tuning;
+int env_int(const char *name, int dflt) {
+  const char *v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+}  // namespace
+
+const Tuning &tuning() { return g_tuning; }
+void reload_tuning() {
+  Tuning t;
+  t.group_linear = env_int("QNN_GROUP_LINEAR", t.group_linear);
+  t.fuse_mlp = env_int("QNN_FUSE_MLP", t.fuse_mlp);
+  t.fuse_moe = env_int("QNN_FUSE_MOE", t.fuse_moe);
+  t.q8_gemm_min_rows = env_int("QNN_Q8_GEMM_MIN_ROWS", t.q8_gemm_min_rows);
+  t.attn_wgs = env_int("QNN_ATTN_WGS", t.attn_wgs);
+  t.attn_min_chunk = env_int("QNN_ATTN_MIN_CHUNK", t.attn_min_chunk);
+  t.gemm_nw = env_int("QNN_GEMM_NW", t.gemm_nw);
+  t.gemm_mb = env_int("QNN_GEMM_MB", t.gemm_mb);
+  t.gg_bw = env_int("QNN_GG_BW", t.gg_bw);
+  t.i4_mfma = env_int("QNN_I4_MFMA", t.i4_mfma);
+  t.i4_lanes = env_int("QNN_I4_LANES", t.i4_lanes);
+  t.i4_tpw = env_int("QNN_I4_TPW", t.i4_tpw);
+  t.i4_target_waves = env_int("QNN_I4_TARGET_WAVES", t.i4_target_waves);
+  t.i4_sps = env_int("QNN_I4_SPS", t.i4_sps);
+  t.i4_wide = env_int("QNN_I4_WIDE", t.i4_wide);
+  t.moe_mt = env_int("QNN_MOE_MT", t.moe_mt);
+  t.moe_sps = env_int("QNN_MOE_SPS", t.moe_sps);
+  g_tuning = t;
+}
+
+namespace {
 
 std::mutex g_lock;
 qnn_ctx_s *g_ctx = nullptr;
@@ -704,7 +735,7 @@ void launch_linear_group(qnn_ctx_s *ctx) {
   if (g.count > 1) ctx->st.linear_grouped += uint64_t(g.count);
 }
 
-bool linear_grouping_enabled() { return env_int("QNN_GROUP_LINEAR", 1) != 0; }
+bool linear_grouping_enabled() { return tuning().group_linear != 0; }
 
 // A recorded one-row GGUF group of exactly a gate and an up projection of one
 // shape, completed by a GLU of their two outputs: one gate/up pair launch
@@ -791,7 +822,7 @@ void settle_pending(qnn_ctx_s *ctx) {
   run_int4(ctx, p.g, p.u, I4_SWIGLU, p.x, p.h, 1, p.in, p.out, nullptr);
 }
 
-bool mlp_fusion_enabled() { return env_int("QNN_FUSE_MLP", 1) != 0; }
+bool mlp_fusion_enabled() { return tuning().fuse_mlp != 0; }
 
 // A gate/up SwiGLU launch gives each row the sums the two I4_STORE launches
 // would (same steps per wave, slices and parts for every 16-row chunk), so
@@ -882,7 +913,7 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
 
 // ---------------------------------------------------------------- Q8_0 multi-row GEMM
 // Rows at which the MFMA GEMM replaces per-row matvecs (one weight pass per row).
-int q8_gemm_min_rows() { return std::max(2, env_int("QNN_Q8_GEMM_MIN_ROWS", 4)); }
+int q8_gemm_min_rows() { return std::max(2, tuning().q8_gemm_min_rows); }
 
 void run_q8_gemm(qnn_ctx_s *ctx, const WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
   const Q8GemmPlan p = q8_gemm_plan(rows, in_dim, out_dim);
@@ -933,6 +964,14 @@ int qnn_last_error(char *buf, int len) {
   return n;
 }
 
+int qnn_reload_tuning(void) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> g(g_lock);
+    reload_tuning();
+    return QNN_OK;
+  });
+}
+
 int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out) {
   return guarded([&] {
     if (!out) fail(QNN_E_ARGUMENT, "out");
@@ -946,6 +985,7 @@ int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out) {
     }
     if (device < 0 || device >= n) fail(QNN_E_ARGUMENT, "device index");
     hip_check(hipSetDevice(device), "hipSetDevice");
+    reload_tuning();  // the QNN_* switches, read once here rather than per launch
     try {
       noalloc_scratch_init(device);  // the static scratch's address on this device, once
     } catch (const Error &) {
@@ -1341,16 +1381,24 @@ int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_
     if (in_dim < 1 || out_dim < 1 || dst == src) fail(QNN_E_ARGUMENT, "Invalid fused SwiGLU dimensions");
     check_weight_desc(gate);
     check_weight_desc(up);
+    // Implementation.inc:1017-1022: two GGUF weights (op 67), two native INT4
+    // weights (op 68), or two native F32/BF16 weights in any mix (op 66); any
+    // other pair is not handled, and the caller falls back.
     const bool gg = is_gguf(gate->encoding) && is_gguf(up->encoding);
     const bool i4 = gate->dtype == QNN_DT_U8 && up->dtype == QNN_DT_U8 && gate->encoding == QNN_WE_NATIVE &&
                     up->encoding == QNN_WE_NATIVE;
-    // Implementation.inc:1017-1022: any other mix is not handled here.
-    if (!gg && !i4) return QNN_NOT_HANDLED;
+    const auto dense = [](const qnn_weight *w) {
+      return w->encoding == QNN_WE_NATIVE && (w->dtype == QNN_DT_F32 || w->dtype == QNN_DT_BF16);
+    };
+    const bool fp = !gg && !i4 && dense(gate) && dense(up);
+    if (!gg && !i4 && !fp) return QNN_NOT_HANDLED;
     const int width = i4 ? qnn_int4_row_bytes(in_dim) : in_dim;
     if (gate->shape0 != out_dim || up->shape0 != out_dim || gate->shape1 != width || up->shape1 != width)
       fail(QNN_E_ARGUMENT, "Invalid fused SwiGLU weight shape");
-    uint64_t pair = i4 ? uint64_t(2) * out_dim * width
-                       : gguf_weight_bytes(gate, out_dim, in_dim) + gguf_weight_bytes(up, out_dim, in_dim);
+    const auto elem_bytes = [](const qnn_weight *w) { return uint64_t(w->dtype == QNN_DT_BF16 ? 2 : 4); };
+    uint64_t pair = i4   ? uint64_t(2) * out_dim * width
+                    : fp ? uint64_t(out_dim) * in_dim * (elem_bytes(gate) + elem_bytes(up))
+                         : gguf_weight_bytes(gate, out_dim, in_dim) + gguf_weight_bytes(up, out_dim, in_dim);
     uint64_t capacity = 0;
     qnn_weight_batch_capacity(ctx, &capacity);
     if (pair > capacity) {  // Implementation.inc:1033-1034
@@ -1382,6 +1430,11 @@ int qnn_swiglu_vector(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_
         run_int4(ctx, eg, eu, I4_SWIGLU, src->ptr, dst->ptr, 1, in_dim, out_dim, nullptr);
       }
       ctx->st.int4_calls += 2;
+    } else if (fp) {  // op 66: one pass over the gate and up rows
+      WeightEntry *eg = pin(acquire_raw(ctx, gate, int64_t(out_dim) * in_dim));
+      WeightEntry *eu = pin(acquire_raw(ctx, up, int64_t(out_dim) * in_dim));
+      dense_swiglu_launch(eg->dptr, eg->raw_dtype == QNN_DT_BF16, eu->dptr, eu->raw_dtype == QNN_DT_BF16, src->ptr,
+                          dst->ptr, out_dim, in_dim, ctx->stream);
     } else {
       WeightEntry *eg = pin(acquire_gguf(ctx, gate, out_dim, in_dim));
       WeightEntry *eu = pin(acquire_gguf(ctx, up, out_dim, in_dim));
@@ -1828,7 +1881,7 @@ int qnn_kernel(qnn_ctx *ctx, int op, int n, qnn_tensor *dst, qnn_tensor *a, qnn_
         check_tensor(ctx, a, int64_t(rows) * experts);
         check_tensor(ctx, dst, int64_t(rows) * k * 2);
         ctx->st.moe_calls++;
-        if (rows == 1 && moe_route_j(experts) && !ctx->capturing && env_int("QNN_FUSE_MOE", 1) != 0 && dst != a) {
+        if (rows == 1 && moe_route_j(experts) && !ctx->capturing && tuning().fuse_moe != 0 && dst != a) {
           ctx->proute = {true, a->ptr, dst->ptr, experts, k, norm};  // launched with the next call
           return QNN_OK;
         }
@@ -2197,7 +2250,7 @@ int qnn_moe_experts(qnn_ctx *ctx, qnn_expert_set *set, qnn_tensor *dst, qnn_tens
     // One token: one launch (bit-identical to the two below) when every
     // workgroup of its grid can be resident; not under capture, where the
     // epoch baked into the launch would repeat on every replay.
-    if (rows == 1 && !ctx->capturing && env_int("QNN_FUSE_MOE", 1) != 0) {
+    if (rows == 1 && !ctx->capturing && tuning().fuse_moe != 0) {
       const MoEDecodePlan d = moe_decode_plan(a, p);
       const int rj = fr.on && p.gsw == 8 ? moe_route_j(set->experts) : 0;
       if (d.ok) {

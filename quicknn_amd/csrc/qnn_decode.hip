@@ -958,8 +958,8 @@ AttnPlan attn_plan(int rows, int heads, int kv_heads, int dim, int position, int
   const int longest = window > 0 ? std::min(window, last_end) : last_end;
   // About two workgroups per CU, chunks of at least 64 keys (measured on
   // MI355X: 512 / 64 beat 256 / 128 and 128 / 256 at 4k and 32k keys).
-  const int target = env_int("QNN_ATTN_WGS", 512);
-  const int min_chunk = std::max(64, env_int("QNN_ATTN_MIN_CHUNK", 64)) / 64 * 64;
+  const int target = std::max(1, tuning().attn_wgs);
+  const int min_chunk = std::max(64, tuning().attn_min_chunk) / 64 * 64;
   int splits = std::max(1, std::min((target + wgs - 1) / wgs, (longest + min_chunk - 1) / min_chunk));
   splits = std::min(splits, kMergeMaxSplits);
   p.chunk = ((longest + splits - 1) / splits + 63) / 64 * 64;

@@ -10,6 +10,8 @@
 // * one row (dense_matvec_launch): one wave per output row; each lane reads
 //   16-byte pieces of the row (4 fp32 or 8 bf16 weights) and the matching
 //   activations, two pieces in flight per iteration, then a butterfly sum.
+// * fused gate/up SwiGLU, one row (dense_swiglu_launch, op 66): as the
+//   matvec, with the gate and up rows of an output read in the same pass.
 // * several rows (dense_gemm_launch): a 256-thread workgroup computes a tile
 //   of 64 outputs x 16 rows; 32-wide K slices of the weight tile and the
 //   activation tile are staged in LDS (weights padded to 33 floats per row so
@@ -93,6 +95,74 @@ __global__ __launch_bounds__(256) void k_dense_matvec(const void *__restrict__ w
   if (lane == 0) y[row] = acc;
 }
 
+// Weights j..j+7 of a row (16-byte aligned): one 16-byte piece of bf16, two
+// of fp32.
+template <bool BF16>
+__device__ __forceinline__ void load8(const uint8_t *row, int j, float (&v)[8]) {
+  if constexpr (BF16) {
+    const uint4 p = *reinterpret_cast<const uint4 *>(row + size_t(j) * 2);
+    const uint32_t u[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(u[i] << 16);
+      v[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4 *>(row + size_t(j) * 4);
+    const float4 b = *reinterpret_cast<const float4 *>(row + size_t(j) * 4 + 16);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  }
+}
+template <bool BF16>
+__device__ __forceinline__ float weight_at(const void *w, size_t i) {
+  return BF16 ? bf16_to_f32(static_cast<const uint16_t *>(w)[i]) : static_cast<const float *>(w)[i];
+}
+
+// Fused gate/up SwiGLU over F32 / BF16 weights, one row (TrySwiGLUVector's
+// op 66, tensor.comp:38-48): h[r] = silu(Wg[r] . x) * (Wu[r] . x), the two
+// rows read in one pass over x.  Gate and up may differ in type.  One wave
+// per output row; VEC: rows are whole 8-element pieces, 16-byte aligned.
+template <bool BG, bool BU, bool VEC>
+__global__ __launch_bounds__(256) void k_dense_swiglu(const void *__restrict__ wg, const void *__restrict__ wu,
+                                                      const float *__restrict__ x, float *__restrict__ y, int n,
+                                                      int k) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;  // whole waves leave together
+  float g = 0.0f, u = 0.0f;
+  if constexpr (VEC) {
+    const uint8_t *rg = static_cast<const uint8_t *>(wg) + size_t(row) * k * (BG ? 2 : 4);
+    const uint8_t *ru = static_cast<const uint8_t *>(wu) + size_t(row) * k * (BU ? 2 : 4);
+    for (int j = lane * 8; j < k; j += 512) {
+      float a[8], b[8], xv[8];
+      load8<BG>(rg, j, a);
+      load8<BU>(ru, j, b);
+      const float4 x0 = *reinterpret_cast<const float4 *>(x + j), x1 = *reinterpret_cast<const float4 *>(x + j + 4);
+      xv[0] = x0.x, xv[1] = x0.y, xv[2] = x0.z, xv[3] = x0.w, xv[4] = x1.x, xv[5] = x1.y, xv[6] = x1.z, xv[7] = x1.w;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        g = fmaf(a[i], xv[i], g);
+        u = fmaf(b[i], xv[i], u);
+      }
+    }
+  } else {
+    for (int j = lane; j < k; j += 64) {
+      const float xv = x[j];
+      g = fmaf(weight_at<BG>(wg, size_t(row) * k + j), xv, g);
+      u = fmaf(weight_at<BU>(wu, size_t(row) * k + j), xv, u);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    g += __shfl_xor(g, o);
+    u += __shfl_xor(u, o);
+  }
+  if (lane == 0) {
+    const float sg = g >= 20.0f ? g : (g <= -20.0f ? 0.0f : g / (1.0f + expf(-g)));  // tensor.comp:22
+    y[row] = sg * u;
+  }
+}
+
 constexpr int kTN = 64, kTM = 16, kTK = 32;
 
 template <bool BF16>
@@ -155,6 +225,24 @@ void dense_matvec_launch(const void *w, int bf16, const float *x, float *y, int 
     else hipLaunchKernelGGL((k_dense_matvec<false, false>), grid, block, 0, s, w, x, y, n, k);
   }
   hip_check(hipGetLastError(), "dense matvec launch");
+}
+
+void dense_swiglu_launch(const void *wg, int bg, const void *wu, int bu, const float *x, float *y, int n, int k,
+                         hipStream_t s) {
+  const bool vec = k % 8 == 0 && reinterpret_cast<uintptr_t>(wg) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(wu) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  const dim3 grid((n + 3) / 4), block(256);
+#define QNN_SWIGLU_CASE(G, U)                                                                     \
+  if (bool(bg) == G && bool(bu) == U) {                                                          \
+    if (vec) hipLaunchKernelGGL((k_dense_swiglu<G, U, true>), grid, block, 0, s, wg, wu, x, y, n, k); \
+    else hipLaunchKernelGGL((k_dense_swiglu<G, U, false>), grid, block, 0, s, wg, wu, x, y, n, k);    \
+  }
+  QNN_SWIGLU_CASE(false, false)
+  QNN_SWIGLU_CASE(false, true)
+  QNN_SWIGLU_CASE(true, false)
+  QNN_SWIGLU_CASE(true, true)
+#undef QNN_SWIGLU_CASE
+  hip_check(hipGetLastError(), "dense swiglu launch");
 }
 
 void dense_gemm_launch(const void *w, int bf16, const float *x, float *y, int m, int n, int k, hipStream_t s) {

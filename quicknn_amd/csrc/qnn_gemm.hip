@@ -339,9 +339,9 @@ Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
   // against 76.8 for 4 waves of two blocks, the same tile; the weight decode
   // per tile is shared by all of them).  Fewer rows: 128 x 96 as 4 waves.
   // QNN_GEMM_NW / QNN_GEMM_MB override.
-  p.nw = env_int("QNN_GEMM_NW", 0);
+  p.nw = tuning().gemm_nw;
   if (p.nw != 4 && p.nw != 8) p.nw = M >= 256 ? 8 : 4;
-  p.mb = env_int("QNN_GEMM_MB", 0);
+  p.mb = tuning().gemm_mb;
   if (p.mb != 1 && p.mb != 2) p.mb = 1;
   const int BM = 32 * p.mb * p.nw;
   p.m_pad = (M + BM - 1) / BM * BM;

@@ -651,7 +651,7 @@ void gguf_gather_launch(const GGLayout &l, const void *w, const float *ids, floa
 
 void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {
   const int tiles8 = (tiles + 7) / 8 * 8;
-  const int forced = env_int("QNN_GG_BW", 0);
+  const int forced = tuning().gg_bw;
   int pick = 1;
   if (forced == 1 || forced == 2) pick = forced;
   else if (size_t(tiles8) * ((l.units + 7) / 8) * 4 >= 16384) pick = 2;  // BW=1 measured faster up to 7k waves

@@ -378,7 +378,7 @@ void launch_tpw(const I4Launch &a, const I4Plan &p, hipStream_t st) {
 }
 // Several tokens over one-lane rows with 4 steps per wave: the matrix-core
 // inner product (QNN_I4_MFMA=0 keeps v_dot4).
-bool mfma_enabled() { return env_int("QNN_I4_MFMA", 1) != 0; }
+bool mfma_enabled() { return tuning().i4_mfma != 0; }
 
 template <int MT, int GSW>
 void launch_one(const I4Launch &a, const I4Plan &p, hipStream_t st) {
@@ -436,7 +436,7 @@ I4Layout int4_layout(int rows, int cols, bool one_lane) {
   // share each activation group), measured fastest at the decode shapes.
   // QNN_I4_LANES selects 2..16 lanes per row instead.
   l.lanes = 1;
-  const int forced = env_int("QNN_I4_LANES", 0);
+  const int forced = tuning().i4_lanes;
   if (!one_lane && (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16)) l.lanes = forced;
   l.rpb = 64 / l.lanes;
   l.steps = (l.groups + l.lanes - 1) / l.lanes;
@@ -450,7 +450,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode, bool wide) {
   const int tiles = mode == I4_SWIGLU ? 2 * l.blocks : l.blocks;
   // Tiles per workgroup (the other 4/T waves of a tile split its K-slice and
   // meet in LDS before any cross-workgroup exchange).
-  const int ft = env_int("QNN_I4_TPW", 1);
+  const int ft = tuning().i4_tpw;
   p.tiles_per_wg = ft == 2 || ft == 4 ? ft : 1;
   while (p.tiles_per_wg < 4 && (4 / p.tiles_per_wg) * l.lanes > 16) p.tiles_per_wg *= 2;  // slice fits x_iters
   const int P = 4 / p.tiles_per_wg;
@@ -467,7 +467,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode, bool wide) {
   // Steps per wave: the largest that splits the K-range into equal workgroup
   // slices (an uneven last slice was measured up to 40% slower) while giving
   // at least `target` waves; failing that, the largest that gives the waves.
-  const int target = env_int("QNN_I4_TARGET_WAVES", p.mt == 1 ? 1 : 3000);
+  const int target = tuning().i4_target_waves > 0 ? tuning().i4_target_waves : (p.mt == 1 ? 1 : 3000);
   const int units = (tiles + p.tiles_per_wg - 1) / p.tiles_per_wg;
   auto waves = [&](int sps) { return size_t(units) * 4 * ((l.steps + P * sps - 1) / (P * sps)); };
   const int *set0 = p.mt == 1 ? kGsw1 : (p.mt <= 4 ? kGswN : kGswBig);
@@ -478,7 +478,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode, bool wide) {
   for (int i = nset0 - 1; i >= 0 && !sps; --i)
     if (set0[i] <= cap && waves(set0[i]) >= size_t(target)) sps = set0[i];
   if (!sps) sps = 1;
-  const int forced = env_int("QNN_I4_SPS", 0);
+  const int forced = tuning().i4_sps;
   if (forced > 0) {  // a power of two: scale pieces hold 4 aligned steps
     sps = 1;
     while (sps * 2 <= std::min(forced, cap)) sps *= 2;
@@ -498,7 +498,7 @@ I4Plan int4_plan(const I4Layout &l, int m, int mode, bool wide) {
   // the caller launches k_int4_matvec (`wide`): the fused MLP builds its down
   // items from the four-wave slices.
   if (wide && mode == I4_STORE && p.mt == 1 && p.tiles_per_wg == 1 && l.lanes == 1 && (p.slices == 2 || p.slices == 4) &&
-      l.steps == P * sps * p.slices && env_int("QNN_I4_WIDE", 1) != 0) {
+      l.steps == P * sps * p.slices && tuning().i4_wide != 0) {
     p.wg_waves = 4 * p.slices;
     p.slices = 1;
     p.lds = dev::xplanes_bytes(p.mt, p.wg_waves * sps * l.lanes);

@@ -33,11 +33,30 @@ __host__ __device__ inline float add_mul_nofma(float a, float b, float c) {
   return a + b * c;
 }
 
-// Integer tuning override from the environment (0 or unset: the default).
-inline int env_int(const char *name, int dflt) {
-  const char *v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
+// Tuning switches: QNN_* environment variables read into one snapshot when a
+// context is created (and by qnn_reload_tuning), never per launch.  A value of
+// 0 in the planners' fields means "the planner's own choice".
+struct Tuning {
+  int group_linear = 1;      // QNN_GROUP_LINEAR: grouped one-row GGUF Linear launches
+  int fuse_mlp = 1;          // QNN_FUSE_MLP: recorded INT4 SwiGLU + down as one launch
+  int fuse_moe = 1;          // QNN_FUSE_MOE: one-token routed experts (and route) as one launch
+  int q8_gemm_min_rows = 4;  // QNN_Q8_GEMM_MIN_ROWS: rows from which Q8_0 Linear takes the GEMM
+  int attn_wgs = 512;        // QNN_ATTN_WGS: cached-attention workgroup target
+  int attn_min_chunk = 64;   // QNN_ATTN_MIN_CHUNK: keys per chunk, at least
+  int gemm_nw = 0;           // QNN_GEMM_NW: waves per Q8_0 GEMM workgroup (4 or 8)
+  int gemm_mb = 0;           // QNN_GEMM_MB: 32-row blocks per GEMM wave (1 or 2)
+  int gg_bw = 0;             // QNN_GG_BW: GGUF units per wave (1 or 2)
+  int i4_mfma = 1;           // QNN_I4_MFMA: multi-token INT4 dot on the int8 matrix cores
+  int i4_lanes = 0;          // QNN_I4_LANES: lanes per INT4 row at upload (1..16)
+  int i4_tpw = 1;            // QNN_I4_TPW: INT4 tiles per workgroup (1, 2, 4)
+  int i4_target_waves = 0;   // QNN_I4_TARGET_WAVES: wave target of the INT4 planner
+  int i4_sps = 0;            // QNN_I4_SPS: INT4 steps per wave
+  int i4_wide = 1;           // QNN_I4_WIDE: one-token 8/16-wave workgroups
+  int moe_mt = 0;            // QNN_MOE_MT: tokens per pass of the multi-token MoE kernels
+  int moe_sps = 0;           // QNN_MOE_SPS: MoE steps per wave
+};
+const Tuning &tuning();
+void reload_tuning();
 
 // ---------------------------------------------------------------------------
 // Device layouts
@@ -291,6 +310,9 @@ void *noalloc_scratch(int device);      // that address, or null if set-up faile
 // Y[m, n] = X[m, k] W^T for several.
 void dense_matvec_launch(const void *w, int bf16, const float *x, float *y, int n, int k, hipStream_t s);
 void dense_gemm_launch(const void *w, int bf16, const float *x, float *y, int m, int n, int k, hipStream_t s);
+// h = silu(Wg x) * (Wu x) for one row; gate and up each F32 (0) or BF16 (1).
+void dense_swiglu_launch(const void *wg, int bg, const void *wu, int bu, const float *x, float *y, int n, int k,
+                         hipStream_t s);
 
 // GGUF (qnn_gguf.hip).
 enum GGMode { GG_STORE = 0, GG_SWIGLU = 2, GG_GEGLU = 3 };

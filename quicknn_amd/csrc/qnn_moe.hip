@@ -680,7 +680,7 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
   // though an expert with several tokens makes several passes over its
   // weights in registers.  QNN_MOE_MT (1, 2, 4) overrides.
   p.mt = 1;
-  const int fmt = env_int("QNN_MOE_MT", 0);
+  const int fmt = tuning().moe_mt;
   if (fmt == 1 || fmt == 2 || fmt == 4) p.mt = fmt;
   // Steps per wave: 8 with one token per pass, 4 with several, measured
   // fastest for 128 experts of 768 x 2048 (one token per pass, 2-64 rows: 8
@@ -691,7 +691,7 @@ MoEPlanSizes moe_plan(const MoELaunch &a) {
   // is faster at 8 (16.55 against 17.91 us) and must sum in the same order as
   // the routes-given launch, so one row keeps 8.  QNN_MOE_SPS overrides.
   // Bounded by the activation-slice LDS budget.
-  const int forced = env_int("QNN_MOE_SPS", 0);
+  const int forced = tuning().moe_sps;
   auto steps = [&](const I4Layout &l, int) {
     const int lds_cap = int((48 << 10) / (size_t(p.mt) * 4 * l.lanes * (dev::kXWords * 4 + 8)));
     const int cap = std::max(1, std::min(8, lds_cap));

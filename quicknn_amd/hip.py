@@ -113,6 +113,7 @@ def lib():
             "qnn_ctx_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(_vp)]),
             "qnn_ctx_destroy": (ctypes.c_int, [_vp]),
             "qnn_get_status": (ctypes.c_int, [_vp, ctypes.POINTER(Status)]),
+            "qnn_reload_tuning": (ctypes.c_int, []),
             "qnn_tensor_new": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp)]),
             "qnn_recycle": (ctypes.c_int, [_vp, ctypes.POINTER(_vp)]),
             "qnn_scratch": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
@@ -198,7 +199,8 @@ def lib():
 
 
 EXPORTED = (
-    "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_tensor_new", "qnn_recycle",
+    "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_reload_tuning", "qnn_tensor_new",
+    "qnn_recycle",
     "qnn_scratch", "qnn_upload_raw", "qnn_download", "qnn_copy", "qnn_flush", "qnn_tensor_count",
     "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
     "qnn_weight_batch_capacity", "qnn_set_weight_evicted", "qnn_enable_weight_prefetch", "qnn_begin_weight_prefetch",
@@ -370,6 +372,12 @@ def _close_open_contexts() -> None:
             c.close()
         except Exception:  # created on another thread, or the runtime already failed
             _open_contexts.discard(c)
+
+
+def reload_tuning() -> None:
+    """qnn_reload_tuning: re-read the QNN_* tuning switches from the environment (the
+    library reads them once when a context is created)."""
+    _raise(lib().qnn_reload_tuning())
 
 
 class GPUContext:

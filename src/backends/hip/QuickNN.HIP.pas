@@ -136,6 +136,7 @@ function qnn_last_error(Buf: PAnsiChar; Len: Integer): Integer; cdecl; external 
 function qnn_ctx_create(Device: Integer; WeightCacheBytes: UInt64; out Ctx: Pointer): Integer; cdecl; external QNN_LIB;
 function qnn_ctx_destroy(Ctx: Pointer): Integer; cdecl; external QNN_LIB;
 function qnn_get_status(Ctx: Pointer; out Status: TQnnStatus): Integer; cdecl; external QNN_LIB;
+function qnn_reload_tuning: Integer; cdecl; external QNN_LIB;
 // ---- resident tensors
 function qnn_tensor_new(Ctx: Pointer; Count: Integer; out T: Pointer): Integer; cdecl; external QNN_LIB;
 function qnn_recycle(Ctx: Pointer; var T: Pointer): Integer; cdecl; external QNN_LIB;

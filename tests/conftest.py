@@ -31,6 +31,22 @@ def ctx():
 
 
 @pytest.fixture
+def tune(monkeypatch):
+    """tune(name, value): set a QNN_* tuning switch for this test.  The library reads the
+    switches once per context (qnn_reload_tuning re-reads them), so each change is followed
+    by a reload, and the test's end restores the environment and reloads again."""
+    from quicknn_amd import hip
+
+    def set_switch(name: str, value: str) -> None:
+        monkeypatch.setenv(name, value)
+        hip.reload_tuning()
+
+    yield set_switch
+    monkeypatch.undo()
+    hip.reload_tuning()
+
+
+@pytest.fixture
 def rng():
     return np.random.default_rng(1234)
 

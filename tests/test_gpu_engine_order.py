@@ -46,7 +46,7 @@ def mlp_reference_order(ctx, x, rows, gate, up, down, hidden, inter):
 
 
 @pytest.mark.parametrize("rows", [1, 8])
-def test_mlp_in_engine_order_fuses_and_matches(ctx, rng, monkeypatch, rows):
+def test_mlp_in_engine_order_fuses_and_matches(ctx, rng, tune, rows):
     hidden, inter = 2560, 9728
     pg, pu, pd = rand_int4(rng, inter, hidden), rand_int4(rng, inter, hidden), rand_int4(rng, hidden, inter)
     gate, up, down = (hip.MemoryBlock.int4(p) for p in (pg, pu, pd))
@@ -58,7 +58,7 @@ def test_mlp_in_engine_order_fuses_and_matches(ctx, rng, monkeypatch, rows):
         assert s1.mlp_fused - s0.mlp_fused == 1  # gate/up SwiGLU + down: one launch
     else:
         assert s1.glu_fused - s0.glu_fused == 1  # gate + up + in-place GO_SWIGLU: one launch
-    monkeypatch.setenv("QNN_FUSE_MLP", "0")
+    tune("QNN_FUSE_MLP", "0")
     plain = mlp_reference_order(ctx, x, rows, gate, up, down, hidden, inter)
     s2 = ctx.status()
     assert s2.mlp_fused == s1.mlp_fused and s2.glu_fused == s1.glu_fused
@@ -68,7 +68,7 @@ def test_mlp_in_engine_order_fuses_and_matches(ctx, rng, monkeypatch, rows):
         assert normwise_rel_err(fused[r], want) <= TOL, r
 
 
-def test_gemma_layer_in_engine_order_groups(ctx, rng, monkeypatch):
+def test_gemma_layer_in_engine_order_groups(ctx, rng, tune):
     """Gemma2.pas:160-188 at batch 1: Project (New + Linear) for q, k, v, then
     gate and up, GO_GEGLU in place, down.  q+k+v share a launch, gate+up+GEGLU
     run as one, and every output equals the ungrouped path."""
@@ -104,7 +104,7 @@ def test_gemma_layer_in_engine_order_groups(ctx, rng, monkeypatch):
     s1 = ctx.status()
     assert s1.linear_grouped - s0.linear_grouped == 3
     assert s1.glu_fused - s0.glu_fused == 1
-    monkeypatch.setenv("QNN_GROUP_LINEAR", "0")
+    tune("QNN_GROUP_LINEAR", "0")
     plain = layer()
     for nm in grouped:
         assert np.array_equal(grouped[nm].view(np.uint32), plain[nm].view(np.uint32)), nm
@@ -216,7 +216,7 @@ def test_moe_forward_from_router_matches_cpu(ctx, rng, bf16_router, rows):
     ctx.Recycle(src)
 
 
-def test_recorded_multi_row_linear_runs_before_moe_experts(ctx, rng, monkeypatch):
+def test_recorded_multi_row_linear_runs_before_moe_experts(ctx, rng, tune):
     """A multi-row Int4Linear into T may be recorded (to meet a GO_SWIGLU); a
     following qnn_moe_experts(src=T) must see T written."""
     E, H, I, k, rows = 4, 256, 128, 2, 3
@@ -242,7 +242,7 @@ def test_recorded_multi_row_linear_runs_before_moe_experts(ctx, rng, monkeypatch
         return res
 
     got, tvals, routes = run()
-    monkeypatch.setenv("QNN_FUSE_MLP", "0")
+    tune("QNN_FUSE_MLP", "0")
     plain, _, _ = run()
     ctx.DestroyExpertSet(s)
     assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))

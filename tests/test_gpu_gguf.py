@@ -112,13 +112,13 @@ def test_linear_rows_and_bias(ctx, rng, enc):
 # small ragged shapes, including launches with fewer units than waves.
 @pytest.mark.parametrize("enc", FMTS, ids=NAMES.get)
 @pytest.mark.parametrize("n,k", [(1, 256), (37, 768), (64, 2048), (130, 2304), (300, 512), (65, 3584)])
-def test_linear_two_units_per_wave_forced(ctx, rng, monkeypatch, enc, n, k):
+def test_linear_two_units_per_wave_forced(ctx, rng, tune, enc, n, k):
     if enc == ENC_Q8_0:
         k = k - 32 if k > 256 else 96  # Q8_0 rows need not fill their last 256-element unit
     data = quantized(rng, enc, n, k)
     x = rng.standard_normal(k).astype(np.float32)
     src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
-    monkeypatch.setenv("QNN_GG_BW", "2")
+    tune("QNN_GG_BW", "2")
     ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, k, enc), None, None, 1, k, n)
     got = ctx.Download(dst)
     assert normwise_rel_err(got, oracle.cpu_linear(data, enc, x, k, n)) <= TOL
@@ -128,18 +128,18 @@ def test_linear_two_units_per_wave_forced(ctx, rng, monkeypatch, enc, n, k):
 
 @pytest.mark.parametrize("eg,eu,n,k", [(ENC_Q2_K, ENC_Q2_K, 700, 1024), (ENC_Q6_K, ENC_Q6_K, 33, 512),
                                        (ENC_Q4_K, ENC_Q4_K, 96, 3584)])
-def test_swiglu_two_units_per_wave_forced(ctx, rng, monkeypatch, eg, eu, n, k):
+def test_swiglu_two_units_per_wave_forced(ctx, rng, tune, eg, eu, n, k):
     pg, pu = quantized(rng, eg, n, k), quantized(rng, eu, n, k)
     x = rng.standard_normal(k).astype(np.float32)
     src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
-    monkeypatch.setenv("QNN_GG_BW", "2")
+    tune("QNN_GG_BW", "2")
     assert ctx.TrySwiGLUVector(dst, src, hip.MemoryBlock.gguf(pg, n, k, eg), hip.MemoryBlock.gguf(pu, n, k, eu), k, n)
     assert normwise_rel_err(ctx.Download(dst), _swiglu_want(pg, eg, pu, eu, x, k, n)) <= TOL
     ctx.Recycle(src)
     ctx.Recycle(dst)
 
 
-def test_q6k_output_head_256000x3584(ctx, rng, monkeypatch):
+def test_q6k_output_head_256000x3584(ctx, rng, tune):
     """configs[2]'s Q6_K output head at full size.  The planner runs it at two
     units per wave (4000 tiles x 14 units: 32000 >= 16384 in gguf_plan); the
     result equals a forced QNN_GG_BW=2 launch bit for bit (BW=1 splits K into 4
@@ -155,7 +155,7 @@ def test_q6k_output_head_256000x3584(ctx, rng, monkeypatch):
     src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
     ctx.Linear(dst, src, w, None, None, 1, k, n)
     auto = ctx.Download(dst)
-    monkeypatch.setenv("QNN_GG_BW", "2")
+    tune("QNN_GG_BW", "2")
     ctx.Linear(dst, src, w, None, None, 1, k, n)
     forced = ctx.Download(dst)
     assert np.array_equal(auto.view(np.uint32), forced.view(np.uint32))

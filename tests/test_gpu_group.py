@@ -56,7 +56,7 @@ def recorded_groups(encs):
 # q's encoding and k/v's: two K-quant encodings share one launch (k_gguf_matvec_mixed).
 @pytest.mark.parametrize("eq,ekv", [(2, 4), (2, 3), (3, 9), (4, 2), (9, 3), (3, 2)],
                          ids=["q4k+q3k", "q4k+q6k", "q6k+q2k", "q3k+q4k", "q2k+q6k", "q6k+q4k"])
-def test_grouped_equals_single(ctx, rng, monkeypatch, eq, ekv):
+def test_grouped_equals_single(ctx, rng, tune, eq, ekv):
     from quicknn_amd import hip
 
     H = 1024
@@ -67,7 +67,7 @@ def test_grouped_equals_single(ctx, rng, monkeypatch, eq, ekv):
     grouped = gemma_like(ctx, hip, ws, x0)
     want = recorded_groups([eq, ekv, ekv, hip.WE_Q2_K, hip.WE_Q2_K])
     assert ctx.status().linear_grouped - g0 == want  # e.g. q+k+v (two encodings) and gate+up
-    monkeypatch.setenv("QNN_GROUP_LINEAR", "0")
+    tune("QNN_GROUP_LINEAR", "0")
     single = gemma_like(ctx, hip, ws, x0)
     assert ctx.status().linear_grouped - g0 == want
     for name in grouped:
@@ -115,7 +115,7 @@ def test_group_limits_and_interleaving(ctx, rng):
                                                              ("GO_GEGLU", "WE_Q4_K", 2816, 1024),
                                                              ("GO_SWIGLU", "WE_Q6_K", 1536, 512),
                                                              ("GO_SWIGLU", "WE_Q8_0", 1000, 768)])
-def test_gate_up_glu_one_launch(ctx, rng, monkeypatch, op_name, enc_name, inter, hidden):
+def test_gate_up_glu_one_launch(ctx, rng, tune, op_name, enc_name, inter, hidden):
     """One-row GGUF Linear gate + up on the same input followed by a GLU of their two outputs
     run as one gate/up pair launch (qnn_status.glu_fused) that still writes both outputs; all
     three outputs are bit-identical to the grouped launch followed by the GLU kernel, and the
@@ -140,7 +140,7 @@ def test_gate_up_glu_one_launch(ctx, rng, monkeypatch, op_name, enc_name, inter,
     n0 = ctx.status().glu_fused
     fused = run()
     n1 = ctx.status().glu_fused
-    monkeypatch.setenv("QNN_GROUP_LINEAR", "0")
+    tune("QNN_GROUP_LINEAR", "0")
     sep = run()
     assert ctx.status().glu_fused == n1
     for a, b, nm in zip(fused, sep, ("gate", "up", "glu")):

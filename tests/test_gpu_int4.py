@@ -96,11 +96,45 @@ def test_swiglu_vector(ctx, rng, n, k):
     assert normwise_rel_err(got, want) <= TOL
 
 
+def silu64(g: np.ndarray) -> np.ndarray:
+    """Clamped SiLU (tensor.comp:22, QwenHybrid.CPU.pas:242-246) in float64."""
+    g = np.asarray(g, np.float64)
+    return np.where(g >= 20.0, g, np.where(g <= -20.0, 0.0, g / (1.0 + np.exp(-np.clip(g, -20.0, 20.0)))))
+
+
+@pytest.mark.parametrize("n,k", [(9728, 2560), (768, 2048), (100, 40), (37, 1001)])
+@pytest.mark.parametrize("gt,ut", [("f32", "f32"), ("bf16", "bf16"), ("f32", "bf16"), ("bf16", "f32")])
+def test_swiglu_vector_dense_pairs(ctx, rng, n, k, gt, ut):
+    """F32 / BF16 gate and up weights, in any mix, run fused as the reference's op 66
+    (Implementation.inc:1017-1023, tensor.comp:38-48): QNN_OK, within 1e-3 of a float64
+    silu(Wg x) * (Wu x) over the same (bf16-widened) weights, including rows that are not
+    whole 16-byte pieces (K = 40, 1001)."""
+    def weight(kind):
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        if kind == "bf16":
+            b = bf16_bits(w)
+            return hip.MemoryBlock.matrix(b), (b.astype(np.uint32) << 16).view(np.float32)
+        return hip.MemoryBlock.matrix(w), w
+    (mg, wg), (mu, wu) = weight(gt), weight(ut)
+    x = rng.standard_normal(k).astype(np.float32)
+    src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
+    assert ctx.TrySwiGLUVector(dst, src, mg, mu, k, n) is True
+    x64 = x.astype(np.float64)
+    want = silu64(wg.astype(np.float64) @ x64) * (wu.astype(np.float64) @ x64)
+    assert normwise_rel_err(ctx.Download(dst), want) <= TOL
+    ctx.Recycle(src)
+    ctx.Recycle(dst)
+
+
 def test_swiglu_unsupported_mix_not_handled(ctx, rng):
+    """Pairs outside ops 66-68 (Implementation.inc:1019-1022) are not handled: an INT4 gate
+    with an F32 up, and an F32 gate with a native INT4 up."""
     x = ctx.UploadRaw(np.ones(64, np.float32))
     dst = ctx.NewTensor(8)
     f = hip.MemoryBlock(np.ones((8, 64), np.float32), (8, 64), hip.DT_F32)
-    assert ctx.TrySwiGLUVector(dst, x, f, f, 64, 8) is False
+    i4 = hip.MemoryBlock.int4(make_int4(rng, 8, 64))
+    assert ctx.TrySwiGLUVector(dst, x, i4, f, 64, 8) is False
+    assert ctx.TrySwiGLUVector(dst, x, f, i4, 64, 8) is False
 
 
 def test_int4_accumulate(ctx, rng):
@@ -167,11 +201,11 @@ def test_non_finite_raises_at_download(ctx):
 
 
 @pytest.mark.parametrize("lanes,tpw", [(2, 1), (4, 2), (16, 4), (8, 2)])
-def test_lane_layouts_and_tile_groupings(ctx, rng, monkeypatch, lanes, tpw):
+def test_lane_layouts_and_tile_groupings(ctx, rng, tune, lanes, tpw):
     """Rows spread over L lanes (QNN_I4_LANES, read when a weight is uploaded) and T tiles per
     workgroup (QNN_I4_TPW) compute the same projections."""
-    monkeypatch.setenv("QNN_I4_LANES", str(lanes))
-    monkeypatch.setenv("QNN_I4_TPW", str(tpw))
+    tune("QNN_I4_LANES", str(lanes))
+    tune("QNN_I4_TPW", str(tpw))
     for n, k in [(2560, 9728), (1000, 2560), (100, 40)]:
         p = make_int4(rng, n, k)
         w = hip.MemoryBlock.int4(p)
@@ -198,7 +232,7 @@ def test_lane_layouts_and_tile_groupings(ctx, rng, monkeypatch, lanes, tpw):
 
 
 @pytest.mark.parametrize("n,k", [(6144, 2048), (1000, 1024), (130, 2040), (70, 2048), (300, 2560)])
-def test_one_token_wide_workgroups_match_slices(ctx, rng, monkeypatch, n, k):
+def test_one_token_wide_workgroups_match_slices(ctx, rng, tune, n, k):
     """One token whose K-range splits evenly into 2 or 4 four-wave slices runs as one 8- or
     16-wave workgroup per tile (no cross-workgroup exchange): bit-identical to the split-K
     launch (QNN_I4_WIDE=0) and within tolerance of the CPU path, including a ragged last
@@ -210,7 +244,7 @@ def test_one_token_wide_workgroups_match_slices(ctx, rng, monkeypatch, n, k):
     src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
     got = {}
     for wide in ("1", "0"):
-        monkeypatch.setenv("QNN_I4_WIDE", wide)
+        tune("QNN_I4_WIDE", wide)
         ctx.Int4Linear(dst, src, w, 1, k, n)
         got[wide] = ctx.Download(dst)
     assert np.array_equal(got["1"].view(np.uint32), got["0"].view(np.uint32)), (n, k)
@@ -220,13 +254,13 @@ def test_one_token_wide_workgroups_match_slices(ctx, rng, monkeypatch, n, k):
 
 
 @pytest.mark.parametrize("rows,tpw", [(4, 1), (5, 1), (8, 1), (8, 2), (6, 4)])
-def test_multi_token_matrix_cores_match_dot4(ctx, rng, monkeypatch, rows, tpw):
+def test_multi_token_matrix_cores_match_dot4(ctx, rng, tune, rows, tpw):
     """4-8 tokens over one-lane rows with 4 steps per wave run the inner product on the int8
     matrix cores: bit-identical to the v_dot4 path (QNN_I4_MFMA=0) and within tolerance of the
     CPU path, including a partial last block of rows, a slice shorter than a wave's steps and
     2 or 4 tiles per workgroup (QNN_I4_TPW)."""
-    monkeypatch.setenv("QNN_I4_SPS", "4")
-    monkeypatch.setenv("QNN_I4_TPW", str(tpw))
+    tune("QNN_I4_SPS", "4")
+    tune("QNN_I4_TPW", str(tpw))
     for n, k in [(2560, 9728), (1000, 2560), (200, 96)]:
         p = make_int4(rng, n, k)
         w = hip.MemoryBlock.int4(p)
@@ -234,7 +268,7 @@ def test_multi_token_matrix_cores_match_dot4(ctx, rng, monkeypatch, rows, tpw):
         src, dst = ctx.UploadRaw(x), ctx.NewTensor(rows * n)
         got = {}
         for mf in ("1", "0"):
-            monkeypatch.setenv("QNN_I4_MFMA", mf)
+            tune("QNN_I4_MFMA", mf)
             ctx.Int4Linear(dst, src, w, rows, k, n)
             got[mf] = ctx.Download(dst).reshape(rows, n)
         assert np.array_equal(got["1"].view(np.uint32), got["0"].view(np.uint32)), (n, k)

@@ -38,7 +38,7 @@ def mlp(ctx, hip, layers, x0, hidden, inter):
 # keeps its four-wave slices.
 @pytest.mark.parametrize("hidden,inter,nl", [(2560, 9728, 3), (1024, 3072, 2), (2048, 768, 2), (512, 1536, 1),
                                              (1024, 2048, 2), (768, 1024, 1)])
-def test_fused_equals_per_op(ctx, rng, monkeypatch, hidden, inter, nl):
+def test_fused_equals_per_op(ctx, rng, tune, hidden, inter, nl):
     from quicknn_amd import hip
 
     layers = [(hip.MemoryBlock.int4(rand_int4(rng, inter, hidden)), hip.MemoryBlock.int4(rand_int4(rng, inter, hidden)),
@@ -47,7 +47,7 @@ def test_fused_equals_per_op(ctx, rng, monkeypatch, hidden, inter, nl):
     before = ctx.status().mlp_fused
     h_f, y_f = mlp(ctx, hip, layers, x0, hidden, inter)
     fused = ctx.status().mlp_fused - before
-    monkeypatch.setenv("QNN_FUSE_MLP", "0")
+    tune("QNN_FUSE_MLP", "0")
     h_p, y_p = mlp(ctx, hip, layers, x0, hidden, inter)
     assert ctx.status().mlp_fused - before == fused  # nothing fused with the switch off
     for i in range(nl):
@@ -136,7 +136,7 @@ def batch_mlp(ctx, hip, g, u, d, x0, rows, hidden, inter):
 
 
 @pytest.mark.parametrize("rows,hidden,inter", [(8, 2560, 9728), (3, 1024, 3072), (20, 512, 1536), (5, 2048, 768)])
-def test_multi_row_gate_up_glu_one_launch(ctx, rng, monkeypatch, rows, hidden, inter):
+def test_multi_row_gate_up_glu_one_launch(ctx, rng, tune, rows, hidden, inter):
     """Int4Linear gate + up on the same rows followed by GO_SWIGLU of their outputs run as one
     gate/up SwiGLU launch (qnn_status.glu_fused) that still writes both outputs; every output is
     bit-identical to the three separate operations (QNN_FUSE_MLP=0)."""
@@ -148,7 +148,7 @@ def test_multi_row_gate_up_glu_one_launch(ctx, rng, monkeypatch, rows, hidden, i
     n0 = ctx.status().glu_fused
     fused = batch_mlp(ctx, hip, g, u, d, x0, rows, hidden, inter)
     n1 = ctx.status().glu_fused
-    monkeypatch.setenv("QNN_FUSE_MLP", "0")
+    tune("QNN_FUSE_MLP", "0")
     sep = batch_mlp(ctx, hip, g, u, d, x0, rows, hidden, inter)
     assert ctx.status().glu_fused == n1
     for a, b, nm in zip(fused, sep, ("gate", "up", "glu", "down")):

@@ -274,7 +274,7 @@ def _run_moe(ctx, s, x, routes, rows, k, hidden):
     (64, 1024, 256, 16),
     (40, 192, 4100, 3),  # many gate/up blocks, ragged
 ])
-def test_moe_decode_single_launch_equals_two_launch(ctx, rng, monkeypatch, E, hidden, inter, k):
+def test_moe_decode_single_launch_equals_two_launch(ctx, rng, tune, E, hidden, inter, k):
     """One token: the single-launch path and the two-launch path give the same bits."""
     ex = Experts(rng, E, hidden, inter)
     s = ctx.CreateExpertSet(ex.bg, ex.bu, ex.bd, hidden, inter)
@@ -284,7 +284,7 @@ def test_moe_decode_single_launch_equals_two_launch(ctx, rng, monkeypatch, E, hi
     one = _run_moe(ctx, s, x, routes, 1, k, hidden)
     again = _run_moe(ctx, s, x, routes, 1, k, hidden)
     assert ctx.status().moe_fused - f0 == 2
-    monkeypatch.setenv("QNN_FUSE_MOE", "0")
+    tune("QNN_FUSE_MOE", "0")
     two = _run_moe(ctx, s, x, routes, 1, k, hidden)
     assert ctx.status().moe_fused - f0 == 2
     ctx.DestroyExpertSet(s)
@@ -293,26 +293,26 @@ def test_moe_decode_single_launch_equals_two_launch(ctx, rng, monkeypatch, E, hi
     assert normwise_rel_err(one.reshape(1, -1)[0], ex.oracle(x, ids, probs)[0]) <= TOL
 
 
-def test_moe_decode_qwen3_equals_two_launch(ctx, rng, monkeypatch, qwen3_moe):
+def test_moe_decode_qwen3_equals_two_launch(ctx, rng, tune, qwen3_moe):
     ex, s = qwen3_moe
     k = 8
     for trial in range(3):  # fresh routes each time: other experts, other flags
         x = rng.standard_normal((1, ex.hidden)).astype(np.float32)
         routes, ids, probs = route_on_gpu(ctx, rng.standard_normal((1, ex.E)).astype(np.float32), k)
-        monkeypatch.delenv("QNN_FUSE_MOE", raising=False)
+        tune("QNN_FUSE_MOE", "1")
         f0 = ctx.status().moe_fused
         one = _run_moe(ctx, s, x, routes, 1, k, ex.hidden)
         assert ctx.status().moe_fused - f0 == 1
-        monkeypatch.setenv("QNN_FUSE_MOE", "0")
+        tune("QNN_FUSE_MOE", "0")
         two = _run_moe(ctx, s, x, routes, 1, k, ex.hidden)
         assert np.array_equal(one.view(np.uint32), two.view(np.uint32)), trial
         assert normwise_rel_err(one, ex.oracle(x, ids, probs)[0]) <= TOL
 
 
 @pytest.mark.parametrize("fuse", ["1", "0"])
-def test_moe_experts_duplicate_route_id(ctx, rng, monkeypatch, fuse):
+def test_moe_experts_duplicate_route_id(ctx, rng, tune, fuse):
     """An expert twice in one token's routes is reported (bit 8), on either path."""
-    monkeypatch.setenv("QNN_FUSE_MOE", fuse)
+    tune("QNN_FUSE_MOE", fuse)
     ex = Experts(rng, 4, 64, 64)
     s = ctx.CreateExpertSet(ex.bg, ex.bu, ex.bd, 64, 64)
     plane = np.concatenate([np.array([2, 2], np.uint32).view(np.float32), np.array([0.5, 0.5], np.float32)])
