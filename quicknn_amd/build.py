@@ -2,7 +2,10 @@
 
 Compiles every HIP source under quicknn_amd/csrc with hipcc for gfx950 and the
 host-only C++ with g++, then links one shared library in-tree
-(quicknn_amd/libqnn_hip.so) so it travels with the source tree.
+(quicknn_amd/libqnn_hip.so) so it travels with the source tree.  A second
+library, libqnn_hip_trace.so, is the same objects with the fused decode-MLP
+kernels built with per-workgroup phase timestamps (QNN_PHASE_TRACE), for
+quicknn_amd/phase_trace.py; nothing else loads it.
 """
 from __future__ import annotations
 
@@ -16,6 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqnn_hip.so")
+TRACE_LIB = os.path.join(HERE, "libqnn_hip_trace.so")  # diagnostic build (phase timestamps)
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
@@ -66,13 +70,23 @@ def build(jobs: int | None = None) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, "-lpthread"])
     os.replace(tmp, LIB)
+    # The phase-trace variant: the fused decode-MLP kernels with per-workgroup
+    # timestamps (QNN_PHASE_TRACE), everything else the same objects.
+    mlp = os.path.join(CSRC, "qnn_mlp.hip")
+    tobj = os.path.join(BUILD, "qnn_mlp.hip.trace.o")
+    _run([HIPCC, *HIP_FLAGS, "-DQNN_PHASE_TRACE", "-c", mlp, "-o", tobj])
+    tobjs = [tobj if o.endswith("qnn_mlp.hip.o") else o for o in objs]
+    tmp = TRACE_LIB + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *tobjs, "-o", tmp, "-lpthread"])
+    os.replace(tmp, TRACE_LIB)
     return LIB
 
 
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
-    if os.path.exists(LIB):
-        os.remove(LIB)
+    for f in (LIB, TRACE_LIB):
+        if os.path.exists(f):
+            os.remove(f)
 
 
 if __name__ == "__main__":

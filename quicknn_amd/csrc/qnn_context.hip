@@ -972,6 +972,31 @@ int qnn_reload_tuning(void) {
   });
 }
 
+int qnn_phase_trace(qnn_ctx *ctx, uint64_t *dst, uint64_t count, uint64_t *copied) {
+  return guarded([&] {
+    check_ctx(ctx);
+    if (!dst || !copied) fail(QNN_E_ARGUMENT, "phase trace buffer");
+    sync(ctx);
+    const int n = mlp_phase_read(dst, size_t(count) * 8);
+    if (n == -2) fail(QNN_E_NOT_SUPPORTED, "not a phase-trace build (libqnn_hip_trace.so)");
+    if (n < 0) fail(QNN_E_INVALID_OP, "phase trace copy");
+    *copied = uint64_t(n);
+    return QNN_OK;
+  });
+}
+
+int qnn_stream_read(qnn_ctx *ctx, qnn_tensor *src, int count, qnn_tensor *dst) {
+  return guarded([&] {
+    check_ctx(ctx);
+    check_tensor(ctx, src, count);
+    check_tensor(ctx, dst, 1);
+    if (count < 4 || count % 4) fail(QNN_E_ARGUMENT, "stream read count");
+    misc_stream_read(src->ptr, size_t(count) * 4, reinterpret_cast<uint32_t *>(dst->ptr), ctx->stream);
+    hip_check(hipGetLastError(), "stream read launch");
+    return QNN_OK;
+  });
+}
+
 int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out) {
   return guarded([&] {
     if (!out) fail(QNN_E_ARGUMENT, "out");

@@ -166,6 +166,7 @@ I4Layout int4_layout(int rows, int cols, bool one_lane = false);
 void int4_dequant_launch(const I4Layout &l, const void *w, float *out, hipStream_t s);
 
 void misc_fill(float *dst, int n, uint32_t bits, hipStream_t s);
+void misc_stream_read(const void *src, size_t bytes, uint32_t *out, hipStream_t s);  // diagnostic HBM stream
 void misc_add(float *dst, const float *a, int n, int cols, int dst_stride, float alpha, int dst_off, int src_off,
               hipStream_t s);
 void misc_glu(float *dst, const float *a, const float *b, int n, int inter, int interleaved, int gelu,
@@ -235,6 +236,11 @@ struct MlpLaunch {
 size_t mlp_lds_bytes(int gg, int gd);
 int mlp_capacity(int gg, int gd, int device);  // co-resident workgroups (0: variant not built)
 bool mlp_launch(const MlpLaunch &a, int gg, int gd, int grid, hipStream_t s);  // false: not launched
+
+// Phase timestamps of the fused MLP kernels (trace builds only): copies up to
+// `bytes` of [workgroup][16] u64 and clears them; words copied, -2 when the
+// library is not a trace build, -1 on a HIP error.
+int mlp_phase_read(void *dst, size_t bytes);
 
 struct MoELaunch {
   const uint8_t *gate_up = nullptr;  // expert e: gate at gate_up + 2e*gu_stride, its up matrix gu_stride after it

@@ -1,6 +1,7 @@
 // qnn_misc.hip -- small ops on the decode path: fill, add, SwiGLU/GEGLU,
 // finite check, RMS/LayerNorm, MoE route, gather and scatter.  Semantics
 // follow the Vulkan shaders cited per kernel.
+#include "qnn_int4_dev.h"
 #include "qnn_route_dev.h"
 
 namespace qnn {
@@ -241,7 +242,32 @@ __global__ void k_pad_rows(float *dst, const float *src, int rows, int cols, int
 // Records the hardware XCC id (HW_REG_XCC_ID) of each workgroup.
 inline int blocks(long long n, int t) { return int((n + t - 1) / t); }
 
+// Plain stream of n16 16-byte pieces (diagnostic: the HBM stream floor the
+// matvec kernels are measured against).  The same loads as their weight
+// stream: non-temporal raw buffer loads, every piece requested at once (each
+// thread issues its U loads before using any); one store per launch at most,
+// on a condition that depends on every byte, so no load can be dropped.
+constexpr int kStreamU = 8;
+__global__ __launch_bounds__(256) void k_stream_read(const void *src, uint32_t n16, uint32_t *out) {
+  const auto r = dev::rsrc(src, size_t(n16) * 16);
+  const uint32_t base = (blockIdx.x * 256u + threadIdx.x) * 16u;
+  const uint32_t stride = gridDim.x * 256u * 16u;
+  uint4 v[kStreamU];
+#pragma unroll
+  for (int i = 0; i < kStreamU; ++i) v[i] = dev::ld128<dev::kStream>(r, base, uint32_t(i) * stride);
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < kStreamU; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
 }  // namespace
+
+void misc_stream_read(const void *src, size_t bytes, uint32_t *out, hipStream_t s) {
+  const uint32_t n16 = uint32_t(bytes / 16);
+  const uint32_t per_wg = 256u * kStreamU;
+  hipLaunchKernelGGL(k_stream_read, dim3((n16 + per_wg - 1) / per_wg), dim3(256), 0, s, src, n16, out);
+}
 
 void misc_fill(float *dst, int n, uint32_t bits, hipStream_t s) {
   hipLaunchKernelGGL(k_fill, dim3(blocks(n, 256)), dim3(256), 0, s, dst, n, bits);

@@ -32,6 +32,24 @@
 namespace qnn {
 namespace {
 
+// Phase timestamps, built only into libqnn_hip_trace.so (-DQNN_PHASE_TRACE):
+// thread 0 of workgroup wg stores the device's real-time counter (100 MHz)
+// when it reaches phase k of the fused kernels; qnn_phase_trace reads them.
+// Nothing else changes: the same work runs in the same order.
+constexpr int kPhaseWGs = 2048, kPhases = 16;
+#ifdef QNN_PHASE_TRACE
+__device__ unsigned long long g_phase[kPhaseWGs * kPhases];
+#define QNN_PHASE(k)                                                                                 \
+  do {                                                                                               \
+    if (threadIdx.x == 0 && blockIdx.x < kPhaseWGs)                                                  \
+      g_phase[blockIdx.x * kPhases + (k)] = __builtin_amdgcn_s_memrealtime();                        \
+  } while (0)
+#else
+#define QNN_PHASE(k) \
+  do {               \
+  } while (0)
+#endif
+
 template <int GG, int GD>
 __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   extern __shared__ uint4 dyn_lds[];
@@ -42,6 +60,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   constexpr int XG = 4 * (GG > GD ? GG : GD);
   const dev::XPlanes xs = dev::xplanes_at(dyn_lds, 1, XG);
   const I4Layout &lg = a.lg, &ld = a.ld;
+  QNN_PHASE(0);
 
   // ---- gate/up item of this workgroup (qnn_int4.hip I4_SWIGLU, T = 1: units
   //      padded to 16 so the gate tile u and the up tile u + 8 share an XCD).
@@ -80,6 +99,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   //         raises the block's flag.
   dev::stage_x<1, GG>(xs, xr, 1, ws0 * 32, sgroups * 32, a.hidden, tid, lane);
   __syncthreads();
+  QNN_PHASE(1);
   float acc[1] = {0.0f};
   if (ns > 0) {
     dev::XPlanes xp = xs;
@@ -91,6 +111,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   }
   if (part > 0) red[part][lane] = acc[0];
   __syncthreads();
+  QNN_PHASE(2);
   if (part == 0 && gu_on) {
     acc[0] += red[1][lane];
     acc[0] += red[2][lane];
@@ -107,7 +128,9 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
       __builtin_amdgcn_s_waitcnt(0);  // the block's h is at the coherence point
       if (lane == 0)
         __hip_atomic_store(a.flags + size_t(blk) * 64, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      QNN_PHASE(4);
     }
+    QNN_PHASE(3);
   }
   if (!dn_on) return;
 
@@ -136,11 +159,13 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
     }
   }
   __syncthreads();
+  QNN_PHASE(5);
   float4 hr[1][dev::x_iters<GD>()];
   dev::load_x<1, GD, dev::kCoherent>(hr, dev::rsrc(a.h, size_t(a.inter) * 4), [](int) { return 0u; }, 1, wsd * 32,
                                     sgd * 32, tid);
   dev::stage_x<1, GD>(xs, hr, 1, wsd * 32, sgd * 32, a.inter, tid, lane);
   __syncthreads();
+  QNN_PHASE(6);
   float scd[GD];
   dev::pick_scales<GD>(scd, qd, s0d);
   acc[0] = 0.0f;
@@ -154,6 +179,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   }
   if (part > 0) red[part][lane] = acc[0];
   __syncthreads();
+  QNN_PHASE(7);
   if (part > 0) return;
   acc[0] += red[1][lane];
   acc[0] += red[2][lane];
@@ -168,6 +194,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   }
   const int row = td * 64 + lane;
   if (row < a.hidden) a.y[row] = acc[0];
+  QNN_PHASE(8);
 }
 
 // An ordinary launch of at most the co-resident workgroup count (the caller
@@ -194,6 +221,20 @@ int capacity_of(int device) {
 }
 
 }  // namespace
+
+int mlp_phase_read(void *dst, size_t bytes) {
+#ifdef QNN_PHASE_TRACE
+  const size_t n = std::min(bytes, sizeof(g_phase));
+  if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_phase), n, 0, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  static const unsigned long long zeros[kPhaseWGs * kPhases] = {};
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_phase), zeros, sizeof(g_phase), 0, hipMemcpyHostToDevice) != hipSuccess) return -1;
+  return int(n / 8);
+#else
+  (void)dst;
+  (void)bytes;
+  return -2;
+#endif
+}
 
 size_t mlp_lds_bytes(int gg, int gd) { return dev::xplanes_bytes(1, 4 * std::max(gg, gd)); }
 

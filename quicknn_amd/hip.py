@@ -114,6 +114,8 @@ def lib():
             "qnn_ctx_destroy": (ctypes.c_int, [_vp]),
             "qnn_get_status": (ctypes.c_int, [_vp, ctypes.POINTER(Status)]),
             "qnn_reload_tuning": (ctypes.c_int, []),
+            "qnn_phase_trace": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]),
+            "qnn_stream_read": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp]),
             "qnn_tensor_new": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp)]),
             "qnn_recycle": (ctypes.c_int, [_vp, ctypes.POINTER(_vp)]),
             "qnn_scratch": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
@@ -199,7 +201,8 @@ def lib():
 
 
 EXPORTED = (
-    "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_reload_tuning", "qnn_tensor_new",
+    "qnn_last_error", "qnn_ctx_create", "qnn_ctx_destroy", "qnn_get_status", "qnn_reload_tuning", "qnn_phase_trace", "qnn_stream_read",
+    "qnn_tensor_new",
     "qnn_recycle",
     "qnn_scratch", "qnn_upload_raw", "qnn_download", "qnn_copy", "qnn_flush", "qnn_tensor_count",
     "qnn_tensor_device_ptr", "qnn_retain_weight", "qnn_preload_weights", "qnn_is_weight_resident",
@@ -407,6 +410,20 @@ class GPUContext:
         s = Status()
         _raise(lib().qnn_get_status(self.h, ctypes.byref(s)))
         return s
+
+    def StreamRead(self, src: Tensor, count: int, dst: Tensor) -> None:
+        """qnn_stream_read: one plain streaming read of count floats of src (diagnostic)."""
+        _raise(lib().qnn_stream_read(self.h, src.handle, count, dst.handle))
+
+    def PhaseTrace(self, workgroups: int = 2048):
+        """qnn_phase_trace: [workgroups, 16] uint64 phase timestamps of the fused MLP kernels
+        (trace builds only), cleared afterwards."""
+        import numpy as np
+
+        buf = np.zeros((workgroups, 16), np.uint64)
+        n = ctypes.c_uint64()
+        _raise(lib().qnn_phase_trace(self.h, ctypes.c_void_p(buf.ctypes.data), buf.size, ctypes.byref(n)))
+        return buf
 
     # -- tensors
     def NewTensor(self, count: int) -> Tensor:

@@ -137,6 +137,8 @@ function qnn_ctx_create(Device: Integer; WeightCacheBytes: UInt64; out Ctx: Poin
 function qnn_ctx_destroy(Ctx: Pointer): Integer; cdecl; external QNN_LIB;
 function qnn_get_status(Ctx: Pointer; out Status: TQnnStatus): Integer; cdecl; external QNN_LIB;
 function qnn_reload_tuning: Integer; cdecl; external QNN_LIB;
+function qnn_phase_trace(Ctx: Pointer; Dst: PUInt64; Count: UInt64; out Copied: UInt64): Integer; cdecl; external QNN_LIB;
+function qnn_stream_read(Ctx: Pointer; Src: Pointer; Count: Integer; Dst: Pointer): Integer; cdecl; external QNN_LIB;
 // ---- resident tensors
 function qnn_tensor_new(Ctx: Pointer; Count: Integer; out T: Pointer): Integer; cdecl; external QNN_LIB;
 function qnn_recycle(Ctx: Pointer; var T: Pointer): Integer; cdecl; external QNN_LIB;

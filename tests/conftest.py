@@ -69,11 +69,15 @@ def normwise_rel_err(y: np.ndarray, r: np.ndarray) -> float:
 
 
 def rand_int4(rng, n: int, k: int) -> np.ndarray:
-    """Valid packed INT4 rows [n, Int4RowBytes(k)] drawn directly (k a multiple of 32):
-    positive fp32 group scales in [0.001, 0.004) and uniform nibbles, the shape of
-    QuantizeInt4's output for N(0, 0.02) weights, without the packing cost."""
-    assert k % 32 == 0
-    g = k // 32
+    """Valid packed INT4 rows [n, Int4RowBytes(k)] drawn directly: positive fp32 group
+    scales in [0.001, 0.004) and uniform nibbles, the shape of QuantizeInt4's output for
+    N(0, 0.02) weights, without the packing cost.  Elements past k in the last group hold
+    nibble 8 (value 0), as QuantizeInt4 writes them."""
+    g = (k + 31) // 32
     p = rng.integers(0, 256, (n, g, 20), dtype=np.uint8)
     p[:, :, :4] = rng.uniform(0.001, 0.004, (n, g)).astype(np.float32)[..., None].view(np.uint8).reshape(n, g, 4)
+    tail = k - 32 * (g - 1)
+    for j in range(tail, 32):  # element j: byte 4 + j // 2, low nibble for even j
+        b = p[:, g - 1, 4 + j // 2]
+        p[:, g - 1, 4 + j // 2] = (b & 0xF0) | 8 if j % 2 == 0 else (b & 0x0F) | 0x80
     return p.reshape(n, g * 20)

@@ -37,7 +37,7 @@ def mlp(ctx, hip, layers, x0, hidden, inter):
 # one-token matvec runs as 16- and 8-wave workgroups while the fused kernel
 # keeps its four-wave slices.
 @pytest.mark.parametrize("hidden,inter,nl", [(2560, 9728, 3), (1024, 3072, 2), (2048, 768, 2), (512, 1536, 1),
-                                             (1024, 2048, 2), (768, 1024, 1)])
+                                             (1024, 2048, 2), (768, 1024, 1), (1024, 1000, 1), (768, 996, 1)])
 def test_fused_equals_per_op(ctx, rng, tune, hidden, inter, nl):
     from quicknn_amd import hip
 
@@ -58,6 +58,8 @@ def test_fused_equals_per_op(ctx, rng, tune, hidden, inter, nl):
     assert normwise_rel_err(y_f[0], want) < 1e-3
     if (hidden, inter) in ((2560, 9728), (1024, 2048), (768, 1024)):
         assert fused == nl  # the benchmark shape and the short down K-ranges run fused
+    if (hidden, inter) in ((1024, 1000), (768, 996)):
+        assert fused == nl  # h rows that end inside a down group
 
 
 def test_recorded_swiglu_settles_on_other_calls(ctx, rng):
