@@ -394,32 +394,49 @@ def run_cfg3(args, hip) -> dict:
     g, u, hh, y, logits = ctx.NewTensor(I), ctx.NewTensor(I), ctx.NewTensor(I), ctx.NewTensor(H), ctx.NewTensor(V)
     # Gemma2's layer (Gemma2.pas:142-198): q, k, v, o, gate, up, GEGLU, down.
     # Attention itself is outside the path; o reads q's output.
-    ops = {
-        "q": lambda lay: ctx.Linear(q, xt, lay["q"], None, None, 1, H, Q),
-        "k": lambda lay: ctx.Linear(k_, xt, lay["k"], None, None, 1, H, KV),
-        "v": lambda lay: ctx.Linear(v_, xt, lay["v"], None, None, 1, H, KV),
-        "o": lambda lay: ctx.Linear(o, q, lay["o"], None, None, 1, Q, H),
-        "gate": lambda lay: ctx.Linear(g, xt, lay["gate"], None, None, 1, H, I),
-        "up": lambda lay: ctx.Linear(u, xt, lay["up"], None, None, 1, H, I),
-        "geglu": lambda lay: ctx.Kernel(hip.GO_GEGLU, I, hh, g, u, None, [I, 0]),
-        "down": lambda lay: ctx.Linear(y, hh, lay["down"], None, None, 1, I, H),
+    # Each op on a given weight (o reads q's output).
+    opw = {
+        "q": lambda w: ctx.Linear(q, xt, w, None, None, 1, H, Q),
+        "k": lambda w: ctx.Linear(k_, xt, w, None, None, 1, H, KV),
+        "v": lambda w: ctx.Linear(v_, xt, w, None, None, 1, H, KV),
+        "o": lambda w: ctx.Linear(o, q, w, None, None, 1, Q, H),
+        "gate": lambda w: ctx.Linear(g, xt, w, None, None, 1, H, I),
+        "up": lambda w: ctx.Linear(u, xt, w, None, None, 1, H, I),
+        "down": lambda w: ctx.Linear(y, hh, w, None, None, 1, I, H),
     }
+    ops = {nm: (lambda lay, nm=nm: opw[nm](lay[nm])) for nm in opw}
+    ops["geglu"] = lambda lay: ctx.Kernel(hip.GO_GEGLU, I, hh, g, u, None, [I, 0])
+    order = ("q", "k", "v", "o", "gate", "up", "geglu", "down")
 
     def step():
         for lay in layers:
-            for fn in ops.values():
-                fn(lay)
+            for nm in order:
+                ops[nm](lay)
 
-    for _ in range(args.warmup):
+    for _ in range(max(1, args.warmup)):
         step()
     ms_step = timed_ms(ctx, step, args.steps)
     us_layer = ms_step * 1000 / L
     act = 4 * (H * 6 + Q * 2 + KV * 2 + I * 5 + H)  # activation reads and writes of the 8 ops
     layer_b = sum(wbytes.values()) + act
+    # Per op: its own launches back to back over copies of its weight totalling
+    # more than 512 MB, so every launch streams from HBM (the layer rotation
+    # above holds 8 copies, 25-135 MB per op, which the MALL could serve).
     per_op = {}
     for nm in ("q", "k", "v", "o", "gate", "up", "down"):
-        t = timed_ms(ctx, lambda: [ops[nm](lay) for lay in layers], max(3, args.steps // 5)) * 1000 / L
-        per_op[nm] = {"us": round(t, 2), "GBps": round(wbytes[nm] / (t * 1e-6) / 1e9, 1)}
+        e, n, kk = shapes[nm]
+        ncopy = max(L, -(-600_000_000 // wbytes[nm]))
+        copies = [lay[nm] for lay in layers] + [hip.MemoryBlock.gguf(data[nm], n, kk, e) for _ in range(ncopy - L)]
+        ctx.PreloadWeights(copies[L:])
+        run = lambda: [opw[nm](w) for w in copies]  # noqa: E731
+        run()  # first launches of this shape outside the timed region
+        ctx.Flush()
+        t = timed_ms(ctx, run, max(2, args.steps // 10)) * 1000 / ncopy
+        per_op[nm] = {"us": round(t, 2), "GBps": round(wbytes[nm] / (t * 1e-6) / 1e9, 1), "copies": ncopy,
+                      "rotation_MB": round(ncopy * wbytes[nm] / 1e6)}
+        del copies
+    ctx.Linear(logits, xt, head_b, None, None, 1, H, V)  # first launch of the head's shape, untimed
+    ctx.Flush()
     head_us = timed_ms(ctx, lambda: ctx.Linear(logits, xt, head_b, None, None, 1, H, V), 20) * 1000
     traffic_calibration_copy(ctx)
     ctx.close()
@@ -454,7 +471,8 @@ def run_cfg3(args, hip) -> dict:
         args, "GGUF K-quant decode HBM GB/s + us/layer, Gemma-2-9B shape", value, "GB/s", ms_step,
         "gguf-w/x16-fixed-act/fp32-acc",
         "synthetic (N(0,0.02) fp32 encoded to GGML blocks; rows past 16384 repeat; x N(0,1)); "
-        f"{L} layer copies rotated ({L * sum(wbytes.values()) / 1e6:.0f} MB)",
+        f"{L} layer copies rotated ({L * sum(wbytes.values()) / 1e6:.0f} MB); per-op figures over > 512 MB of "
+        "copies of each op's weight",
         {"workload": "configs[2]: Gemma-2-9B layer, hidden 3584, q/o Q4_K, k/v Q3_K, gate/up Q2_K + GEGLU, "
                      "down Q6_K, batch 1; head Q6_K 256000x3584", "global_batch": 1},
         us_per_layer=round(us_layer, 2), pct_of_hbm_peak=round(100 * value / HBM_PEAK_GBS, 2), per_op=per_op,
@@ -463,7 +481,8 @@ def run_cfg3(args, hip) -> dict:
                   "frac": round(per_op[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
                   "kernel": f"k_gguf_matvec ({dom}: {shapes[dom][1]}x{shapes[dom][2]})",
                   "kernel_us": per_op[dom]["us"], "bytes_per_launch": wbytes[dom],
-                  "timing": f"HIP events around {L}-launch runs of the op"},
+                  "timing": f"HIP events around back-to-back launches over {per_op[dom]['copies']} copies "
+                            f"({per_op[dom]['rotation_MB']} MB) of the op's weight"},
         cpu_baseline=cpu, setup_s=round(gen_s, 1))
 
 
@@ -492,40 +511,53 @@ def run_cfg4(args, hip) -> dict:
     for rows in (1, 16):
         x = rng.standard_normal((rows, H)).astype(np.float32)
         xt = ctx.UploadRaw(x)
+        # Batch 1: each layer copy gets E/K router outputs whose top-8 are the
+        # disjoint expert groups 8j..8j+7 (those logits raised by 10), so one
+        # rotation reads every expert of every copy (L x 128 experts, 1.5 GB)
+        # and no step finds its experts in the MALL.  Batch 16: one random
+        # router output per copy (about 80 distinct experts each, 950 MB).
+        nr = E // K if rows == 1 else 1
         routes, logit_t, distinct, first_logits = [], [], 0, None
-        for l in range(L):  # each layer copy gets its own router logits
-            lg = rng.standard_normal((rows, E)).astype(np.float32)
-            first_logits = lg if first_logits is None else first_logits
-            lt = ctx.UploadRaw(lg)
-            rt = ctx.NewTensor(2 * rows * K)
-            ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, rt, lt, None, None, [rows, E, K, 1])
-            routes.append(rt)
-            logit_t.append(lt)
-            distinct += len(set(ctx.Download(rt)[:rows * K].view(np.uint32).tolist()))
+        for l in range(L):
+            for j in range(nr):
+                lg = rng.standard_normal((rows, E)).astype(np.float32)
+                if rows == 1:
+                    lg[:, K * j:K * (j + 1)] += np.float32(10.0)
+                first_logits = lg if first_logits is None else first_logits
+                lt = ctx.UploadRaw(lg)
+                rt = ctx.NewTensor(2 * rows * K)
+                ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, rt, lt, None, None, [rows, E, K, 1])
+                routes.append((sets[l], rt))
+                logit_t.append(lt)
+                distinct += len(set(ctx.Download(rt)[:rows * K].view(np.uint32).tolist()))
+        calls = len(routes)
         out = ctx.NewTensor(rows * H)
 
         def step():
-            for l in range(L):
-                ctx.MoEExperts(sets[l], out, xt, routes[l], rows, K)
+            for st, rt in routes:
+                ctx.MoEExperts(st, out, xt, rt, rows, K)
 
         def route_step():  # GO_MOE_ROUTE again on the same logits: the same routes
-            for l in range(L):
-                ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, routes[l], logit_t[l], None, None, [rows, E, K, 1])
+            for (st, rt), lt in zip(routes, logit_t):
+                ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, rt, lt, None, None, [rows, E, K, 1])
 
         def layer_step():  # route then experts, as a decode layer issues them
-            for l in range(L):
-                ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, routes[l], logit_t[l], None, None, [rows, E, K, 1])
-                ctx.MoEExperts(sets[l], out, xt, routes[l], rows, K)
+            for (st, rt), lt in zip(routes, logit_t):
+                ctx.Kernel(hip.GO_MOE_ROUTE, 2 * rows * K, rt, lt, None, None, [rows, E, K, 1])
+                ctx.MoEExperts(st, out, xt, rt, rows, K)
 
         for _ in range(args.warmup):
             step()
             route_step()
+        layer_step()
+        ctx.Flush()
         ms = timed_ms(ctx, step, args.steps)
-        us_route = timed_ms(ctx, route_step, args.steps) * 1000 / L
-        us_both = timed_ms(ctx, layer_step, args.steps) * 1000 / L
-        us_layer = ms * 1000 / L
-        nbytes = distinct / L * per_expert + 4 * rows * (2 * H + 2 * K)
-        res[rows] = {"ms_step": ms, "us_per_layer": round(us_layer, 2), "distinct_experts": round(distinct / L, 1),
+        us_route = timed_ms(ctx, route_step, args.steps) * 1000 / calls
+        us_both = timed_ms(ctx, layer_step, args.steps) * 1000 / calls
+        us_layer = ms * 1000 / calls
+        nbytes = distinct / calls * per_expert + 4 * rows * (2 * H + 2 * K)
+        res[rows] = {"ms_step": ms, "us_per_layer": round(us_layer, 2), "distinct_experts": round(distinct / calls, 1),
+                     "rotation_MB": round(distinct * per_expert / 1e6),
                      "GBps": round(nbytes / (us_layer * 1e-6) / 1e9, 1), "bytes": nbytes, "x": x,
                      "logits": first_logits, "route_us": round(us_route, 2), "route_plus_experts_us": round(us_both, 2)}
     traffic_calibration_copy(ctx)
@@ -549,19 +581,23 @@ def run_cfg4(args, hip) -> dict:
         args, "MoE routed-expert HBM GB/s + us/layer, Qwen3-30B-A3B shape INT4", r1["GBps"], "GB/s", r1["ms_step"],
         "int4-w/x16-fixed-act/fp32-acc",
         "synthetic (N(0,0.02) bf16 experts packed to INT4; router logits N(0,1), top-8 renormalised); "
-        f"{L} layer copies with their own routes rotated",
+        f"{L} expert-set copies x {E // K} disjoint top-8 routes rotated at batch 1 ({r1['rotation_MB']} MB of "
+        "distinct experts per rotation, beyond the MALL)",
         {"workload": "configs[3]: 128 experts, hidden 2048, expert inter 768, top-8, batch 1 (batch 16 below)",
          "global_batch": 1},
         us_per_layer=r1["us_per_layer"], distinct_experts=r1["distinct_experts"],
         route_us=r1["route_us"], route_plus_experts_us=r1["route_plus_experts_us"],
         pct_of_hbm_peak=round(100 * r1["GBps"] / HBM_PEAK_GBS, 2),
         batch16={k: v for k, v in res[16].items()
-                 if k in ("us_per_layer", "distinct_experts", "GBps", "route_us", "route_plus_experts_us")},
+                 if k in ("us_per_layer", "distinct_experts", "GBps", "route_us", "route_plus_experts_us",
+                          "rotation_MB")},
+        rotation_MB=r1["rotation_MB"],
         roofline={"bound": "hbm", "achieved": r1["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": round(r1["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
                   "kernel": "k_moe_decode (one qnn_moe_experts call for one token: a single launch)",
                   "kernel_us": r1["us_per_layer"], "bytes_per_launch": round(r1["bytes"]),
-                  "timing": f"HIP events around {args.steps}x{L} calls"},
+                  "timing": f"HIP events around {args.steps}x{L * E // K} calls, each on experts no earlier call "
+                            "of the rotation read"},
         cpu_baseline=cpu, setup_s=round(gen_s, 1))
 
 
