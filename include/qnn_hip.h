@@ -67,10 +67,10 @@ extern "C" {
 #define QNN_WE_Q4_K 2
 #define QNN_WE_Q6_K 3
 #define QNN_WE_Q3_K 4
-#define QNN_WE_Q5_K 5      /* read from GGUF tables; no kernel here */
-#define QNN_WE_IQ4_NL 6    /* read from GGUF tables; no kernel here */
+#define QNN_WE_Q5_K 5
+#define QNN_WE_IQ4_NL 6
 #define QNN_WE_IQ3_S 7     /* read from GGUF tables; no kernel here */
-#define QNN_WE_IQ4_XS 8    /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ4_XS 8
 #define QNN_WE_Q2_K 9
 #define QNN_WE_IQ2_XXS 10  /* read from GGUF tables; no kernel here */
 #define QNN_WE_IQ2_S 11    /* read from GGUF tables; no kernel here */

@@ -245,8 +245,9 @@ void qo_int4_dequant_row(const uint8_t *row, int cols, float *out) {
 // ===========================================================================
 int qo_gguf_block_elements(int enc) {  // :67-75
   switch (enc) {
-    case QO_ENC_Q8_0: return 32;
-    case QO_ENC_Q4_K: case QO_ENC_Q6_K: case QO_ENC_Q3_K: case QO_ENC_Q2_K: return 256;
+    case QO_ENC_Q8_0: case QO_ENC_IQ4_NL: return 32;
+    case QO_ENC_Q4_K: case QO_ENC_Q6_K: case QO_ENC_Q3_K: case QO_ENC_Q2_K: case QO_ENC_Q5_K: case QO_ENC_IQ4_XS:
+      return 256;
     default: return -1;
   }
 }
@@ -257,9 +258,15 @@ int qo_gguf_block_bytes(int enc) {  // :77-93
     case QO_ENC_Q4_K: return 144;
     case QO_ENC_Q6_K: return 210;
     case QO_ENC_Q3_K: return 110;
+    case QO_ENC_Q5_K: return 176;
+    case QO_ENC_IQ4_NL: return 18;
+    case QO_ENC_IQ4_XS: return 136;
     default: return -1;
   }
 }
+
+// IQ4_NL_VALUES (:34): the non-linear 4-bit codebook of IQ4_NL and IQ4_XS.
+static const int kIQ4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 
 // GGUFValue (:136-253), the scalar per-element decode.
 float qo_gguf_value(const uint8_t *data, int enc, int64_t index) {
@@ -274,7 +281,8 @@ float qo_gguf_value(const uint8_t *data, int enc, int64_t index) {
       int q = (b[16 + (i / 128) * 32 + i % 32] >> (((i % 128) / 32) * 2)) & 3;
       return (half_at(b + 80) * float(b[group] & 15)) * float(q) - half_at(b + 82) * float(b[group] >> 4);
     }
-    case QO_ENC_Q4_K: {  // :189-207
+    case QO_ENC_Q4_K:
+    case QO_ENC_Q5_K: {  // :189-207 (Q5_K: quants at 48, the fifth bit from byte 16 + i % 32)
       int group = i / 32, scale, minimum;
       if (group < 4) {
         scale = b[4 + group] & 63;
@@ -283,8 +291,20 @@ float qo_gguf_value(const uint8_t *data, int enc, int64_t index) {
         scale = (b[8 + group] & 15) | ((b[group] >> 6) << 4);
         minimum = (b[8 + group] >> 4) | ((b[4 + group] >> 6) << 4);
       }
-      int q = (b[16 + (i / 64) * 32 + i % 32] >> ((group & 1) * 4)) & 15;
+      const int quant_offset = enc == QO_ENC_Q5_K ? 48 : 16;
+      int q = (b[quant_offset + (i / 64) * 32 + i % 32] >> ((group & 1) * 4)) & 15;
+      if (enc == QO_ENC_Q5_K) q |= ((b[16 + i % 32] >> group) & 1) << 4;
       return (half_at(b) * float(scale)) * float(q) - half_at(b + 2) * float(minimum);
+    }
+    case QO_ENC_IQ4_NL: {  // :229-233
+      int q = (b[2 + i % 16] >> ((i / 16) * 4)) & 15;
+      return half_at(b) * float(kIQ4[q]);
+    }
+    case QO_ENC_IQ4_XS: {  // :234-241
+      int group = i / 32;
+      int scale = ((b[4 + group / 2] >> ((group % 2) * 4)) & 15) | ((((int(b[2]) | (int(b[3]) << 8)) >> (group * 2)) & 3) << 4);
+      int q = (b[8 + group * 16 + i % 16] >> (((i % 32) / 16) * 4)) & 15;
+      return (half_at(b) * float(scale - 32)) * float(kIQ4[q]);
     }
     case QO_ENC_Q6_K: {  // :208-219
       int part = i / 128, quarter = (i % 128) / 32, lane = i % 32;
@@ -308,8 +328,43 @@ float qo_gguf_value(const uint8_t *data, int enc, int64_t index) {
 // GGUFDecodeBlock AVX2 branch (:290-364) with DecodeLow4 / DecodeBits /
 // DecodeSigned32 (src/io/QuickNN.GGUF.Decode.AVX2.inc:7-83): per-subblock
 // Scale = d*sc and Bias = -(dmin*m), then cvt(q)*Scale + Bias.
+// DecodeIQ4 (Decode.AVX2.inc:85-118): 16 bytes, low nibbles are elements
+// 0-15 and high nibbles 16-31, each cvt(codebook byte) * scale.
+static void decode_iq4(const uint8_t *src, float *dst, float scale) {
+  for (int i = 0; i < 32; ++i) {
+    const int q = (src[i % 16] >> ((i / 16) * 4)) & 15;
+    dst[i] = float(kIQ4[q]) * scale;
+  }
+}
+
 int qo_gguf_decode_block(const uint8_t *b, int enc, float *out) {
   switch (enc) {
+    case QO_ENC_Q5_K: {  // :296-312 with DecodeBits (:30-66): q = low4 | high1 << 4, cvt(q) * Scale + Bias
+      float d = half_at(b), dm = half_at(b + 2);
+      for (int g = 0; g < 8; ++g) {
+        int scale, minimum;
+        if (g < 4) { scale = b[4 + g] & 63; minimum = b[8 + g] & 63; }
+        else { scale = (b[8 + g] & 15) | ((b[g] >> 6) << 4); minimum = (b[8 + g] >> 4) | ((b[4 + g] >> 6) << 4); }
+        const float s = d * float(scale), bias = -(dm * float(minimum));
+        const uint8_t *low = b + 48 + (g / 2) * 32, *high = b + 16;
+        for (int i = 0; i < 32; ++i) {
+          const int q = ((low[i] >> ((g & 1) * 4)) & 15) | (((high[i] >> g) & 1) << 4);
+          out[g * 32 + i] = float(q) * s + bias;
+        }
+      }
+      return 0;
+    }
+    case QO_ENC_IQ4_NL:  // :338
+      decode_iq4(b + 2, out, half_at(b));
+      return 0;
+    case QO_ENC_IQ4_XS: {  // :339-348
+      const float d = half_at(b);
+      for (int g = 0; g < 8; ++g) {
+        const int scale = (((b[4 + g / 2] >> ((g & 1) * 4)) & 15) | ((((int(b[2]) | (int(b[3]) << 8)) >> (g * 2)) & 3) << 4)) - 32;
+        decode_iq4(b + 8 + g * 16, out + g * 32, d * float(scale));
+      }
+      return 0;
+    }
     case QO_ENC_Q8_0: {  // DecodeSigned32 (:68-83)
       __m256 d = _mm256_set1_ps(half_at(b));
       for (int c = 0; c < 4; ++c) {
@@ -420,8 +475,9 @@ int qo_gguf_read4(const uint8_t *data, int enc, int64_t index, float *o) {
     for (int t = 0; t < 4; ++t) o[t] = d * float(signed_byte(uint8_t(w >> (8 * t))));
     return 0;
   }
-  if (enc == QO_ENC_Q4_K) {
-    uint64_t base = (idx >> 8) * 144u;
+  if (enc == QO_ENC_Q4_K || enc == QO_ENC_Q5_K) {  // :605-617
+    const bool q5 = enc == QO_ENC_Q5_K;
+    uint64_t base = (idx >> 8) * (q5 ? 176u : 144u);
     uint32_t scale, minimum;
     if (group < 4) {
       scale = packed_byte(data, base + 4u + group) & 63u;
@@ -430,10 +486,32 @@ int qo_gguf_read4(const uint8_t *data, int enc, int64_t index, float *o) {
       scale = (packed_byte(data, base + 8u + group) & 15u) | ((packed_byte(data, base + group) >> 6) << 4);
       minimum = (packed_byte(data, base + 8u + group) >> 4) | ((packed_byte(data, base + 4u + group) >> 6) << 4);
     }
-    uint32_t w = packed_word(data, base + 16u + (item >> 6) * 32u + lane);
+    uint32_t w = packed_word(data, base + (q5 ? 48u : 16u) + (item >> 6) * 32u + lane);
+    uint32_t hw = q5 ? packed_word(data, base + 16u + lane) : 0u;
     float a = packed_half(data, base) * float(scale);
     float m = packed_half(data, base + 2u) * float(minimum);
-    for (int t = 0; t < 4; ++t) o[t] = a * float(((w >> (8 * t)) >> ((group & 1u) * 4u)) & 15u) - m;
+    for (int t = 0; t < 4; ++t) {
+      uint32_t q = ((w >> (8 * t)) >> ((group & 1u) * 4u)) & 15u;
+      if (q5) q |= ((((hw >> (8 * t)) & 255u) >> group) & 1u) << 4;
+      o[t] = a * float(q) - m;
+    }
+    return 0;
+  }
+  if (enc == QO_ENC_IQ4_NL) {  // :636-640
+    uint64_t base = (idx >> 5) * 18u;
+    uint32_t i = uint32_t(idx & 31u);
+    uint32_t w = packed_word(data, base + 2u + i % 16u);
+    float d = packed_half(data, base);
+    for (int t = 0; t < 4; ++t) o[t] = d * float(kIQ4[(((w >> (8 * t)) & 255u) >> ((i / 16u) * 4u)) & 15u]);
+    return 0;
+  }
+  if (enc == QO_ENC_IQ4_XS) {  // :641-647
+    uint64_t base = (idx >> 8) * 136u;
+    uint32_t scale = ((packed_byte(data, base + 4u + group / 2u) >> ((group % 2u) * 4u)) & 15u) |
+                     ((((packed_byte(data, base + 2u) | (packed_byte(data, base + 3u) << 8)) >> (group * 2u)) & 3u) << 4);
+    uint32_t w = packed_word(data, base + 8u + group * 16u + item % 16u);
+    float a = packed_half(data, base) * float(int(scale) - 32);
+    for (int t = 0; t < 4; ++t) o[t] = a * float(kIQ4[(((w >> (8 * t)) & 255u) >> (((item % 32u) / 16u) * 4u)) & 15u]);
     return 0;
   }
   if (enc == QO_ENC_Q6_K) {
@@ -623,17 +701,95 @@ static float packed_dot_q3k(const uint8_t *b, const float *x, int blocks) {
   return hreduce(_mm256_add_ps(acc0, acc1));
 }
 
+// PackedDotQ5K (src/io/QuickNN.GGUF.Dot.AVX2.inc:113-236): PackedDotQ4K with
+// the quants at 48 and the fifth bit of element i from byte 16 + i % 32,
+// shifted by the sub-block index.
+static float packed_dot_q5k(const uint8_t *b, const float *x, int blocks) {
+  __m256 acc0 = _mm256_setzero_ps(), acc1 = _mm256_setzero_ps();
+  const __m256i mask = _mm256_set1_epi32(15), one = _mm256_set1_epi32(1);
+  for (int blk = 0; blk < blocks; ++blk, b += 176) {
+    float d = half_at(b), dm = half_at(b + 2);
+    for (int g = 0; g < 8; ++g, x += 32) {
+      int sc, m;
+      if (g < 4) { sc = b[4 + g] & 63; m = b[8 + g] & 63; }
+      else { sc = ((b[g] >> 6) << 4) | (b[8 + g] & 15); m = ((b[4 + g] >> 6) << 4) | (b[8 + g] >> 4); }
+      __m256 s = _mm256_mul_ps(_mm256_set1_ps(float(sc)), _mm256_set1_ps(d));
+      __m256 mm = _mm256_mul_ps(_mm256_set1_ps(float(m)), _mm256_set1_ps(dm));
+      const uint8_t *q = b + 48 + (g >> 1) * 32;
+      __m128i shift = _mm_cvtsi32_si128((g & 1) * 4), hshift = _mm_cvtsi32_si128(g);
+      for (int c = 0; c < 4; ++c) {
+        __m256i v = _mm256_and_si256(_mm256_srl_epi32(load_u8x8_epi32(q + c * 8), shift), mask);
+        __m256i h = _mm256_and_si256(_mm256_srl_epi32(load_u8x8_epi32(b + 16 + c * 8), hshift), one);
+        v = _mm256_or_si256(v, _mm256_slli_epi32(h, 4));
+        __m256 t = _mm256_sub_ps(_mm256_mul_ps(_mm256_cvtepi32_ps(v), s), mm);
+        t = _mm256_mul_ps(t, _mm256_loadu_ps(x + c * 8));
+        if (c & 1) acc1 = _mm256_add_ps(acc1, t);
+        else acc0 = _mm256_add_ps(acc0, t);
+      }
+    }
+  }
+  return hreduce(_mm256_add_ps(acc0, acc1));
+}
+
+// The codebook values of 8 nibbles as floats (vpshufb of the 16-byte table,
+// vpmovsxbd, vcvtdq2ps).
+static __m256 iq4_8(const uint8_t *src, int hi) {
+  int v[8];
+  for (int j = 0; j < 8; ++j) v[j] = kIQ4[(src[j] >> (hi * 4)) & 15];
+  return _mm256_cvtepi32_ps(_mm256_setr_epi32(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]));
+}
+
+// PackedDotIQ4XS (Dot.AVX2.inc:238-328): per sub-block s = d * (sc - 32); per
+// 8 elements t = cvt(code) * s, t = t * x; pieces alternate between two
+// accumulators (elements 0-7, 16-23 in the first; 8-15, 24-31 in the second).
+static float packed_dot_iq4xs(const uint8_t *b, const float *x, int blocks) {
+  __m256 acc0 = _mm256_setzero_ps(), acc1 = _mm256_setzero_ps();
+  for (int blk = 0; blk < blocks; ++blk, b += 136) {
+    const float d = half_at(b);
+    for (int g = 0; g < 8; ++g, x += 32) {
+      const int sc = (((b[4 + g / 2] >> ((g & 1) * 4)) & 15) | ((((int(b[2]) | (int(b[3]) << 8)) >> (g * 2)) & 3) << 4)) - 32;
+      const __m256 s = _mm256_mul_ps(_mm256_set1_ps(float(sc)), _mm256_set1_ps(d));
+      const uint8_t *q = b + 8 + g * 16;
+      for (int c = 0; c < 4; ++c) {  // low nibbles 0-7, 8-15, then high nibbles 16-23, 24-31
+        __m256 t = _mm256_mul_ps(iq4_8(q + (c & 1) * 8, c >> 1), s);
+        t = _mm256_mul_ps(t, _mm256_loadu_ps(x + c * 8));
+        if (c & 1) acc1 = _mm256_add_ps(acc1, t);
+        else acc0 = _mm256_add_ps(acc0, t);
+      }
+    }
+  }
+  return hreduce(_mm256_add_ps(acc0, acc1));
+}
+
+// PackedDotIQ4NL (Dot.AVX2.inc:370-421): one accumulator; per 8 elements
+// t = cvt(code) * d, t = t * x, acc += t.
+static float packed_dot_iq4nl(const uint8_t *b, const float *x, int blocks) {
+  __m256 acc = _mm256_setzero_ps();
+  for (int blk = 0; blk < blocks; ++blk, b += 18, x += 32) {
+    const __m256 d = _mm256_set1_ps(half_at(b));
+    for (int c = 0; c < 4; ++c) {
+      __m256 t = _mm256_mul_ps(iq4_8(b + 2 + (c & 1) * 8, c >> 1), d);
+      t = _mm256_mul_ps(t, _mm256_loadu_ps(x + c * 8));
+      acc = _mm256_add_ps(acc, t);
+    }
+  }
+  return hreduce(acc);
+}
+
 // GGUFTryDot (src/io/QuickNN.GGUF.Quantization.pas:255-272) for the formats
 // in scope; returns NaN where the reference returns False (Q2_K, partial
 // super-blocks), leaving the caller to decode + VectorDot.
 static bool try_dot(const uint8_t *data, int enc, const float *x, int count, float &value) {
   if (count < 32 || count % 32 != 0) return false;
-  if (enc != QO_ENC_Q8_0 && count % 256 != 0) return false;
+  if (enc != QO_ENC_Q8_0 && enc != QO_ENC_IQ4_NL && count % 256 != 0) return false;
   switch (enc) {
     case QO_ENC_Q8_0: value = packed_dot_q8(data, x, count / 32); return true;
     case QO_ENC_Q6_K: value = packed_dot_q6k(data, x, count / 256); return true;
     case QO_ENC_Q3_K: value = packed_dot_q3k(data, x, count / 256); return true;
     case QO_ENC_Q4_K: value = packed_dot_q4k(data, x, count / 256); return true;
+    case QO_ENC_Q5_K: value = packed_dot_q5k(data, x, count / 256); return true;
+    case QO_ENC_IQ4_NL: value = packed_dot_iq4nl(data, x, count / 32); return true;
+    case QO_ENC_IQ4_XS: value = packed_dot_iq4xs(data, x, count / 256); return true;
   }
   return false;
 }

@@ -309,8 +309,9 @@ void *ensure_staging(qnn_ctx_s *ctx, size_t bytes) {
 // ---------------------------------------------------------------- weight cache
 int gguf_block_elements(int enc) {  // GGUF.Quantization.pas:67-75 (formats in this backend)
   switch (enc) {
-    case QNN_WE_Q8_0: return 32;
-    case QNN_WE_Q4_K: case QNN_WE_Q6_K: case QNN_WE_Q3_K: case QNN_WE_Q2_K: return 256;
+    case QNN_WE_Q8_0: case QNN_WE_IQ4_NL: return 32;
+    case QNN_WE_Q4_K: case QNN_WE_Q6_K: case QNN_WE_Q3_K: case QNN_WE_Q2_K: case QNN_WE_Q5_K: case QNN_WE_IQ4_XS:
+      return 256;
   }
   return -1;
 }
@@ -321,6 +322,9 @@ int gguf_block_bytes(int enc) {  // GGUF.Quantization.pas:77-93
     case QNN_WE_Q6_K: return 210;
     case QNN_WE_Q3_K: return 110;
     case QNN_WE_Q2_K: return 84;
+    case QNN_WE_Q5_K: return 176;
+    case QNN_WE_IQ4_NL: return 18;
+    case QNN_WE_IQ4_XS: return 136;
   }
   return -1;
 }
@@ -770,8 +774,10 @@ void record_linear(qnn_ctx_s *ctx, WeightEntry *e, const float *x, float *y, int
   // A second encoding may join (a layer's q/k/v often mix quant types): K-quants
   // at one unit per wave, at most two encodings per launch.
   const int enc = e->gg.enc;
-  const bool enc_ok = g.enc == enc || (bw == 1 && enc != QNN_WE_Q8_0 && g.enc != QNN_WE_Q8_0 &&
-                                       (g.enc2 < 0 || g.enc2 == enc));
+  auto mixable = [](int v) {  // the K-quants k_gguf_matvec_mixed is built for
+    return v == QNN_WE_Q4_K || v == QNN_WE_Q6_K || v == QNN_WE_Q3_K || v == QNN_WE_Q2_K;
+  };
+  const bool enc_ok = g.enc == enc || (bw == 1 && mixable(enc) && mixable(g.enc) && (g.enc2 < 0 || g.enc2 == enc));
   bool fits = g.count > 0 && g.count < kGGMaxGroup && g.x == x && enc_ok && g.bw == bw;
   for (int i = 0; fits && i < g.count; ++i) fits = g.y[i] != y;
   if (!fits) settle_pending(ctx);

@@ -1,4 +1,5 @@
-// qnn_gguf.hip -- GGML block formats (Q8_0, Q4_K, Q6_K, Q3_K, Q2_K) for gfx950.
+// qnn_gguf.hip -- GGML block formats (Q8_0, Q4_K, Q5_K, Q6_K, Q3_K, Q2_K,
+// IQ4_NL, IQ4_XS) for gfx950.
 //
 // Formats and decode rules: src/io/QuickNN.GGUF.Quantization.pas:136-253
 // (GGUFValue); the matvec replaces op 65 (ggufvector.comp:34-52) and the GGUF
@@ -15,7 +16,10 @@
 //   Q3_K  (110 B): main hmask|qs 96 (C=6), side1 scales (12), side2 d (2)
 //   Q2_K   (84 B): main scales|qs 80 (C=5), side1 d|dmin (4)
 //   Q8_0 (8x34 B): main 8x32 quants (C=16), side1 8 fp16 d (16)
-// so every wave load is a 16-byte (or 12/4/2-byte) load by 64 consecutive
+//   Q5_K  (176 B): main 176 (C=11)
+//   IQ4_XS (136 B): main quants 128 (C=8), side1 d|scales_h|scales_l (8)
+//   IQ4_NL (8x18 B): main 8x16 quants (C=8), side1 8 fp16 d (16)
+// so every wave load is a 16-byte (or 12/8/4/2-byte) load by 64 consecutive
 // lanes.  Bytes per weight are unchanged.
 //
 // Matvec.  The activation slice is quantised per 32 elements to 16-bit fixed
@@ -27,7 +31,11 @@
 //   Q6_K: sum = s2 * d*sc * (dot(q6, X) - 32 sum(X))            (q6 = q + 32)
 //   Q3_K: sum = s2 * d*(sc-32) * (dot(q3, X) - 4 sum(X))        (q3 = q + 4)
 //   Q8_0: sum = s2 * d * dot(q, X)
-// where X = 256 q1 + q2 and every dot is exact integer arithmetic.
+//   Q5_K: as Q4_K with 5-bit q (the fifth bit from qh)
+//   IQ4_NL: sum = s2 * d * dot(v, X)                      (v = codebook byte)
+//   IQ4_XS: sum = s2 * d*(ls-32) * dot(v, X)              (sub-block 32)
+// where X = 256 q1 + q2 and every dot is exact integer arithmetic; the IQ4
+// nibbles become their signed codebook bytes by a byte-permute lookup.
 #include "qnn_int4_dev.h"  // buffer-load helpers (rsrc, ld128, ld32f) and the exchange
 
 namespace qnn {
@@ -78,6 +86,33 @@ template <> struct Fmt<QNN_WE_Q6_K> { static constexpr int C = 13, S1 = 2, S2 = 
 template <> struct Fmt<QNN_WE_Q3_K> { static constexpr int C = 6, S1 = 12, S2 = 2; };
 template <> struct Fmt<QNN_WE_Q2_K> { static constexpr int C = 5, S1 = 4, S2 = 0; };
 template <> struct Fmt<QNN_WE_Q8_0> { static constexpr int C = 16, S1 = 16, S2 = 0; };
+template <> struct Fmt<QNN_WE_Q5_K> { static constexpr int C = 11, S1 = 0, S2 = 0; };
+template <> struct Fmt<QNN_WE_IQ4_XS> { static constexpr int C = 8, S1 = 8, S2 = 0; };
+template <> struct Fmt<QNN_WE_IQ4_NL> { static constexpr int C = 8, S1 = 16, S2 = 0; };
+
+// IQ4_NL_VALUES (src/io/QuickNN.GGUF.Quantization.pas:34) as signed bytes,
+// four per word: the codebook of IQ4_NL and IQ4_XS.
+constexpr uint32_t kIQ4W0 = 0xBFAD9881u;  // -127, -104,  -83,  -65
+constexpr uint32_t kIQ4W1 = 0xF6EADDCFu;  //  -49,  -35,  -22,  -10
+constexpr uint32_t kIQ4W2 = 0x26190D01u;  //    1,   13,   25,   38
+constexpr uint32_t kIQ4W3 = 0x71594535u;  //   53,   69,   89,  113
+__host__ __device__ constexpr int iq4_value(int q) {
+  return int(int8_t(((q < 4 ? kIQ4W0 : q < 8 ? kIQ4W1 : q < 12 ? kIQ4W2 : kIQ4W3) >> (8 * (q & 3))) & 255u));
+}
+static_assert(iq4_value(0) == -127 && iq4_value(1) == -104 && iq4_value(2) == -83 && iq4_value(3) == -65 &&
+                  iq4_value(4) == -49 && iq4_value(5) == -35 && iq4_value(6) == -22 && iq4_value(7) == -10 &&
+                  iq4_value(8) == 1 && iq4_value(9) == 13 && iq4_value(10) == 25 && iq4_value(11) == 38 &&
+                  iq4_value(12) == 53 && iq4_value(13) == 69 && iq4_value(14) == 89 && iq4_value(15) == 113,
+              "IQ4_NL_VALUES");
+// Four nibbles (one per byte, 0-15) -> their four codebook bytes: two byte
+// permutes over the 8-entry halves, then a per-byte select on bit 3.
+__device__ __forceinline__ uint32_t iq4_bytes(uint32_t nib) {
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kIQ4W1, kIQ4W0, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(kIQ4W3, kIQ4W2, sel);
+  const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & m) | (lo & ~m);
+}
 
 struct Planes {
   const uint8_t *main;
@@ -107,6 +142,13 @@ __device__ __forceinline__ void plane_addr(int enc, const GGLayout &l, int t, in
     case QNN_WE_Q6_K: if (o < 208) main_at(o); else s1_at(o - 208); break;
     case QNN_WE_Q3_K: if (o < 96) main_at(o); else if (o < 108) s1_at(o - 96); else s2_at(o - 108); break;
     case QNN_WE_Q2_K: if (o < 80) main_at(o); else s1_at(o - 80); break;
+    case QNN_WE_Q5_K: main_at(o); break;
+    case QNN_WE_IQ4_XS: if (o < 8) s1_at(o); else main_at(o - 8); break;
+    case QNN_WE_IQ4_NL: {  // unit of 8 blocks: block k = o / 18, byte j = o % 18: d at j < 2, quants after
+      const int k = o / 18, j = o % 18;
+      if (j < 2) s1_at(2 * k + j); else main_at(16 * k + j - 2);
+      break;
+    }
     default: {  // Q8_0 unit: block k = o / 34, byte j = o % 34: d at j < 2, quants after
       const int k = o / 34, j = o % 34;
       if (j < 2) s1_at(2 * k + j); else main_at(32 * k + j - 2);
@@ -137,7 +179,8 @@ __device__ float gguf_value_tiled(int enc, const GGLayout &l, const Planes &p, i
       const int q = int((B(16 + (i / 128) * 32 + i % 32) >> (((i % 128) / 32) * 2)) & 3);
       return (H(80) * float(B(group) & 15)) * float(q) - H(82) * float(B(group) >> 4);
     }
-    case QNN_WE_Q4_K: {
+    case QNN_WE_Q4_K:
+    case QNN_WE_Q5_K: {  // Q5_K: quants at 48, the fifth bit from byte 16 + i % 32
       const int group = i / 32;
       int scale, minimum;
       if (group < 4) {
@@ -147,8 +190,21 @@ __device__ float gguf_value_tiled(int enc, const GGLayout &l, const Planes &p, i
         scale = int((B(8 + group) & 15) | ((B(group) >> 6) << 4));
         minimum = int((B(8 + group) >> 4) | ((B(4 + group) >> 6) << 4));
       }
-      const int q = int((B(16 + (i / 64) * 32 + i % 32) >> ((group & 1) * 4)) & 15);
+      int q = int((B((enc == QNN_WE_Q5_K ? 48 : 16) + (i / 64) * 32 + i % 32) >> ((group & 1) * 4)) & 15);
+      if (enc == QNN_WE_Q5_K) q |= int((B(16 + i % 32) >> group) & 1u) << 4;
       return (H(0) * float(scale)) * float(q) - H(2) * float(minimum);
+    }
+    case QNN_WE_IQ4_NL: {
+      const int k = i / 32, j = i % 32;
+      const int q = int((B(18 * k + 2 + j % 16) >> ((j / 16) * 4)) & 15);
+      return H(18 * k) * float(iq4_value(q));
+    }
+    case QNN_WE_IQ4_XS: {
+      const int group = i / 32;
+      const int scale = int(((B(4 + group / 2) >> ((group % 2) * 4)) & 15) |
+                            ((((B(2) | (B(3) << 8)) >> (group * 2)) & 3) << 4));
+      const int q = int((B(8 + group * 16 + i % 16) >> (((i % 32) / 16) * 4)) & 15);
+      return (H(0) * float(scale - 32)) * float(iq4_value(q));
     }
     case QNN_WE_Q6_K: {
       const int part = i / 128, quarter = (i % 128) / 32, lane = i % 32;
@@ -182,7 +238,7 @@ __global__ void k_gguf_repack(const uint8_t *__restrict__ src, GGLayout l, uint8
   for (int o = 0; o < ub; ++o) {
     uint8_t v = 0;
     if (row < l.rows) {
-      const size_t so = size_t(u) * ub + o;  // Q8_0 units past the row end are zero blocks (d = 0)
+      const size_t so = size_t(u) * ub + o;  // Q8_0 / IQ4_NL units past the row end are zero blocks (d = 0)
       if (so < row_bytes) v = src[size_t(row) * row_bytes + so];
     }
     int plane;
@@ -390,6 +446,83 @@ __device__ float unit_q2_k(const uint4 *mw, uint32_t side, const XSlice<NG> &xs,
   return acc;
 }
 
+template <int NG>
+__device__ float unit_q5_k(const uint4 *mw, const XSlice<NG> &xs, int g0) {
+  const uint4 hd = mw[0];
+  const float d = half_f(hd.x & 0xFFFFu), dmin = half_f(hd.x >> 16);
+  const uint32_t s0 = hd.y, s4 = hd.z, s8 = hd.w;
+  auto byte = [&](int b) -> uint32_t {
+    const uint32_t w = b < 4 ? s0 : (b < 8 ? s4 : s8);
+    return (w >> (8 * (b & 3))) & 255u;
+  };
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int sc, m;
+    if (j < 4) {
+      sc = int(byte(j) & 63);
+      m = int(byte(4 + j) & 63);
+    } else {
+      sc = int((byte(4 + j) & 15) | ((byte(j - 4) >> 6) << 4));
+      m = int((byte(4 + j) >> 4) | ((byte(j) >> 6) << 4));
+    }
+    int ah = 0, al = 0;
+    // sub-block j: low nibbles at bytes 48 + (j/2)*32 (chunks 3 + 2*(j/2), +1),
+    // fifth bits at bytes 16..47 (chunks 1, 2), bit j
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t qd = sel4u(mw[3 + 2 * (j >> 1) + c], w), hb = sel4u(mw[1 + c], w);
+        const uint32_t q = (((j & 1) ? (qd >> 4) : qd) & 0x0F0F0F0Fu) | (((hb >> j) & 0x01010101u) << 4);
+        xdot(q, xs.h[g0 + j][4 * c + w], xs.l[g0 + j][4 * c + w], ah, al);
+      }
+    const float isum = float(combine<NG>(ah, al));
+    acc = fmaf(xs.s2[g0 + j], (d * float(sc)) * isum - (dmin * float(m)) * float(xs.sum32[g0 + j]), acc);
+  }
+  return acc;
+}
+
+// The integer dot of one 32-group of IQ4 nibbles (16 bytes: low nibbles are
+// elements 0-15, high nibbles 16-31) with the group's activation planes.
+template <int NG>
+__device__ __forceinline__ int iq4_group_dot(const uint4 &qs, const XSlice<NG> &xs, int g) {
+  int ah = 0, al = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const uint32_t qd = sel4u(qs, w & 3);
+    const uint32_t v = iq4_bytes(((w < 4) ? qd : (qd >> 4)) & 0x0F0F0F0Fu);
+    xdot(v, xs.h[g][w], xs.l[g][w], ah, al);
+  }
+  return combine<NG>(ah, al);
+}
+
+template <int NG>
+__device__ float unit_iq4_nl(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int g0) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {  // block k: quants in chunk k, d in side half k
+    const uint32_t dw = sel4u(s1, k >> 1);
+    const float d = half_f((k & 1) ? (dw >> 16) : (dw & 0xFFFFu));
+    acc = fmaf(float(iq4_group_dot<NG>(mw[k], xs, g0 + k)), d * xs.s2[g0 + k], acc);
+  }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_iq4_xs(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int g0) {
+  // side: bytes 0-1 d, 2-3 scales_h, 4-7 scales_l
+  const float d = half_f(s1.x & 0xFFFFu);
+  const uint32_t sh = s1.x >> 16, sl = s1.y;
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int ls = int(((sl >> (4 * j)) & 15) | (((sh >> (2 * j)) & 3) << 4)) - 32;
+    acc = fmaf(float(iq4_group_dot<NG>(mw[j], xs, g0 + j)), (d * float(ls)) * xs.s2[g0 + j], acc);
+  }
+  return acc;
+}
+
 // Workgroup = 4 waves on one 64-row tile (SWIGLU: 32 gate rows in lanes
 // 0-31, the same 32 up rows in lanes 32-63); slice = 4*BW units, wave w
 // streams units [w*BW, (w+1)*BW) of it.
@@ -457,6 +590,11 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
 #pragma unroll
     for (int c = 0; c < F::C; ++c) mw[b][c] = wload(mp + c * 64);
     if (F::S1 == 16) s1v[b] = wload(reinterpret_cast<const uint4 *>(P.side1) + tu * 64 + srow);
+    if (F::S1 == 8) {
+      const uint2 *q = reinterpret_cast<const uint2 *>(P.side1) + tu * 64 + srow;
+      const uint2 v = make_uint2(wload(reinterpret_cast<const uint32_t *>(q)), wload(reinterpret_cast<const uint32_t *>(q) + 1));
+      s1v[b] = make_uint4(v.x, v.y, 0u, 0u);
+    }
     if (F::S1 == 12) {
       const uint32_t *q = reinterpret_cast<const uint32_t *>(P.side1 + (tu * 64 + srow) * 12);
       s1v[b] = make_uint4(wload(q), wload(q + 1), wload(q + 2), 0u);
@@ -510,6 +648,9 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
       if (ENC == QNN_WE_Q6_K) acc += unit_q6_k<NG>(mw[b], s1w[b], xs, g0);
       if (ENC == QNN_WE_Q3_K) acc += unit_q3_k<NG>(mw[b], s1v[b], s2w[b], xs, g0);
       if (ENC == QNN_WE_Q2_K) acc += unit_q2_k<NG>(mw[b], s1w[b], xs, g0);
+      if (ENC == QNN_WE_Q5_K) acc += unit_q5_k<NG>(mw[b], xs, g0);
+      if (ENC == QNN_WE_IQ4_NL) acc += unit_iq4_nl<NG>(mw[b], s1v[b], xs, g0);
+      if (ENC == QNN_WE_IQ4_XS) acc += unit_iq4_xs<NG>(mw[b], s1v[b], xs, g0);
     }
   }
 
@@ -613,9 +754,14 @@ GGLayout gguf_layout(int enc, int rows, int cols) {
     case QNN_WE_Q3_K: l.main_chunks = 6; l.side1_bytes = 12; l.side2_bytes = 2; l.unit_bytes = 110; break;
     case QNN_WE_Q2_K: l.main_chunks = 5; l.side1_bytes = 4; l.side2_bytes = 0; l.unit_bytes = 84; break;
     case QNN_WE_Q8_0: l.main_chunks = 16; l.side1_bytes = 16; l.side2_bytes = 0; l.unit_bytes = 272; break;
+    case QNN_WE_Q5_K: l.main_chunks = 11; l.side1_bytes = 0; l.side2_bytes = 0; l.unit_bytes = 176; break;
+    case QNN_WE_IQ4_XS: l.main_chunks = 8; l.side1_bytes = 8; l.side2_bytes = 0; l.unit_bytes = 136; break;
+    case QNN_WE_IQ4_NL: l.main_chunks = 8; l.side1_bytes = 16; l.side2_bytes = 0; l.unit_bytes = 144; break;
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
-  l.src_row_bytes = enc == QNN_WE_Q8_0 ? (cols / 32) * 34 : (cols / 256) * l.unit_bytes;
+  l.src_row_bytes = enc == QNN_WE_Q8_0     ? (cols / 32) * 34
+                    : enc == QNN_WE_IQ4_NL ? (cols / 32) * 18
+                                           : (cols / 256) * l.unit_bytes;
   const size_t tu64 = size_t(l.tiles) * l.units * 64;
   auto up256 = [](size_t b) { return (b + 255) & ~size_t(255); };
   l.side1_off = up256(tu64 * l.main_chunks * 16);
@@ -682,6 +828,9 @@ void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s) {
     case QNN_WE_Q3_K: launch_enc<QNN_WE_Q3_K>(g, bw, s); break;
     case QNN_WE_Q2_K: launch_enc<QNN_WE_Q2_K>(g, bw, s); break;
     case QNN_WE_Q8_0: launch_enc<QNN_WE_Q8_0>(g, bw, s); break;
+    case QNN_WE_Q5_K: launch_enc<QNN_WE_Q5_K>(g, bw, s); break;
+    case QNN_WE_IQ4_NL: launch_enc<QNN_WE_IQ4_NL>(g, bw, s); break;
+    case QNN_WE_IQ4_XS: launch_enc<QNN_WE_IQ4_XS>(g, bw, s); break;
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
   hip_check(hipGetLastError(), "gguf matvec launch");

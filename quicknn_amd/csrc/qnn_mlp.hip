@@ -36,8 +36,8 @@ namespace {
 // thread 0 of workgroup wg stores the device's real-time counter (100 MHz)
 // when it reaches phase k of the fused kernels; qnn_phase_trace reads them.
 // Nothing else changes: the same work runs in the same order.
-constexpr int kPhaseWGs = 2048, kPhases = 16;
 #ifdef QNN_PHASE_TRACE
+constexpr int kPhaseWGs = 2048, kPhases = 16;
 __device__ unsigned long long g_phase[kPhaseWGs * kPhases];
 #define QNN_PHASE(k)                                                                                 \
   do {                                                                                               \

@@ -213,6 +213,93 @@ void enc_q2_k(const float *x, uint8_t *b) {
   }
 }
 
+// Q5_K (176 B): Q4_K's d, dmin and 6-bit scales and mins, 5-bit quants: the
+// low 4 bits at 48 + (i/64)*32 + i%32 (nibble by sub-block parity), the fifth
+// bit of element i in byte 16 + i%32, bit i/32.
+void enc_q5_k(const float *x, uint8_t *b) {
+  std::memset(b, 0, 176);
+  float scale[8], mins[8];
+  for (int j = 0; j < 8; ++j) {
+    float lo = 0, hi = -INFINITY;
+    for (int i = 0; i < 32; ++i) { lo = std::min(lo, x[j * 32 + i]); hi = std::max(hi, x[j * 32 + i]); }
+    scale[j] = (hi - lo) / 31.0f;
+    mins[j] = -lo;
+  }
+  put_half(b, *std::max_element(scale, scale + 8) / 63.0f);
+  put_half(b + 2, *std::max_element(mins, mins + 8) / 63.0f);
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8))), dmin = from_half(uint16_t(b[2] | (b[3] << 8)));
+  int sc[8], m[8];
+  for (int j = 0; j < 8; ++j) {
+    sc[j] = d > 0 ? clampi(rnd(scale[j] / d), 0, 63) : 0;
+    m[j] = dmin > 0 ? clampi(rnd(mins[j] / dmin), 0, 63) : 0;
+  }
+  for (int j = 0; j < 4; ++j) {
+    b[4 + j] = uint8_t((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+    b[8 + j] = uint8_t((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+    b[12 + j] = uint8_t((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+  }
+  for (int i = 0; i < 256; ++i) {
+    const int j = i / 32;
+    const float s = d * float(sc[j]), off = dmin * float(m[j]);
+    const int q = s > 0 ? clampi(rnd((x[i] + off) / s), 0, 31) : 0;
+    b[48 + (i / 64) * 32 + i % 32] |= uint8_t((q & 15) << ((j & 1) * 4));
+    b[16 + i % 32] |= uint8_t(((q >> 4) & 1) << j);
+  }
+}
+
+// IQ4_NL / IQ4_XS codebook (src/io/QuickNN.GGUF.Quantization.pas:34).
+const int kIQ4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+int iq4_nearest(float v) {  // index of the codebook value nearest v
+  int best = 0;
+  for (int q = 1; q < 16; ++q)
+    if (std::fabs(float(kIQ4[q]) - v) < std::fabs(float(kIQ4[best]) - v)) best = q;
+  return best;
+}
+// 32 values with scale d: element i's nibble in byte i % 16, high half for i >= 16.
+void put_iq4_32(const float *x, float d, uint8_t *qs) {
+  std::memset(qs, 0, 16);
+  for (int i = 0; i < 32; ++i) {
+    const int q = d != 0 ? iq4_nearest(x[i] / d) : 8;  // codebook[8] = 1: small, any is exact for d = 0
+    qs[i % 16] |= uint8_t(q << ((i / 16) * 4));
+  }
+}
+// The signed value of largest magnitude, so that it maps onto codebook[0] = -127.
+float signed_amax(const float *x, int n) {
+  float m = 0;
+  for (int i = 0; i < n; ++i)
+    if (std::fabs(x[i]) > std::fabs(m)) m = x[i];
+  return m;
+}
+
+// IQ4_NL (18 B per 32): fp16 d, 16 bytes of codebook nibbles.
+void enc_iq4_nl(const float *x, uint8_t *b) {
+  put_half(b, signed_amax(x, 32) / -127.0f);
+  put_iq4_32(x, from_half(uint16_t(b[0] | (b[1] << 8))), b + 2);
+}
+
+// IQ4_XS (136 B per 256): fp16 d, 6-bit signed sub-block scales (low nibbles
+// at 4 + j/2, high 2 bits of scale j at bits 2j of the 16-bit word at 2),
+// then 8 x 16 bytes of codebook nibbles.
+void enc_iq4_xs(const float *x, uint8_t *b) {
+  std::memset(b, 0, 136);
+  float s[8], smax = 0;
+  for (int j = 0; j < 8; ++j) {
+    s[j] = signed_amax(x + 32 * j, 32) / -127.0f;
+    if (std::fabs(s[j]) > std::fabs(smax)) smax = s[j];
+  }
+  put_half(b, smax / -32.0f);
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8)));
+  uint32_t high = 0;
+  for (int j = 0; j < 8; ++j) {
+    const int ls = (d != 0 ? clampi(rnd(s[j] / d), -32, 31) : 0) + 32;
+    b[4 + j / 2] |= uint8_t((ls & 15) << ((j % 2) * 4));
+    high |= uint32_t((ls >> 4) & 3) << (2 * j);
+    put_iq4_32(x + 32 * j, d * float(ls - 32), b + 8 + 16 * j);
+  }
+  b[2] = uint8_t(high & 255);
+  b[3] = uint8_t(high >> 8);
+}
+
 }  // namespace
 
 extern "C" {
@@ -256,6 +343,9 @@ int qnn_gguf_quantize(int encoding, const float *src, int64_t n, uint8_t *dst) {
     case QNN_WE_Q6_K: elems = 256; bytes = 210; fn = enc_q6_k; break;
     case QNN_WE_Q3_K: elems = 256; bytes = 110; fn = enc_q3_k; break;
     case QNN_WE_Q2_K: elems = 256; bytes = 84; fn = enc_q2_k; break;
+    case QNN_WE_Q5_K: elems = 256; bytes = 176; fn = enc_q5_k; break;
+    case QNN_WE_IQ4_NL: elems = 32; bytes = 18; fn = enc_iq4_nl; break;
+    case QNN_WE_IQ4_XS: elems = 256; bytes = 136; fn = enc_iq4_xs; break;
     default: return QNN_E_NOT_SUPPORTED;
   }
   if (!src || !dst || n < 0 || n % elems) return QNN_E_ARGUMENT;

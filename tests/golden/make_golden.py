@@ -44,6 +44,13 @@ FORMATS = [
     (oracle.ENC_Q3_K, "Q3_K", 256, 110, (108,)),
     (oracle.ENC_Q2_K, "Q2_K", 256, 84, (80, 82)),
 ]
+# Formats added later draw from their own random stream, so the fixtures of
+# the formats above stay as they were.
+FORMATS_EXT = [
+    (oracle.ENC_Q5_K, "Q5_K", 256, 176, (0, 2)),
+    (oracle.ENC_IQ4_NL, "IQ4_NL", 32, 18, (0,)),
+    (oracle.ENC_IQ4_XS, "IQ4_XS", 256, 136, (0,)),
+]
 
 
 def hexf(a) -> str:
@@ -83,7 +90,13 @@ def blocks(rng) -> dict:
                       "cols": cols, "input_hex": src.tobytes().hex(), "packed_hex": hexb(packed),
                       "values_hex": hexf(oracle.int4_dequant(packed, cols)[0])})
     out["INT4"] = cases
-    for enc, name, elems, nbytes, halves in FORMATS:
+    out.update(gguf_blocks(rng, FORMATS))
+    return out
+
+
+def gguf_blocks(rng, formats) -> dict:
+    out = {}
+    for enc, name, elems, nbytes, halves in formats:
         enc_block = hip.gguf_quantize(enc, (rng.standard_normal(elems) * 0.02).astype(np.float32))
         rnd = random_block(rng, nbytes, halves)
         cases = []
@@ -102,7 +115,13 @@ def matvecs(rng) -> dict:
     x = rng.standard_normal(k).astype(np.float32)
     y = oracle.cpu_linear(packed, oracle.ENC_INT4, x, k, 64)
     out["INT4"] = {"rows": 64, "cols": k, "w_hex": hexb(packed), "x_hex": hexf(x), "y_hex": hexf(y)}
-    for enc, name, elems, nbytes, _ in FORMATS:
+    out.update(gguf_matvecs(rng, FORMATS))
+    return out
+
+
+def gguf_matvecs(rng, formats) -> dict:
+    out = {}
+    for enc, name, elems, nbytes, _ in formats:
         kk = max(64, elems)
         wb = hip.gguf_quantize(enc, (rng.standard_normal(64 * kk) * 0.02).astype(np.float32))
         x = rng.standard_normal(kk).astype(np.float32)
@@ -134,7 +153,7 @@ def sha256s() -> dict:
     out = {"int4_qwen3_4b_layer0_seed1000": {
         "shapes": [[9728, 2560], [9728, 2560], [2560, 9728]],
         "sha256": [hashlib.sha256(m.tobytes()).hexdigest() for m in bench_layer0()]}}
-    for enc, name, elems, nbytes, _ in FORMATS:
+    for enc, name, elems, nbytes, _ in FORMATS + FORMATS_EXT:
         r = np.random.default_rng(2000 + enc)
         n, kk = 512, 3584 if elems == 256 else 3072
         w = (r.standard_normal(n * kk, dtype=np.float32) * np.float32(0.02))
@@ -147,6 +166,9 @@ def main() -> None:
     rng = np.random.default_rng(20240601)
     files = {"blocks.json": blocks(rng), "matvec.json": matvecs(rng), "moe_route.json": moe_route(rng),
              "sha256.json": sha256s()}
+    rng_ext = np.random.default_rng(20261202)
+    files["blocks.json"].update(gguf_blocks(rng_ext, FORMATS_EXT))
+    files["matvec.json"].update(gguf_matvecs(rng_ext, FORMATS_EXT))
     for fname, data in files.items():
         with open(os.path.join(OUT, fname), "w") as f:
             json.dump(data, f, indent=1)

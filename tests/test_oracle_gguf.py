@@ -10,11 +10,15 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q6_K, ENC_Q8_0, BLOCK_BYTES, BLOCK_ELEMENTS
+from oracle import (ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q8_0, BLOCK_BYTES,
+                    BLOCK_ELEMENTS)
 
-FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K]
+FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS]
 # fp16 fields (byte offsets within a block)
-HALF_FIELDS = {ENC_Q8_0: [0], ENC_Q4_K: [0, 2], ENC_Q6_K: [208], ENC_Q3_K: [108], ENC_Q2_K: [80, 82]}
+HALF_FIELDS = {ENC_Q8_0: [0], ENC_Q4_K: [0, 2], ENC_Q6_K: [208], ENC_Q3_K: [108], ENC_Q2_K: [80, 82],
+               ENC_Q5_K: [0, 2], ENC_IQ4_NL: [0], ENC_IQ4_XS: [0]}
+# IQ4_NL_VALUES (src/io/QuickNN.GGUF.Quantization.pas:34), typed in from the format definition
+IQ4 = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
 
 
 def f16(v: float) -> int:
@@ -137,6 +141,60 @@ def test_q2_k_known_answer():
     assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q2_K, 256), want)
 
 
+def test_q5_k_known_answer():
+    # Q4_K's fields (d = 1, dmin = 0.25, scale 2j+1, min j) with 5-bit quants q = (3i) % 32: the low
+    # nibble at 48 + (i/64)*32 + i%32, the fifth bit in byte 16 + i%32 at bit i/32.
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.frombuffer(struct.pack("<H", f16(1.0)), np.uint8)
+    b[2:4] = np.frombuffer(struct.pack("<H", f16(0.25)), np.uint8)
+    sc = [2 * j + 1 for j in range(8)]
+    mn = [j for j in range(8)]
+    for j in range(4):
+        b[4 + j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        b[8 + j] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        b[12 + j] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    q = np.array([(3 * i) % 32 for i in range(256)])
+    for i in range(256):
+        j = i // 32
+        b[48 + (i // 64) * 32 + i % 32] |= (q[i] & 15) << ((j & 1) * 4)
+        b[16 + i % 32] |= ((q[i] >> 4) & 1) << j
+    want = np.array([sc[i // 32] * q[i] - 0.25 * mn[i // 32] for i in range(256)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q5_K, 256), want)
+    # a Q4_K block reads the same quants' low nibbles at 16, so the fifth bit is the only difference
+    assert np.any(q >= 16)
+
+
+def test_iq4_nl_known_answer():
+    # d = 0.5; element i: nibble of byte 2 + i % 16 (high half for i >= 16), q = (5i + 3) % 16.
+    b = np.zeros(18 * 2, np.uint8)
+    for blk, d in enumerate((0.5, -2.0)):
+        b[18 * blk:18 * blk + 2] = np.frombuffer(struct.pack("<H", f16(d)), np.uint8)
+    q = np.array([(5 * i + 3) % 16 for i in range(64)])
+    for i in range(64):
+        blk, j = i // 32, i % 32
+        b[18 * blk + 2 + j % 16] |= q[i] << ((j // 16) * 4)
+    want = np.array([(0.5 if i < 32 else -2.0) * IQ4[q[i]] for i in range(64)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_IQ4_NL, 64), want)
+
+
+def test_iq4_xs_known_answer():
+    # d = 0.25; 6-bit sub-block scales ls (value ls - 32) with every high-bit pattern; q = (7i) % 16.
+    b = np.zeros(136, np.uint8)
+    b[0:2] = np.frombuffer(struct.pack("<H", f16(0.25)), np.uint8)
+    ls = [0, 5, 31, 32, 33, 47, 63, 16]
+    high = 0
+    for j in range(8):
+        b[4 + j // 2] |= (ls[j] & 15) << ((j % 2) * 4)
+        high |= ((ls[j] >> 4) & 3) << (2 * j)
+    b[2], b[3] = high & 255, high >> 8
+    q = np.array([(7 * i) % 16 for i in range(256)])
+    for i in range(256):
+        j = i // 32
+        b[8 + j * 16 + i % 16] |= q[i] << (((i % 32) // 16) * 4)
+    want = np.array([0.25 * (ls[i // 32] - 32) * IQ4[q[i]] for i in range(256)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_IQ4_XS, 256), want)
+
+
 @pytest.mark.parametrize("enc", FMTS)
 def test_packed_dot_and_linear_brute_force(rng, enc):
     k = 1024
@@ -162,5 +220,6 @@ def test_product_encoder_round_trip(rng, enc):
     dec = oracle.gguf_dequant_scalar(blocks, enc, 4096)
     assert np.all(np.isfinite(dec))
     rel = np.linalg.norm(dec - w) / np.linalg.norm(w)
-    bound = {ENC_Q8_0: 0.01, ENC_Q6_K: 0.03, ENC_Q4_K: 0.12, ENC_Q3_K: 0.25, ENC_Q2_K: 0.45}[enc]
+    bound = {ENC_Q8_0: 0.01, ENC_Q6_K: 0.03, ENC_Q4_K: 0.12, ENC_Q3_K: 0.25, ENC_Q2_K: 0.45, ENC_Q5_K: 0.06,
+             ENC_IQ4_NL: 0.12, ENC_IQ4_XS: 0.12}[enc]
     assert rel < bound, rel
