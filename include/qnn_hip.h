@@ -155,6 +155,7 @@ typedef struct {
   uint64_t moe_route_fused; /* of those, with the preceding GO_MOE_ROUTE computed in the launch (no reference counterpart) */
   uint64_t glu_fused;      /* multi-row Int4Linear gate + up + GO_SWIGLU triples run as one launch (no reference counterpart) */
   uint64_t async_weight_batches, async_weight_bytes; /* PrefetchWeights batches copied on the copy stream, and their bytes */
+  uint64_t gemm_h16;       /* Q8_0 multi-row Linear calls run over the weight's pre-expanded fp16 copy (no reference counterpart) */
 } qnn_status;
 
 /* ---------------------------------------------------------------------------

@@ -161,6 +161,7 @@ void reload_tuning() {
   t.fuse_mlp = env_int("QNN_FUSE_MLP", t.fuse_mlp);
   t.fuse_moe = env_int("QNN_FUSE_MOE", t.fuse_moe);
   t.q8_gemm_min_rows = env_int("QNN_Q8_GEMM_MIN_ROWS", t.q8_gemm_min_rows);
+  t.gemm_h16 = env_int("QNN_GEMM_H16", t.gemm_h16);
   t.attn_wgs = env_int("QNN_ATTN_WGS", t.attn_wgs);
   t.attn_min_chunk = env_int("QNN_ATTN_MIN_CHUNK", t.attn_min_chunk);
   t.gemm_nw = env_int("QNN_GEMM_NW", t.gemm_nw);
@@ -360,7 +361,7 @@ void evict_one_or_fail(qnn_ctx_s *ctx) {  // EvictOne (QuickNN.Vulkan.pas:551-57
     if (e->pins == 0 && e->op_pins == 0 && (!oldest || e->last_use < oldest->last_use)) oldest = e;
   }
   if (!oldest) fail(QNN_E_RANGE, "VRAM cache cannot hold the active chain");
-  if (ctx->on_evicted) ctx->on_evicted(oldest->identity, ctx->on_evicted_user);
+  if (ctx->on_evicted && !oldest->derived) ctx->on_evicted(oldest->identity, ctx->on_evicted_user);
   ctx->weights.erase(oldest->key);
   ctx->weight_bytes -= oldest->bytes;
   (void)hipFree(oldest->dptr);
@@ -394,8 +395,10 @@ WeightEntry *insert(qnn_ctx_s *ctx, WeightEntry *e) {
   e->last_use = ++ctx->clock;
   ctx->weights[e->key] = e;
   ctx->weight_bytes += e->bytes;
-  ctx->st.weight_uploads++;
-  ctx->st.weight_upload_bytes += e->source_bytes;
+  if (!e->derived) {  // a copy made on the device is not an upload
+    ctx->st.weight_uploads++;
+    ctx->st.weight_upload_bytes += e->source_bytes;
+  }
   return e;
 }
 
@@ -921,7 +924,53 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
 // Rows at which the MFMA GEMM replaces per-row matvecs (one weight pass per row).
 int q8_gemm_min_rows() { return std::max(2, tuning().q8_gemm_min_rows); }
 
-void run_q8_gemm(qnn_ctx_s *ctx, const WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
+// The fp16 copy of a resident Q8_0 weight for the GEMM (k_h16_gemm), found or
+// made on the device: a cache entry of its own (key + "/h16"), evicted like
+// any other (its eviction is not reported).  Null under graph capture when
+// it does not exist yet (making it allocates).
+WeightEntry *q8_h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
+  const std::string key = w->key + "/h16";
+  if (WeightEntry *h = lookup(ctx, key)) return h;
+  if (ctx->capturing) return nullptr;
+  auto *e = new WeightEntry();
+  e->key = key;
+  e->identity = w->identity;
+  e->kind = WKind::Raw;
+  e->derived = true;
+  e->bytes = q8_h16_bytes(w->gg.rows, w->gg.cols);
+  e->source_bytes = 0;
+  try {
+    e->dptr = alloc_weight(ctx, e->bytes);
+    q8_expand_h16_launch(w->gg, w->dptr, e->dptr, ctx->stream);
+  } catch (...) {
+    if (e->dptr) (void)hipFree(e->dptr);
+    delete e;
+    throw;
+  }
+  return insert(ctx, e);
+}
+
+void run_q8_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
+  if (tuning().gemm_h16 > 0 && rows >= tuning().gemm_h16) {
+    w->op_pins++;  // making the copy may evict: not the weight it is made from
+    WeightEntry *h = nullptr;
+    try {
+      h = q8_h16_entry(ctx, w);
+    } catch (...) {
+      w->op_pins--;
+      throw;
+    }
+    w->op_pins--;
+    if (h) {
+      const Q8GemmPlan p = q8_h16_plan(rows, in_dim, out_dim);
+      const size_t frag_off = 0, exp_off = (p.frag_bytes + 255) & ~size_t(255);
+      uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, exp_off + p.exp_bytes));
+      q8_h16_gemm_launch(p, x, rows, in_dim, out_dim, w->gg, w->dptr, h->dptr, ws + frag_off,
+                         reinterpret_cast<int *>(ws + exp_off), y, ctx->stream);
+      ctx->st.gemm_h16++;
+      return;
+    }
+  }
   const Q8GemmPlan p = q8_gemm_plan(rows, in_dim, out_dim);
   const size_t frag_off = 0, exp_off = (p.frag_bytes + 255) & ~size_t(255);
   uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, exp_off + p.exp_bytes));

@@ -324,7 +324,252 @@ __global__ __launch_bounds__(NW * 64) void k_q8_gemm(const GemmArgs g) {
   }
 }
 
+// ---- the same product over a pre-expanded fp16 copy of the weight ----------
+// The copy holds, for every weight, the fp16 value store_b decodes into LDS
+// (RNE(q * d * 2^-ew[n])), laid out as v_mfma_f32_32x32x16_f16 B fragments:
+// piece (n32, ks, lane) = 8 halfs W[32 n32 + lane % 32][16 ks + 8 (lane / 32) + 0..7]
+// at ((n32 * ksteps + ks) * 64 + lane) * 16 bytes; rows past N and columns
+// past K hold zeros.  It is made once per weight (k_q8_expand_h16) and kept
+// in the weight cache beside the Q8_0 copy.
+__global__ __launch_bounds__(256) void k_q8_expand_h16(GGLayout l, const uint8_t *__restrict__ w, int ksteps,
+                                                       size_t pieces, uint4 *__restrict__ out) {
+  const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= pieces) return;
+  const int lane = int(idx & 63);
+  const size_t nk = idx >> 6;
+  const int ks = int(nk % ksteps), n32 = int(nk / ksteps);
+  const int n = n32 * 32 + (lane & 31), k0 = ks * 16 + 8 * (lane >> 5);
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (n < l.rows && k0 < l.cols) {
+    const int kb = k0 >> 5, e0 = k0 & 31;
+    const int t = n >> 6, r = n & 63, u = kb >> 3, k8 = kb & 7;
+    const size_t tu = size_t(t) * l.units + u;
+    const uint32_t dword = *reinterpret_cast<const uint32_t *>(w + l.side1_off + (tu * 64 + r) * 16 + 4 * (k8 >> 1));
+    const float scale = ldexpf(1.0f, -reinterpret_cast<const int *>(w + l.rowexp_off)[n]);
+    const float ds = half_bits_to_f((k8 & 1) ? (dword >> 16) : (dword & 0xFFFFu)) * scale;  // exact
+    const uint2 q = *reinterpret_cast<const uint2 *>(w + ((tu * 16 + 2 * k8 + (e0 >> 4)) * 64 + r) * 16 + (e0 & 15));
+    const uint32_t qw[2] = {q.x, q.y};
+    uint32_t hw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t word = qw[i >> 1] >> (16 * (i & 1));
+      hw[i] = pack_h2(float(int(int8_t(word & 255u))) * ds, float(int(int8_t((word >> 8) & 255u))) * ds);
+    }
+    v = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  }
+  out[idx] = v;
+}
+
+// Workgroup tile 128 x 192 (a 512 x 12288 product is 4 x 64 = 256
+// workgroups, one per CU), four waves of 64 x 96 (2 x 3 MFMA tiles), K-tiles
+// of 64.  A K-tile's fragments (A: 4 x 4 pieces, B: 6 x 4 pieces of 1 KiB)
+// go from global memory straight into LDS (buffer_load ... lds: each lane's
+// 16 bytes land at M0 + 16 lane, so a piece keeps its [lane] order) through
+// HST stages of 40 KiB (all 160 KiB of the CU's LDS: the loads run up to
+// three K-tiles ahead).  Per K-tile, one barrier: after it the K-tile's stage
+// is free (every wave holds its fragments in registers) and takes the loads
+// of K-tile kt + HST; then each wave reads the next K-tile's fragments (20
+// pieces, 80 VGPRs) while its MFMAs run on the current ones.  Per 32 x 32
+// tile the MFMAs run over K in order, as in k_q8_gemm, so C is the same, bit
+// for bit.
+constexpr int HBM = 128, HBN = 192, HKT = 4;  // rows, columns, K-steps (of 16) per K-tile
+constexpr int HAP = HBM / 32 * HKT, HBP = HBN / 32 * HKT;  // 1 KiB pieces per K-tile: 16 + 24
+constexpr int HPW = (HAP + HBP) / 4;                        // pieces each wave loads per K-tile: 10
+constexpr int HST = 4;                                      // LDS stages
+constexpr size_t kH16Lds = size_t(HST) * (HAP + HBP) * 1024;
+static_assert(HAP % 4 == 0 && kH16Lds <= 160 * 1024, "h16 tiling");
+struct H16Args {
+  const uint4 *afrag;  // [m_pad / 32][ksteps][64]
+  const int *ea;
+  const uint4 *wfrag;  // [n_pad / 32][ksteps][64]
+  const int *ew;       // [rows] weight row exponents
+  float *c;
+  int M, N, ksteps, ktiles, mtiles, ntiles;
+};
+
+// One 1 KiB piece from global memory into LDS at `lds` (wave-uniform).  The
+// compiler does not see these writes to LDS: h16_vmwait orders them.
+__device__ __forceinline__ void h16_dma(Rsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r),
+               "s"(soff)
+               : "memory");
+}
+// Wait until at most N of this wave's vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void h16_vmwait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+extern __shared__ uint4 h16_lds[];  // HST stages of [HAP + HBP] pieces: A [m32][ks], then B [n32][ks]
+
+struct H16Frags {
+  half8 a[HKT][2], b[HKT][3];
+};
+
+__global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
+  const int b = blockIdx.x;
+  const int xcd = b & 7, kq = b >> 3;  // the M-tiles of an N-tile share blockIdx % 8 (an XCD, its L2)
+  const int q = kq / g.mtiles;
+  const int ntile = q * 8 + xcd, mtile = kq - q * g.mtiles;
+  if (ntile >= g.ntiles) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  const Rsrc ar = rsrc(g.afrag, size_t(g.mtiles) * (HBM / 32) * g.ksteps * 1024);
+  const Rsrc br = rsrc(g.wfrag, size_t(g.ntiles) * (HBN / 32) * g.ksteps * 1024);
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(h16_lds));
+  // This wave loads pieces p = wave + 4 i of every K-tile: i < HAP / 4 are A pieces.
+  uint32_t voff[HPW];
+#pragma unroll
+  for (int i = 0; i < HPW; ++i) {
+    const int p = wave + 4 * i;
+    if (i < HAP / 4) {
+      voff[i] = uint32_t(((size_t(mtile) * (HBM / 32) + p / HKT) * g.ksteps + p % HKT) * 1024 + lane * 16);
+    } else {
+      const int pb = p - HAP;
+      voff[i] = uint32_t(((size_t(ntile) * (HBN / 32) + pb / HKT) * g.ksteps + pb % HKT) * 1024 + lane * 16);
+    }
+  }
+  auto dma = [&](int kt, int i) {
+    const uint32_t st = lds0 + uint32_t(kt % HST) * ((HAP + HBP) * 1024u);
+    h16_dma(i < HAP / 4 ? ar : br, __builtin_amdgcn_readfirstlane(st + uint32_t(wave + 4 * i) * 1024u), voff[i],
+            uint32_t(kt) * (HKT * 1024u));
+  };
+  // Piece r of this wave's 5 HKT per K-tile: K-step r / 5, then A rows wm*2 + 0..1, B columns wn*3 + 0..2.
+  auto read1 = [&](H16Frags &f, const uint4 *st, int r) {
+    const int ks = r / 5, j = r % 5;
+    if (j < 2)
+      __builtin_memcpy(&f.a[ks][j], &st[((wm * 2 + j) * HKT + ks) * 64 + lane], 16);
+    else
+      __builtin_memcpy(&f.b[ks][j - 2], &st[(HAP + (wn * 3 + j - 2) * HKT + ks) * 64 + lane], 16);
+  };
+
+  f32x16 acc[2][3];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // K-tile kt: wait for K-tile kt + 1 (this wave's pieces, then everybody's:
+  // K-tile kt's stage is then free), then the 24 MFMAs of K-tile kt, each
+  // followed by one read of K-tile kt + 1's fragments and every second one by
+  // one load of K-tile kt + HST into kt's stage, in this order (an MFMA does
+  // not wait behind the wave's memory instructions).
+  auto tile = [&](auto REFILL, const H16Frags &cur, H16Frags &nxt, int kt) {
+    if (decltype(REFILL)::value)
+      h16_vmwait<HPW * (HST - 2)>();
+    else
+      h16_vmwait<0>();
+    __syncthreads();
+    const uint4 *st = h16_lds + ((kt + 1) % HST) * ((HAP + HBP) * 64);  // past the end: unused
+#pragma unroll
+    for (int j = 0; j < 6 * HKT; ++j) {
+      const int ks = j / 6, mb = (j % 6) / 3, nb = j % 3;
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.a[ks][mb], cur.b[ks][nb], acc[mb][nb], 0, 0, 0);
+      if (j < 5 * HKT) read1(nxt, st, j);
+      if (decltype(REFILL)::value && (j & 1) && j / 2 < HPW) dma(kt + HST, j / 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < HST; ++d)
+    if (d < g.ktiles)
+#pragma unroll
+      for (int i = 0; i < HPW; ++i) dma(d, i);
+  H16Frags f0, f1;
+  if (HST - 1 < g.ktiles)
+    h16_vmwait<HPW * (HST - 1)>();
+  else
+    h16_vmwait<0>();
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 5 * HKT; ++r) read1(f0, h16_lds, r);
+  using Y = std::true_type;
+  using N = std::false_type;
+  int kt = 0;
+  for (; kt + 1 + HST < g.ktiles; kt += 2) {  // both K-tiles refill
+    tile(Y(), f0, f1, kt);
+    tile(Y(), f1, f0, kt + 1);
+  }
+  for (; kt < g.ktiles; kt += 2) {
+    if (kt + HST < g.ktiles)
+      tile(Y(), f0, f1, kt);
+    else
+      tile(N(), f0, f1, kt);
+    if (kt + 1 < g.ktiles) tile(N(), f1, f0, kt + 1);
+  }
+
+  // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32 x 32 tile.
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) {
+    const int col = ntile * HBN + (wn * 3 + nb) * 32 + (lane & 31);
+    if (col >= g.N) continue;
+    const int ew = g.ew[col];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = mtile * HBM + (wm * 2 + mb) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], g.ea[row] + ew);
+      }
+    }
+  }
+}
+
 }  // namespace
+
+size_t q8_h16_bytes(int rows, int cols) {
+  const size_t n_pad = size_t((rows + HBN - 1) / HBN) * HBN, k_pad = size_t((cols + 63) / 64) * 64;
+  return n_pad * k_pad * 2;
+}
+
+void q8_expand_h16_launch(const GGLayout &l, const void *w, void *out, hipStream_t s) {
+  const int ksteps = (l.cols + 63) / 64 * 4;
+  const size_t pieces = q8_h16_bytes(l.rows, l.cols) / 16;
+  hipLaunchKernelGGL(k_q8_expand_h16, dim3((pieces + 255) / 256), dim3(256), 0, s, l, static_cast<const uint8_t *>(w),
+                     ksteps, pieces, static_cast<uint4 *>(out));
+  hip_check(hipGetLastError(), "q8 fp16 expansion");
+}
+
+Q8GemmPlan q8_h16_plan(int M, int K, int N) {
+  Q8GemmPlan p;
+  p.m_pad = (M + HBM - 1) / HBM * HBM;
+  p.k_pad = (K + 63) / 64 * 64;
+  p.ksteps = p.k_pad / 16;
+  p.mtiles = p.m_pad / HBM;
+  p.ntiles = (N + HBN - 1) / HBN;
+  p.frag_bytes = size_t(p.m_pad) * p.k_pad * 2;
+  p.exp_bytes = size_t(p.m_pad) * 4;
+  return p;
+}
+
+void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
+                        const void *w16, void *frag, int *ea, float *c, hipStream_t s) {
+  hipLaunchKernelGGL(k_act_rowexp, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.m_pad, ea);
+  const size_t pieces = size_t(p.m_pad / 32) * p.ksteps * 64;
+  hipLaunchKernelGGL(k_act_frag, dim3((pieces + 255) / 256), dim3(256), 0, s, a, ea, M, K, p.ksteps, pieces,
+                     static_cast<uint4 *>(frag));
+  H16Args g;
+  g.afrag = static_cast<const uint4 *>(frag);
+  g.ea = ea;
+  g.wfrag = static_cast<const uint4 *>(w16);
+  g.ew = reinterpret_cast<const int *>(static_cast<const uint8_t *>(w) + l.rowexp_off);
+  g.c = c;
+  g.M = M;
+  g.N = N;
+  g.ksteps = p.ksteps;
+  g.ktiles = p.ksteps / HKT;
+  g.mtiles = p.mtiles;
+  g.ntiles = p.ntiles;
+  const int grid = (p.ntiles + 7) / 8 * 8 * p.mtiles;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&k_h16_gemm), hipFuncAttributeMaxDynamicSharedMemorySize, int(kH16Lds));
+  hip_check(attr, "fp16-copy gemm LDS size");
+  hipLaunchKernelGGL(k_h16_gemm, dim3(grid), dim3(256), kH16Lds, s, g);
+  hip_check(hipGetLastError(), "q8 fp16-copy gemm launch");
+}
 
 void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s) {
   const int rows = l.tiles * 64;

@@ -41,6 +41,7 @@ struct Tuning {
   int fuse_mlp = 1;          // QNN_FUSE_MLP: recorded INT4 SwiGLU + down as one launch
   int fuse_moe = 1;          // QNN_FUSE_MOE: one-token routed experts (and route) as one launch
   int q8_gemm_min_rows = 4;  // QNN_Q8_GEMM_MIN_ROWS: rows from which Q8_0 Linear takes the GEMM
+  int gemm_h16 = 128;        // QNN_GEMM_H16: rows from which the GEMM runs over a pre-expanded fp16 copy (0: never)
   int attn_wgs = 512;        // QNN_ATTN_WGS: cached-attention workgroup target
   int attn_min_chunk = 64;   // QNN_ATTN_MIN_CHUNK: keys per chunk, at least
   int gemm_nw = 0;           // QNN_GEMM_NW: waves per Q8_0 GEMM workgroup (4 or 8)
@@ -107,6 +108,8 @@ struct WeightEntry {
   uint64_t last_use = 0;
   int raw_dtype = 0;       // Raw: dtype of the copied vector
   hipEvent_t ready = nullptr;  // written by an asynchronous prefetch: the compute stream waits for it first
+  bool derived = false;        // made on the device from another entry (the fp16 copy of a Q8_0 weight):
+                               // its eviction is not reported through OnWeightEvicted
   I4Layout i4;
   GGLayout gg;
 };
@@ -297,6 +300,14 @@ Q8GemmPlan q8_gemm_plan(int M, int K, int N);
 void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
                     void *frag, int *ea, float *c, hipStream_t s);
 void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
+// The same product over a pre-expanded fp16 copy of the weight (qnn_gemm.hip,
+// k_h16_gemm): q8_h16_bytes of device memory per weight, made once by
+// q8_expand_h16_launch; the results equal q8_gemm_launch's bit for bit.
+size_t q8_h16_bytes(int rows, int cols);
+void q8_expand_h16_launch(const GGLayout &l, const void *w, void *out, hipStream_t s);
+Q8GemmPlan q8_h16_plan(int M, int K, int N);
+void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
+                        const void *w16, void *frag, int *ea, float *c, hipStream_t s);
 // Multi-row Q8_0 projection with activations quantised per 32-element block to
 // int8, on the int8 matrix cores (qnn_gemm_i8.hip).  K % 32 == 0.
 size_t q8_i8_workspace(int M, int K);

@@ -91,7 +91,7 @@ class Status(ctypes.Structure):
         "gemm_calls", "gguf_calls", "int4_calls", "moe_calls", "weight_uploads", "weight_upload_bytes",
         "weight_cache_hits", "weight_cache_misses", "weight_evictions", "readbacks", "submissions",
         "weight_bytes", "weight_limit", "activation_bytes", "activation_peak_bytes", "mlp_fused", "linear_grouped", "moe_fused", "moe_route_fused",
-        "glu_fused", "async_weight_batches", "async_weight_bytes")]
+        "glu_fused", "async_weight_batches", "async_weight_bytes", "gemm_h16")]
 
 
 _lib = None

@@ -92,6 +92,7 @@ type
     WeightBytes, WeightLimit, ActivationBytes, ActivationPeakBytes: UInt64;
     MLPFused, LinearGrouped, MoEFused, MoERouteFused, GLUFused: UInt64;
     AsyncWeightBatches, AsyncWeightBytes: UInt64;
+    GemmH16: UInt64;
   end;
 
   TQnnWeightEvictedFn = procedure(Identity: UInt64; User: Pointer); cdecl;

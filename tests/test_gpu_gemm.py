@@ -47,6 +47,28 @@ def test_prefill_shape_matches_cpu_paths(ctx, rng):
         assert normwise_rel_err(got[r], want[r]) <= TOL, r
 
 
+@pytest.mark.parametrize("m,k,n", [(512, 3072, 12288), (128, 3072, 12288), (257, 1024, 97), (300, 640, 200),
+                                   (130, 96, 1000), (1000, 4096, 385)])
+def test_fp16_copy_equals_decoding_kernel(ctx, rng, tune, m, k, n):
+    """From QNN_GEMM_H16 rows (default 128) the product runs over a pre-expanded fp16 copy
+    of the weight (k_h16_gemm, qnn_status.gemm_h16), made once and cached: every output equals
+    the kernel that decodes the Q8_0 blocks per K-tile (k_q8_gemm), bit for bit, including
+    ragged M, N and K; the second call reuses the copy."""
+    w = q8(rng, n, k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    h0 = ctx.status().gemm_h16
+    fast = run_linear(ctx, w, a, n)
+    again = run_linear(ctx, w, a, n)
+    assert ctx.status().gemm_h16 - h0 == 2
+    tune("QNN_GEMM_H16", "0")
+    dec = run_linear(ctx, w, a, n)
+    assert ctx.status().gemm_h16 - h0 == 2
+    assert np.array_equal(fast.view(np.uint32), dec.view(np.uint32))
+    assert np.array_equal(again.view(np.uint32), fast.view(np.uint32))
+    for r in (0, m // 2, m - 1):
+        assert normwise_rel_err(fast[r], oracle.cpu_linear(w, ENC_Q8_0, a[r], k, n)) <= TOL, r
+
+
 @pytest.mark.parametrize("m,k,n", [(4, 96, 100), (5, 32, 64), (257, 1024, 97), (300, 640, 200), (33, 4096, 4096),
                                    (16, 2048, 6144)])
 def test_ragged_shapes(ctx, rng, m, k, n):

@@ -41,6 +41,42 @@ def run(ctx, w, xt, yt):
     return ctx.Download(yt)
 
 
+def test_fp16_gemm_copy_is_an_unreported_cache_entry(small, rng):
+    """The pre-expanded fp16 copy the Q8_0 GEMM makes from a resident weight (k_h16_gemm) is a
+    cache entry of its own: LRU eviction may drop it while the Q8_0 weight stays resident, and
+    that eviction is not reported through OnWeightEvicted (no weight left the cache); the next
+    GEMM on the weight makes it again, with the same result.  Runs first: an empty 9 MiB cache
+    holds one Q8_0 weight (2.2 MB) with its fp16 copy (4.3 MB) and a second Q8_0 weight, not
+    a second fp16 copy."""
+    from quicknn_amd import hip
+
+    ctx = small
+    m, k, n = 128, 1024, 2048
+    ws = [hip.MemoryBlock.gguf(hip.gguf_quantize(hip.WE_Q8_0, (rng.standard_normal(n * k) * 0.02).astype(np.float32)),
+                               n, k, hip.WE_Q8_0) for _ in range(2)]
+    a = ctx.UploadRaw(rng.standard_normal((m, k)).astype(np.float32))
+    y, y1, x1 = ctx.NewTensor(m * n), ctx.NewTensor(n), ctx.UploadRaw(rng.standard_normal(k).astype(np.float32))
+    seen = []
+    ctx.OnWeightEvicted = seen.append
+    s0 = ctx.status()
+    ctx.Linear(y, a, ws[0], None, None, m, k, n)  # the Q8_0 copy and its fp16 copy
+    first = ctx.Download(y).copy()
+    ctx.Linear(y1, x1, ws[0], None, None, 1, k, n)  # one row: the Q8_0 copy only, now the newer entry
+    ctx.Download(y1)
+    ctx.Linear(y, a, ws[1], None, None, m, k, n)  # room for its fp16 copy: the first fp16 copy goes
+    ctx.Download(y)
+    assert ctx.status().weight_evictions - s0.weight_evictions == 1
+    assert seen == []
+    assert ctx.IsWeightResident(ws[0], n, k)
+    ctx.Linear(y, a, ws[0], None, None, m, k, n)  # makes the fp16 copy again
+    assert np.array_equal(ctx.Download(y).view(np.uint32), first.view(np.uint32))
+    assert ctx.status().gemm_h16 - s0.gemm_h16 == 3
+    ctx.OnWeightEvicted = None
+    for t in (a, y, y1, x1):
+        ctx.Recycle(t)
+    ctx.Flush()
+
+
 def test_lru_eviction_and_reupload(small, rng):
     ctx = small
     ws = mats(rng, 4)
