@@ -171,7 +171,7 @@ int qnn_last_error(char *buf, int len);
 int qnn_ctx_create(int device, uint64_t weight_cache_bytes, qnn_ctx **out);
 int qnn_ctx_destroy(qnn_ctx *ctx);
 int qnn_get_status(qnn_ctx *ctx, qnn_status *out);
-/* Re-reads the QNN_* tuning switches (INTEGRATION.md lists them) from the
+/* Re-reads the QNN_* tuning switches (experiment settings) from the
  * environment.  They are read once when a context is created, not per call;
  * this picks up a change made afterwards (tests and sweeps).  No reference
  * counterpart. */

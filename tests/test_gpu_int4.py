@@ -3,7 +3,7 @@
 Dequantised weights must match bit for bit; matvec / SwiGLU / accumulate
 outputs must match the reference CPU path (TCPUProjection.Linear,
 src/backends/cpu/QuickNN.CPU.Inference.pas:316-428) within a normwise relative
-error of 1e-3 (max|y-r| / max|r|), as BASELINE.json states; the kernels
+error of 1e-3 (max|y-r| / max|r|), the benchmark definition's bar; the kernels
 accumulate in fp32 in a different order, so they are not bit-identical.
 """
 import threading
