@@ -388,7 +388,11 @@ struct H16Args {
 };
 
 // One 1 KiB piece from global memory into LDS at `lds` (wave-uniform).  The
-// compiler does not see these writes to LDS: h16_vmwait orders them.
+// compiler does not see these writes to LDS: h16_vmwait orders them.  (Its
+// own LDS-DMA builtin would make it wait for every outstanding load before
+// any LDS read, draining the prefetch each K-tile.)  M0 is set here before
+// each load; nothing else in this kernel uses M0 (gfx950's LDS instructions
+// do not read it), which the kernel's assembly shows.
 __device__ __forceinline__ void h16_dma(Rsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r),
                "s"(soff)
