@@ -60,15 +60,24 @@ __device__ __forceinline__ int range_exp(float amax) {
 }
 
 // ---- activation preparation ------------------------------------------------
-// One workgroup per row: ea[m] from max |A[m][.]| (float4 loads, LDS reduction).
-__global__ __launch_bounds__(256) void k_act_rowexp(const float *__restrict__ a, int M, int K, int m_pad,
-                                                    int *__restrict__ ea) {
+// One launch, one workgroup per row of A (m_pad of them): the row's exponent
+// ea[m] from max |A[m][.]| (range_exp), then its fp16 values A·2^-ea (exact
+// scaling, one RNE rounding) written as the fragments of
+// v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane) = 8 halfs
+// A[m32*32 + lane%32][ks*16 + 8*(lane/32) + 0..7], so thread t's group of 8
+// columns g goes to piece (m / 32, g / 2) at lane m % 32 + 32 (g % 2).  The
+// second pass re-reads the row (12 KiB at K = 3072) from the cache.  Rows
+// past M and columns past K give exponent 0 and zero pieces.
+__global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ a, int M, int K, int ksteps,
+                                                  int *__restrict__ ea, uint4 *__restrict__ frag) {
   __shared__ float red[4];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const bool in = row < M;
+  const float *r = a + size_t(in ? row : 0) * K;
+  const bool vec = (K & 3) == 0;
   float amax = 0.0f;
-  if (row < M) {
-    const float *r = a + size_t(row) * K;
-    if ((K & 3) == 0) {
+  if (in) {
+    if (vec) {
       const float4 *r4 = reinterpret_cast<const float4 *>(r);
       for (int k = tid; k < K / 4; k += 256) {
         const float4 v = r4[k];
@@ -81,37 +90,30 @@ __global__ __launch_bounds__(256) void k_act_rowexp(const float *__restrict__ a,
   for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
   if (lane == 0) red[tid >> 6] = amax;
   __syncthreads();
-  if (tid == 0) ea[row] = range_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-}
-
-// Fragment order for v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane)
-// = 8 halfs A[m32*32 + lane%32][ks*16 + 8*(lane/32) + 0..7].
-__global__ __launch_bounds__(256) void k_act_frag(const float *__restrict__ a, const int *__restrict__ ea, int M,
-                                                  int K, int ksteps, size_t pieces, uint4 *__restrict__ out) {
-  const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= pieces) return;
-  const int lane = int(idx & 63);
-  const size_t mk = idx >> 6;
-  const int ks = int(mk % ksteps), m32 = int(mk / ksteps);
-  const int row = m32 * 32 + (lane & 31), k0 = ks * 16 + 8 * (lane >> 5);
-  float v[8];
+  const int e = range_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  if (tid == 0) ea[row] = e;
+  const float sc = ldexpf(1.0f, -e);
+  uint4 *dst = frag + size_t(row >> 5) * ksteps * 64 + (row & 31);
+  for (int g = tid; g < 2 * ksteps; g += 256) {
+    const int k0 = 8 * g;
+    float v[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-  if (row < M) {
-    const float *r = a + size_t(row) * K;
-    const float s = ldexpf(1.0f, -ea[row]);
-    if (k0 + 8 <= K && (K & 3) == 0) {
-      const float4 x0 = *reinterpret_cast<const float4 *>(r + k0), x1 = *reinterpret_cast<const float4 *>(r + k0 + 4);
-      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-    } else {
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    if (in) {
+      if (vec && k0 + 8 <= K) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(r + k0), x1 = *reinterpret_cast<const float4 *>(r + k0 + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+      } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (k0 + i < K) v[i] = r[k0 + i];
+        for (int i = 0; i < 8; ++i)
+          if (k0 + i < K) v[i] = r[k0 + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] *= sc;  // exact: power of two
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] *= s;  // exact: power of two
+    dst[size_t(g >> 1) * 64 + 32 * (g & 1)] =
+        make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7]));
   }
-  out[idx] = make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7]));
 }
 
 // ---- weight row exponents (at upload) --------------------------------------
@@ -551,10 +553,7 @@ Q8GemmPlan q8_h16_plan(int M, int K, int N) {
 
 void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
                         const void *w16, void *frag, int *ea, float *c, hipStream_t s) {
-  hipLaunchKernelGGL(k_act_rowexp, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.m_pad, ea);
-  const size_t pieces = size_t(p.m_pad / 32) * p.ksteps * 64;
-  hipLaunchKernelGGL(k_act_frag, dim3((pieces + 255) / 256), dim3(256), 0, s, a, ea, M, K, p.ksteps, pieces,
-                     static_cast<uint4 *>(frag));
+  hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
   H16Args g;
   g.afrag = static_cast<const uint4 *>(frag);
   g.ea = ea;
@@ -605,10 +604,7 @@ Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
 
 void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
                     void *frag, int *ea, float *c, hipStream_t s) {
-  hipLaunchKernelGGL(k_act_rowexp, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.m_pad, ea);
-  const size_t pieces = size_t(p.m_pad / 32) * p.ksteps * 64;
-  hipLaunchKernelGGL(k_act_frag, dim3((pieces + 255) / 256), dim3(256), 0, s, a, ea, M, K, p.ksteps, pieces,
-                     static_cast<uint4 *>(frag));
+  hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
   GemmArgs g;
   g.afrag = static_cast<const uint4 *>(frag);
   g.ea = ea;
