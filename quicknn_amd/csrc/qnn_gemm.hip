@@ -310,17 +310,31 @@ __global__ __launch_bounds__(NW * 64) void k_q8_gemm(const GemmArgs g) {
   }
 
   // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32x32 tile.
+  // The row and column exponents are loaded before any store of C: as far as
+  // the compiler knows C may alias them, so a load after a store waits for it.
+  int ear[MB][16], ewr[3];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = mtile * BM + wave * 32 * MB + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      ear[mb][i] = row < g.M ? g.ea[row] : 0;
+    }
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) {
+    const int col = ntile * BN + nb * 32 + (lane & 31);
+    ewr[nb] = col < g.N ? reinterpret_cast<const int *>(g.w + g.l.rowexp_off)[col] : 0;
+  }
 #pragma unroll
   for (int nb = 0; nb < 3; ++nb) {
     const int col = ntile * BN + nb * 32 + (lane & 31);
     if (col >= g.N) continue;
-    const int ew = reinterpret_cast<const int *>(g.w + g.l.rowexp_off)[col];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = mtile * BM + wave * 32 * MB + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], g.ea[row] + ew);
+        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]);
       }
     }
   }
@@ -508,17 +522,31 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   }
 
   // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32 x 32 tile.
+  // The row and column exponents are loaded before any store of C: as far as
+  // the compiler knows C may alias them, so a load after a store waits for it.
+  int ear[2][16], ewr[3];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = mtile * HBM + (wm * 2 + mb) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      ear[mb][i] = row < g.M ? g.ea[row] : 0;
+    }
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) {
+    const int col = ntile * HBN + (wn * 3 + nb) * 32 + (lane & 31);
+    ewr[nb] = col < g.N ? g.ew[col] : 0;
+  }
 #pragma unroll
   for (int nb = 0; nb < 3; ++nb) {
     const int col = ntile * HBN + (wn * 3 + nb) * 32 + (lane & 31);
     if (col >= g.N) continue;
-    const int ew = g.ew[col];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = mtile * HBM + (wm * 2 + mb) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], g.ea[row] + ew);
+        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]);
       }
     }
   }
