@@ -312,6 +312,8 @@ __global__ __launch_bounds__(NW * 64) void k_q8_gemm(const GemmArgs g) {
   // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32x32 tile.
   // The row and column exponents are loaded before any store of C: as far as
   // the compiler knows C may alias them, so a load after a store waits for it.
+  // C is written with streaming stores: every workgroup writes its tile at the
+  // same moment, and keeping the lines out of the L2 shortens that burst.
   int ear[MB][16], ewr[3];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
@@ -334,7 +336,8 @@ __global__ __launch_bounds__(NW * 64) void k_q8_gemm(const GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = mtile * BM + wave * 32 * MB + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]);
+        if (row < g.M)
+          __builtin_nontemporal_store(ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]), &g.c[size_t(row) * g.N + col]);
       }
     }
   }
@@ -524,6 +527,8 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32 x 32 tile.
   // The row and column exponents are loaded before any store of C: as far as
   // the compiler knows C may alias them, so a load after a store waits for it.
+  // C is written with streaming stores: every workgroup writes its tile at the
+  // same moment, and keeping the lines out of the L2 shortens that burst.
   int ear[2][16], ewr[3];
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
@@ -546,7 +551,8 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = mtile * HBM + (wm * 2 + mb) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < g.M) g.c[size_t(row) * g.N + col] = ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]);
+        if (row < g.M)
+          __builtin_nontemporal_store(ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]), &g.c[size_t(row) * g.N + col]);
       }
     }
   }

@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm_i8(const I8GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int row = m32 * 32 + 8 * (i >> 2) + 4 * hi + (i & 3);
-      if (row < g.M) g.c[size_t(row) * g.N + col] = acc[j][i];
+      if (row < g.M) __builtin_nontemporal_store(acc[j][i], &g.c[size_t(row) * g.N + col]);  // streaming: see qnn_gemm.hip
     }
   }
 }
