@@ -796,11 +796,13 @@ void gguf_gather_launch(const GGLayout &l, const void *w, const float *ids, floa
 }
 
 void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {
-  const int tiles8 = (tiles + 7) / 8 * 8;
+  (void)tiles;
   const int forced = tuning().gg_bw;
+  // One unit per wave at every shape: the Gemma-2 Q6_K head (256000 x 3584,
+  // 64k waves) measured 134.4 us against 145.2 us at two units per wave, its
+  // down projection 13.1 against 13.8 us.  QNN_GG_BW=2 selects two.
   int pick = 1;
   if (forced == 1 || forced == 2) pick = forced;
-  else if (size_t(tiles8) * ((l.units + 7) / 8) * 4 >= 16384) pick = 2;  // BW=1 measured faster up to 7k waves
   *bw = pick;
   *slices = (l.units + 4 * pick - 1) / (4 * pick);
 }

@@ -111,9 +111,9 @@ def test_linear_rows_and_bias(ctx, rng, enc):
         assert normwise_rel_err(got[r], want) <= TOL, r
 
 
-# Two 256-element units per wave (k_gguf_matvec<ENC, 2>): the planner picks it
-# for large launches (the Q6_K output head below); QNN_GG_BW=2 forces it at
-# small ragged shapes, including launches with fewer units than waves.
+# Two 256-element units per wave (k_gguf_matvec<ENC, 2>), which the planner no
+# longer picks by itself: QNN_GG_BW=2 forces it at small ragged shapes,
+# including launches with fewer units than waves (and at the Q6_K head below).
 @pytest.mark.parametrize("enc", FMTS, ids=NAMES.get)
 @pytest.mark.parametrize("n,k", [(1, 256), (37, 768), (64, 2048), (130, 2304), (300, 512), (65, 3584)])
 def test_linear_two_units_per_wave_forced(ctx, rng, tune, enc, n, k):
@@ -144,13 +144,14 @@ def test_swiglu_two_units_per_wave_forced(ctx, rng, tune, eg, eu, n, k):
 
 
 def test_q6k_output_head_256000x3584(ctx, rng, tune):
-    """configs[2]'s Q6_K output head at full size.  The planner runs it at two
-    units per wave (4000 tiles x 14 units: 32000 >= 16384 in gguf_plan); the
-    result equals a forced QNN_GG_BW=2 launch bit for bit (BW=1 splits K into 4
-    slices, BW=2 into 2, so the sums would differ in their last bits).  Rows
-    are encoded from a prime period of 4099 rows (so no tile or unit index
-    lines up with the repetition); a spread of 640 rows, the first and last 64
-    included, is checked against the CPU path on those rows."""
+    """configs[2]'s Q6_K output head at full size.  The planner runs it at one
+    unit per wave (4000 tiles x 4 K-slices of 4, 4, 4 and 2 units); the result
+    equals a forced QNN_GG_BW=1 launch bit for bit, and a forced QNN_GG_BW=2
+    launch (2 slices of 8 and 6 units: other sums, other last bits) is within
+    the bar too.  Rows are encoded from a prime period of 4099 rows (so no
+    tile or unit index lines up with the repetition); a spread of 640 rows,
+    the first and last 64 included, is checked against the CPU path on those
+    rows."""
     enc, n, k, period = ENC_Q6_K, 256000, 3584, 4099
     base = quantized(rng, enc, period, k).reshape(period, -1)
     data = np.tile(base, (n // period + 1, 1))[:n]
@@ -159,13 +160,17 @@ def test_q6k_output_head_256000x3584(ctx, rng, tune):
     src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
     ctx.Linear(dst, src, w, None, None, 1, k, n)
     auto = ctx.Download(dst)
-    tune("QNN_GG_BW", "2")
+    tune("QNN_GG_BW", "1")
     ctx.Linear(dst, src, w, None, None, 1, k, n)
     forced = ctx.Download(dst)
     assert np.array_equal(auto.view(np.uint32), forced.view(np.uint32))
+    tune("QNN_GG_BW", "2")
+    ctx.Linear(dst, src, w, None, None, 1, k, n)
+    two = ctx.Download(dst)
     rows = np.unique(np.concatenate([np.arange(64), rng.choice(n, 512, replace=False), np.arange(n - 64, n)]))
     want = oracle.cpu_linear(np.ascontiguousarray(base[rows % period]), enc, x, k, len(rows))
     assert normwise_rel_err(auto[rows], want) <= TOL
+    assert normwise_rel_err(two[rows], want) <= TOL
     ctx.Recycle(src)
     ctx.Recycle(dst)
 
