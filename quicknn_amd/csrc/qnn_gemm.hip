@@ -60,18 +60,22 @@ __device__ __forceinline__ int range_exp(float amax) {
 }
 
 // ---- activation preparation ------------------------------------------------
-// One launch, one workgroup per row of A (m_pad of them): the row's exponent
-// ea[m] from max |A[m][.]| (range_exp), then its fp16 values A·2^-ea (exact
-// scaling, one RNE rounding) written as the fragments of
-// v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane) = 8 halfs
-// A[m32*32 + lane%32][ks*16 + 8*(lane/32) + 0..7], so thread t's group of 8
-// columns g goes to piece (m / 32, g / 2) at lane m % 32 + 32 (g % 2).  The
-// second pass re-reads the row (12 KiB at K = 3072) from the cache.  Rows
-// past M and columns past K give exponent 0 and zero pieces.
-__global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ a, int M, int K, int ksteps,
-                                                  int *__restrict__ ea, uint4 *__restrict__ frag) {
-  __shared__ float red[4];
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+// One launch: workgroup b owns rows 4b .. 4b + 3 of A (m_pad rows in all),
+// four waves per row.  A row's waves read it, take ea[m] from max |A[m][.]|
+// (range_exp; the four waves meet in LDS), then re-read it from the cache and
+// write its fp16 values A·2^-ea (exact scaling, one RNE rounding) as the
+// fragments of v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane) = 8
+// halfs A[m32*32 + lane%32][ks*16 + 8*(lane/32) + 0..7], so the row's group
+// of 8 columns g goes to piece (m / 32, g / 2) at lane m % 32 + 32 (g % 2).
+// The four rows of a workgroup fill the same 64-byte segments together (one
+// row per workgroup wrote every segment in four visits: twice the bytes).
+// Rows past M and columns past K give exponent 0 and zero pieces.
+__global__ __launch_bounds__(1024) void k_act_prep(const float *__restrict__ a, int M, int K, int ksteps,
+                                                   int *__restrict__ ea, uint4 *__restrict__ frag) {
+  __shared__ float red[4][4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rw = wave >> 2, part = wave & 3;
+  const int t = part * 64 + lane;  // thread of the row, 0 .. 255
+  const int row = blockIdx.x * 4 + rw;
   const bool in = row < M;
   const float *r = a + size_t(in ? row : 0) * K;
   const bool vec = (K & 3) == 0;
@@ -79,22 +83,22 @@ __global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ a, i
   if (in) {
     if (vec) {
       const float4 *r4 = reinterpret_cast<const float4 *>(r);
-      for (int k = tid; k < K / 4; k += 256) {
+      for (int k = t; k < K / 4; k += 256) {
         const float4 v = r4[k];
         amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
       }
     } else {
-      for (int k = tid; k < K; k += 256) amax = fmaxf(amax, fabsf(r[k]));
+      for (int k = t; k < K; k += 256) amax = fmaxf(amax, fabsf(r[k]));
     }
   }
   for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if (lane == 0) red[tid >> 6] = amax;
+  if (lane == 0) red[rw][part] = amax;
   __syncthreads();
-  const int e = range_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-  if (tid == 0) ea[row] = e;
+  const int e = range_exp(fmaxf(fmaxf(red[rw][0], red[rw][1]), fmaxf(red[rw][2], red[rw][3])));
+  if (t == 0) ea[row] = e;
   const float sc = ldexpf(1.0f, -e);
   uint4 *dst = frag + size_t(row >> 5) * ksteps * 64 + (row & 31);
-  for (int g = tid; g < 2 * ksteps; g += 256) {
+  for (int g = t; g < 2 * ksteps; g += 256) {
     const int k0 = 8 * g;
     float v[8];
 #pragma unroll
@@ -587,7 +591,7 @@ Q8GemmPlan q8_h16_plan(int M, int K, int N) {
 
 void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
                         const void *w16, void *frag, int *ea, float *c, hipStream_t s) {
-  hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
+  hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad / 4), dim3(1024), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
   H16Args g;
   g.afrag = static_cast<const uint4 *>(frag);
   g.ea = ea;
@@ -638,7 +642,7 @@ Q8GemmPlan q8_gemm_plan(int M, int K, int N) {
 
 void q8_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
                     void *frag, int *ea, float *c, hipStream_t s) {
-  hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad), dim3(256), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
+  hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad / 4), dim3(1024), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
   GemmArgs g;
   g.afrag = static_cast<const uint4 *>(frag);
   g.ea = ea;
