@@ -74,7 +74,7 @@ extern "C" {
 #define QNN_WE_Q2_K 9
 #define QNN_WE_IQ2_XXS 10  /* read from GGUF tables; no kernel here */
 #define QNN_WE_IQ2_S 11    /* read from GGUF tables; no kernel here */
-#define QNN_WE_Q2_0 12     /* read from GGUF tables; no kernel here */
+#define QNN_WE_Q2_0 12
 #define QNN_WE_IQ3_XXS 13  /* read from GGUF tables; no kernel here */
 
 /* ---- TSafeTensorType ordinals (src/io/QuickNN.SafeTensors.pas:34-77) ---- */

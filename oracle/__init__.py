@@ -25,11 +25,12 @@ ENC_Q6_K = 3
 ENC_Q3_K = 4
 ENC_Q2_K = 9
 ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS = 5, 6, 8
-GGUF_ENCODINGS = (ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS)
+ENC_Q2_0 = 12
+GGUF_ENCODINGS = (ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0)
 BLOCK_ELEMENTS = {ENC_Q8_0: 32, ENC_Q4_K: 256, ENC_Q6_K: 256, ENC_Q3_K: 256, ENC_Q2_K: 256, ENC_Q5_K: 256,
-                  ENC_IQ4_NL: 32, ENC_IQ4_XS: 256}
+                  ENC_IQ4_NL: 32, ENC_IQ4_XS: 256, ENC_Q2_0: 64}
 BLOCK_BYTES = {ENC_Q8_0: 34, ENC_Q4_K: 144, ENC_Q6_K: 210, ENC_Q3_K: 110, ENC_Q2_K: 84, ENC_Q5_K: 176,
-               ENC_IQ4_NL: 18, ENC_IQ4_XS: 136}
+               ENC_IQ4_NL: 18, ENC_IQ4_XS: 136, ENC_Q2_0: 18}
 
 _lib = None
 

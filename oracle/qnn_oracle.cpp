@@ -246,6 +246,7 @@ void qo_int4_dequant_row(const uint8_t *row, int cols, float *out) {
 int qo_gguf_block_elements(int enc) {  // :67-75
   switch (enc) {
     case QO_ENC_Q8_0: case QO_ENC_IQ4_NL: return 32;
+    case QO_ENC_Q2_0: return 64;
     case QO_ENC_Q4_K: case QO_ENC_Q6_K: case QO_ENC_Q3_K: case QO_ENC_Q2_K: case QO_ENC_Q5_K: case QO_ENC_IQ4_XS:
       return 256;
     default: return -1;
@@ -261,6 +262,7 @@ int qo_gguf_block_bytes(int enc) {  // :77-93
     case QO_ENC_Q5_K: return 176;
     case QO_ENC_IQ4_NL: return 18;
     case QO_ENC_IQ4_XS: return 136;
+    case QO_ENC_Q2_0: return 18;
     default: return -1;
   }
 }
@@ -296,6 +298,8 @@ float qo_gguf_value(const uint8_t *data, int enc, int64_t index) {
       if (enc == QO_ENC_Q5_K) q |= ((b[16 + i % 32] >> group) & 1) << 4;
       return (half_at(b) * float(scale)) * float(q) - half_at(b + 2) * float(minimum);
     }
+    case QO_ENC_Q2_0:  // :146-147: fp16 d, then 2-bit q four to a byte; d * (q - 1)
+      return half_at(b) * float(int((b[2 + i / 4] >> ((i % 4) * 2)) & 3) - 1);
     case QO_ENC_IQ4_NL: {  // :229-233
       int q = (b[2 + i % 16] >> ((i / 16) * 4)) & 15;
       return half_at(b) * float(kIQ4[q]);
@@ -339,6 +343,9 @@ static void decode_iq4(const uint8_t *src, float *dst, float scale) {
 
 int qo_gguf_decode_block(const uint8_t *b, int enc, float *out) {
   switch (enc) {
+    case QO_ENC_Q2_0:  // :285-289: element by element through GGUFValue
+      for (int i = 0; i < 64; ++i) out[i] = qo_gguf_value(b, enc, i);
+      return 0;
     case QO_ENC_Q5_K: {  // :296-312 with DecodeBits (:30-66): q = low4 | high1 << 4, cvt(q) * Scale + Bias
       float d = half_at(b), dm = half_at(b + 2);
       for (int g = 0; g < 8; ++g) {
@@ -457,6 +464,13 @@ static float packed_half(const uint8_t *data, uint64_t off) { return half_at(dat
 
 int qo_gguf_read4(const uint8_t *data, int enc, int64_t index, float *o) {
   if (index % 4) return -1;
+  if (enc == QO_ENC_Q2_0) {  // :592 (encodings >= 10: four readGGUF), :486-489
+    for (int t = 0; t < 4; ++t) {
+      uint64_t i = uint64_t(index) + t, base = (i / 64u) * 18u, e = i % 64u;
+      o[t] = packed_half(data, base) * float(int((packed_byte(data, base + 2u + e / 4u) >> ((e % 4u) * 2u)) & 3u) - 1);
+    }
+    return 0;
+  }
   uint64_t idx = uint64_t(index);
   uint32_t item = idx & 255u, lane = item & 31u, group = item >> 5u;
   if (enc == QO_ENC_Q2_K) {

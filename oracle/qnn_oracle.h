@@ -11,7 +11,8 @@
  * invariants, brute force) lives in tests/test_oracle_*.py.
  *
  * Encodings follow TQNNWeightEncoding (src/core/QuickNN.Common.pas:130-131):
- *   0 native, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q3_K, 5 Q5_K, 6 IQ4_NL, 8 IQ4_XS, 9 Q2_K.
+ *   0 native, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q3_K, 5 Q5_K, 6 IQ4_NL, 8 IQ4_XS, 9 Q2_K,
+ *   12 Q2_0.
  * The oracle uses QO_ENC_INT4 (-1) for QuickNN's native packed INT4 rows.
  */
 #ifndef QNN_ORACLE_H
@@ -30,6 +31,7 @@ extern "C" {
 #define QO_ENC_IQ4_NL 6
 #define QO_ENC_IQ4_XS 8
 #define QO_ENC_Q2_K 9
+#define QO_ENC_Q2_0 12
 
 /* Status codes: 0 ok, -1 argument error (EArgumentException). */
 

@@ -311,6 +311,7 @@ void *ensure_staging(qnn_ctx_s *ctx, size_t bytes) {
 int gguf_block_elements(int enc) {  // GGUF.Quantization.pas:67-75 (formats in this backend)
   switch (enc) {
     case QNN_WE_Q8_0: case QNN_WE_IQ4_NL: return 32;
+    case QNN_WE_Q2_0: return 64;
     case QNN_WE_Q4_K: case QNN_WE_Q6_K: case QNN_WE_Q3_K: case QNN_WE_Q2_K: case QNN_WE_Q5_K: case QNN_WE_IQ4_XS:
       return 256;
   }
@@ -326,6 +327,7 @@ int gguf_block_bytes(int enc) {  // GGUF.Quantization.pas:77-93
     case QNN_WE_Q5_K: return 176;
     case QNN_WE_IQ4_NL: return 18;
     case QNN_WE_IQ4_XS: return 136;
+    case QNN_WE_Q2_0: return 18;
   }
   return -1;
 }

@@ -1,5 +1,5 @@
 // qnn_gguf.hip -- GGML block formats (Q8_0, Q4_K, Q5_K, Q6_K, Q3_K, Q2_K,
-// IQ4_NL, IQ4_XS) for gfx950.
+// IQ4_NL, IQ4_XS, Q2_0) for gfx950.
 //
 // Formats and decode rules: src/io/QuickNN.GGUF.Quantization.pas:136-253
 // (GGUFValue); the matvec replaces op 65 (ggufvector.comp:34-52) and the GGUF
@@ -19,6 +19,7 @@
 //   Q5_K  (176 B): main 176 (C=11)
 //   IQ4_XS (136 B): main quants 128 (C=8), side1 d|scales_h|scales_l (8)
 //   IQ4_NL (8x18 B): main 8x16 quants (C=8), side1 8 fp16 d (16)
+//   Q2_0  (4x18 B): main 4x16 quants (C=4), side1 4 fp16 d (8)
 // so every wave load is a 16-byte (or 12/8/4/2-byte) load by 64 consecutive
 // lanes.  Bytes per weight are unchanged.
 //
@@ -34,8 +35,13 @@
 //   Q5_K: as Q4_K with 5-bit q (the fifth bit from qh)
 //   IQ4_NL: sum = s2 * d * dot(v, X)                      (v = codebook byte)
 //   IQ4_XS: sum = s2 * d*(ls-32) * dot(v, X)              (sub-block 32)
+//   Q2_0:   sum = s2 * d * (dot(q, X) - sum(X))           (value d*(q-1))
 // where X = 256 q1 + q2 and every dot is exact integer arithmetic; the IQ4
-// nibbles become their signed codebook bytes by a byte-permute lookup.
+// nibbles become their signed codebook bytes by a byte-permute lookup.  A
+// Q2_0 byte holds four consecutive elements, so its activation slice is
+// staged with each 16-element run transposed as a 4x4 byte matrix: word t
+// then holds elements t, t+4, t+8, t+12, which is what one shift and mask of
+// a quant word yields.
 #include "qnn_int4_dev.h"  // buffer-load helpers (rsrc, ld128, ld32f) and the exchange
 
 namespace qnn {
@@ -89,6 +95,7 @@ template <> struct Fmt<QNN_WE_Q8_0> { static constexpr int C = 16, S1 = 16, S2 =
 template <> struct Fmt<QNN_WE_Q5_K> { static constexpr int C = 11, S1 = 0, S2 = 0; };
 template <> struct Fmt<QNN_WE_IQ4_XS> { static constexpr int C = 8, S1 = 8, S2 = 0; };
 template <> struct Fmt<QNN_WE_IQ4_NL> { static constexpr int C = 8, S1 = 16, S2 = 0; };
+template <> struct Fmt<QNN_WE_Q2_0> { static constexpr int C = 4, S1 = 8, S2 = 0; };
 
 // IQ4_NL_VALUES (src/io/QuickNN.GGUF.Quantization.pas:34) as signed bytes,
 // four per word: the codebook of IQ4_NL and IQ4_XS.
@@ -112,6 +119,15 @@ __device__ __forceinline__ uint32_t iq4_bytes(uint32_t nib) {
   const uint32_t hi = __builtin_amdgcn_perm(kIQ4W3, kIQ4W2, sel);
   const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
   return (hi & m) | (lo & ~m);
+}
+
+// Lane t (0-3) of each quad of lanes receives byte t of the quad's four
+// words, the word of lane s in byte s: a 4x4 byte transpose.
+__device__ __forceinline__ uint32_t quad_transpose(uint32_t v, int t) {
+  const uint32_t v0 = dev::dpp<0x00>(v), v1 = dev::dpp<0x55>(v), v2 = dev::dpp<0xAA>(v), v3 = dev::dpp<0xFF>(v);
+  const uint32_t lo = __builtin_amdgcn_perm(v1, v0, uint32_t(t) | (uint32_t(t + 4) << 8) | 0x0C0C0000u);
+  const uint32_t hi = __builtin_amdgcn_perm(v3, v2, 0x0C0Cu | (uint32_t(t) << 16) | (uint32_t(t + 4) << 24));
+  return lo | hi;
 }
 
 struct Planes {
@@ -144,7 +160,8 @@ __device__ __forceinline__ void plane_addr(int enc, const GGLayout &l, int t, in
     case QNN_WE_Q2_K: if (o < 80) main_at(o); else s1_at(o - 80); break;
     case QNN_WE_Q5_K: main_at(o); break;
     case QNN_WE_IQ4_XS: if (o < 8) s1_at(o); else main_at(o - 8); break;
-    case QNN_WE_IQ4_NL: {  // unit of 8 blocks: block k = o / 18, byte j = o % 18: d at j < 2, quants after
+    case QNN_WE_IQ4_NL:
+    case QNN_WE_Q2_0: {  // unit of 8 (4) blocks: block k = o / 18, byte j = o % 18: d at j < 2, quants after
       const int k = o / 18, j = o % 18;
       if (j < 2) s1_at(2 * k + j); else main_at(16 * k + j - 2);
       break;
@@ -199,6 +216,11 @@ __device__ float gguf_value_tiled(int enc, const GGLayout &l, const Planes &p, i
       const int q = int((B(18 * k + 2 + j % 16) >> ((j / 16) * 4)) & 15);
       return H(18 * k) * float(iq4_value(q));
     }
+    case QNN_WE_Q2_0: {  // GGUF.Quantization.pas:146-147
+      const int k = i / 64, j = i % 64;
+      const int q = int((B(18 * k + 2 + j / 4) >> ((j % 4) * 2)) & 3);
+      return H(18 * k) * float(q - 1);
+    }
     case QNN_WE_IQ4_XS: {
       const int group = i / 32;
       const int scale = int(((B(4 + group / 2) >> ((group % 2) * 4)) & 15) |
@@ -238,7 +260,7 @@ __global__ void k_gguf_repack(const uint8_t *__restrict__ src, GGLayout l, uint8
   for (int o = 0; o < ub; ++o) {
     uint8_t v = 0;
     if (row < l.rows) {
-      const size_t so = size_t(u) * ub + o;  // Q8_0 / IQ4_NL units past the row end are zero blocks (d = 0)
+      const size_t so = size_t(u) * ub + o;  // Q8_0 / IQ4_NL / Q2_0 units past the row end are zero blocks (d = 0)
       if (so < row_bytes) v = src[size_t(row) * row_bytes + so];
     }
     int plane;
@@ -509,6 +531,33 @@ __device__ float unit_iq4_nl(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, in
   return acc;
 }
 
+// Q2_0: block k (64 elements, groups g0 + 2k and g0 + 2k + 1) in chunk k, its
+// d in side half k.  Quant word w of the chunk holds elements 16w..16w+15,
+// four per byte; shift 2t and mask give elements 16w + t + {0, 4, 8, 12},
+// the order of the transposed activation word 4(w & 1) + t.
+template <int NG>
+__device__ float unit_q2_0(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int g0) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t dw = sel4u(s1, k >> 1);
+    const float d = half_f((k & 1) ? (dw >> 16) : (dw & 0xFFFFu));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int g = g0 + 2 * k + h;
+      int ah = 0, al = 0;
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const uint32_t qw = sel4u(mw[k], 2 * h + w);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) xdot((qw >> (2 * t)) & 0x03030303u, xs.h[g][4 * w + t], xs.l[g][4 * w + t], ah, al);
+      }
+      acc = fmaf(float(combine<NG>(ah, al) - xs.sum32[g]), d * xs.s2[g], acc);
+    }
+  }
+  return acc;
+}
+
 template <int NG>
 __device__ float unit_iq4_xs(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int g0) {
   // side: bytes 0-1 d, 2-3 scales_h, 4-7 scales_l
@@ -620,8 +669,12 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
     dev::quant_elem(v.y, gs, b1[1], b2[1]);
     dev::quant_elem(v.z, gs, b1[2], b2[2]);
     dev::quant_elem(v.w, gs, b1[3], b2[3]);
-    const uint32_t hw = dev::join2(dev::pack2(b1[0], b1[1]), dev::pack2(b1[2], b1[3]));
-    const uint32_t lw = dev::join2(dev::pack2(b2[0], b2[1]), dev::pack2(b2[2], b2[3]));
+    uint32_t hw = dev::join2(dev::pack2(b1[0], b1[1]), dev::pack2(b1[2], b1[3]));
+    uint32_t lw = dev::join2(dev::pack2(b2[0], b2[1]), dev::pack2(b2[2], b2[3]));
+    if constexpr (ENC == QNN_WE_Q2_0) {  // 4x4 byte transpose over the quad of lanes holding a 16-element run
+      hw = quad_transpose(hw, lane & 3);
+      lw = quad_transpose(lw, lane & 3);
+    }
     const int s16 = dev::sum_lanes4(dev::quant_sum<4>(b1, b2));  // 16-element sum
     const int s32 = s16 + int(dev::dpp<0x141>(uint32_t(s16)));
     if (e < U * 256) {
@@ -651,6 +704,7 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
       if (ENC == QNN_WE_Q5_K) acc += unit_q5_k<NG>(mw[b], xs, g0);
       if (ENC == QNN_WE_IQ4_NL) acc += unit_iq4_nl<NG>(mw[b], s1v[b], xs, g0);
       if (ENC == QNN_WE_IQ4_XS) acc += unit_iq4_xs<NG>(mw[b], s1v[b], xs, g0);
+      if (ENC == QNN_WE_Q2_0) acc += unit_q2_0<NG>(mw[b], s1v[b], xs, g0);
     }
   }
 
@@ -757,10 +811,12 @@ GGLayout gguf_layout(int enc, int rows, int cols) {
     case QNN_WE_Q5_K: l.main_chunks = 11; l.side1_bytes = 0; l.side2_bytes = 0; l.unit_bytes = 176; break;
     case QNN_WE_IQ4_XS: l.main_chunks = 8; l.side1_bytes = 8; l.side2_bytes = 0; l.unit_bytes = 136; break;
     case QNN_WE_IQ4_NL: l.main_chunks = 8; l.side1_bytes = 16; l.side2_bytes = 0; l.unit_bytes = 144; break;
+    case QNN_WE_Q2_0: l.main_chunks = 4; l.side1_bytes = 8; l.side2_bytes = 0; l.unit_bytes = 72; break;
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
   l.src_row_bytes = enc == QNN_WE_Q8_0     ? (cols / 32) * 34
                     : enc == QNN_WE_IQ4_NL ? (cols / 32) * 18
+                    : enc == QNN_WE_Q2_0   ? (cols / 64) * 18
                                            : (cols / 256) * l.unit_bytes;
   const size_t tu64 = size_t(l.tiles) * l.units * 64;
   auto up256 = [](size_t b) { return (b + 255) & ~size_t(255); };
@@ -833,6 +889,7 @@ void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s) {
     case QNN_WE_Q5_K: launch_enc<QNN_WE_Q5_K>(g, bw, s); break;
     case QNN_WE_IQ4_NL: launch_enc<QNN_WE_IQ4_NL>(g, bw, s); break;
     case QNN_WE_IQ4_XS: launch_enc<QNN_WE_IQ4_XS>(g, bw, s); break;
+    case QNN_WE_Q2_0: launch_enc<QNN_WE_Q2_0>(g, bw, s); break;
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
   hip_check(hipGetLastError(), "gguf matvec launch");

@@ -277,6 +277,32 @@ void enc_iq4_nl(const float *x, uint8_t *b) {
   put_iq4_32(x, from_half(uint16_t(b[0] | (b[1] << 8))), b + 2);
 }
 
+// Q2_0 (18 B per 64): fp16 d, then 2-bit q, four elements to a byte (element
+// i at bits 2(i % 4) of byte 2 + i / 4); value d * (q - 1), q - 1 in -1..2.
+// d maps the largest-magnitude element to 2 or to -1, whichever leaves the
+// smaller squared error.
+void enc_q2_0(const float *x, uint8_t *b) {
+  std::memset(b, 0, 18);
+  const float m = signed_amax(x, 64);
+  float best_d = 0.0f, best_err = -1.0f;
+  for (float cand : {m / 2.0f, -m}) {
+    const float d = from_half(to_half(cand));
+    float err = 0.0f;
+    for (int i = 0; i < 64; ++i) {
+      const int q = d != 0 ? clampi(rnd(x[i] / d), -1, 2) : 0;
+      const float e = x[i] - d * float(q);
+      err += e * e;
+    }
+    if (best_err < 0 || err < best_err) { best_err = err; best_d = cand; }
+  }
+  put_half(b, best_d);
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8)));
+  for (int i = 0; i < 64; ++i) {
+    const int q = (d != 0 ? clampi(rnd(x[i] / d), -1, 2) : 0) + 1;
+    b[2 + i / 4] |= uint8_t(q << ((i % 4) * 2));
+  }
+}
+
 // IQ4_XS (136 B per 256): fp16 d, 6-bit signed sub-block scales (low nibbles
 // at 4 + j/2, high 2 bits of scale j at bits 2j of the 16-bit word at 2),
 // then 8 x 16 bytes of codebook nibbles.
@@ -346,6 +372,7 @@ int qnn_gguf_quantize(int encoding, const float *src, int64_t n, uint8_t *dst) {
     case QNN_WE_Q5_K: elems = 256; bytes = 176; fn = enc_q5_k; break;
     case QNN_WE_IQ4_NL: elems = 32; bytes = 18; fn = enc_iq4_nl; break;
     case QNN_WE_IQ4_XS: elems = 256; bytes = 136; fn = enc_iq4_xs; break;
+    case QNN_WE_Q2_0: elems = 64; bytes = 18; fn = enc_q2_0; break;
     default: return QNN_E_NOT_SUPPORTED;
   }
   if (!src || !dst || n < 0 || n % elems) return QNN_E_ARGUMENT;

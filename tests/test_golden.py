@@ -21,8 +21,10 @@ from tests.conftest import normwise_rel_err
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 ENC = {"Q8_0": oracle.ENC_Q8_0, "Q4_K": oracle.ENC_Q4_K, "Q6_K": oracle.ENC_Q6_K, "Q3_K": oracle.ENC_Q3_K,
-       "Q2_K": oracle.ENC_Q2_K, "Q5_K": oracle.ENC_Q5_K, "IQ4_NL": oracle.ENC_IQ4_NL, "IQ4_XS": oracle.ENC_IQ4_XS}
-ELEMS = {"Q8_0": 32, "Q4_K": 256, "Q6_K": 256, "Q3_K": 256, "Q2_K": 256, "Q5_K": 256, "IQ4_NL": 32, "IQ4_XS": 256}
+       "Q2_K": oracle.ENC_Q2_K, "Q5_K": oracle.ENC_Q5_K, "IQ4_NL": oracle.ENC_IQ4_NL, "IQ4_XS": oracle.ENC_IQ4_XS,
+       "Q2_0": oracle.ENC_Q2_0}
+ELEMS = {"Q8_0": 32, "Q4_K": 256, "Q6_K": 256, "Q3_K": 256, "Q2_K": 256, "Q5_K": 256, "IQ4_NL": 32, "IQ4_XS": 256,
+         "Q2_0": 64}
 
 
 def load(name):

@@ -1,4 +1,4 @@
-"""GPU parity of the GGUF path (Q8_0, Q4_K, Q5_K, Q6_K, Q3_K, Q2_K, IQ4_NL, IQ4_XS) against the CPU oracle.
+"""GPU parity of the GGUF path (Q8_0, Q4_K, Q5_K, Q6_K, Q3_K, Q2_K, IQ4_NL, IQ4_XS, Q2_0) against the CPU oracle.
 
 Dequantised weights must equal GGUFValue (GGUF.Quantization.pas:136-253) bit
 for bit (as floats: +0 == -0, the reference's own decoders differ there);
@@ -10,17 +10,17 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import (BLOCK_BYTES, BLOCK_ELEMENTS, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K, ENC_Q6_K,
-                    ENC_Q8_0)
+from oracle import (BLOCK_BYTES, BLOCK_ELEMENTS, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K,
+                    ENC_Q6_K, ENC_Q8_0)
 from quicknn_amd import hip
 from tests.conftest import normwise_rel_err
 from tests.test_oracle_gguf import random_blocks
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
-FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS]
+FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0]
 NAMES = {ENC_Q8_0: "q8_0", ENC_Q4_K: "q4_k", ENC_Q6_K: "q6_k", ENC_Q3_K: "q3_k", ENC_Q2_K: "q2_k", ENC_Q5_K: "q5_k",
-         ENC_IQ4_NL: "iq4_nl", ENC_IQ4_XS: "iq4_xs"}
+         ENC_IQ4_NL: "iq4_nl", ENC_IQ4_XS: "iq4_xs", ENC_Q2_0: "q2_0"}
 
 
 def quantized(rng, enc, n, k, scale=0.02):
@@ -72,6 +72,7 @@ def test_dequant_offset_slice(ctx, rng):
     (ENC_Q4_K, 5, 256), (ENC_Q6_K, 70, 768), (ENC_Q3_K, 129, 1280), (ENC_Q2_K, 63, 512), (ENC_Q8_0, 33, 96),
     (ENC_Q5_K, 4096, 3584), (ENC_IQ4_XS, 4096, 4096), (ENC_IQ4_NL, 2048, 3584), (ENC_Q5_K, 5, 256),
     (ENC_IQ4_XS, 70, 768), (ENC_IQ4_NL, 33, 96), (ENC_IQ4_NL, 129, 1312),
+    (ENC_Q2_0, 4096, 3584), (ENC_Q2_0, 14336, 3584), (ENC_Q2_0, 33, 192), (ENC_Q2_0, 129, 1344), (ENC_Q2_0, 7, 64),
 ])
 def test_linear_m1(ctx, rng, enc, n, k):
     data = quantized(rng, enc, n, k)
@@ -119,6 +120,8 @@ def test_linear_rows_and_bias(ctx, rng, enc):
 def test_linear_two_units_per_wave_forced(ctx, rng, tune, enc, n, k):
     if enc in (ENC_Q8_0, ENC_IQ4_NL):
         k = k - 32 if k > 256 else 96  # rows of 32-element blocks need not fill their last 256-element unit
+    if enc == ENC_Q2_0:
+        k = k - 64 if k > 256 else 192  # likewise for 64-element blocks
     data = quantized(rng, enc, n, k)
     x = rng.standard_normal(k).astype(np.float32)
     src, dst = ctx.UploadRaw(x), ctx.NewTensor(n)
@@ -196,7 +199,8 @@ def _swiglu_want(pg, eg, pu, eu, x, k, n):
     (ENC_Q2_K, ENC_Q2_K, 14336, 3584), (ENC_Q4_K, ENC_Q4_K, 1000, 768), (ENC_Q8_0, ENC_Q8_0, 96, 64),
     (ENC_Q6_K, ENC_Q6_K, 33, 256), (ENC_Q3_K, ENC_Q3_K, 257, 512), (ENC_Q4_K, ENC_Q6_K, 500, 512),
     (ENC_Q5_K, ENC_Q5_K, 1000, 768), (ENC_IQ4_XS, ENC_IQ4_XS, 300, 512), (ENC_IQ4_NL, ENC_IQ4_NL, 96, 160),
-    (ENC_IQ4_NL, ENC_IQ4_XS, 200, 512),
+    (ENC_IQ4_NL, ENC_IQ4_XS, 200, 512), (ENC_Q2_0, ENC_Q2_0, 300, 448), (ENC_Q2_0, ENC_Q2_0, 9728, 2560),
+    (ENC_Q2_0, ENC_Q4_K, 200, 512),
 ])
 def test_swiglu_vector(ctx, rng, eg, eu, n, k):
     pg, pu = quantized(rng, eg, n, k), quantized(rng, eu, n, k)

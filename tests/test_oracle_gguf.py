@@ -10,13 +10,13 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import (ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q8_0, BLOCK_BYTES,
-                    BLOCK_ELEMENTS)
+from oracle import (ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q8_0,
+                    BLOCK_BYTES, BLOCK_ELEMENTS)
 
-FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS]
+FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0]
 # fp16 fields (byte offsets within a block)
 HALF_FIELDS = {ENC_Q8_0: [0], ENC_Q4_K: [0, 2], ENC_Q6_K: [208], ENC_Q3_K: [108], ENC_Q2_K: [80, 82],
-               ENC_Q5_K: [0, 2], ENC_IQ4_NL: [0], ENC_IQ4_XS: [0]}
+               ENC_Q5_K: [0, 2], ENC_IQ4_NL: [0], ENC_IQ4_XS: [0], ENC_Q2_0: [0]}
 # IQ4_NL_VALUES (src/io/QuickNN.GGUF.Quantization.pas:34), typed in from the format definition
 IQ4 = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
 
@@ -177,6 +177,23 @@ def test_iq4_nl_known_answer():
     assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_IQ4_NL, 64), want)
 
 
+def test_q2_0_known_answer():
+    # Two blocks, d = 0.5 and -2.0; element i: 2-bit q at bits 2(i % 4) of byte 2 + i / 4, q = (3i + 1) % 4;
+    # value d * (q - 1).  Every q occurs in every bit position of a byte.
+    b = np.zeros(18 * 2, np.uint8)
+    for blk, d in enumerate((0.5, -2.0)):
+        b[18 * blk:18 * blk + 2] = np.frombuffer(struct.pack("<H", f16(d)), np.uint8)
+    q = np.array([(3 * i + 1) % 4 for i in range(128)])
+    for i in range(128):
+        blk, j = i // 64, i % 64
+        b[18 * blk + 2 + j // 4] |= q[i] << ((j % 4) * 2)
+    want = np.array([(0.5 if i < 64 else -2.0) * (q[i] - 1) for i in range(128)], np.float32)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_Q2_0, 128), want)
+    assert np.array_equal(oracle.gguf_read4_all(b, ENC_Q2_0, 128), want)
+    # the CPU Linear decodes the row and runs VectorDot (no packed dot for Q2_0); these sums are exact
+    assert oracle.cpu_linear(b, ENC_Q2_0, np.ones(128, np.float32), 128, 1)[0] == want.sum()
+
+
 def test_iq4_xs_known_answer():
     # d = 0.25; 6-bit sub-block scales ls (value ls - 32) with every high-bit pattern; q = (7i) % 16.
     b = np.zeros(136, np.uint8)
@@ -221,5 +238,5 @@ def test_product_encoder_round_trip(rng, enc):
     assert np.all(np.isfinite(dec))
     rel = np.linalg.norm(dec - w) / np.linalg.norm(w)
     bound = {ENC_Q8_0: 0.01, ENC_Q6_K: 0.03, ENC_Q4_K: 0.12, ENC_Q3_K: 0.25, ENC_Q2_K: 0.45, ENC_Q5_K: 0.06,
-             ENC_IQ4_NL: 0.12, ENC_IQ4_XS: 0.12}[enc]
+             ENC_IQ4_NL: 0.12, ENC_IQ4_XS: 0.12, ENC_Q2_0: 0.45}[enc]
     assert rel < bound, rel
