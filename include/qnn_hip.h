@@ -69,13 +69,13 @@ extern "C" {
 #define QNN_WE_Q3_K 4
 #define QNN_WE_Q5_K 5
 #define QNN_WE_IQ4_NL 6
-#define QNN_WE_IQ3_S 7     /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ3_S 7
 #define QNN_WE_IQ4_XS 8
 #define QNN_WE_Q2_K 9
-#define QNN_WE_IQ2_XXS 10  /* read from GGUF tables; no kernel here */
-#define QNN_WE_IQ2_S 11    /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ2_XXS 10
+#define QNN_WE_IQ2_S 11
 #define QNN_WE_Q2_0 12
-#define QNN_WE_IQ3_XXS 13  /* read from GGUF tables; no kernel here */
+#define QNN_WE_IQ3_XXS 13
 
 /* ---- TSafeTensorType ordinals (src/io/QuickNN.SafeTensors.pas:34-77) ---- */
 #define QNN_ST_UNKNOWN (-1)

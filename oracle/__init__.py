@@ -26,11 +26,16 @@ ENC_Q3_K = 4
 ENC_Q2_K = 9
 ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS = 5, 6, 8
 ENC_Q2_0 = 12
-GGUF_ENCODINGS = (ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0)
+ENC_IQ3_S, ENC_IQ2_XXS, ENC_IQ2_S, ENC_IQ3_XXS = 7, 10, 11, 13
+GGUF_ENCODINGS = (ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0,
+                  ENC_IQ2_XXS, ENC_IQ2_S, ENC_IQ3_XXS, ENC_IQ3_S)
 BLOCK_ELEMENTS = {ENC_Q8_0: 32, ENC_Q4_K: 256, ENC_Q6_K: 256, ENC_Q3_K: 256, ENC_Q2_K: 256, ENC_Q5_K: 256,
-                  ENC_IQ4_NL: 32, ENC_IQ4_XS: 256, ENC_Q2_0: 64}
+                  ENC_IQ4_NL: 32, ENC_IQ4_XS: 256, ENC_Q2_0: 64, ENC_IQ2_XXS: 256, ENC_IQ2_S: 256, ENC_IQ3_XXS: 256,
+                  ENC_IQ3_S: 256}
 BLOCK_BYTES = {ENC_Q8_0: 34, ENC_Q4_K: 144, ENC_Q6_K: 210, ENC_Q3_K: 110, ENC_Q2_K: 84, ENC_Q5_K: 176,
-               ENC_IQ4_NL: 18, ENC_IQ4_XS: 136, ENC_Q2_0: 18}
+               ENC_IQ4_NL: 18, ENC_IQ4_XS: 136, ENC_Q2_0: 18, ENC_IQ2_XXS: 66, ENC_IQ2_S: 82, ENC_IQ3_XXS: 98,
+               ENC_IQ3_S: 110}
+IQ_TABLES = {"IQ2_XXS_GRID": 0, "IQ2_S_GRID": 1, "IQ3_XXS_GRID": 2, "IQ3_S_GRID": 3, "IQ2_SIGNS": 4}
 
 _lib = None
 
@@ -66,6 +71,7 @@ def lib():
             "qo_vector_dot": (ctypes.c_float, [ctypes.c_int, _f32p, _f32p]),
             "qo_int4_vector_dot": (ctypes.c_float, [ctypes.c_int, _f32p, _u8p]),
             "qo_packed_dot": (ctypes.c_float, [_u8p, ctypes.c_int, _f32p, ctypes.c_int]),
+            "qo_iq_table": (ctypes.c_int, [ctypes.c_int, _vp]),
             "qo_pool_create": (_vp, [ctypes.c_int]),
             "qo_pool_destroy": (None, [_vp]),
             "qo_pool_threads": (ctypes.c_int, [_vp]),
@@ -176,6 +182,15 @@ def gguf_read4_all(data: np.ndarray, enc: int, count: int) -> np.ndarray:
 
 
 # ---- dots and the CPU projection ----
+def iq_table(name: str) -> bytes:
+    """The oracle's copy of an IQ2/IQ3 table (IQ_TABLES) as little-endian bytes."""
+    which = IQ_TABLES[name]
+    n = lib().qo_iq_table(which, None)
+    buf = ctypes.create_string_buffer(n)
+    lib().qo_iq_table(which, buf)
+    return buf.raw
+
+
 def vector_dot(a: np.ndarray, b: np.ndarray) -> float:
     """VectorDot (CPU.Inference.AVX2.inc:7-67)."""
     a = np.ascontiguousarray(a, np.float32)

@@ -8,6 +8,9 @@
 //
 // Reference paths are relative to the QuickNN source tree.
 #include "qnn_oracle.h"
+// The IQ2/IQ3 codebooks (GGML's; the reference's src/io/QuickNN.GGUF.Tables.inc),
+// pinned against digests of the reference's tables in tests/test_oracle_gguf.py.
+#include "../quicknn_amd/csrc/qnn_iq_grids.h"
 
 #include <immintrin.h>
 
@@ -247,6 +250,7 @@ int qo_gguf_block_elements(int enc) {  // :67-75
   switch (enc) {
     case QO_ENC_Q8_0: case QO_ENC_IQ4_NL: return 32;
     case QO_ENC_Q2_0: return 64;
+    case QO_ENC_IQ2_XXS: case QO_ENC_IQ2_S: case QO_ENC_IQ3_XXS: case QO_ENC_IQ3_S: return 256;
     case QO_ENC_Q4_K: case QO_ENC_Q6_K: case QO_ENC_Q3_K: case QO_ENC_Q2_K: case QO_ENC_Q5_K: case QO_ENC_IQ4_XS:
       return 256;
     default: return -1;
@@ -263,9 +267,37 @@ int qo_gguf_block_bytes(int enc) {  // :77-93
     case QO_ENC_IQ4_NL: return 18;
     case QO_ENC_IQ4_XS: return 136;
     case QO_ENC_Q2_0: return 18;
+    case QO_ENC_IQ2_XXS: return 66;
+    case QO_ENC_IQ2_S: return 82;
+    case QO_ENC_IQ3_XXS: return 98;
+    case QO_ENC_IQ3_S: return 110;
     default: return -1;
   }
 }
+
+// IQ2_XXS_GRID, IQ2_S_GRID, IQ3_XXS_GRID, IQ3_S_GRID, IQ2_SIGNS (Tables.inc:20-309).
+static constexpr auto kG2XXS = qnn_iq::iq2xxs_grid();
+static constexpr auto kG2S = qnn_iq::iq2s_grid();
+static constexpr auto kG3XXS = qnn_iq::iq3xxs_grid();
+static constexpr auto kG3S = qnn_iq::iq3s_grid();
+static constexpr auto kSigns = qnn_iq::iq2_signs();
+
+int qo_iq_table(int which, uint8_t *out) {
+  const void *p;
+  int n;
+  switch (which) {
+    case 0: p = kG2XXS.v; n = sizeof(kG2XXS.v); break;
+    case 1: p = kG2S.v; n = sizeof(kG2S.v); break;
+    case 2: p = kG3XXS.v; n = sizeof(kG3XXS.v); break;
+    case 3: p = kG3S.v; n = sizeof(kG3S.v); break;
+    case 4: p = kSigns.v; n = sizeof(kSigns.v); break;
+    default: return -1;
+  }
+  if (out) std::memcpy(out, p, size_t(n));
+  return n;
+}
+
+static uint32_t le32(const uint8_t *p) { return p[0] | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16) | (uint32_t(p[3]) << 24); }
 
 // IQ4_NL_VALUES (:34): the non-linear 4-bit codebook of IQ4_NL and IQ4_XS.
 static const int kIQ4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
@@ -297,6 +329,43 @@ float qo_gguf_value(const uint8_t *data, int enc, int64_t index) {
       int q = (b[quant_offset + (i / 64) * 32 + i % 32] >> ((group & 1) * 4)) & 15;
       if (enc == QO_ENC_Q5_K) q |= ((b[16 + i % 32] >> group) & 1) << 4;
       return (half_at(b) * float(scale)) * float(q) - half_at(b + 2) * float(minimum);
+    }
+    case QO_ENC_IQ3_XXS: {  // :148-157 (Pascal evaluates the scale in double; every value here is exact)
+      const int group = i / 32;
+      const uint32_t bits = le32(b + 66 + group * 4);
+      const uint32_t signs = kSigns.v[(bits >> (7 * ((i % 32) / 8))) & 127];
+      int q = int((kG3XXS.v[b[2 + i / 4]] >> ((i % 4) * 8)) & 255);
+      if (signs & (1u << (i % 8))) q = -q;
+      return float((double(half_at(b)) * (0.5 + double(bits >> 28)) * 0.5) * q);
+    }
+    case QO_ENC_IQ2_XXS:
+    case QO_ENC_IQ2_S: {  // :158-179
+      const int group = i / 32, lane = (i % 32) / 8;
+      uint64_t grid;
+      uint32_t signs;
+      float delta;
+      if (enc == QO_ENC_IQ2_XXS) {
+        const uint32_t quant_bits = le32(b + 6 + group * 8);
+        grid = kG2XXS.v[b[2 + group * 8 + lane]];
+        signs = kSigns.v[(quant_bits >> (7 * lane)) & 127];
+        delta = float(double(half_at(b)) * (0.5 + double(quant_bits >> 28)) * 0.25);
+      } else {
+        grid = kG2S.v[b[2 + group * 4 + lane] | (((b[66 + group] >> (lane * 2)) & 3) << 8)];
+        signs = b[34 + i / 8];
+        const int q = (b[74 + group] >> (((i % 32) / 16) * 4)) & 15;
+        delta = float(double(half_at(b)) * (0.5 + q) * 0.25);
+      }
+      int q = int((grid >> ((i % 8) * 8)) & 255);
+      if (signs & (1u << (i % 8))) q = -q;
+      return delta * float(q);
+    }
+    case QO_ENC_IQ3_S: {  // :242-251
+      const int group = i / 32;
+      const int grid_index = b[2 + i / 4] | (((b[66 + group] >> ((i % 32) / 4)) & 1) << 8);
+      int q = int((kG3S.v[grid_index] >> ((i % 4) * 8)) & 255);
+      if (b[74 + i / 8] & (1 << (i % 8))) q = -q;
+      const int scale = 1 + 2 * ((b[106 + group / 2] >> ((group % 2) * 4)) & 15);
+      return (half_at(b) * float(scale)) * float(q);
     }
     case QO_ENC_Q2_0:  // :146-147: fp16 d, then 2-bit q four to a byte; d * (q - 1)
       return half_at(b) * float(int((b[2 + i / 4] >> ((i % 4) * 2)) & 3) - 1);
@@ -344,8 +413,28 @@ static void decode_iq4(const uint8_t *src, float *dst, float scale) {
 int qo_gguf_decode_block(const uint8_t *b, int enc, float *out) {
   switch (enc) {
     case QO_ENC_Q2_0:  // :285-289: element by element through GGUFValue
-      for (int i = 0; i < 64; ++i) out[i] = qo_gguf_value(b, enc, i);
+    case QO_ENC_IQ2_XXS:
+    case QO_ENC_IQ2_S:
+    case QO_ENC_IQ3_XXS:
+      for (int i = 0; i < qo_gguf_block_elements(enc); ++i) out[i] = qo_gguf_value(b, enc, i);
       return 0;
+    case QO_ENC_IQ3_S: {  // :350-361: signed grid bytes (SignedIQ3Grid, :594-605), then q * (d * scale) per 32
+      int8_t quants[256];
+      for (int i = 0; i < 64; ++i) {
+        const int grid = b[2 + i] | (((b[66 + i / 8] >> (i % 8)) & 1) << 8);
+        const int signs = (b[74 + i / 2] >> ((i & 1) * 4)) & 15;
+        for (int t = 0; t < 4; ++t) {
+          const int q = int((kG3S.v[grid] >> (t * 8)) & 255);
+          quants[i * 4 + t] = int8_t((signs >> t) & 1 ? -q : q);
+        }
+      }
+      const float d = half_at(b);
+      for (int g = 0; g < 8; ++g) {
+        const float sc = d * float(1 + 2 * ((b[106 + g / 2] >> ((g & 1) * 4)) & 15));
+        for (int i = 0; i < 32; ++i) out[g * 32 + i] = float(quants[g * 32 + i]) * sc;
+      }
+      return 0;
+    }
     case QO_ENC_Q5_K: {  // :296-312 with DecodeBits (:30-66): q = low4 | high1 << 4, cvt(q) * Scale + Bias
       float d = half_at(b), dm = half_at(b + 2);
       for (int g = 0; g < 8; ++g) {
@@ -462,12 +551,62 @@ static uint32_t packed_word(const uint8_t *data, uint64_t off) {
 }
 static float packed_half(const uint8_t *data, uint64_t off) { return half_at(data + off); }
 
+// readGGUF (gguf.glsl:477-512) for encodings 10-13: one value.
+static float shader_read(const uint8_t *data, int enc, uint64_t index) {
+  if (enc == QO_ENC_IQ3_XXS) {  // :478-485
+    const uint64_t base = (index / 256u) * 98u;
+    const uint32_t i = uint32_t(index & 255u), group = i / 32u;
+    const uint32_t bits = packed_word(data, base + 66u + group * 4u);
+    const uint32_t signs = kSigns.v[(bits >> (7u * ((i % 32u) / 8u))) & 127u];
+    int q = int((kG3XXS.v[packed_byte(data, base + 2u + i / 4u)] >> ((i % 4u) * 8u)) & 255u);
+    if (signs & (1u << (i % 8u))) q = -q;
+    return (packed_half(data, base) * (0.5f + float(bits >> 28u)) * 0.5f) * float(q);
+  }
+  if (enc == QO_ENC_Q2_0) {  // :486-490
+    const uint64_t base = (index / 64u) * 18u, i = index % 64u;
+    return packed_half(data, base) * float(int((packed_byte(data, base + 2u + i / 4u) >> ((i % 4u) * 2u)) & 3u) - 1);
+  }
+  // IQ2_XXS / IQ2_S (:491-512)
+  const uint32_t i = uint32_t(index & 255u), group = i / 32u, lane = (i % 32u) / 8u;
+  const uint64_t base = (index / 256u) * (enc == QO_ENC_IQ2_XXS ? 66u : 82u);
+  uint64_t grid;
+  uint32_t signs;
+  float delta;
+  if (enc == QO_ENC_IQ2_XXS) {
+    const uint32_t word = packed_word(data, base + 6u + group * 8u);
+    grid = kG2XXS.v[packed_byte(data, base + 2u + group * 8u + lane)];
+    signs = kSigns.v[(word >> (7u * lane)) & 127u];
+    delta = packed_half(data, base) * (0.5f + float(word >> 28u)) * 0.25f;
+  } else {
+    grid = kG2S.v[packed_byte(data, base + 2u + group * 4u + lane) |
+                  (((packed_byte(data, base + 66u + group) >> (lane * 2u)) & 3u) << 8u)];
+    signs = packed_byte(data, base + 34u + i / 8u);
+    const uint32_t scale = (packed_byte(data, base + 74u + group) >> (((i % 32u) / 16u) * 4u)) & 15u;
+    delta = packed_half(data, base) * (0.5f + float(scale)) * 0.25f;
+  }
+  int q = int((grid >> ((i % 8u) * 8u)) & 255u);
+  if (signs & (1u << (i % 8u))) q = -q;
+  return delta * float(q);
+}
+
 int qo_gguf_read4(const uint8_t *data, int enc, int64_t index, float *o) {
   if (index % 4) return -1;
-  if (enc == QO_ENC_Q2_0) {  // :592 (encodings >= 10: four readGGUF), :486-489
+  if (enc == QO_ENC_Q2_0 || enc == QO_ENC_IQ2_XXS || enc == QO_ENC_IQ2_S || enc == QO_ENC_IQ3_XXS) {
+    for (int t = 0; t < 4; ++t) o[t] = shader_read(data, enc, uint64_t(index) + t);  // :592 (encodings >= 10)
+    return 0;
+  }
+  if (enc == QO_ENC_IQ3_S) {  // :648-655 (readGGUF4's last case)
+    const uint64_t base = (uint64_t(index) >> 8) * 110u;
+    const uint32_t item = uint32_t(index) & 255u, group = item / 32u;
+    const uint32_t grid = packed_byte(data, base + 2u + item / 4u) |
+                          (((packed_byte(data, base + 66u + group) >> ((item % 32u) / 4u)) & 1u) << 8);
+    const uint32_t sb = packed_byte(data, base + 74u + item / 8u);
+    const uint32_t scale = 1u + 2u * ((packed_byte(data, base + 106u + group / 2u) >> ((group % 2u) * 4u)) & 15u);
+    const float a = packed_half(data, base) * float(scale);
     for (int t = 0; t < 4; ++t) {
-      uint64_t i = uint64_t(index) + t, base = (i / 64u) * 18u, e = i % 64u;
-      o[t] = packed_half(data, base) * float(int((packed_byte(data, base + 2u + e / 4u) >> ((e % 4u) * 2u)) & 3u) - 1);
+      int q = int((kG3S.v[grid] >> (8 * t)) & 255u);
+      if ((sb >> (uint32_t(t) + (item & 4u))) & 1u) q = -q;
+      o[t] = a * float(q);
     }
     return 0;
   }

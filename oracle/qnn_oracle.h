@@ -11,8 +11,8 @@
  * invariants, brute force) lives in tests/test_oracle_*.py.
  *
  * Encodings follow TQNNWeightEncoding (src/core/QuickNN.Common.pas:130-131):
- *   0 native, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q3_K, 5 Q5_K, 6 IQ4_NL, 8 IQ4_XS, 9 Q2_K,
- *   12 Q2_0.
+ *   0 native, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q3_K, 5 Q5_K, 6 IQ4_NL, 7 IQ3_S, 8 IQ4_XS,
+ *   9 Q2_K, 10 IQ2_XXS, 11 IQ2_S, 12 Q2_0, 13 IQ3_XXS.
  * The oracle uses QO_ENC_INT4 (-1) for QuickNN's native packed INT4 rows.
  */
 #ifndef QNN_ORACLE_H
@@ -32,6 +32,10 @@ extern "C" {
 #define QO_ENC_IQ4_XS 8
 #define QO_ENC_Q2_K 9
 #define QO_ENC_Q2_0 12
+#define QO_ENC_IQ3_S 7
+#define QO_ENC_IQ2_XXS 10
+#define QO_ENC_IQ2_S 11
+#define QO_ENC_IQ3_XXS 13
 
 /* Status codes: 0 ok, -1 argument error (EArgumentException). */
 
@@ -48,6 +52,10 @@ float qo_gguf_value(const uint8_t *data, int enc, int64_t index);     /* :136-25
 int qo_gguf_decode_block(const uint8_t *block, int enc, float *out);  /* :274-368 */
 int qo_gguf_dequantize(const uint8_t *data, int enc, int64_t count, float *out); /* :370-383 */
 int qo_gguf_read4(const uint8_t *data, int enc, int64_t index, float *out4);
+/* The IQ2/IQ3 tables as little-endian bytes: 0 IQ2_XXS_GRID, 1 IQ2_S_GRID,
+   2 IQ3_XXS_GRID, 3 IQ3_S_GRID, 4 IQ2_SIGNS (Tables.inc:20-309); returns the
+   byte count (out may be NULL), -1 for another index. */
+int qo_iq_table(int which, uint8_t *out);
                                 /* shaders/gguf.glsl:591-655 (readGGUF4) */
 
 /* ---- AVX2 dots (CPU.Inference.AVX2.inc, GGUF.Dot.AVX2.inc) ---- */

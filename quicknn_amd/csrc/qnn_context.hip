@@ -312,6 +312,7 @@ int gguf_block_elements(int enc) {  // GGUF.Quantization.pas:67-75 (formats in t
   switch (enc) {
     case QNN_WE_Q8_0: case QNN_WE_IQ4_NL: return 32;
     case QNN_WE_Q2_0: return 64;
+    case QNN_WE_IQ2_XXS: case QNN_WE_IQ2_S: case QNN_WE_IQ3_XXS: case QNN_WE_IQ3_S:
     case QNN_WE_Q4_K: case QNN_WE_Q6_K: case QNN_WE_Q3_K: case QNN_WE_Q2_K: case QNN_WE_Q5_K: case QNN_WE_IQ4_XS:
       return 256;
   }
@@ -328,6 +329,10 @@ int gguf_block_bytes(int enc) {  // GGUF.Quantization.pas:77-93
     case QNN_WE_IQ4_NL: return 18;
     case QNN_WE_IQ4_XS: return 136;
     case QNN_WE_Q2_0: return 18;
+    case QNN_WE_IQ2_XXS: return 66;
+    case QNN_WE_IQ2_S: return 82;
+    case QNN_WE_IQ3_XXS: return 98;
+    case QNN_WE_IQ3_S: return 110;
   }
   return -1;
 }

@@ -1,5 +1,5 @@
 // qnn_gguf.hip -- GGML block formats (Q8_0, Q4_K, Q5_K, Q6_K, Q3_K, Q2_K,
-// IQ4_NL, IQ4_XS, Q2_0) for gfx950.
+// IQ4_NL, IQ4_XS, Q2_0, IQ2_XXS, IQ2_S, IQ3_XXS, IQ3_S) for gfx950.
 //
 // Formats and decode rules: src/io/QuickNN.GGUF.Quantization.pas:136-253
 // (GGUFValue); the matvec replaces op 65 (ggufvector.comp:34-52) and the GGUF
@@ -20,6 +20,10 @@
 //   IQ4_XS (136 B): main quants 128 (C=8), side1 d|scales_h|scales_l (8)
 //   IQ4_NL (8x18 B): main 8x16 quants (C=8), side1 8 fp16 d (16)
 //   Q2_0  (4x18 B): main 4x16 quants (C=4), side1 4 fp16 d (8)
+//   IQ2_XXS (66 B): main 64 (C=4), side1 d (2)
+//   IQ2_S   (82 B): main qs|signs|qh|scales 80 (C=5), side1 d (2)
+//   IQ3_XXS (98 B): main qs|signs+scales 96 (C=6), side1 d (2)
+//   IQ3_S  (110 B): main qs|signs 96 (C=6), side1 qh|scales (12), side2 d (2)
 // so every wave load is a 16-byte (or 12/8/4/2-byte) load by 64 consecutive
 // lanes.  Bytes per weight are unchanged.
 //
@@ -36,13 +40,18 @@
 //   IQ4_NL: sum = s2 * d * dot(v, X)                      (v = codebook byte)
 //   IQ4_XS: sum = s2 * d*(ls-32) * dot(v, X)              (sub-block 32)
 //   Q2_0:   sum = s2 * d * (dot(q, X) - sum(X))           (value d*(q-1))
+//   IQ2/IQ3: sum = s2 * delta * dot(+-grid, X)   (per 32-group; IQ2_S per 16)
 // where X = 256 q1 + q2 and every dot is exact integer arithmetic; the IQ4
 // nibbles become their signed codebook bytes by a byte-permute lookup.  A
 // Q2_0 byte holds four consecutive elements, so its activation slice is
 // staged with each 16-element run transposed as a 4x4 byte matrix: word t
 // then holds elements t, t+4, t+8, t+12, which is what one shift and mask of
-// a quant word yields.
+// a quant word yields.  The IQ2/IQ3 grid codebook and a table of byte sign
+// masks are copied into LDS by every workgroup; each 8 weights then take one
+// grid lookup (two 4-byte entries for IQ3), one mask lookup, and the signs
+// are applied to the grid bytes as (g ^ m) + (m & 0x01010101).
 #include "qnn_int4_dev.h"  // buffer-load helpers (rsrc, ld128, ld32f) and the exchange
+#include "qnn_iq_grids.h"
 
 namespace qnn {
 namespace {
@@ -96,6 +105,42 @@ template <> struct Fmt<QNN_WE_Q5_K> { static constexpr int C = 11, S1 = 0, S2 = 
 template <> struct Fmt<QNN_WE_IQ4_XS> { static constexpr int C = 8, S1 = 8, S2 = 0; };
 template <> struct Fmt<QNN_WE_IQ4_NL> { static constexpr int C = 8, S1 = 16, S2 = 0; };
 template <> struct Fmt<QNN_WE_Q2_0> { static constexpr int C = 4, S1 = 8, S2 = 0; };
+template <> struct Fmt<QNN_WE_IQ2_XXS> { static constexpr int C = 4, S1 = 2, S2 = 0; };
+template <> struct Fmt<QNN_WE_IQ2_S> { static constexpr int C = 5, S1 = 2, S2 = 0; };
+template <> struct Fmt<QNN_WE_IQ3_XXS> { static constexpr int C = 6, S1 = 2, S2 = 0; };
+template <> struct Fmt<QNN_WE_IQ3_S> { static constexpr int C = 6, S1 = 12, S2 = 2; };
+
+// ---------------------------------------------------------------- IQ2/IQ3 tables
+// The codebooks (qnn_iq_grids.h), expanded at compile time into device memory,
+// and byte sign masks: entry s has byte i = 0xFF where bit i of s is set.
+constexpr qnn_iq::Table<uint64_t, 256> sign_masks() {
+  qnn_iq::Table<uint64_t, 256> t{};
+  for (int s = 0; s < 256; ++s)
+    for (int i = 0; i < 8; ++i)
+      if ((s >> i) & 1) t.v[s] |= uint64_t(0xFF) << (8 * i);
+  return t;
+}
+__device__ const qnn_iq::Table<uint64_t, 256> kIQ2XXSGrid = qnn_iq::iq2xxs_grid();
+__device__ const qnn_iq::Table<uint64_t, 1024> kIQ2SGrid = qnn_iq::iq2s_grid();
+__device__ const qnn_iq::Table<uint32_t, 256> kIQ3XXSGrid = qnn_iq::iq3xxs_grid();
+__device__ const qnn_iq::Table<uint32_t, 512> kIQ3SGrid = qnn_iq::iq3s_grid();
+__device__ const qnn_iq::Table<uint8_t, 128> kIQ2Signs = qnn_iq::iq2_signs();
+__device__ const qnn_iq::Table<uint64_t, 256> kSignMasks = sign_masks();
+
+template <int ENC> constexpr bool kIsIQ =
+    ENC == QNN_WE_IQ2_XXS || ENC == QNN_WE_IQ2_S || ENC == QNN_WE_IQ3_XXS || ENC == QNN_WE_IQ3_S;
+// Bytes of the format's codebook (0 for the other formats).
+template <int ENC> constexpr int kIQGridBytes = ENC == QNN_WE_IQ2_XXS ? 2048 : ENC == QNN_WE_IQ2_S ? 8192
+                                                : ENC == QNN_WE_IQ3_XXS ? 1024 : ENC == QNN_WE_IQ3_S ? 2048 : 0;
+template <int ENC> __device__ __forceinline__ const uint4 *iq_grid_src() {
+  if constexpr (ENC == QNN_WE_IQ2_XXS) return reinterpret_cast<const uint4 *>(kIQ2XXSGrid.v);
+  if constexpr (ENC == QNN_WE_IQ2_S) return reinterpret_cast<const uint4 *>(kIQ2SGrid.v);
+  if constexpr (ENC == QNN_WE_IQ3_XXS) return reinterpret_cast<const uint4 *>(kIQ3XXSGrid.v);
+  return reinterpret_cast<const uint4 *>(kIQ3SGrid.v);
+}
+// IQ2_SIGNS (7 stored sign bits -> 8, even parity) without the table.
+__device__ __forceinline__ uint32_t iq2_sign8(uint32_t s7) { return s7 | ((__builtin_popcount(s7) & 1u) << 7); }
+__device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
 
 // IQ4_NL_VALUES (src/io/QuickNN.GGUF.Quantization.pas:34) as signed bytes,
 // four per word: the codebook of IQ4_NL and IQ4_XS.
@@ -160,6 +205,14 @@ __device__ __forceinline__ void plane_addr(int enc, const GGLayout &l, int t, in
     case QNN_WE_Q2_K: if (o < 80) main_at(o); else s1_at(o - 80); break;
     case QNN_WE_Q5_K: main_at(o); break;
     case QNN_WE_IQ4_XS: if (o < 8) s1_at(o); else main_at(o - 8); break;
+    case QNN_WE_IQ2_XXS: case QNN_WE_IQ2_S: case QNN_WE_IQ3_XXS: if (o < 2) s1_at(o); else main_at(o - 2); break;
+    case QNN_WE_IQ3_S:  // d | qs 64 | qh 8 | signs 32 | scales 4
+      if (o < 2) s2_at(o);
+      else if (o < 66) main_at(o - 2);
+      else if (o < 74) s1_at(o - 66);
+      else if (o < 106) main_at(o - 10);
+      else s1_at(o - 98);
+      break;
     case QNN_WE_IQ4_NL:
     case QNN_WE_Q2_0: {  // unit of 8 (4) blocks: block k = o / 18, byte j = o % 18: d at j < 2, quants after
       const int k = o / 18, j = o % 18;
@@ -215,6 +268,44 @@ __device__ float gguf_value_tiled(int enc, const GGLayout &l, const Planes &p, i
       const int k = i / 32, j = i % 32;
       const int q = int((B(18 * k + 2 + j % 16) >> ((j / 16) * 4)) & 15);
       return H(18 * k) * float(iq4_value(q));
+    }
+    case QNN_WE_IQ3_XXS: {  // GGUF.Quantization.pas:148-157
+      const int group = i / 32;
+      const uint32_t bits = B(66 + group * 4) | (B(67 + group * 4) << 8) | (B(68 + group * 4) << 16) |
+                            (B(69 + group * 4) << 24);
+      const uint32_t signs = kIQ2Signs.v[(bits >> (7 * ((i % 32) / 8))) & 127];
+      int q = int((kIQ3XXSGrid.v[B(2 + i / 4)] >> ((i % 4) * 8)) & 255);
+      if (signs & (1u << (i % 8))) q = -q;
+      return (H(0) * (0.5f + float(bits >> 28)) * 0.5f) * float(q);
+    }
+    case QNN_WE_IQ2_XXS:
+    case QNN_WE_IQ2_S: {  // :158-179
+      const int group = i / 32, lane = (i % 32) / 8;
+      uint64_t grid;
+      uint32_t signs;
+      float delta;
+      if (enc == QNN_WE_IQ2_XXS) {
+        const uint32_t bits = B(6 + group * 8) | (B(7 + group * 8) << 8) | (B(8 + group * 8) << 16) |
+                              (B(9 + group * 8) << 24);
+        grid = kIQ2XXSGrid.v[B(2 + group * 8 + lane)];
+        signs = kIQ2Signs.v[(bits >> (7 * lane)) & 127];
+        delta = H(0) * (0.5f + float(bits >> 28)) * 0.25f;
+      } else {
+        grid = kIQ2SGrid.v[B(2 + group * 4 + lane) | (((B(66 + group) >> (lane * 2)) & 3) << 8)];
+        signs = B(34 + i / 8);
+        delta = H(0) * (0.5f + float((B(74 + group) >> (((i % 32) / 16) * 4)) & 15)) * 0.25f;
+      }
+      int q = int((grid >> ((i % 8) * 8)) & 255);
+      if (signs & (1u << (i % 8))) q = -q;
+      return delta * float(q);
+    }
+    case QNN_WE_IQ3_S: {  // :242-251
+      const int group = i / 32;
+      const uint32_t gi = B(2 + i / 4) | (((B(66 + group) >> ((i % 32) / 4)) & 1) << 8);
+      int q = int((kIQ3SGrid.v[gi] >> ((i % 4) * 8)) & 255);
+      if (B(74 + i / 8) & (1u << (i % 8))) q = -q;
+      const int scale = 1 + 2 * int((B(106 + group / 2) >> ((group % 2) * 4)) & 15);
+      return (H(0) * float(scale)) * float(q);
     }
     case QNN_WE_Q2_0: {  // GGUF.Quantization.pas:146-147
       const int k = i / 64, j = i % 64;
@@ -558,6 +649,109 @@ __device__ float unit_q2_0(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int 
   return acc;
 }
 
+// IQ2/IQ3 units.  `grid` and `mask` point at the LDS copies of the codebook
+// and of the sign masks.  8 weights (lane L of a 32-group) are one 8-byte
+// grid entry (IQ2) or two 4-byte entries (IQ3) against activation words 2L
+// and 2L + 1 of the group.
+template <int NG>
+__device__ __forceinline__ void iq_dot8(uint64_t grid, uint64_t mask, const XSlice<NG> &xs, int g, int L, int &ah,
+                                        int &al) {
+  xdot(apply_sign(uint32_t(grid), uint32_t(mask)), xs.h[g][2 * L], xs.l[g][2 * L], ah, al);
+  xdot(apply_sign(uint32_t(grid >> 32), uint32_t(mask >> 32)), xs.h[g][2 * L + 1], xs.l[g][2 * L + 1], ah, al);
+}
+
+template <int NG>
+__device__ float unit_iq2_xxs(const uint4 *mw, uint32_t dh, const XSlice<NG> &xs, int g0, const uint64_t *grid,
+                              const uint64_t *mask) {
+  const float d = half_f(dh);
+  float acc = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {  // group g: 4 grid indices, then 4 x 7 sign bits and a 4-bit scale
+    const uint32_t idx = sel4u(mw[g >> 1], 2 * (g & 1)), bits = sel4u(mw[g >> 1], 2 * (g & 1) + 1);
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int L = 0; L < 4; ++L)
+      iq_dot8<NG>(grid[(idx >> (8 * L)) & 255u], mask[iq2_sign8((bits >> (7 * L)) & 127u)], xs, g0 + g, L, ah, al);
+    const float delta = d * (0.5f + float(bits >> 28)) * 0.25f;
+    acc = fmaf(float(combine<NG>(ah, al)), delta * xs.s2[g0 + g], acc);
+  }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_iq2_s(const uint4 *mw, uint32_t dh, const XSlice<NG> &xs, int g0, const uint64_t *grid,
+                            const uint64_t *mask) {
+  // main: qs 0-31 (chunks 0-1), signs 32-63 (chunks 2-3), qh 64-71 and scales 72-79 (chunk 4)
+  const float d = half_f(dh);
+  float acc = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const uint32_t qs = sel4u(mw[g >> 2], g & 3), sg = sel4u(mw[2 + (g >> 2)], g & 3);
+    const uint32_t qh = (sel4u(mw[4], g >> 2) >> (8 * (g & 3))) & 255u;
+    const uint32_t sc = (sel4u(mw[4], 2 + (g >> 2)) >> (8 * (g & 3))) & 255u;
+    int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+#pragma unroll
+    for (int L = 0; L < 4; ++L) {
+      const uint32_t gi = ((qs >> (8 * L)) & 255u) | (((qh >> (2 * L)) & 3u) << 8);
+      if (L < 2) iq_dot8<NG>(grid[gi], mask[(sg >> (8 * L)) & 255u], xs, g0 + g, L, ah0, al0);
+      else iq_dot8<NG>(grid[gi], mask[(sg >> (8 * L)) & 255u], xs, g0 + g, L, ah1, al1);
+    }
+    const float d0 = d * (0.5f + float(sc & 15u)) * 0.25f, d1 = d * (0.5f + float(sc >> 4)) * 0.25f;
+    acc = fmaf(float(combine<NG>(ah0, al0)), d0 * xs.s2[g0 + g], acc);
+    acc = fmaf(float(combine<NG>(ah1, al1)), d1 * xs.s2[g0 + g], acc);
+  }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_iq3_xxs(const uint4 *mw, uint32_t dh, const XSlice<NG> &xs, int g0, const uint32_t *grid,
+                              const uint64_t *mask) {
+  // main: 64 grid indices (chunks 0-3, 8 per group), then 8 words of 4 x 7 sign bits and a 4-bit scale
+  const float d = half_f(dh);
+  float acc = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const uint32_t i0 = sel4u(mw[g >> 1], 2 * (g & 1)), i1 = sel4u(mw[g >> 1], 2 * (g & 1) + 1);
+    const uint32_t bits = sel4u(mw[4 + (g >> 2)], g & 3);
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int L = 0; L < 4; ++L) {
+      const uint32_t iw = L < 2 ? i0 : i1;
+      const uint32_t a = grid[(iw >> (16 * (L & 1))) & 255u], b = grid[(iw >> (16 * (L & 1) + 8)) & 255u];
+      iq_dot8<NG>(uint64_t(a) | (uint64_t(b) << 32), mask[iq2_sign8((bits >> (7 * L)) & 127u)], xs, g0 + g, L, ah, al);
+    }
+    const float delta = d * (0.5f + float(bits >> 28)) * 0.5f;
+    acc = fmaf(float(combine<NG>(ah, al)), delta * xs.s2[g0 + g], acc);
+  }
+  return acc;
+}
+
+template <int NG>
+__device__ float unit_iq3_s(const uint4 *mw, uint4 s1, uint32_t dh, const XSlice<NG> &xs, int g0,
+                            const uint32_t *grid, const uint64_t *mask) {
+  // main: 64 low grid-index bytes (chunks 0-3), 32 sign bytes (chunks 4-5); side1: qh 8 | scales 4
+  const float d = half_f(dh);
+  float acc = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const uint32_t i0 = sel4u(mw[g >> 1], 2 * (g & 1)), i1 = sel4u(mw[g >> 1], 2 * (g & 1) + 1);
+    const uint32_t sg = sel4u(mw[4 + (g >> 2)], g & 3);
+    const uint32_t qh = (sel4u(s1, g >> 2) >> (8 * (g & 3))) & 255u;
+    const uint32_t sc = (s1.z >> (4 * g)) & 15u;
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int L = 0; L < 4; ++L) {
+      const uint32_t iw = L < 2 ? i0 : i1;
+      const int j = 2 * L;  // 4-element pieces j, j + 1 of the group
+      const uint32_t a = grid[((iw >> (16 * (L & 1))) & 255u) | (((qh >> j) & 1u) << 8)];
+      const uint32_t b = grid[((iw >> (16 * (L & 1) + 8)) & 255u) | (((qh >> (j + 1)) & 1u) << 8)];
+      iq_dot8<NG>(uint64_t(a) | (uint64_t(b) << 32), mask[(sg >> (8 * L)) & 255u], xs, g0 + g, L, ah, al);
+    }
+    acc = fmaf(float(combine<NG>(ah, al)), (d * float(1u + 2u * sc)) * xs.s2[g0 + g], acc);
+  }
+  return acc;
+}
+
 template <int NG>
 __device__ float unit_iq4_xs(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int g0) {
   // side: bytes 0-1 d, 2-3 scales_h, 4-7 scales_l
@@ -618,6 +812,19 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
                            dev::ld32f(xsrc, kb + 12, 0));
     }
   }
+  // 1b) IQ2/IQ3: the codebook and the sign masks, for LDS
+  constexpr int kGridU4 = kIQGridBytes<ENC> / 16;
+  constexpr int kTabU4 = kIsIQ<ENC> ? kGridU4 + 128 : 0;
+  constexpr int kTabIt = (kTabU4 + 255) / 256;
+  uint4 tr[kTabIt > 0 ? kTabIt : 1];
+  if constexpr (kIsIQ<ENC>) {
+    const uint4 *masks = reinterpret_cast<const uint4 *>(kSignMasks.v);
+#pragma unroll
+    for (int it = 0; it < kTabIt; ++it) {  // every lane loads (pieces past the table re-read the last mask)
+      const int t = it * 256 + tid;
+      tr[it] = t < kGridU4 ? iq_grid_src<ENC>()[t] : masks[min(t - kGridU4, 127)];
+    }
+  }
   // 2) weights of this wave's units
   int stile = tile, srow = lane;
   const void *wb = a.w;
@@ -656,6 +863,12 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
   // 3) quantise the activation slice (natural element order)
   __shared__ XSlice<NG> xs;
   __shared__ float red[3][64];
+  __shared__ uint4 iq_tab[kTabU4 > 0 ? kTabU4 : 1];
+  if constexpr (kIsIQ<ENC>) {
+#pragma unroll
+    for (int it = 0; it < kTabIt; ++it)
+      if (it * 256 + tid < kTabU4) iq_tab[it * 256 + tid] = tr[it];
+  }
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
     const int e = (it * 256 + tid) * 4;
@@ -705,6 +918,15 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
       if (ENC == QNN_WE_IQ4_NL) acc += unit_iq4_nl<NG>(mw[b], s1v[b], xs, g0);
       if (ENC == QNN_WE_IQ4_XS) acc += unit_iq4_xs<NG>(mw[b], s1v[b], xs, g0);
       if (ENC == QNN_WE_Q2_0) acc += unit_q2_0<NG>(mw[b], s1v[b], xs, g0);
+      if constexpr (kIsIQ<ENC>) {
+        const uint64_t *mask = reinterpret_cast<const uint64_t *>(iq_tab + kGridU4);
+        const uint64_t *g64 = reinterpret_cast<const uint64_t *>(iq_tab);
+        const uint32_t *g32 = reinterpret_cast<const uint32_t *>(iq_tab);
+        if (ENC == QNN_WE_IQ2_XXS) acc += unit_iq2_xxs<NG>(mw[b], s1w[b], xs, g0, g64, mask);
+        if (ENC == QNN_WE_IQ2_S) acc += unit_iq2_s<NG>(mw[b], s1w[b], xs, g0, g64, mask);
+        if (ENC == QNN_WE_IQ3_XXS) acc += unit_iq3_xxs<NG>(mw[b], s1w[b], xs, g0, g32, mask);
+        if (ENC == QNN_WE_IQ3_S) acc += unit_iq3_s<NG>(mw[b], s1v[b], s2w[b], xs, g0, g32, mask);
+      }
     }
   }
 
@@ -812,6 +1034,10 @@ GGLayout gguf_layout(int enc, int rows, int cols) {
     case QNN_WE_IQ4_XS: l.main_chunks = 8; l.side1_bytes = 8; l.side2_bytes = 0; l.unit_bytes = 136; break;
     case QNN_WE_IQ4_NL: l.main_chunks = 8; l.side1_bytes = 16; l.side2_bytes = 0; l.unit_bytes = 144; break;
     case QNN_WE_Q2_0: l.main_chunks = 4; l.side1_bytes = 8; l.side2_bytes = 0; l.unit_bytes = 72; break;
+    case QNN_WE_IQ2_XXS: l.main_chunks = 4; l.side1_bytes = 2; l.side2_bytes = 0; l.unit_bytes = 66; break;
+    case QNN_WE_IQ2_S: l.main_chunks = 5; l.side1_bytes = 2; l.side2_bytes = 0; l.unit_bytes = 82; break;
+    case QNN_WE_IQ3_XXS: l.main_chunks = 6; l.side1_bytes = 2; l.side2_bytes = 0; l.unit_bytes = 98; break;
+    case QNN_WE_IQ3_S: l.main_chunks = 6; l.side1_bytes = 12; l.side2_bytes = 2; l.unit_bytes = 110; break;
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
   l.src_row_bytes = enc == QNN_WE_Q8_0     ? (cols / 32) * 34
@@ -890,6 +1116,10 @@ void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s) {
     case QNN_WE_IQ4_NL: launch_enc<QNN_WE_IQ4_NL>(g, bw, s); break;
     case QNN_WE_IQ4_XS: launch_enc<QNN_WE_IQ4_XS>(g, bw, s); break;
     case QNN_WE_Q2_0: launch_enc<QNN_WE_Q2_0>(g, bw, s); break;
+    case QNN_WE_IQ2_XXS: launch_enc<QNN_WE_IQ2_XXS>(g, bw, s); break;
+    case QNN_WE_IQ2_S: launch_enc<QNN_WE_IQ2_S>(g, bw, s); break;
+    case QNN_WE_IQ3_XXS: launch_enc<QNN_WE_IQ3_XXS>(g, bw, s); break;
+    case QNN_WE_IQ3_S: launch_enc<QNN_WE_IQ3_S>(g, bw, s); break;
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
   hip_check(hipGetLastError(), "gguf matvec launch");

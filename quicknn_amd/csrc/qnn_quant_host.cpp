@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../../include/qnn_hip.h"
+#include "qnn_iq_grids.h"
 
 namespace {
 
@@ -303,6 +304,147 @@ void enc_q2_0(const float *x, uint8_t *b) {
   }
 }
 
+// ---- IQ2 / IQ3 grid formats.  Each 8 (IQ2) or 4 (IQ3) magnitudes |x| / delta
+// take the nearest codebook entry (least squares, brute force), the signs
+// are stored as bits.  IQ2_XXS and IQ3_XXS store 7 of 8 sign bits, the eighth
+// being their parity: where the signs of 8 elements have odd parity, the
+// element of least magnitude takes the other sign.
+static constexpr auto kHostG2XXS = qnn_iq::iq2xxs_grid();
+static constexpr auto kHostG2S = qnn_iq::iq2s_grid();
+static constexpr auto kHostG3XXS = qnn_iq::iq3xxs_grid();
+static constexpr auto kHostG3S = qnn_iq::iq3s_grid();
+
+template <class T, int N>
+int nearest_entry(const qnn_iq::Table<T, N> &grid, int bytes, const float *mag) {
+  int best = 0;
+  float best_err = INFINITY;
+  for (int e = 0; e < N; ++e) {
+    float err = 0.0f;
+    for (int i = 0; i < bytes; ++i) {
+      const float d = mag[i] - float((grid.v[e] >> (8 * i)) & 255u);
+      err += d * d;
+    }
+    if (err < best_err) { best_err = err; best = e; }
+  }
+  return best;
+}
+
+// Sign bits of 8 elements (bit i: x[i] < 0); with `even`, forced to even parity.
+uint32_t sign_bits8(const float *x, bool even) {
+  uint32_t s = 0;
+  int least = 0;
+  for (int i = 0; i < 8; ++i) {
+    if (x[i] < 0) s |= 1u << i;
+    if (std::fabs(x[i]) < std::fabs(x[least])) least = i;
+  }
+  if (even && (__builtin_popcount(s) & 1)) s ^= 1u << least;
+  return s;
+}
+
+float amax_of(const float *x, int n) {
+  float m = 0;
+  for (int i = 0; i < n; ++i) m = std::max(m, std::fabs(x[i]));
+  return m;
+}
+
+// d for per-group steps delta_g = d * f(n_g), n_g in 0..15 with f(15) the largest step.
+float grid_d(const float *x, int group, float top_level, float f15) {
+  float m = 0;
+  for (int g = 0; g < 256 / group; ++g) m = std::max(m, amax_of(x + g * group, group) / top_level);
+  return m / f15;
+}
+int step_index(float want, float d, float unit, float offset) {  // n with d * (offset + n) * unit nearest want
+  return d > 0 ? clampi(rnd(want / (d * unit) - offset), 0, 15) : 0;
+}
+
+// IQ2_XXS (66 B per 256): fp16 d; per 32-group 4 grid-index bytes and a word of
+// 4 x 7 sign bits with a 4-bit scale n on top; delta = d (0.5 + n) / 4.
+void enc_iq2_xxs(const float *x, uint8_t *b) {
+  std::memset(b, 0, 66);
+  put_half(b, grid_d(x, 32, 43.0f, 15.5f * 0.25f));
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8)));
+  for (int g = 0; g < 8; ++g) {
+    const float *xg = x + 32 * g;
+    const int n = step_index(amax_of(xg, 32) / 43.0f, d, 0.25f, 0.5f);
+    const float delta = d * (0.5f + float(n)) * 0.25f;
+    uint32_t bits = uint32_t(n) << 28;
+    for (int L = 0; L < 4; ++L) {
+      float mag[8];
+      for (int i = 0; i < 8; ++i) mag[i] = delta > 0 ? std::fabs(xg[8 * L + i]) / delta : 0.0f;
+      b[2 + 8 * g + L] = uint8_t(nearest_entry(kHostG2XXS, 8, mag));
+      bits |= (sign_bits8(xg + 8 * L, true) & 127u) << (7 * L);
+    }
+    std::memcpy(b + 6 + 8 * g, &bits, 4);
+  }
+}
+
+// IQ2_S (82 B per 256): fp16 d, 32 low index bytes, 32 sign bytes, 8 bytes of
+// 4 x 2 high index bits, 8 bytes of two 4-bit scales (per 16 elements).
+void enc_iq2_s(const float *x, uint8_t *b) {
+  std::memset(b, 0, 82);
+  put_half(b, grid_d(x, 16, 43.0f, 15.5f * 0.25f));
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8)));
+  for (int g = 0; g < 8; ++g) {
+    for (int h = 0; h < 2; ++h) {
+      const float *xh = x + 32 * g + 16 * h;
+      const int n = step_index(amax_of(xh, 16) / 43.0f, d, 0.25f, 0.5f);
+      const float delta = d * (0.5f + float(n)) * 0.25f;
+      b[74 + g] |= uint8_t(n << (4 * h));
+      for (int L = 2 * h; L < 2 * h + 2; ++L) {
+        float mag[8];
+        for (int i = 0; i < 8; ++i) mag[i] = delta > 0 ? std::fabs(x[32 * g + 8 * L + i]) / delta : 0.0f;
+        const int e = nearest_entry(kHostG2S, 8, mag);
+        b[2 + 4 * g + L] = uint8_t(e & 255);
+        b[66 + g] |= uint8_t((e >> 8) << (2 * L));
+        b[34 + 4 * g + L] = uint8_t(sign_bits8(x + 32 * g + 8 * L, false));
+      }
+    }
+  }
+}
+
+// IQ3_XXS (98 B per 256): fp16 d, 64 grid-index bytes (one per 4 elements), 8
+// words of 4 x 7 sign bits with a 4-bit scale n on top; delta = d (0.5 + n) / 2.
+void enc_iq3_xxs(const float *x, uint8_t *b) {
+  std::memset(b, 0, 98);
+  put_half(b, grid_d(x, 32, 62.0f, 15.5f * 0.5f));
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8)));
+  for (int g = 0; g < 8; ++g) {
+    const float *xg = x + 32 * g;
+    const int n = step_index(amax_of(xg, 32) / 62.0f, d, 0.5f, 0.5f);
+    const float delta = d * (0.5f + float(n)) * 0.5f;
+    uint32_t bits = uint32_t(n) << 28;
+    for (int j = 0; j < 8; ++j) {
+      float mag[4];
+      for (int i = 0; i < 4; ++i) mag[i] = delta > 0 ? std::fabs(xg[4 * j + i]) / delta : 0.0f;
+      b[2 + 8 * g + j] = uint8_t(nearest_entry(kHostG3XXS, 4, mag));
+    }
+    for (int L = 0; L < 4; ++L) bits |= (sign_bits8(xg + 8 * L, true) & 127u) << (7 * L);
+    std::memcpy(b + 66 + 4 * g, &bits, 4);
+  }
+}
+
+// IQ3_S (110 B per 256): fp16 d, 64 low index bytes, 8 bytes of high index
+// bits, 32 sign bytes, 4 bytes of 4-bit scales s; step d (1 + 2 s).
+void enc_iq3_s(const float *x, uint8_t *b) {
+  std::memset(b, 0, 110);
+  put_half(b, grid_d(x, 32, 15.0f, 31.0f));
+  const float d = from_half(uint16_t(b[0] | (b[1] << 8)));
+  for (int g = 0; g < 8; ++g) {
+    const float *xg = x + 32 * g;
+    const int s = d > 0 ? clampi(rnd((amax_of(xg, 32) / 15.0f / d - 1.0f) / 2.0f), 0, 15) : 0;
+    const float step = d * float(1 + 2 * s);
+    b[106 + g / 2] |= uint8_t(s << (4 * (g % 2)));
+    for (int j = 0; j < 8; ++j) {
+      float mag[4];
+      for (int i = 0; i < 4; ++i) mag[i] = step > 0 ? std::fabs(xg[4 * j + i]) / step : 0.0f;
+      const int e = nearest_entry(kHostG3S, 4, mag);
+      b[2 + 8 * g + j] = uint8_t(e & 255);
+      b[66 + g] |= uint8_t((e >> 8) << j);
+    }
+    for (int L = 0; L < 4; ++L) b[74 + 4 * g + L] = uint8_t(sign_bits8(xg + 8 * L, false));
+  }
+}
+
 // IQ4_XS (136 B per 256): fp16 d, 6-bit signed sub-block scales (low nibbles
 // at 4 + j/2, high 2 bits of scale j at bits 2j of the 16-bit word at 2),
 // then 8 x 16 bytes of codebook nibbles.
@@ -373,6 +515,10 @@ int qnn_gguf_quantize(int encoding, const float *src, int64_t n, uint8_t *dst) {
     case QNN_WE_IQ4_NL: elems = 32; bytes = 18; fn = enc_iq4_nl; break;
     case QNN_WE_IQ4_XS: elems = 256; bytes = 136; fn = enc_iq4_xs; break;
     case QNN_WE_Q2_0: elems = 64; bytes = 18; fn = enc_q2_0; break;
+    case QNN_WE_IQ2_XXS: elems = 256; bytes = 66; fn = enc_iq2_xxs; break;
+    case QNN_WE_IQ2_S: elems = 256; bytes = 82; fn = enc_iq2_s; break;
+    case QNN_WE_IQ3_XXS: elems = 256; bytes = 98; fn = enc_iq3_xxs; break;
+    case QNN_WE_IQ3_S: elems = 256; bytes = 110; fn = enc_iq3_s; break;
     default: return QNN_E_NOT_SUPPORTED;
   }
   if (!src || !dst || n < 0 || n % elems) return QNN_E_ARGUMENT;

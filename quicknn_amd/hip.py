@@ -71,9 +71,11 @@ _ERRORS = {c.code: c for c in (EArgumentException, ERangeError, ENotSupportedExc
 DT_F16, DT_BF16, DT_F32, DT_S8, DT_U8 = 1, 2, 3, 5, 6
 WE_NATIVE, WE_Q8_0, WE_Q4_K, WE_Q6_K, WE_Q3_K, WE_Q2_K = 0, 1, 2, 3, 4, 9
 WE_Q5_K, WE_IQ4_NL, WE_IQ4_XS, WE_Q2_0 = 5, 6, 8, 12
+WE_IQ3_S, WE_IQ2_XXS, WE_IQ2_S, WE_IQ3_XXS = 7, 10, 11, 13
 GGUF_BLOCK = {WE_Q8_0: (32, 34), WE_Q4_K: (256, 144), WE_Q6_K: (256, 210), WE_Q3_K: (256, 110),
               WE_Q2_K: (256, 84), WE_Q5_K: (256, 176), WE_IQ4_NL: (32, 18), WE_IQ4_XS: (256, 136),
-              WE_Q2_0: (64, 18)}
+              WE_Q2_0: (64, 18), WE_IQ2_XXS: (256, 66), WE_IQ2_S: (256, 82), WE_IQ3_XXS: (256, 98),
+              WE_IQ3_S: (256, 110)}
 
 # ---- op codes (Context.API.inc:167-258) ----
 GO_FILL, GO_NORM, GO_ADD, GO_SWIGLU, GO_FINITE = 0, 2, 4, 9, 13

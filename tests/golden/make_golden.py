@@ -54,6 +54,12 @@ FORMATS_EXT = [
 FORMATS_EXT2 = [
     (oracle.ENC_Q2_0, "Q2_0", 64, 18, (0,)),
 ]
+FORMATS_EXT3 = [
+    (oracle.ENC_IQ2_XXS, "IQ2_XXS", 256, 66, (0,)),
+    (oracle.ENC_IQ2_S, "IQ2_S", 256, 82, (0,)),
+    (oracle.ENC_IQ3_XXS, "IQ3_XXS", 256, 98, (0,)),
+    (oracle.ENC_IQ3_S, "IQ3_S", 256, 110, (0,)),
+]
 
 
 def hexf(a) -> str:
@@ -156,7 +162,7 @@ def sha256s() -> dict:
     out = {"int4_qwen3_4b_layer0_seed1000": {
         "shapes": [[9728, 2560], [9728, 2560], [2560, 9728]],
         "sha256": [hashlib.sha256(m.tobytes()).hexdigest() for m in bench_layer0()]}}
-    for enc, name, elems, nbytes, _ in FORMATS + FORMATS_EXT + FORMATS_EXT2:
+    for enc, name, elems, nbytes, _ in FORMATS + FORMATS_EXT + FORMATS_EXT2 + FORMATS_EXT3:
         r = np.random.default_rng(2000 + enc)
         n, kk = 512, 3584 if elems == 256 else 3072
         w = (r.standard_normal(n * kk, dtype=np.float32) * np.float32(0.02))
@@ -175,6 +181,9 @@ def main() -> None:
     rng_ext2 = np.random.default_rng(20261215)
     files["blocks.json"].update(gguf_blocks(rng_ext2, FORMATS_EXT2))
     files["matvec.json"].update(gguf_matvecs(rng_ext2, FORMATS_EXT2))
+    rng_ext3 = np.random.default_rng(20261216)
+    files["blocks.json"].update(gguf_blocks(rng_ext3, FORMATS_EXT3))
+    files["matvec.json"].update(gguf_matvecs(rng_ext3, FORMATS_EXT3))
     for fname, data in files.items():
         with open(os.path.join(OUT, fname), "w") as f:
             json.dump(data, f, indent=1)

@@ -22,9 +22,10 @@ from tests.conftest import normwise_rel_err
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 ENC = {"Q8_0": oracle.ENC_Q8_0, "Q4_K": oracle.ENC_Q4_K, "Q6_K": oracle.ENC_Q6_K, "Q3_K": oracle.ENC_Q3_K,
        "Q2_K": oracle.ENC_Q2_K, "Q5_K": oracle.ENC_Q5_K, "IQ4_NL": oracle.ENC_IQ4_NL, "IQ4_XS": oracle.ENC_IQ4_XS,
-       "Q2_0": oracle.ENC_Q2_0}
+       "Q2_0": oracle.ENC_Q2_0, "IQ2_XXS": oracle.ENC_IQ2_XXS, "IQ2_S": oracle.ENC_IQ2_S,
+       "IQ3_XXS": oracle.ENC_IQ3_XXS, "IQ3_S": oracle.ENC_IQ3_S}
 ELEMS = {"Q8_0": 32, "Q4_K": 256, "Q6_K": 256, "Q3_K": 256, "Q2_K": 256, "Q5_K": 256, "IQ4_NL": 32, "IQ4_XS": 256,
-         "Q2_0": 64}
+         "Q2_0": 64, "IQ2_XXS": 256, "IQ2_S": 256, "IQ3_XXS": 256, "IQ3_S": 256}
 
 
 def load(name):

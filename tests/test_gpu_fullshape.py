@@ -169,7 +169,9 @@ def test_outlier_activations_fused_mlp_qwen3_4b(ctx):
 
 @pytest.mark.parametrize("enc,n,k", [(hip.WE_Q4_K, 4096, 3584), (hip.WE_Q6_K, 3584, 14336),
                                      (hip.WE_Q3_K, 2048, 3584), (hip.WE_Q2_K, 4096, 3584),
-                                     (hip.WE_Q8_0, 4096, 3584), (hip.WE_Q2_0, 4096, 3584)])
+                                     (hip.WE_Q8_0, 4096, 3584), (hip.WE_Q2_0, 4096, 3584),
+                                     (hip.WE_IQ2_XXS, 4096, 3584), (hip.WE_IQ2_S, 4096, 3584),
+                                     (hip.WE_IQ3_XXS, 4096, 3584), (hip.WE_IQ3_S, 4096, 3584)])
 def test_outlier_activations_gguf_linear(ctx, enc, n, k):
     rng = np.random.default_rng(enc)
     d = gguf_matrix(rng, enc, n, k)

@@ -1,4 +1,5 @@
-"""GPU parity of the GGUF path (Q8_0, Q4_K, Q5_K, Q6_K, Q3_K, Q2_K, IQ4_NL, IQ4_XS, Q2_0) against the CPU oracle.
+"""GPU parity of the GGUF path (Q8_0, Q4_K, Q5_K, Q6_K, Q3_K, Q2_K, IQ4_NL, IQ4_XS, Q2_0, IQ2_XXS, IQ2_S, IQ3_XXS,
+IQ3_S) against the CPU oracle.
 
 Dequantised weights must equal GGUFValue (GGUF.Quantization.pas:136-253) bit
 for bit (as floats: +0 == -0, the reference's own decoders differ there);
@@ -10,17 +11,19 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import (BLOCK_BYTES, BLOCK_ELEMENTS, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K,
-                    ENC_Q6_K, ENC_Q8_0)
+from oracle import (BLOCK_BYTES, BLOCK_ELEMENTS, ENC_IQ2_S, ENC_IQ2_XXS, ENC_IQ3_S, ENC_IQ3_XXS, ENC_IQ4_NL, ENC_IQ4_XS,
+                    ENC_Q2_0, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q8_0)
 from quicknn_amd import hip
 from tests.conftest import normwise_rel_err
 from tests.test_oracle_gguf import random_blocks
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
-FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0]
+FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_IQ2_XXS, ENC_IQ2_S,
+        ENC_IQ3_XXS, ENC_IQ3_S]
 NAMES = {ENC_Q8_0: "q8_0", ENC_Q4_K: "q4_k", ENC_Q6_K: "q6_k", ENC_Q3_K: "q3_k", ENC_Q2_K: "q2_k", ENC_Q5_K: "q5_k",
-         ENC_IQ4_NL: "iq4_nl", ENC_IQ4_XS: "iq4_xs", ENC_Q2_0: "q2_0"}
+         ENC_IQ4_NL: "iq4_nl", ENC_IQ4_XS: "iq4_xs", ENC_Q2_0: "q2_0", ENC_IQ2_XXS: "iq2_xxs", ENC_IQ2_S: "iq2_s",
+         ENC_IQ3_XXS: "iq3_xxs", ENC_IQ3_S: "iq3_s"}
 
 
 def quantized(rng, enc, n, k, scale=0.02):
@@ -73,6 +76,8 @@ def test_dequant_offset_slice(ctx, rng):
     (ENC_Q5_K, 4096, 3584), (ENC_IQ4_XS, 4096, 4096), (ENC_IQ4_NL, 2048, 3584), (ENC_Q5_K, 5, 256),
     (ENC_IQ4_XS, 70, 768), (ENC_IQ4_NL, 33, 96), (ENC_IQ4_NL, 129, 1312),
     (ENC_Q2_0, 4096, 3584), (ENC_Q2_0, 14336, 3584), (ENC_Q2_0, 33, 192), (ENC_Q2_0, 129, 1344), (ENC_Q2_0, 7, 64),
+    (ENC_IQ2_XXS, 4096, 3584), (ENC_IQ2_S, 4096, 3584), (ENC_IQ3_XXS, 4096, 4096), (ENC_IQ3_S, 3584, 14336),
+    (ENC_IQ2_XXS, 5, 256), (ENC_IQ2_S, 70, 768), (ENC_IQ3_XXS, 129, 1280), (ENC_IQ3_S, 63, 512),
 ])
 def test_linear_m1(ctx, rng, enc, n, k):
     data = quantized(rng, enc, n, k)
@@ -200,7 +205,8 @@ def _swiglu_want(pg, eg, pu, eu, x, k, n):
     (ENC_Q6_K, ENC_Q6_K, 33, 256), (ENC_Q3_K, ENC_Q3_K, 257, 512), (ENC_Q4_K, ENC_Q6_K, 500, 512),
     (ENC_Q5_K, ENC_Q5_K, 1000, 768), (ENC_IQ4_XS, ENC_IQ4_XS, 300, 512), (ENC_IQ4_NL, ENC_IQ4_NL, 96, 160),
     (ENC_IQ4_NL, ENC_IQ4_XS, 200, 512), (ENC_Q2_0, ENC_Q2_0, 300, 448), (ENC_Q2_0, ENC_Q2_0, 9728, 2560),
-    (ENC_Q2_0, ENC_Q4_K, 200, 512),
+    (ENC_Q2_0, ENC_Q4_K, 200, 512), (ENC_IQ2_XXS, ENC_IQ2_XXS, 1000, 768), (ENC_IQ2_S, ENC_IQ2_S, 96, 3584),
+    (ENC_IQ3_XXS, ENC_IQ3_XXS, 257, 512), (ENC_IQ3_S, ENC_IQ3_S, 4096, 2560), (ENC_IQ2_S, ENC_IQ3_XXS, 200, 512),
 ])
 def test_swiglu_vector(ctx, rng, eg, eu, n, k):
     pg, pu = quantized(rng, eg, n, k), quantized(rng, eu, n, k)
@@ -218,5 +224,5 @@ def test_gguf_argument_errors(ctx, rng):
         ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, 500, enc), None, None, 1, 500, n)
     with pytest.raises(hip.EArgumentException):  # more rows than the block holds
         ctx.Linear(ctx.NewTensor(2 * n), src, hip.MemoryBlock.gguf(data, n, k, enc), None, None, 1, k, 2 * n)
-    with pytest.raises(hip.ENotSupportedException):  # IQ3_S and the other grid formats are not handled
-        ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, k, 7), None, None, 1, k, n)
+    with pytest.raises(hip.ENotSupportedException):  # an encoding outside TQNNWeightEncoding
+        ctx.Linear(dst, src, hip.MemoryBlock.gguf(data, n, k, 14), None, None, 1, k, n)

@@ -2,21 +2,28 @@
 the three independent reference decoders (scalar GGUFValue :136-253, the AVX2
 block decoders :274-368, the shader's readGGUF4 gguf.glsl:591-655) must agree
 on random valid blocks; hand-built blocks give known answers from the format
-definitions; the packed AVX2 dots agree with a double-precision dot over the
-decoded weights; the product's block encoders round-trip."""
+definitions; the IQ2/IQ3 tables match digests of the reference's own tables
+(tests/golden/iq_grids.json); the packed AVX2 dots agree with a
+double-precision dot over the decoded weights; the product's block encoders
+round-trip."""
+import hashlib
+import json
+import os
 import struct
 
 import numpy as np
 import pytest
 
 import oracle
-from oracle import (ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_Q2_K, ENC_Q3_K, ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q8_0,
-                    BLOCK_BYTES, BLOCK_ELEMENTS)
+from oracle import (ENC_IQ2_S, ENC_IQ2_XXS, ENC_IQ3_S, ENC_IQ3_XXS, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_Q2_K, ENC_Q3_K,
+                    ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q8_0, BLOCK_BYTES, BLOCK_ELEMENTS)
 
-FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0]
+FMTS = [ENC_Q8_0, ENC_Q4_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_Q5_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_IQ2_XXS, ENC_IQ2_S,
+        ENC_IQ3_XXS, ENC_IQ3_S]
 # fp16 fields (byte offsets within a block)
 HALF_FIELDS = {ENC_Q8_0: [0], ENC_Q4_K: [0, 2], ENC_Q6_K: [208], ENC_Q3_K: [108], ENC_Q2_K: [80, 82],
-               ENC_Q5_K: [0, 2], ENC_IQ4_NL: [0], ENC_IQ4_XS: [0], ENC_Q2_0: [0]}
+               ENC_Q5_K: [0, 2], ENC_IQ4_NL: [0], ENC_IQ4_XS: [0], ENC_Q2_0: [0], ENC_IQ2_XXS: [0], ENC_IQ2_S: [0],
+               ENC_IQ3_XXS: [0], ENC_IQ3_S: [0]}
 # IQ4_NL_VALUES (src/io/QuickNN.GGUF.Quantization.pas:34), typed in from the format definition
 IQ4 = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
 
@@ -194,6 +201,125 @@ def test_q2_0_known_answer():
     assert oracle.cpu_linear(b, ENC_Q2_0, np.ones(128, np.float32), 128, 1)[0] == want.sum()
 
 
+def iq_grid(name):
+    width = 4 if name.startswith("IQ3") else 8
+    return np.frombuffer(oracle.iq_table(name), np.uint32 if width == 4 else np.uint64)
+
+
+def test_iq_tables_match_reference_digests():
+    """The codebooks and the sign table, as the oracle and the kernels build them, hash to the
+    digests of the reference's own tables (Tables.inc:20-309, gguf.glsl:20-460)."""
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "iq_grids.json")) as f:
+        want = json.load(f)
+    for name, entry in want.items():
+        data = oracle.iq_table(name)
+        assert len(data) == entry["entries"] * (1 if name == "IQ2_SIGNS" else 4 if name.startswith("IQ3") else 8)
+        assert hashlib.sha256(data).hexdigest() == entry["sha256"], name
+
+
+def test_iq_table_invariants():
+    """What the format definitions fix without the tables: IQ2_SIGNS[i] is i with an eighth bit for even
+    parity; every grid is strictly increasing; IQ2 entries take the levels 8, 25, 43, IQ3_XXS 4..52 by 8
+    and 62, IQ3_S the odd numbers 1..15."""
+    signs = np.frombuffer(oracle.iq_table("IQ2_SIGNS"), np.uint8)
+    assert [int(v) for v in signs] == [i | ((bin(i).count("1") & 1) << 7) for i in range(128)]
+    for name, levels in (("IQ2_XXS_GRID", {8, 25, 43}), ("IQ2_S_GRID", {8, 25, 43}),
+                         ("IQ3_XXS_GRID", {4, 12, 20, 28, 36, 44, 52, 62}), ("IQ3_S_GRID", set(range(1, 16, 2)))):
+        g = iq_grid(name)
+        assert np.all(g[1:] > g[:-1]), name
+        assert set(np.unique(g.view(np.uint8)).tolist()) <= levels, name
+
+
+def _put_half(b, off, v):
+    b[off:off + 2] = np.frombuffer(struct.pack("<H", f16(v)), np.uint8)
+
+
+def _grid_bytes(entry, width):
+    return [(int(entry) >> (8 * i)) & 255 for i in range(width)]
+
+
+def test_iq2_xxs_known_answer():
+    # d = 0.5; group g: scale n = g (delta = 0.5 (0.5 + g) / 4); lane L: grid index 37g + 11L + 5 (mod 256),
+    # 7 stored sign bits 5g + 3L (mod 128), the eighth from parity.
+    grid, b = iq_grid("IQ2_XXS_GRID"), np.zeros(66, np.uint8)
+    _put_half(b, 0, 0.5)
+    want = np.zeros(256, np.float32)
+    for g in range(8):
+        bits = g << 28
+        for L in range(4):
+            idx, s7 = (37 * g + 11 * L + 5) % 256, (5 * g + 3 * L) % 128
+            b[2 + 8 * g + L] = idx
+            bits |= s7 << (7 * L)
+            s8 = s7 | ((bin(s7).count("1") & 1) << 7)
+            for e, v in enumerate(_grid_bytes(grid[idx], 8)):
+                want[32 * g + 8 * L + e] = np.float32(0.5 * (0.5 + g) * 0.25) * (-v if s8 >> e & 1 else v)
+        b[6 + 8 * g:10 + 8 * g] = np.frombuffer(struct.pack("<I", bits), np.uint8)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_IQ2_XXS, 256), want)
+
+
+def test_iq2_s_known_answer():
+    # d = -0.25; lane L of group g: 10-bit index (97g + 29L + 3) mod 1024 (low byte, 2 high bits in the
+    # group's qh byte), sign byte 17g + 61L (mod 256), scale nibbles g (elements 0-15) and 15 - g (16-31).
+    grid, b = iq_grid("IQ2_S_GRID"), np.zeros(82, np.uint8)
+    _put_half(b, 0, -0.25)
+    want = np.zeros(256, np.float32)
+    for g in range(8):
+        b[74 + g] = g | ((15 - g) << 4)
+        for L in range(4):
+            idx, sg = (97 * g + 29 * L + 3) % 1024, (17 * g + 61 * L) % 256
+            b[2 + 4 * g + L] = idx & 255
+            b[66 + g] |= (idx >> 8) << (2 * L)
+            b[34 + 4 * g + L] = sg
+            n = g if L < 2 else 15 - g
+            for e, v in enumerate(_grid_bytes(grid[idx], 8)):
+                want[32 * g + 8 * L + e] = np.float32(-0.25 * (0.5 + n) * 0.25) * (-v if sg >> e & 1 else v)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_IQ2_S, 256), want)
+
+
+def test_iq3_xxs_known_answer():
+    # d = 2; 4-element piece j (0-63): grid index 53j + 7 (mod 256); group g: scale n = 15 - g
+    # (delta = 2 (0.5 + n) / 2), 7 stored sign bits per 8 elements (9g + 5L) mod 128, the eighth from parity.
+    grid, b = iq_grid("IQ3_XXS_GRID"), np.zeros(98, np.uint8)
+    _put_half(b, 0, 2.0)
+    want = np.zeros(256, np.float32)
+    for j in range(64):
+        b[2 + j] = (53 * j + 7) % 256
+    for g in range(8):
+        bits = (15 - g) << 28
+        for L in range(4):
+            s7 = (9 * g + 5 * L) % 128
+            bits |= s7 << (7 * L)
+            s8 = s7 | ((bin(s7).count("1") & 1) << 7)
+            for e in range(8):
+                i = 32 * g + 8 * L + e
+                v = _grid_bytes(grid[b[2 + i // 4]], 4)[i % 4]
+                want[i] = np.float32(2.0 * (0.5 + 15 - g) * 0.5) * (-v if s8 >> e & 1 else v)
+        b[66 + 4 * g:70 + 4 * g] = np.frombuffer(struct.pack("<I", bits), np.uint8)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_IQ3_XXS, 256), want)
+
+
+def test_iq3_s_known_answer():
+    # d = 0.125; piece j: 9-bit index (41j + 13) mod 512 (low byte; high bit j % 8 of byte 66 + j / 8);
+    # sign byte per 8 elements 23k + 1 (mod 256); group g: scale 1 + 2 (3g mod 16).
+    grid, b = iq_grid("IQ3_S_GRID"), np.zeros(110, np.uint8)
+    _put_half(b, 0, 0.125)
+    for j in range(64):
+        idx = (41 * j + 13) % 512
+        b[2 + j] = idx & 255
+        b[66 + j // 8] |= (idx >> 8) << (j % 8)
+    for k in range(32):
+        b[74 + k] = (23 * k + 1) % 256
+    for g in range(8):
+        b[106 + g // 2] |= ((3 * g) % 16) << (4 * (g % 2))
+    want = np.zeros(256, np.float32)
+    for i in range(256):
+        j, g = i // 4, i // 32
+        v = _grid_bytes(grid[(41 * j + 13) % 512], 4)[i % 4]
+        sign = ((23 * (i // 8) + 1) % 256) >> (i % 8) & 1
+        want[i] = np.float32(0.125 * (1 + 2 * ((3 * g) % 16))) * (-v if sign else v)
+    assert np.array_equal(oracle.gguf_dequant_scalar(b, ENC_IQ3_S, 256), want)
+
+
 def test_iq4_xs_known_answer():
     # d = 0.25; 6-bit sub-block scales ls (value ls - 32) with every high-bit pattern; q = (7i) % 16.
     b = np.zeros(136, np.uint8)
@@ -238,5 +364,6 @@ def test_product_encoder_round_trip(rng, enc):
     assert np.all(np.isfinite(dec))
     rel = np.linalg.norm(dec - w) / np.linalg.norm(w)
     bound = {ENC_Q8_0: 0.01, ENC_Q6_K: 0.03, ENC_Q4_K: 0.12, ENC_Q3_K: 0.25, ENC_Q2_K: 0.45, ENC_Q5_K: 0.06,
-             ENC_IQ4_NL: 0.12, ENC_IQ4_XS: 0.12, ENC_Q2_0: 0.45}[enc]
+             ENC_IQ4_NL: 0.12, ENC_IQ4_XS: 0.12, ENC_Q2_0: 0.45, ENC_IQ2_XXS: 0.4, ENC_IQ2_S: 0.3, ENC_IQ3_XXS: 0.25,
+             ENC_IQ3_S: 0.2}[enc]
     assert rel < bound, rel
