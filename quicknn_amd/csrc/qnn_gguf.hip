@@ -112,12 +112,24 @@ template <> struct Fmt<QNN_WE_IQ3_S> { static constexpr int C = 6, S1 = 12, S2 =
 
 // ---------------------------------------------------------------- IQ2/IQ3 tables
 // The codebooks (qnn_iq_grids.h), expanded at compile time into device memory,
-// and byte sign masks: entry s has byte i = 0xFF where bit i of s is set.
+// and byte sign masks: entry s of the 256 has byte i = 0xFF where bit i of s
+// is set (IQ2_S, IQ3_S: 8 stored sign bits); entry s of the 128 is the mask of
+// IQ2_SIGNS[s] (IQ2_XXS, IQ3_XXS: 7 stored bits, the eighth their parity).
+constexpr uint64_t byte_mask(int s) {
+  uint64_t m = 0;
+  for (int i = 0; i < 8; ++i)
+    if ((s >> i) & 1) m |= uint64_t(0xFF) << (8 * i);
+  return m;
+}
 constexpr qnn_iq::Table<uint64_t, 256> sign_masks() {
   qnn_iq::Table<uint64_t, 256> t{};
-  for (int s = 0; s < 256; ++s)
-    for (int i = 0; i < 8; ++i)
-      if ((s >> i) & 1) t.v[s] |= uint64_t(0xFF) << (8 * i);
+  for (int s = 0; s < 256; ++s) t.v[s] = byte_mask(s);
+  return t;
+}
+constexpr qnn_iq::Table<uint64_t, 128> sign_masks7() {
+  qnn_iq::Table<uint64_t, 128> t{};
+  const auto signs = qnn_iq::iq2_signs();
+  for (int s = 0; s < 128; ++s) t.v[s] = byte_mask(signs.v[s]);
   return t;
 }
 __device__ const qnn_iq::Table<uint64_t, 256> kIQ2XXSGrid = qnn_iq::iq2xxs_grid();
@@ -126,6 +138,7 @@ __device__ const qnn_iq::Table<uint32_t, 256> kIQ3XXSGrid = qnn_iq::iq3xxs_grid(
 __device__ const qnn_iq::Table<uint32_t, 512> kIQ3SGrid = qnn_iq::iq3s_grid();
 __device__ const qnn_iq::Table<uint8_t, 128> kIQ2Signs = qnn_iq::iq2_signs();
 __device__ const qnn_iq::Table<uint64_t, 256> kSignMasks = sign_masks();
+__device__ const qnn_iq::Table<uint64_t, 128> kSignMasks7 = sign_masks7();
 
 template <int ENC> constexpr bool kIsIQ =
     ENC == QNN_WE_IQ2_XXS || ENC == QNN_WE_IQ2_S || ENC == QNN_WE_IQ3_XXS || ENC == QNN_WE_IQ3_S;
@@ -138,8 +151,12 @@ template <int ENC> __device__ __forceinline__ const uint4 *iq_grid_src() {
   if constexpr (ENC == QNN_WE_IQ3_XXS) return reinterpret_cast<const uint4 *>(kIQ3XXSGrid.v);
   return reinterpret_cast<const uint4 *>(kIQ3SGrid.v);
 }
-// IQ2_SIGNS (7 stored sign bits -> 8, even parity) without the table.
-__device__ __forceinline__ uint32_t iq2_sign8(uint32_t s7) { return s7 | ((__builtin_popcount(s7) & 1u) << 7); }
+// 16-byte pieces of the sign-mask table a format uses.
+template <int ENC> constexpr int kIQMaskU4 = (ENC == QNN_WE_IQ2_XXS || ENC == QNN_WE_IQ3_XXS) ? 64 : 128;
+template <int ENC> __device__ __forceinline__ const uint4 *iq_mask_src() {
+  if constexpr (kIQMaskU4<ENC> == 64) return reinterpret_cast<const uint4 *>(kSignMasks7.v);
+  return reinterpret_cast<const uint4 *>(kSignMasks.v);
+}
 __device__ __forceinline__ uint32_t apply_sign(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
 
 // IQ4_NL_VALUES (src/io/QuickNN.GGUF.Quantization.pas:34) as signed bytes,
@@ -650,7 +667,8 @@ __device__ float unit_q2_0(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, int 
 }
 
 // IQ2/IQ3 units.  `grid` and `mask` point at the LDS copies of the codebook
-// and of the sign masks.  8 weights (lane L of a 32-group) are one 8-byte
+// and of the sign masks (indexed by the 7 stored bits for IQ2_XXS and
+// IQ3_XXS, by the sign byte for IQ2_S and IQ3_S).  8 weights (lane L of a 32-group) are one 8-byte
 // grid entry (IQ2) or two 4-byte entries (IQ3) against activation words 2L
 // and 2L + 1 of the group.
 template <int NG>
@@ -671,7 +689,7 @@ __device__ float unit_iq2_xxs(const uint4 *mw, uint32_t dh, const XSlice<NG> &xs
     int ah = 0, al = 0;
 #pragma unroll
     for (int L = 0; L < 4; ++L)
-      iq_dot8<NG>(grid[(idx >> (8 * L)) & 255u], mask[iq2_sign8((bits >> (7 * L)) & 127u)], xs, g0 + g, L, ah, al);
+      iq_dot8<NG>(grid[(idx >> (8 * L)) & 255u], mask[(bits >> (7 * L)) & 127u], xs, g0 + g, L, ah, al);
     const float delta = d * (0.5f + float(bits >> 28)) * 0.25f;
     acc = fmaf(float(combine<NG>(ah, al)), delta * xs.s2[g0 + g], acc);
   }
@@ -718,7 +736,7 @@ __device__ float unit_iq3_xxs(const uint4 *mw, uint32_t dh, const XSlice<NG> &xs
     for (int L = 0; L < 4; ++L) {
       const uint32_t iw = L < 2 ? i0 : i1;
       const uint32_t a = grid[(iw >> (16 * (L & 1))) & 255u], b = grid[(iw >> (16 * (L & 1) + 8)) & 255u];
-      iq_dot8<NG>(uint64_t(a) | (uint64_t(b) << 32), mask[iq2_sign8((bits >> (7 * L)) & 127u)], xs, g0 + g, L, ah, al);
+      iq_dot8<NG>(uint64_t(a) | (uint64_t(b) << 32), mask[(bits >> (7 * L)) & 127u], xs, g0 + g, L, ah, al);
     }
     const float delta = d * (0.5f + float(bits >> 28)) * 0.5f;
     acc = fmaf(float(combine<NG>(ah, al)), delta * xs.s2[g0 + g], acc);
@@ -814,15 +832,15 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
   }
   // 1b) IQ2/IQ3: the codebook and the sign masks, for LDS
   constexpr int kGridU4 = kIQGridBytes<ENC> / 16;
-  constexpr int kTabU4 = kIsIQ<ENC> ? kGridU4 + 128 : 0;
+  constexpr int kTabU4 = kIsIQ<ENC> ? kGridU4 + kIQMaskU4<ENC> : 0;
   constexpr int kTabIt = (kTabU4 + 255) / 256;
   uint4 tr[kTabIt > 0 ? kTabIt : 1];
   if constexpr (kIsIQ<ENC>) {
-    const uint4 *masks = reinterpret_cast<const uint4 *>(kSignMasks.v);
+    const uint4 *masks = iq_mask_src<ENC>();
 #pragma unroll
     for (int it = 0; it < kTabIt; ++it) {  // every lane loads (pieces past the table re-read the last mask)
       const int t = it * 256 + tid;
-      tr[it] = t < kGridU4 ? iq_grid_src<ENC>()[t] : masks[min(t - kGridU4, 127)];
+      tr[it] = t < kGridU4 ? iq_grid_src<ENC>()[t] : masks[min(t - kGridU4, kIQMaskU4<ENC> - 1)];
     }
   }
   // 2) weights of this wave's units
@@ -966,6 +984,13 @@ template <int ENC, int BW>
 __global__ __launch_bounds__(256) void k_gguf_matvec(const GGGroup grp) {
   gguf_item<ENC, BW>(grp, group_member(grp));
 }
+// The IQ2/IQ3 matvecs at one unit per wave, held to 128 VGPRs (4 waves per
+// SIMD): IQ2_S at 14336 x 3584 (3.5 workgroups per CU) measured 14.8 us at
+// the compiler's own 130 VGPRs (3 waves per SIMD) and 13.8 us so.
+template <int ENC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gguf_matvec_iq(const GGGroup grp) {
+  gguf_item<ENC, 1>(grp, group_member(grp));
+}
 // Members of two K-quant encodings in one launch (a layer's q/k/v often mix
 // quant types), one unit per wave; each workgroup runs its member's own code.
 template <int E0, int E1>
@@ -1011,7 +1036,8 @@ void launch_mixed(const GGGroup &g, int e1, hipStream_t st) {
 template <int ENC>
 void launch_enc(const GGGroup &g, int bw, hipStream_t st) {
   const int grid = g.start[g.count];
-  if (bw == 2) hipLaunchKernelGGL((k_gguf_matvec<ENC, 2>), dim3(grid), dim3(256), 0, st, g);
+  if (kIsIQ<ENC> && bw == 1) hipLaunchKernelGGL((k_gguf_matvec_iq<ENC>), dim3(grid), dim3(256), 0, st, g);
+  else if (bw == 2) hipLaunchKernelGGL((k_gguf_matvec<ENC, 2>), dim3(grid), dim3(256), 0, st, g);
   else hipLaunchKernelGGL((k_gguf_matvec<ENC, 1>), dim3(grid), dim3(256), 0, st, g);
 }
 
