@@ -164,6 +164,7 @@ void reload_tuning() {
   t.gemm_h16 = env_int("QNN_GEMM_H16", t.gemm_h16);
   t.attn_wgs = env_int("QNN_ATTN_WGS", t.attn_wgs);
   t.attn_min_chunk = env_int("QNN_ATTN_MIN_CHUNK", t.attn_min_chunk);
+  t.attn_dma = env_int("QNN_ATTN_DMA", t.attn_dma);
   t.gemm_nw = env_int("QNN_GEMM_NW", t.gemm_nw);
   t.gemm_mb = env_int("QNN_GEMM_MB", t.gemm_mb);
   t.gg_bw = env_int("QNN_GG_BW", t.gg_bw);

@@ -486,6 +486,228 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
   }
 }
 
+// ---------------------------------------------------------------------------
+// The 64-key chunk at dim 128 (a split of a few thousand keys).  q, the
+// chunk's K^T rows (128 x 256 B) and its V rows (64 x 512 B) are requested
+// straight into LDS, in that order, by buffer loads that write LDS: no
+// registers hold them, so the whole chunk is in flight at once.  Each wave
+// then waits for its q and K pieces only; the scores and the softmax run
+// while V is still arriving, and the wave waits for V before the values.
+// The arithmetic is k_attn's for this shape, in the same order (4 channel
+// parts of 32 per key summed in part order; per head one online-softmax step
+// over the 64 keys with the same lane butterflies, here head g in wave g % 4
+// instead of all heads in wave 0; 8 key lanes of 8 keys each in key order,
+// then the lane shuffle and the LDS sum of the four waves), so the two
+// kernels give the same bits.
+constexpr int kDmaKeys = 64, kDmaDim = 128;
+constexpr int attn_dma_qfloats(int gb) { return gb * kDmaDim < 256 ? 256 : gb * kDmaDim; }  // whole 1 KiB pieces
+constexpr size_t attn_dma_lds(int gb) {
+  return size_t(2 * kDmaKeys * kDmaDim + attn_dma_qfloats(gb) + gb * kDmaKeys + 4 * gb +
+                (3 * gb * kDmaDim > 4 * gb * kDmaKeys ? 3 * gb * kDmaDim : 4 * gb * kDmaKeys)) * 4;
+}
+typedef __amdgpu_buffer_rsrc_t AttnRsrc;
+__device__ __forceinline__ AttnRsrc attn_rsrc(const void *base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(uint32_t(min(bytes, size_t(0xFFFFFFFFu)))),
+                                           0x00020000);
+}
+// 1 KiB (16 B per lane, in lane order) from global memory at voff + soff into
+// LDS at `lds` (wave-uniform).  The compiler does not see the LDS write: the
+// waits before the barriers order it.  M0 is set here before each load;
+// nothing else in k_attn_dma uses M0 (gfx950's LDS instructions do not read
+// it), which the kernel's assembly shows.
+__device__ __forceinline__ void attn_dma(AttnRsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff),
+               "s"(r), "s"(soff)
+               : "memory");
+}
+// Wait until at most N of this wave's vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void attn_vmwait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int GB>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restrict__ q, const float *__restrict__ cache,
+                                                           float *__restrict__ out, float *__restrict__ opart,
+                                                           float *__restrict__ mlpart, AttnArgs a) {
+  extern __shared__ float lds[];
+  constexpr int QF = attn_dma_qfloats(GB);
+  float *kls = lds;                          // [128 channels][64 keys]
+  float *vls = kls + kDmaDim * kDmaKeys;     // [64 keys][128 channels]
+  float *qs = vls + kDmaKeys * kDmaDim;      // [GB][128] (QF floats)
+  float *ps = qs + QF;                       // [GB][64]
+  float *red = ps + GB * kDmaKeys;           // [4][GB] (keep, sum, max; the fourth keeps xred 16-byte aligned)
+  float *xred = red + 4 * GB;                // score parts [4][GB][64], then value lanes [3][GB][128]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kh = blockIdx.x / a.gpk, h0 = kh * a.group + (blockIdx.x % a.gpk) * GB;
+  const int r = blockIdx.y, s = blockIdx.z;
+  int start, end;
+  key_range(a, r, start, end);
+  const int k0 = start + s * kDmaKeys, nkeys = min(end - k0, kDmaKeys);  // none past the row's last key
+  const size_t width = size_t(a.kv_heads) * kDmaDim;
+  const float *kt = cache + size_t(kh) * kDmaDim * a.cap;
+  const float *vb = cache + size_t(a.cap) * width + size_t(kh) * a.cap * kDmaDim;
+  const unsigned *mask = reinterpret_cast<const unsigned *>(cache + 2 * size_t(a.cap) * width) + size_t(r) * a.cap;
+
+  // 1) q, then K^T, then V of the chunk into LDS.  Wave w: q piece w (if any;
+  //    GB heads of 128 floats are GB / 2 pieces, a lone head half of one),
+  //    channels 32w..32w+31 of K^T (8 pieces of 4 channels x 64 keys), keys
+  //    16w..16w+15 of V (8 pieces of 2 keys x 128 channels).  Loads past q's
+  //    heads or past this KV head's K^T or V region return 0; keys past the
+  //    chunk's end are loaded but never used.
+  constexpr int QP = QF / 256;  // q pieces
+  const int nk = max(nkeys, 0);
+  {
+    const uint32_t base = uint32_t(reinterpret_cast<uintptr_t>(lds));
+    if (wave < QP) {
+      const AttnRsrc qr = attn_rsrc(q + (size_t(r) * a.heads + h0) * kDmaDim, size_t(GB) * kDmaDim * 4);
+      attn_dma(qr, __builtin_amdgcn_readfirstlane(base + 65536u + uint32_t(wave) * 1024u),
+               uint32_t(wave) * 1024u + uint32_t(lane) * 16u, 0u);
+    }
+    if (nk > 0) {
+      const AttnRsrc kr = attn_rsrc(kt, size_t(kDmaDim) * a.cap * 4);
+      const AttnRsrc vr = attn_rsrc(vb, size_t(a.cap) * kDmaDim * 4);
+      const uint32_t kvoff = uint32_t((size_t(wave * 32 + lane / 16) * a.cap + k0 + (lane % 16) * 4) * 4);
+      const uint32_t vvoff = uint32_t((size_t(k0 + wave * 16 + lane / 32) * kDmaDim + (lane % 32) * 4) * 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        attn_dma(kr, __builtin_amdgcn_readfirstlane(base + uint32_t(wave * 8 + i) * 1024u), kvoff,
+                 uint32_t(i) * 16u * uint32_t(a.cap));
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        attn_dma(vr, __builtin_amdgcn_readfirstlane(base + 32768u + uint32_t(wave * 8 + i) * 1024u), vvoff,
+                 uint32_t(i) * 1024u);
+      attn_vmwait<8>();  // q and K landed (V may still be in flight)
+    } else {
+      attn_vmwait<0>();
+    }
+  }
+  __syncthreads();
+
+  const float mul = a.scale > 0.0f ? a.scale : 1.0f / sqrtf(float(kDmaDim));
+  float m_run[GB], l_run[GB], keep[GB];
+  float4 acc[GB];
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.0f;
+    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const int key_t = lane, part = wave;  // scores: key, 32-channel part
+  const int kk = tid / 32, c4 = tid % 32;  // values: key lane, float4 channel group
+  if (nk > 0) {
+    // ---- scores: part `wave` of the channels for key `lane`
+    bool valid = key_t < nk;
+    if (valid && a.masked) valid = mask[k0 + key_t] != 0u;
+    float sc[GB];
+#pragma unroll
+    for (int g = 0; g < GB; ++g) sc[g] = 0.0f;
+    if (valid) {
+      float kv[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) kv[u] = kls[(part * 32 + u) * kDmaKeys + key_t];
+#pragma unroll
+      for (int u = 0; u < 32; ++u)
+#pragma unroll
+        for (int g = 0; g < GB; ++g) sc[g] += qs[g * kDmaDim + part * 32 + u] * kv[u];
+    }
+#pragma unroll
+    for (int g = 0; g < GB; ++g) xred[(part * GB + g) * kDmaKeys + key_t] = sc[g];
+    __syncthreads();
+    // ---- head g's online-softmax step in wave g % 4
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      if (g % 4 != wave) continue;
+      float v = xred[g * kDmaKeys + key_t];
+      for (int p = 1; p < 4; ++p) v += xred[(p * GB + g) * kDmaKeys + key_t];
+      v *= mul;
+      if (a.softcap > 0.0f) v = a.softcap * tanhf(fminf(fmaxf(v / a.softcap, -20.0f), 20.0f));
+      float mx = valid ? v : -INFINITY;
+      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float m_new = fmaxf(m_run[g], mx);
+      const float kp = m_new == -INFINITY ? 1.0f : expf(m_run[g] - m_new);
+      const float p = (valid && m_new > -INFINITY) ? expf(v - m_new) : 0.0f;
+      ps[g * kDmaKeys + key_t] = p;
+      float ls = p;
+      for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off);
+      if (key_t == 0) {
+        red[g] = kp;
+        red[GB + g] = l_run[g] * kp + ls;
+        red[2 * GB + g] = m_new;
+      }
+    }
+    attn_vmwait<0>();  // V landed
+    __syncthreads();   // publishes ps, the running state and every wave's V pieces
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      keep[g] = red[g];
+      l_run[g] = red[GB + g];
+      m_run[g] = red[2 * GB + g];
+      acc[g].x *= keep[g];
+      acc[g].y *= keep[g];
+      acc[g].z *= keep[g];
+      acc[g].w *= keep[g];
+    }
+    // ---- values: key lane kk takes keys kk, kk + 8, ..., in key order
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int key = kk + u * 8;
+      if (key < nk) {
+        const float4 v = *reinterpret_cast<const float4 *>(vls + key * kDmaDim + c4 * 4);
+#pragma unroll
+        for (int g = 0; g < GB; ++g) {
+          const float w = ps[g * kDmaKeys + key];
+          acc[g].x += w * v.x;
+          acc[g].y += w * v.y;
+          acc[g].z += w * v.z;
+          acc[g].w += w * v.w;
+        }
+      }
+    }
+    __syncthreads();  // xred is rewritten below
+  }
+  // ---- the 8 key lanes: two per wave meet by a lane shuffle, then the four waves in LDS
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    acc[g].x += __shfl_down(acc[g].x, 32);
+    acc[g].y += __shfl_down(acc[g].y, 32);
+    acc[g].z += __shfl_down(acc[g].z, 32);
+    acc[g].w += __shfl_down(acc[g].w, 32);
+  }
+  if (wave > 0 && lane < 32)
+#pragma unroll
+    for (int g = 0; g < GB; ++g)
+      *reinterpret_cast<float4 *>(xred + (size_t(wave - 1) * GB + g) * kDmaDim + c4 * 4) = acc[g];
+  __syncthreads();
+  if (tid >= 32) return;
+#pragma unroll
+  for (int g = 0; g < GB; ++g)
+    for (int l = 0; l < 3; ++l) {
+      const float4 o = *reinterpret_cast<const float4 *>(xred + (size_t(l) * GB + g) * kDmaDim + c4 * 4);
+      acc[g].x += o.x;
+      acc[g].y += o.y;
+      acc[g].z += o.z;
+      acc[g].w += o.w;
+    }
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    const size_t row_head = size_t(r) * a.heads + h0 + g;
+    float4 o = acc[g];
+    if (a.splits == 1) {
+      const float l = l_run[g];
+      o = make_float4(o.x / l, o.y / l, o.z / l, o.w / l);
+      *reinterpret_cast<float4 *>(out + row_head * kDmaDim + c4 * 4) = o;
+    } else {
+      *reinterpret_cast<float4 *>(opart + (size_t(s) * a.rows * a.heads + row_head) * kDmaDim + c4 * 4) = o;
+    }
+    if (a.splits > 1 && tid == 0) {
+      float *ml = mlpart + (size_t(s) * a.rows * a.heads + row_head) * 2;
+      ml[0] = m_run[g];
+      ml[1] = l_run[g];
+    }
+  }
+}
+
 // Merge the key chunks: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
 // One workgroup per (row, head).  Thread t owns float4 channel group t % G
 // (G = dim / 4 groups, dim % 4 == 0) and every (256 / G)-th chunk from t / G;
@@ -997,8 +1219,36 @@ void attn_launch(const float *q, const float *cache, float *out, float *ws, cons
                                size_t(a.kl > 1 ? a.kl : 0) * p.gb * dim);
   const size_t lds = (size_t(p.gb) * dim + size_t(p.gb) * kAttnSub + p.gb * 4 + xred) * 4;
   dim3 grid(kv_heads * a.gpk, rows, p.splits);
+  // The LDS-stream kernel: dim 128, 64-key chunks, every chunk start a multiple
+  // of 4 keys (16-byte K^T pieces), and a capacity of whole 16-byte rows.
+  bool dma = tuning().attn_dma != 0 && dim == kDmaDim && p.chunk == kDmaKeys && cap % 4 == 0 && a.kl == 8 &&
+             a.lpk == 32 && a.parts == 4;
+  for (int r = 0; dma && r < rows; ++r) {
+    const int e = position + r + 1;
+    dma = (window > 0 && e > window ? e - window : 0) % 4 == 0;
+  }
+  if (dma) {
+    static bool attr[9] = {};
+    const size_t dl = attn_dma_lds(p.gb);
+    auto go = [&](auto kern) {
+      if (!attr[p.gb]) {
+        hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      int(dl)),
+                  "attention LDS size");
+        attr[p.gb] = true;
+      }
+      kern<<<grid, kAttnThreads, dl, s>>>(q, cache, out, opart, ml, a);
+    };
+    switch (p.gb) {
+      case 8: go(k_attn_dma<8>); break;
+      case 4: go(k_attn_dma<4>); break;
+      case 2: go(k_attn_dma<2>); break;
+      default: go(k_attn_dma<1>); break;
+    }
+  }
 #define QNN_ATTN(G, N) k_attn<G, N><<<grid, kAttnThreads, lds, s>>>(q, cache, out, opart, ml, a)
-  if (a.nd4 == 1) {
+  if (dma) {
+  } else if (a.nd4 == 1) {
     switch (p.gb) {
       case 8: QNN_ATTN(8, 1); break;
       case 4: QNN_ATTN(4, 1); break;

@@ -44,6 +44,7 @@ struct Tuning {
   int gemm_h16 = 128;        // QNN_GEMM_H16: rows from which the GEMM runs over a pre-expanded fp16 copy (0: never)
   int attn_wgs = 512;        // QNN_ATTN_WGS: cached-attention workgroup target
   int attn_min_chunk = 64;   // QNN_ATTN_MIN_CHUNK: keys per chunk, at least
+  int attn_dma = 1;          // QNN_ATTN_DMA: 64-key chunks at dim 128 streamed into LDS
   int gemm_nw = 0;           // QNN_GEMM_NW: waves per Q8_0 GEMM workgroup (4 or 8)
   int gemm_mb = 0;           // QNN_GEMM_MB: 32-row blocks per GEMM wave (1 or 2)
   int gg_bw = 0;             // QNN_GG_BW: GGUF units per wave (1 or 2)

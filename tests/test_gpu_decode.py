@@ -120,11 +120,16 @@ ATTN = [
     (1, 16, 2, 1152, 300, 290, 0, 0.0, 0.0, False),       # 8 heads per workgroup, two float4 groups per lane
     (2, 8, 4, 66, 200, 150, 0, 0.0, 0.0, False),          # dim not a multiple of 4
     (2, 8, 2, 128, 3000, 2500, 1000, 30.0, 0.0, True),    # window and mask together
+    (1, 32, 8, 128, 5000, 4999, 4096, 0.0, 0.0, False),   # window, 64-key chunks from key 904
+    (1, 32, 8, 128, 8192, 2047, 0, 20.0, 0.125, False),   # softcap and scale on 64-key chunks
 ]
 
 
 @pytest.mark.parametrize("case", ATTN, ids=[f"r{c[0]}h{c[1]}k{c[2]}d{c[3]}p{c[5]}w{c[6]}m{int(c[9])}" for c in ATTN])
-def test_cached_attention_matches_oracle(ctx, rng, case):
+def test_cached_attention_matches_oracle(ctx, rng, tune, case):
+    """Against the oracle within 1e-4 per head row.  At dim 128 with 64-key chunks whose starts are
+    multiples of 4 the call takes the kernel that streams each chunk into LDS; it must give the same
+    bits as the general kernel (QNN_ATTN_DMA=0), which every other shape takes."""
     rows, heads, kvh, dim, cap, pos, window, softcap, scale, masked = case
     n = pos + rows
     size = 2 * cap * kvh * dim + (rows * cap if masked else 0)
@@ -144,6 +149,10 @@ def test_cached_attention_matches_oracle(ctx, rng, case):
     w = want.reshape(rows * heads, dim)
     for i in range(rows * heads):
         assert normwise_rel_err(got[i], w[i]) <= 1e-4, i
+    tune("QNN_ATTN_DMA", "0")
+    ctx.CachedAttention(to, tq, tc, rows, cap, heads, kvh, dim, pos, window, softcap, scale, masked)
+    general = ctx.Download(to).reshape(rows * heads, dim)
+    assert np.array_equal(got.view(np.uint32), general.view(np.uint32))
     for z in (tq, tc, to):
         ctx.Recycle(z)
 
