@@ -932,24 +932,34 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
 // Rows at which the MFMA GEMM replaces per-row matvecs (one weight pass per row).
 int q8_gemm_min_rows() { return std::max(2, tuning().q8_gemm_min_rows); }
 
-// The fp16 copy of a resident Q8_0 weight for the GEMM (k_h16_gemm), found or
+// The fp16 copy of a resident GGUF weight for the GEMM (k_h16_gemm), found or
 // made on the device: a cache entry of its own (key + "/h16"), evicted like
-// any other (its eviction is not reported).  Null under graph capture when
-// it does not exist yet (making it allocates).
-WeightEntry *q8_h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
+// any other (its eviction is not reported).  A Q8_0 copy scales by the
+// weight's own row exponents; a copy of any other encoding carries its row
+// exponents after the values.  Null under graph capture when it does not
+// exist yet (making it allocates).
+WeightEntry *h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
   const std::string key = w->key + "/h16";
   if (WeightEntry *h = lookup(ctx, key)) return h;
   if (ctx->capturing) return nullptr;
+  const bool own_exp = w->gg.enc != QNN_WE_Q8_0;
+  const size_t vbytes = q8_h16_bytes(w->gg.rows, w->gg.cols);
   auto *e = new WeightEntry();
   e->key = key;
   e->identity = w->identity;
   e->kind = WKind::Raw;
   e->derived = true;
-  e->bytes = q8_h16_bytes(w->gg.rows, w->gg.cols);
+  e->bytes = vbytes + (own_exp ? (size_t(w->gg.rows) * 4 + 255) / 256 * 256 : 0);
   e->source_bytes = 0;
   try {
     e->dptr = alloc_weight(ctx, e->bytes);
-    q8_expand_h16_launch(w->gg, w->dptr, e->dptr, ctx->stream);
+    if (own_exp) {
+      int *ew = reinterpret_cast<int *>(static_cast<uint8_t *>(e->dptr) + vbytes);
+      gguf_rowexp_launch(w->gg, w->dptr, ew, w->gg.rows, ctx->stream);
+      gguf_expand_h16_launch(w->gg, w->dptr, ew, e->dptr, ctx->stream);
+    } else {
+      q8_expand_h16_launch(w->gg, w->dptr, e->dptr, ctx->stream);
+    }
   } catch (...) {
     if (e->dptr) (void)hipFree(e->dptr);
     delete e;
@@ -958,32 +968,43 @@ WeightEntry *q8_h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
   return insert(ctx, e);
 }
 
-void run_q8_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
+// Multi-row GGUF projection.  From QNN_GEMM_H16 rows: k_h16_gemm over the
+// weight's fp16 copy (any encoding); otherwise, and under capture while no
+// copy exists, a Q8_0 weight from q8_gemm_min_rows rows takes k_q8_gemm,
+// which decodes its tiles.  False when neither applies: the caller then runs
+// one matvec per row.
+bool run_gguf_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
+  const bool q8 = w->gg.enc == QNN_WE_Q8_0;
   if (tuning().gemm_h16 > 0 && rows >= tuning().gemm_h16) {
     w->op_pins++;  // making the copy may evict: not the weight it is made from
     WeightEntry *h = nullptr;
     try {
-      h = q8_h16_entry(ctx, w);
+      h = h16_entry(ctx, w);
     } catch (...) {
       w->op_pins--;
       throw;
     }
     w->op_pins--;
     if (h) {
+      const int *ew = q8 ? reinterpret_cast<const int *>(static_cast<const uint8_t *>(w->dptr) + w->gg.rowexp_off)
+                         : reinterpret_cast<const int *>(static_cast<const uint8_t *>(h->dptr) +
+                                                         q8_h16_bytes(w->gg.rows, w->gg.cols));
       const Q8GemmPlan p = q8_h16_plan(rows, in_dim, out_dim);
       const size_t frag_off = 0, exp_off = (p.frag_bytes + 255) & ~size_t(255);
       uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, exp_off + p.exp_bytes));
-      q8_h16_gemm_launch(p, x, rows, in_dim, out_dim, w->gg, w->dptr, h->dptr, ws + frag_off,
+      q8_h16_gemm_launch(p, x, rows, in_dim, out_dim, ew, h->dptr, ws + frag_off,
                          reinterpret_cast<int *>(ws + exp_off), y, ctx->stream);
       ctx->st.gemm_h16++;
-      return;
+      return true;
     }
   }
+  if (!q8 || rows < q8_gemm_min_rows()) return false;
   const Q8GemmPlan p = q8_gemm_plan(rows, in_dim, out_dim);
   const size_t frag_off = 0, exp_off = (p.frag_bytes + 255) & ~size_t(255);
   uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, exp_off + p.exp_bytes));
   q8_gemm_launch(p, x, rows, in_dim, out_dim, w->gg, w->dptr, ws + frag_off, reinterpret_cast<int *>(ws + exp_off), y,
                  ctx->stream);
+  return true;
 }
 
 // ---------------------------------------------------------------- GGUF projection
@@ -1579,13 +1600,11 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
         record_linear(ctx, e, src->ptr, dst->ptr, out_dim);
       } else {
         settle_pending(ctx);
-        if (w->encoding != QNN_WE_Q8_0 || rows < q8_gemm_min_rows()) {
-          // Matvec per row (op 65); rows > 1 of K-quants reuse it row by row.
+        if (rows < 2 || !run_gguf_gemm(ctx, e, src->ptr, dst->ptr, rows, in_dim, out_dim)) {
+          // Matvec per row (op 65).
           for (int r = 0; r < rows; ++r)
             run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim,
                      out_dim);
-        } else {
-          run_q8_gemm(ctx, e, src->ptr, dst->ptr, rows, in_dim, out_dim);
         }
         if (has_bias) {
           WeightEntry *b = pin(acquire_raw(ctx, bias, out_dim));

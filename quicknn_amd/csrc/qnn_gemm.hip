@@ -44,20 +44,6 @@ __device__ __forceinline__ float half_bits_to_f(uint32_t h) {
   __builtin_memcpy(&f, &b, 2);
   return float(f);
 }
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {  // two RNE fp16 in one dword
-  const _Float16 x = _Float16(a), y = _Float16(b);
-  uint16_t u, v;
-  __builtin_memcpy(&u, &x, 2);
-  __builtin_memcpy(&v, &y, 2);
-  return uint32_t(u) | (uint32_t(v) << 16);
-}
-// Exponent e with |v| * 2^-e in (2^13, 2^14] (0 for zero or non-finite v).
-__device__ __forceinline__ int range_exp(float amax) {
-  if (!(amax > 0.0f) || !isfinite(amax)) return 0;
-  int ex;
-  (void)frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
-  return ex - 14;
-}
 
 // ---- activation preparation ------------------------------------------------
 // One launch: workgroup b owns rows 4b .. 4b + 3 of A (m_pad rows in all),
@@ -589,14 +575,14 @@ Q8GemmPlan q8_h16_plan(int M, int K, int N) {
   return p;
 }
 
-void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
-                        const void *w16, void *frag, int *ea, float *c, hipStream_t s) {
+void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const int *ew, const void *w16,
+                        void *frag, int *ea, float *c, hipStream_t s) {
   hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad / 4), dim3(1024), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
   H16Args g;
   g.afrag = static_cast<const uint4 *>(frag);
   g.ea = ea;
   g.wfrag = static_cast<const uint4 *>(w16);
-  g.ew = reinterpret_cast<const int *>(static_cast<const uint8_t *>(w) + l.rowexp_off);
+  g.ew = ew;
   g.c = c;
   g.M = M;
   g.N = N;

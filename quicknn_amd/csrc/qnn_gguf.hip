@@ -387,6 +387,48 @@ __global__ void k_gguf_dequant(GGLayout l, const uint8_t *__restrict__ w, float 
   out[idx] = gguf_value_tiled(l.enc, l, p, row / 64, k / 256, row & 63, k % 256);
 }
 
+// fp16 copy for the multi-row GEMM (k_h16_gemm).  Row exponents: one
+// workgroup per row of the copy, the largest |GGUFValue| of the row (rows past
+// the weight give 0).
+__global__ __launch_bounds__(256) void k_gguf_rowexp(GGLayout l, const uint8_t *__restrict__ w, int *__restrict__ ew) {
+  __shared__ float red[4];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  float amax = 0.0f;
+  if (row < l.rows) {
+    const Planes p = planes_of(l, w);
+    for (int k = tid; k < l.cols; k += 256)
+      amax = fmaxf(amax, fabsf(gguf_value_tiled(l.enc, l, p, row / 64, k / 256, row & 63, k % 256)));
+  }
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  if (tid == 0) ew[row] = range_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+// The values: piece (n32, ks, lane) = 8 halfs RNE(W[n][k] * 2^-ew[n]) for
+// n = n32*32 + lane % 32, k = ks*16 + 8*(lane / 32) + 0..7 (the B operand
+// fragments of v_mfma_f32_32x32x16_f16); rows past N and columns past K are
+// zero.
+__global__ __launch_bounds__(256) void k_gguf_expand_h16(GGLayout l, const uint8_t *__restrict__ w,
+                                                         const int *__restrict__ ew, int ksteps, size_t pieces,
+                                                         uint4 *__restrict__ out) {
+  const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= pieces) return;
+  const int lane = int(idx & 63);
+  const size_t nk = idx >> 6;
+  const int ks = int(nk % ksteps), n32 = int(nk / ksteps);
+  const int n = n32 * 32 + (lane & 31), k0 = ks * 16 + 8 * (lane >> 5);
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (n < l.rows && k0 < l.cols) {  // cols is a multiple of 32: all 8 columns are in the row
+    const Planes p = planes_of(l, w);
+    const float sc = ldexpf(1.0f, -ew[n]);
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = gguf_value_tiled(l.enc, l, p, n / 64, (k0 + i) / 256, n & 63, (k0 + i) % 256) * sc;
+    v = make_uint4(pack_h2(f[0], f[1]), pack_h2(f[2], f[3]), pack_h2(f[4], f[5]), pack_h2(f[6], f[7]));
+  }
+  out[idx] = v;
+}
+
 // Gather (Context.Implementation.inc:1228-1267, tensor.comp:245-251 with a
 // GGUF weight): out[r][k] = value of row ids[r] (raw token bits) column k, or 0
 // for ids at or past the vocabulary.
@@ -1101,6 +1143,19 @@ void gguf_gather_launch(const GGLayout &l, const void *w, const float *ids, floa
   hipLaunchKernelGGL(k_gguf_gather, dim3((total + 255) / 256), dim3(256), 0, s, l, static_cast<const uint8_t *>(w),
                      reinterpret_cast<const unsigned *>(ids), out, rows, vocab);
   hip_check(hipGetLastError(), "gguf gather launch");
+}
+
+void gguf_rowexp_launch(const GGLayout &l, const void *w, int *ew, int rows_pad, hipStream_t s) {
+  hipLaunchKernelGGL(k_gguf_rowexp, dim3(rows_pad), dim3(256), 0, s, l, static_cast<const uint8_t *>(w), ew);
+  hip_check(hipGetLastError(), "gguf row exponents");
+}
+
+void gguf_expand_h16_launch(const GGLayout &l, const void *w, const int *ew, void *out, hipStream_t s) {
+  const int ksteps = (l.cols + 63) / 64 * 4;
+  const size_t pieces = q8_h16_bytes(l.rows, l.cols) / 16;
+  hipLaunchKernelGGL(k_gguf_expand_h16, dim3((pieces + 255) / 256), dim3(256), 0, s, l,
+                     static_cast<const uint8_t *>(w), ew, ksteps, pieces, static_cast<uint4 *>(out));
+  hip_check(hipGetLastError(), "gguf fp16 expansion");
 }
 
 void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices) {

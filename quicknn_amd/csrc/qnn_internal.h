@@ -85,6 +85,22 @@ struct I4Layout {
   __host__ __device__ size_t bytes() const { return nib_bytes() + scale_bytes(); }
 };
 
+// fp16 operands of the GEMMs: exponent e with |v| * 2^-e in (2^13, 2^14] (0
+// for zero or non-finite v), and two round-to-nearest-even fp16 in a dword.
+__device__ __forceinline__ int range_exp(float amax) {
+  if (!(amax > 0.0f) || !isfinite(amax)) return 0;
+  int ex;
+  (void)frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+  return ex - 14;
+}
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  const _Float16 x = _Float16(a), y = _Float16(b);
+  uint16_t u, v;
+  __builtin_memcpy(&u, &x, 2);
+  __builtin_memcpy(&v, &y, 2);
+  return uint32_t(u) | (uint32_t(v) << 16);
+}
+
 // GGUF tiled layout (qnn_gguf.hip): tiles of 64 rows, 256-element units,
 // a 16-byte-aligned main plane plus up to two small side planes.
 struct GGLayout {
@@ -304,11 +320,18 @@ void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
 // The same product over a pre-expanded fp16 copy of the weight (qnn_gemm.hip,
 // k_h16_gemm): q8_h16_bytes of device memory per weight, made once by
 // q8_expand_h16_launch; the results equal q8_gemm_launch's bit for bit.
+// `ew` is the weight's row exponents (a Q8_0 weight's own, at rowexp_off).
 size_t q8_h16_bytes(int rows, int cols);
 void q8_expand_h16_launch(const GGLayout &l, const void *w, void *out, hipStream_t s);
 Q8GemmPlan q8_h16_plan(int M, int K, int N);
-void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const GGLayout &l, const void *w,
-                        const void *w16, void *frag, int *ea, float *c, hipStream_t s);
+void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const int *ew, const void *w16,
+                        void *frag, int *ea, float *c, hipStream_t s);
+// The fp16 copy of a weight of any other GGUF encoding (qnn_gguf.hip): its
+// row exponents (range_exp of the row's largest |value|, one int per row of
+// the copy's q8_h16_bytes rows), then the values RNE(v * 2^-e) in
+// k_h16_gemm's fragment order.
+void gguf_rowexp_launch(const GGLayout &l, const void *w, int *ew, int rows_pad, hipStream_t s);
+void gguf_expand_h16_launch(const GGLayout &l, const void *w, const int *ew, void *out, hipStream_t s);
 // Multi-row Q8_0 projection with activations quantised per 32-element block to
 // int8, on the int8 matrix cores (qnn_gemm_i8.hip).  K % 32 == 0.
 size_t q8_i8_workspace(int M, int K);

@@ -1,4 +1,5 @@
-"""GPU parity of the multi-row Q8_0 projection (prefill GEMM on fp16 MFMA).
+"""GPU parity of the multi-row GGUF projection (prefill GEMM on fp16 MFMA): Q8_0, and every
+other encoding over the weight's fp16 copy.
 
 TQNNGPUContext.Linear with Rows > 1 on a Q8_0 weight (Context.Implementation.inc:852-883,
 gemm.comp) must match the reference CPU paths within a normwise relative error of 1e-3
@@ -11,7 +12,8 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import ENC_Q8_0
+from oracle import (ENC_IQ2_S, ENC_IQ2_XXS, ENC_IQ3_S, ENC_IQ3_XXS, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_Q2_K, ENC_Q3_K,
+                    ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q8_0)
 from quicknn_amd import hip
 from tests.conftest import normwise_rel_err
 
@@ -23,10 +25,10 @@ def q8(rng, n, k, scale=0.02):
     return hip.gguf_quantize(ENC_Q8_0, (rng.standard_normal((n, k)) * scale).astype(np.float32))
 
 
-def run_linear(ctx, w, a, n, bias=None):
+def run_linear(ctx, w, a, n, bias=None, enc=ENC_Q8_0):
     m, k = a.shape
     src, dst = ctx.UploadRaw(a), ctx.NewTensor(m * n)
-    ctx.Linear(dst, src, hip.MemoryBlock.gguf(w, n, k, ENC_Q8_0), None,
+    ctx.Linear(dst, src, hip.MemoryBlock.gguf(w, n, k, enc), None,
                None if bias is None else hip.MemoryBlock.vector(bias), m, k, n)
     out = ctx.Download(dst).reshape(m, n)
     ctx.Recycle(src)
@@ -129,6 +131,51 @@ def test_small_rows_use_matvec_and_agree(ctx, rng):
     two = run_linear(ctx, w, a[:2], n)     # matvec per row
     for r in range(2):
         assert normwise_rel_err(full[r], two[r]) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# The other encodings (Context.Implementation.inc:852-883: gemm.comp decodes any
+# of them through readGGUF).  From QNN_GEMM_H16 rows (default 128) the product
+# runs over the weight's fp16 copy, whose values are RNE(W * 2^-e) with e from
+# the row's largest |value| (k_gguf_rowexp, k_gguf_expand_h16), then k_h16_gemm;
+# fewer rows run one matvec per row.  Both within 1e-3 of the CPU paths.
+# ---------------------------------------------------------------------------
+GEMM_FMTS = [ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_IQ2_XXS, ENC_IQ2_S,
+             ENC_IQ3_XXS, ENC_IQ3_S]
+
+
+@pytest.mark.parametrize("enc", GEMM_FMTS)
+@pytest.mark.parametrize("m,k,n", [(128, 1024, 300), (200, 768, 97)])
+def test_other_encodings_fp16_copy_gemm(ctx, rng, tune, enc, m, k, n):
+    w = hip.gguf_quantize(enc, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    h0 = ctx.status().gemm_h16
+    got = run_linear(ctx, w, a, n, enc=enc)
+    again = run_linear(ctx, w, a, n, enc=enc)  # the cached copy
+    assert ctx.status().gemm_h16 - h0 == 2
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+    for r in (0, m // 2, m - 1):
+        assert normwise_rel_err(got[r], oracle.cpu_linear(w, enc, a[r], k, n)) <= TOL, r
+    want = oracle.gguf_gemm_scalar(w, enc, a, n, row_begin=m - 2, row_end=m)
+    for r in (m - 2, m - 1):
+        assert normwise_rel_err(got[r], want[r]) <= TOL, r
+    tune("QNN_GEMM_H16", "0")
+    per_row = run_linear(ctx, w, a, n, enc=enc)
+    assert ctx.status().gemm_h16 - h0 == 2
+    for r in range(0, m, 37):
+        assert normwise_rel_err(got[r], per_row[r]) <= TOL, r
+
+
+def test_other_encoding_prefill_shape(ctx, rng):
+    """The Gemma-2-9B q projection (Q4_K 4096 x 3584) over a 512-token prefill, one GEMM."""
+    m, k, n = 512, 3584, 4096
+    w = hip.gguf_quantize(ENC_Q4_K, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    h0 = ctx.status().gemm_h16
+    got = run_linear(ctx, w, a, n, enc=ENC_Q4_K)
+    assert ctx.status().gemm_h16 - h0 == 1
+    for r in (0, 1, 255, 256, 511):
+        assert normwise_rel_err(got[r], oracle.cpu_linear(w, ENC_Q4_K, a[r], k, n)) <= TOL, r
 
 
 # ---------------------------------------------------------------------------
