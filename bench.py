@@ -794,7 +794,8 @@ def run_cfg6(args, hip) -> dict:
         sample=sample, rope_us=round(rope_us, 2), setup_s=round(gen_s, 1),
         roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                  "kernel": "k_attn + k_attn_merge (one qnn_cached_attention call)",
+                  "kernel": "k_attn_dma + k_attn_merge (one qnn_cached_attention call; 64-key chunks streamed "
+                            "into LDS; the 32768-key calls take k_attn)",
                   "kernel_us": round(us4k, 2), "bytes_per_launch": bytes4k,
                   "timing": f"HIP events around {args.steps}x{LAYERS} calls"},
         cpu_baseline=cpu)
