@@ -93,12 +93,17 @@ def test_router_weight_feeds_vector_linear(ctx, tmp_path, rng, bf16):
 
 
 # GGML storage type of each encoding (GGUF.Quantization.pas:44-60).
-GGML_TYPE = {oracle.ENC_Q8_0: 8, oracle.ENC_Q4_K: 12, oracle.ENC_Q6_K: 14, oracle.ENC_Q3_K: 11, oracle.ENC_Q2_K: 10}
+GGML_TYPE = {oracle.ENC_Q8_0: 8, oracle.ENC_Q4_K: 12, oracle.ENC_Q6_K: 14, oracle.ENC_Q3_K: 11, oracle.ENC_Q2_K: 10,
+             oracle.ENC_Q5_K: 13, oracle.ENC_IQ4_NL: 20, oracle.ENC_IQ4_XS: 23, oracle.ENC_Q2_0: 42,
+             oracle.ENC_IQ2_XXS: 16, oracle.ENC_IQ2_S: 22, oracle.ENC_IQ3_XXS: 18, oracle.ENC_IQ3_S: 21}
 
 
 def test_gguf_file_feeds_linear(ctx, tmp_path, rng):
     shapes = {oracle.ENC_Q4_K: (512, 3584), oracle.ENC_Q6_K: (300, 3584), oracle.ENC_Q8_0: (256, 3072),
-              oracle.ENC_Q3_K: (128, 3584), oracle.ENC_Q2_K: (200, 14336)}
+              oracle.ENC_Q3_K: (128, 3584), oracle.ENC_Q2_K: (200, 14336), oracle.ENC_Q5_K: (96, 2048),
+              oracle.ENC_IQ4_NL: (70, 1056), oracle.ENC_IQ4_XS: (64, 2048), oracle.ENC_Q2_0: (33, 1088),
+              oracle.ENC_IQ2_XXS: (64, 1024), oracle.ENC_IQ2_S: (40, 768), oracle.ENC_IQ3_XXS: (80, 1024),
+              oracle.ENC_IQ3_S: (50, 1280)}
     blocks, tensors = {}, []
     for enc, (n, k) in shapes.items():
         blocks[enc] = hip.gguf_quantize(enc, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))

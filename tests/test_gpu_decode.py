@@ -271,7 +271,8 @@ def test_sampling_excluded_tokens_and_errors(ctx):
 
 
 # ---------------------------------------------------------------- gather
-@pytest.mark.parametrize("kind", ["f32", "bf16", "s8", "q4_k", "q6_k", "q8_0"])
+@pytest.mark.parametrize("kind", ["f32", "bf16", "s8", "q4_k", "q6_k", "q8_0", "q5_k", "iq4_xs", "q2_0", "iq2_xxs",
+                                  "iq3_s"])
 def test_gather_embedding_rows(ctx, rng, kind):
     """Gather: token rows of the table, bit-exact; ids at or past the vocabulary give zeros."""
     vocab, dim = 1000, 512
@@ -289,7 +290,8 @@ def test_gather_embedding_rows(ctx, rng, kind):
         scales = hip.MemoryBlock.vector(s)
         rows_f = q.astype(np.float32) * s[:, None]
     else:
-        enc = {"q4_k": hip.WE_Q4_K, "q6_k": hip.WE_Q6_K, "q8_0": hip.WE_Q8_0}[kind]
+        enc = {"q4_k": hip.WE_Q4_K, "q6_k": hip.WE_Q6_K, "q8_0": hip.WE_Q8_0, "q5_k": hip.WE_Q5_K,
+               "iq4_xs": hip.WE_IQ4_XS, "q2_0": hip.WE_Q2_0, "iq2_xxs": hip.WE_IQ2_XXS, "iq3_s": hip.WE_IQ3_S}[kind]
         blocks = hip.gguf_quantize(enc, table)
         w = hip.MemoryBlock.gguf(blocks, vocab, dim, enc)
         rows_f = oracle.gguf_dequant_scalar(blocks, enc, vocab * dim).reshape(vocab, dim)
