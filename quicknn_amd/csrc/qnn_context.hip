@@ -162,12 +162,14 @@ void reload_tuning() {
   t.fuse_moe = env_int("QNN_FUSE_MOE", t.fuse_moe);
   t.q8_gemm_min_rows = env_int("QNN_Q8_GEMM_MIN_ROWS", t.q8_gemm_min_rows);
   t.gemm_h16 = env_int("QNN_GEMM_H16", t.gemm_h16);
+  t.gguf_gemm_rows = env_int("QNN_GGUF_GEMM_ROWS", t.gguf_gemm_rows);
   t.attn_wgs = env_int("QNN_ATTN_WGS", t.attn_wgs);
   t.attn_min_chunk = env_int("QNN_ATTN_MIN_CHUNK", t.attn_min_chunk);
   t.attn_dma = env_int("QNN_ATTN_DMA", t.attn_dma);
   t.gemm_nw = env_int("QNN_GEMM_NW", t.gemm_nw);
   t.gemm_mb = env_int("QNN_GEMM_MB", t.gemm_mb);
   t.gg_bw = env_int("QNN_GG_BW", t.gg_bw);
+  t.gg_mt = env_int("QNN_GG_MT", t.gg_mt);
   t.i4_mfma = env_int("QNN_I4_MFMA", t.i4_mfma);
   t.i4_lanes = env_int("QNN_I4_LANES", t.i4_lanes);
   t.i4_tpw = env_int("QNN_I4_TPW", t.i4_tpw);
@@ -968,14 +970,18 @@ WeightEntry *h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
   return insert(ctx, e);
 }
 
-// Multi-row GGUF projection.  From QNN_GEMM_H16 rows: k_h16_gemm over the
-// weight's fp16 copy (any encoding); otherwise, and under capture while no
-// copy exists, a Q8_0 weight from q8_gemm_min_rows rows takes k_q8_gemm,
-// which decodes its tiles.  False when neither applies: the caller then runs
-// one matvec per row.
+// Multi-row GGUF projection.  From QNN_GEMM_H16 rows (Q8_0) or
+// QNN_GGUF_GEMM_ROWS rows (the other encodings): k_h16_gemm over the weight's
+// fp16 copy; otherwise, and under capture while no copy exists, a Q8_0 weight
+// from q8_gemm_min_rows rows takes k_q8_gemm, which decodes its tiles.  False
+// when neither applies: the caller then runs the matvec, up to kGGMaxTokens
+// rows per pass.  (Measured at 14336 x 3584, Q2_K / IQ2_XXS: the copy's GEMM
+// is faster from about 12 rows; at 4096 x 3584 Q4_K from about 24; at
+// 3584 x 14336 Q6_K, 19 column tiles only, from about 40.)
 bool run_gguf_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
   const bool q8 = w->gg.enc == QNN_WE_Q8_0;
-  if (tuning().gemm_h16 > 0 && rows >= tuning().gemm_h16) {
+  const int from = q8 ? tuning().gemm_h16 : tuning().gguf_gemm_rows;
+  if (from > 0 && rows >= from) {
     w->op_pins++;  // making the copy may evict: not the weight it is made from
     WeightEntry *h = nullptr;
     try {
@@ -1008,6 +1014,25 @@ bool run_gguf_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int
 }
 
 // ---------------------------------------------------------------- GGUF projection
+// nt (2..kGGMaxTokens) rows of x through one pass over the weight.
+void run_gguf_mt(qnn_ctx_s *ctx, const WeightEntry *w, const float *x, float *y, int nt, int out_dim) {
+  GGArgs a;
+  a.l = w->gg;
+  a.w = w->dptr;
+  a.x = x;
+  a.x_vec4 = (w->gg.cols % 4 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  a.y = y;
+  a.n = out_dim;
+  a.tiles = w->gg.tiles;
+  a.mode = GG_STORE;
+  const int slices = (w->gg.units + 3) / 4;  // one unit per wave, four per workgroup
+  ensure_splitk(ctx, slices > 1 ? size_t(a.tiles) * slices * 64 * kGGMaxTokens : 0, size_t(a.tiles) * kCounterStride);
+  a.partial = ctx->partial;
+  a.counters = ctx->counters;
+  a.err = ctx->error_flag;
+  gguf_matvec_mt_launch(a, slices, nt, ctx->stream);
+}
+
 void run_gguf(qnn_ctx_s *ctx, const WeightEntry *w, const WeightEntry *w2, int mode, const float *x, float *y,
               int out_dim, float *g_out, float *u_out) {
   GGArgs a;
@@ -1601,10 +1626,17 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
       } else {
         settle_pending(ctx);
         if (rows < 2 || !run_gguf_gemm(ctx, e, src->ptr, dst->ptr, rows, in_dim, out_dim)) {
-          // Matvec per row (op 65).
-          for (int r = 0; r < rows; ++r)
-            run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim,
-                     out_dim);
+          // The matvec (op 65): up to kGGMaxTokens rows per pass over the weight.
+          for (int r = 0; r < rows; r += kGGMaxTokens) {
+            const int nt = std::min(kGGMaxTokens, rows - r);
+            if (nt == 1 || tuning().gg_mt == 0) {
+              for (int t = r; t < r + nt; ++t)
+                run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(t) * in_dim, dst->ptr + size_t(t) * out_dim,
+                         out_dim);
+            } else {
+              run_gguf_mt(ctx, e, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim, nt, out_dim);
+            }
+          }
         }
         if (has_bias) {
           WeightEntry *b = pin(acquire_raw(ctx, bias, out_dim));

@@ -826,6 +826,71 @@ __device__ float unit_iq4_xs(const uint4 *mw, uint4 s1, const XSlice<NG> &xs, in
   return acc;
 }
 
+// Quantise one token's activation slice (U units, elements in natural order;
+// pieces past the nu units in the slice are zero) into `xs`: the INT4
+// kernels' fixed-point staging arithmetic (qnn_int4_dev.h), the 8 lanes of a
+// 32-group meeting through DPP.  XIT float4 per thread.
+template <int ENC, int U, int XIT>
+__device__ __forceinline__ void stage_slice(XSlice<U * 8> &xs, const float4 (&xr)[XIT], int nu, int tid, int lane) {
+#pragma unroll
+  for (int it = 0; it < XIT; ++it) {
+    const int e = (it * 256 + tid) * 4;
+    const float4 v = e < nu * 256 ? xr[it] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const dev::GroupScale gs =
+        dev::group_scale(dev::max_lanes8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)))));
+    uint32_t b1[4], b2[4];
+    dev::quant_elem(v.x, gs, b1[0], b2[0]);
+    dev::quant_elem(v.y, gs, b1[1], b2[1]);
+    dev::quant_elem(v.z, gs, b1[2], b2[2]);
+    dev::quant_elem(v.w, gs, b1[3], b2[3]);
+    uint32_t hw = dev::join2(dev::pack2(b1[0], b1[1]), dev::pack2(b1[2], b1[3]));
+    uint32_t lw = dev::join2(dev::pack2(b2[0], b2[1]), dev::pack2(b2[2], b2[3]));
+    if constexpr (ENC == QNN_WE_Q2_0) {  // 4x4 byte transpose over the quad of lanes holding a 16-element run
+      hw = quad_transpose(hw, lane & 3);
+      lw = quad_transpose(lw, lane & 3);
+    }
+    const int s16 = dev::sum_lanes4(dev::quant_sum<4>(b1, b2));  // 16-element sum
+    const int s32 = s16 + int(dev::dpp<0x141>(uint32_t(s16)));
+    if (e < U * 256) {
+      const int g = e >> 5, k = (e >> 2) & 7;
+      xs.h[g][k] = hw;
+      xs.l[g][k] = lw;
+      if ((lane & 3) == 0) xs.sum16[g][(lane >> 2) & 1] = s16;
+      if ((lane & 7) == 0) {
+        xs.s2[g] = gs.s1 * 0.00390625f;
+        xs.sum32[g] = s32;
+      }
+    }
+  }
+}
+
+// One unit's dot for format ENC (mw: main chunks; s1v, s1w, s2w: side fields;
+// iq: the LDS codebook and sign masks of the IQ2/IQ3 formats).
+template <int ENC, int NG>
+__device__ __forceinline__ float unit_dot(const uint4 *mw, uint4 s1v, uint32_t s1w, uint32_t s2w,
+                                          const XSlice<NG> &xs, int g0, const uint4 *iq) {
+  if constexpr (ENC == QNN_WE_Q8_0) return unit_q8_0<NG>(mw, s1v, xs, g0);
+  if constexpr (ENC == QNN_WE_Q4_K) return unit_q4_k<NG>(mw, xs, g0);
+  if constexpr (ENC == QNN_WE_Q6_K) return unit_q6_k<NG>(mw, s1w, xs, g0);
+  if constexpr (ENC == QNN_WE_Q3_K) return unit_q3_k<NG>(mw, s1v, s2w, xs, g0);
+  if constexpr (ENC == QNN_WE_Q2_K) return unit_q2_k<NG>(mw, s1w, xs, g0);
+  if constexpr (ENC == QNN_WE_Q5_K) return unit_q5_k<NG>(mw, xs, g0);
+  if constexpr (ENC == QNN_WE_IQ4_NL) return unit_iq4_nl<NG>(mw, s1v, xs, g0);
+  if constexpr (ENC == QNN_WE_IQ4_XS) return unit_iq4_xs<NG>(mw, s1v, xs, g0);
+  if constexpr (ENC == QNN_WE_Q2_0) return unit_q2_0<NG>(mw, s1v, xs, g0);
+  if constexpr (kIsIQ<ENC>) {
+    constexpr int kGridU4 = kIQGridBytes<ENC> / 16;
+    const uint64_t *mask = reinterpret_cast<const uint64_t *>(iq + kGridU4);
+    const uint64_t *g64 = reinterpret_cast<const uint64_t *>(iq);
+    const uint32_t *g32 = reinterpret_cast<const uint32_t *>(iq);
+    if constexpr (ENC == QNN_WE_IQ2_XXS) return unit_iq2_xxs<NG>(mw, s1w, xs, g0, g64, mask);
+    if constexpr (ENC == QNN_WE_IQ2_S) return unit_iq2_s<NG>(mw, s1w, xs, g0, g64, mask);
+    if constexpr (ENC == QNN_WE_IQ3_XXS) return unit_iq3_xxs<NG>(mw, s1w, xs, g0, g32, mask);
+    if constexpr (ENC == QNN_WE_IQ3_S) return unit_iq3_s<NG>(mw, s1v, s2w, xs, g0, g32, mask);
+  }
+  return 0.0f;
+}
+
 // Workgroup = 4 waves on one 64-row tile (SWIGLU: 32 gate rows in lanes
 // 0-31, the same 32 up rows in lanes 32-63); slice = 4*BW units, wave w
 // streams units [w*BW, (w+1)*BW) of it.
@@ -929,38 +994,7 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
     for (int it = 0; it < kTabIt; ++it)
       if (it * 256 + tid < kTabU4) iq_tab[it * 256 + tid] = tr[it];
   }
-#pragma unroll
-  for (int it = 0; it < XIT; ++it) {
-    const int e = (it * 256 + tid) * 4;
-    const float4 v = e < nu * 256 ? xr[it] : make_float4(0.f, 0.f, 0.f, 0.f);
-    // the INT4 kernels' fixed-point staging arithmetic (qnn_int4_dev.h); the
-    // 8 lanes of a 32-group meet through DPP
-    const dev::GroupScale gs =
-        dev::group_scale(dev::max_lanes8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)))));
-    uint32_t b1[4], b2[4];
-    dev::quant_elem(v.x, gs, b1[0], b2[0]);
-    dev::quant_elem(v.y, gs, b1[1], b2[1]);
-    dev::quant_elem(v.z, gs, b1[2], b2[2]);
-    dev::quant_elem(v.w, gs, b1[3], b2[3]);
-    uint32_t hw = dev::join2(dev::pack2(b1[0], b1[1]), dev::pack2(b1[2], b1[3]));
-    uint32_t lw = dev::join2(dev::pack2(b2[0], b2[1]), dev::pack2(b2[2], b2[3]));
-    if constexpr (ENC == QNN_WE_Q2_0) {  // 4x4 byte transpose over the quad of lanes holding a 16-element run
-      hw = quad_transpose(hw, lane & 3);
-      lw = quad_transpose(lw, lane & 3);
-    }
-    const int s16 = dev::sum_lanes4(dev::quant_sum<4>(b1, b2));  // 16-element sum
-    const int s32 = s16 + int(dev::dpp<0x141>(uint32_t(s16)));
-    if (e < U * 256) {
-      const int g = e >> 5, k = (e >> 2) & 7;
-      xs.h[g][k] = hw;
-      xs.l[g][k] = lw;
-      if ((lane & 3) == 0) xs.sum16[g][(lane >> 2) & 1] = s16;
-      if ((lane & 7) == 0) {
-        xs.s2[g] = gs.s1 * 0.00390625f;
-        xs.sum32[g] = s32;
-      }
-    }
-  }
+  stage_slice<ENC, U>(xs, xr, nu, tid, lane);
   __syncthreads();
 
   // 4) unit dots
@@ -1033,6 +1067,116 @@ template <int ENC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gguf_matvec_iq(const GGGroup grp) {
   gguf_item<ENC, 1>(grp, group_member(grp));
 }
+// Up to MT tokens (rows of x, `ntok` valid, the rest zero) in one pass over
+// the weights: the per-token Linear of 2 to 127 rows, MT at a time.  The
+// workgroup and plan are the one-token kernel's at one unit per wave; each
+// token has its own activation slice in LDS, the wave's unit is loaded once
+// and dotted with every slice, and the split-K exchange carries MT partial
+// sums per row.  Per token the arithmetic is the one-token kernel's.
+template <int ENC, int MT>
+__global__ __launch_bounds__(256) void k_gguf_matvec_mt(const GGArgs a, int slices, int ntok) {
+  using F = Fmt<ENC>;
+  constexpr int U = 4, NG = U * 8;
+  int tile, slice;
+  if (!map_tile_slice(int(blockIdx.x), slices, a.tiles, tile, slice)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const GGLayout &l = a.l;
+  const int u0 = slice * U, nu = min(U, l.units - u0);
+  const bool on = wave < nu;
+
+  // 1) the tokens' activation slices (buffer loads past the last token read 0)
+  float4 xr[MT][1];
+  const dev::Rsrc xsrc = dev::rsrc(a.x, size_t(ntok) * l.cols * 4);
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const uint32_t kb = uint32_t(size_t(m) * l.cols * 4 + size_t(u0 * 256 + tid * 4) * 4);
+    if (a.x_vec4) {
+      const uint4 v = dev::ld128(xsrc, kb, 0);
+      xr[m][0] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    } else {
+      xr[m][0] = make_float4(dev::ld32f(xsrc, kb, 0), dev::ld32f(xsrc, kb + 4, 0), dev::ld32f(xsrc, kb + 8, 0),
+                             dev::ld32f(xsrc, kb + 12, 0));
+    }
+  }
+  // 1b) IQ2/IQ3: the codebook and the sign masks, for LDS
+  constexpr int kGridU4 = kIQGridBytes<ENC> / 16;
+  constexpr int kTabU4 = kIsIQ<ENC> ? kGridU4 + kIQMaskU4<ENC> : 0;
+  constexpr int kTabIt = (kTabU4 + 255) / 256;
+  uint4 tr[kTabIt > 0 ? kTabIt : 1];
+  if constexpr (kIsIQ<ENC>) {
+    const uint4 *masks = iq_mask_src<ENC>();
+#pragma unroll
+    for (int it = 0; it < kTabIt; ++it) {
+      const int t = it * 256 + tid;
+      tr[it] = t < kGridU4 ? iq_grid_src<ENC>()[t] : masks[min(t - kGridU4, kIQMaskU4<ENC> - 1)];
+    }
+  }
+  // 2) this wave's unit (past the slice's units: its last unit, unused)
+  const Planes P = planes_of(l, a.w);
+  uint4 mw[F::C];
+  uint4 s1v = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t s1w = 0, s2w = 0;
+  {
+    const size_t tu = size_t(tile) * l.units + (u0 + min(wave, nu - 1));
+    const uint4 *mp = reinterpret_cast<const uint4 *>(P.main) + (tu * F::C) * 64 + lane;
+#pragma unroll
+    for (int c = 0; c < F::C; ++c) mw[c] = wload(mp + c * 64);
+    if (F::S1 == 16) s1v = wload(reinterpret_cast<const uint4 *>(P.side1) + tu * 64 + lane);
+    if (F::S1 == 8) {
+      const uint32_t *q = reinterpret_cast<const uint32_t *>(P.side1) + (tu * 64 + lane) * 2;
+      s1v = make_uint4(wload(q), wload(q + 1), 0u, 0u);
+    }
+    if (F::S1 == 12) {
+      const uint32_t *q = reinterpret_cast<const uint32_t *>(P.side1 + (tu * 64 + lane) * 12);
+      s1v = make_uint4(wload(q), wload(q + 1), wload(q + 2), 0u);
+    }
+    if (F::S1 == 4) s1w = wload(reinterpret_cast<const uint32_t *>(P.side1) + tu * 64 + lane);
+    if (F::S1 == 2) s1w = wload(reinterpret_cast<const uint16_t *>(P.side1) + tu * 64 + lane);
+    if (F::S2 == 2) s2w = wload(reinterpret_cast<const uint16_t *>(P.side2) + tu * 64 + lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3) the slices into LDS
+  __shared__ XSlice<NG> xs[MT];
+  __shared__ float red[4][MT][64];
+  __shared__ uint4 iq_tab[kTabU4 > 0 ? kTabU4 : 1];
+  if constexpr (kIsIQ<ENC>) {
+#pragma unroll
+    for (int it = 0; it < kTabIt; ++it)
+      if (it * 256 + tid < kTabU4) iq_tab[it * 256 + tid] = tr[it];
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) stage_slice<ENC, U>(xs[m], xr[m], nu, tid, lane);
+  __syncthreads();
+  // 4) the unit against every valid token, one token at a time (the loop is
+  //    kept rolled: unrolled, the compiler holds every token's unpacked
+  //    weights at once, 256 VGPRs and one wave per SIMD)
+#pragma unroll 1
+  for (int m = 0; m < ntok; ++m)
+    red[wave][m][lane] = on ? unit_dot<ENC, NG>(mw, s1v, s1w, s2w, xs[m], wave * 8, iq_tab) : 0.0f;
+  // 5) the 4 waves (fixed order), then split-K across workgroups
+  __syncthreads();
+  if (wave > 0) return;
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    acc[m] = m < ntok ? ((red[0][m][lane] + red[1][m][lane]) + red[2][m][lane]) + red[3][m][lane] : 0.0f;
+  if (slices > 1) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) dev::xstore(a.partial + ((size_t(tile) * slices + slice) * MT + m) * 64 + lane, acc[m]);
+    unsigned *ctr = &a.counters[size_t(tile) * kCounterStride];
+    if (!dev::last_arrival(ctr, unsigned(slices), lane)) return;
+    const float *pt = a.partial + size_t(tile) * slices * MT * 64 + lane;
+    dev::sum_slices<MT, 4>(acc, [&](int sl, int m) { return pt + (size_t(sl) * MT + m) * 64; }, slices);
+    dev::reset_counter(ctr, lane);
+  }
+  // 6) y rows of the valid tokens
+  const int row = tile * 64 + lane;
+  if (row < a.n)
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      if (m < ntok) a.y[size_t(m) * a.n + row] = acc[m];
+}
+
 // Members of two K-quant encodings in one launch (a layer's q/k/v often mix
 // quant types), one unit per wave; each workgroup runs its member's own code.
 template <int E0, int E1>
@@ -1204,6 +1348,30 @@ void gguf_group_launch(const GGGroup &g, int bw, hipStream_t s) {
     default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
   }
   hip_check(hipGetLastError(), "gguf matvec launch");
+}
+
+void gguf_matvec_mt_launch(const GGArgs &a, int slices, int ntok, hipStream_t s) {
+  if (ntok < 1 || ntok > kGGMaxTokens) fail(QNN_E_INVALID_OP, "gguf multi-token width");
+  const int grid = (a.tiles + 7) / 8 * 8 * slices;
+#define QNN_GG_MT(E) hipLaunchKernelGGL((k_gguf_matvec_mt<E, kGGMaxTokens>), dim3(grid), dim3(256), 0, s, a, slices, ntok)
+  switch (a.l.enc) {
+    case QNN_WE_Q4_K: QNN_GG_MT(QNN_WE_Q4_K); break;
+    case QNN_WE_Q6_K: QNN_GG_MT(QNN_WE_Q6_K); break;
+    case QNN_WE_Q3_K: QNN_GG_MT(QNN_WE_Q3_K); break;
+    case QNN_WE_Q2_K: QNN_GG_MT(QNN_WE_Q2_K); break;
+    case QNN_WE_Q8_0: QNN_GG_MT(QNN_WE_Q8_0); break;
+    case QNN_WE_Q5_K: QNN_GG_MT(QNN_WE_Q5_K); break;
+    case QNN_WE_IQ4_NL: QNN_GG_MT(QNN_WE_IQ4_NL); break;
+    case QNN_WE_IQ4_XS: QNN_GG_MT(QNN_WE_IQ4_XS); break;
+    case QNN_WE_Q2_0: QNN_GG_MT(QNN_WE_Q2_0); break;
+    case QNN_WE_IQ2_XXS: QNN_GG_MT(QNN_WE_IQ2_XXS); break;
+    case QNN_WE_IQ2_S: QNN_GG_MT(QNN_WE_IQ2_S); break;
+    case QNN_WE_IQ3_XXS: QNN_GG_MT(QNN_WE_IQ3_XXS); break;
+    case QNN_WE_IQ3_S: QNN_GG_MT(QNN_WE_IQ3_S); break;
+    default: fail(QNN_E_NOT_SUPPORTED, "GGUF encoding not supported by the HIP backend");
+  }
+#undef QNN_GG_MT
+  hip_check(hipGetLastError(), "gguf multi-token matvec launch");
 }
 
 void gguf_matvec_launch(const GGArgs &a, int bw, int slices, hipStream_t s) {

@@ -41,13 +41,15 @@ struct Tuning {
   int fuse_mlp = 1;          // QNN_FUSE_MLP: recorded INT4 SwiGLU + down as one launch
   int fuse_moe = 1;          // QNN_FUSE_MOE: one-token routed experts (and route) as one launch
   int q8_gemm_min_rows = 4;  // QNN_Q8_GEMM_MIN_ROWS: rows from which Q8_0 Linear takes the GEMM
-  int gemm_h16 = 128;        // QNN_GEMM_H16: rows from which the GEMM runs over a pre-expanded fp16 copy (0: never)
+  int gemm_h16 = 128;        // QNN_GEMM_H16: rows from which Q8_0 Linear runs over a pre-expanded fp16 copy (0: never)
+  int gguf_gemm_rows = 32;   // QNN_GGUF_GEMM_ROWS: the same for the other GGUF encodings (0: never)
   int attn_wgs = 512;        // QNN_ATTN_WGS: cached-attention workgroup target
   int attn_min_chunk = 64;   // QNN_ATTN_MIN_CHUNK: keys per chunk, at least
   int attn_dma = 1;          // QNN_ATTN_DMA: 64-key chunks at dim 128 streamed into LDS
   int gemm_nw = 0;           // QNN_GEMM_NW: waves per Q8_0 GEMM workgroup (4 or 8)
   int gemm_mb = 0;           // QNN_GEMM_MB: 32-row blocks per GEMM wave (1 or 2)
   int gg_bw = 0;             // QNN_GG_BW: GGUF units per wave (1 or 2)
+  int gg_mt = 1;             // QNN_GG_MT: GGUF Linear of 2..127 rows, up to 8 rows per pass (0: one per row)
   int i4_mfma = 1;           // QNN_I4_MFMA: multi-token INT4 dot on the int8 matrix cores
   int i4_lanes = 0;          // QNN_I4_LANES: lanes per INT4 row at upload (1..16)
   int i4_tpw = 1;            // QNN_I4_TPW: INT4 tiles per workgroup (1, 2, 4)
@@ -378,6 +380,11 @@ void gguf_repack_launch(const uint8_t *src, const GGLayout &l, void *dst, hipStr
 void gguf_dequant_launch(const GGLayout &l, const void *w, float *out, hipStream_t s);
 void gguf_plan(const GGLayout &l, int tiles, int *bw, int *slices);
 void gguf_matvec_launch(const GGArgs &a, int bw, int slices, hipStream_t s);
+// 2 to kGGMaxTokens tokens (rows of a.x, a.x row stride a.l.cols, a.y row
+// stride a.n) in one pass over the weights, one unit per wave (qnn_gguf.hip).
+// Needs kGGMaxTokens partial sums per split-K slot.
+constexpr int kGGMaxTokens = 8;
+void gguf_matvec_mt_launch(const GGArgs &a, int slices, int ntok, hipStream_t s);
 // Up to kGGMaxGroup matvecs of one encoding and plan width in one launch:
 // member i owns workgroups [start[i], start[i+1]) (multiples of 8, so each
 // member keeps its XCD-aware tile map).

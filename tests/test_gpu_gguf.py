@@ -117,6 +117,30 @@ def test_linear_rows_and_bias(ctx, rng, enc):
         assert normwise_rel_err(got[r], want) <= TOL, r
 
 
+@pytest.mark.parametrize("enc", FMTS, ids=NAMES.get)
+def test_linear_multi_token_equals_per_row(ctx, rng, tune, enc):
+    """2 to 127 rows run up to 8 rows per pass over the weight (k_gguf_matvec_mt): every row equals
+    the one-row matvec bit for bit (QNN_GG_MT=0 runs one launch per row) and is within 1e-3 of the
+    CPU path; ragged shapes (n not a multiple of 64, K not a multiple of 1024)."""
+    n, k = 200, 1280 if BLOCK_ELEMENTS[enc] == 256 else 1344
+    data = quantized(rng, enc, n, k)
+    w = hip.MemoryBlock.gguf(data, n, k, enc)
+    for rows in (2, 8, 11):
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        src, dst = ctx.UploadRaw(x), ctx.NewTensor(rows * n)
+        ctx.Linear(dst, src, w, None, None, rows, k, n)
+        got = ctx.Download(dst).reshape(rows, n)
+        tune("QNN_GG_MT", "0")
+        ctx.Linear(dst, src, w, None, None, rows, k, n)
+        per_row = ctx.Download(dst).reshape(rows, n)
+        tune("QNN_GG_MT", "1")
+        assert np.array_equal(got.view(np.uint32), per_row.view(np.uint32)), rows
+        for r in range(rows):
+            assert normwise_rel_err(got[r], oracle.cpu_linear(data, enc, x[r], k, n)) <= TOL, (rows, r)
+        ctx.Recycle(src)
+        ctx.Recycle(dst)
+
+
 # Two 256-element units per wave (k_gguf_matvec<ENC, 2>), which the planner no
 # longer picks by itself: QNN_GG_BW=2 forces it at small ragged shapes,
 # including launches with fewer units than waves (and at the Q6_K head below).
