@@ -996,10 +996,16 @@ bool run_gguf_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int
                          : reinterpret_cast<const int *>(static_cast<const uint8_t *>(h->dptr) +
                                                          q8_h16_bytes(w->gg.rows, w->gg.cols));
       const Q8GemmPlan p = q8_h16_plan(rows, in_dim, out_dim);
+      // Small grids split K (the other encodings only: a Q8_0 copy's product
+      // stays bit-identical to the decoding kernel's).
+      const int ksplit = q8 ? 1 : h16_ksplit(p, out_dim);
       const size_t frag_off = 0, exp_off = (p.frag_bytes + 255) & ~size_t(255);
-      uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, exp_off + p.exp_bytes));
+      const size_t part_off = (exp_off + p.exp_bytes + 255) & ~size_t(255);
+      const size_t part_bytes = ksplit > 1 ? size_t(ksplit) * rows * out_dim * 4 : 0;
+      uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, part_off + part_bytes));
       q8_h16_gemm_launch(p, x, rows, in_dim, out_dim, ew, h->dptr, ws + frag_off,
-                         reinterpret_cast<int *>(ws + exp_off), y, ctx->stream);
+                         reinterpret_cast<int *>(ws + exp_off), y, ctx->stream, ksplit,
+                         reinterpret_cast<float *>(ws + part_off));
       ctx->st.gemm_h16++;
       return true;
     }

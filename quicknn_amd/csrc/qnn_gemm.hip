@@ -392,8 +392,8 @@ struct H16Args {
   const int *ea;
   const uint4 *wfrag;  // [n_pad / 32][ksteps][64]
   const int *ew;       // [rows] weight row exponents
-  float *c;
-  int M, N, ksteps, ktiles, mtiles, ntiles;
+  float *c;            // ksplit 1: C [M][N]; else the slices' partial products [ksplit][M][N]
+  int M, N, ksteps, ktiles, mtiles, ntiles, ksplit;
 };
 
 // One 1 KiB piece from global memory into LDS at `lds` (wave-uniform).  The
@@ -421,10 +421,15 @@ struct H16Frags {
 
 __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   const int b = blockIdx.x;
-  const int xcd = b & 7, kq = b >> 3;  // the M-tiles of an N-tile share blockIdx % 8 (an XCD, its L2)
-  const int q = kq / g.mtiles;
-  const int ntile = q * 8 + xcd, mtile = kq - q * g.mtiles;
-  if (ntile >= g.ntiles) return;
+  // Units (N-tile, K-slice) are dealt to the XCDs in turn; the M-tiles of a
+  // unit share blockIdx % 8 (an XCD, its L2, which then fetches the unit's
+  // weight columns once).
+  const int xcd = b & 7, kq = b >> 3;
+  const int q = kq / g.mtiles, mtile = kq - q * g.mtiles, unit = q * 8 + xcd;
+  if (unit >= g.ntiles * g.ksplit) return;
+  const int ntile = unit % g.ntiles, ks = unit / g.ntiles;
+  // K-slice ks: K-tiles [kt0, kt0 + nkt).
+  const int kt0 = ks * g.ktiles / g.ksplit, nkt = (ks + 1) * g.ktiles / g.ksplit - kt0;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 
@@ -446,7 +451,7 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   auto dma = [&](int kt, int i) {
     const uint32_t st = lds0 + uint32_t(kt % HST) * ((HAP + HBP) * 1024u);
     h16_dma(i < HAP / 4 ? ar : br, __builtin_amdgcn_readfirstlane(st + uint32_t(wave + 4 * i) * 1024u), voff[i],
-            uint32_t(kt) * (HKT * 1024u));
+            uint32_t(kt0 + kt) * (HKT * 1024u));
   };
   // Piece r of this wave's 5 HKT per K-tile: K-step r / 5, then A rows wm*2 + 0..1, B columns wn*3 + 0..2.
   auto read1 = [&](H16Frags &f, const uint4 *st, int r) {
@@ -488,11 +493,11 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   };
 #pragma unroll
   for (int d = 0; d < HST; ++d)
-    if (d < g.ktiles)
+    if (d < nkt)
 #pragma unroll
       for (int i = 0; i < HPW; ++i) dma(d, i);
   H16Frags f0, f1;
-  if (HST - 1 < g.ktiles)
+  if (HST - 1 < nkt)
     h16_vmwait<HPW * (HST - 1)>();
   else
     h16_vmwait<0>();
@@ -502,16 +507,16 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   using Y = std::true_type;
   using N = std::false_type;
   int kt = 0;
-  for (; kt + 1 + HST < g.ktiles; kt += 2) {  // both K-tiles refill
+  for (; kt + 1 + HST < nkt; kt += 2) {  // both K-tiles refill
     tile(Y(), f0, f1, kt);
     tile(Y(), f1, f0, kt + 1);
   }
-  for (; kt < g.ktiles; kt += 2) {
-    if (kt + HST < g.ktiles)
+  for (; kt < nkt; kt += 2) {
+    if (kt + HST < nkt)
       tile(Y(), f0, f1, kt);
     else
       tile(N(), f0, f1, kt);
-    if (kt + 1 < g.ktiles) tile(N(), f1, f0, kt + 1);
+    if (kt + 1 < nkt) tile(N(), f1, f0, kt + 1);
   }
 
   // Epilogue: lane holds C[8*(i/4) + 4*(lane/32) + i%4][lane%32] of each 32 x 32 tile.
@@ -542,7 +547,8 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
       for (int i = 0; i < 16; ++i) {
         const int row = mtile * HBM + (wm * 2 + mb) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
         if (row < g.M)
-          __builtin_nontemporal_store(ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]), &g.c[size_t(row) * g.N + col]);
+          __builtin_nontemporal_store(ldexpf(acc[mb][nb][i], ear[mb][i] + ewr[nb]),
+                                      &g.c[(size_t(ks) * g.M + row) * g.N + col]);
       }
     }
   }
@@ -575,27 +581,63 @@ Q8GemmPlan q8_h16_plan(int M, int K, int N) {
   return p;
 }
 
+// C = the K-slices' partial products summed in slice order (float4 pieces).
+__global__ __launch_bounds__(256) void k_sum_kslices(float4 *__restrict__ c, const float4 *__restrict__ part,
+                                                     size_t count4, int slices) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= count4) return;
+  float4 v = part[i];
+  for (int s = 1; s < slices; ++s) {
+    const float4 o = part[size_t(s) * count4 + i];
+    v.x += o.x;
+    v.y += o.y;
+    v.z += o.z;
+    v.w += o.w;
+  }
+  c[i] = v;
+}
+
+// K-slices for a grid of few tiles: as many as keep every workgroup of the
+// launch resident at once.  The kernel takes a CU's whole LDS (one workgroup
+// per CU), and an XCD (32 CUs) holds ceil(ntiles * ksplit / 8) units of
+// mtiles workgroups; at least 8 K-tiles per slice, at most 8 slices.
+int h16_ksplit(const Q8GemmPlan &p, int N) {
+  const int ktiles = p.ksteps / HKT;
+  if (N % 4 != 0) return 1;
+  int best = 1;
+  for (int s = 2; s <= 8 && ktiles / s >= 8; ++s)
+    if ((p.ntiles * s + 7) / 8 * p.mtiles <= 32) best = s;
+  return best;
+}
+
 void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const int *ew, const void *w16,
-                        void *frag, int *ea, float *c, hipStream_t s) {
+                        void *frag, int *ea, float *c, hipStream_t s, int ksplit, float *part) {
   hipLaunchKernelGGL(k_act_prep, dim3(p.m_pad / 4), dim3(1024), 0, s, a, M, K, p.ksteps, ea, static_cast<uint4 *>(frag));
   H16Args g;
   g.afrag = static_cast<const uint4 *>(frag);
   g.ea = ea;
   g.wfrag = static_cast<const uint4 *>(w16);
   g.ew = ew;
-  g.c = c;
+  g.c = ksplit > 1 ? part : c;
   g.M = M;
   g.N = N;
   g.ksteps = p.ksteps;
   g.ktiles = p.ksteps / HKT;
   g.mtiles = p.mtiles;
   g.ntiles = p.ntiles;
-  const int grid = (p.ntiles + 7) / 8 * 8 * p.mtiles;
+  g.ksplit = std::max(1, ksplit);
+  const int grid = (p.ntiles * g.ksplit + 7) / 8 * 8 * p.mtiles;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void *>(&k_h16_gemm), hipFuncAttributeMaxDynamicSharedMemorySize, int(kH16Lds));
   hip_check(attr, "fp16-copy gemm LDS size");
   hipLaunchKernelGGL(k_h16_gemm, dim3(grid), dim3(256), kH16Lds, s, g);
   hip_check(hipGetLastError(), "q8 fp16-copy gemm launch");
+  if (g.ksplit > 1) {
+    const size_t count4 = size_t(M) * N / 4;
+    hipLaunchKernelGGL(k_sum_kslices, dim3((count4 + 255) / 256), dim3(256), 0, s, reinterpret_cast<float4 *>(c),
+                       reinterpret_cast<const float4 *>(part), count4, g.ksplit);
+    hip_check(hipGetLastError(), "gemm K-slice sum launch");
+  }
 }
 
 void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s) {

@@ -326,8 +326,12 @@ void q8_rowexp_launch(const GGLayout &l, void *w, hipStream_t s);
 size_t q8_h16_bytes(int rows, int cols);
 void q8_expand_h16_launch(const GGLayout &l, const void *w, void *out, hipStream_t s);
 Q8GemmPlan q8_h16_plan(int M, int K, int N);
+// ksplit > 1 (h16_ksplit: small grids) splits K over that many workgroups per
+// tile, their partial products in `part` (ksplit * M * N floats, N % 4 == 0),
+// summed in slice order by a second launch; ksplit 1 writes C directly.
+int h16_ksplit(const Q8GemmPlan &p, int N);
 void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N, const int *ew, const void *w16,
-                        void *frag, int *ea, float *c, hipStream_t s);
+                        void *frag, int *ea, float *c, hipStream_t s, int ksplit = 1, float *part = nullptr);
 // The fp16 copy of a weight of any other GGUF encoding (qnn_gguf.hip): its
 // row exponents (range_exp of the row's largest |value|, one int per row of
 // the copy's q8_h16_bytes rows), then the values RNE(v * 2^-e) in

@@ -138,15 +138,16 @@ def test_small_rows_use_matvec_and_agree(ctx, rng):
 # of them through readGGUF).  From QNN_GGUF_GEMM_ROWS rows (default 32) the
 # product runs over the weight's fp16 copy, whose values are RNE(W * 2^-e) with
 # e from the row's largest |value| (k_gguf_rowexp, k_gguf_expand_h16), then
-# k_h16_gemm; fewer rows run the matvec, up to 8 rows per pass.  Both within
-# 1e-3 of the CPU paths.
+# k_h16_gemm (grids under 128 tiles split K over up to 8 workgroups per tile,
+# summed in slice order); fewer rows run the matvec, up to 8 rows per pass.
+# Both within 1e-3 of the CPU paths.
 # ---------------------------------------------------------------------------
 GEMM_FMTS = [ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_IQ4_NL, ENC_IQ4_XS, ENC_Q2_0, ENC_IQ2_XXS, ENC_IQ2_S,
              ENC_IQ3_XXS, ENC_IQ3_S]
 
 
 @pytest.mark.parametrize("enc", GEMM_FMTS)
-@pytest.mark.parametrize("m,k,n", [(128, 1024, 300), (200, 768, 97), (32, 1024, 130)])
+@pytest.mark.parametrize("m,k,n", [(128, 1024, 300), (200, 768, 97), (32, 1024, 130), (64, 3584, 512)])
 def test_other_encodings_fp16_copy_gemm(ctx, rng, tune, enc, m, k, n):
     w = hip.gguf_quantize(enc, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
     a = rng.standard_normal((m, k)).astype(np.float32)
