@@ -975,9 +975,10 @@ WeightEntry *h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
 // fp16 copy; otherwise, and under capture while no copy exists, a Q8_0 weight
 // from q8_gemm_min_rows rows takes k_q8_gemm, which decodes its tiles.  False
 // when neither applies: the caller then runs the matvec, up to kGGMaxTokens
-// rows per pass.  (Measured at 14336 x 3584, Q2_K / IQ2_XXS: the copy's GEMM
-// is faster from about 12 rows; at 4096 x 3584 Q4_K from about 24; at
-// 3584 x 14336 Q6_K, 19 column tiles only, from about 40.)
+// rows per pass.  (Measured with the GEMM's K-slices: at 8 rows the matvec is
+// faster for Q4_K 4096 x 3584 (15.7 against 24.2 us) and Q6_K 3584 x 14336,
+// even for Q2_K 14336 x 3584, slower for IQ2_XXS; from 16 rows the GEMM is
+// faster for all of them.)
 bool run_gguf_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
   const bool q8 = w->gg.enc == QNN_WE_Q8_0;
   const int from = q8 ? tuning().gemm_h16 : tuning().gguf_gemm_rows;

@@ -1068,7 +1068,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   gguf_item<ENC, 1>(grp, group_member(grp));
 }
 // Up to MT tokens (rows of x, `ntok` valid, the rest zero) in one pass over
-// the weights: the per-token Linear of 2 to 127 rows, MT at a time.  The
+// the weights: a Linear of a few rows, MT at a time.  The
 // workgroup and plan are the one-token kernel's at one unit per wave; each
 // token has its own activation slice in LDS, the wave's unit is loaded once
 // and dotted with every slice, and the split-K exchange carries MT partial

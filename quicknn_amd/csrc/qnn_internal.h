@@ -42,14 +42,14 @@ struct Tuning {
   int fuse_moe = 1;          // QNN_FUSE_MOE: one-token routed experts (and route) as one launch
   int q8_gemm_min_rows = 4;  // QNN_Q8_GEMM_MIN_ROWS: rows from which Q8_0 Linear takes the GEMM
   int gemm_h16 = 128;        // QNN_GEMM_H16: rows from which Q8_0 Linear runs over a pre-expanded fp16 copy (0: never)
-  int gguf_gemm_rows = 32;   // QNN_GGUF_GEMM_ROWS: the same for the other GGUF encodings (0: never)
+  int gguf_gemm_rows = 12;   // QNN_GGUF_GEMM_ROWS: the same for the other GGUF encodings (0: never)
   int attn_wgs = 512;        // QNN_ATTN_WGS: cached-attention workgroup target
   int attn_min_chunk = 64;   // QNN_ATTN_MIN_CHUNK: keys per chunk, at least
   int attn_dma = 1;          // QNN_ATTN_DMA: 64-key chunks at dim 128 streamed into LDS
   int gemm_nw = 0;           // QNN_GEMM_NW: waves per Q8_0 GEMM workgroup (4 or 8)
   int gemm_mb = 0;           // QNN_GEMM_MB: 32-row blocks per GEMM wave (1 or 2)
   int gg_bw = 0;             // QNN_GG_BW: GGUF units per wave (1 or 2)
-  int gg_mt = 1;             // QNN_GG_MT: GGUF Linear of 2..127 rows, up to 8 rows per pass (0: one per row)
+  int gg_mt = 1;             // QNN_GG_MT: GGUF Linear below the GEMM, up to 8 rows per pass (0: one per row)
   int i4_mfma = 1;           // QNN_I4_MFMA: multi-token INT4 dot on the int8 matrix cores
   int i4_lanes = 0;          // QNN_I4_LANES: lanes per INT4 row at upload (1..16)
   int i4_tpw = 1;            // QNN_I4_TPW: INT4 tiles per workgroup (1, 2, 4)

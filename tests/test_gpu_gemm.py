@@ -135,7 +135,7 @@ def test_small_rows_use_matvec_and_agree(ctx, rng):
 
 # ---------------------------------------------------------------------------
 # The other encodings (Context.Implementation.inc:852-883: gemm.comp decodes any
-# of them through readGGUF).  From QNN_GGUF_GEMM_ROWS rows (default 32) the
+# of them through readGGUF).  From QNN_GGUF_GEMM_ROWS rows (default 12) the
 # product runs over the weight's fp16 copy, whose values are RNE(W * 2^-e) with
 # e from the row's largest |value| (k_gguf_rowexp, k_gguf_expand_h16), then
 # k_h16_gemm (grids under 128 tiles split K over up to 8 workgroups per tile,
