@@ -249,7 +249,9 @@ int qnn_end_weight_prefetch(qnn_ctx *ctx);     /* EndWeightPrefetch: waits and r
  * ------------------------------------------------------------------------- */
 /* Linear (Context.API.inc:117-122, Implementation.inc:813-899).  GGUF weights:
  * rows == 1 runs the packed matvec (op 65), rows > 1 the multi-row product
- * (gemm.comp); Q8_0 with rows >= 4 runs the fp16-MFMA GEMM.  F32 and BF16
+ * (gemm.comp): the fp16-MFMA GEMM for Q8_0 from 4 rows and for the other
+ * encodings from 12 (over a cached fp16 copy of the weight), otherwise the
+ * matvec up to 8 rows per pass over the weight.  F32 and BF16
  * weights [out_dim, in_dim] (the router and native-precision layers) run an
  * fp32 matvec (rows == 1) or fp32 GEMM (rows > 1); bf16 widens exactly.  One-row calls
  * without bias are recorded and launched by the next call on the context;
