@@ -419,6 +419,9 @@ struct H16Frags {
   half8 a[HKT][2], b[HKT][3];
 };
 
+// KS: the launch slices K (g.ksplit > 1); the instance without slices keeps
+// the plain N-tile mapping and loop bounds.
+template <bool KS>
 __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   const int b = blockIdx.x;
   // Units (N-tile, K-slice) are dealt to the XCDs in turn; the M-tiles of a
@@ -426,10 +429,11 @@ __global__ __launch_bounds__(256) void k_h16_gemm(const H16Args g) {
   // weight columns once).
   const int xcd = b & 7, kq = b >> 3;
   const int q = kq / g.mtiles, mtile = kq - q * g.mtiles, unit = q * 8 + xcd;
-  if (unit >= g.ntiles * g.ksplit) return;
-  const int ntile = unit % g.ntiles, ks = unit / g.ntiles;
+  if (unit >= (KS ? g.ntiles * g.ksplit : g.ntiles)) return;
+  const int ntile = KS ? unit % g.ntiles : unit, ks = KS ? unit / g.ntiles : 0;
   // K-slice ks: K-tiles [kt0, kt0 + nkt).
-  const int kt0 = ks * g.ktiles / g.ksplit, nkt = (ks + 1) * g.ktiles / g.ksplit - kt0;
+  const int kt0 = KS ? ks * g.ktiles / g.ksplit : 0;
+  const int nkt = KS ? (ks + 1) * g.ktiles / g.ksplit - kt0 : g.ktiles;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 
@@ -627,10 +631,18 @@ void q8_h16_gemm_launch(const Q8GemmPlan &p, const float *a, int M, int K, int N
   g.ntiles = p.ntiles;
   g.ksplit = std::max(1, ksplit);
   const int grid = (p.ntiles * g.ksplit + 7) / 8 * 8 * p.mtiles;
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(&k_h16_gemm), hipFuncAttributeMaxDynamicSharedMemorySize, int(kH16Lds));
+  static const hipError_t attr = [] {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_h16_gemm<false>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(kH16Lds));
+    return e != hipSuccess ? e
+                           : hipFuncSetAttribute(reinterpret_cast<const void *>(&k_h16_gemm<true>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, int(kH16Lds));
+  }();
   hip_check(attr, "fp16-copy gemm LDS size");
-  hipLaunchKernelGGL(k_h16_gemm, dim3(grid), dim3(256), kH16Lds, s, g);
+  if (g.ksplit > 1)
+    hipLaunchKernelGGL(k_h16_gemm<true>, dim3(grid), dim3(256), kH16Lds, s, g);
+  else
+    hipLaunchKernelGGL(k_h16_gemm<false>, dim3(grid), dim3(256), kH16Lds, s, g);
   hip_check(hipGetLastError(), "q8 fp16-copy gemm launch");
   if (g.ksplit > 1) {
     const size_t count4 = size_t(M) * N / 4;
