@@ -47,15 +47,19 @@ __device__ __forceinline__ float half_bits_to_f(uint32_t h) {
 
 // ---- activation preparation ------------------------------------------------
 // One launch: workgroup b owns rows 4b .. 4b + 3 of A (m_pad rows in all),
-// four waves per row.  A row's waves read it, take ea[m] from max |A[m][.]|
-// (range_exp; the four waves meet in LDS), then re-read it from the cache and
-// write its fp16 values A·2^-ea (exact scaling, one RNE rounding) as the
-// fragments of v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane) = 8
-// halfs A[m32*32 + lane%32][ks*16 + 8*(lane/32) + 0..7], so the row's group
-// of 8 columns g goes to piece (m / 32, g / 2) at lane m % 32 + 32 (g % 2).
-// The four rows of a workgroup fill the same 64-byte segments together (one
-// row per workgroup wrote every segment in four visits: twice the bytes).
-// Rows past M and columns past K give exponent 0 and zero pieces.
+// four waves per row.  A row's 256 threads take its groups of 8 columns
+// g = t, t + 256, ...: each thread requests its first AP_HOLD groups at once
+// and keeps them in registers (the whole row up to K = 8192), takes ea[m]
+// from max |A[m][.]| (range_exp; the four waves meet in LDS), then writes
+// the fp16 values A·2^-ea (exact scaling, one RNE rounding) as the fragments
+// of v_mfma_f32_32x32x16_f16's A operand: piece (m32, ks, lane) = 8 halfs
+// A[m32*32 + lane%32][ks*16 + 8*(lane/32) + 0..7], so the row's group g goes
+// to piece (m / 32, g / 2) at lane m % 32 + 32 (g % 2).  Groups past the held
+// ones are read twice (once for the maximum, once for the values).  The four
+// rows of a workgroup fill the same 64-byte segments together (one row per
+// workgroup wrote every segment in four visits: twice the bytes).  Rows past
+// M and columns past K give exponent 0 and zero pieces.
+constexpr int AP_HOLD = 4;
 __global__ __launch_bounds__(1024) void k_act_prep(const float *__restrict__ a, int M, int K, int ksteps,
                                                    int *__restrict__ ea, uint4 *__restrict__ frag) {
   __shared__ float red[4][4];
@@ -65,17 +69,43 @@ __global__ __launch_bounds__(1024) void k_act_prep(const float *__restrict__ a, 
   const bool in = row < M;
   const float *r = a + size_t(in ? row : 0) * K;
   const bool vec = (K & 3) == 0;
-  float amax = 0.0f;
-  if (in) {
-    if (vec) {
-      const float4 *r4 = reinterpret_cast<const float4 *>(r);
-      for (int k = t; k < K / 4; k += 256) {
-        const float4 v = r4[k];
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-      }
+  const int groups = 2 * ksteps;  // groups of 8 columns, K padded to 16
+  auto load8 = [&](int g, float (&v)[8]) {
+    const int k0 = 8 * g;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    if (!in) return;
+    if (vec && k0 + 8 <= K) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(r + k0), x1 = *reinterpret_cast<const float4 *>(r + k0 + 4);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
     } else {
-      for (int k = t; k < K; k += 256) amax = fmaxf(amax, fabsf(r[k]));
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (k0 + i < K) v[i] = r[k0 + i];
     }
+  };
+  auto vmax = [](float m, const float (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    return m;
+  };
+  float held[AP_HOLD][8];
+#pragma unroll
+  for (int c = 0; c < AP_HOLD; ++c) {
+    if (t + 256 * c < groups) {
+      load8(t + 256 * c, held[c]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) held[c][i] = 0.0f;
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < AP_HOLD; ++c) amax = vmax(amax, held[c]);
+  for (int g = t + 256 * AP_HOLD; g < groups; g += 256) {
+    float v[8];
+    load8(g, v);
+    amax = vmax(amax, v);
   }
   for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
   if (lane == 0) red[rw][part] = amax;
@@ -84,25 +114,19 @@ __global__ __launch_bounds__(1024) void k_act_prep(const float *__restrict__ a, 
   if (t == 0) ea[row] = e;
   const float sc = ldexpf(1.0f, -e);
   uint4 *dst = frag + size_t(row >> 5) * ksteps * 64 + (row & 31);
-  for (int g = t; g < 2 * ksteps; g += 256) {
-    const int k0 = 8 * g;
-    float v[8];
+  auto put = [&](int g, float (&v)[8]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    if (in) {
-      if (vec && k0 + 8 <= K) {
-        const float4 x0 = *reinterpret_cast<const float4 *>(r + k0), x1 = *reinterpret_cast<const float4 *>(r + k0 + 4);
-        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (k0 + i < K) v[i] = r[k0 + i];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] *= sc;  // exact: power of two
-    }
+    for (int i = 0; i < 8; ++i) v[i] *= sc;  // exact: power of two
     dst[size_t(g >> 1) * 64 + 32 * (g & 1)] =
         make_uint4(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]), pack_h2(v[6], v[7]));
+  };
+#pragma unroll
+  for (int c = 0; c < AP_HOLD; ++c)
+    if (t + 256 * c < groups) put(t + 256 * c, held[c]);
+  for (int g = t + 256 * AP_HOLD; g < groups; g += 256) {
+    float v[8];
+    load8(g, v);
+    put(g, v);
   }
 }
 

@@ -49,8 +49,10 @@ def test_prefill_shape_matches_cpu_paths(ctx, rng):
         assert normwise_rel_err(got[r], want[r]) <= TOL, r
 
 
+# K = 9216 and 10240: rows longer than the activation preparation holds in
+# registers (8192 columns), whose last groups it reads twice.
 @pytest.mark.parametrize("m,k,n", [(512, 3072, 12288), (128, 3072, 12288), (257, 1024, 97), (300, 640, 200),
-                                   (130, 96, 1000), (1000, 4096, 385)])
+                                   (130, 96, 1000), (1000, 4096, 385), (130, 9216, 96), (128, 10240, 200)])
 def test_fp16_copy_equals_decoding_kernel(ctx, rng, tune, m, k, n):
     """From QNN_GEMM_H16 rows (default 128) the product runs over a pre-expanded fp16 copy
     of the weight (k_h16_gemm, qnn_status.gemm_h16), made once and cached: every output equals
@@ -147,7 +149,8 @@ GEMM_FMTS = [ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_IQ4_NL, ENC_I
 
 
 @pytest.mark.parametrize("enc", GEMM_FMTS)
-@pytest.mark.parametrize("m,k,n", [(128, 1024, 300), (200, 768, 97), (32, 1024, 130), (64, 3584, 512)])
+@pytest.mark.parametrize("m,k,n", [(128, 1024, 300), (200, 768, 97), (32, 1024, 130), (64, 3584, 512),
+                                   (16, 10240, 64)])
 def test_other_encodings_fp16_copy_gemm(ctx, rng, tune, enc, m, k, n):
     w = hip.gguf_quantize(enc, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
     a = rng.standard_normal((m, k)).astype(np.float32)
