@@ -149,8 +149,9 @@ GEMM_FMTS = [ENC_Q4_K, ENC_Q5_K, ENC_Q6_K, ENC_Q3_K, ENC_Q2_K, ENC_IQ4_NL, ENC_I
 
 
 @pytest.mark.parametrize("enc", GEMM_FMTS)
+# (16, 4352, 96): 68 K-tiles over 8 slices of 8 or 9 (uneven K-slices).
 @pytest.mark.parametrize("m,k,n", [(128, 1024, 300), (200, 768, 97), (32, 1024, 130), (64, 3584, 512),
-                                   (16, 10240, 64)])
+                                   (16, 10240, 64), (16, 4352, 96)])
 def test_other_encodings_fp16_copy_gemm(ctx, rng, tune, enc, m, k, n):
     w = hip.gguf_quantize(enc, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
     a = rng.standard_normal((m, k)).astype(np.float32)
