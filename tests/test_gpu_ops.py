@@ -10,9 +10,11 @@
 * CheckFinite / GO_FINITE: Download raises on NaN/Inf and leaves the
   destination untouched (Context.Implementation.inc:745-756); clean data passes.
 * Copy with offsets, partial Download, Scratch slots, Recycle, events.
-* HIP graph capture of a decode MLP (fused gate/up, down, GO_ADD residual):
-  every replay, with eager work and synchronisations between replays, equals
-  the eager result bit for bit.
+* HIP graph capture of a decode MLP (fused gate/up, down, GO_ADD residual),
+  and of GGUF projections of 1, 6 and 64 rows (one-token matvec, multi-token
+  matvec, fp16-copy GEMM with K-slices) with a 4096-key cached attention
+  (LDS-streamed kernel and chunk merge): every replay, with eager work and
+  synchronisations between replays, equals the eager result bit for bit.
 """
 import numpy as np
 import pytest
@@ -246,4 +248,74 @@ def test_graph_replays_match_eager(ctx, rng):
     want = oracle.cpu_mlp(g.data, u.data, d.data, oracle.ENC_INT4, xs[0], hidden, inter)[0] + xs[0]
     assert normwise_rel_err(eager[0], want) < 1e-3
     for t in (x, h, y, other):
+        ctx.Recycle(t)
+
+
+def test_graph_replays_gguf_projections_and_attention_match_eager(ctx, rng):
+    """Capture a Q4_K projection of one row, a Q6_K projection of six rows, a Q4_K projection of
+    64 rows (its fp16 copy, made by the eager runs, split over two K-slices and summed by a second
+    launch) and a cached attention over 4096 keys at head dim 128; replay with eager work between."""
+    from quicknn_amd import hip
+
+    k, n = 1024, 384
+    w4 = hip.MemoryBlock.gguf(hip.gguf_quantize(hip.WE_Q4_K, (rng.standard_normal(n * k) * 0.02).astype(np.float32)),
+                              n, k, hip.WE_Q4_K)
+    w6 = hip.MemoryBlock.gguf(hip.gguf_quantize(hip.WE_Q6_K, (rng.standard_normal(n * k) * 0.02).astype(np.float32)),
+                              n, k, hip.WE_Q6_K)
+    heads, kvh, dim, cap = 32, 8, 128, 4096
+    cache = ctx.UploadRaw(rng.standard_normal(2 * cap * kvh * dim).astype(np.float32))
+    rows = (1, 6, 64)
+    xs = [ctx.NewTensor(r * k) for r in rows]
+    ys = [ctx.NewTensor(r * n) for r in rows]
+    q, o, other = ctx.NewTensor(heads * dim), ctx.NewTensor(heads * dim), ctx.NewTensor(4096)
+    h0 = ctx.status().gemm_h16
+
+    def step():
+        ctx.Linear(ys[0], xs[0], w4, None, None, 1, k, n)
+        ctx.Linear(ys[1], xs[1], w6, None, None, 6, k, n)
+        ctx.Linear(ys[2], xs[2], w4, None, None, 64, k, n)
+        ctx.CachedAttention(o, q, cache, 1, cap, heads, kvh, dim, cap - 1)
+
+    sets = [([rng.standard_normal(r * k).astype(np.float32) for r in rows],
+             (rng.standard_normal(heads * dim) * 0.3).astype(np.float32)) for _ in range(3)]
+
+    def load(i):
+        tmp = [ctx.UploadRaw(v) for v in sets[i][0]] + [ctx.UploadRaw(sets[i][1])]
+        for dst, src, cnt in zip(xs + [q], tmp, [r * k for r in rows] + [heads * dim]):
+            ctx.Copy(dst, src, cnt)
+        return tmp
+
+    eager = []
+    for i in range(len(sets)):  # eager results (also make the fp16 copy and size every workspace)
+        tmp = load(i)
+        step()
+        eager.append([ctx.Download(t) for t in ys + [o]])
+        for t in tmp:
+            ctx.Recycle(t)
+    assert ctx.status().gemm_h16 - h0 == len(sets)
+    ctx.GraphBegin()
+    step()
+    gid = ctx.GraphEnd()
+    for rep in range(3):
+        for i in range(len(sets)):
+            tmp = load(i)
+            ctx.Kernel(hip.GO_FILL, 4096, other, None, None, None, [f32_bits(float(rep))])  # eager work
+            ctx.GraphLaunch(gid)
+            got = [ctx.Download(t) for t in ys + [o]]
+            for j, (gv, ev) in enumerate(zip(got, eager[i])):
+                assert np.array_equal(gv.view(np.uint32), ev.view(np.uint32)), (rep, i, j)
+            assert np.all(ctx.Download(other) == np.float32(rep))
+            for t in tmp:
+                ctx.Recycle(t)
+    # the eager runs against the CPU path
+    w4b, w6b = w4.data, w6.data
+    x0, q0 = sets[0]
+    assert normwise_rel_err(eager[0][0], oracle.cpu_linear(w4b, oracle.ENC_Q4_K, x0[0], k, n)) <= 1e-3
+    for r in (0, 5):
+        assert normwise_rel_err(eager[0][1][r * n:(r + 1) * n],
+                                oracle.cpu_linear(w6b, oracle.ENC_Q6_K, x0[1][r * k:(r + 1) * k], k, n)) <= 1e-3
+    for r in (0, 63):
+        assert normwise_rel_err(eager[0][2][r * n:(r + 1) * n],
+                                oracle.cpu_linear(w4b, oracle.ENC_Q4_K, x0[2][r * k:(r + 1) * k], k, n)) <= 1e-3
+    for t in xs + ys + [q, o, other, cache]:
         ctx.Recycle(t)
