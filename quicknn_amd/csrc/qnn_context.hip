@@ -163,6 +163,7 @@ void reload_tuning() {
   t.q8_gemm_min_rows = env_int("QNN_Q8_GEMM_MIN_ROWS", t.q8_gemm_min_rows);
   t.gemm_h16 = env_int("QNN_GEMM_H16", t.gemm_h16);
   t.gguf_gemm_rows = env_int("QNN_GGUF_GEMM_ROWS", t.gguf_gemm_rows);
+  t.gemm_max_rows = env_int("QNN_GEMM_MAX_ROWS", t.gemm_max_rows);
   t.attn_wgs = env_int("QNN_ATTN_WGS", t.attn_wgs);
   t.attn_min_chunk = env_int("QNN_ATTN_MIN_CHUNK", t.attn_min_chunk);
   t.attn_dma = env_int("QNN_ATTN_DMA", t.attn_dma);
@@ -883,6 +884,8 @@ bool try_fused_mlp(qnn_ctx_s *ctx, WeightEntry *d, float *y) {
   qnn_ctx_s::Pending &p = ctx->pending;
   const I4Layout &lg = p.g->i4, &ld = d->i4;
   if (lg.lanes != 1 || ld.lanes != 1 || p.in % 4 || p.out % 4) return false;
+  // Its weight resources span whole matrices (32-bit offsets).
+  if (std::max(lg.nib_bytes(), ld.nib_bytes()) > 0xFFFFFFFFull) return false;
   const I4Plan pg = int4_plan(lg, 1, I4_SWIGLU), pd = int4_plan(ld, 1, I4_STORE);
   if (pg.tiles_per_wg != 1 || pd.tiles_per_wg != 1 || pg.gsw > 8 || pd.gsw > 8) return false;
   const int grid = std::max(pg.grid, pd.grid);
@@ -970,6 +973,15 @@ WeightEntry *h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
   return insert(ctx, e);
 }
 
+// Rows per GEMM launch: the activation fragments (2 bytes per element, K
+// padded to 64) stay below 4 GiB; QNN_GEMM_MAX_ROWS lowers it (tests).
+int gemm_max_rows(int in_dim) {
+  const size_t k_pad = (size_t(in_dim) + 63) / 64 * 64;
+  size_t m = std::max<size_t>(128, 0xFFFFFFFFull / (k_pad * 2) / 128 * 128);
+  if (tuning().gemm_max_rows > 0) m = std::min(m, size_t(tuning().gemm_max_rows));
+  return int(std::min<size_t>(m, size_t(1) << 30));
+}
+
 // Multi-row GGUF projection.  From QNN_GEMM_H16 rows (Q8_0) or
 // QNN_GGUF_GEMM_ROWS rows (the other encodings): k_h16_gemm over the weight's
 // fp16 copy; otherwise, and under capture while no copy exists, a Q8_0 weight
@@ -982,7 +994,11 @@ WeightEntry *h16_entry(qnn_ctx_s *ctx, const WeightEntry *w) {
 bool run_gguf_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int rows, int in_dim, int out_dim) {
   const bool q8 = w->gg.enc == QNN_WE_Q8_0;
   const int from = q8 ? tuning().gemm_h16 : tuning().gguf_gemm_rows;
-  if (from > 0 && rows >= from) {
+  // The GEMM kernels address the weight (its tiles, or its fp16 copy) and the
+  // activation fragments with 32-bit buffer offsets: larger weights take the
+  // matvec, and the caller passes at most gemm_max_rows rows.
+  const size_t copy_bytes = q8_h16_bytes(w->gg.rows, w->gg.cols) + (size_t(w->gg.rows) * 4 + 255) / 256 * 256;
+  if (from > 0 && rows >= from && copy_bytes <= 0xFFFFFFFFull) {
     w->op_pins++;  // making the copy may evict: not the weight it is made from
     WeightEntry *h = nullptr;
     try {
@@ -1011,7 +1027,7 @@ bool run_gguf_gemm(qnn_ctx_s *ctx, WeightEntry *w, const float *x, float *y, int
       return true;
     }
   }
-  if (!q8 || rows < q8_gemm_min_rows()) return false;
+  if (!q8 || rows < q8_gemm_min_rows() || w->gg.total > 0xFFFFFFFFull) return false;
   const Q8GemmPlan p = q8_gemm_plan(rows, in_dim, out_dim);
   const size_t frag_off = 0, exp_off = (p.frag_bytes + 255) & ~size_t(255);
   uint8_t *ws = static_cast<uint8_t *>(ensure_work(ctx, exp_off + p.exp_bytes));
@@ -1632,16 +1648,20 @@ int qnn_linear(qnn_ctx *ctx, qnn_tensor *dst, qnn_tensor *src, const qnn_weight 
         record_linear(ctx, e, src->ptr, dst->ptr, out_dim);
       } else {
         settle_pending(ctx);
-        if (rows < 2 || !run_gguf_gemm(ctx, e, src->ptr, dst->ptr, rows, in_dim, out_dim)) {
+        const int chunk = gemm_max_rows(in_dim);
+        for (int r0 = 0; r0 < rows; r0 += chunk) {
+          const int rr = std::min(chunk, rows - r0);
+          const float *xs = src->ptr + size_t(r0) * in_dim;
+          float *ys = dst->ptr + size_t(r0) * out_dim;
+          if (rr >= 2 && run_gguf_gemm(ctx, e, xs, ys, rr, in_dim, out_dim)) continue;
           // The matvec (op 65): up to kGGMaxTokens rows per pass over the weight.
-          for (int r = 0; r < rows; r += kGGMaxTokens) {
-            const int nt = std::min(kGGMaxTokens, rows - r);
+          for (int r = 0; r < rr; r += kGGMaxTokens) {
+            const int nt = std::min(kGGMaxTokens, rr - r);
             if (nt == 1 || tuning().gg_mt == 0) {
               for (int t = r; t < r + nt; ++t)
-                run_gguf(ctx, e, nullptr, GG_STORE, src->ptr + size_t(t) * in_dim, dst->ptr + size_t(t) * out_dim,
-                         out_dim);
+                run_gguf(ctx, e, nullptr, GG_STORE, xs + size_t(t) * in_dim, ys + size_t(t) * out_dim, out_dim);
             } else {
-              run_gguf_mt(ctx, e, src->ptr + size_t(r) * in_dim, dst->ptr + size_t(r) * out_dim, nt, out_dim);
+              run_gguf_mt(ctx, e, xs + size_t(r) * in_dim, ys + size_t(r) * out_dim, nt, out_dim);
             }
           }
         }

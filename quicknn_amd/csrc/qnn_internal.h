@@ -43,6 +43,7 @@ struct Tuning {
   int q8_gemm_min_rows = 4;  // QNN_Q8_GEMM_MIN_ROWS: rows from which Q8_0 Linear takes the GEMM
   int gemm_h16 = 128;        // QNN_GEMM_H16: rows from which Q8_0 Linear runs over a pre-expanded fp16 copy (0: never)
   int gguf_gemm_rows = 12;   // QNN_GGUF_GEMM_ROWS: the same for the other GGUF encodings (0: never)
+  int gemm_max_rows = 0;     // QNN_GEMM_MAX_ROWS: rows per GEMM launch, at most (0: the 4 GiB fragment limit)
   int attn_wgs = 512;        // QNN_ATTN_WGS: cached-attention workgroup target
   int attn_min_chunk = 64;   // QNN_ATTN_MIN_CHUNK: keys per chunk, at least
   int attn_dma = 1;          // QNN_ATTN_DMA: 64-key chunks at dim 128 streamed into LDS

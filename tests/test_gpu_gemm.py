@@ -73,6 +73,27 @@ def test_fp16_copy_equals_decoding_kernel(ctx, rng, tune, m, k, n):
         assert normwise_rel_err(fast[r], oracle.cpu_linear(w, ENC_Q8_0, a[r], k, n)) <= TOL, r
 
 
+@pytest.mark.parametrize("enc", [ENC_Q8_0, ENC_Q4_K])
+def test_rows_in_several_gemm_launches(ctx, rng, tune, enc):
+    """Rows beyond one launch's limit run as consecutive launches (the limit keeps the activation
+    fragments below 4 GiB; QNN_GEMM_MAX_ROWS lowers it): 300 rows as 128 + 128 + 44.  Q8_0 takes
+    its fp16 copy for the two full launches and decodes its tiles for the last, both the same bits
+    as one launch over all rows; Q4_K takes its copy for all three."""
+    m, k, n = 300, 1024, 200
+    w = hip.gguf_quantize(enc, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    whole = run_linear(ctx, w, a, n, enc=enc)
+    tune("QNN_GEMM_MAX_ROWS", "128")
+    h0 = ctx.status().gemm_h16
+    parts = run_linear(ctx, w, a, n, enc=enc)
+    assert ctx.status().gemm_h16 - h0 == (2 if enc == ENC_Q8_0 else 3)
+    if enc == ENC_Q8_0:
+        assert np.array_equal(parts.view(np.uint32), whole.view(np.uint32))
+    for r in (0, 127, 128, 255, 256, 299):
+        assert normwise_rel_err(parts[r], oracle.cpu_linear(w, enc, a[r], k, n)) <= TOL, r
+        assert normwise_rel_err(parts[r], whole[r]) <= TOL, r
+
+
 @pytest.mark.parametrize("m,k,n", [(4, 96, 100), (5, 32, 64), (257, 1024, 97), (300, 640, 200), (33, 4096, 4096),
                                    (16, 2048, 6144)])
 def test_ragged_shapes(ctx, rng, m, k, n):
