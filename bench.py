@@ -422,7 +422,7 @@ def run_cfg3(args, hip) -> dict:
     # Per op: its own launches back to back over copies of its weight totalling
     # more than 512 MB, so every launch streams from HBM (the layer rotation
     # above holds 8 copies, 25-135 MB per op, which the MALL could serve).
-    per_op = {}
+    per_op, multi_row = {}, {}
     for nm in ("q", "k", "v", "o", "gate", "up", "down"):
         e, n, kk = shapes[nm]
         ncopy = max(L, -(-600_000_000 // wbytes[nm]))
@@ -434,10 +434,32 @@ def run_cfg3(args, hip) -> dict:
         t = timed_ms(ctx, run, max(2, args.steps // 10)) * 1000 / ncopy
         per_op[nm] = {"us": round(t, 2), "GBps": round(wbytes[nm] / (t * 1e-6) / 1e9, 1), "copies": ncopy,
                       "rotation_MB": round(ncopy * wbytes[nm] / 1e6)}
+        if nm == "q":
+            # Eight rows through one Linear (the multi-token matvec, all eight
+            # per pass over the weight), over the same cold rotation.
+            x8, y8 = ctx.UploadRaw(rng.standard_normal((8, H)).astype(np.float32)), ctx.NewTensor(8 * Q)
+            run8 = lambda: [ctx.Linear(y8, x8, w, None, None, 8, H, Q) for w in copies]  # noqa: E731
+            run8()
+            ctx.Flush()
+            t8 = timed_ms(ctx, run8, max(2, args.steps // 10)) * 1000 / ncopy
+            multi_row["q_8_rows"] = {"us": round(t8, 2), "GBps": round(wbytes[nm] / (t8 * 1e-6) / 1e9, 1),
+                                     "copies": ncopy, "path": "k_gguf_matvec_mt: 8 rows per pass over the weight"}
+            ctx.Recycle(x8)
+            ctx.Recycle(y8)
         del copies
     ctx.Linear(logits, xt, head_b, None, None, 1, H, V)  # first launch of the head's shape, untimed
     ctx.Flush()
     head_us = timed_ms(ctx, lambda: ctx.Linear(logits, xt, head_b, None, None, 1, H, V), 20) * 1000
+    # A 512-row prefill through q (the fp16-copy GEMM over each weight's
+    # cached fp16 copy, made by the first, untimed call), over the layer copies.
+    x512, y512 = ctx.UploadRaw(rng.standard_normal((512, H)).astype(np.float32)), ctx.NewTensor(512 * Q)
+    run512 = lambda: [ctx.Linear(y512, x512, lay["q"], None, None, 512, H, Q) for lay in layers]  # noqa: E731
+    run512()
+    ctx.Flush()
+    t512 = timed_ms(ctx, run512, max(2, args.steps // 5)) * 1000 / L
+    multi_row["q_512_rows"] = {"us": round(t512, 2), "TFLOPs": round(2 * 512 * H * Q / (t512 * 1e-6) / 1e12, 1),
+                               "path": "k_h16_gemm over the cached fp16 copy (K split over 2 slices, summed by "
+                                       "k_sum_kslices), after k_act_prep"}
     traffic_calibration_copy(ctx)
     ctx.close()
     dom = max(per_op, key=lambda nm: per_op[nm]["us"])
@@ -477,6 +499,7 @@ def run_cfg3(args, hip) -> dict:
                      "down Q6_K, batch 1; head Q6_K 256000x3584", "global_batch": 1},
         us_per_layer=round(us_layer, 2), pct_of_hbm_peak=round(100 * value / HBM_PEAK_GBS, 2), per_op=per_op,
         head={"us": round(head_us, 2), "GBps": round(head.size / (head_us * 1e-6) / 1e9, 1)},
+        multi_row_linear=multi_row,
         roofline={"bound": "hbm", "achieved": per_op[dom]["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": round(per_op[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
                   "kernel": f"k_gguf_matvec ({dom}: {shapes[dom][1]}x{shapes[dom][2]})",
