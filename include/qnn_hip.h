@@ -176,12 +176,13 @@ int qnn_get_status(qnn_ctx *ctx, qnn_status *out);
  * this picks up a change made afterwards (tests and sweeps).  No reference
  * counterpart. */
 int qnn_reload_tuning(void);
-/* Diagnostic: per-workgroup phase timestamps of the fused decode-MLP kernels
- * (device real-time counter, 100 MHz), as [workgroup][16] words, from a
- * library built with QNN_PHASE_TRACE (libqnn_hip_trace.so; the same kernels
- * with timestamps).  Waits for the context's work, copies up to `count` words
- * into dst, sets *copied and clears the timestamps.  QNN_E_NOT_SUPPORTED in
- * the ordinary build.  No reference counterpart. */
+/* Diagnostic: per-workgroup phase timestamps (device real-time counter,
+ * 100 MHz) of the fused decode-MLP kernel, as [2048 workgroups][16] words,
+ * followed by the same for the one-token MoE kernel, from a library built
+ * with QNN_PHASE_TRACE (libqnn_hip_trace.so; the same kernels with
+ * timestamps).  Waits for the context's work, copies up to `count` words into
+ * dst, sets *copied and clears the timestamps.  QNN_E_NOT_SUPPORTED in the
+ * ordinary build.  No reference counterpart. */
 int qnn_phase_trace(qnn_ctx *ctx, uint64_t *dst, uint64_t count, uint64_t *copied);
 /* Diagnostic: one plain streaming read of the first `count` floats of src
  * (count a multiple of 4), issued as the matvec kernels issue their weight

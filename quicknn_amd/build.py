@@ -70,12 +70,16 @@ def build(jobs: int | None = None) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, "-lpthread"])
     os.replace(tmp, LIB)
-    # The phase-trace variant: the fused decode-MLP kernels with per-workgroup
-    # timestamps (QNN_PHASE_TRACE), everything else the same objects.
-    mlp = os.path.join(CSRC, "qnn_mlp.hip")
-    tobj = os.path.join(BUILD, "qnn_mlp.hip.trace.o")
-    _run([HIPCC, *HIP_FLAGS, "-DQNN_PHASE_TRACE", "-c", mlp, "-o", tobj])
-    tobjs = [tobj if o.endswith("qnn_mlp.hip.o") else o for o in objs]
+    # The phase-trace variant: the fused decode-MLP and one-token MoE kernels
+    # with per-workgroup timestamps (QNN_PHASE_TRACE), everything else the
+    # same objects.
+    traced = {}
+    for name in ("qnn_mlp.hip", "qnn_moe.hip"):
+        tobj = os.path.join(BUILD, name + ".trace.o")
+        _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(name, []), "-DQNN_PHASE_TRACE", "-c", os.path.join(CSRC, name),
+              "-o", tobj])
+        traced[os.path.join(BUILD, name + ".o")] = tobj
+    tobjs = [traced.get(o, o) for o in objs]
     tmp = TRACE_LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *tobjs, "-o", tmp, "-lpthread"])
     os.replace(tmp, TRACE_LIB)

@@ -1109,10 +1109,17 @@ int qnn_phase_trace(qnn_ctx *ctx, uint64_t *dst, uint64_t count, uint64_t *copie
     check_ctx(ctx);
     if (!dst || !copied) fail(QNN_E_ARGUMENT, "phase trace buffer");
     sync(ctx);
-    const int n = mlp_phase_read(dst, size_t(count) * 8);
+    // [2048][16] words of the fused decode MLP, then [2048][16] of the one-token MoE kernel.
+    constexpr uint64_t kWords = 2048 * 16;
+    const int n = mlp_phase_read(dst, size_t(std::min(count, kWords)) * 8);
     if (n == -2) fail(QNN_E_NOT_SUPPORTED, "not a phase-trace build (libqnn_hip_trace.so)");
     if (n < 0) fail(QNN_E_INVALID_OP, "phase trace copy");
-    *copied = uint64_t(n);
+    int n2 = 0;
+    if (count > kWords) {
+      n2 = moe_phase_read(dst + kWords, size_t(std::min(count - kWords, kWords)) * 8);
+      if (n2 < 0) fail(QNN_E_INVALID_OP, "phase trace copy");
+    }
+    *copied = uint64_t(n) + uint64_t(n2);
     return QNN_OK;
   });
 }

@@ -441,6 +441,24 @@ void launch_mt(const MoELaunch &a, const MoEPlanSizes &p, hipStream_t s) {
 // per slot, so every arrival of a down block has the same blockIdx % 8.
 size_t moe_decode_lds(int g) { return dev::xplanes_bytes(1, 4 * g); }
 
+// Phase timestamps of k_moe_decode, built only into libqnn_hip_trace.so
+// (-DQNN_PHASE_TRACE), as in the fused decode MLP: thread 0 of workgroup wg
+// stores the device's real-time counter (100 MHz) at phase k; nothing else
+// changes.
+#ifdef QNN_PHASE_TRACE
+constexpr int kMoEPhaseWGs = 2048, kMoEPhases = 16;
+__device__ unsigned long long g_moe_phase[kMoEPhaseWGs * kMoEPhases];
+#define QNN_MOE_PHASE(k)                                                                             \
+  do {                                                                                               \
+    if (threadIdx.x == 0 && blockIdx.x < kMoEPhaseWGs)                                               \
+      g_moe_phase[blockIdx.x * kMoEPhases + (k)] = __builtin_amdgcn_s_memrealtime();                 \
+  } while (0)
+#else
+#define QNN_MOE_PHASE(k) \
+  do {                   \
+  } while (0)
+#endif
+
 // J > 0: the token's routes are computed here from a.logits (GO_MOE_ROUTE
 // recorded just before, J = experts/64 rounded up to a power of two), by every
 // wave with the route op's own code, and workgroup 0 writes them to the
@@ -458,6 +476,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   constexpr int XG = 4 * (GG > GD ? GG : GD);
   const dev::XPlanes xs = dev::xplanes_at(dyn_lds, 1, XG);
   const I4Layout &lg = a.gu, &ld = a.dn;
+  QNN_MOE_PHASE(0);
 
   // ---- route ranks: lane i < k holds route i; rank = its position in
   //      ascending expert id (ties: lower route index, reported as invalid).
@@ -541,6 +560,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   //         2 x slices arrivals of a pair writes its h rows and raises its flag.
   dev::stage_x<1, GG>(xs, xr, 1, ws0 * 32, sgroups * 32, a.hidden, tid, lane);
   __syncthreads();
+  QNN_MOE_PHASE(1);
   float acc[1] = {0.0f};
   if (ns > 0) {
     dev::XPlanes xp = xs;
@@ -552,6 +572,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   }
   if (part > 0) red[part][lane] = acc[0];
   __syncthreads();
+  QNN_MOE_PHASE(2);
   if (part == 0 && gu_on) {
     acc[0] = ((acc[0] + red[1][lane]) + red[2][lane]) + red[3][lane];
     dev::xstore(a.partial + (size_t(tile) * slices_gu + slice) * 64 + lane, acc[0]);
@@ -566,7 +587,9 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
       __builtin_amdgcn_s_waitcnt(0);  // the block's h is at the coherence point
       if (lane == 0)
         __hip_atomic_store(a.flags + size_t(pair) * 64, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      QNN_MOE_PHASE(4);
     }
+    QNN_MOE_PHASE(3);
   }
   if (!dn_on) return;
 
@@ -601,11 +624,13 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
     }
   }
   __syncthreads();
+  QNN_MOE_PHASE(5);
   float4 hr[1][dev::x_iters<GD>()];
   dev::load_x<1, GD, dev::kCoherent>(hr, dev::rsrc(a.h + size_t(dslot) * a.inter, size_t(a.inter) * 4),
                                     [](int) { return 0u; }, 1, wsd * 32, sgd * 32, tid);
   dev::stage_x<1, GD>(xs, hr, 1, wsd * 32, sgd * 32, a.inter, tid, lane);
   __syncthreads();
+  QNN_MOE_PHASE(6);
   float scd[GD];
   dev::pick_scales<GD>(scd, qd, s0d);
   acc[0] = 0.0f;
@@ -619,6 +644,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   }
   if (part > 0) red[part][lane] = acc[0];
   __syncthreads();
+  QNN_MOE_PHASE(7);
   if (part > 0) return;
   acc[0] = ((acc[0] + red[1][lane]) + red[2][lane]) + red[3][lane];
   dev::xstore(a.partial_dn + ((size_t(td) * k + dslot) * slices_dn + sld) * 64 + lane, acc[0]);
@@ -646,6 +672,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   dev::reset_counter(ctr, lane);
   const int row = td * 64 + lane;
   if (row < a.hidden) a.out[row] = out;
+  QNN_MOE_PHASE(8);
 }
 
 template <int G, int J>
@@ -755,6 +782,21 @@ MoEDecodePlan moe_decode_plan(const MoELaunch &a, const MoEPlanSizes &p) {
 int moe_route_j(int experts) {
   const int j = (experts + 63) / 64;
   return j <= 1 ? 1 : (j <= 2 ? 2 : (j <= 4 ? 4 : (j <= 8 ? 8 : (j <= 16 ? 16 : 0))));
+}
+
+int moe_phase_read(void *dst, size_t bytes) {
+#ifdef QNN_PHASE_TRACE
+  const size_t n = std::min(bytes, sizeof(g_moe_phase));
+  if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_moe_phase), n, 0, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  static const unsigned long long zeros[kMoEPhaseWGs * kMoEPhases] = {};
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_moe_phase), zeros, sizeof(g_moe_phase), 0, hipMemcpyHostToDevice) != hipSuccess)
+    return -1;
+  return int(n / 8);
+#else
+  (void)dst;
+  (void)bytes;
+  return -2;
+#endif
 }
 
 int moe_decode_capacity(const MoEPlanSizes &p, int route_j, int device) {

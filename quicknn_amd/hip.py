@@ -419,15 +419,15 @@ class GPUContext:
         """qnn_stream_read: one plain streaming read of count floats of src (diagnostic)."""
         _raise(lib().qnn_stream_read(self.h, src.handle, count, dst.handle))
 
-    def PhaseTrace(self, workgroups: int = 2048):
-        """qnn_phase_trace: [workgroups, 16] uint64 phase timestamps of the fused MLP kernels
-        (trace builds only), cleared afterwards."""
+    def PhaseTrace(self, kernel: str = "mlp"):
+        """qnn_phase_trace: [2048, 16] uint64 phase timestamps of the fused MLP kernel ("mlp") or of
+        the one-token MoE kernel ("moe") (trace builds only); both are cleared afterwards."""
         import numpy as np
 
-        buf = np.zeros((workgroups, 16), np.uint64)
+        buf = np.zeros((2, 2048, 16), np.uint64)
         n = ctypes.c_uint64()
         _raise(lib().qnn_phase_trace(self.h, ctypes.c_void_p(buf.ctypes.data), buf.size, ctypes.byref(n)))
-        return buf
+        return buf[1 if kernel == "moe" else 0]
 
     # -- tensors
     def NewTensor(self, count: int) -> Tensor:

@@ -1,6 +1,6 @@
 """Where the time of one fused decode-MLP launch goes, and the HBM stream floor.
 
-    python -m quicknn_amd.phase_trace [--runs N] [--no-stream]
+    python -m quicknn_amd.phase_trace [--runs N] [--no-stream] [--moe]
 
 Loads libqnn_hip_trace.so (the library built with QNN_PHASE_TRACE: the same
 kernels, with thread 0 of every workgroup storing the device real-time
@@ -17,6 +17,13 @@ Phases of k_int4_mlp:
   exchanged (every item), 4 h block and flag published (last arrival of the
   block), 5 h flags of the slice seen, 6 h slice staged, 7 down parts in LDS,
   8 y stored (last arrival of the tile).
+
+--moe times the one-token routed-expert launch (k_moe_decode) of
+`bench.py --config 4` instead: 128 INT4 experts of 2048 -> 2 x 768 -> 2048 in
+4 expert sets, top-8 routes whose experts are the disjoint groups 8j..8j+7,
+so that each rotation reads every expert of every set (1.5 GB) and no launch
+finds its experts in the MALL.  Its phases are those of the MLP kernel, with
+an expert slot's gate/up tiles and blocks of h in place of the layer's.
 
 The stream floor: one plain streaming read (qnn_stream_read: non-temporal
 16-byte loads, every piece requested at once, as the weight loads of the
@@ -77,17 +84,11 @@ def timeline(ctx, hip, blocks, runs: int):
         ctx.EventRecord(1)
         ctx.Flush()
         us_layer.append(ctx.EventElapsedMs(0, 1) * 1000 / LAYERS)
-        ts = ctx.PhaseTrace().astype(np.int64)  # the last layer's launch
-        starts = ts[:, 0][ts[:, 0] > 0]
-        t0 = starts.min()
-        row = {}
-        for k in range(9):
-            v = ts[:, k]
-            v = v[v >= t0]  # every workgroup rewrites phase 0; earlier values are an earlier launch's
-            if v.size:
-                us = (v - t0) / 100.0
-                row[k] = (float(us.min()), float(np.median(us)), float(us.max()), int(v.size))
-        per_run.append(row)
+        per_run.append(phases_of(ctx.PhaseTrace()))  # the last layer's launch
+    return summarise(per_run), float(np.median(us_layer))
+
+
+def summarise(per_run):
     out = {}
     for k in range(9):
         vals = [r[k] for r in per_run if k in r]
@@ -95,7 +96,64 @@ def timeline(ctx, hip, blocks, runs: int):
             a = np.array([v[:3] for v in vals])
             out[k] = {"first_us": round(float(np.median(a[:, 0])), 2), "median_us": round(float(np.median(a[:, 1])), 2),
                       "last_us": round(float(np.median(a[:, 2])), 2), "workgroups": vals[0][3]}
-    return out, float(np.median(us_layer))
+    return out
+
+
+def phases_of(ts):
+    """{phase: (earliest, median, latest us after the first start, workgroups)} of one launch's stamps."""
+    ts = ts.astype(np.int64)
+    starts = ts[:, 0][ts[:, 0] > 0]
+    t0 = starts.min()
+    row = {}
+    for k in range(9):
+        v = ts[:, k]
+        v = v[v >= t0]  # every workgroup rewrites phase 0; earlier values are an earlier launch's
+        if v.size:
+            us = (v - t0) / 100.0
+            row[k] = (float(us.min()), float(np.median(us)), float(us.max()), int(v.size))
+    return row
+
+
+MOE_E, MOE_H, MOE_I, MOE_K, MOE_SETS = 128, 2048, 768, 8, 4
+
+
+def moe_timeline(ctx, hip, runs: int):
+    rng = np.random.default_rng(17)
+
+    def mat(n, k):
+        w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+        return hip.MemoryBlock.int4(hip.quantize_int4((w.view(np.uint32) >> 16).astype(np.uint16)))
+
+    sets = [ctx.CreateExpertSet([mat(MOE_I, MOE_H) for _ in range(MOE_E)], [mat(MOE_I, MOE_H) for _ in range(MOE_E)],
+                                [mat(MOE_H, MOE_I) for _ in range(MOE_E)], MOE_H, MOE_I) for _ in range(MOE_SETS)]
+    x = ctx.UploadRaw(rng.standard_normal(MOE_H).astype(np.float32))
+    out = ctx.NewTensor(MOE_H)
+    routes = []
+    for st in sets:
+        for j in range(MOE_E // MOE_K):
+            lg = rng.standard_normal((1, MOE_E)).astype(np.float32)
+            lg[:, MOE_K * j:MOE_K * (j + 1)] += np.float32(10.0)
+            lt, rt = ctx.UploadRaw(lg), ctx.NewTensor(2 * MOE_K)
+            ctx.Kernel(hip.GO_MOE_ROUTE, 2 * MOE_K, rt, lt, None, None, [1, MOE_E, MOE_K, 1])
+            routes.append((st, rt))
+
+    def step():
+        for st, rt in routes:
+            ctx.MoEExperts(st, out, x, rt, 1, MOE_K)
+
+    for _ in range(3):
+        step()
+    ctx.Flush()
+    ctx.PhaseTrace("moe")  # clear
+    per_run, us_call = [], []
+    for _ in range(runs):
+        ctx.EventRecord(0)
+        step()
+        ctx.EventRecord(1)
+        ctx.Flush()
+        us_call.append(ctx.EventElapsedMs(0, 1) * 1000 / len(routes))
+        per_run.append(phases_of(ctx.PhaseTrace("moe")))  # the last call's launch
+    return summarise(per_run), float(np.median(us_call))
 
 
 def stream_floor(ctx, hip, sizes_mb=(16.0, 32.0, 46.8), total_mb=600.0, reps=3):
@@ -128,12 +186,29 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--runs", type=int, default=5)
     ap.add_argument("--no-stream", action="store_true")
+    ap.add_argument("--moe", action="store_true", help="the one-token routed-expert launch instead")
     args = ap.parse_args()
     from quicknn_amd import build, hip
 
     if not os.path.exists(build.TRACE_LIB):
         raise SystemExit(f"{build.TRACE_LIB} is not built: run __graft_entry__.build()")
     hip.LIB_PATH = build.TRACE_LIB
+    if args.moe:
+        ctx = hip.GPUContext(0)
+        s0 = ctx.status()
+        phases, us_call = moe_timeline(ctx, hip, args.runs)
+        if ctx.status().moe_fused == s0.moe_fused:
+            raise SystemExit("the one-token experts did not run as one launch")
+        print(f"kernel k_moe_decode: {us_call:.2f} us per call (HIP events, 64-call runs over 4 expert sets, "
+              f"median of {args.runs})")
+        print(f"{'phase':<20s} {'first':>8s} {'median':>8s} {'last':>8s} {'workgroups':>11s}")
+        for k, v in phases.items():
+            print(f"{k} {PHASES[k]:<18s} {v['first_us']:8.2f} {v['median_us']:8.2f} {v['last_us']:8.2f} "
+                  f"{v['workgroups']:11d}")
+        print(json.dumps({"kernel": "k_moe_decode", "us_per_call": round(us_call, 2),
+                          "phases": {PHASES[k]: v for k, v in phases.items()}}))
+        ctx.close()
+        return 0
     rng = np.random.default_rng(2024)
     blocks = layers(hip, rng)
     ctx = hip.GPUContext(0)
