@@ -603,6 +603,13 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
     dev::load_wq<GD>(wd, qd, dev::block_nib_rsrc(db, ld, td), dev::block_scl_rsrc(db + ld.nib_bytes(), ld, td), ld,
                      td, s0d, lane);
   }
+  // Lane j: the probability of slot j (ascending expert id), for the down
+  // combine, taken now rather than on the combine's dependent path.
+  float pslot = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const float pj = __shfl(prob, src_of(j));
+    if (lane == j) pslot = pj;
+  }
 
   // ---- 3) down: wait for the blocks of h_slot in the K-slice, stage, dot
   //         with the weights in registers, split-K exchange; the last arrival
@@ -649,26 +656,30 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   acc[0] = ((acc[0] + red[1][lane]) + red[2][lane]) + red[3][lane];
   dev::xstore(a.partial_dn + ((size_t(td) * k + dslot) * slices_dn + sld) * 64 + lane, acc[0]);
   unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
-  if (!dev::last_arrival(ctr, unsigned(k * slices_dn), lane)) return;
+  const bool last = dev::last_arrival(ctr, unsigned(k * slices_dn), lane);
+  QNN_MOE_PHASE(9);
+  if (!last) return;
   const float *pt = a.partial_dn + size_t(td) * k * slices_dn * 64 + lane;
   // The k x slices partial sums (expert-major) load 32 at a time; each
   // expert's y sums its slices in slice order, and out adds the experts in
   // ascending id order.
   float out = 0.0f, y = 0.0f;
   const int total = k * slices_dn;
-  for (int i0 = 0; i0 < total; i0 += 32) {
-    float v[32];
+  for (int i0 = 0; i0 < total; i0 += 16) {
+    float v[16];
 #pragma unroll
-    for (int i = 0; i < 32; ++i)
+    for (int i = 0; i < 16; ++i)
       if (i0 + i < total) v[i] = dev::xload(pt + size_t(i0 + i) * 64);
 #pragma unroll
-    for (int i = 0; i < 32; ++i)
+    for (int i = 0; i < 16; ++i)
       if (i0 + i < total) {
         const int j = (i0 + i) / slices_dn, s = i0 + i - j * slices_dn;
         y = s == 0 ? v[i] : y + v[i];
-        if (s == slices_dn - 1) out = add_mul_nofma(out, y, __shfl(prob, src_of(j)));  // moe.comp:70 / :126: out + y*p
+        if (s == slices_dn - 1)  // moe.comp:70 / :126: out + y*p
+          out = add_mul_nofma(out, y, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pslot), j)));
       }
   }
+  QNN_MOE_PHASE(10);
   dev::reset_counter(ctr, lane);
   const int row = td * 64 + lane;
   if (row < a.hidden) a.out[row] = out;

@@ -46,7 +46,7 @@ if ROOT not in sys.path:
 
 HIDDEN, INTER, LAYERS = 2560, 9728, 36
 PHASES = ["start", "x staged", "gate/up parts", "gate/up exchanged", "h published", "h slice seen", "h staged",
-          "down parts", "y stored"]
+          "down parts", "y stored", "down ticket taken", "down partials summed"]
 
 
 def layers(hip, rng):
@@ -90,7 +90,7 @@ def timeline(ctx, hip, blocks, runs: int):
 
 def summarise(per_run):
     out = {}
-    for k in range(9):
+    for k in range(len(PHASES)):
         vals = [r[k] for r in per_run if k in r]
         if vals:
             a = np.array([v[:3] for v in vals])
@@ -105,7 +105,7 @@ def phases_of(ts):
     starts = ts[:, 0][ts[:, 0] > 0]
     t0 = starts.min()
     row = {}
-    for k in range(9):
+    for k in range(len(PHASES)):
         v = ts[:, k]
         v = v[v >= t0]  # every workgroup rewrites phase 0; earlier values are an earlier launch's
         if v.size:
