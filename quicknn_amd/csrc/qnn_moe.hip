@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   const int nsd = max(0, min(sps_dn, ld.steps - s0d));
   const int sgd = min(4 * sps_dn, ld.groups - wsd);
 
-  const int eg = expert_of(slot), ed = expert_of(dslot);
+  const int eg = expert_of(slot);
 
   // ---- 1) loads: x slice and gate/up weights to registers
   float4 xr[1][dev::x_iters<GG>()];
@@ -599,6 +599,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   uint4 wd[GD];
   uint4 qd[QD];
   {
+    const int ed = expert_of(dslot);  // after the gate/up loads are issued
     const uint8_t *db = a.down + size_t(ed) * a.dn_stride;
     dev::load_wq<GD>(wd, qd, dev::block_nib_rsrc(db, ld, td), dev::block_scl_rsrc(db + ld.nib_bytes(), ld, td), ld,
                      td, s0d, lane);
