@@ -122,6 +122,7 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
       const float *pt = a.partial_gu + size_t(tile & ~1) * a.slices_gu * 64 + lane;
       float gu[2];  // gate and up, their slices loaded in one batch
       dev::sum_slices<2, 16>(gu, [&](int s, int m) { return pt + size_t(m * a.slices_gu + s) * 64; }, a.slices_gu);
+      QNN_PHASE(11);
       dev::reset_counter(ctr, lane);
       const int blk = tile >> 1, row = blk * 64 + lane;
       if (row < a.inter) dev::xstore(a.h + row, dev::silu(gu[0]) * gu[1]);
@@ -187,9 +188,12 @@ __global__ __launch_bounds__(256) void k_int4_mlp(const MlpLaunch a) {
   if (a.slices_dn > 1) {
     dev::xstore(a.partial_dn + (size_t(td) * a.slices_dn + sld) * 64 + lane, acc[0]);
     unsigned *ctr = &a.counters_dn[size_t(td) * kCounterStride];
-    if (!dev::last_arrival(ctr, unsigned(a.slices_dn), lane)) return;
+    const bool last = dev::last_arrival(ctr, unsigned(a.slices_dn), lane);
+    QNN_PHASE(9);
+    if (!last) return;
     const float *pt = a.partial_dn + size_t(td) * a.slices_dn * 64 + lane;
     dev::sum_slices<1, 32>(acc, [&](int s, int) { return pt + size_t(s) * 64; }, a.slices_dn);
+    QNN_PHASE(10);
     dev::reset_counter(ctr, lane);
   }
   const int row = td * 64 + lane;

@@ -581,6 +581,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
       const float *pt = a.partial + size_t(tile & ~1) * slices_gu * 64 + lane;
       float gu[2];  // gate and up, their slices loaded in one batch
       dev::sum_slices<2, 16>(gu, [&](int s, int m) { return pt + size_t(m * slices_gu + s) * 64; }, slices_gu);
+      QNN_MOE_PHASE(11);
       dev::reset_counter(ctr, lane);
       const int row = blk * 64 + lane;
       if (row < a.inter) dev::xstore(a.h + size_t(slot) * a.inter + row, dev::silu(gu[0]) * gu[1]);

@@ -16,7 +16,9 @@ Phases of k_int4_mlp:
   0 start, 1 x slice staged, 2 gate/up parts in LDS, 3 gate/up partial sum
   exchanged (every item), 4 h block and flag published (last arrival of the
   block), 5 h flags of the slice seen, 6 h slice staged, 7 down parts in LDS,
-  8 y stored (last arrival of the tile).
+  8 y stored (last arrival of the tile); 9 down partial stored and ticket
+  taken (every down item), 10 the tile's down partials loaded and summed and
+  11 a block's gate/up partials loaded and summed (last arrivals).
 
 --moe times the one-token routed-expert launch (k_moe_decode) of
 `bench.py --config 4` instead: 128 INT4 experts of 2048 -> 2 x 768 -> 2048 in
@@ -46,7 +48,7 @@ if ROOT not in sys.path:
 
 HIDDEN, INTER, LAYERS = 2560, 9728, 36
 PHASES = ["start", "x staged", "gate/up parts", "gate/up exchanged", "h published", "h slice seen", "h staged",
-          "down parts", "y stored", "down ticket taken", "down partials summed"]
+          "down parts", "y stored", "down ticket taken", "down partials summed", "gate/up partials summed"]
 
 
 def layers(hip, rng):
