@@ -178,7 +178,8 @@ int qnn_get_status(qnn_ctx *ctx, qnn_status *out);
 int qnn_reload_tuning(void);
 /* Diagnostic: per-workgroup phase timestamps (device real-time counter,
  * 100 MHz) of the fused decode-MLP kernel, as [2048 workgroups][16] words,
- * followed by the same for the one-token MoE kernel, from a library built
+ * followed by the same for the one-token MoE kernel and for the LDS-streamed
+ * cached-attention kernel, from a library built
  * with QNN_PHASE_TRACE (libqnn_hip_trace.so; the same kernels with
  * timestamps).  Waits for the context's work, copies up to `count` words into
  * dst, sets *copied and clears the timestamps.  QNN_E_NOT_SUPPORTED in the

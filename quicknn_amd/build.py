@@ -70,11 +70,11 @@ def build(jobs: int | None = None) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, "-lpthread"])
     os.replace(tmp, LIB)
-    # The phase-trace variant: the fused decode-MLP and one-token MoE kernels
-    # with per-workgroup timestamps (QNN_PHASE_TRACE), everything else the
-    # same objects.
+    # The phase-trace variant: the fused decode-MLP, one-token MoE and
+    # LDS-streamed attention kernels with per-workgroup timestamps
+    # (QNN_PHASE_TRACE), everything else the same objects.
     traced = {}
-    for name in ("qnn_mlp.hip", "qnn_moe.hip"):
+    for name in ("qnn_mlp.hip", "qnn_moe.hip", "qnn_decode.hip"):
         tobj = os.path.join(BUILD, name + ".trace.o")
         _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(name, []), "-DQNN_PHASE_TRACE", "-c", os.path.join(CSRC, name),
               "-o", tobj])

@@ -1109,17 +1109,21 @@ int qnn_phase_trace(qnn_ctx *ctx, uint64_t *dst, uint64_t count, uint64_t *copie
     check_ctx(ctx);
     if (!dst || !copied) fail(QNN_E_ARGUMENT, "phase trace buffer");
     sync(ctx);
-    // [2048][16] words of the fused decode MLP, then [2048][16] of the one-token MoE kernel.
+    // [2048][16] words of the fused decode MLP, then of the one-token MoE kernel, then of k_attn_dma.
     constexpr uint64_t kWords = 2048 * 16;
     const int n = mlp_phase_read(dst, size_t(std::min(count, kWords)) * 8);
     if (n == -2) fail(QNN_E_NOT_SUPPORTED, "not a phase-trace build (libqnn_hip_trace.so)");
     if (n < 0) fail(QNN_E_INVALID_OP, "phase trace copy");
-    int n2 = 0;
+    int n2 = 0, n3 = 0;
     if (count > kWords) {
       n2 = moe_phase_read(dst + kWords, size_t(std::min(count - kWords, kWords)) * 8);
       if (n2 < 0) fail(QNN_E_INVALID_OP, "phase trace copy");
     }
-    *copied = uint64_t(n) + uint64_t(n2);
+    if (count > 2 * kWords) {
+      n3 = attn_phase_read(dst + 2 * kWords, size_t(std::min(count - 2 * kWords, kWords)) * 8);
+      if (n3 < 0) fail(QNN_E_INVALID_OP, "phase trace copy");
+    }
+    *copied = uint64_t(n) + uint64_t(n2) + uint64_t(n3);
     return QNN_OK;
   });
 }

@@ -19,6 +19,7 @@
 #include <cmath>
 
 #include "qnn_exchange.h"
+#include "qnn_lanes.h"
 
 namespace qnn {
 namespace {
@@ -526,6 +527,24 @@ __device__ __forceinline__ void attn_vmwait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Phase timestamps of k_attn_dma, built only into libqnn_hip_trace.so
+// (-DQNN_PHASE_TRACE): thread 0 of the workgroup with linear index w stores
+// the device's real-time counter (100 MHz) at phase k; nothing else changes.
+#ifdef QNN_PHASE_TRACE
+constexpr int kAttnPhaseWGs = 2048, kAttnPhases = 16;
+__device__ unsigned long long g_attn_phase[kAttnPhaseWGs * kAttnPhases];
+#define QNN_ATTN_PHASE(k)                                                                                         \
+  do {                                                                                                            \
+    const unsigned w_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);                           \
+    if (threadIdx.x == 0 && w_ < unsigned(kAttnPhaseWGs))                                                         \
+      g_attn_phase[w_ * kAttnPhases + (k)] = __builtin_amdgcn_s_memrealtime();                                    \
+  } while (0)
+#else
+#define QNN_ATTN_PHASE(k) \
+  do {                    \
+  } while (0)
+#endif
+
 template <int GB>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restrict__ q, const float *__restrict__ cache,
                                                            float *__restrict__ out, float *__restrict__ opart,
@@ -549,6 +568,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restri
   const float *vb = cache + size_t(a.cap) * width + size_t(kh) * a.cap * kDmaDim;
   const unsigned *mask = reinterpret_cast<const unsigned *>(cache + 2 * size_t(a.cap) * width) + size_t(r) * a.cap;
 
+  QNN_ATTN_PHASE(0);
   // 1) q, then K^T, then V of the chunk into LDS.  Wave w: q piece w (if any;
   //    GB heads of 128 floats are GB / 2 pieces, a lone head half of one),
   //    channels 32w..32w+31 of K^T (8 pieces of 4 channels x 64 keys), keys
@@ -583,6 +603,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restri
     }
   }
   __syncthreads();
+  QNN_ATTN_PHASE(1);
 
   const float mul = a.scale > 0.0f ? a.scale : 1.0f / sqrtf(float(kDmaDim));
   float m_run[GB], l_run[GB], keep[GB];
@@ -623,21 +644,33 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restri
       v *= mul;
       if (a.softcap > 0.0f) v = a.softcap * tanhf(fminf(fmaxf(v / a.softcap, -20.0f), 20.0f));
       float mx = valid ? v : -INFINITY;
-      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      mx = fmaxf(mx, dev::xor_lanes<32>(mx));  // the butterfly of __shfl_xor(., 32 .. 1), on the VALU
+      mx = fmaxf(mx, dev::xor_lanes<16>(mx));
+      mx = fmaxf(mx, dev::xor_lanes<8>(mx));
+      mx = fmaxf(mx, dev::xor_lanes<4>(mx));
+      mx = fmaxf(mx, dev::xor_lanes<2>(mx));
+      mx = fmaxf(mx, dev::xor_lanes<1>(mx));
       const float m_new = fmaxf(m_run[g], mx);
       const float kp = m_new == -INFINITY ? 1.0f : expf(m_run[g] - m_new);
       const float p = (valid && m_new > -INFINITY) ? expf(v - m_new) : 0.0f;
       ps[g * kDmaKeys + key_t] = p;
       float ls = p;
-      for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off);
+      ls += dev::xor_lanes<32>(ls);
+      ls += dev::xor_lanes<16>(ls);
+      ls += dev::xor_lanes<8>(ls);
+      ls += dev::xor_lanes<4>(ls);
+      ls += dev::xor_lanes<2>(ls);
+      ls += dev::xor_lanes<1>(ls);
       if (key_t == 0) {
         red[g] = kp;
         red[GB + g] = l_run[g] * kp + ls;
         red[2 * GB + g] = m_new;
       }
     }
+    QNN_ATTN_PHASE(2);
     attn_vmwait<0>();  // V landed
     __syncthreads();   // publishes ps, the running state and every wave's V pieces
+    QNN_ATTN_PHASE(3);
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
       keep[g] = red[g];
@@ -665,20 +698,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restri
       }
     }
     __syncthreads();  // xred is rewritten below
+    QNN_ATTN_PHASE(4);
   }
-  // ---- the 8 key lanes: two per wave meet by a lane shuffle, then the four waves in LDS
+  // ---- the 8 key lanes: two per wave meet by a lane exchange (lanes 0-31
+  //      take lanes 32-63; the upper lanes' sums are not used), then the
+  //      four waves in LDS
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
-    acc[g].x += __shfl_down(acc[g].x, 32);
-    acc[g].y += __shfl_down(acc[g].y, 32);
-    acc[g].z += __shfl_down(acc[g].z, 32);
-    acc[g].w += __shfl_down(acc[g].w, 32);
+    acc[g].x += dev::xor_lanes<32>(acc[g].x);
+    acc[g].y += dev::xor_lanes<32>(acc[g].y);
+    acc[g].z += dev::xor_lanes<32>(acc[g].z);
+    acc[g].w += dev::xor_lanes<32>(acc[g].w);
   }
   if (wave > 0 && lane < 32)
 #pragma unroll
     for (int g = 0; g < GB; ++g)
       *reinterpret_cast<float4 *>(xred + (size_t(wave - 1) * GB + g) * kDmaDim + c4 * 4) = acc[g];
   __syncthreads();
+  QNN_ATTN_PHASE(5);
   if (tid >= 32) return;
 #pragma unroll
   for (int g = 0; g < GB; ++g)
@@ -706,6 +743,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restri
       ml[1] = l_run[g];
     }
   }
+  QNN_ATTN_PHASE(6);
 }
 
 // Merge the key chunks: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
@@ -1275,6 +1313,21 @@ void attn_launch(const float *q, const float *cache, float *out, float *ws, cons
       k_attn_merge_general<<<mg, 256, 0, s>>>(out, opart, ml, p.splits, rows * heads, dim, dspan, sg);
     }
   }
+}
+
+int attn_phase_read(void *dst, size_t bytes) {
+#ifdef QNN_PHASE_TRACE
+  const size_t n = std::min(bytes, sizeof(g_attn_phase));
+  if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_attn_phase), n, 0, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  static const unsigned long long zeros[kAttnPhaseWGs * kAttnPhases] = {};
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_attn_phase), zeros, sizeof(g_attn_phase), 0, hipMemcpyHostToDevice) != hipSuccess)
+    return -1;
+  return int(n / 8);
+#else
+  (void)dst;
+  (void)bytes;
+  return -2;
+#endif
 }
 
 size_t sample_workspace_floats(int vocab, int k) {

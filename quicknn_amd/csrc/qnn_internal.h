@@ -264,7 +264,8 @@ bool mlp_launch(const MlpLaunch &a, int gg, int gd, int grid, hipStream_t s);  /
 // `bytes` of [workgroup][16] u64 and clears them; words copied, -2 when the
 // library is not a trace build, -1 on a HIP error.
 int mlp_phase_read(void *dst, size_t bytes);
-int moe_phase_read(void *dst, size_t bytes);  // the one-token MoE kernel's, likewise
+int moe_phase_read(void *dst, size_t bytes);   // the one-token MoE kernel's, likewise
+int attn_phase_read(void *dst, size_t bytes);  // the LDS-streamed attention kernel's, likewise
 
 struct MoELaunch {
   const uint8_t *gate_up = nullptr;  // expert e: gate at gate_up + 2e*gu_stride, its up matrix gu_stride after it

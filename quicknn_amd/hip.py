@@ -420,14 +420,15 @@ class GPUContext:
         _raise(lib().qnn_stream_read(self.h, src.handle, count, dst.handle))
 
     def PhaseTrace(self, kernel: str = "mlp"):
-        """qnn_phase_trace: [2048, 16] uint64 phase timestamps of the fused MLP kernel ("mlp") or of
-        the one-token MoE kernel ("moe") (trace builds only); both are cleared afterwards."""
+        """qnn_phase_trace: [2048, 16] uint64 phase timestamps of the fused MLP kernel ("mlp"), the
+        one-token MoE kernel ("moe") or the LDS-streamed attention kernel ("attn") (trace builds
+        only); all three are cleared afterwards."""
         import numpy as np
 
-        buf = np.zeros((2, 2048, 16), np.uint64)
+        buf = np.zeros((3, 2048, 16), np.uint64)
         n = ctypes.c_uint64()
         _raise(lib().qnn_phase_trace(self.h, ctypes.c_void_p(buf.ctypes.data), buf.size, ctypes.byref(n)))
-        return buf[1 if kernel == "moe" else 0]
+        return buf[{"mlp": 0, "moe": 1, "attn": 2}[kernel]]
 
     # -- tensors
     def NewTensor(self, count: int) -> Tensor:

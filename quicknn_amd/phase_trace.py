@@ -1,6 +1,6 @@
 """Where the time of one fused decode-MLP launch goes, and the HBM stream floor.
 
-    python -m quicknn_amd.phase_trace [--runs N] [--no-stream] [--moe]
+    python -m quicknn_amd.phase_trace [--runs N] [--no-stream] [--moe | --attn]
 
 Loads libqnn_hip_trace.so (the library built with QNN_PHASE_TRACE: the same
 kernels, with thread 0 of every workgroup storing the device real-time
@@ -26,6 +26,12 @@ Phases of k_int4_mlp:
 so that each rotation reads every expert of every set (1.5 GB) and no launch
 finds its experts in the MALL.  Its phases are those of the MLP kernel, with
 an expert slot's gate/up tiles and blocks of h in place of the layer's.
+
+--attn times the 4096-key cached attention of `bench.py --config 6` (32
+query heads, 8 KV heads, head dim 128, one f32 cache per layer, 36 layers):
+phases of k_attn_dma 0 start, 1 q and K landed, 2 scores and softmax, 3 V
+landed, 4 values accumulated, 5 key lanes summed, 6 chunk output stored (the
+chunk merge is a second launch).
 
 The stream floor: one plain streaming read (qnn_stream_read: non-temporal
 16-byte loads, every piece requested at once, as the weight loads of the
@@ -90,9 +96,9 @@ def timeline(ctx, hip, blocks, runs: int):
     return summarise(per_run), float(np.median(us_layer))
 
 
-def summarise(per_run):
+def summarise(per_run, nphases=None):
     out = {}
-    for k in range(len(PHASES)):
+    for k in range(nphases or len(PHASES)):
         vals = [r[k] for r in per_run if k in r]
         if vals:
             a = np.array([v[:3] for v in vals])
@@ -101,13 +107,13 @@ def summarise(per_run):
     return out
 
 
-def phases_of(ts):
+def phases_of(ts, nphases=None):
     """{phase: (earliest, median, latest us after the first start, workgroups)} of one launch's stamps."""
     ts = ts.astype(np.int64)
     starts = ts[:, 0][ts[:, 0] > 0]
     t0 = starts.min()
     row = {}
-    for k in range(len(PHASES)):
+    for k in range(nphases or len(PHASES)):
         v = ts[:, k]
         v = v[v >= t0]  # every workgroup rewrites phase 0; earlier values are an earlier launch's
         if v.size:
@@ -117,6 +123,36 @@ def phases_of(ts):
 
 
 MOE_E, MOE_H, MOE_I, MOE_K, MOE_SETS = 128, 2048, 768, 8, 4
+ATTN_PHASES = ["start", "q and K landed", "scores and softmax", "V landed", "values accumulated",
+               "key lanes summed", "chunk output stored"]
+A_HEADS, A_KV, A_DIM, A_KEYS, A_LAYERS = 32, 8, 128, 4096, 36
+
+
+def attn_timeline(ctx, hip, runs: int):
+    """One decode query over 4096 cached keys per layer, one cache per layer (bench.py --config 6)."""
+    rng = np.random.default_rng(5)
+    caches = [ctx.UploadRaw(rng.standard_normal(2 * A_KEYS * A_KV * A_DIM).astype(np.float32))
+              for _ in range(A_LAYERS)]
+    q = ctx.UploadRaw((rng.standard_normal(A_HEADS * A_DIM) * 0.3).astype(np.float32))
+    o = ctx.NewTensor(A_HEADS * A_DIM)
+
+    def step():
+        for c in caches:
+            ctx.CachedAttention(o, q, c, 1, A_KEYS, A_HEADS, A_KV, A_DIM, A_KEYS - 1)
+
+    for _ in range(3):
+        step()
+    ctx.Flush()
+    ctx.PhaseTrace("attn")  # clear
+    per_run, us_call = [], []
+    for _ in range(runs):
+        ctx.EventRecord(0)
+        step()
+        ctx.EventRecord(1)
+        ctx.Flush()
+        us_call.append(ctx.EventElapsedMs(0, 1) * 1000 / A_LAYERS)
+        per_run.append(phases_of(ctx.PhaseTrace("attn"), len(ATTN_PHASES)))  # the last call's launch
+    return summarise(per_run, len(ATTN_PHASES)), float(np.median(us_call))
 
 
 def moe_timeline(ctx, hip, runs: int):
@@ -189,12 +225,26 @@ def main() -> int:
     ap.add_argument("--runs", type=int, default=5)
     ap.add_argument("--no-stream", action="store_true")
     ap.add_argument("--moe", action="store_true", help="the one-token routed-expert launch instead")
+    ap.add_argument("--attn", action="store_true", help="the 4096-key cached-attention launch instead")
     args = ap.parse_args()
     from quicknn_amd import build, hip
 
     if not os.path.exists(build.TRACE_LIB):
         raise SystemExit(f"{build.TRACE_LIB} is not built: run __graft_entry__.build()")
     hip.LIB_PATH = build.TRACE_LIB
+    if args.attn:
+        ctx = hip.GPUContext(0)
+        phases, us_call = attn_timeline(ctx, hip, args.runs)
+        print(f"kernel k_attn_dma (+ k_attn_merge): {us_call:.2f} us per call (HIP events, 36-call runs, "
+              f"median of {args.runs})")
+        print(f"{'phase':<22s} {'first':>8s} {'median':>8s} {'last':>8s} {'workgroups':>11s}")
+        for k, v in phases.items():
+            print(f"{k} {ATTN_PHASES[k]:<20s} {v['first_us']:8.2f} {v['median_us']:8.2f} {v['last_us']:8.2f} "
+                  f"{v['workgroups']:11d}")
+        print(json.dumps({"kernel": "k_attn_dma", "us_per_call": round(us_call, 2),
+                          "phases": {ATTN_PHASES[k]: v for k, v in phases.items()}}))
+        ctx.close()
+        return 0
     if args.moe:
         ctx = hip.GPUContext(0)
         s0 = ctx.status()
