@@ -159,11 +159,7 @@ __device__ __forceinline__ void block_max_sum(float (&v)[GB], float *red, bool i
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
-    float x = v[g];
-    for (int off = 32; off > 0; off >>= 1) {
-      const float o = __shfl_xor(x, off);
-      x = is_max ? fmaxf(x, o) : x + o;
-    }
+    const float x = is_max ? dev::wave_max_xor(v[g]) : dev::wave_sum_xor(v[g]);
     if (lane == 0) red[g * 4 + wave] = x;
   }
   __syncthreads();
@@ -308,14 +304,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
       if (part == 0) {
 #pragma unroll
         for (int g = 0; g < GB; ++g) {
-          float mx = valid ? sc[g] : -INFINITY;
-          for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+          const float mx = dev::wave_max_xor(valid ? sc[g] : -INFINITY);
           const float m_new = fmaxf(m_run[g], mx);
           keep[g] = m_new == -INFINITY ? 1.0f : expf(m_run[g] - m_new);
           const float p = (valid && m_new > -INFINITY) ? expf(sc[g] - m_new) : 0.0f;
           ps[g * kAttnSub + key_t] = p;
-          float ls = p;
-          for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off);
+          const float ls = dev::wave_sum_xor(p);
           l_run[g] = l_run[g] * keep[g] + ls;
           m_run[g] = m_new;
           if (key_t == 0) {
@@ -405,10 +399,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(const float *__restrict__
     for (int g = 0; g < GB; ++g)
 #pragma unroll
       for (int i = 0; i < ND4; ++i) {
-        acc[g][i].x += __shfl_down(acc[g][i].x, 32);
-        acc[g][i].y += __shfl_down(acc[g][i].y, 32);
-        acc[g][i].z += __shfl_down(acc[g][i].z, 32);
-        acc[g][i].w += __shfl_down(acc[g][i].w, 32);
+        acc[g][i].x += dev::xor_lanes<32>(acc[g][i].x);  // lanes 0-31 take 32-63 (the upper sums are unused)
+        acc[g][i].y += dev::xor_lanes<32>(acc[g][i].y);
+        acc[g][i].z += dev::xor_lanes<32>(acc[g][i].z);
+        acc[g][i].w += dev::xor_lanes<32>(acc[g][i].w);
       }
     const int w = tid >> 6, ln = tid & 63;
     if (w > 0 && ln < 32)
@@ -644,23 +638,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dma(const float *__restri
       v *= mul;
       if (a.softcap > 0.0f) v = a.softcap * tanhf(fminf(fmaxf(v / a.softcap, -20.0f), 20.0f));
       float mx = valid ? v : -INFINITY;
-      mx = fmaxf(mx, dev::xor_lanes<32>(mx));  // the butterfly of __shfl_xor(., 32 .. 1), on the VALU
-      mx = fmaxf(mx, dev::xor_lanes<16>(mx));
-      mx = fmaxf(mx, dev::xor_lanes<8>(mx));
-      mx = fmaxf(mx, dev::xor_lanes<4>(mx));
-      mx = fmaxf(mx, dev::xor_lanes<2>(mx));
-      mx = fmaxf(mx, dev::xor_lanes<1>(mx));
+      mx = dev::wave_max_xor(mx);
       const float m_new = fmaxf(m_run[g], mx);
       const float kp = m_new == -INFINITY ? 1.0f : expf(m_run[g] - m_new);
       const float p = (valid && m_new > -INFINITY) ? expf(v - m_new) : 0.0f;
       ps[g * kDmaKeys + key_t] = p;
-      float ls = p;
-      ls += dev::xor_lanes<32>(ls);
-      ls += dev::xor_lanes<16>(ls);
-      ls += dev::xor_lanes<8>(ls);
-      ls += dev::xor_lanes<4>(ls);
-      ls += dev::xor_lanes<2>(ls);
-      ls += dev::xor_lanes<1>(ls);
+      const float ls = dev::wave_sum_xor(p);
       if (key_t == 0) {
         red[g] = kp;
         red[GB + g] = l_run[g] * kp + ls;
@@ -778,15 +761,13 @@ __global__ __launch_bounds__(256) void k_attn_merge(float *out, const float *opa
     m = ml.x;
     l = ml.y;
   }
-  float M = m;
-  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+  float M = dev::wave_max_xor(m);
   if (lane == 0) red[0][wave] = M;
   __syncthreads();
   M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
   const float w = m > -INFINITY ? expf(m - M) : 0.0f;
   wsh[tid] = w;
-  float L = l * w;
-  for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+  float L = dev::wave_sum_xor(l * w);
   if (lane == 0) red[1][wave] = L;
   __syncthreads();
   L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);

@@ -35,5 +35,24 @@ __device__ __forceinline__ float xor_lanes(float x) {
   }
 }
 
+// The full-wave butterflies of __shfl_xor(x, 32), (.., 16), .., (.., 1), in
+// that order: every lane ends with the wave's maximum or sum.
+__device__ __forceinline__ float wave_max_xor(float x) {
+  x = fmaxf(x, xor_lanes<32>(x));
+  x = fmaxf(x, xor_lanes<16>(x));
+  x = fmaxf(x, xor_lanes<8>(x));
+  x = fmaxf(x, xor_lanes<4>(x));
+  x = fmaxf(x, xor_lanes<2>(x));
+  return fmaxf(x, xor_lanes<1>(x));
+}
+__device__ __forceinline__ float wave_sum_xor(float x) {
+  x += xor_lanes<32>(x);
+  x += xor_lanes<16>(x);
+  x += xor_lanes<8>(x);
+  x += xor_lanes<4>(x);
+  x += xor_lanes<2>(x);
+  return x + xor_lanes<1>(x);
+}
+
 }  // namespace dev
 }  // namespace qnn
