@@ -18,6 +18,7 @@
 //   the 64 lanes of a wave read 64 different banks), and each thread
 //   accumulates 4 rows of one output.
 #include "qnn_internal.h"
+#include "qnn_lanes.h"
 
 namespace qnn {
 namespace {
@@ -90,8 +91,7 @@ __global__ __launch_bounds__(256) void k_dense_matvec(const void *__restrict__ w
       acc = fmaf(wv, x[j], acc);
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  acc = dev::wave_sum_xor(acc);
   if (lane == 0) y[row] = acc;
 }
 
@@ -152,11 +152,8 @@ __global__ __launch_bounds__(256) void k_dense_swiglu(const void *__restrict__ w
       u = fmaf(weight_at<BU>(wu, size_t(row) * k + j), xv, u);
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    g += __shfl_xor(g, o);
-    u += __shfl_xor(u, o);
-  }
+  g = dev::wave_sum_xor(g);
+  u = dev::wave_sum_xor(u);
   if (lane == 0) {
     const float sg = g >= 20.0f ? g : (g <= -20.0f ? 0.0f : g / (1.0f + expf(-g)));  // tensor.comp:22
     y[row] = sg * u;

@@ -12,6 +12,7 @@
 // slower.
 #pragma once
 #include "qnn_internal.h"
+#include "qnn_lanes.h"
 
 namespace qnn {
 namespace dev {
@@ -40,7 +41,7 @@ __device__ __forceinline__ bool last_arrival(unsigned *counter, unsigned arrival
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   unsigned ticket = 0;
   if (lane == 0) ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  ticket = __shfl(ticket, 0);
+  ticket = __builtin_amdgcn_readfirstlane(ticket);  // lane 0's (every lane is active)
   if (ticket != arrivals - 1) return false;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   return true;

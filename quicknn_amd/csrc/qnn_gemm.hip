@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "qnn_internal.h"
+#include "qnn_lanes.h"
 
 namespace qnn {
 namespace {
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(1024) void k_act_prep(const float *__restrict__ a, 
     load8(g, v);
     amax = vmax(amax, v);
   }
-  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  amax = dev::wave_max_xor(amax);
   if (lane == 0) red[rw][part] = amax;
   __syncthreads();
   const int e = range_exp(fmaxf(fmaxf(red[rw][0], red[rw][1]), fmaxf(red[rw][2], red[rw][3])));

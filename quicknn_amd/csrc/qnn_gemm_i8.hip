@@ -39,6 +39,7 @@
 // converts its half).  About 33 VALU instructions per int8 MFMA remain,
 // against the 32 of the convert-and-fma epilogue itself.
 #include "qnn_internal.h"
+#include "qnn_lanes.h"
 
 namespace qnn {
 namespace {
@@ -80,9 +81,9 @@ __global__ __launch_bounds__(256) void k_q8_act_quant(const float *__restrict__ 
   float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (row < M) v = *reinterpret_cast<const float4 *>(a + size_t(row) * K + size_t(kb) * 32 + 4 * p);
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+  amax = fmaxf(amax, dev::xor_lanes<1>(amax));  // the eight lanes of the block
+  amax = fmaxf(amax, dev::xor_lanes<2>(amax));
+  amax = fmaxf(amax, dev::xor_lanes<4>(amax));
   const float d = amax / 127.0f;
   const float inv = d != 0.0f ? 1.0f / d : 0.0f;
   const uint32_t word = (uint32_t(int(roundf(v.x * inv))) & 255u) | (uint32_t(int(roundf(v.y * inv))) & 255u) << 8 |

@@ -399,7 +399,7 @@ __global__ __launch_bounds__(256) void k_gguf_rowexp(GGLayout l, const uint8_t *
     for (int k = tid; k < l.cols; k += 256)
       amax = fmaxf(amax, fabsf(gguf_value_tiled(l.enc, l, p, row / 64, k / 256, row & 63, k % 256)));
   }
-  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  amax = dev::wave_max_xor(amax);
   if ((tid & 63) == 0) red[tid >> 6] = amax;
   __syncthreads();
   if (tid == 0) ew[row] = range_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
@@ -1041,7 +1041,7 @@ __device__ __forceinline__ void gguf_item(const GGGroup &grp, const int mi) {
   }
   // 6) epilogue
   if (a.mode >= GG_SWIGLU) {
-    const float u = __shfl_down(acc, 32);
+    const float u = dev::xor_lanes<32>(acc);  // lanes 0-31 take 32-63
     const int row = tile * 32 + lane;
     if (lane < 32 && row < a.n) {
       if (a.g_out) {

@@ -13,26 +13,29 @@ namespace qnn {
 namespace dev {
 
 template <int OFF>
-__device__ __forceinline__ float xor_lanes(float x) {
+__device__ __forceinline__ int xor_lanes_i(int v) {
   static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane xor");
-  const int v = __float_as_int(x);
   if constexpr (OFF == 1) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
   } else if constexpr (OFF == 2) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
   } else if constexpr (OFF == 4) {
     const int lo = __builtin_amdgcn_mov_dpp(v, 0x114, 0xF, 0xF, false);  // row_shr:4 -> lane - 4
     const int hi = __builtin_amdgcn_mov_dpp(v, 0x104, 0xF, 0xF, false);  // row_shl:4 -> lane + 4
-    return __int_as_float((__lane_id() & 4) ? lo : hi);
+    return (__lane_id() & 4) ? lo : hi;
   } else if constexpr (OFF == 8) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false));  // row_ror:8 in 16-lane rows
+    return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);  // row_ror:8 in 16-lane rows
   } else if constexpr (OFF == 16) {
     const auto r = __builtin_amdgcn_permlane16_swap(unsigned(v), unsigned(v), false, false);
-    return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+    return int((__lane_id() & 16) ? r[0] : r[1]);
   } else {
     const auto r = __builtin_amdgcn_permlane32_swap(unsigned(v), unsigned(v), false, false);
-    return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+    return int((__lane_id() & 32) ? r[0] : r[1]);
   }
+}
+template <int OFF>
+__device__ __forceinline__ float xor_lanes(float x) {
+  return __int_as_float(xor_lanes_i<OFF>(__float_as_int(x)));
 }
 
 // The full-wave butterflies of __shfl_xor(x, 32), (.., 16), .., (.., 1), in

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(64) void k_moe_route(float *routes, const float *lo
     taken[e] = 0;
     mx = fmaxf(mx, v);
   }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = dev::wave_max_xor(mx);
   // The lane's own LDS entries: partial lane + 64*i sums experts lane + 64*i + 256*m, ascending m.
   float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int i = 0; i < 4; ++i)
@@ -165,15 +165,22 @@ __global__ __launch_bounds__(64) void k_moe_route(float *routes, const float *lo
         bid = e;
       }
     }
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(best, o);
-      const int oi = __shfl_xor(bid, o);
+    auto step = [&](auto off) {  // the butterfly of __shfl_xor(., 32 .. 1), on the VALU
+      constexpr int O = decltype(off)::value;
+      const float ov = dev::xor_lanes<O>(best);
+      const int oi = dev::xor_lanes_i<O>(bid);
       if (route_better(ov, oi, best, bid)) {
         best = ov;
         bid = oi;
       }
-    }
-    bid = __shfl(bid, 0);  // k <= experts: a candidate always exists
+    };
+    step(std::integral_constant<int, 32>());
+    step(std::integral_constant<int, 16>());
+    step(std::integral_constant<int, 8>());
+    step(std::integral_constant<int, 4>());
+    step(std::integral_constant<int, 2>());
+    step(std::integral_constant<int, 1>());
+    bid = __builtin_amdgcn_readfirstlane(bid);  // lane 0's; k <= experts: a candidate always exists
     if (lane == 0) taken[bid] = 1;
     if (lane == r) {
       my_id = bid;
@@ -182,7 +189,7 @@ __global__ __launch_bounds__(64) void k_moe_route(float *routes, const float *lo
     __syncthreads();
   }
   float total = 0.0f;
-  for (int r = 0; r < k; ++r) total += __shfl(my_p, r);  // rank order
+  for (int r = 0; r < k; ++r) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), r));  // rank order
   if (lane < k) {
     const int target = row * k + lane;
     routes[target] = __uint_as_float(uint32_t(my_id));

@@ -285,7 +285,7 @@ __global__ __launch_bounds__(256) void k_moe(const MoELaunch a, const int slices
     if (DOWN) {
       if (j == 0 && row < nout) dev::xstore(a.y + size_t(R) * a.hidden + row, v);
     } else {
-      const float u = __shfl_down(v, 32);
+      const float u = dev::xor_lanes<32>(v);  // lanes 0-31 take 32-63
       if (lane < 32 && j == 0 && row < nout) a.h[size_t(R) * a.inter + row] = dev::silu(v) * u;
     }
   };
@@ -507,7 +507,8 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
     atomicOr(a.err, 8);
   auto src_of = [&](int slot) { return __ffsll((unsigned long long)__ballot(lane < k && rank == slot)) - 1; };
   auto expert_of = [&](int slot) {  // clamped so addresses stay inside the set; scalar (uniform) for the resources
-    return __builtin_amdgcn_readfirstlane(int(min(uint32_t(__shfl(id, src_of(slot))), uint32_t(a.experts - 1))));
+    return __builtin_amdgcn_readfirstlane(
+        int(min(uint32_t(__builtin_amdgcn_readlane(int(id), src_of(slot))), uint32_t(a.experts - 1))));
   };
 
   // ---- gate/up item
@@ -609,7 +610,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoELaunch a, const int
   // combine, taken now rather than on the combine's dependent path.
   float pslot = 0.0f;
   for (int j = 0; j < k; ++j) {
-    const float pj = __shfl(prob, src_of(j));
+    const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), src_of(j)));
     if (lane == j) pslot = pj;
   }
 

@@ -38,8 +38,13 @@ __device__ __forceinline__ float route_denominator(float q0, float q1, float q2,
   q0 = q0 + q2;  // s = 128
   q1 = q1 + q3;
   float s = q0 + q1;  // s = 64
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) s = s + __shfl_down(s, d, 64);  // lanes < d hold the tree's values
+  // lanes < d hold the tree's values: lane i adds lane i + d = i ^ d
+  s = s + xor_lanes<32>(s);
+  s = s + xor_lanes<16>(s);
+  s = s + xor_lanes<8>(s);
+  s = s + xor_lanes<4>(s);
+  s = s + xor_lanes<2>(s);
+  s = s + xor_lanes<1>(s);
   return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(s)));
 }
 
@@ -66,8 +71,7 @@ __device__ __forceinline__ void route_select(RouteRow<J> &r, const float *l, int
 #pragma unroll
   for (int j = 0; j < J; ++j)
     if (j * 64 + lane < experts) mx = fmaxf(mx, v[j]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = wave_max_xor(mx);
   float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // partials lane + 64*i: experts (i + 4m)*64 + lane
 #pragma unroll
   for (int j = 0; j < J; ++j) {
